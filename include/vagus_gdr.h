@@ -1,0 +1,121 @@
+/*
+ * vagus_gdr.h — C ABI of the MI355X (gfx950) gated delta-rule core.
+ *
+ * Replaces the backend call of the reference's GPU scan path,
+ * infra/components/linear_attention.py:474-497 (fla_scan → fla's
+ * chunk_gated_delta_rule / chunk_kda / chunk_simple_gla), selected by
+ * GatedDeltaNet._pick_impl / _scan (:755-812), and the single-token
+ * recurrence it runs for decode (recurrent_scan at L == 1, :945-947).
+ *
+ * Semantics, per (sequence, head), with state S in R^{dk x dv}
+ * (linear_attention.py:8-11, :161-195):
+ *     S_t = (I - beta_t k_t k_t^T) Diag(a_t) S_{t-1} + beta_t k_t v_t^T
+ *     o_t = scale * S_t^T q_t,          a_t = exp(g_t)
+ * use_delta = 0 drops the erase term: S_t = Diag(a_t) S_{t-1} + k_t v_t^T.
+ *
+ * Conventions shared by every entry point
+ *   - Pointers are device pointers (hipMalloc'd or torch tensors); all
+ *     tensors are dense row-major (contiguous).  Inputs are read-only.
+ *   - Token layout: q, k  [n_tokens, H, dk];  v, o  [n_tokens, H, dv];
+ *     g  [n_tokens, H] (gate_kind 1) or [n_tokens, H, dk] (gate_kind 2), fp32;
+ *     beta [n_tokens, H] fp32.  n_tokens = B * T for a dense batch.
+ *   - Sequences: with cu_seqlens == NULL the batch is dense, B sequences of
+ *     T tokens (sequence b owns tokens [b*T, (b+1)*T)).  Otherwise
+ *     cu_seqlens is a device int32 array of n_seqs + 1 offsets into a packed
+ *     stream of n_tokens = T tokens (B must be 1); each segment is clamped to
+ *     [0, T], so a malformed table cannot address memory outside the tensors.
+ *   - States: initial_state / final_state are fp32 [n_seqs, H, dk, dv]
+ *     (n_seqs = B for a dense batch), either may be NULL (zeros / not
+ *     written).  They may alias (in-place update).
+ *   - dtype is the element type of q, k, v and o.
+ *   - Every call is asynchronous on `stream`, allocates nothing and never
+ *     synchronises.  Calls are reentrant.  Return 0 on success; on failure a
+ *     VGDR_ERR_* code and a message readable with vgdr_last_error() (a
+ *     per-thread string).
+ */
+#ifndef VAGUS_GDR_H
+#define VAGUS_GDR_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum vgdr_status {
+    VGDR_OK = 0,
+    VGDR_ERR_INVALID = 1,      /* misuse: bad shape / pointer / flag (reference: AssertionError)  */
+    VGDR_ERR_UNSUPPORTED = 2,  /* valid but not implemented (reference: NotImplementedError)      */
+    VGDR_ERR_HIP = 3           /* the HIP runtime reported an error (reference: RuntimeError)      */
+};
+
+enum vgdr_dtype { VGDR_F32 = 0, VGDR_BF16 = 1, VGDR_F16 = 2 };
+
+enum vgdr_gate {
+    VGDR_GATE_NONE = 0,        /* a_t = 1 (g ignored, may be NULL)      — DeltaNet               */
+    VGDR_GATE_SCALAR = 1,      /* g [n_tokens, H]: one decay per head   — Gated DeltaNet (GDN)   */
+    VGDR_GATE_VECTOR = 2       /* g [n_tokens, H, dk]: per key channel  — Kimi Delta Attn (KDA)  */
+};
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int vgdr_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *vgdr_last_error(void);
+
+/*
+ * Chunkwise prefill.  Replaces fla's chunk_gated_delta_rule (gate_kind 0/1,
+ * use_delta 1), chunk_kda (gate_kind 2) and chunk_simple_gla (use_delta 0)
+ * as called at linear_attention.py:474-497, with the reference's WY chunk
+ * semantics (chunk_scan :237-309, chunk_scan_vec :312-425).
+ *
+ * chunk_size is accepted for interface parity: 64 and 32 select the kernel's
+ * chunk length; the result is chunk-size invariant up to rounding.
+ * Supported: dk in {64, 128}, dv a multiple of 16 (any count of 64-column
+ * tiles).  `workspace` must be NULL for a dense batch; for a packed batch it
+ * may point to vgdr_varlen_workspace_size(n_seqs) bytes prepared by
+ * vgdr_varlen_prepare (it then holds the longest-first schedule), or be NULL
+ * (segments are scheduled in index order).
+ */
+int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta,
+                   const void *q, const void *k, const void *v,
+                   const float *g, const float *beta,
+                   void *o, const float *initial_state, float *final_state,
+                   const int32_t *cu_seqlens, const void *workspace,
+                   int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                   float scale, int chunk_size, hipStream_t stream);
+
+/*
+ * Token-by-token recurrence.  The decode step is T = 1 with
+ * initial_state == final_state (in place), replacing recurrent_scan at
+ * linear_attention.py:945-947 and the state.copy_ at :950.  Any T works (the
+ * reference's fused_recurrent semantics).  dk in {64, 128}, dv in {64, 128}.
+ */
+int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta,
+                       const void *q, const void *k, const void *v,
+                       const float *g, const float *beta,
+                       void *o, const float *initial_state, float *final_state,
+                       const int32_t *cu_seqlens,
+                       int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                       float scale, hipStream_t stream);
+
+/*
+ * Packed-batch schedule.  No reference counterpart (the reference has no
+ * cu_seqlens, see infra/inference/generator.py:19-22); fla builds the same
+ * integer tables for its varlen kernels.  Writes into `workspace`
+ * (vgdr_varlen_workspace_size(n_seqs) bytes, int32 fields in this order):
+ *     lens[n_seqs], chunks[n_seqs], chunk_offsets[n_seqs + 1], order[n_seqs]
+ * lens = cu[n+1] - cu[n] (clamped into [0, n_tokens]), chunks =
+ * ceil(lens / chunk_size), chunk_offsets = exclusive prefix sum of chunks,
+ * order = segments sorted longest first, ties by index.
+ */
+int64_t vgdr_varlen_workspace_size(int64_t n_seqs);
+int vgdr_varlen_prepare(const int32_t *cu_seqlens, int64_t n_seqs, int64_t n_tokens,
+                        int chunk_size, void *workspace, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VAGUS_GDR_H */

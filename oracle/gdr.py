@@ -1,0 +1,295 @@
+"""CPU restatement of the gated delta-rule scans — the oracle (test infrastructure).
+
+This module restates, in plain torch on the CPU, the algorithm of the
+reference's hot path ``infra/components/linear_attention.py``.  It is the
+checker for the HIP kernels in ``vagus_amd`` and the timed CPU baseline of
+``bench.py``; nothing in the product imports it.
+
+Per head, with state S in R^{dk x dv}, log-decay g_t <= 0 (a_t = exp(g_t),
+a scalar for GDN or a per-key-channel vector for KDA) and write strength
+beta_t (linear_attention.py:8-11):
+
+    S_t = (I - beta_t k_t k_t^T) Diag(a_t) S_{t-1} + beta_t k_t v_t^T
+    o_t = scale * S_t^T q_t
+
+Functions and the reference lines they follow:
+
+    recurrent       linear_attention.py:161-195   the definition
+    chunk_scalar    linear_attention.py:237-309   WY chunk form, scalar / no gate
+    chunk_vector    linear_attention.py:312-425   WY chunk form, per-channel gate
+    chunk           linear_attention.py:251-252   dispatch on g.dim()
+    varlen          (no reference counterpart)    per-segment loop over cu_seqlens
+    chunk_table     (no reference counterpart)    integer chunk / schedule table
+    chunk_scan_flops linear_attention.py:128-143  FLOPs per token per head
+
+Layouts follow the reference (linear_attention.py:146-154): q, k (B, L, H, dk),
+v (B, L, H, dv), g (B, L, H) or (B, L, H, dk), beta (B, L, H), S0 (B, H, dk, dv).
+Computation is fp64 when q is fp64, else fp32 (linear_attention.py:157-158);
+o is returned in q.dtype and S in the compute dtype.
+
+How each function is pinned (tests/test_oracle.py): ``recurrent`` against
+closed forms (causal linear attention, pure decay, one-token write, the
+delta-rule overwrite identity) and against an independent dense-matrix
+statement of the update above; the chunk forms against ``recurrent`` at
+1e-12 in fp64, chunk-size / padding invariance and the scalar == constant
+vector-gate reduction; ``varlen`` by segment isolation; ``chunk_table`` by
+brute-force enumeration; ``chunk_scan_flops`` by the reference's known answers.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+
+def compute_dtype(x: torch.Tensor) -> torch.dtype:
+    """fp64 stays fp64 (the exactness oracle), everything else runs in fp32
+    (linear_attention.py:157-158)."""
+    return torch.float64 if x.dtype == torch.float64 else torch.float32
+
+
+# ---------------------------------------------------------------------------
+# the definition
+# ---------------------------------------------------------------------------
+
+def recurrent(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True):
+    """Token-by-token recurrence (linear_attention.py:161-195).
+
+    Per step: decay the key rows of S (scalar or per channel), read what S
+    returns for k_t, write beta_t k_t (v_t - k_t^T S)^T (or k_t v_t^T without
+    the delta rule), then read out o_t = scale q_t^T S *after* the write.
+    L == 0 returns an empty o and S0 unchanged (as a copy in compute dtype).
+    """
+    B, L, H, dk = q.shape
+    dv = v.shape[-1]
+    ct = compute_dtype(q)
+    qs = q.to(ct) * scale
+    kc, vc = k.to(ct), v.to(ct)
+    S = torch.zeros(B, H, dk, dv, dtype=ct) if S0 is None else S0.to(ct).clone()
+    o = torch.zeros(B, L, H, dv, dtype=ct)
+    for t in range(L):
+        if g is not None:
+            a = g[:, t].to(ct).exp()
+            if a.dim() == 2:                       # (B, H): one decay per head
+                S = S * a[:, :, None, None]
+            else:                                  # (B, H, dk): per key row
+                S = S * a[:, :, :, None]
+        kt, vt = kc[:, t], vc[:, t]                # (B, H, dk), (B, H, dv)
+        if delta:
+            read = torch.matmul(kt.unsqueeze(-2), S).squeeze(-2)          # k_t^T S  (B, H, dv)
+            wt = kt * beta[:, t].to(ct).unsqueeze(-1)
+            S = S + wt.unsqueeze(-1) * (vt - read).unsqueeze(-2)
+        else:
+            S = S + kt.unsqueeze(-1) * vt.unsqueeze(-2)
+        o[:, t] = torch.matmul(qs[:, t].unsqueeze(-2), S).squeeze(-2)
+    return o.to(q.dtype), S
+
+
+# ---------------------------------------------------------------------------
+# chunk forms
+# ---------------------------------------------------------------------------
+
+def _pad_tokens(x, pad):
+    """Append `pad` zero tokens along dim 1."""
+    if pad == 0 or x is None:
+        return x
+    shape = list(x.shape)
+    shape[1] = pad
+    return torch.cat([x, x.new_zeros(shape)], dim=1)
+
+
+def _blocks(x, N, C):
+    """(B, N*C, H, ...) -> (B, H, N, C, ...)."""
+    B, _, H = x.shape[:3]
+    rest = x.shape[3:]
+    y = x.reshape(B, N, C, H, *rest)
+    perm = (0, 3, 1, 2) + tuple(range(4, 4 + len(rest)))
+    return y.permute(*perm)
+
+
+def chunk_scalar(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
+                 chunk_size: int = 64):
+    """WY chunk form for a scalar (or absent) gate (linear_attention.py:237-309).
+
+    Within a chunk with entry state S, gamma = in-chunk cumsum of g,
+    D_ij = exp(gamma_i - gamma_j) on i >= j (masked before the exp), and
+        W   = (I + Bm)^-1 diag(beta) K,         Bm_ij = beta_i k_i.k_j  (j < i)
+        U   = (I + Bm*D)^-1 diag(beta) V
+        U~  = U - diag(G) W S
+        o   = diag(G) Q S + (Q K^T * D) U~
+        S' <- G_C S + K^T diag(G_C / G_j) U~
+    Without the delta rule W = 0 and U = V.  Padding tokens (q = k = v = 0,
+    g = 0, beta = 0) are inert and the output is cut back to L.  A 4-D g is a
+    per-channel gate and goes to chunk_vector (linear_attention.py:251-252).
+    """
+    if g is not None and g.dim() == 4:
+        return chunk_vector(q, k, v, g, beta, S0, scale=scale, delta=delta,
+                            chunk_size=chunk_size)
+    B, L, H, dk = q.shape
+    dv = v.shape[-1]
+    C = chunk_size
+    ct = compute_dtype(q)
+    pad = (-L) % C
+    N = (L + pad) // C
+    qs = _blocks(_pad_tokens(q.to(ct) * scale, pad), N, C)                 # (B, H, N, C, dk)
+    kc = _blocks(_pad_tokens(k.to(ct), pad), N, C)
+    vc = _blocks(_pad_tokens(v.to(ct), pad), N, C)
+    if g is None:
+        gam = torch.zeros(B, H, N, C, dtype=ct)
+    else:
+        gam = _blocks(_pad_tokens(g.to(ct), pad), N, C).cumsum(-1)         # log G_i
+    if delta:
+        bt = _blocks(_pad_tokens(beta.to(ct), pad), N, C)                  # (B, H, N, C)
+    lower = torch.ones(C, C, dtype=torch.bool).tril()
+    strict = lower.tril(-1)
+    eye = torch.eye(C, dtype=ct)
+    S = torch.zeros(B, H, dk, dv, dtype=ct) if S0 is None else S0.to(ct).clone()
+    out = []
+    for n in range(N):
+        Qn, Kn, Vn, gm = qs[:, :, n], kc[:, :, n], vc[:, :, n], gam[:, :, n]
+        diff = gm.unsqueeze(-1) - gm.unsqueeze(-2)                        # gamma_i - gamma_j
+        D = torch.where(lower, diff, torch.full_like(diff, -math.inf)).exp()
+        Gi = gm.exp().unsqueeze(-1)                                       # G_i     (B, H, C, 1)
+        Gtail = (gm[..., -1:] - gm).exp().unsqueeze(-1)                   # G_C/G_j (B, H, C, 1)
+        Aqk = torch.matmul(Qn, Kn.transpose(-1, -2)) * D
+        if delta:
+            bn = bt[:, :, n].unsqueeze(-1)                                # (B, H, C, 1)
+            Bm = bn * torch.matmul(Kn, Kn.transpose(-1, -2)) * strict
+            W = torch.linalg.solve_triangular(eye + Bm, bn * Kn, upper=False, unitriangular=True)
+            U = torch.linalg.solve_triangular(eye + Bm * D, bn * Vn, upper=False, unitriangular=True)
+            Ut = U - Gi * torch.matmul(W, S)
+        else:
+            Ut = Vn
+        out.append(Gi * torch.matmul(Qn, S) + torch.matmul(Aqk, Ut))
+        S = gm[..., -1].exp()[..., None, None] * S + torch.matmul(Kn.transpose(-1, -2), Gtail * Ut)
+    o = torch.stack(out, dim=2) if N else torch.zeros(B, H, 0, C, dv, dtype=ct)
+    o = o.permute(0, 2, 3, 1, 4).reshape(B, N * C, H, dv)[:, :L]
+    return o.to(q.dtype), S
+
+
+def chunk_vector(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
+                 chunk_size: int = 64):
+    """WY chunk form for a per-channel gate g (B, L, H, dk) (linear_attention.py:312-425).
+
+    Every inner product becomes a gated one,
+        <x_i, y_j>_g = sum_c x_i[c] y_j[c] exp(gamma_i[c] - gamma_j[c])   (i >= j),
+    whose exponents are <= 0, and per chunk
+        (I + M) W = diag(beta) (K * G),  (I + M) U = diag(beta) V,   M_ij = beta_i <k_i, k_j>_g (j < i)
+        U~  = U - W S
+        o   = (Q * G) S + A U~,          A_ij = <q_i, k_j>_g (j <= i)
+        S' <- G_C (.) S + (K * G_C / G_j)^T U~     (G_C scales the key rows of S)
+    Without the delta rule U~ = V.  The pairwise exponent tensor is built one
+    chunk at a time.
+    """
+    B, L, H, dk = q.shape
+    dv = v.shape[-1]
+    C = chunk_size
+    ct = compute_dtype(q)
+    pad = (-L) % C
+    N = (L + pad) // C
+    qs = _blocks(_pad_tokens(q.to(ct) * scale, pad), N, C)                 # (B, H, N, C, dk)
+    kc = _blocks(_pad_tokens(k.to(ct), pad), N, C)
+    vc = _blocks(_pad_tokens(v.to(ct), pad), N, C)
+    gam = _blocks(_pad_tokens(g.to(ct), pad), N, C).cumsum(3)              # (B, H, N, C, dk)
+    if delta:
+        bt = _blocks(_pad_tokens(beta.to(ct), pad), N, C)
+    lower = torch.ones(C, C, dtype=torch.bool).tril()
+    strict = lower.tril(-1)
+    eye = torch.eye(C, dtype=ct)
+    S = torch.zeros(B, H, dk, dv, dtype=ct) if S0 is None else S0.to(ct).clone()
+    out = []
+    for n in range(N):
+        Qn, Kn, Vn, gm = qs[:, :, n], kc[:, :, n], vc[:, :, n], gam[:, :, n]
+        diff = gm.unsqueeze(3) - gm.unsqueeze(2)                          # (B, H, C, C, dk)
+        E = torch.where(lower[None, None, :, :, None], diff,
+                        torch.full_like(diff, -math.inf)).exp()
+        G = gm.exp()                                                      # (B, H, C, dk)
+        Gtail = (gm[:, :, -1:, :] - gm).exp()                             # G_C / G_j
+
+        def gated(x, y):
+            return torch.einsum('bhic,bhijc,bhjc->bhij', x, E, y)
+
+        A = gated(Qn, Kn)
+        if delta:
+            bn = bt[:, :, n].unsqueeze(-1)
+            M = bn * gated(Kn, Kn) * strict
+            W = torch.linalg.solve_triangular(eye + M, bn * (Kn * G), upper=False, unitriangular=True)
+            U = torch.linalg.solve_triangular(eye + M, bn * Vn, upper=False, unitriangular=True)
+            Ut = U - torch.matmul(W, S)
+        else:
+            Ut = Vn
+        out.append(torch.matmul(Qn * G, S) + torch.matmul(A, Ut))
+        S = G[:, :, -1, :, None] * S + torch.matmul((Kn * Gtail).transpose(-1, -2), Ut)
+    o = torch.stack(out, dim=2) if N else torch.zeros(B, H, 0, C, dv, dtype=ct)
+    o = o.permute(0, 2, 3, 1, 4).reshape(B, N * C, H, dv)[:, :L]
+    return o.to(q.dtype), S
+
+
+def chunk(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True, chunk_size: int = 64):
+    """Dispatch on the gate's rank, as chunk_scan does (linear_attention.py:251-252)."""
+    fn = chunk_vector if (g is not None and g.dim() == 4) else chunk_scalar
+    return fn(q, k, v, g, beta, S0, scale=scale, delta=delta, chunk_size=chunk_size)
+
+
+# ---------------------------------------------------------------------------
+# packed variable-length batches
+# ---------------------------------------------------------------------------
+
+def varlen(fn, q, k, v, g, beta, S0, cu_seqlens, **kw):
+    """Run `fn` (recurrent / chunk) on each segment [cu[n], cu[n+1]) of a packed
+    (1, T, H, d) stream with its own entry state S0[n] (or zeros).  Returns the
+    packed o (1, T, H, dv) and the stacked final states (N, H, dk, dv)."""
+    cu = [int(x) for x in torch.as_tensor(cu_seqlens).tolist()]
+    assert q.shape[0] == 1, 'packed varlen input has batch 1'
+    N = len(cu) - 1
+    ct = compute_dtype(q)
+    dk, dv, H = q.shape[-1], v.shape[-1], q.shape[2]
+    outs, states = [], []
+    for n in range(N):
+        s, e = cu[n], cu[n + 1]
+        sl = slice(s, e)
+        s0 = None if S0 is None else S0[n:n + 1]
+        gn = None if g is None else g[:, sl]
+        bn = None if beta is None else beta[:, sl]
+        if e > s:
+            o, S = fn(q[:, sl], k[:, sl], v[:, sl], gn, bn, s0, **kw)
+        else:
+            o = q.new_zeros(1, 0, H, dv)
+            S = torch.zeros(1, H, dk, dv, dtype=ct) if s0 is None else s0.to(ct).clone()
+        outs.append(o)
+        states.append(S)
+    o = torch.cat(outs, dim=1) if outs else q.new_zeros(1, 0, H, dv)
+    return o, torch.cat(states, dim=0)
+
+
+def chunk_table(cu_seqlens, chunk_size: int):
+    """Integer schedule table of a packed batch, computed on the host.
+
+    Returns a dict of int32 numpy arrays:
+        lens[n]          = cu[n+1] - cu[n]
+        chunks[n]        = ceil(lens[n] / chunk_size)
+        chunk_offsets[n] = sum_{m<n} chunks[m]          (length N+1, last = total)
+        order[p]         = segments sorted by length, longest first, ties by index
+    """
+    cu = np.asarray(torch.as_tensor(cu_seqlens).cpu().numpy(), dtype=np.int64)
+    lens = cu[1:] - cu[:-1]
+    chunks = (lens + chunk_size - 1) // chunk_size
+    offs = np.zeros(len(lens) + 1, dtype=np.int64)
+    offs[1:] = np.cumsum(chunks)
+    order = np.array(sorted(range(len(lens)), key=lambda n: (-lens[n], n)), dtype=np.int64)
+    return {'lens': lens.astype(np.int32), 'chunks': chunks.astype(np.int32),
+            'chunk_offsets': offs.astype(np.int32), 'order': order.astype(np.int32)}
+
+
+# ---------------------------------------------------------------------------
+# accounting
+# ---------------------------------------------------------------------------
+
+def chunk_scan_flops(dk: int, dv: int, chunk: int, delta: bool) -> float:
+    """Matmul FLOPs per token per head, forward + backward (x3), of the chunked
+    algorithm (linear_attention.py:128-143): state terms (6 or 4) dk dv plus the
+    intra-chunk terms 2C (3dk + 2dv) with the delta rule, 2C (dk + dv) without."""
+    state = (6 if delta else 4) * dk * dv
+    intra = 2 * chunk * ((3 * dk + 2 * dv) if delta else (dk + dv))
+    return 3.0 * (state + intra)

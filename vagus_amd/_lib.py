@@ -1,0 +1,67 @@
+"""ctypes binding of libvagus_gdr.so (the C ABI of include/vagus_gdr.h).
+
+The library is loaded lazily on first use and there is no fallback: a missing
+library raises RuntimeError with the build command, so a GPU run can never
+silently execute something other than the HIP kernels.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'libvagus_gdr.so')
+
+VGDR_OK, VGDR_ERR_INVALID, VGDR_ERR_UNSUPPORTED, VGDR_ERR_HIP = 0, 1, 2, 3
+VGDR_F32, VGDR_BF16, VGDR_F16 = 0, 1, 2
+VGDR_GATE_NONE, VGDR_GATE_SCALAR, VGDR_GATE_VECTOR = 0, 1, 2
+
+# every symbol the header declares, with its ctypes signature
+_P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+SIGNATURES = {
+    'vgdr_version': (_I, []),
+    'vgdr_last_error': (ctypes.c_char_p, []),
+    'vgdr_chunk_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                            _L, _L, _L, _L, _L, _L, _F, _I, _P]),
+    'vgdr_recurrent_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                _L, _L, _L, _L, _L, _L, _F, _P]),
+    'vgdr_varlen_workspace_size': (_L, [_L]),
+    'vgdr_varlen_prepare': (_I, [_P, _L, _L, _I, _P, _P]),
+}
+
+_lib = None
+_lock = threading.Lock()
+
+
+def load(path: str = LIB_PATH) -> ctypes.CDLL:
+    """The loaded library (cached).  Raises RuntimeError when it is not built."""
+    global _lib
+    if _lib is not None and path == LIB_PATH:
+        return _lib
+    with _lock:
+        if _lib is not None and path == LIB_PATH:
+            return _lib
+        if not os.path.exists(path):
+            raise RuntimeError(f'vagus_amd: {path} is not built; run `python -m vagus_amd.build` '
+                               '(the HIP kernels are the only implementation)')
+        lib = ctypes.CDLL(path)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if path == LIB_PATH:
+            _lib = lib
+        return lib
+
+
+def check(rc: int) -> None:
+    """Map a status code to the reference's exception types
+    (linear_attention.py:452-461: RuntimeError / NotImplementedError / AssertionError)."""
+    if rc == VGDR_OK:
+        return
+    msg = load().vgdr_last_error().decode(errors='replace')
+    if rc == VGDR_ERR_INVALID:
+        raise AssertionError(msg)
+    if rc == VGDR_ERR_UNSUPPORTED:
+        raise NotImplementedError(msg)
+    raise RuntimeError(msg)

@@ -1,0 +1,159 @@
+// extern "C" entry points of libvagus_gdr.so (declared in include/vagus_gdr.h).
+// Argument checking, status codes, the per-thread error string, and the
+// dispatch to the kernel launchers.  Nothing here allocates or synchronises.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/vagus_gdr.h"
+#include "gdr_kernels.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+int hip_status(hipError_t e, const char *what) {
+    if (e == hipSuccess) return VGDR_OK;
+    return fail(VGDR_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// checks shared by both scan entry points; returns VGDR_OK or an error code
+int check_common(const char *fn, int dtype, int gate_kind, int use_delta, const void *q, const void *k,
+                 const void *v, const float *g, const float *beta, const void *o,
+                 const int32_t *cu, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                 int64_t n_seqs) {
+    if (dtype != VGDR_F32 && dtype != VGDR_BF16 && dtype != VGDR_F16)
+        return fail(VGDR_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+    if (gate_kind < VGDR_GATE_NONE || gate_kind > VGDR_GATE_VECTOR)
+        return fail(VGDR_ERR_INVALID, "%s: unknown gate_kind %d", fn, gate_kind);
+    if (B < 0 || T < 0 || H <= 0 || n_seqs < 0)
+        return fail(VGDR_ERR_INVALID, "%s: bad sizes B=%lld T=%lld H=%lld n_seqs=%lld", fn, (long long)B,
+                    (long long)T, (long long)H, (long long)n_seqs);
+    if (dk != 64 && dk != 128)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: dk=%lld (supported: 64, 128)", fn, (long long)dk);
+    if (cu) {
+        if (B != 1) return fail(VGDR_ERR_INVALID, "%s: a packed batch (cu_seqlens) needs B == 1", fn);
+    } else if (n_seqs != B) {
+        return fail(VGDR_ERR_INVALID, "%s: n_seqs (%lld) must equal B (%lld) for a dense batch", fn,
+                    (long long)n_seqs, (long long)B);
+    }
+    if (B * T > 0 && (!q || !k || !v || !o))
+        return fail(VGDR_ERR_INVALID, "%s: q, k, v and o are required", fn);
+    if (gate_kind != VGDR_GATE_NONE && B * T > 0 && !g)
+        return fail(VGDR_ERR_INVALID, "%s: gate_kind %d needs g", fn, gate_kind);
+    if (use_delta && B * T > 0 && !beta) return fail(VGDR_ERR_INVALID, "%s: the delta rule needs beta", fn);
+    if (n_seqs > 0x7fffffffLL / H) return fail(VGDR_ERR_INVALID, "%s: too many (sequence, head) pairs", fn);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v))
+        return fail(VGDR_ERR_INVALID, "%s: q, k and v must be 16-byte aligned", fn);
+    if (gate_kind == VGDR_GATE_VECTOR && !aligned16(g))
+        return fail(VGDR_ERR_INVALID, "%s: a per-channel g must be 16-byte aligned", fn);
+    return VGDR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int vgdr_version(void) { return 100; }
+
+const char *vgdr_last_error(void) { return g_err; }
+
+int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                   const float *g, const float *beta, void *o, const float *initial_state,
+                   float *final_state, const int32_t *cu_seqlens, const void *workspace, int64_t B,
+                   int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
+                   int chunk_size, hipStream_t stream) {
+    g_err[0] = 0;
+    int rc = check_common("vgdr_chunk_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o, cu_seqlens,
+                          B, T, H, dk, dv, n_seqs);
+    if (rc) return rc;
+    if (dv <= 0 || dv % 16)
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_chunk_fwd: dv=%lld (must be a positive multiple of 16)",
+                    (long long)dv);
+    if (!aligned16(o)) return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: o must be 16-byte aligned");
+    if (workspace && !cu_seqlens)
+        return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: a workspace is only used with cu_seqlens");
+    int chunk = chunk_size <= 32 ? 32 : 64;
+    if (dtype == VGDR_F32 && dk == 128) chunk = 32;   // the fp32 128-key tile needs the short chunk
+    vgdr::ChunkParams p{};
+    p.q = q; p.k = k; p.v = v;
+    p.g = gate_kind == VGDR_GATE_NONE ? nullptr : g;
+    p.beta = beta;
+    p.o = o;
+    p.h0 = initial_state;
+    p.ht = final_state;
+    p.cu = cu_seqlens;
+    p.order = workspace ? reinterpret_cast<const int32_t *>(workspace) + 3 * n_seqs + 1 : nullptr;
+    p.T = T;
+    p.n_tokens = B * T;
+    p.H = (int)H;
+    p.DV = (int)dv;
+    p.n_seqs = (int)n_seqs;
+    p.n_tiles = (int)((dv + vgdr::chunk_tile_cols() - 1) / vgdr::chunk_tile_cols());
+    p.use_delta = use_delta ? 1 : 0;
+    p.scale = scale;
+    if ((int64_t)p.n_seqs * p.H * p.n_tiles > 0x7fffffffLL)
+        return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: grid too large");
+    return hip_status(vgdr::chunk_fwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, p, stream),
+                      "vgdr_chunk_fwd launch");
+}
+
+int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                       const float *g, const float *beta, void *o, const float *initial_state,
+                       float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H,
+                       int64_t dk, int64_t dv, int64_t n_seqs, float scale, hipStream_t stream) {
+    g_err[0] = 0;
+    int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o,
+                          cu_seqlens, B, T, H, dk, dv, n_seqs);
+    if (rc) return rc;
+    if (dv != 64 && dv != 128)
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_recurrent_fwd: dv=%lld (supported: 64, 128)", (long long)dv);
+    if (!aligned16(initial_state) || !aligned16(final_state))
+        return fail(VGDR_ERR_INVALID, "vgdr_recurrent_fwd: states must be 16-byte aligned");
+    vgdr::RecParams p{};
+    p.q = q; p.k = k; p.v = v;
+    p.g = gate_kind == VGDR_GATE_NONE ? nullptr : g;
+    p.beta = beta;
+    p.o = o;
+    p.h0 = initial_state;
+    p.ht = final_state;
+    p.cu = cu_seqlens;
+    p.T = T;
+    p.n_tokens = B * T;
+    p.H = (int)H;
+    p.n_seqs = (int)n_seqs;
+    p.use_delta = use_delta ? 1 : 0;
+    p.scale = scale;
+    return hip_status(vgdr::recurrent_fwd(dtype, (int)dk, (int)dv, gate_kind == VGDR_GATE_VECTOR, p, stream),
+                      "vgdr_recurrent_fwd launch");
+}
+
+int64_t vgdr_varlen_workspace_size(int64_t n_seqs) {
+    return n_seqs < 0 ? 0 : (4 * n_seqs + 1) * (int64_t)sizeof(int32_t);
+}
+
+int vgdr_varlen_prepare(const int32_t *cu_seqlens, int64_t n_seqs, int64_t n_tokens, int chunk_size,
+                        void *workspace, hipStream_t stream) {
+    g_err[0] = 0;
+    if (n_seqs < 0 || n_seqs > 0x7fffffffLL || n_tokens < 0)
+        return fail(VGDR_ERR_INVALID, "vgdr_varlen_prepare: bad sizes");
+    if (n_seqs > 0 && (!cu_seqlens || !workspace))
+        return fail(VGDR_ERR_INVALID, "vgdr_varlen_prepare: cu_seqlens and workspace are required");
+    if (chunk_size <= 0) return fail(VGDR_ERR_INVALID, "vgdr_varlen_prepare: chunk_size must be positive");
+    return hip_status(vgdr::varlen_prepare(cu_seqlens, (int)n_seqs, n_tokens, chunk_size,
+                                           reinterpret_cast<int32_t *>(workspace), stream),
+                      "vgdr_varlen_prepare launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+// Kernel parameter blocks and launcher declarations shared by the C ABI
+// (gdr_api.hip) and the kernel translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace vgdr {
+
+struct ChunkParams {
+    const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
+    const float *g;               // [n_tokens, H] or [n_tokens, H, dk]; NULL = no gate
+    const float *beta;            // [n_tokens, H]; unused without the delta rule
+    void *o;                      // [n_tokens, H, dv]
+    const float *h0;              // [n_seqs, H, dk, dv] or NULL
+    float *ht;                    // [n_seqs, H, dk, dv] or NULL
+    const int32_t *cu;            // [n_seqs + 1] or NULL (dense)
+    const int32_t *order;         // schedule: position -> sequence, or NULL (identity)
+    int64_t T;                    // tokens per sequence (dense batch)
+    int64_t n_tokens;             // total tokens (clamp bound for cu)
+    int H, DV, n_seqs, n_tiles;
+    int use_delta;
+    float scale;
+};
+
+struct RecParams {
+    const void *q, *k, *v;
+    const float *g;
+    const float *beta;
+    void *o;
+    const float *h0;
+    float *ht;
+    const int32_t *cu;
+    int64_t T;
+    int64_t n_tokens;
+    int H, n_seqs;
+    int use_delta;
+    float scale;
+};
+
+// dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.
+hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, const ChunkParams &p,
+                     hipStream_t stream);
+int chunk_tile_cols();
+
+hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
+                         hipStream_t stream);
+
+hipError_t varlen_prepare(const int32_t *cu, int n_seqs, int64_t n_tokens, int chunk,
+                          int32_t *ws, hipStream_t stream);
+
+}  // namespace vgdr

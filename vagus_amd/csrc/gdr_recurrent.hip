@@ -1,0 +1,228 @@
+// Token-by-token gated delta rule (the decode step at T = 1) for gfx950.
+//
+// One workgroup of 256 threads owns one (sequence, head) and keeps the whole
+// fp32 state S[DK][DV] in registers for the length of its token range.  Thread
+// (row group rg, column group cg) holds rows rg + NRG*i (i < RPT) of the four
+// columns 4cg..4cg+3, so each state load / store is one coalesced 16-byte
+// access and a wavefront covers whole contiguous rows.  Per token
+// (linear_attention.py:176-193):
+//     S' = Diag(a) S                                  (a = exp(g): scalar or per row)
+//     kS = k^T S',  qS = q^T S',  qk = q . k          one pass, one reduction
+//     u  = beta (v - kS)   (v without the delta rule)
+//     o  = scale (qS + qk u)                          = scale q^T (S' + k u^T)
+//     S  = S' + k u^T
+// so S is read once and written once per call regardless of T.
+#include "gdr_common.hpp"
+#include "gdr_kernels.hpp"
+
+namespace vgdr {
+
+template <int DK, int DV, typename E, int GATE>
+__global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
+    constexpr int NT = 256;
+    constexpr int NCG = DV / 4;             // column groups (float4 each)
+    constexpr int NRG = NT / NCG;           // row groups
+    constexpr int RPT = DK / NRG;           // rows per thread
+    constexpr int NWV = NT / 64;
+    static_assert(NT % NCG == 0 && DK % NRG == 0 && 64 % NCG == 0, "thread layout");
+    using EL = Elem<E>;
+
+    __shared__ __attribute__((aligned(16))) float qs[DK];
+    __shared__ __attribute__((aligned(16))) float ks[DK];
+    __shared__ __attribute__((aligned(16))) float vs[DV];
+    __shared__ __attribute__((aligned(16))) float gv[GATE == 2 ? DK : 1];
+    __shared__ __attribute__((aligned(16))) float red[NWV][2][DV];
+    __shared__ float redqk[NWV];
+    __shared__ float sc[2];                 // decay (scalar gate), beta
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cg = tid % NCG, rg = tid / NCG;
+    const int h = blockIdx.x % p.H;
+    const int seq = blockIdx.x / p.H;
+    int64_t bos, eos;
+    if (p.cu) {
+        int64_t a = p.cu[seq], b = p.cu[seq + 1];
+        a = a < 0 ? 0 : (a > p.n_tokens ? p.n_tokens : a);
+        b = b < a ? a : (b > p.n_tokens ? p.n_tokens : b);
+        bos = a;
+        eos = b;
+    } else {
+        bos = (int64_t)seq * p.T;
+        eos = bos + p.T;
+    }
+    const E *qg = reinterpret_cast<const E *>(p.q);
+    const E *kg = reinterpret_cast<const E *>(p.k);
+    const E *vg = reinterpret_cast<const E *>(p.v);
+    E *og = reinterpret_cast<E *>(p.o);
+    const int H = p.H;
+
+    const int64_t sbase = ((int64_t)seq * H + h) * DK * DV;
+    f32x4 S[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i)
+        S[i] = p.h0 ? ld4(p.h0 + sbase + (int64_t)(rg + NRG * i) * DV + 4 * cg) : f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t t = bos; t < eos; ++t) {
+        // token operands -> LDS (fp32)
+        const int64_t qo = (t * H + h) * DK, vo = (t * H + h) * DV;
+        for (int i = tid; i < DK; i += NT) {
+            qs[i] = EL::to_f(qg[qo + i]) * p.scale;
+            ks[i] = EL::to_f(kg[qo + i]);
+            if constexpr (GATE == 2) gv[i] = __expf(p.g[qo + i]);
+        }
+        for (int i = tid; i < DV; i += NT) vs[i] = EL::to_f(vg[vo + i]);
+        if (tid == 0) {
+            sc[0] = (GATE == 1 && p.g) ? __expf(p.g[t * H + h]) : 1.f;
+            sc[1] = p.use_delta ? p.beta[t * H + h] : 0.f;
+        }
+        __syncthreads();
+
+        f32x4 kS = {0.f, 0.f, 0.f, 0.f}, qS = {0.f, 0.f, 0.f, 0.f};
+        float qk = 0.f;
+        const float a0 = sc[0];
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const int r = rg + NRG * i;
+            const float a = (GATE == 2) ? gv[r] : a0;
+            S[i] *= a;
+            kS += ks[r] * S[i];
+            qS += qs[r] * S[i];
+            qk += qs[r] * ks[r];
+        }
+        // reduce over the row groups of this wave (lanes NCG apart share columns)
+#pragma unroll
+        for (int off = NCG; off < 64; off <<= 1) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                kS[e] += __shfl_xor(kS[e], off);
+                qS[e] += __shfl_xor(qS[e], off);
+            }
+            qk += __shfl_xor(qk, off);
+        }
+        if (lane < NCG) {
+            st4(&red[wave][0][4 * cg], kS);
+            st4(&red[wave][1][4 * cg], qS);
+        }
+        if (lane == 0) redqk[wave] = qk;
+        __syncthreads();
+        kS = ld4(&red[0][0][4 * cg]);
+        qS = ld4(&red[0][1][4 * cg]);
+        qk = redqk[0];
+#pragma unroll
+        for (int w = 1; w < NWV; ++w) {
+            kS += ld4(&red[w][0][4 * cg]);
+            qS += ld4(&red[w][1][4 * cg]);
+            qk += redqk[w];
+        }
+        const f32x4 v4 = ld4(&vs[4 * cg]);
+        const f32x4 u = p.use_delta ? sc[1] * (v4 - kS) : v4;
+        const f32x4 o = qS + qk * u;                     // q was pre-scaled
+        if (rg == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) og[vo + 4 * cg + e] = EL::from_f(o[e]);
+        }
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) S[i] += ks[rg + NRG * i] * u;
+        __syncthreads();                                 // LDS reused by the next token
+    }
+
+    if (p.ht) {
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) st4(p.ht + sbase + (int64_t)(rg + NRG * i) * DV + 4 * cg, S[i]);
+    }
+}
+
+template <int DK, int DV, typename E, int GATE>
+static hipError_t launch_rec(const RecParams &p, hipStream_t stream) {
+    const int64_t blocks = (int64_t)p.n_seqs * p.H;
+    if (blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL((recurrent_kernel<DK, DV, E, GATE>), dim3((unsigned)blocks), dim3(256), 0,
+                       stream, p);
+    return hipGetLastError();
+}
+
+template <int DK, int DV, typename E>
+static hipError_t rec_gate(int gate_vector, const RecParams &p, hipStream_t s) {
+    return gate_vector ? launch_rec<DK, DV, E, 2>(p, s) : launch_rec<DK, DV, E, 1>(p, s);
+}
+
+template <typename E>
+static hipError_t rec_shape(int dk, int dv, int gate_vector, const RecParams &p, hipStream_t s) {
+    if (dk == 64) return dv == 64 ? rec_gate<64, 64, E>(gate_vector, p, s) : rec_gate<64, 128, E>(gate_vector, p, s);
+    return dv == 64 ? rec_gate<128, 64, E>(gate_vector, p, s) : rec_gate<128, 128, E>(gate_vector, p, s);
+}
+
+hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
+                         hipStream_t stream) {
+    if (dtype == 1) return rec_shape<__bf16>(dk, dv, gate_vector, p, stream);
+    if (dtype == 2) return rec_shape<_Float16>(dk, dv, gate_vector, p, stream);
+    return rec_shape<float>(dk, dv, gate_vector, p, stream);
+}
+
+// ---------------------------------------------------------------------------
+// packed-batch schedule: lens, chunk counts, chunk offsets, longest-first order
+// ---------------------------------------------------------------------------
+__device__ inline int64_t seg_len(const int32_t *cu, int n, int64_t n_tokens) {
+    int64_t a = cu[n], b = cu[n + 1];
+    a = a < 0 ? 0 : (a > n_tokens ? n_tokens : a);
+    b = b < a ? a : (b > n_tokens ? n_tokens : b);
+    return b - a;
+}
+
+__global__ void __launch_bounds__(256) varlen_rank_kernel(const int32_t *cu, int n_seqs, int64_t n_tokens,
+                                                          int chunk, int32_t *ws, int sort) {
+    const int s = blockIdx.x * 256 + threadIdx.x;
+    if (s >= n_seqs) return;
+    int32_t *lens = ws, *chunks = ws + n_seqs, *order = ws + 3 * n_seqs + 1;
+    const int64_t L = seg_len(cu, s, n_tokens);
+    lens[s] = (int32_t)L;
+    chunks[s] = (int32_t)((L + chunk - 1) / chunk);
+    if (!sort) {
+        order[s] = s;
+        return;
+    }
+    int rank = 0;
+    for (int t = 0; t < n_seqs; ++t) {
+        const int64_t Lt = seg_len(cu, t, n_tokens);
+        rank += (Lt > L) || (Lt == L && t < s);
+    }
+    order[rank] = s;
+}
+
+// exclusive prefix sum of chunks -> chunk_offsets[0..n_seqs], one workgroup
+__global__ void __launch_bounds__(1024) varlen_offsets_kernel(int n_seqs, int32_t *ws) {
+    __shared__ int64_t part[1024];
+    const int32_t *chunks = ws + n_seqs;
+    int32_t *offs = ws + 2 * n_seqs;
+    const int tid = threadIdx.x;
+    const int per = (n_seqs + 1023) / 1024;
+    const int lo = tid * per, hi = lo + per < n_seqs ? lo + per : n_seqs;
+    int64_t sum = 0;
+    for (int i = lo; i < hi; ++i) sum += chunks[i];
+    part[tid] = sum;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {        // Hillis-Steele inclusive scan
+        const int64_t x = tid >= off ? part[tid - off] : 0;
+        __syncthreads();
+        part[tid] += x;
+        __syncthreads();
+    }
+    int64_t run = tid ? part[tid - 1] : 0;
+    for (int i = lo; i < hi; ++i) {
+        offs[i] = (int32_t)run;
+        run += chunks[i];
+    }
+    if (tid == 1023) offs[n_seqs] = (int32_t)part[1023];
+}
+
+hipError_t varlen_prepare(const int32_t *cu, int n_seqs, int64_t n_tokens, int chunk, int32_t *ws,
+                          hipStream_t stream) {
+    if (n_seqs <= 0) return hipSuccess;
+    const int sort = n_seqs <= 16384;                 // O(n^2) ranking; beyond that index order
+    hipLaunchKernelGGL(varlen_rank_kernel, dim3((n_seqs + 255) / 256), dim3(256), 0, stream, cu, n_seqs,
+                       n_tokens, chunk, ws, sort);
+    hipLaunchKernelGGL(varlen_offsets_kernel, dim3(1), dim3(1024), 0, stream, n_seqs, ws);
+    return hipGetLastError();
+}
+
+}  // namespace vgdr
