@@ -1,0 +1,230 @@
+#!/usr/bin/env python
+"""Benchmark of the gated delta-rule core on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Headline (the JSON line's `value`): chunked GDN prefill of the 340M layer
+shape, B=8 T=4096 H=8 dk=dv=128, chunk 64, bf16 q/k/v, fp32 gates / beta /
+states (entry state 0.1 N(0,1)); a step is one `chunk_gated_delta_rule` call
+over the whole batch with its inputs resident in HBM; value = tokens/s
+(B*T tokens per step).  Three copies of the inputs (3 x 218 MB) are rotated
+so that no step finds its operands in the 256 MB Infinity Cache.
+
+Also reported on the same line:
+  roofline      the prefill kernel's achieved algorithmic TFLOP/s (180,224 FLOP
+                per token-head, the forward third of chunk_scan_flops) over bf16
+                dense MFMA peak, from HIP events around each launch on the
+                kernel's stream; `traffic` = measured HBM bytes per launch
+                (rocprofv3 FETCH_SIZE + WRITE_SIZE, see profiles/) when present
+  decode        one recurrent decode step at the 1.3B layer shape (B=64 H=16
+                dk=dv=128) rotating 24 layer states (1.5 GB), in algorithmic
+                GB/s (132,104 B per sequence-head) over 8 TB/s
+  kda, varlen   KDA prefill (B=4 T=8192 H=8) and packed GDN prefill (32
+                segments U[128, 8192], H=16) tokens/s and TFLOP/s
+  cpu_baseline  the oracle's torch fp32 chunk form (the reference's CPU path)
+                over the full headline workload on the host cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0          # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0              # MI355X HBM3E
+FLOP_PER_TOKEN_HEAD = 180224       # chunk_scan_flops(128, 128, 64, True) / 3
+PREFILL_BYTES_PER_TOKEN_HEAD = 1032
+DECODE_BYTES_PER_SEQ_HEAD = 132104
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def time_steps(torch, fn, steps, warmup, rotate):
+    """Run `warmup` untimed steps, then exactly `steps` timed steps; returns
+    (total seconds by host clock around synchronize, per-step event ms list)."""
+    for i in range(warmup):
+        fn(i % rotate)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        fn(i % rotate)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return t1 - t0, [a.elapsed_time(b) for a, b in ev]
+
+
+def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
+    xs = [workloads.workload(name, device='cuda') for _ in range(copies)]
+    kda = xs[0].g is not None and xs[0].g.dim() == 4
+    fn_op = ops.chunk_kda if kda else ops.chunk_gated_delta_rule
+
+    def step(i):
+        x = xs[i]
+        fn_op(x.q, x.k, x.v, x.g, x.beta, initial_state=x.initial_state, output_final_state=True,
+              cu_seqlens=x.cu_seqlens)
+
+    total, ms = time_steps(torch, step, steps, warmup, copies)
+    tokens = xs[0].q.shape[0] * xs[0].q.shape[1]
+    H = xs[0].q.shape[2]
+    avg_ms = statistics.mean(ms)
+    del xs
+    return dict(tokens=tokens, H=H, total_s=total, step_ms=ms, avg_ms=avg_ms,
+                tok_s=steps * tokens / total,
+                tflops=tokens * H * FLOP_PER_TOKEN_HEAD / (avg_ms * 1e-3) / 1e12)
+
+
+def bench_decode(torch, ops, workloads, steps, warmup, B=64, H=16, layers=24):
+    states = [torch.randn(B, H, 128, 128, device='cuda') for _ in range(layers)]
+    x = workloads.make_inputs(B, 1, H, 128, 128, gate='scalar', dtype=torch.bfloat16, seed=4, device='cuda')
+
+    def step(i):
+        ops.fused_recurrent_gated_delta_rule(x.q, x.k, x.v, x.g, x.beta, initial_state=states[i],
+                                             inplace_final_state=True)
+
+    total, ms = time_steps(torch, step, max(steps, layers), max(warmup, layers), layers)
+    avg_ms = statistics.mean(ms)
+    byts = B * H * DECODE_BYTES_PER_SEQ_HEAD
+    del states
+    return dict(avg_us=avg_ms * 1e3, GBs=byts / (avg_ms * 1e-3) / 1e9, bytes=byts)
+
+
+def cpu_baseline(torch, workloads):
+    """The oracle's torch fp32 chunk form over the full headline workload."""
+    from oracle import gdr
+    cores = min(len(os.sched_getaffinity(0)), int(os.environ.get('OMP_NUM_THREADS', '1024')))
+    torch.set_num_threads(cores)
+    x = workloads.workload('gdn_340m')
+    q, k, v = x.q.float(), x.k.float(), x.v.float()
+
+    def run():
+        gdr.chunk_scalar(q, k, v, x.g, x.beta, x.initial_state, scale=128 ** -0.5, chunk_size=64)
+
+    run()                                              # warmup
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    med = statistics.median(ts)
+    tokens = q.shape[0] * q.shape[1]
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open('/proc/cpuinfo') as f:
+            cpu = next(l.split(':', 1)[1].strip() for l in f if l.startswith('model name'))
+    except Exception:
+        pass
+    return {'value': round(tokens / med, 1), 'unit': 'tok/s', 'cores': cores, 'kind': 'port',
+            'sample': f'full gdn_340m workload (B8 T4096 H8 dk=dv=128, chunk 64), oracle.gdr.chunk_scalar '
+                      f'in fp32, median of 3 after 1 warmup, {med:.2f} s per run, {cpu}'}
+
+
+def measured_traffic(workload):
+    """HBM bytes per launch of the prefill kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json), if one exists."""
+    path = os.path.join(ROOT, 'profiles', 'traffic.json')
+    try:
+        with open(path) as f:
+            rec = json.load(f).get(workload)
+        return None if rec is None else int(rec['bytes_per_launch'])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=30)
+    ap.add_argument('--warmup', type=int, default=6)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--prefill-only', action='store_true', help='only the headline prefill (for profiling)')
+    ap.add_argument('--calibrate-copy', action='store_true',
+                    help='run only a plain 1 GiB device copy (x5): the reference point that scales '
+                         'rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes')
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f'bench.py: this build measures one GPU only (the gated delta-rule core has no '
+              f'cross-GPU path here); --gpus {args.gpus} is not supported', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from vagus_amd import ops, workloads
+
+    assert torch.cuda.is_available(), 'bench.py needs a GPU'
+    torch.backends.cuda.matmul.allow_tf32 = False
+    if args.calibrate_copy:
+        src = torch.ones(1 << 28, dtype=torch.float32, device='cuda')      # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({'calibrate_copy_bytes': src.numel() * 4, 'launches': 5}), flush=True)
+        return
+
+    log('[bench] prefill gdn_340m')
+    pre = bench_prefill(torch, ops, workloads, 'gdn_340m', args.steps, args.warmup)
+    extra = {}
+    if not args.prefill_only:
+        log('[bench] decode 1.3B layer shape')
+        dec = bench_decode(torch, ops, workloads, args.steps, args.warmup)
+        extra['decode'] = {'workload': 'gdn decode step B64 H16 dk=dv=128, 24 rotating layer states',
+                           'us_per_step': round(dec['avg_us'], 2), 'achieved_GBs': round(dec['GBs'], 1),
+                           'peak_GBs': PEAK_HBM_GBS, 'frac': round(dec['GBs'] / PEAK_HBM_GBS, 4),
+                           'bytes_per_step': dec['bytes']}
+        for name in ('kda_prefill', 'gdn_varlen'):
+            log(f'[bench] prefill {name}')
+            r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))
+            extra[name] = {'tok_s': round(r['tok_s'], 1), 'ms_per_step': round(r['avg_ms'], 4),
+                           'tflops': round(r['tflops'], 2),
+                           'frac_mfma': round(r['tflops'] / PEAK_BF16_TFLOPS, 5), 'tokens': r['tokens']}
+    cpu = None
+    if not args.no_cpu_baseline:
+        log('[bench] cpu baseline')
+        cpu = cpu_baseline(torch, workloads)
+
+    tokens, H = pre['tokens'], pre['H']
+    achieved = pre['tflops']
+    hbm_gbs = tokens * H * PREFILL_BYTES_PER_TOKEN_HEAD / (pre['avg_ms'] * 1e-3) / 1e9
+    line = {
+        'metric': 'prefill tok/s + MFMA util; decode-step HBM GB/s vs peak (GDN/KDA, 1 GPU)',
+        'value': round(pre['tok_s'], 1),
+        'unit': 'tok/s',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(pre['total_s'] * 1e3 / args.steps, 4),
+        'higher_is_better': True,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'bf16',
+        'data': 'synthetic (seeded; q,k L2-normalised N(0,1), v N(0,1), beta sigmoid(N), g logsigmoid(N+4))',
+        'config': {'workload': 'gdn_340m: GDN chunked prefill, 340M layer shape', 'B': 8, 'T': 4096,
+                   'H': 8, 'dk': 128, 'dv': 128, 'chunk': 64, 'initial_state': '0.1*N(0,1)',
+                   'tokens_per_step': tokens},
+        'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS,
+                     'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_BF16_TFLOPS, 5),
+                     'traffic': measured_traffic('gdn_340m'),
+                     'kernel_avg_ms': round(pre['avg_ms'], 4),
+                     'hbm_algorithmic_GBs': round(hbm_gbs, 1)},
+        'cpu_baseline': cpu,
+        **extra,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()
