@@ -70,19 +70,24 @@ const char *vgdr_last_error(void);
  * as called at linear_attention.py:474-497, with the reference's WY chunk
  * semantics (chunk_scan :237-309, chunk_scan_vec :312-425).
  *
- * chunk_size is accepted for interface parity: 64 and 32 select the kernel's
- * chunk length; the result is chunk-size invariant up to rounding.
- * Supported: dk in {64, 128}, dv a multiple of 16 (any count of 64-column
- * tiles).  `workspace` must be NULL for a dense batch; for a packed batch it
- * may point to vgdr_varlen_workspace_size(n_seqs) bytes prepared by
- * vgdr_varlen_prepare (it then holds the longest-first schedule), or be NULL
- * (segments are scheduled in index order).
+ * chunk_size is accepted for interface parity: values <= 32 select 32-token
+ * chunks, larger ones 64 (fp32 always uses 32); the result is
+ * chunk-size invariant up to rounding.  Supported: dk in {64, 128}, dv a
+ * positive multiple of 16.
+ *
+ * The caller provides `workspace` (16-byte aligned device memory of at least
+ * vgdr_chunk_workspace_size(...) bytes, contents irrelevant): it holds the
+ * per-chunk intermediate products and, for a packed batch, the segment table
+ * (see vgdr_varlen_prepare).  Calls sharing one workspace must not overlap.
  */
+int64_t vgdr_chunk_workspace_size(int dtype, int64_t B, int64_t T, int64_t H, int64_t dk,
+                                  int64_t n_seqs, int varlen, int chunk_size);
+
 int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta,
                    const void *q, const void *k, const void *v,
                    const float *g, const float *beta,
                    void *o, const float *initial_state, float *final_state,
-                   const int32_t *cu_seqlens, const void *workspace,
+                   const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
                    int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
                    float scale, int chunk_size, hipStream_t stream);
 

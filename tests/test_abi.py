@@ -39,11 +39,12 @@ def test_library_loads_and_exports_every_symbol():
 
 def _chunk_call(**over):
     a = dict(dtype=1, gate=1, delta=1, q=None, k=None, v=None, g=None, beta=None, o=None, h0=None,
-             ht=None, cu=None, ws=None, B=2, T=0, H=4, dk=128, dv=128, N=2, scale=1.0, chunk=64)
+             ht=None, cu=None, ws=None, nbytes=0, B=2, T=0, H=4, dk=128, dv=128, N=2, scale=1.0, chunk=64)
     a.update(over)
     return _lib.load().vgdr_chunk_fwd(a['dtype'], a['gate'], a['delta'], a['q'], a['k'], a['v'], a['g'],
-                                      a['beta'], a['o'], a['h0'], a['ht'], a['cu'], a['ws'], a['B'], a['T'],
-                                      a['H'], a['dk'], a['dv'], a['N'], a['scale'], a['chunk'], None)
+                                      a['beta'], a['o'], a['h0'], a['ht'], a['cu'], a['ws'], a['nbytes'],
+                                      a['B'], a['T'], a['H'], a['dk'], a['dv'], a['N'], a['scale'],
+                                      a['chunk'], None)
 
 
 def test_argument_checks_return_status_codes():
@@ -59,6 +60,15 @@ def test_argument_checks_return_status_codes():
     assert _chunk_call(T=4, q=16, k=32, v=48, o=64, g=None) == _lib.VGDR_ERR_INVALID  # gate needs g
     assert _chunk_call(T=4, q=16, k=32, v=48, o=64, g=80, beta=None) == _lib.VGDR_ERR_INVALID
     assert _chunk_call(T=4, q=17, k=32, v=48, o=64, g=80, beta=96) == _lib.VGDR_ERR_INVALID  # alignment
+    # the workspace must be present and large enough
+    need = L.vgdr_chunk_workspace_size(1, 2, 64, 4, 128, 2, 0, 64)
+    assert need == 2 * 1 * 4 * 2 * 64 * 64 * 2
+    assert _chunk_call(T=64, q=16, k=32, v=48, o=64, g=80, beta=96, ws=None) == _lib.VGDR_ERR_INVALID
+    assert _chunk_call(T=64, q=16, k=32, v=48, o=64, g=80, beta=96, ws=4096, nbytes=need - 1) == _lib.VGDR_ERR_INVALID
+    assert b'workspace' in L.vgdr_last_error()
+    # fp32 with 128-wide keys runs 32-token chunks; packed batches add the segment table
+    assert L.vgdr_chunk_workspace_size(0, 1, 64, 1, 128, 1, 0, 64) == 2 * 1 * 2 * 32 * 32 * 4
+    assert L.vgdr_chunk_workspace_size(1, 1, 100, 2, 64, 3, 1, 64) == 256 + (2 + 3) * 2 * 2 * 64 * 64 * 2
     rc = L.vgdr_recurrent_fwd(1, 1, 1, None, None, None, None, None, None, None, None, None,
                               1, 0, 4, 128, 256, 1, 1.0, None)
     assert rc == _lib.VGDR_ERR_UNSUPPORTED

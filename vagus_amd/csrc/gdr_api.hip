@@ -61,7 +61,50 @@ int check_common(const char *fn, int dtype, int gate_kind, int use_delta, const 
     return VGDR_OK;
 }
 
+// chunk length the kernels use: 32 when asked for <= 32, else 64; fp32 always
+// uses 32 (its double-buffered 64-token tiles overflow LDS)
+int effective_chunk(int dtype, int64_t dk, int chunk_size) {
+    (void)dk;
+    if (dtype == VGDR_F32) return 32;
+    return chunk_size <= 32 ? 32 : 64;
+}
+
+struct ChunkWs {
+    int64_t slots;        // chunk slots of the prep kernel (an upper bound on chunks)
+    int64_t blocks_off;   // byte offset of the per-(chunk, head) TE / A blocks
+    int64_t total;        // bytes
+};
+
+ChunkWs chunk_layout(int dtype, int chunk, int64_t B, int64_t T, int64_t H, int64_t n_seqs, bool varlen) {
+    ChunkWs w{};
+    if (varlen) {
+        w.slots = (B * T + chunk - 1) / chunk + n_seqs;     // each segment adds at most one partial chunk
+        w.blocks_off = ((4 * n_seqs + 1) * 4 + 255) / 256 * 256;
+    } else {
+        w.slots = B * ((T + chunk - 1) / chunk);
+        w.blocks_off = 0;
+    }
+    w.total = w.blocks_off + vgdr::chunk_blocks_bytes(dtype, chunk, w.slots, H);
+    if (w.slots == 0) w.total = varlen ? w.blocks_off : 0;
+    return w;
+}
+
 }  // namespace
+
+namespace vgdr {
+int device_cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+}  // namespace vgdr
 
 extern "C" {
 
@@ -69,10 +112,17 @@ int vgdr_version(void) { return 100; }
 
 const char *vgdr_last_error(void) { return g_err; }
 
+int64_t vgdr_chunk_workspace_size(int dtype, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t n_seqs,
+                                   int varlen, int chunk_size) {
+    if (B < 0 || T < 0 || H <= 0 || n_seqs < 0) return 0;
+    const int chunk = effective_chunk(dtype, dk, chunk_size);
+    return chunk_layout(dtype, chunk, B, T, H, n_seqs, varlen).total;
+}
+
 int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
                    const float *g, const float *beta, void *o, const float *initial_state,
-                   float *final_state, const int32_t *cu_seqlens, const void *workspace, int64_t B,
-                   int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
+                   float *final_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                   int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
                    int chunk_size, hipStream_t stream) {
     g_err[0] = 0;
     int rc = check_common("vgdr_chunk_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o, cu_seqlens,
@@ -82,30 +132,34 @@ int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta, const void *q, const
         return fail(VGDR_ERR_UNSUPPORTED, "vgdr_chunk_fwd: dv=%lld (must be a positive multiple of 16)",
                     (long long)dv);
     if (!aligned16(o)) return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: o must be 16-byte aligned");
-    if (workspace && !cu_seqlens)
-        return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: a workspace is only used with cu_seqlens");
-    int chunk = chunk_size <= 32 ? 32 : 64;
-    if (dtype == VGDR_F32 && dk == 128) chunk = 32;   // the fp32 128-key tile needs the short chunk
+    const int chunk = effective_chunk(dtype, dk, chunk_size);
+    const ChunkWs ws = chunk_layout(dtype, chunk, B, T, H, n_seqs, cu_seqlens != nullptr);
+    if (ws.total > 0 && (!workspace || workspace_bytes < ws.total || !aligned16(workspace)))
+        return fail(VGDR_ERR_INVALID,
+                    "vgdr_chunk_fwd: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)",
+                    (long long)ws.total, (long long)workspace_bytes, workspace);
+    if (ws.slots * H > 0x7fffffffLL || (n_seqs * H + 7) / 8 * 8 * ((dv + 31) / 32) > 0x7fffffffLL)
+        return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: grid too large");
     vgdr::ChunkParams p{};
+    p.geo.cu = cu_seqlens;
+    p.geo.T = T;
+    p.geo.n_tokens = B * T;
+    p.geo.n_seqs = (int)n_seqs;
+    p.geo.chunks_per_seq = (int)((T + chunk - 1) / chunk);
     p.q = q; p.k = k; p.v = v;
     p.g = gate_kind == VGDR_GATE_NONE ? nullptr : g;
     p.beta = beta;
     p.o = o;
     p.h0 = initial_state;
     p.ht = final_state;
-    p.cu = cu_seqlens;
-    p.order = workspace ? reinterpret_cast<const int32_t *>(workspace) + 3 * n_seqs + 1 : nullptr;
-    p.T = T;
-    p.n_tokens = B * T;
+    p.blocks = static_cast<char *>(workspace) + ws.blocks_off;
     p.H = (int)H;
     p.DV = (int)dv;
-    p.n_seqs = (int)n_seqs;
-    p.n_tiles = (int)((dv + vgdr::chunk_tile_cols() - 1) / vgdr::chunk_tile_cols());
+    p.n_chunk_slots = (int)ws.slots;
     p.use_delta = use_delta ? 1 : 0;
     p.scale = scale;
-    if ((int64_t)p.n_seqs * p.H * p.n_tiles > 0x7fffffffLL)
-        return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: grid too large");
-    return hip_status(vgdr::chunk_fwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, p, stream),
+    int32_t *table = cu_seqlens ? static_cast<int32_t *>(workspace) : nullptr;
+    return hip_status(vgdr::chunk_fwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, p, table, stream),
                       "vgdr_chunk_fwd launch");
 }
 

@@ -1,524 +1,836 @@
-// Fused chunkwise prefill of the gated delta rule (GDN scalar gate, KDA
-// per-channel gate, optional delta rule) for gfx950.
+// Chunkwise prefill of the gated delta rule (GDN scalar gate, KDA
+// per-channel gate, optional delta rule) for gfx950, as two kernels.
 //
-// One workgroup owns one (sequence, head, 16*NW-column dv tile) and walks the
-// sequence chunk by chunk.  Wave w owns the 16 dv columns [16w, 16w+16) of the
-// tile and keeps their fp32 state S[0:DK, cols] in MFMA accumulators (C
-// layout, DK/16 tiles) for the whole sequence: the state chain
-//     U~ = U - W S,   o = (Q*G) S + A U~,   S <- Gc (.) S + (K*Gend)^T U~
-// runs register-to-register, with no LDS round trip and no barrier.
-// The chunk-local, state-independent operands (K K^T and Q K^T gated and
-// masked, T = (I + M)^-1, W = T diag(beta) (K*G)) are built cooperatively in
-// LDS once per chunk.  Math: linear_attention.py:237-309 (scalar) and
-// :312-425 (per-channel gate), in its unified per-channel form
-//     M_ij = beta_i <k_i, k_j>_g (j < i),   A_ij = scale <q_i, k_j>_g (j <= i)
-//     T = (I + M)^-1,  W = T diag(beta) (K*G),  U = T diag(beta) V
-// where <x_i, y_j>_g = sum_c x_i[c] y_j[c] exp(gamma_i[c] - gamma_j[c]) and
-// gamma is the in-chunk cumulative log decay (a scalar per token for GDN).
+// Math (linear_attention.py:237-309 scalar, :312-425 per channel), in the
+// unified per-channel form.  Per chunk of CH tokens with cumulative log decay
+// gamma (a scalar per token for GDN, a DK-vector for KDA), G_i = exp(gamma_i),
+// Gend_i = exp(gamma_C - gamma_i), Gc = exp(gamma_C):
+//     M_ij = beta_i <k_i, k_j>_g   (j < i)         A_ij = scale <q_i, k_j>_g   (j <= i)
+//     TE   = (I + M)^-1 diag(beta)
+//     X    = V - (K*G) S                           (the WY form's U - W S, refactored:
+//     U~   = TE X                                   W = TE (K*G), U = TE V)
+//     o    = scale (Q*G) S + A U~
+//     S   <- Gc (.) S + (K*Gend)^T U~
+// with <x_i, y_j>_g = sum_c x_i[c] y_j[c] exp(gamma_i[c] - gamma_j[c]).
 //
-// Per-channel gates reach the MFMA through a sub-block factorisation:
-// for token blocks I >= J of 16 and reference row r = 16 I,
-//     exp(gamma_i - gamma_j) = exp(gamma_i - gamma_r) * exp(gamma_r - gamma_j)
+// chunk_prep_kernel  (one workgroup per (chunk, head); no dependence between
+//     chunks, so the whole batch runs in parallel at high occupancy) builds the
+//     state-independent TE and A of every chunk and stores them in MFMA
+//     fragment order (see frag_pos).
+// chunk_state_kernel (one workgroup per (sequence, head, 16*NW-column dv
+//     tile)) walks the chunks in order.  Wave w owns 16 state columns and keeps
+//     them in fp32 MFMA accumulators (C layout) for the whole sequence; the
+//     products above run register-to-register.  The next chunk's operands
+//     (K, Q, V rows, TE and A) are copied global -> LDS asynchronously into the
+//     other half of a double buffer while the current chunk computes.
+//
+// Per-channel gates reach the MFMA through a sub-block factorisation: for
+// token blocks I >= J of 16 and reference row r = 16 I,
+//     exp(gamma_i - gamma_j) = exp(gamma_i - gamma_r) * exp(gamma_r - gamma_j).
 // Off-diagonal blocks (j < r <= i) have both exponents <= 0.  A diagonal
 // block's second factor is >= 1, bounded by the block's own decay range; a
 // block whose range exceeds Elem<E>::gate_range nats takes an exact pairwise
-// path instead (never forming an overflowing exponential).
+// path instead, so no overflowing exponential is ever formed.
 #include "gdr_common.hpp"
 #include "gdr_kernels.hpp"
 
 namespace vgdr {
 
-template <int DK, int CH, int NW, typename E, int GATE>
-struct ChunkLayout {
-    static constexpr int NT = 64 * NW;                // threads
-    static constexpr int DVT = 16 * NW;               // dv columns per workgroup
-    static constexpr int NB = CH / 16;                // token blocks per chunk
-    static constexpr int NKB = DK / 16;               // key blocks
-    static constexpr int PK = DK + Elem<E>::pad;      // pitch of [CH][DK] E arrays
-    static constexpr int PC = CH + Elem<E>::pad;      // pitch of [*][CH] E arrays
-    static constexpr int PV = DVT + Elem<E>::pad;     // pitch of the staged V rows
-    static constexpr int PF = CH + 4;                 // pitch of [CH][CH] fp32 arrays
-    static constexpr int PG = DK + 4;                 // pitch of the per-channel gamma table
-    static constexpr int ES = sizeof(E);
-
-    static constexpr int szKs = CH * PK * ES;
-    static constexpr int szKsT = DK * PC * ES;
-    static constexpr int szVsT = DVT * PC * ES;
-    static constexpr int szAqk = CH * PC * ES;
-    static constexpr int szMW = cmax(CH * PF * 4, CH * PK * ES);              // M, then W
-    static constexpr int szT = CH * PF * 4;
-    static constexpr int szTT = cmax(cmax(CH * PF * 4, CH * PC * ES), CH * PV * ES);  // V rows, TT, then TE
-    static constexpr int szGam = (GATE == 2 ? CH * PG : CH) * 4;
-
-    static constexpr int oKs = 0;
-    static constexpr int oQs = oKs + szKs;
-    static constexpr int oKsT = oQs + szKs;
-    static constexpr int oVsT = oKsT + szKsT;
-    static constexpr int oAqk = oVsT + szVsT;
-    static constexpr int oMW = oAqk + szAqk;
-    static constexpr int oT = oMW + szMW;
-    static constexpr int oTT = oT + szT;
-    static constexpr int oGam = oTT + szTT;
-    static constexpr int oBeta = oGam + szGam;
-    static constexpr int oG = oBeta + CH * 4;         // scalar gate: G_i = exp(gamma_i)
-    static constexpr int oGend = oG + CH * 4;         // scalar gate: exp(gamma_C - gamma_i)
-    static constexpr int oGc = oGend + CH * 4;        // exp(gamma_C): DK values (vector) / 1
-    static constexpr int oFlag = oGc + DK * 4;        // diag-block pairwise flags
-    static constexpr int BYTES = oFlag + 16;
-    static_assert(BYTES <= 160 * 1024, "LDS budget exceeded");
-    static_assert(oQs % 16 == 0 && oKsT % 16 == 0 && oVsT % 16 == 0 && oAqk % 16 == 0 &&
-                      oMW % 16 == 0 && oT % 16 == 0 && oTT % 16 == 0 && oGam % 16 == 0,
-                  "LDS arrays must stay 16-byte aligned");
-};
-
-// Copy rows [0, CH) x cols [0, NCOL) of a token-major global matrix into LDS
-// (row pitch P), zero-filling rows >= valid_rows and columns >= valid_cols.
-// Global row t starts at src + t * stride.  All loads are issued before any
-// store so their latencies overlap.
-template <typename E, int CH, int NCOL, int P, int NT>
-__device__ inline void load_rows(E *dst, const E *src, int64_t stride, int valid_rows,
-                                 int valid_cols, int tid) {
-    constexpr int VE = 16 / sizeof(E);                // elements per 16-byte vector
-    constexpr int VPR = NCOL / VE;                    // vectors per row
-    constexpr int NV = CH * VPR;
-    static_assert(NCOL % VE == 0 && NV % NT == 0, "tile does not split evenly");
-    constexpr int PER = NV / NT;
-    Vec16 r[PER];
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int vi = tid + i * NT;
-        const int row = vi / VPR, col = (vi % VPR) * VE;
-        if (row < valid_rows && col < valid_cols)
-            r[i] = *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + col);
-        else
-            r[i] = Vec16{{0u, 0u, 0u, 0u}};
-    }
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-        const int vi = tid + i * NT;
-        const int row = vi / VPR, col = (vi % VPR) * VE;
-        uint32_t *d = reinterpret_cast<uint32_t *>(dst + row * P + col);
-        // 8-byte stores: the padded pitch keeps rows 8- but not 16-byte aligned
-        reinterpret_cast<uint2 *>(d)[0] = uint2{r[i].w[0], r[i].w[1]};
-        reinterpret_cast<uint2 *>(d)[1] = uint2{r[i].w[2], r[i].w[3]};
-    }
+// fragment-order position of element (16 I + m, 16 kb + 4 g + j) of a CH x CH
+// tile block: lane 16 g + m of a wavefront reads its four elements of tile
+// (I, kb) as one contiguous vector, and a wavefront reads a whole tile as one
+// contiguous run of 64 * 4 elements.
+template <int NB>
+__device__ __forceinline__ int frag_pos(int I, int kb, int lane) {
+    return ((I * NB + kb) * 64 + lane) * 4;
 }
 
-template <int DK, int CH, int NW, typename E, int GATE>
-__global__ void __launch_bounds__(64 * NW, 1) chunk_fwd_kernel(const ChunkParams p) {
-    using L = ChunkLayout<DK, CH, NW, E, GATE>;
-    using EL = Elem<E>;
-    using F = typename EL::frag;
-    constexpr int NT = L::NT, NB = L::NB, NKB = L::NKB, DVT = L::DVT;
-    constexpr int PK = L::PK, PC = L::PC, PF = L::PF, PG = L::PG, PV = L::PV;
-
-    __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
-    E *Ks = reinterpret_cast<E *>(smem + L::oKs);
-    E *Qs = reinterpret_cast<E *>(smem + L::oQs);
-    E *KsT = reinterpret_cast<E *>(smem + L::oKsT);
-    E *VsT = reinterpret_cast<E *>(smem + L::oVsT);
-    E *Aqk = reinterpret_cast<E *>(smem + L::oAqk);
-    float *Mf = reinterpret_cast<float *>(smem + L::oMW);
-    E *Ws = reinterpret_cast<E *>(smem + L::oMW);
-    float *Tf = reinterpret_cast<float *>(smem + L::oT);
-    float *TTf = reinterpret_cast<float *>(smem + L::oTT);
-    E *TE = reinterpret_cast<E *>(smem + L::oTT);
-    E *Vrow = reinterpret_cast<E *>(smem + L::oTT);
-    float *gam = reinterpret_cast<float *>(smem + L::oGam);
-    float *bet = reinterpret_cast<float *>(smem + L::oBeta);
-    float *Gs = reinterpret_cast<float *>(smem + L::oG);
-    float *Gend = reinterpret_cast<float *>(smem + L::oGend);
-    float *Gc = reinterpret_cast<float *>(smem + L::oGc);
-    int *flag = reinterpret_cast<int *>(smem + L::oFlag);
-
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int g4 = lane >> 4, r16 = lane & 15;
-
-    // ---- work item --------------------------------------------------------
-    const int tile = blockIdx.x % p.n_tiles;
-    const int unit = blockIdx.x / p.n_tiles;
-    const int h = unit % p.H;
-    const int pos = unit / p.H;
-    const int seq = p.order ? p.order[pos] : pos;
-    int64_t bos, eos;
-    if (p.cu) {
-        int64_t a = p.cu[seq], b = p.cu[seq + 1];
-        a = a < 0 ? 0 : (a > p.n_tokens ? p.n_tokens : a);
-        b = b < a ? a : (b > p.n_tokens ? p.n_tokens : b);
+__device__ __forceinline__ void seq_bounds(const SeqGeom &g, int seq, int64_t &bos, int64_t &eos) {
+    if (g.cu) {
+        int64_t a = g.cu[seq], b = g.cu[seq + 1];
+        a = a < 0 ? 0 : (a > g.n_tokens ? g.n_tokens : a);
+        b = b < a ? a : (b > g.n_tokens ? g.n_tokens : b);
         bos = a;
         eos = b;
     } else {
-        bos = (int64_t)seq * p.T;
-        eos = bos + p.T;
+        bos = (int64_t)seq * g.T;
+        eos = bos + g.T;
     }
-    const int H = p.H, DV = p.DV;
-    const int col0 = tile * DVT;
-    const int wcol = col0 + 16 * wave;               // this wave's first dv column
-    const bool wvalid = wcol < DV;                   // DV % 16 == 0
-    const E *qg = reinterpret_cast<const E *>(p.q);
-    const E *kg = reinterpret_cast<const E *>(p.k);
-    const E *vg = reinterpret_cast<const E *>(p.v);
-    E *og = reinterpret_cast<E *>(p.o);
-    const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
+}
 
-    // ---- entry state (C layout: S[kt][j] = S[16kt + 4g + j][wcol + r16]) ---
+__device__ __forceinline__ int64_t chunk_base(const SeqGeom &g, int seq) {
+    return g.cu ? (int64_t)g.chunk_offs[seq] : (int64_t)seq * g.chunks_per_seq;
+}
+
+template <typename E>
+__device__ __forceinline__ typename Elem<E>::frag gfrag(const E *p) {
+    return *reinterpret_cast<const typename Elem<E>::frag *>(p);
+}
+
+// ---------------------------------------------------------------------------
+// LDS tiles written by the asynchronous global->LDS path
+// ---------------------------------------------------------------------------
+// A row-major tile of NCOL-element rows stored without padding; its 16-byte
+// units are XOR-swizzled within each row (unit c of row r sits at unit
+// position c ^ (r % UPR)), so that the fragment reads of 16 consecutive rows
+// at one column spread over all LDS banks.
+// global -> LDS copies of 16 / 4 bytes per lane: lane L writes LDS base + L * size
+// (global_load_lds_dword{,x4}; the LDS base goes in M0).  Written as inline asm
+// on purpose: the compiler then does not know that the instruction writes LDS,
+// so it never makes later LDS reads of the *other* double-buffer slot wait for
+// the copy.  Completion is managed explicitly: dma_wait() (s_waitcnt vmcnt(0))
+// by every issuing wave, then a barrier, before any lane reads the slot; the
+// memory clobber keeps the compiler from moving LDS accesses across the copy.
+// M0 is set inside the asm and is otherwise unused by these kernels (no
+// movrel / LDS-parameter instructions), so clobbering it is safe here.
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void lds_dma16(const void *src, void *lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_base))) : "memory", "m0");
+}
+__device__ __forceinline__ void lds_dma4(const void *src, void *lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_base))) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+template <typename E, int NCOL>
+struct Swz {
+    static constexpr int VE = 16 / sizeof(E);
+    static constexpr int UPR = NCOL / VE;                     // 16-byte units per row
+    static_assert((UPR & (UPR - 1)) == 0, "units per row must be a power of two");
+    __device__ static __forceinline__ int at(int r, int c) {
+        return r * NCOL + (((c / VE) ^ (r & (UPR - 1))) * VE) + (c & (VE - 1));
+    }
+};
+
+// Issue the asynchronous copy of rows [0, CH) x columns [0, NCOL) of a token-
+// major global matrix (row r at src + r * stride) into a swizzled LDS tile.
+// Rows >= valid_rows and columns >= valid_cols are zero-filled with ordinary
+// LDS stores instead.  global_load_lds writes lane L's 16 bytes at the
+// wave-uniform LDS base + 16 L, so each wave fills 64 consecutive units and the
+// swizzle is applied by choosing which global unit each lane fetches.
+// Completion: s_waitcnt vmcnt(0) by the issuing wave, then a barrier.
+template <typename E, int CH, int NCOL, int NT, bool SWIZZLE = true>
+__device__ __forceinline__ void dma_rows(E *lds, const E *src, int64_t stride, int valid_rows, int valid_cols,
+                                int tid) {
+    using S = Swz<E, NCOL>;
+    constexpr int UNITS = CH * S::UPR;
+    constexpr int NWV = NT / 64;
+    static_assert(UNITS % NT == 0, "tile does not split evenly over the workgroup");
+    const int wave = tid >> 6, lane = tid & 63;
+    // zero-fill first: an ordinary LDS store issued after a DMA into the same
+    // array would make the compiler wait for that DMA
+#pragma unroll
+    for (int i = 0; i < UNITS / NT; ++i) {
+        const int u = (wave + NWV * i) * 64 + lane;
+        const int r = u / S::UPR, pp = u % S::UPR;
+        const int c = SWIZZLE ? (pp ^ (r & (S::UPR - 1))) : pp;
+        if (!(r < valid_rows && c * S::VE < valid_cols))
+            *reinterpret_cast<Vec16 *>(lds + u * S::VE) = Vec16{{0u, 0u, 0u, 0u}};
+    }
+#pragma unroll
+    for (int i = 0; i < UNITS / NT; ++i) {
+        const int wu = (wave + NWV * i) * 64;                 // first unit of this wave's run
+        const int u = wu + lane;
+        const int r = u / S::UPR, pp = u % S::UPR;
+        const int c = SWIZZLE ? (pp ^ (r & (S::UPR - 1))) : pp;
+        if (r < valid_rows && c * S::VE < valid_cols)
+            lds_dma16(src + (int64_t)r * stride + c * S::VE, lds + wu * S::VE);
+    }
+}
+
+// contiguous copy of n16 16-byte units (identity layout)
+template <typename E, int NUNITS, int NT>
+__device__ __forceinline__ void dma_flat(E *lds, const E *src, int tid) {
+    constexpr int VE = 16 / sizeof(E);
+    static_assert(NUNITS % NT == 0, "block does not split evenly over the workgroup");
+    const int wave = tid >> 6, lane = tid & 63;
+#pragma unroll
+    for (int i = 0; i < NUNITS / NT; ++i) {
+        const int wu = (wave + (NT / 64) * i) * 64;
+        lds_dma16(src + (wu + lane) * VE, lds + wu * VE);
+    }
+}
+
+__device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Workgroup barrier that orders LDS traffic only: waits for this wave's LDS
+// operations, then s_barrier.  Unlike __syncthreads() it does not wait for
+// outstanding global memory operations, so an asynchronous copy into the other
+// double-buffer slot keeps flowing across it.  The memory clobber stops the
+// compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ===========================================================================
+// chunk_prep_kernel: per (chunk, head) TE and A
+// ===========================================================================
+template <int DK, int CH, typename E, int GATE>
+struct PrepLayout {
+    static constexpr int PF = CH + 4, PG = DK + 4;
+    static constexpr int STAGE = 2 * CH * DK * (int)sizeof(E);    // K, Q rows (swizzled)
+    static constexpr int SOLVE = 2 * CH * PF * 4;                  // M, T (reuse the stage)
+    static constexpr int UNION = cmax(STAGE, SOLVE);
+};
+
+template <int DK, int CH, typename E, int GATE>
+__global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
+    using EL = Elem<E>;
+    using F = typename EL::frag;
+    using L = PrepLayout<DK, CH, E, GATE>;
+    using SK = Swz<E, DK>;
+    constexpr int NT = 256, NW = 4, NB = CH / 16, NKB = DK / 16, PF = L::PF, PG = L::PG;
+    constexpr int NL = NB * (NB + 1) / 2;
+    constexpr int JPW = (NL + NW - 1) / NW;                    // tile jobs per wave
+
+    __shared__ __attribute__((aligned(16))) char smem[L::UNION];
+    __shared__ __attribute__((aligned(16))) float gam[GATE == 2 ? CH * PG : CH];
+    __shared__ __attribute__((aligned(16))) float bet[CH];
+    __shared__ int flag[4];
+    E *Kst = reinterpret_cast<E *>(smem);
+    E *Qst = Kst + CH * DK;
+    float *Mf = reinterpret_cast<float *>(smem);                // after the products are done
+    float *Tf = Mf + CH * PF;
+
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int g4 = lane >> 4, r16 = lane & 15;
+    const int H = p.H;
+    const int h = blockIdx.x % H;
+    const int64_t slot = blockIdx.x / H;
+
+    // ---- which chunk ------------------------------------------------------
+    int seq;
+    int64_t cin;
+    if (p.geo.cu) {
+        const int32_t *offs = p.geo.chunk_offs;
+        if (slot >= offs[p.geo.n_seqs]) return;               // beyond the last chunk
+        int lo = 0, hi = p.geo.n_seqs - 1;                     // largest s with offs[s] <= slot
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (offs[mid] <= slot) lo = mid; else hi = mid - 1;
+        }
+        seq = lo;
+        cin = slot - offs[lo];
+    } else {
+        seq = (int)(slot / p.geo.chunks_per_seq);
+        cin = slot % p.geo.chunks_per_seq;
+        if (seq >= p.geo.n_seqs) return;
+    }
+    int64_t bos, eos;
+    seq_bounds(p.geo, seq, bos, eos);
+    const int64_t t0 = bos + cin * CH;
+    const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+    const int64_t sqk = (int64_t)H * DK;
+    const E *kg = reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK;
+    const E *qg = reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK;
+    E *blk = reinterpret_cast<E *>(p.blocks) + (slot * H + h) * 2 * CH * CH;   // TE, then A
+
+    // ---- stage K, Q rows; cumulative decay; beta --------------------------
+    dma_rows<E, CH, DK, NT>(Kst, kg, sqk, clen, DK, tid);
+    dma_rows<E, CH, DK, NT>(Qst, qg, sqk, clen, DK, tid);
+    if (tid < CH) bet[tid] = (p.use_delta && tid < clen) ? p.beta[(t0 + tid) * H + h] : 0.f;
+    if constexpr (GATE == 2) {
+        for (int vi = tid; vi < CH * DK / 4; vi += NT) {
+            const int row = vi / (DK / 4), col = (vi % (DK / 4)) * 4;
+            st4(gam + row * PG + col,
+                row < clen ? ld4(p.g + ((t0 + row) * H + h) * DK + col) : f32x4{0.f, 0.f, 0.f, 0.f});
+        }
+        if (tid < 4) flag[tid] = 0;
+        __syncthreads();
+        constexpr int NP = NT / DK, SEG = CH / NP;
+        const int cc = tid % DK, part = tid / DK;
+        float acc = 0.f;
+        for (int t = part * SEG; t < (part + 1) * SEG; ++t) {
+            acc += gam[t * PG + cc];
+            gam[t * PG + cc] = acc;
+        }
+        __syncthreads();
+        float off = 0.f;
+        for (int q2 = 0; q2 < part; ++q2) off += gam[((q2 + 1) * SEG - 1) * PG + cc];
+        __syncthreads();
+        if (part > 0)
+            for (int t = part * SEG; t < (part + 1) * SEG; ++t) gam[t * PG + cc] += off;
+        __syncthreads();
+        for (int it = tid; it < NB * DK; it += NT) {
+            const int b = it / DK, c2 = it % DK;
+            if (gam[(16 * b) * PG + c2] - gam[(16 * b + 15) * PG + c2] > EL::gate_range) flag[b] = 1;
+        }
+    } else {
+        if (wave == 0) {
+            float x = (p.g && lane < clen) ? p.g[(t0 + lane) * H + h] : 0.f;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const float y = __shfl_up(x, o);
+                if (lane >= o) x += y;
+            }
+            if (lane < CH) gam[lane] = x;
+        }
+    }
+    dma_wait();
+    __syncthreads();
+
+    // ---- K K^T (-> M) and Q K^T (-> A), lower tile pairs -----------------
+    // Job (I, J) computes X = K_J Y_I^T for Y in {K, Q}; the C layout then
+    // holds X[4g + jj][r] = <y_i, k_j> for i = 16I + r, j = 16J + 4g + jj, four
+    // consecutive j of row i: exactly the fragment (I, J) of A / M.
+    f32x4 res_q[JPW], res_k[JPW];
+#pragma unroll
+    for (int s = 0; s < JPW; ++s) {
+        const int job = wave + NW * s;
+        res_q[s] = res_k[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (job >= NL) continue;
+        int I = 0, J = job;
+        while (J > I) { J -= I + 1; ++I; }
+        const int jrow = 16 * J + r16, irow = 16 * I + r16;
+        F a[NKB], bq[NKB], bk[NKB];
+#pragma unroll
+        for (int kt = 0; kt < NKB; ++kt) {
+            const int cc = 16 * kt + 4 * g4;
+            a[kt] = ld_frag<E>(Kst + SK::at(jrow, cc));
+            bq[kt] = ld_frag<E>(Qst + SK::at(irow, cc));
+            bk[kt] = ld_frag<E>(Kst + SK::at(irow, cc));
+        }
+        bool pairwise = false;
+        if constexpr (GATE == 2) {
+            pairwise = (I == J) && flag[I];
+            const int rr = 16 * I;
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt) {
+                const int cc = 16 * kt + 4 * g4;
+                const f32x4 gr = ld4(gam + rr * PG + cc);
+                const f32x4 ea = exp4(gr - ld4(gam + jrow * PG + cc));      // <= 1 off the diagonal
+                const f32x4 eb = exp4(ld4(gam + irow * PG + cc) - gr);      // <= 1
+                a[kt] = EL::cvt(EL::tof(a[kt]) * ea);
+                bq[kt] = EL::cvt(EL::tof(bq[kt]) * eb);
+                bk[kt] = EL::cvt(EL::tof(bk[kt]) * eb);
+            }
+        }
+        f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+        if (!pairwise) {
+#pragma unroll
+            for (int kt = 0; kt < NKB; kt += 2) {
+                accq = mfma_kb2(a[kt], bq[kt], a[kt + 1], bq[kt + 1], accq);
+                acck = mfma_kb2(a[kt], bk[kt], a[kt + 1], bk[kt + 1], acck);
+            }
+        } else if constexpr (GATE == 2) {
+            // exact pairwise products for a diagonal block with a large decay range
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int jt = 16 * J + 4 * g4 + jj;
+                float sq = 0.f, sk = 0.f;
+                if (jt <= irow) {
+                    for (int cc = 0; cc < DK; cc += 4) {
+                        const f32x4 e = exp4(ld4(gam + irow * PG + cc) - ld4(gam + jt * PG + cc));
+                        const f32x4 kj = EL::tof(ld_frag<E>(Kst + SK::at(jt, cc))) * e;
+                        const f32x4 yq = EL::tof(ld_frag<E>(Qst + SK::at(irow, cc))) * kj;
+                        const f32x4 yk = EL::tof(ld_frag<E>(Kst + SK::at(irow, cc))) * kj;
+                        sq += yq[0] + yq[1] + yq[2] + yq[3];
+                        sk += yk[0] + yk[1] + yk[2] + yk[3];
+                    }
+                }
+                accq[jj] = sq;
+                acck[jj] = sk;
+            }
+        }
+        f32x4 aq, mk;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int jt = 16 * J + 4 * g4 + jj;
+            // computed for every lane and then selected: a lane-dependent branch
+            // here becomes an exec-skip right after the MFMAs above
+            float d = 1.f;
+            if constexpr (GATE != 2) {
+                const float e = __expf(gam[irow] - gam[jt]);
+                d = (jt <= irow) ? e : 0.f;
+            }
+            aq[jj] = (jt <= irow) ? p.scale * accq[jj] * d : 0.f;
+            mk[jj] = (jt < irow) ? bet[irow] * acck[jj] * d : 0.f;
+        }
+        res_q[s] = aq;
+        res_k[s] = mk;
+    }
+    __syncthreads();                                           // K, Q reads done: M, T reuse the stage
+#pragma unroll
+    for (int s = 0; s < JPW; ++s) {
+        const int job = wave + NW * s;
+        if (job >= NL) continue;
+        int I = 0, J = job;
+        while (J > I) { J -= I + 1; ++I; }
+        st_frag<E>(blk + CH * CH + frag_pos<NB>(I, J, lane), EL::cvt(res_q[s]));
+        if (p.use_delta) st4(Mf + (16 * I + r16) * PF + 16 * J + 4 * g4, res_k[s]);
+    }
+    if (!p.use_delta) return;
+    __syncthreads();
+
+    // ---- T = (I + M)^-1: 16x16 diagonal blocks by forward substitution ---
+    if (wave == 0 && lane < 16 * NB) {
+        const int b = lane >> 4, jc = lane & 15;
+        float t[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float *mrow = Mf + (16 * b + i) * PF + 16 * b;
+            float acc = (i == jc) ? 1.f : 0.f;
+#pragma unroll
+            for (int m4 = 0; m4 < 16; m4 += 4) {
+                if (m4 >= i) break;
+                const f32x4 mv = ld4(mrow + m4);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (m4 + e < i) acc -= mv[e] * t[m4 + e];
+            }
+            t[i] = acc;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) Tf[(16 * b + i) * PF + 16 * b + jc] = t[i];
+    }
+    __syncthreads();
+    // off-diagonal blocks by distance: T_IJ = -T_II sum_{K=J}^{I-1} M_IK T_KJ
+#pragma unroll
+    for (int dist = 1; dist < NB; ++dist) {
+        for (int J = wave; J < NB - dist; J += NW) {
+            const int I = J + dist;
+            f32x4 X = {0.f, 0.f, 0.f, 0.f};
+            for (int K = J; K < I; ++K) {
+                const float *tc = Tf + (16 * K + 4 * g4) * PF + 16 * J + r16;    // column of T_KJ
+                X = mfma_kb1(ld4(Mf + (16 * I + r16) * PF + 16 * K + 4 * g4),
+                             f32x4{tc[0], tc[PF], tc[2 * PF], tc[3 * PF]}, X);
+            }
+            const f32x4 Y = mfma_kb1(ld4(Tf + (16 * I + r16) * PF + 16 * I + 4 * g4), X,
+                                     f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int j = 0; j < 4; ++j) Tf[(16 * I + 4 * g4 + j) * PF + 16 * J + r16] = -Y[j];
+        }
+        __syncthreads();
+    }
+    // ---- TE = T diag(beta), lower tiles, fragment order ---------------------
+    for (int tjob = wave; tjob < NL; tjob += NW) {
+        int I = 0, kb = tjob;
+        while (kb > I) { kb -= I + 1; ++I; }
+        const int row = 16 * I + r16, c0 = 16 * kb + 4 * g4;
+        f32x4 t = ld4(Tf + row * PF + c0) * ld4(bet + c0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (c0 + e > row) t[e] = 0.f;
+        st_frag<E>(blk + frag_pos<NB>(I, kb, lane), EL::cvt(t));
+    }
+}
+
+// ===========================================================================
+// chunk_state_kernel: the chunk recurrence and the outputs
+// ===========================================================================
+template <int DK, int CH, int NW, typename E, int GATE>
+struct StateLayout {
+    static constexpr int NT = 64 * NW, NB = CH / 16, NKB = DK / 16, DVT = 16 * NW;
+    static constexpr int ES = sizeof(E);
+    static constexpr int PC = CH + Elem<E>::pad;              // K^T pitch
+    static constexpr int PV = DVT + Elem<E>::pad;             // output staging pitch
+    // one double-buffer slot: K, Q (swizzled), V (swizzled), TE + A (fragment order), g (scalar gate)
+    static constexpr int SLOT = (2 * CH * DK + CH * DVT + 2 * CH * CH) * ES + (GATE == 2 ? 0 : CH * 4);
+    static constexpr int BYTES = 2 * SLOT + DK * PC * ES + CH * PV * ES + (GATE == 2 ? CH * DK * 4 : 4 * 4) +
+                                 (2 * CH + (GATE == 2 ? DK : 4)) * 4;
+    static constexpr bool FITS = BYTES <= 160 * 1024;
+};
+
+// One double-buffer slot of the state kernel.  The two slots are distinct LDS
+// objects and every access names its slot at compile time, so the compiler
+// can tell that reads of the current slot never alias the asynchronous copy
+// into the other one (and does not make them wait for it).
+template <int DK, int CH, int NW, typename E, int GATE>
+struct StateSlot {
+    E *K, *Q, *V, *B;
+    float *g;
+};
+
+template <int V_> struct SlotTag { static constexpr int value = V_; };
+
+// asynchronous copy of chunk c's operands (K, Q, V rows, TE + A blocks, scalar g)
+template <int DK, int CH, int NW, typename E, int GATE>
+__device__ __forceinline__ void state_issue(const StateSlot<DK, CH, NW, E, GATE> &sl, int c, int64_t bos, int64_t eos,
+                                   int64_t cbase, int h, const E *kg, const E *qg, const E *vg, const E *blocks,
+                                   const ChunkParams &p, int col0, int tid) {
+    using L = StateLayout<DK, CH, NW, E, GATE>;
+    const int H = p.H;
+    const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * p.DV;
+    const int64_t t0 = bos + (int64_t)c * CH;
+    const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+    if constexpr (GATE != 2) {
+        const int wave = tid >> 6, lane = tid & 63;
+        if (wave == 0 && lane < CH && !(p.g && lane < clen)) sl.g[lane] = 0.f;
+    }
+    dma_rows<E, CH, DK, L::NT>(sl.K, kg + t0 * sqk, sqk, clen, DK, tid);
+    dma_rows<E, CH, DK, L::NT>(sl.Q, qg + t0 * sqk, sqk, clen, DK, tid);
+    dma_rows<E, CH, L::DVT, L::NT>(sl.V, vg + t0 * sv, sv, clen, p.DV - col0, tid);
+    dma_flat<E, 2 * CH * CH * L::ES / 16, L::NT>(sl.B, blocks + ((cbase + c) * H + h) * 2 * CH * CH, tid);
+    if constexpr (GATE != 2) {
+        const int wave = tid >> 6, lane = tid & 63;
+        if (wave == 0 && lane < CH && p.g && lane < clen) lds_dma4(p.g + (t0 + lane) * H + h, sl.g);
+    }
+}
+
+template <int DK, int CH, int NW>
+__device__ __forceinline__ void state_issue_g(float *gamv, int c, int64_t bos, int64_t eos, int h, const ChunkParams &p,
+                                     int tid) {
+    const int64_t t0 = bos + (int64_t)c * CH;
+    const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+    dma_rows<float, CH, DK, 64 * NW, false>(gamv, p.g + (t0 * p.H + h) * DK, (int64_t)p.H * DK, clen, DK, tid);
+}
+
+template <int DK, int CH, int NW, typename E, int GATE, bool DELTA>
+__global__ void __launch_bounds__(64 * NW) chunk_state_kernel(const ChunkParams p) {
+    using L = StateLayout<DK, CH, NW, E, GATE>;
+    static_assert(L::FITS, "LDS budget exceeded");
+    using EL = Elem<E>;
+    using F = typename EL::frag;
+    using SK = Swz<E, DK>;
+    using SV = Swz<E, L::DVT>;
+    using Slot = StateSlot<DK, CH, NW, E, GATE>;
+    constexpr int NT = L::NT, NB = L::NB, NKB = L::NKB, DVT = L::DVT;
+    constexpr int PC = L::PC, PV = L::PV;
+
+    __shared__ __attribute__((aligned(16))) E K0[CH * DK];
+    __shared__ __attribute__((aligned(16))) E K1[CH * DK];
+    __shared__ __attribute__((aligned(16))) E Q0[CH * DK];
+    __shared__ __attribute__((aligned(16))) E Q1[CH * DK];
+    __shared__ __attribute__((aligned(16))) E V0[CH * DVT];
+    __shared__ __attribute__((aligned(16))) E V1[CH * DVT];
+    __shared__ __attribute__((aligned(16))) E B0[2 * CH * CH];      // TE, then A
+    __shared__ __attribute__((aligned(16))) E B1[2 * CH * CH];
+    __shared__ __attribute__((aligned(16))) float g0[GATE == 2 ? 4 : CH];
+    __shared__ __attribute__((aligned(16))) float g1[GATE == 2 ? 4 : CH];
+    __shared__ __attribute__((aligned(16))) E KsT[DK * PC];
+    __shared__ __attribute__((aligned(16))) E Os[CH * PV];
+    __shared__ __attribute__((aligned(16))) float gamv[GATE == 2 ? CH * DK : 4];
+    __shared__ __attribute__((aligned(16))) float Gs[CH];
+    __shared__ __attribute__((aligned(16))) float Gend[CH];
+    __shared__ __attribute__((aligned(16))) float Gc[GATE == 2 ? DK : 4];
+    const Slot slot0{K0, Q0, V0, B0, g0}, slot1{K1, Q1, V1, B1, g1};
+
+    // the wave index is uniform: readfirstlane makes every per-wave condition a scalar branch
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int g4 = lane >> 4, r16 = lane & 15;
+    const int H = p.H, DV = p.DV;
+
+    // ---- work item: the dv tiles of one (sequence, head) share an XCD ------
+    const int b = blockIdx.x;
+    const int xcd = b & 7, y = b >> 3;
+    const int tile = y % p.n_tiles;
+    const int pos = (y / p.n_tiles) * 8 + xcd;
+    if (pos >= p.geo.n_seqs * H) return;
+    const int h = pos % H;
+    const int spos = pos / H;
+    const int seq = p.geo.order ? p.geo.order[spos] : spos;
+    int64_t bos, eos;
+    seq_bounds(p.geo, seq, bos, eos);
+    const int64_t cbase = chunk_base(p.geo, seq);
+    const int col0 = tile * DVT;
+    const int wcol = 16 * wave;                                  // within the tile
+    const bool wvalid = col0 + wcol < DV;                        // DV % 16 == 0
+    const int64_t sv = (int64_t)H * DV;
+    const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
+    const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
+    const E *vg = reinterpret_cast<const E *>(p.v) + (int64_t)h * DV + col0;
+    E *og = reinterpret_cast<E *>(p.o) + (int64_t)h * DV + col0;
+    const E *blocks = reinterpret_cast<const E *>(p.blocks);
+
+    // ---- entry state (C layout: S[kt][j] = S[16kt + 4g + j][col0 + wcol + r16]) --
     f32x4 S[NKB];
-    const int64_t sbase = ((int64_t)seq * H + h) * DK * DV;
+    const int64_t sbase = ((int64_t)seq * H + h) * DK * DV + col0 + wcol + r16;
 #pragma unroll
     for (int kt = 0; kt < NKB; ++kt)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV + wcol + r16]
-                                        : 0.f;
+            S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
 
     const int64_t len = eos - bos;
     const int nchunks = (int)((len + CH - 1) / CH);
-    for (int c = 0; c < nchunks; ++c) {
+
+    // outputs of a finished chunk: staged rows -> global, 16-byte stores
+    constexpr int VE = 16 / L::ES;
+    auto flush = [&](int64_t t0, int clen) {
+        for (int vi = tid; vi < CH * (DVT / VE); vi += NT) {
+            const int row = vi / (DVT / VE), col = (vi % (DVT / VE)) * VE;
+            if (row < clen && col0 + col < DV) {
+                const uint2 *s2 = reinterpret_cast<const uint2 *>(Os + row * PV + col);
+                const uint2 lo = s2[0], hi = s2[1];
+                *reinterpret_cast<Vec16 *>(og + (t0 + row) * sv + col) = Vec16{{lo.x, lo.y, hi.x, hi.y}};
+            }
+        }
+    };
+
+    // one chunk, with its operands in slot SL (known at compile time)
+    auto step = [&](auto tag, int c) {
+        constexpr int SL = decltype(tag)::value;
+        const Slot &cur = SL ? slot1 : slot0;
+        const Slot &nxt = SL ? slot0 : slot1;
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
-        __syncthreads();                              // previous chunk's LDS readers are done
+        E *Kst = cur.K;
+        E *Qst = cur.Q;
+        const E *Vst = cur.V;
+        const E *TEs = cur.B;
+        const E *Aqs = cur.B + CH * CH;
 
-        // ---- L1: chunk inputs -> LDS ----------------------------------------
-        load_rows<E, CH, DK, PK, NT>(Ks, kg + t0 * sqk + (int64_t)h * DK, sqk, clen, DK, tid);
-        load_rows<E, CH, DK, PK, NT>(Qs, qg + t0 * sqk + (int64_t)h * DK, sqk, clen, DK, tid);
-        load_rows<E, CH, DVT, PV, NT>(Vrow, vg + t0 * sv + (int64_t)h * DV + col0, sv, clen,
-                                      DV - col0, tid);
-        if constexpr (GATE == 2) {
-            constexpr int NV = CH * DK / 4;
-            static_assert(NV % NT == 0, "gate tile does not split evenly");
-            f32x4 r[NV / NT];
-#pragma unroll
-            for (int i = 0; i < NV / NT; ++i) {
-                const int vi = tid + i * NT, row = vi / (DK / 4), col = (vi % (DK / 4)) * 4;
-                r[i] = row < clen ? ld4(p.g + ((t0 + row) * H + h) * DK + col) : f32x4{0, 0, 0, 0};
-            }
-#pragma unroll
-            for (int i = 0; i < NV / NT; ++i) {
-                const int vi = tid + i * NT, row = vi / (DK / 4), col = (vi % (DK / 4)) * 4;
-                st4(gam + row * PG + col, r[i]);
-            }
-        } else {
-            if (tid < CH) gam[tid] = (p.g && tid < clen) ? p.g[(t0 + tid) * H + h] : 0.f;
-        }
-        if (tid < CH) bet[tid] = (p.use_delta && tid < clen) ? p.beta[(t0 + tid) * H + h] : 0.f;
-        __syncthreads();
+        dma_wait();
+        lds_barrier();                                        // chunk c landed; chunk c-1 fully consumed
+        if (c + 1 < nchunks)                                  // into the slot chunk c-1 used
+            state_issue<DK, CH, NW, E, GATE>(nxt, c + 1, bos, eos, cbase, h, kg, qg, vg, blocks, p, col0, tid);
+        if (c > 0) flush(t0 - CH, CH);                        // every chunk but the last is full
 
-        // ---- L1b: transposes, cumulative decay --------------------------------
-        // KsT[c][t..t+3] = Ks[t..t+3][c];  VsT[n][t..t+3] = Vrow[t..t+3][n]
-        for (int it = tid; it < DK * (CH / 4); it += NT) {
-            const int cc = it % DK, t = (it / DK) * 4;
-            F x = {Ks[(t + 0) * PK + cc], Ks[(t + 1) * PK + cc], Ks[(t + 2) * PK + cc],
-                   Ks[(t + 3) * PK + cc]};
-            st_frag<E>(KsT + cc * PC + t, x);
-        }
-        for (int it = tid; it < DVT * (CH / 4); it += NT) {
-            const int n = it % DVT, t = (it / DVT) * 4;
-            F x = {Vrow[(t + 0) * PV + n], Vrow[(t + 1) * PV + n], Vrow[(t + 2) * PV + n],
-                   Vrow[(t + 3) * PV + n]};
-            st_frag<E>(VsT + n * PC + t, x);
-        }
+        // ---- gates and the transposed keys --------------------------------
         if constexpr (GATE == 2) {
-            // per-channel inclusive scan over CH tokens: NP parts of CH/NP tokens
+            // per-channel inclusive scan: NP parts of SEG tokens per channel
+            static_assert(NT % DK == 0, "one or more whole threads per channel");
             constexpr int NP = NT / DK;
             constexpr int SEG = CH / NP;
-            static_assert(NP >= 1 && CH % NP == 0, "scan split");
-            const int cc = tid % DK, part = tid / DK;
-            if (part < NP) {
+            {
+                const int cc = tid % DK, part = tid / DK;
                 float acc = 0.f;
                 for (int t = part * SEG; t < (part + 1) * SEG; ++t) {
-                    acc += gam[t * PG + cc];
-                    gam[t * PG + cc] = acc;
+                    acc += gamv[t * DK + cc];
+                    gamv[t * DK + cc] = acc;
                 }
             }
-            __syncthreads();
-            float off = 0.f;                          // totals of the earlier parts, read
-            if (part < NP)                            // before any part is updated
-                for (int q2 = 0; q2 < part; ++q2) off += gam[((q2 + 1) * SEG - 1) * PG + cc];
-            if (tid < NB) flag[tid] = 0;
-            __syncthreads();
-            if (part < NP && part > 0)
-                for (int t = part * SEG; t < (part + 1) * SEG; ++t) gam[t * PG + cc] += off;
-            __syncthreads();
-            if (tid < DK) Gc[tid] = __expf(gam[(CH - 1) * PG + tid]);
-            // diagonal sub-block decay ranges -> pairwise fallback flags
-            for (int it = tid; it < NB * DK; it += NT) {
-                const int b = it / DK, cc2 = it % DK;
-                const float range = gam[(16 * b) * PG + cc2] - gam[(16 * b + 15) * PG + cc2];
-                if (range > EL::gate_range) flag[b] = 1;          // benign race: all write 1
+            if constexpr (NP > 1) {
+                lds_barrier();
+                const int cc = tid % DK, part = tid / DK;
+                float off = 0.f;
+                for (int q2 = 0; q2 < part; ++q2) off += gamv[((q2 + 1) * SEG - 1) * DK + cc];
+                lds_barrier();
+                if (part > 0)
+                    for (int t = part * SEG; t < (part + 1) * SEG; ++t) gamv[t * DK + cc] += off;
+            }
+            lds_barrier();
+            for (int cc = tid; cc < DK; cc += NT) Gc[cc] = __expf(gamv[(CH - 1) * DK + cc]);
+            // KsT = (K * Gend)^T, K <- K * G, Q <- scale * Q * G (each element owned by one item)
+            for (int it = tid; it < DK * (CH / 4); it += NT) {
+                const int cc = it % DK, t = (it / DK) * 4;
+                const float last = gamv[(CH - 1) * DK + cc];
+                const f32x4 gm = {gamv[(t + 0) * DK + cc], gamv[(t + 1) * DK + cc], gamv[(t + 2) * DK + cc],
+                                  gamv[(t + 3) * DK + cc]};
+                const f32x4 G = exp4(gm), Ge = exp4(last - gm);
+                f32x4 kx;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) kx[e] = EL::to_f(Kst[SK::at(t + e, cc)]);
+                st_frag<E>(KsT + cc * PC + t, EL::cvt(kx * Ge));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    Kst[SK::at(t + e, cc)] = EL::from_f(kx[e] * G[e]);
+                    Qst[SK::at(t + e, cc)] = EL::from_f(EL::to_f(Qst[SK::at(t + e, cc)]) * G[e] * p.scale);
+                }
             }
         } else {
             if (wave == 0) {
-                float x = gam[lane < CH ? lane : CH - 1];
+                float x = cur.g[lane < CH ? lane : CH - 1];
                 if (lane >= CH) x = 0.f;
 #pragma unroll
                 for (int o = 1; o < 64; o <<= 1) {
-                    const float y = __shfl_up(x, o);
-                    if (lane >= o) x += y;
+                    const float yv = __shfl_up(x, o);
+                    if (lane >= o) x += yv;
                 }
                 const float last = __shfl(x, CH - 1);
                 if (lane < CH) {
-                    gam[lane] = x;
                     Gs[lane] = __expf(x);
                     Gend[lane] = __expf(last - x);
                 }
                 if (lane == 0) Gc[0] = __expf(last);
             }
-        }
-        __syncthreads();
-
-        // ---- L3: gated K K^T (-> M) and Q K^T (-> Aqk), lower blocks ---------
-        // Job (I, J, which) computes X = K_J Y_I^T (Y = K or Q), so that the C
-        // layout holds X[4g + jj][r] = <y_i, k_j> with i = 16I + r, j = 16J + 4g + jj:
-        // four consecutive j of one row i, stored with one vector write.
-        {
-            constexpr int NL = NB * (NB + 1) / 2;
-            const int njobs = p.use_delta ? 2 * NL : NL;
-            for (int job = wave; job < njobs; job += NW) {
-                const bool isq = job < NL;           // Q jobs first (always present)
-                int tI = isq ? job : job - NL;
-                int I = 0;
-                while (tI > I) { tI -= I + 1; ++I; }
-                const int J = tI;
-                const E *Ys = isq ? Qs : Ks;
-                const int i_tok = 16 * I + r16;
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-                bool pairwise = false;
-                if constexpr (GATE == 2) pairwise = (I == J) && flag[I];
-                if (!pairwise) {
-                    if constexpr (GATE == 2) {
-                        const int rr = 16 * I;
-                        acc = contract(acc, NKB,
-                            [&](int kb) {     // A: k_j * exp(gamma_r - gamma_j)
-                                const int cc = 16 * kb + 4 * g4, jt = 16 * J + r16;
-                                f32x4 x = EL::tof(ld_frag<E>(Ks + jt * PK + cc));
-                                f32x4 e = exp4(ld4(gam + rr * PG + cc) - ld4(gam + jt * PG + cc));
-                                return EL::cvt(x * e);
-                            },
-                            [&](int kb) {     // B: y_i * exp(gamma_i - gamma_r)
-                                const int cc = 16 * kb + 4 * g4;
-                                f32x4 x = EL::tof(ld_frag<E>(Ys + i_tok * PK + cc));
-                                f32x4 e = exp4(ld4(gam + i_tok * PG + cc) - ld4(gam + rr * PG + cc));
-                                return EL::cvt(x * e);
-                            });
-                    } else {
-                        acc = contract(acc, NKB,
-                            [&](int kb) { return ld_frag<E>(Ks + (16 * J + r16) * PK + 16 * kb + 4 * g4); },
-                            [&](int kb) { return ld_frag<E>(Ys + i_tok * PK + 16 * kb + 4 * g4); });
-                    }
-                } else if constexpr (GATE == 2) {
-                    // exact pairwise products for a diagonal block with a large decay range
-#pragma unroll
-                    for (int jj = 0; jj < 4; ++jj) {
-                        const int j_tok = 16 * J + 4 * g4 + jj;
-                        float s = 0.f;
-                        if (j_tok <= i_tok) {
-                            for (int cc = 0; cc < DK; cc += 4) {
-                                f32x4 y = EL::tof(ld_frag<E>(Ys + i_tok * PK + cc));
-                                f32x4 kx = EL::tof(ld_frag<E>(Ks + j_tok * PK + cc));
-                                f32x4 e = exp4(ld4(gam + i_tok * PG + cc) - ld4(gam + j_tok * PG + cc));
-                                f32x4 t4 = y * kx * e;
-                                s += t4[0] + t4[1] + t4[2] + t4[3];
-                            }
-                        }
-                        acc[jj] = s;
-                    }
-                }
-                // epilogue: decay (scalar gate), beta / scale, masks
-                f32x4 out;
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) {
-                    const int j_tok = 16 * J + 4 * g4 + jj;
-                    float d = 1.f;
-                    if constexpr (GATE != 2) d = (j_tok <= i_tok) ? __expf(gam[i_tok] - gam[j_tok]) : 0.f;
-                    const float x = acc[jj] * d;
-                    out[jj] = isq ? ((j_tok <= i_tok) ? p.scale * x : 0.f)
-                                  : ((j_tok < i_tok) ? bet[i_tok] * x : 0.f);
-                }
-                if (isq)
-                    st_frag<E>(Aqk + i_tok * PC + 16 * J + 4 * g4, EL::cvt(out));
-                else
-                    st4(Mf + i_tok * PF + 16 * J + 4 * g4, out);
-            }
-        }
-        __syncthreads();
-
-        // Q -> scale * (Q * G) for the state read-out (raw Q no longer needed)
-        for (int it = tid; it < CH * (DK / 4); it += NT) {
-            const int t = it / (DK / 4), cc = (it % (DK / 4)) * 4;
-            f32x4 x = EL::tof(ld_frag<E>(Qs + t * PK + cc));
-            f32x4 gf;
-            if constexpr (GATE == 2) gf = exp4(ld4(gam + t * PG + cc));
-            else gf = f32x4{Gs[t], Gs[t], Gs[t], Gs[t]};
-            st_frag<E>(Qs + t * PK + cc, EL::cvt(x * gf * p.scale));
-        }
-
-        if (p.use_delta) {
-            // ---- L4: T = (I + M)^-1, diagonal 16x16 blocks by substitution ----
-            if (wave == 0 && lane < 16 * NB) {
-                const int b = lane >> 4, jc = lane & 15;
-                float t[16];
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    float acc = (i == jc) ? 1.f : 0.f;
-                    const float *mrow = Mf + (16 * b + i) * PF + 16 * b;
-#pragma unroll
-                    for (int m = 0; m < i; ++m) acc -= mrow[m] * t[m];
-                    t[i] = acc;
-                }
-#pragma unroll
-                for (int i = 0; i < 16; ++i) Tf[(16 * b + i) * PF + 16 * b + jc] = t[i];
-#pragma unroll
-                for (int i = 0; i < 16; i += 4)
-                    st4(TTf + (16 * b + jc) * PF + 16 * b + i, f32x4{t[i], t[i + 1], t[i + 2], t[i + 3]});
-            }
-            __syncthreads();
-            // off-diagonal blocks: T_IJ = -T_II sum_{K=J}^{I-1} M_IK T_KJ, by distance
-#pragma unroll
-            for (int dist = 1; dist < NB; ++dist) {
-                for (int jb = wave; jb < NB - dist; jb += NW) {
-                    const int J = jb, I = jb + dist;
-                    f32x4 X = {0.f, 0.f, 0.f, 0.f};
-                    for (int K = J; K < I; ++K)
-                        X = mfma_kb1(ld4(Mf + (16 * I + r16) * PF + 16 * K + 4 * g4),
-                                     ld4(TTf + (16 * J + r16) * PF + 16 * K + 4 * g4), X);
-                    const f32x4 Y = mfma_kb1(ld4(Tf + (16 * I + r16) * PF + 16 * I + 4 * g4), X,
-                                             f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) Tf[(16 * I + 4 * g4 + j) * PF + 16 * J + r16] = -Y[j];
-                    st4(TTf + (16 * J + r16) * PF + 16 * I + 4 * g4, -Y);
-                }
-                __syncthreads();
-            }
-            // TE = T diag(beta) (lower triangle), in the element type.  TE overwrites
-            // TT, which the barrier above retired.
-            for (int it = tid; it < CH * (CH / 4); it += NT) {
-                const int i = it / (CH / 4), j = (it % (CH / 4)) * 4;
-                f32x4 t = ld4(Tf + i * PF + j) * ld4(bet + j);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (j + e > i) t[e] = 0.f;
-                st_frag<E>(TE + i * PC + j, EL::cvt(t));
-            }
-            // KsT -> (K * G)^T
             for (int it = tid; it < DK * (CH / 4); it += NT) {
                 const int cc = it % DK, t = (it / DK) * 4;
-                f32x4 x = EL::tof(ld_frag<E>(KsT + cc * PC + t));
-                f32x4 gf;
-                if constexpr (GATE == 2)
-                    gf = exp4(f32x4{gam[(t + 0) * PG + cc], gam[(t + 1) * PG + cc],
-                                    gam[(t + 2) * PG + cc], gam[(t + 3) * PG + cc]});
-                else
-                    gf = ld4(Gs + t);
-                st_frag<E>(KsT + cc * PC + t, EL::cvt(x * gf));
+                F x = {Kst[SK::at(t, cc)], Kst[SK::at(t + 1, cc)], Kst[SK::at(t + 2, cc)], Kst[SK::at(t + 3, cc)]};
+                st_frag<E>(KsT + cc * PC + t, x);
             }
-            __syncthreads();
-            // ---- L6: W^T = (K*G)^T TE^T -> Ws (row-major W) --------------------
-            for (int job = wave; job < NKB * NB; job += NW) {
-                const int a = job % NKB, b = job / NKB;
-                f32x4 acc = contract(f32x4{0.f, 0.f, 0.f, 0.f}, b + 1,
-                    [&](int kb) { return ld_frag<E>(KsT + (16 * a + r16) * PC + 16 * kb + 4 * g4); },
-                    [&](int kb) { return ld_frag<E>(TE + (16 * b + r16) * PC + 16 * kb + 4 * g4); });
-                st_frag<E>(Ws + (16 * b + r16) * PK + 16 * a + 4 * g4, EL::cvt(acc));
-            }
-            __syncthreads();
         }
-        // KsT -> (K * Gend)^T, rebuilt from the raw row-major K
-        for (int it = tid; it < DK * (CH / 4); it += NT) {
-            const int cc = it % DK, t = (it / DK) * 4;
-            f32x4 x = {EL::to_f(Ks[(t + 0) * PK + cc]), EL::to_f(Ks[(t + 1) * PK + cc]),
-                       EL::to_f(Ks[(t + 2) * PK + cc]), EL::to_f(Ks[(t + 3) * PK + cc])};
-            f32x4 gf;
-            if constexpr (GATE == 2) {
-                const float last = gam[(CH - 1) * PG + cc];
-                gf = exp4(f32x4{last - gam[(t + 0) * PG + cc], last - gam[(t + 1) * PG + cc],
-                                last - gam[(t + 2) * PG + cc], last - gam[(t + 3) * PG + cc]});
-            } else {
-                gf = ld4(Gend + t);
-            }
-            st_frag<E>(KsT + cc * PC + t, EL::cvt(x * gf));
+        lds_barrier();
+        if constexpr (GATE == 2) {
+            if (c + 1 < nchunks) state_issue_g<DK, CH, NW>(gamv, c + 1, bos, eos, h, p, tid);   // buffer is free
         }
-        __syncthreads();
 
-        // ---- S phase: this wave's 16 state columns, registers only -----------
+        // ---- this wave's 16 state columns ---------------------------------
         if (wvalid) {
-            const E *Vw = VsT + (16 * wave + r16) * PC;      // this lane's V column
-            f32x4 U[NB];
-#pragma unroll
-            for (int I = 0; I < NB; ++I) {
-                if (p.use_delta)
-                    U[I] = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
-                        [&](int kb) { return ld_frag<E>(TE + (16 * I + r16) * PC + 16 * kb + 4 * g4); },
-                        [&](int kb) { return ld_frag<E>(Vw + 16 * kb + 4 * g4); });
-                else
-                    U[I] = EL::tof(ld_frag<E>(Vw + 16 * I + 4 * g4));
-            }
             F Sb[NKB];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) Sb[kt] = EL::cvt(S[kt]);
-            if (p.use_delta) {
+            f32x4 U[NB];
+#pragma unroll
+            for (int I = 0; I < NB; ++I)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) U[I][j] = EL::to_f(Vst[SV::at(16 * I + 4 * g4 + j, wcol + r16)]);
+            if constexpr (DELTA) {
+                // X = V - (K*G) S  (independent accumulation chains per token block) ;  U~ = TE X
+                f32x4 P[NB];
+#pragma unroll
+                for (int I = 0; I < NB; ++I) P[I] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kt = 0; kt < NKB; kt += 2) {
+                    F a0[NB], a1[NB];
+#pragma unroll
+                    for (int I = 0; I < NB; ++I) {
+                        a0[I] = ld_frag<E>(Kst + SK::at(16 * I + r16, 16 * kt + 4 * g4));
+                        a1[I] = ld_frag<E>(Kst + SK::at(16 * I + r16, 16 * kt + 16 + 4 * g4));
+                    }
+#pragma unroll
+                    for (int I = 0; I < NB; ++I) P[I] = mfma_kb2(a0[I], Sb[kt], a1[I], Sb[kt + 1], P[I]);
+                }
+                F Xb[NB];
+#pragma unroll
+                for (int I = 0; I < NB; ++I) {
+                    if constexpr (GATE != 2) P[I] *= ld4(Gs + 16 * I + 4 * g4);
+                    Xb[I] = EL::cvt(U[I] - P[I]);
+                }
 #pragma unroll
                 for (int I = 0; I < NB; ++I)
-                    U[I] -= contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
-                        [&](int kt) { return ld_frag<E>(Ws + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
-                        [&](int kt) { return Sb[kt]; });
+                    U[I] = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
+                        [&](int kb) { return ld_frag<E>(TEs + frag_pos<NB>(I, kb, lane)); },
+                        [&](int kb) { return Xb[kb]; });
             }
             F Ub[NB];
 #pragma unroll
             for (int I = 0; I < NB; ++I) Ub[I] = EL::cvt(U[I]);
-            // o = scale (Q*G) S + A U~
+            // o = scale (Q*G) S + A U~   -> staging rows
+            f32x4 O[NB];
+#pragma unroll
+            for (int I = 0; I < NB; ++I) O[I] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < NKB; kt += 2) {
+                F a0[NB], a1[NB];
+#pragma unroll
+                for (int I = 0; I < NB; ++I) {
+                    a0[I] = ld_frag<E>(Qst + SK::at(16 * I + r16, 16 * kt + 4 * g4));
+                    a1[I] = ld_frag<E>(Qst + SK::at(16 * I + r16, 16 * kt + 16 + 4 * g4));
+                }
+#pragma unroll
+                for (int I = 0; I < NB; ++I) O[I] = mfma_kb2(a0[I], Sb[kt], a1[I], Sb[kt + 1], O[I]);
+            }
 #pragma unroll
             for (int I = 0; I < NB; ++I) {
-                f32x4 O = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
-                    [&](int kt) { return ld_frag<E>(Qs + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
-                    [&](int kt) { return Sb[kt]; });
-                O = contract(O, I + 1,
-                    [&](int kb) { return ld_frag<E>(Aqk + (16 * I + r16) * PC + 16 * kb + 4 * g4); },
+                if constexpr (GATE != 2) O[I] *= ld4(Gs + 16 * I + 4 * g4) * p.scale;
+                O[I] = contract(O[I], I + 1,
+                    [&](int kb) { return ld_frag<E>(Aqs + frag_pos<NB>(I, kb, lane)); },
                     [&](int kb) { return Ub[kb]; });
+                E *orow = Os + (16 * I + 4 * g4) * PV + wcol + r16;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = 16 * I + 4 * g4 + j;
-                    if (row < clen) og[(t0 + row) * sv + (int64_t)h * DV + wcol + r16] = EL::from_f(O[j]);
-                }
+                for (int j = 0; j < 4; ++j) orow[j * PV] = EL::from_f(O[I][j]);
             }
-            // S <- Gc (.) S + (K*Gend)^T U~
+            // S <- Gc (.) S + (K*Gend)^T U~   (independent chains per key block)
+            F Wb[NB];
+#pragma unroll
+            for (int I = 0; I < NB; ++I) {
+                if constexpr (GATE != 2) Wb[I] = EL::cvt(U[I] * ld4(Gend + 16 * I + 4 * g4));
+                else Wb[I] = Ub[I];
+            }
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) {
                 if constexpr (GATE == 2) S[kt] *= ld4(Gc + 16 * kt + 4 * g4);
                 else S[kt] *= Gc[0];
-                S[kt] = contract(S[kt], NB,
-                    [&](int kb) { return ld_frag<E>(KsT + (16 * kt + r16) * PC + 16 * kb + 4 * g4); },
-                    [&](int kb) { return Ub[kb]; });
+            }
+#pragma unroll
+            for (int kb = 0; kb < NB; kb += 2) {
+                F a0[NKB], a1[NKB];
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt) {
+                    a0[kt] = ld_frag<E>(KsT + (16 * kt + r16) * PC + 16 * kb + 4 * g4);
+                    a1[kt] = ld_frag<E>(KsT + (16 * kt + r16) * PC + 16 * kb + 16 + 4 * g4);
+                }
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt) S[kt] = mfma_kb2(a0[kt], Wb[kb], a1[kt], Wb[kb + 1], S[kt]);
             }
         }
+        (void)clen;
+    };
+
+    if (nchunks > 0) {
+        state_issue<DK, CH, NW, E, GATE>(slot0, 0, bos, eos, cbase, h, kg, qg, vg, blocks, p, col0, tid);
+        if constexpr (GATE == 2) state_issue_g<DK, CH, NW>(gamv, 0, bos, eos, h, p, tid);
+    }
+    for (int c = 0; c < nchunks; c += 2) {
+        step(SlotTag<0>{}, c);
+        if (c + 1 < nchunks) step(SlotTag<1>{}, c + 1);
+    }
+    lds_barrier();
+    if (nchunks > 0) {
+        const int64_t tl = bos + (int64_t)(nchunks - 1) * CH;
+        flush(tl, (int)(eos - tl));
     }
 
     if (p.ht && wvalid) {
 #pragma unroll
         for (int kt = 0; kt < NKB; ++kt)
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                p.ht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV + wcol + r16] = S[kt][j];
+            for (int j = 0; j < 4; ++j) p.ht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] = S[kt][j];
     }
 }
 
+// ===========================================================================
+// launch
+// ===========================================================================
+// The delta rule is a template parameter of the state kernel: a run-time
+// branch around the TE product put a control-flow join right after its last
+// MFMA, and for chunk_state_kernel<64, 64, 2, bf16/f16, 2> hipcc (AMD clang 22)
+// then emitted reads of that MFMA's accumulators without the required wait
+// states (wrong outputs in token block 3).  Without the join there is no
+// such read.
+template <int DK, int CH, typename E, int GATE, bool DELTA>
+static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hipStream_t stream) {
+    if constexpr (StateLayout<DK, CH, 4, E, GATE>::FITS) {
+        if (nw == 4) {
+            hipLaunchKernelGGL((chunk_state_kernel<DK, CH, 4, E, GATE, DELTA>), dim3((unsigned)state_blocks),
+                               dim3(256), 0, stream, p);
+            return;
+        }
+    }
+    hipLaunchKernelGGL((chunk_state_kernel<DK, CH, 2, E, GATE, DELTA>), dim3((unsigned)state_blocks), dim3(128), 0,
+                       stream, p);
+}
+
 template <int DK, int CH, typename E, int GATE>
-static hipError_t launch_chunk(const ChunkParams &p, hipStream_t stream) {
-    constexpr int NW = 4;
-    const int64_t blocks = (int64_t)p.n_seqs * p.H * p.n_tiles;
-    if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((chunk_fwd_kernel<DK, CH, NW, E, GATE>), dim3((unsigned)blocks), dim3(64 * NW),
-                       0, stream, p);
+static hipError_t launch_chunk(const ChunkParams &p, int nw, hipStream_t stream) {
+    const int64_t prep_blocks = (int64_t)p.n_chunk_slots * p.H;
+    if (prep_blocks > 0)
+        hipLaunchKernelGGL((chunk_prep_kernel<DK, CH, E, GATE>), dim3((unsigned)prep_blocks), dim3(256), 0,
+                           stream, p);
+    const int64_t units = (int64_t)p.geo.n_seqs * p.H;
+    const int64_t state_blocks = (units + 7) / 8 * 8 * p.n_tiles;
+    if (state_blocks > 0) {
+        if (p.use_delta) launch_state<DK, CH, E, GATE, true>(p, nw, state_blocks, stream);
+        else launch_state<DK, CH, E, GATE, false>(p, nw, state_blocks, stream);
+    }
     return hipGetLastError();
 }
 
-int chunk_tile_cols() { return 64; }
+template <int DK, int CH, typename E, int GATE>
+static int state_waves(int64_t units, int dv, int cus) {
+    // 64-column tiles once the (sequence, head) pairs fill the chip and the tile fits LDS
+    if (!StateLayout<DK, CH, 4, E, GATE>::FITS) return 2;
+    return units * ((dv + 63) / 64) >= cus ? 4 : 2;
+}
 
-// dtype x dk x chunk x gate dispatch
-hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, const ChunkParams &p,
+int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H) {
+    const int64_t es = dtype == 0 ? 4 : 2;
+    return chunk_slots * H * 2 * chunk * chunk * es;
+}
+
+template <int DK, int CH, typename E, int GATE>
+static hipError_t run_chunk(ChunkParams p, hipStream_t stream) {
+    const int nw = state_waves<DK, CH, E, GATE>((int64_t)p.geo.n_seqs * p.H, p.DV, device_cu_count());
+    p.n_tiles = (p.DV + 16 * nw - 1) / (16 * nw);
+    return launch_chunk<DK, CH, E, GATE>(p, nw, stream);
+}
+
+hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table,
                      hipStream_t stream) {
-#define VGDR_GATES(DK_, CH_, E_)                                                       \
-    return gate_vector ? launch_chunk<DK_, CH_, E_, 2>(p, stream)                      \
-                       : launch_chunk<DK_, CH_, E_, 1>(p, stream);
+    if (p.geo.n_seqs == 0) return hipSuccess;                  // nothing to do (and no table to read)
+    if (p.geo.cu) {
+        hipError_t e = varlen_prepare(p.geo.cu, p.geo.n_seqs, p.geo.n_tokens, chunk, table, stream);
+        if (e != hipSuccess) return e;
+        p.geo.chunk_offs = table + 2 * p.geo.n_seqs;
+        p.geo.order = table + 3 * p.geo.n_seqs + 1;
+    }
+#define VGDR_GATES(DK_, CH_, E_)                                                           \
+    return gate_vector ? run_chunk<DK_, CH_, E_, 2>(p, stream) : run_chunk<DK_, CH_, E_, 1>(p, stream);
     if (dtype == 1) {
         if (dk == 64) { if (chunk == 32) { VGDR_GATES(64, 32, __bf16) } VGDR_GATES(64, 64, __bf16) }
         if (chunk == 32) { VGDR_GATES(128, 32, __bf16) } VGDR_GATES(128, 64, __bf16)
@@ -527,8 +839,8 @@ hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, const ChunkP
         if (dk == 64) { if (chunk == 32) { VGDR_GATES(64, 32, _Float16) } VGDR_GATES(64, 64, _Float16) }
         if (chunk == 32) { VGDR_GATES(128, 32, _Float16) } VGDR_GATES(128, 64, _Float16)
     }
-    // fp32: the 128-key tile only fits LDS with 32-token chunks
-    if (dk == 64) { if (chunk == 32) { VGDR_GATES(64, 32, float) } VGDR_GATES(64, 64, float) }
+    // fp32 runs 32-token chunks (the double-buffered fp32 tiles of 64 tokens overflow LDS)
+    if (dk == 64) { VGDR_GATES(64, 32, float) }
     VGDR_GATES(128, 32, float)
 #undef VGDR_GATES
 }

@@ -41,22 +41,22 @@ template <> struct Elem<float> {
     using frag = f32x4;                       // one k-block share of a lane
     static constexpr int pad = 4;             // LDS row padding (elements)
     static constexpr float gate_range = 60.f; // KDA sub-block factorisation limit (nats)
-    __device__ static inline float to_f(float x) { return x; }
-    __device__ static inline float from_f(float x) { return x; }
-    __device__ static inline frag cvt(f32x4 x) { return x; }
-    __device__ static inline f32x4 tof(frag x) { return x; }
+    __device__ static __forceinline__ float to_f(float x) { return x; }
+    __device__ static __forceinline__ float from_f(float x) { return x; }
+    __device__ static __forceinline__ frag cvt(f32x4 x) { return x; }
+    __device__ static __forceinline__ f32x4 tof(frag x) { return x; }
 };
 
 template <> struct Elem<__bf16> {
     using frag = bf16x4;
     static constexpr int pad = 4;
     static constexpr float gate_range = 60.f;
-    __device__ static inline float to_f(__bf16 x) { return (float)x; }
-    __device__ static inline __bf16 from_f(float x) { return (__bf16)x; }
-    __device__ static inline frag cvt(f32x4 x) {
+    __device__ static __forceinline__ float to_f(__bf16 x) { return (float)x; }
+    __device__ static __forceinline__ __bf16 from_f(float x) { return (__bf16)x; }
+    __device__ static __forceinline__ frag cvt(f32x4 x) {
         return frag{(__bf16)x[0], (__bf16)x[1], (__bf16)x[2], (__bf16)x[3]};
     }
-    __device__ static inline f32x4 tof(frag x) {
+    __device__ static __forceinline__ f32x4 tof(frag x) {
         return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
     }
 };
@@ -65,12 +65,12 @@ template <> struct Elem<_Float16> {
     using frag = f16x4;
     static constexpr int pad = 4;
     static constexpr float gate_range = 8.f;  // fp16 overflows past e^11
-    __device__ static inline float to_f(_Float16 x) { return (float)x; }
-    __device__ static inline _Float16 from_f(float x) { return (_Float16)x; }
-    __device__ static inline frag cvt(f32x4 x) {
+    __device__ static __forceinline__ float to_f(_Float16 x) { return (float)x; }
+    __device__ static __forceinline__ _Float16 from_f(float x) { return (_Float16)x; }
+    __device__ static __forceinline__ frag cvt(f32x4 x) {
         return frag{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
     }
-    __device__ static inline f32x4 tof(frag x) {
+    __device__ static __forceinline__ f32x4 tof(frag x) {
         return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
     }
 };
@@ -78,33 +78,33 @@ template <> struct Elem<_Float16> {
 // ---------------------------------------------------------------------------
 // MFMA over k-blocks
 // ---------------------------------------------------------------------------
-__device__ inline f32x4 mfma_kb1(f32x4 a, f32x4 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_kb1(f32x4 a, f32x4 b, f32x4 c) {
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[0], c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[1], c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[2], c, 0, 0, 0);
     c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[3], c, 0, 0, 0);
     return c;
 }
-__device__ inline f32x4 mfma_kb2(f32x4 a0, f32x4 b0, f32x4 a1, f32x4 b1, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_kb2(f32x4 a0, f32x4 b0, f32x4 a1, f32x4 b1, f32x4 c) {
     return mfma_kb1(a1, b1, mfma_kb1(a0, b0, c));
 }
 
-__device__ inline f32x4 mfma_kb2(bf16x4 a0, bf16x4 b0, bf16x4 a1, bf16x4 b1, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_kb2(bf16x4 a0, bf16x4 b0, bf16x4 a1, bf16x4 b1, f32x4 c) {
     bf16x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
     bf16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
-__device__ inline f32x4 mfma_kb1(bf16x4 a, bf16x4 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_kb1(bf16x4 a, bf16x4 b, f32x4 c) {
     const bf16x4 z = {};
     return mfma_kb2(a, b, z, z, c);
 }
 
-__device__ inline f32x4 mfma_kb2(f16x4 a0, f16x4 b0, f16x4 a1, f16x4 b1, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_kb2(f16x4 a0, f16x4 b0, f16x4 a1, f16x4 b1, f32x4 c) {
     f16x8 a = __builtin_shufflevector(a0, a1, 0, 1, 2, 3, 4, 5, 6, 7);
     f16x8 b = __builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7);
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
-__device__ inline f32x4 mfma_kb1(f16x4 a, f16x4 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_kb1(f16x4 a, f16x4 b, f32x4 c) {
     const f16x4 z = {};
     return mfma_kb2(a, b, z, z, c);
 }
@@ -112,7 +112,7 @@ __device__ inline f32x4 mfma_kb1(f16x4 a, f16x4 b, f32x4 c) {
 // c += sum over k-blocks kb in [0, n) of A(kb) * B(kb); fa / fb return the
 // lane's fragment of k-block kb.
 template <typename FA, typename FB>
-__device__ inline f32x4 contract(f32x4 c, int n, FA fa, FB fb) {
+__device__ __forceinline__ f32x4 contract(f32x4 c, int n, FA fa, FB fb) {
     int kb = 0;
 #pragma unroll
     for (; kb + 1 < n; kb += 2) c = mfma_kb2(fa(kb), fb(kb), fa(kb + 1), fb(kb + 1), c);
@@ -122,18 +122,18 @@ __device__ inline f32x4 contract(f32x4 c, int n, FA fa, FB fb) {
 
 // LDS fragment access: four consecutive elements, aligned to their size.
 template <typename E>
-__device__ inline typename Elem<E>::frag ld_frag(const E *p) {
+__device__ __forceinline__ typename Elem<E>::frag ld_frag(const E *p) {
     return *reinterpret_cast<const typename Elem<E>::frag *>(p);
 }
 template <typename E>
-__device__ inline void st_frag(E *p, typename Elem<E>::frag x) {
+__device__ __forceinline__ void st_frag(E *p, typename Elem<E>::frag x) {
     *reinterpret_cast<typename Elem<E>::frag *>(p) = x;
 }
 
-__device__ inline f32x4 ld4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
-__device__ inline void st4(float *p, f32x4 x) { *reinterpret_cast<f32x4 *>(p) = x; }
+__device__ __forceinline__ f32x4 ld4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+__device__ __forceinline__ void st4(float *p, f32x4 x) { *reinterpret_cast<f32x4 *>(p) = x; }
 
-__device__ inline f32x4 exp4(f32x4 x) {
+__device__ __forceinline__ f32x4 exp4(f32x4 x) {
     return f32x4{__expf(x[0]), __expf(x[1]), __expf(x[2]), __expf(x[3])};
 }
 

@@ -7,18 +7,30 @@
 
 namespace vgdr {
 
+// Sequence geometry shared by the chunk kernels: a dense batch (cu == NULL,
+// n_seqs sequences of T tokens) or a packed one indexed by cu (clamped).
+struct SeqGeom {
+    const int32_t *cu;            // [n_seqs + 1] or NULL
+    const int32_t *chunk_offs;    // [n_seqs + 1] first global chunk of each sequence (packed only)
+    const int32_t *order;         // schedule position -> sequence, or NULL (identity)
+    int64_t T;                    // tokens per sequence (dense)
+    int64_t n_tokens;             // total tokens
+    int n_seqs;
+    int chunks_per_seq;           // dense: ceil(T / CH)
+};
+
 struct ChunkParams {
+    SeqGeom geo;
     const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
     const float *g;               // [n_tokens, H] or [n_tokens, H, dk]; NULL = no gate
     const float *beta;            // [n_tokens, H]; unused without the delta rule
     void *o;                      // [n_tokens, H, dv]
     const float *h0;              // [n_seqs, H, dk, dv] or NULL
     float *ht;                    // [n_seqs, H, dk, dv] or NULL
-    const int32_t *cu;            // [n_seqs + 1] or NULL (dense)
-    const int32_t *order;         // schedule: position -> sequence, or NULL (identity)
-    int64_t T;                    // tokens per sequence (dense batch)
-    int64_t n_tokens;             // total tokens (clamp bound for cu)
-    int H, DV, n_seqs, n_tiles;
+    void *blocks;                 // per (chunk, head): TE and A tiles, fragment order
+    int H, DV;
+    int n_tiles;                  // dv tiles per (sequence, head)
+    int n_chunk_slots;            // chunk-prep grid size / H (upper bound of chunks)
     int use_delta;
     float scale;
 };
@@ -39,14 +51,18 @@ struct RecParams {
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.
-hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, const ChunkParams &p,
+// Runs the varlen schedule (if packed), the chunk-prep and the chunk-state
+// kernels on `stream`.
+hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table,
                      hipStream_t stream);
-int chunk_tile_cols();
+int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H);
 
 hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
                          hipStream_t stream);
 
 hipError_t varlen_prepare(const int32_t *cu, int n_seqs, int64_t n_tokens, int chunk,
                           int32_t *ws, hipStream_t stream);
+
+int device_cu_count();
 
 }  // namespace vgdr

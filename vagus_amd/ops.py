@@ -158,16 +158,15 @@ def _chunk(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_
     o = c.new_output()
     S = c.new_state() if output_final_state else None
     L = _lib.load()
-    ws = None
+    varlen = c.cu is not None
+    nbytes = L.vgdr_chunk_workspace_size(_DTYPES[c.dtype], c.B, c.T, c.H, c.dkp, c.N, int(varlen),
+                                         int(chunk_size))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
     with torch.cuda.device(c.device):
-        stream = _stream(c.device)
-        if c.cu is not None and c.N > 0:
-            ws = torch.empty(L.vgdr_varlen_workspace_size(c.N), dtype=torch.uint8, device=c.device)
-            _lib.check(L.vgdr_varlen_prepare(_ptr(c.cu), c.N, c.T, int(chunk_size), _ptr(ws), stream))
         _lib.check(L.vgdr_chunk_fwd(
             _DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
-            _ptr(c.beta), _ptr(o), _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws),
-            c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size), stream))
+            _ptr(c.beta), _ptr(o), _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws), nbytes,
+            c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size), _stream(c.device)))
     return c.unpad_o(o), c.unpad_state(S)
 
 
