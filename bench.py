@@ -10,12 +10,22 @@ over the whole batch with its inputs resident in HBM; value = tokens/s
 (B*T tokens per step).  Three copies of the inputs (3 x 218 MB) are rotated
 so that no step finds its operands in the 256 MB Infinity Cache.
 
+The prefill runs as two kernels per call: chunk_prep (every (chunk, head) in
+parallel: the intra-chunk Q K^T and K K^T products and the triangular
+inverse) and chunk_state (the sequential chunk recurrence per (sequence,
+head, dv tile)), the dominant one.  The timed steps issue them as
+vgdr_chunk_prep + vgdr_chunk_state with an event in between (identical GPU
+work to vgdr_chunk_fwd), so each kernel has its own event-timed duration.
+
 Also reported on the same line:
-  roofline      the prefill kernel's achieved algorithmic TFLOP/s (180,224 FLOP
-                per token-head, the forward third of chunk_scan_flops) over bf16
-                dense MFMA peak, from HIP events around each launch on the
-                kernel's stream; `traffic` = measured HBM bytes per launch
-                (rocprofv3 FETCH_SIZE + WRITE_SIZE, see profiles/) when present
+  roofline      chunk_state's achieved algorithmic TFLOP/s over bf16 dense MFMA
+                peak: 6 dk dv + 4 C dv FLOP per token-head (the three state
+                products and the two intra-chunk products with V) per launch,
+                over its event-timed average duration; `traffic` = its measured
+                HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE scaled
+                by a plain-copy calibration, profiles/traffic.json) when present
+  path          both kernels together against the reference's own count,
+                forward chunk_scan_flops / 3 = 180,224 FLOP per token-head
   decode        one recurrent decode step at the 1.3B layer shape (B=64 H=16
                 dk=dv=128) rotating 24 layer states (1.5 GB), in algorithmic
                 GB/s (132,104 B per sequence-head) over 8 TB/s
@@ -40,52 +50,75 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0          # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0              # MI355X HBM3E
-FLOP_PER_TOKEN_HEAD = 180224       # chunk_scan_flops(128, 128, 64, True) / 3
+DK = DV = 128
+CHUNK = 64
+FLOP_PER_TOKEN_HEAD = 180224       # chunk_scan_flops(128, 128, 64, True) / 3 (the reference's count)
 PREFILL_BYTES_PER_TOKEN_HEAD = 1032
 DECODE_BYTES_PER_SEQ_HEAD = 132104
+# chunk_state per token-head: (K*G) S, (Q*G) S, (K*Gend)^T U~ (2 dk dv each) + TE X, A U~ (2 C dv each)
+STATE_FLOP_PER_TOKEN_HEAD = 6 * DK * DV + 4 * CHUNK * DV                    # 131,072
+# chunk_state bytes per token-head: q, k, v (bf16), scalar g, TE + A blocks (2 C^2 bf16 per chunk),
+# o (bf16), entry + final state (2 dk dv fp32 per sequence-head, amortised over T = 4096)
+STATE_BYTES_PER_TOKEN_HEAD = 2 * (2 * DK + DV) + 4 + 2 * 2 * CHUNK + 2 * DV + 2 * DK * DV * 4 // 4096
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
+    """Timed chunked prefill.  Each step issues chunk_prep, an event, then
+    chunk_state on the current stream; returns host-clock totals and the two
+    kernels' event-timed durations."""
+    xs = [workloads.workload(name, device='cuda') for _ in range(copies)]
+    x0 = xs[0]
+    gate = 'none' if x0.g is None else ('vector' if x0.g.dim() == 4 else 'scalar')
+
+    def step(i, mid=None):
+        x = xs[i % copies]
+        ops.chunk_scan(x.q, x.k, x.v, x.g, x.beta, gate=gate, delta=True, initial_state=x.initial_state,
+                       output_final_state=True, cu_seqlens=x.cu_seqlens, phase_event=mid)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        a, m, b = ev[i]
+        a.record(stream)
+        step(i, m)
+        b.record(stream)
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    prep_ms = [a.elapsed_time(m) for a, m, _ in ev]
+    state_ms = [m.elapsed_time(b) for _, m, b in ev]
+    tokens = x0.q.shape[0] * x0.q.shape[1]
+    H = x0.q.shape[2]
+    del xs
+    op_ms = statistics.mean(p + q for p, q in zip(prep_ms, state_ms))
+    return dict(tokens=tokens, H=H, total_s=total, tok_s=steps * tokens / total,
+                prep_ms=statistics.mean(prep_ms), state_ms=statistics.mean(state_ms), op_ms=op_ms,
+                path_tflops=tokens * H * FLOP_PER_TOKEN_HEAD / (op_ms * 1e-3) / 1e12,
+                state_tflops=tokens * H * STATE_FLOP_PER_TOKEN_HEAD / (statistics.mean(state_ms) * 1e-3) / 1e12)
+
+
 def time_steps(torch, fn, steps, warmup, rotate):
-    """Run `warmup` untimed steps, then exactly `steps` timed steps; returns
-    (total seconds by host clock around synchronize, per-step event ms list)."""
+    """`warmup` untimed steps, then exactly `steps` timed ones; returns (host
+    seconds around synchronize, per-step event ms)."""
     for i in range(warmup):
         fn(i % rotate)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         ev[i][0].record(stream)
         fn(i % rotate)
         ev[i][1].record(stream)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    return t1 - t0, [a.elapsed_time(b) for a, b in ev]
-
-
-def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
-    xs = [workloads.workload(name, device='cuda') for _ in range(copies)]
-    kda = xs[0].g is not None and xs[0].g.dim() == 4
-    fn_op = ops.chunk_kda if kda else ops.chunk_gated_delta_rule
-
-    def step(i):
-        x = xs[i]
-        fn_op(x.q, x.k, x.v, x.g, x.beta, initial_state=x.initial_state, output_final_state=True,
-              cu_seqlens=x.cu_seqlens)
-
-    total, ms = time_steps(torch, step, steps, warmup, copies)
-    tokens = xs[0].q.shape[0] * xs[0].q.shape[1]
-    H = xs[0].q.shape[2]
-    avg_ms = statistics.mean(ms)
-    del xs
-    return dict(tokens=tokens, H=H, total_s=total, step_ms=ms, avg_ms=avg_ms,
-                tok_s=steps * tokens / total,
-                tflops=tokens * H * FLOP_PER_TOKEN_HEAD / (avg_ms * 1e-3) / 1e12)
+    return time.perf_counter() - t0, [a.elapsed_time(b) for a, b in ev]
 
 
 def bench_decode(torch, ops, workloads, steps, warmup, B=64, H=16, layers=24):
@@ -133,15 +166,16 @@ def cpu_baseline(torch, workloads):
                       f'in fp32, median of 3 after 1 warmup, {med:.2f} s per run, {cpu}'}
 
 
-def measured_traffic(workload):
-    """HBM bytes per launch of the prefill kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (profiles/traffic.json), if one exists."""
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` ('chunk_state' / 'chunk_prep') on
+    `workload`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/traffic.json), if one exists."""
     path = os.path.join(ROOT, 'profiles', 'traffic.json')
     try:
         with open(path) as f:
-            rec = json.load(f).get(workload)
-        return None if rec is None else int(rec['bytes_per_launch'])
-    except (OSError, ValueError, KeyError):
+            rec = json.load(f)[workload][kernel]
+        return int(rec['bytes_per_launch'])
+    except (OSError, ValueError, KeyError, TypeError):
         return None
 
 
@@ -188,17 +222,20 @@ def main():
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
             r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))
-            extra[name] = {'tok_s': round(r['tok_s'], 1), 'ms_per_step': round(r['avg_ms'], 4),
-                           'tflops': round(r['tflops'], 2),
-                           'frac_mfma': round(r['tflops'] / PEAK_BF16_TFLOPS, 5), 'tokens': r['tokens']}
+            extra[name] = {'tok_s': round(r['tok_s'], 1), 'op_ms': round(r['op_ms'], 4),
+                           'prep_ms': round(r['prep_ms'], 4), 'state_ms': round(r['state_ms'], 4),
+                           'path_tflops': round(r['path_tflops'], 2),
+                           'path_frac_mfma': round(r['path_tflops'] / PEAK_BF16_TFLOPS, 5),
+                           'state_tflops': round(r['state_tflops'], 2), 'tokens': r['tokens']}
     cpu = None
     if not args.no_cpu_baseline:
         log('[bench] cpu baseline')
         cpu = cpu_baseline(torch, workloads)
 
     tokens, H = pre['tokens'], pre['H']
-    achieved = pre['tflops']
-    hbm_gbs = tokens * H * PREFILL_BYTES_PER_TOKEN_HEAD / (pre['avg_ms'] * 1e-3) / 1e9
+    achieved = pre['state_tflops']
+    state_gbs = tokens * H * STATE_BYTES_PER_TOKEN_HEAD / (pre['state_ms'] * 1e-3) / 1e9
+    path_gbs = tokens * H * PREFILL_BYTES_PER_TOKEN_HEAD / (pre['op_ms'] * 1e-3) / 1e9
     line = {
         'metric': 'prefill tok/s + MFMA util; decode-step HBM GB/s vs peak (GDN/KDA, 1 GPU)',
         'value': round(pre['tok_s'], 1),
@@ -217,9 +254,17 @@ def main():
                    'tokens_per_step': tokens},
         'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS,
                      'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_BF16_TFLOPS, 5),
-                     'traffic': measured_traffic('gdn_340m'),
-                     'kernel_avg_ms': round(pre['avg_ms'], 4),
-                     'hbm_algorithmic_GBs': round(hbm_gbs, 1)},
+                     'traffic': measured_traffic('gdn_340m', 'chunk_state'),
+                     'kernel': 'chunk_state_kernel', 'kernel_avg_ms': round(pre['state_ms'], 4),
+                     'flop_per_launch': tokens * H * STATE_FLOP_PER_TOKEN_HEAD,
+                     'algorithmic_bytes_per_launch': tokens * H * STATE_BYTES_PER_TOKEN_HEAD,
+                     'hbm_algorithmic_GBs': round(state_gbs, 1)},
+        'path': {'kernels': 'chunk_prep_kernel + chunk_state_kernel', 'op_ms': round(pre['op_ms'], 4),
+                 'prep_ms': round(pre['prep_ms'], 4), 'state_ms': round(pre['state_ms'], 4),
+                 'achieved_tflops': round(pre['path_tflops'], 2),
+                 'frac_mfma': round(pre['path_tflops'] / PEAK_BF16_TFLOPS, 5),
+                 'flop_per_token_head': FLOP_PER_TOKEN_HEAD, 'hbm_algorithmic_GBs': round(path_gbs, 1),
+                 'prep_traffic': measured_traffic('gdn_340m', 'chunk_prep')},
         'cpu_baseline': cpu,
         **extra,
     }

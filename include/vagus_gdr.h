@@ -92,6 +92,31 @@ int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta,
                    float scale, int chunk_size, hipStream_t stream);
 
 /*
+ * The two phases of vgdr_chunk_fwd as separate calls (same arguments, same
+ * checks; no reference counterpart).  vgdr_chunk_prep builds the packed-batch
+ * schedule and, for every (chunk, head) in parallel, the state-independent
+ * intra-chunk blocks, into `workspace`; it reads q, k, g, beta and cu_seqlens.
+ * vgdr_chunk_state then runs the sequential chunk recurrence from that
+ * workspace and writes o and final_state.  prep followed by state on one
+ * stream (same arguments, workspace untouched in between) equals
+ * vgdr_chunk_fwd.  For callers that time or schedule the phases separately.
+ */
+int vgdr_chunk_prep(int dtype, int gate_kind, int use_delta,
+                    const void *q, const void *k, const void *v,
+                    const float *g, const float *beta,
+                    void *o, const float *initial_state, float *final_state,
+                    const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                    int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                    float scale, int chunk_size, hipStream_t stream);
+int vgdr_chunk_state(int dtype, int gate_kind, int use_delta,
+                     const void *q, const void *k, const void *v,
+                     const float *g, const float *beta,
+                     void *o, const float *initial_state, float *final_state,
+                     const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                     int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                     float scale, int chunk_size, hipStream_t stream);
+
+/*
  * Token-by-token recurrence.  The decode step is T = 1 with
  * initial_state == final_state (in place), replacing recurrent_scan at
  * linear_attention.py:945-947 and the state.copy_ at :950.  Any T works (the

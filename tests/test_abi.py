@@ -37,11 +37,11 @@ def test_library_loads_and_exports_every_symbol():
     assert L.vgdr_varlen_workspace_size(-1) == 0
 
 
-def _chunk_call(**over):
+def _chunk_call(fn='vgdr_chunk_fwd', **over):
     a = dict(dtype=1, gate=1, delta=1, q=None, k=None, v=None, g=None, beta=None, o=None, h0=None,
              ht=None, cu=None, ws=None, nbytes=0, B=2, T=0, H=4, dk=128, dv=128, N=2, scale=1.0, chunk=64)
     a.update(over)
-    return _lib.load().vgdr_chunk_fwd(a['dtype'], a['gate'], a['delta'], a['q'], a['k'], a['v'], a['g'],
+    return getattr(_lib.load(), fn)(a['dtype'], a['gate'], a['delta'], a['q'], a['k'], a['v'], a['g'],
                                       a['beta'], a['o'], a['h0'], a['ht'], a['cu'], a['ws'], a['nbytes'],
                                       a['B'], a['T'], a['H'], a['dk'], a['dv'], a['N'], a['scale'],
                                       a['chunk'], None)
@@ -74,6 +74,17 @@ def test_argument_checks_return_status_codes():
     assert rc == _lib.VGDR_ERR_UNSUPPORTED
     assert L.vgdr_varlen_prepare(None, 4, 100, 64, None, None) == _lib.VGDR_ERR_INVALID
     assert L.vgdr_varlen_prepare(None, 0, 0, 64, None, None) == _lib.VGDR_OK
+
+
+@pytest.mark.parametrize('fn', ['vgdr_chunk_prep', 'vgdr_chunk_state'])
+def test_phase_entry_points_check_like_the_fused_one(fn):
+    L = _lib.load()
+    assert _chunk_call(fn, dtype=7) == _lib.VGDR_ERR_INVALID
+    assert fn.encode() in L.vgdr_last_error()
+    assert _chunk_call(fn, dk=256) == _lib.VGDR_ERR_UNSUPPORTED
+    assert _chunk_call(fn, T=64, q=16, k=32, v=48, o=64, g=80, beta=96, ws=None) == _lib.VGDR_ERR_INVALID
+    assert b'workspace' in L.vgdr_last_error()
+    assert _chunk_call(fn, B=0, N=0) == _lib.VGDR_OK                  # no sequences: nothing to launch
 
 
 def test_status_codes_map_to_reference_exceptions():

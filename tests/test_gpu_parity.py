@@ -203,6 +203,22 @@ def test_varlen_schedule_table_bit_exact():
         assert np.array_equal(got[3 * N + 1:], want['order'])
 
 
+@pytest.mark.parametrize('gate', ['scalar', 'vector'])
+def test_split_phases_equal_fused_call_bit_exact(gate):
+    """vgdr_chunk_prep + vgdr_chunk_state (an event between them) == vgdr_chunk_fwd, bit for bit,
+    for a dense and a packed batch."""
+    case(f'prep + state vs fwd, {gate}')
+    dense = workloads.make_inputs(2, 200, 2, 128, 128, gate=gate, dtype=torch.bfloat16, s0_scale=0.1, seed=12)
+    packed = workloads.make_varlen_inputs([5, 130, 64, 0, 257], 2, 128, 128, gate=gate, dtype=torch.bfloat16,
+                                          s0_scale=0.1, seed=13)
+    for x in (dense.to(DEV), packed.to(DEV)):
+        kw = dict(gate=gate, delta=True, scale=0.1, initial_state=x.initial_state, output_final_state=True,
+                  cu_seqlens=x.cu_seqlens)
+        o1, S1 = ops.chunk_scan(x.q, x.k, x.v, x.g, x.beta, **kw)
+        o2, S2 = ops.chunk_scan(x.q, x.k, x.v, x.g, x.beta, phase_event=torch.cuda.Event(), **kw)
+        assert torch.equal(o1, o2) and torch.equal(S1, S2)
+
+
 def test_empty_sequence_passes_state_through():
     case('empty input')
     S0 = torch.randn(2, 2, 64, 64, device=DEV)

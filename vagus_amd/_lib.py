@@ -24,6 +24,10 @@ SIGNATURES = {
     'vgdr_chunk_workspace_size': (_L, [_I, _L, _L, _L, _L, _L, _I, _I]),
     'vgdr_chunk_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                             _L, _L, _L, _L, _L, _L, _F, _I, _P]),
+    'vgdr_chunk_prep': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
+                             _L, _L, _L, _L, _L, _L, _F, _I, _P]),
+    'vgdr_chunk_state': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
+                              _L, _L, _L, _L, _L, _L, _F, _I, _P]),
     'vgdr_recurrent_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                 _L, _L, _L, _L, _L, _L, _F, _P]),
     'vgdr_varlen_workspace_size': (_L, [_L]),

@@ -89,6 +89,49 @@ ChunkWs chunk_layout(int dtype, int chunk, int64_t B, int64_t T, int64_t H, int6
     return w;
 }
 
+// the three chunk entry points: validation, workspace layout, then the phases asked for
+int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_delta, const void *q, const void *k,
+               const void *v, const float *g, const float *beta, void *o, const float *initial_state,
+               float *final_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B,
+               int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
+               hipStream_t stream) {
+    g_err[0] = 0;
+    int rc = check_common(fn, dtype, gate_kind, use_delta, q, k, v, g, beta, o, cu_seqlens,
+                          B, T, H, dk, dv, n_seqs);
+    if (rc) return rc;
+    if (dv <= 0 || dv % 16)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: dv=%lld (must be a positive multiple of 16)", fn, (long long)dv);
+    if (!aligned16(o)) return fail(VGDR_ERR_INVALID, "%s: o must be 16-byte aligned", fn);
+    const int chunk = effective_chunk(dtype, dk, chunk_size);
+    const ChunkWs ws = chunk_layout(dtype, chunk, B, T, H, n_seqs, cu_seqlens != nullptr);
+    if (ws.total > 0 && (!workspace || workspace_bytes < ws.total || !aligned16(workspace)))
+        return fail(VGDR_ERR_INVALID, "%s: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)", fn,
+                    (long long)ws.total, (long long)workspace_bytes, workspace);
+    if (ws.slots * H > 0x7fffffffLL || (n_seqs * H + 7) / 8 * 8 * ((dv + 31) / 32) > 0x7fffffffLL)
+        return fail(VGDR_ERR_INVALID, "%s: grid too large", fn);
+    vgdr::ChunkParams p{};
+    p.geo.cu = cu_seqlens;
+    p.geo.T = T;
+    p.geo.n_tokens = B * T;
+    p.geo.n_seqs = (int)n_seqs;
+    p.geo.chunks_per_seq = (int)((T + chunk - 1) / chunk);
+    p.q = q; p.k = k; p.v = v;
+    p.g = gate_kind == VGDR_GATE_NONE ? nullptr : g;
+    p.beta = beta;
+    p.o = o;
+    p.h0 = initial_state;
+    p.ht = final_state;
+    p.blocks = static_cast<char *>(workspace) + ws.blocks_off;
+    p.H = (int)H;
+    p.DV = (int)dv;
+    p.n_chunk_slots = (int)ws.slots;
+    p.use_delta = use_delta ? 1 : 0;
+    p.scale = scale;
+    int32_t *table = cu_seqlens ? static_cast<int32_t *>(workspace) : nullptr;
+    return hip_status(vgdr::chunk_fwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, p, table, phases, stream),
+                      fn);
+}
+
 }  // namespace
 
 namespace vgdr {
@@ -119,49 +162,22 @@ int64_t vgdr_chunk_workspace_size(int dtype, int64_t B, int64_t T, int64_t H, in
     return chunk_layout(dtype, chunk, B, T, H, n_seqs, varlen).total;
 }
 
-int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
-                   const float *g, const float *beta, void *o, const float *initial_state,
-                   float *final_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
-                   int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
-                   int chunk_size, hipStream_t stream) {
-    g_err[0] = 0;
-    int rc = check_common("vgdr_chunk_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o, cu_seqlens,
-                          B, T, H, dk, dv, n_seqs);
-    if (rc) return rc;
-    if (dv <= 0 || dv % 16)
-        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_chunk_fwd: dv=%lld (must be a positive multiple of 16)",
-                    (long long)dv);
-    if (!aligned16(o)) return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: o must be 16-byte aligned");
-    const int chunk = effective_chunk(dtype, dk, chunk_size);
-    const ChunkWs ws = chunk_layout(dtype, chunk, B, T, H, n_seqs, cu_seqlens != nullptr);
-    if (ws.total > 0 && (!workspace || workspace_bytes < ws.total || !aligned16(workspace)))
-        return fail(VGDR_ERR_INVALID,
-                    "vgdr_chunk_fwd: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)",
-                    (long long)ws.total, (long long)workspace_bytes, workspace);
-    if (ws.slots * H > 0x7fffffffLL || (n_seqs * H + 7) / 8 * 8 * ((dv + 31) / 32) > 0x7fffffffLL)
-        return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd: grid too large");
-    vgdr::ChunkParams p{};
-    p.geo.cu = cu_seqlens;
-    p.geo.T = T;
-    p.geo.n_tokens = B * T;
-    p.geo.n_seqs = (int)n_seqs;
-    p.geo.chunks_per_seq = (int)((T + chunk - 1) / chunk);
-    p.q = q; p.k = k; p.v = v;
-    p.g = gate_kind == VGDR_GATE_NONE ? nullptr : g;
-    p.beta = beta;
-    p.o = o;
-    p.h0 = initial_state;
-    p.ht = final_state;
-    p.blocks = static_cast<char *>(workspace) + ws.blocks_off;
-    p.H = (int)H;
-    p.DV = (int)dv;
-    p.n_chunk_slots = (int)ws.slots;
-    p.use_delta = use_delta ? 1 : 0;
-    p.scale = scale;
-    int32_t *table = cu_seqlens ? static_cast<int32_t *>(workspace) : nullptr;
-    return hip_status(vgdr::chunk_fwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, p, table, stream),
-                      "vgdr_chunk_fwd launch");
+#define VGDR_CHUNK_ARGS                                                                                    \
+    int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v, const float *g,     \
+        const float *beta, void *o, const float *initial_state, float *final_state, const int32_t *cu_seqlens, \
+        void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,     \
+        int64_t n_seqs, float scale, int chunk_size, hipStream_t stream
+#define VGDR_CHUNK_PASS                                                                                    \
+    dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state, final_state, cu_seqlens, workspace,      \
+        workspace_bytes, B, T, H, dk, dv, n_seqs, scale, chunk_size, stream
+
+int vgdr_chunk_fwd(VGDR_CHUNK_ARGS) {
+    return chunk_call("vgdr_chunk_fwd", vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, VGDR_CHUNK_PASS);
 }
+int vgdr_chunk_prep(VGDR_CHUNK_ARGS) { return chunk_call("vgdr_chunk_prep", vgdr::CHUNK_PREP, VGDR_CHUNK_PASS); }
+int vgdr_chunk_state(VGDR_CHUNK_ARGS) { return chunk_call("vgdr_chunk_state", vgdr::CHUNK_STATE, VGDR_CHUNK_PASS); }
+#undef VGDR_CHUNK_ARGS
+#undef VGDR_CHUNK_PASS
 
 int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
                        const float *g, const float *beta, void *o, const float *initial_state,

@@ -787,14 +787,14 @@ static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hip
 }
 
 template <int DK, int CH, typename E, int GATE>
-static hipError_t launch_chunk(const ChunkParams &p, int nw, hipStream_t stream) {
+static hipError_t launch_chunk(const ChunkParams &p, int nw, int phases, hipStream_t stream) {
     const int64_t prep_blocks = (int64_t)p.n_chunk_slots * p.H;
-    if (prep_blocks > 0)
+    if ((phases & CHUNK_PREP) && prep_blocks > 0)
         hipLaunchKernelGGL((chunk_prep_kernel<DK, CH, E, GATE>), dim3((unsigned)prep_blocks), dim3(256), 0,
                            stream, p);
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
     const int64_t state_blocks = (units + 7) / 8 * 8 * p.n_tiles;
-    if (state_blocks > 0) {
+    if ((phases & CHUNK_STATE) && state_blocks > 0) {
         if (p.use_delta) launch_state<DK, CH, E, GATE, true>(p, nw, state_blocks, stream);
         else launch_state<DK, CH, E, GATE, false>(p, nw, state_blocks, stream);
     }
@@ -814,23 +814,25 @@ int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H)
 }
 
 template <int DK, int CH, typename E, int GATE>
-static hipError_t run_chunk(ChunkParams p, hipStream_t stream) {
+static hipError_t run_chunk(ChunkParams p, int phases, hipStream_t stream) {
     const int nw = state_waves<DK, CH, E, GATE>((int64_t)p.geo.n_seqs * p.H, p.DV, device_cu_count());
     p.n_tiles = (p.DV + 16 * nw - 1) / (16 * nw);
-    return launch_chunk<DK, CH, E, GATE>(p, nw, stream);
+    return launch_chunk<DK, CH, E, GATE>(p, nw, phases, stream);
 }
 
-hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table,
+hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table, int phases,
                      hipStream_t stream) {
     if (p.geo.n_seqs == 0) return hipSuccess;                  // nothing to do (and no table to read)
     if (p.geo.cu) {
-        hipError_t e = varlen_prepare(p.geo.cu, p.geo.n_seqs, p.geo.n_tokens, chunk, table, stream);
-        if (e != hipSuccess) return e;
+        if (phases & CHUNK_PREP) {
+            hipError_t e = varlen_prepare(p.geo.cu, p.geo.n_seqs, p.geo.n_tokens, chunk, table, stream);
+            if (e != hipSuccess) return e;
+        }
         p.geo.chunk_offs = table + 2 * p.geo.n_seqs;
         p.geo.order = table + 3 * p.geo.n_seqs + 1;
     }
 #define VGDR_GATES(DK_, CH_, E_)                                                           \
-    return gate_vector ? run_chunk<DK_, CH_, E_, 2>(p, stream) : run_chunk<DK_, CH_, E_, 1>(p, stream);
+    return gate_vector ? run_chunk<DK_, CH_, E_, 2>(p, phases, stream) : run_chunk<DK_, CH_, E_, 1>(p, phases, stream);
     if (dtype == 1) {
         if (dk == 64) { if (chunk == 32) { VGDR_GATES(64, 32, __bf16) } VGDR_GATES(64, 64, __bf16) }
         if (chunk == 32) { VGDR_GATES(128, 32, __bf16) } VGDR_GATES(128, 64, __bf16)

@@ -51,9 +51,11 @@ struct RecParams {
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.
-// Runs the varlen schedule (if packed), the chunk-prep and the chunk-state
-// kernels on `stream`.
-hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table,
+// phases: CHUNK_PREP runs the packed-batch schedule (if packed) and the
+// chunk-prep kernel; CHUNK_STATE runs the chunk-state kernel, which reads what
+// the prep phase left in the workspace.  Both are launched on `stream`.
+enum { CHUNK_PREP = 1, CHUNK_STATE = 2 };
+hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table, int phases,
                      hipStream_t stream);
 int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H);
 

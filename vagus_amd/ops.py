@@ -150,8 +150,15 @@ class _Call:
         return S[:, :, :self.dk, :self.dv].contiguous()
 
 
-def _chunk(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state, cu_seqlens,
-           chunk_size):
+def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None, output_final_state=False,
+               cu_seqlens=None, chunk_size=64, phase_event=None):
+    """Chunkwise prefill, the general form behind chunk_gated_delta_rule,
+    chunk_kda and chunk_simple_gla: gate in {'none', 'scalar', 'vector'},
+    delta selects the delta rule.  Returns (o, final_state or None).
+
+    phase_event: optional torch.cuda.Event recorded on the current stream
+    between the chunk-prep and the chunk-state kernels (the same two launches
+    either way), so that a caller can time the two phases separately."""
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=gate, delta=delta,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
     scale = c.dk ** -0.5 if scale is None else float(scale)
@@ -163,10 +170,15 @@ def _chunk(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_
                                          int(chunk_size))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
     with torch.cuda.device(c.device):
-        _lib.check(L.vgdr_chunk_fwd(
-            _DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
-            _ptr(c.beta), _ptr(o), _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws), nbytes,
-            c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size), _stream(c.device)))
+        args = (_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
+                _ptr(c.beta), _ptr(o), _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws), nbytes,
+                c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size), _stream(c.device))
+        if phase_event is None:
+            _lib.check(L.vgdr_chunk_fwd(*args))
+        else:
+            _lib.check(L.vgdr_chunk_prep(*args))
+            phase_event.record(torch.cuda.current_stream(c.device))
+            _lib.check(L.vgdr_chunk_state(*args))
     return c.unpad_o(o), c.unpad_state(S)
 
 
@@ -186,7 +198,7 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     final_state None unless output_final_state."""
     _unsupported(use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
                  use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel)
-    return _chunk(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True,
+    return chunk_scan(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True,
                   scale=scale, initial_state=initial_state, output_final_state=output_final_state,
                   cu_seqlens=cu_seqlens, chunk_size=chunk_size)
 
@@ -203,7 +215,7 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
     _unsupported(use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
                  use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel,
                  use_gate_in_kernel=use_gate_in_kernel, safe_gate=safe_gate)
-    return _chunk(q, k, v, g, beta, gate='vector', delta=True, scale=scale,
+    return chunk_scan(q, k, v, g, beta, gate='vector', delta=True, scale=scale,
                   initial_state=initial_state, output_final_state=output_final_state,
                   cu_seqlens=cu_seqlens, chunk_size=chunk_size)
 
@@ -212,7 +224,7 @@ def chunk_simple_gla(q, k, v, g, scale=None, initial_state=None, output_final_st
                      cu_seqlens=None, chunk_size=64):
     """Gated linear attention without the delta rule (the call at linear_attention.py:495-497):
     S_t = a_t S_{t-1} + k_t v_t^T.  g: (B, T, H) or None."""
-    return _chunk(q, k, v, g, None, gate='scalar' if g is not None else 'none', delta=False,
+    return chunk_scan(q, k, v, g, None, gate='scalar' if g is not None else 'none', delta=False,
                   scale=scale, initial_state=initial_state, output_final_state=output_final_state,
                   cu_seqlens=cu_seqlens, chunk_size=chunk_size)
 
@@ -292,7 +304,7 @@ def hip_scan(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_size: int
     """The contract of fla_scan (linear_attention.py:428-498): chunked scan from
     entry state S0 (or zeros), always returning (o in q.dtype, final S fp32).
     g: None, (B, L, H) or (B, L, H, dk)."""
-    return _chunk(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale,
+    return chunk_scan(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale,
                   initial_state=S0, output_final_state=True, cu_seqlens=cu_seqlens,
                   chunk_size=chunk_size)
 
