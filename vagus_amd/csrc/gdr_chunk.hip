@@ -45,6 +45,19 @@ __device__ __forceinline__ int frag_pos(int I, int kb, int lane) {
     return ((I * NB + kb) * 64 + lane) * 4;
 }
 
+// The per-(chunk slot, head) block chunk_prep leaves in the workspace: TE and
+// A (CH x CH each, element type, fragment order), then for the scalar gate
+// G_t = exp(gamma_t) and Gend_t = exp(gamma_C - gamma_t) (CH floats each;
+// gamma is constant past a partial chunk's end, so G[CH - 1] is the chunk's
+// total decay).  Blocks are 16-byte multiples.
+template <typename E, int CH>
+struct ChunkBlock {
+    static constexpr int TEA = 2 * CH * CH;                                   // elements of TE and A
+    static constexpr int GOFF = TEA * (int)sizeof(E);                         // byte offset of G, Gend
+    static constexpr int BYTES = GOFF + 2 * CH * 4;
+    static_assert(BYTES % 16 == 0, "blocks are copied in 16-byte units");
+};
+
 __device__ __forceinline__ void seq_bounds(const SeqGeom &g, int seq, int64_t &bos, int64_t &eos) {
     if (g.cu) {
         int64_t a = g.cu[seq], b = g.cu[seq + 1];
@@ -82,18 +95,20 @@ __device__ __forceinline__ typename Elem<E>::frag gfrag(const E *p) {
 // by every issuing wave, then a barrier, before any lane reads the slot; the
 // memory clobber keeps the compiler from moving LDS accesses across the copy.
 // M0 is set inside the asm and is otherwise unused by these kernels (no
-// movrel / LDS-parameter instructions), so clobbering it is safe here.
+// movrel / LDS-parameter instructions), so clobbering it is safe here.  An
+// LDS DMA that reads M0 needs one wait state after the SALU write of M0
+// (a GFX9-family hazard), hence the s_nop between the two.
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
 }
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void *src, void *lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off"
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
                  :: "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_base))) : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma4(const void *src, void *lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off"
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                  :: "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(lds_base))) : "memory", "m0");
 }
 #pragma clang diagnostic pop
@@ -227,7 +242,8 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     const int64_t sqk = (int64_t)H * DK;
     const E *kg = reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK;
     const E *qg = reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK;
-    E *blk = reinterpret_cast<E *>(p.blocks) + (slot * H + h) * 2 * CH * CH;   // TE, then A
+    char *blk_base = reinterpret_cast<char *>(p.blocks) + (slot * H + h) * ChunkBlock<E, CH>::BYTES;
+    E *blk = reinterpret_cast<E *>(blk_base);                                    // TE, then A
 
     // ---- stage K, Q rows; cumulative decay; beta --------------------------
     dma_rows<E, CH, DK, NT>(Kst, kg, sqk, clen, DK, tid);
@@ -267,7 +283,13 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
                 const float y = __shfl_up(x, o);
                 if (lane >= o) x += y;
             }
-            if (lane < CH) gam[lane] = x;
+            const float last = __shfl(x, CH - 1);
+            if (lane < CH) {
+                gam[lane] = x;
+                float *gblk = reinterpret_cast<float *>(blk_base + ChunkBlock<E, CH>::GOFF);
+                gblk[lane] = __expf(x);
+                gblk[CH + lane] = __expf(last - x);
+            }
         }
     }
     dma_wait();
@@ -464,7 +486,8 @@ __device__ __forceinline__ void state_issue(const StateSlot<DK, CH, NW, E, GATE>
     dma_rows<E, CH, DK, L::NT>(sl.K, kg + t0 * sqk, sqk, clen, DK, tid);
     dma_rows<E, CH, DK, L::NT>(sl.Q, qg + t0 * sqk, sqk, clen, DK, tid);
     dma_rows<E, CH, L::DVT, L::NT>(sl.V, vg + t0 * sv, sv, clen, p.DV - col0, tid);
-    dma_flat<E, 2 * CH * CH * L::ES / 16, L::NT>(sl.B, blocks + ((cbase + c) * H + h) * 2 * CH * CH, tid);
+    const char *bk = reinterpret_cast<const char *>(blocks) + ((cbase + c) * H + h) * ChunkBlock<E, CH>::BYTES;
+    dma_flat<E, 2 * CH * CH * L::ES / 16, L::NT>(sl.B, reinterpret_cast<const E *>(bk), tid);
     if constexpr (GATE != 2) {
         const int wave = tid >> 6, lane = tid & 63;
         if (wave == 0 && lane < CH && p.g && lane < clen) lds_dma4(p.g + (t0 + lane) * H + h, sl.g);
@@ -765,6 +788,292 @@ __global__ void __launch_bounds__(64 * NW) chunk_state_kernel(const ChunkParams 
 }
 
 // ===========================================================================
+// chunk_state_tr_kernel: the chunk recurrence for 16-bit elements with a
+// scalar gate or none, on LDS transpose reads
+// ===========================================================================
+// gfx950 ds_read_b64_tr_b16: within each 16-lane group, source lane s gives the
+// address of 4 consecutive 16-bit elements, and result lane d receives element
+// d % 4 of source lanes d / 4 + 4 i (i = 0..3).  With source lane s pointing at
+// row k0 + s / 4, columns c0 + 4 (s % 4) of a row-major tile, lane d receives
+// rows k0 .. k0 + 3 of column c0 + d: the C-layout / B-operand fragment of the
+// tile, or the A-operand fragment of its transpose, read straight from
+// row-major storage.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s16x4 lds_tr16(const void *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)const_cast<void *>(p));
+}
+template <typename E>
+__device__ __forceinline__ typename Elem<E>::frag ld_tr(const E *p) {
+    return __builtin_bit_cast(typename Elem<E>::frag, lds_tr16(p));
+}
+
+// Values the compiler must treat as unknown where they are produced.  Address
+// arithmetic derived from them is redone next to each use instead of being
+// hoisted out of the chunk loop, which would pin one register per fragment
+// address (and per slot) for the whole kernel.
+__device__ __forceinline__ int opaque_v(int x) { asm volatile("" : "+v"(x)); return x; }
+__device__ __forceinline__ int opaque_s(int x) { asm volatile("" : "+s"(x)); return x; }
+// the value is computed at this point in program order
+template <typename T> __device__ __forceinline__ void pin_v(const T &x) { asm volatile("" ::"v"(x)); }
+
+// Copies by the producer waves of chunk_state_tr_kernel: plain 16-byte global
+// loads into registers (every load of a chunk in flight at once), then 16-byte
+// LDS stores.  Measured on MI355X with all CUs streaming data that is not yet
+// cached, this path moves several times more bytes per CU than
+// global_load_lds, whose throughput from HBM is far lower than from L2.
+// Rows [0, CH) x columns [0, NCOL) of a token-major matrix into a swizzled
+// tile; rows >= valid_rows and columns >= valid_cols read as zeros.
+template <typename E, int CH, int NCOL, int NPT>
+struct RowCopy {
+    using S = Swz<E, NCOL>;
+    static constexpr int UNITS = CH * S::UPR;
+    static constexpr int PER = (UNITS + NPT - 1) / NPT;
+    Vec16 r[PER];
+    __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = pt + NPT * i, row = u / S::UPR, cu = u % S::UPR;
+            const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * S::VE < valid_cols;
+            r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * S::VE)
+                      : Vec16{{0u, 0u, 0u, 0u}};
+        }
+    }
+    __device__ __forceinline__ void store(E *lds, int pt) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = pt + NPT * i, row = u / S::UPR, cu = u % S::UPR;
+            if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + S::at(row, cu * S::VE)) = r[i];
+        }
+    }
+};
+
+// Contiguous 16-byte units (the chunk_prep block).
+template <int UNITS, int NPT>
+struct FlatCopy {
+    static constexpr int PER = (UNITS + NPT - 1) / NPT;
+    Vec16 r[PER];
+    __device__ __forceinline__ void load(const void *src, int pt) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = pt + NPT * i;
+            if (UNITS % NPT == 0 || u < UNITS) r[i] = reinterpret_cast<const Vec16 *>(src)[u];
+        }
+    }
+    __device__ __forceinline__ void store(void *lds, int pt) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = pt + NPT * i;
+            if (UNITS % NPT == 0 || u < UNITS) reinterpret_cast<Vec16 *>(lds)[u] = r[i];
+        }
+    }
+};
+
+// Differences from chunk_state_kernel, all to shorten the per-chunk chain:
+//   * NP producer waves (the last ones) copy the next chunk's operands into
+//     the other half of the double buffer while the NW compute waves work:
+//     the compute waves never touch the memory pipeline except to store o;
+//   * the decay factors G, Gend come precomputed from chunk_prep;
+//   * (K*Gend)^T for the state update and V in C layout come from transpose
+//     reads of the row-major K and V tiles: no transposed copy of K;
+//   * the output is computed transposed, O^T = S^T (scale Q*G)^T + U~^T A^T:
+//     S's and U~'s C-layout accumulators are the A operands, Q and A are read
+//     as for O, and each lane ends up holding four consecutive columns of one
+//     token, which it stores to global memory directly (no staging).
+// One workgroup barrier per chunk: the double-buffer hand-over.
+template <int DK, int CH, int NW, int NP, typename E, bool DELTA>
+__global__ void __launch_bounds__(64 * (NW + NP)) chunk_state_tr_kernel(const ChunkParams p) {
+    static_assert(sizeof(E) == 2, "transpose reads take 16-bit elements");
+    using EL = Elem<E>;
+    using F = typename EL::frag;
+    using CB = ChunkBlock<E, CH>;
+    constexpr int NB = CH / 16, NKB = DK / 16, DVT = 16 * NW, NPT = 64 * NP;
+    using SK = Swz<E, DK>;
+    using SV = Swz<E, DVT>;
+    static_assert(NB % 2 == 0 && NKB % 2 == 0, "k-blocks are consumed in pairs");
+
+    __shared__ __attribute__((aligned(16))) E K0[CH * DK];
+    __shared__ __attribute__((aligned(16))) E K1[CH * DK];
+    __shared__ __attribute__((aligned(16))) E Q0[CH * DK];
+    __shared__ __attribute__((aligned(16))) E Q1[CH * DK];
+    __shared__ __attribute__((aligned(16))) E V0[CH * DVT];
+    __shared__ __attribute__((aligned(16))) E V1[CH * DVT];
+    __shared__ __attribute__((aligned(16))) char B0[CB::BYTES];     // TE, A, G, Gend
+    __shared__ __attribute__((aligned(16))) char B1[CB::BYTES];
+
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int H = p.H, DV = p.DV;
+    const bool producer = wave >= NW;
+
+    // ---- work item: the dv tiles of one (sequence, head) share an XCD ------
+    const int b = blockIdx.x;
+    const int xcd = b & 7, y = b >> 3;
+    const int tile = y % p.n_tiles;
+    const int pos = (y / p.n_tiles) * 8 + xcd;
+    if (pos >= p.geo.n_seqs * H) return;
+    const int h = pos % H;
+    const int spos = pos / H;
+    const int seq = p.geo.order ? p.geo.order[spos] : spos;
+    int64_t bos, eos;
+    seq_bounds(p.geo, seq, bos, eos);
+    const int64_t cbase = chunk_base(p.geo, seq);
+    const int col0 = tile * DVT;
+    const int wcol = 16 * wave;                                  // within the tile
+    const bool wvalid = !producer && col0 + wcol < DV;           // DV % 16 == 0
+    const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
+    const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
+    const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
+    const E *vg = reinterpret_cast<const E *>(p.v) + (int64_t)h * DV + col0;
+    const char *blocks = reinterpret_cast<const char *>(p.blocks);
+    const int64_t len = eos - bos;
+    const int nchunks = (int)((len + CH - 1) / CH);
+
+    // producer: one chunk's operands (K, Q, V rows, the block) in registers.
+    // load(c) may run ahead of the slot hand-over; store(c) writes slot c & 1.
+    RowCopy<E, CH, DK, NPT> ck, cq;
+    RowCopy<E, CH, DVT, NPT> cv;
+    FlatCopy<CB::BYTES / 16, NPT> cb;
+    auto load = [&](int c, int pt) {
+        const int64_t t0 = bos + (int64_t)c * CH;
+        const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+        cb.load(blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES, pt);
+        ck.load(kg + t0 * sqk, sqk, clen, DK, pt);
+        cv.load(vg + t0 * sv, sv, clen, DV - col0, pt);
+        cq.load(qg + t0 * sqk, sqk, clen, DK, pt);
+    };
+    auto store = [&](int c, int z, int pt) {
+        const bool odd = c & 1;
+        cb.store((odd ? B1 : B0) + z, pt);
+        ck.store((odd ? K1 : K0) + z, pt);
+        cv.store((odd ? V1 : V0) + z, pt);
+        cq.store((odd ? Q1 : Q0) + z, pt);
+    };
+
+    // ---- entry state (C layout: S[kt][j] = S[16kt + 4g + j][col0 + wcol + r]) --
+    f32x4 S[NKB];
+    {
+        const int g4 = lane >> 4, r16 = lane & 15;
+        const int64_t sbase = ((int64_t)seq * H + h) * DK * DV + col0 + wcol + r16;
+#pragma unroll
+        for (int kt = 0; kt < NKB; ++kt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
+    }
+
+    if (producer && nchunks > 0) {
+        load(0, tid - 64 * NW);
+        store(0, 0, tid - 64 * NW);
+        if (nchunks > 1) load(1, tid - 64 * NW);              // in flight across the first hand-over
+    }
+    for (int c = 0; c < nchunks; ++c) {
+        const int z = opaque_s(0);
+        lds_barrier();                                        // chunk c in place; chunk c-1 fully consumed
+        if (producer) {
+            const int pt = opaque_v(tid - 64 * NW);
+            if (c + 1 < nchunks) store(c + 1, z, pt);         // into the slot chunk c-1 used
+            if (c + 2 < nchunks) load(c + 2, pt);             // lands while chunk c computes
+            continue;
+        }
+        if (!wvalid) continue;
+        const int ln = opaque_v(lane);
+        const int g4 = ln >> 4, r16 = ln & 15;
+        const int64_t t0 = bos + (int64_t)c * CH;
+        const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+        const bool odd = c & 1;
+        const E *Kst = (odd ? K1 : K0) + z, *Qst = (odd ? Q1 : Q0) + z, *Vst = (odd ? V1 : V0) + z;
+        const char *Bst = (odd ? B1 : B0) + z;
+        const E *TEs = reinterpret_cast<const E *>(Bst), *Aqs = TEs + CH * CH;
+        const float *gs = reinterpret_cast<const float *>(Bst + CB::GOFF), *ge = gs + CH;
+        E *og = reinterpret_cast<E *>(p.o) + (int64_t)h * DV + col0 + wcol + 4 * g4;
+
+        F Sb[NKB];
+#pragma unroll
+        for (int kt = 0; kt < NKB; ++kt) Sb[kt] = EL::cvt(S[kt]);
+        // V rows in C layout: U[I][j] = V[16 I + 4 g + j][wcol + r]
+        f32x4 U[NB];
+#pragma unroll
+        for (int I = 0; I < NB; ++I)
+            U[I] = EL::tof(ld_tr<E>(Vst + SV::at(16 * I + 4 * g4 + (r16 >> 2), wcol + 4 * (r16 & 3))));
+        if constexpr (DELTA) {
+            // X = V - (K*G) S  (independent accumulation chains per token block) ;  U~ = TE X
+            f32x4 P[NB];
+#pragma unroll
+            for (int I = 0; I < NB; ++I) P[I] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < NKB; kt += 2) {
+                F a0[NB], a1[NB];
+#pragma unroll
+                for (int I = 0; I < NB; ++I) {
+                    a0[I] = ld_frag<E>(Kst + SK::at(16 * I + r16, 16 * kt + 4 * g4));
+                    a1[I] = ld_frag<E>(Kst + SK::at(16 * I + r16, 16 * kt + 16 + 4 * g4));
+                }
+#pragma unroll
+                for (int I = 0; I < NB; ++I) P[I] = mfma_kb2(a0[I], Sb[kt], a1[I], Sb[kt + 1], P[I]);
+            }
+            F Xb[NB];
+#pragma unroll
+            for (int I = 0; I < NB; ++I) Xb[I] = EL::cvt(U[I] - P[I] * ld4(gs + 16 * I + 4 * g4));
+#pragma unroll
+            for (int I = 0; I < NB; ++I)
+                U[I] = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
+                    [&](int kb) { return ld_frag<E>(TEs + frag_pos<NB>(I, kb, ln)); },
+                    [&](int kb) { return Xb[kb]; });
+        }
+        F Ub[NB];
+#pragma unroll
+        for (int I = 0; I < NB; ++I) Ub[I] = EL::cvt(U[I]);
+
+        // ---- O^T = S^T (scale Q*G)^T + U~^T A^T; lane (g, r) holds token 16 I + r,
+        //      columns wcol + 4 g .. + 3, stored directly -------------------
+#pragma unroll
+        for (int I = 0; I < NB; ++I) {
+            f32x4 OT = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kt = 0; kt < NKB; kt += 2)
+                OT = mfma_kb2(Sb[kt], ld_frag<E>(Qst + SK::at(16 * I + r16, 16 * kt + 4 * g4)),
+                              Sb[kt + 1], ld_frag<E>(Qst + SK::at(16 * I + r16, 16 * kt + 16 + 4 * g4)), OT);
+            OT *= p.scale * gs[16 * I + r16];
+            OT = contract(OT, I + 1, [&](int kb) { return Ub[kb]; },
+                          [&](int kb) { return ld_frag<E>(Aqs + frag_pos<NB>(I, kb, ln)); });
+            // convert before the lane-dependent store condition: the accumulator
+            // is read in straight-line code, not behind an exec-skip branch
+            const F ob = EL::cvt(OT);
+            pin_v(ob);
+            const int row = 16 * I + r16;
+            if (row < clen) *reinterpret_cast<F *>(og + (t0 + row) * sv) = ob;
+        }
+
+        // ---- S <- Gc S + (K*Gend)^T U~  (independent chains per key block) --
+        F Wb[NB];
+#pragma unroll
+        for (int I = 0; I < NB; ++I) Wb[I] = EL::cvt(U[I] * ld4(ge + 16 * I + 4 * g4));
+        const float gc = gs[CH - 1];
+#pragma unroll
+        for (int kt = 0; kt < NKB; ++kt) S[kt] *= gc;
+#pragma unroll
+        for (int kb = 0; kb < NB; kb += 2) {
+            F a0[NKB], a1[NKB];
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt) {
+                a0[kt] = ld_tr<E>(Kst + SK::at(16 * kb + 4 * g4 + (r16 >> 2), 16 * kt + 4 * (r16 & 3)));
+                a1[kt] = ld_tr<E>(Kst + SK::at(16 * kb + 16 + 4 * g4 + (r16 >> 2), 16 * kt + 4 * (r16 & 3)));
+            }
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt) S[kt] = mfma_kb2(a0[kt], Wb[kb], a1[kt], Wb[kb + 1], S[kt]);
+        }
+    }
+
+    if (p.ht && wvalid) {
+        const int g4 = lane >> 4, r16 = lane & 15;
+        const int64_t sbase = ((int64_t)seq * H + h) * DK * DV + col0 + wcol + r16;
+#pragma unroll
+        for (int kt = 0; kt < NKB; ++kt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p.ht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] = S[kt][j];
+    }
+}
+
+// ===========================================================================
 // launch
 // ===========================================================================
 // The delta rule is a template parameter of the state kernel: a run-time
@@ -775,6 +1084,16 @@ __global__ void __launch_bounds__(64 * NW) chunk_state_kernel(const ChunkParams 
 // such read.
 template <int DK, int CH, typename E, int GATE, bool DELTA>
 static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hipStream_t stream) {
+    if constexpr (sizeof(E) == 2 && GATE != 2) {
+        // 16-bit elements, scalar gate or none: the transpose-read kernel, 4 producer waves
+        if (nw == 4)
+            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, DELTA>), dim3((unsigned)state_blocks),
+                               dim3(64 * 8), 0, stream, p);
+        else
+            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 4, E, DELTA>), dim3((unsigned)state_blocks),
+                               dim3(64 * 6), 0, stream, p);
+        return;
+    }
     if constexpr (StateLayout<DK, CH, 4, E, GATE>::FITS) {
         if (nw == 4) {
             hipLaunchKernelGGL((chunk_state_kernel<DK, CH, 4, E, GATE, DELTA>), dim3((unsigned)state_blocks),
@@ -810,7 +1129,7 @@ static int state_waves(int64_t units, int dv, int cus) {
 
 int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H) {
     const int64_t es = dtype == 0 ? 4 : 2;
-    return chunk_slots * H * 2 * chunk * chunk * es;
+    return chunk_slots * H * (2 * chunk * chunk * es + 2 * chunk * 4);     // ChunkBlock<E, chunk>::BYTES
 }
 
 template <int DK, int CH, typename E, int GATE>
