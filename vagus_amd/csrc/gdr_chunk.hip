@@ -36,13 +36,20 @@
 
 namespace vgdr {
 
-// fragment-order position of element (16 I + m, 16 kb + 4 g + j) of a CH x CH
-// tile block: lane 16 g + m of a wavefront reads its four elements of tile
-// (I, kb) as one contiguous vector, and a wavefront reads a whole tile as one
-// contiguous run of 64 * 4 elements.
+// Fragment order of a CH x CH block of 16 x 16 tiles, by tile pairs: the
+// eight elements lane 16 g + m contributes to one 16x16x32 MFMA over k-blocks
+// (2 q, 2 q + 1), i.e. elements (16 I + m, 16 (2 q) + 4 g + j) and
+// (16 I + m, 16 (2 q + 1) + 4 g + j), j = 0..3, are contiguous, and a
+// wavefront reads a tile pair as one contiguous run of 64 * 8 elements.
+// frag_pair_pos gives the start of a lane's eight; frag_pos the four of one tile.
+template <int NB>
+__device__ __forceinline__ int frag_pair_pos(int I, int q, int lane) {
+    static_assert(NB % 2 == 0, "tiles are paired");
+    return ((I * (NB / 2) + q) * 64 + lane) * 8;
+}
 template <int NB>
 __device__ __forceinline__ int frag_pos(int I, int kb, int lane) {
-    return ((I * NB + kb) * 64 + lane) * 4;
+    return frag_pair_pos<NB>(I, kb >> 1, lane) + (kb & 1) * 4;
 }
 
 // The per-(chunk slot, head) block chunk_prep leaves in the workspace: TE and
@@ -384,6 +391,12 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         while (J > I) { J -= I + 1; ++I; }
         st_frag<E>(blk + CH * CH + frag_pos<NB>(I, J, lane), EL::cvt(res_q[s]));
         if (p.use_delta) st4(Mf + (16 * I + r16) * PF + 16 * J + 4 * g4, res_k[s]);
+    }
+    // the upper tile (I, I + 1) shares a pair with diagonal tile (I, I) for even I: zeros
+    if (wave < NB / 2) {
+        const F zero = EL::cvt(f32x4{0.f, 0.f, 0.f, 0.f});
+        st_frag<E>(blk + CH * CH + frag_pos<NB>(2 * wave, 2 * wave + 1, lane), zero);
+        st_frag<E>(blk + frag_pos<NB>(2 * wave, 2 * wave + 1, lane), zero);
     }
     if (!p.use_delta) return;
     __syncthreads();
@@ -816,33 +829,87 @@ __device__ __forceinline__ int opaque_s(int x) { asm volatile("" : "+s"(x)); ret
 // the value is computed at this point in program order
 template <typename T> __device__ __forceinline__ void pin_v(const T &x) { asm volatile("" ::"v"(x)); }
 
-// Copies by the producer waves of chunk_state_tr_kernel: plain 16-byte global
-// loads into registers (every load of a chunk in flight at once), then 16-byte
-// LDS stores.  Measured on MI355X with all CUs streaming data that is not yet
-// cached, this path moves several times more bytes per CU than
-// global_load_lds, whose throughput from HBM is far lower than from L2.
-// Rows [0, CH) x columns [0, NCOL) of a token-major matrix into a swizzled
-// tile; rows >= valid_rows and columns >= valid_cols read as zeros.
-template <typename E, int CH, int NCOL, int NPT>
+// LDS layout of chunk_state_tr_kernel.  Rows are padded by 16 bytes (the
+// fragment reads of 16 consecutive rows then hit distinct banks) and every
+// fragment address is a per-lane base plus a compile-time offset.  K and Q
+// rows hold their columns in paired order: the 16-byte unit 4 q + g of a row
+// holds columns 32 q + 4 g .. + 3 and 32 q + 16 + 4 g .. + 3, the eight
+// elements lane group g contributes to one 16x16x32 MFMA over k-blocks
+// (2 q, 2 q + 1) -- one 16-byte read per MFMA operand.
+template <int DK>
+struct KQRows {
+    static constexpr int PITCH = DK + 8;                               // elements
+    // element offset of column c (a multiple of 4) within a row
+    __host__ __device__ static constexpr int col(int c) { return (c / 32) * 32 + ((c % 16) / 4) * 8 + ((c % 32) / 16) * 4; }
+};
+
+// Copies by the producer waves: plain 16-byte global loads into registers
+// (every load of a chunk in flight at once), then LDS stores.  Measured on
+// MI355X with all CUs streaming data not yet cached, this path moves several
+// times more bytes per CU than global_load_lds, whose throughput from HBM is
+// far lower than from L2.  Rows [0, CH) x columns [0, NCOL) of a token-major
+// matrix; rows >= valid_rows and columns >= valid_cols read as zeros.
+// PAIRED: K/Q layout above; else rows of pitch NCOL + 8, natural column order.
+template <typename E, int CH, int NCOL, int NPT, bool PAIRED>
 struct RowCopy {
-    using S = Swz<E, NCOL>;
-    static constexpr int UNITS = CH * S::UPR;
-    static constexpr int PER = (UNITS + NPT - 1) / NPT;
+    static constexpr int VE = 16 / (int)sizeof(E), UPR = NCOL / VE, UNITS = CH * UPR;
+    static constexpr int PER = (UNITS + NPT - 1) / NPT, PITCH = NCOL + 8;
     Vec16 r[PER];
     __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int u = pt + NPT * i, row = u / S::UPR, cu = u % S::UPR;
-            const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * S::VE < valid_cols;
-            r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * S::VE)
+            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
+            const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * VE < valid_cols;
+            r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * VE)
                       : Vec16{{0u, 0u, 0u, 0u}};
         }
     }
     __device__ __forceinline__ void store(E *lds, int pt) const {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int u = pt + NPT * i, row = u / S::UPR, cu = u % S::UPR;
-            if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + S::at(row, cu * S::VE)) = r[i];
+            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
+            if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + row * PITCH + cu * VE) = r[i];
+        }
+    }
+};
+
+// lane l receives x from lane l ^ 2 (DPP quad_perm [2, 3, 0, 1]; register only)
+__device__ __forceinline__ uint32_t from_lane_xor2(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);
+}
+
+// K / Q rows into the paired-column layout (KQRows).  Loads are the plain
+// contiguous ones (lane l: unit l of its row group); lanes l and l ^ 2 hold
+// units u and u ^ 2 of one 32-column group, swap halves through DPP, and each
+// writes one whole paired unit: 4 q + 2 a from units 4 q + a, 4 q + a + 2 (the
+// lower halves) or 4 q + 2 a + 1 (the upper halves).
+template <typename E, int CH, int NCOL, int NPT>
+struct RowCopy<E, CH, NCOL, NPT, true> {
+    static constexpr int VE = 16 / (int)sizeof(E), UPR = NCOL / VE, UNITS = CH * UPR;
+    static constexpr int PER = (UNITS + NPT - 1) / NPT, PITCH = KQRows<NCOL>::PITCH;
+    static_assert(UPR % 4 == 0 && NPT % 64 == 0, "quads of lanes hold whole 32-column groups");
+    Vec16 r[PER];
+    __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
+            const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * VE < valid_cols;
+            r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * VE)
+                      : Vec16{{0u, 0u, 0u, 0u}};
+        }
+    }
+    __device__ __forceinline__ void store(E *lds, int pt) const {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR, a = cu & 3;
+            Vec16 o;                                           // unit cu ^ 2, from lane ^ 2
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o.w[k] = from_lane_xor2(r[i].w[k]);
+            const bool lo = a < 2;
+            const Vec16 d = lo ? Vec16{{r[i].w[0], r[i].w[1], o.w[0], o.w[1]}}
+                               : Vec16{{o.w[2], o.w[3], r[i].w[2], r[i].w[3]}};
+            const int off = row * PITCH + 32 * (cu >> 2) + (lo ? 16 * a : 16 * (a - 2) + 8);
+            if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + off) = d;
         }
     }
 };
@@ -868,11 +935,25 @@ struct FlatCopy {
     }
 };
 
+template <typename E>
+__device__ __forceinline__ typename Elem<E>::frag2 ld_pair(const E *p) {
+    return *reinterpret_cast<const typename Elem<E>::frag2 *>(p);
+}
+// two transpose reads (k-blocks 2 q and 2 q + 1) as one MFMA operand
+template <typename E>
+__device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const E *p1) {
+    const typename Elem<E>::frag a = ld_tr<E>(p0), b = ld_tr<E>(p1);
+    return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
 // Differences from chunk_state_kernel, all to shorten the per-chunk chain:
 //   * NP producer waves (the last ones) copy the next chunk's operands into
-//     the other half of the double buffer while the NW compute waves work:
-//     the compute waves never touch the memory pipeline except to store o;
+//     the other half of the double buffer while the NW compute waves work,
+//     issuing the loads of chunk c + 2 as soon as chunk c + 1 is stored;
 //   * the decay factors G, Gend come precomputed from chunk_prep;
+//   * every MFMA operand is one 16-byte LDS read or one register pair (the
+//     layouts above and the paired TE / A blocks), addresses fold into
+//     instruction offsets;
 //   * (K*Gend)^T for the state update and V in C layout come from transpose
 //     reads of the row-major K and V tiles: no transposed copy of K;
 //   * the output is computed transposed, O^T = S^T (scale Q*G)^T + U~^T A^T:
@@ -880,23 +961,26 @@ struct FlatCopy {
 //     as for O, and each lane ends up holding four consecutive columns of one
 //     token, which it stores to global memory directly (no staging).
 // One workgroup barrier per chunk: the double-buffer hand-over.
+// One workgroup per CU (LDS-limited) of NW + NP <= 8 waves: at most two waves per
+// SIMD, so the compiler may use up to 256 registers per wave for lookahead.
 template <int DK, int CH, int NW, int NP, typename E, bool DELTA>
-__global__ void __launch_bounds__(64 * (NW + NP)) chunk_state_tr_kernel(const ChunkParams p) {
+__global__ void __launch_bounds__(64 * (NW + NP)) __attribute__((amdgpu_waves_per_eu(1, 2)))
+chunk_state_tr_kernel(const ChunkParams p) {
     static_assert(sizeof(E) == 2, "transpose reads take 16-bit elements");
     using EL = Elem<E>;
-    using F = typename EL::frag;
+    using F2 = typename EL::frag2;
     using CB = ChunkBlock<E, CH>;
+    using KQ = KQRows<DK>;
     constexpr int NB = CH / 16, NKB = DK / 16, DVT = 16 * NW, NPT = 64 * NP;
-    using SK = Swz<E, DK>;
-    using SV = Swz<E, DVT>;
+    constexpr int PK = KQ::PITCH, PV = DVT + 8;
     static_assert(NB % 2 == 0 && NKB % 2 == 0, "k-blocks are consumed in pairs");
 
-    __shared__ __attribute__((aligned(16))) E K0[CH * DK];
-    __shared__ __attribute__((aligned(16))) E K1[CH * DK];
-    __shared__ __attribute__((aligned(16))) E Q0[CH * DK];
-    __shared__ __attribute__((aligned(16))) E Q1[CH * DK];
-    __shared__ __attribute__((aligned(16))) E V0[CH * DVT];
-    __shared__ __attribute__((aligned(16))) E V1[CH * DVT];
+    __shared__ __attribute__((aligned(16))) E K0[CH * PK];
+    __shared__ __attribute__((aligned(16))) E K1[CH * PK];
+    __shared__ __attribute__((aligned(16))) E Q0[CH * PK];
+    __shared__ __attribute__((aligned(16))) E Q1[CH * PK];
+    __shared__ __attribute__((aligned(16))) E V0[CH * PV];
+    __shared__ __attribute__((aligned(16))) E V1[CH * PV];
     __shared__ __attribute__((aligned(16))) char B0[CB::BYTES];     // TE, A, G, Gend
     __shared__ __attribute__((aligned(16))) char B1[CB::BYTES];
 
@@ -929,8 +1013,8 @@ __global__ void __launch_bounds__(64 * (NW + NP)) chunk_state_tr_kernel(const Ch
 
     // producer: one chunk's operands (K, Q, V rows, the block) in registers.
     // load(c) may run ahead of the slot hand-over; store(c) writes slot c & 1.
-    RowCopy<E, CH, DK, NPT> ck, cq;
-    RowCopy<E, CH, DVT, NPT> cv;
+    RowCopy<E, CH, DK, NPT, true> ck, cq;
+    RowCopy<E, CH, DVT, NPT, false> cv;
     FlatCopy<CB::BYTES / 16, NPT> cb;
     auto load = [&](int c, int pt) {
         const int64_t t0 = bos + (int64_t)c * CH;
@@ -980,86 +1064,89 @@ __global__ void __launch_bounds__(64 * (NW + NP)) chunk_state_tr_kernel(const Ch
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
         const bool odd = c & 1;
-        const E *Kst = (odd ? K1 : K0) + z, *Qst = (odd ? Q1 : Q0) + z, *Vst = (odd ? V1 : V0) + z;
+        // per-lane bases; every fragment below is base + a compile-time offset
+        const E *Krow = (odd ? K1 : K0) + z + r16 * PK + 8 * g4;                 // row r, unit g
+        const E *Qrow = (odd ? Q1 : Q0) + z + r16 * PK + 8 * g4;
+        const E *Ktr = (odd ? K1 : K0) + z + (4 * g4 + (r16 >> 2)) * PK + 8 * (r16 & 3);
+        const E *Vtr = (odd ? V1 : V0) + z + (4 * g4 + (r16 >> 2)) * PV + wcol + 4 * (r16 & 3);
         const char *Bst = (odd ? B1 : B0) + z;
-        const E *TEs = reinterpret_cast<const E *>(Bst), *Aqs = TEs + CH * CH;
+        const E *TEs = reinterpret_cast<const E *>(Bst) + 8 * ln, *Aqs = TEs + CH * CH;
         const float *gs = reinterpret_cast<const float *>(Bst + CB::GOFF), *ge = gs + CH;
         E *og = reinterpret_cast<E *>(p.o) + (int64_t)h * DV + col0 + wcol + 4 * g4;
 
-        F Sb[NKB];
+        F2 Sb[NKB / 2];
 #pragma unroll
-        for (int kt = 0; kt < NKB; ++kt) Sb[kt] = EL::cvt(S[kt]);
+        for (int q = 0; q < NKB / 2; ++q) Sb[q] = EL::cvt2(S[2 * q], S[2 * q + 1]);
         // V rows in C layout: U[I][j] = V[16 I + 4 g + j][wcol + r]
         f32x4 U[NB];
 #pragma unroll
-        for (int I = 0; I < NB; ++I)
-            U[I] = EL::tof(ld_tr<E>(Vst + SV::at(16 * I + 4 * g4 + (r16 >> 2), wcol + 4 * (r16 & 3))));
-        if constexpr (DELTA) {
-            // X = V - (K*G) S  (independent accumulation chains per token block) ;  U~ = TE X
-            f32x4 P[NB];
-#pragma unroll
-            for (int I = 0; I < NB; ++I) P[I] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int kt = 0; kt < NKB; kt += 2) {
-                F a0[NB], a1[NB];
-#pragma unroll
-                for (int I = 0; I < NB; ++I) {
-                    a0[I] = ld_frag<E>(Kst + SK::at(16 * I + r16, 16 * kt + 4 * g4));
-                    a1[I] = ld_frag<E>(Kst + SK::at(16 * I + r16, 16 * kt + 16 + 4 * g4));
-                }
-#pragma unroll
-                for (int I = 0; I < NB; ++I) P[I] = mfma_kb2(a0[I], Sb[kt], a1[I], Sb[kt + 1], P[I]);
-            }
-            F Xb[NB];
-#pragma unroll
-            for (int I = 0; I < NB; ++I) Xb[I] = EL::cvt(U[I] - P[I] * ld4(gs + 16 * I + 4 * g4));
-#pragma unroll
-            for (int I = 0; I < NB; ++I)
-                U[I] = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
-                    [&](int kb) { return ld_frag<E>(TEs + frag_pos<NB>(I, kb, ln)); },
-                    [&](int kb) { return Xb[kb]; });
-        }
-        F Ub[NB];
-#pragma unroll
-        for (int I = 0; I < NB; ++I) Ub[I] = EL::cvt(U[I]);
+        for (int I = 0; I < NB; ++I) U[I] = EL::tof(ld_tr<E>(Vtr + 16 * I * PV));
 
-        // ---- O^T = S^T (scale Q*G)^T + U~^T A^T; lane (g, r) holds token 16 I + r,
-        //      columns wcol + 4 g .. + 3, stored directly -------------------
+        // ---- phase 1: everything that needs only the entry state, 2 NB independent
+        //      accumulation chains: P = K S (C layout) and OT = S^T Q^T, i.e. O^T
+        //      without its scale and intra-chunk term (lane (g, r): token 16 I + r,
+        //      columns wcol + 4 g .. + 3) -----------------------------------
+        f32x4 P[NB], OT[NB];
+#pragma unroll
+        for (int I = 0; I < NB; ++I) P[I] = OT[I] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < NKB / 2; ++q) {
+#pragma unroll
+            for (int I = 0; I < NB; ++I) {
+                if constexpr (DELTA) P[I] = mfma_pair(ld_pair<E>(Krow + 16 * I * PK + 32 * q), Sb[q], P[I]);
+                OT[I] = mfma_pair(Sb[q], ld_pair<E>(Qrow + 16 * I * PK + 32 * q), OT[I]);
+            }
+        }
+
+        // ---- phase 2: X = V - (K*G) S ;  U~ = TE X ---------------------------
+        if constexpr (DELTA) {
+            F2 Xb[NB / 2];
+#pragma unroll
+            for (int q = 0; q < NB / 2; ++q)
+                Xb[q] = EL::cvt2(U[2 * q] - P[2 * q] * ld4(gs + 32 * q + 4 * g4),
+                                 U[2 * q + 1] - P[2 * q + 1] * ld4(gs + 32 * q + 16 + 4 * g4));
+#pragma unroll
+            for (int I = 0; I < NB; ++I) {
+                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int q = 0; 2 * q <= I; ++q)
+                    acc = mfma_pair(ld_pair<E>(TEs + frag_pair_pos<NB>(I, q, 0)), Xb[q], acc);
+                U[I] = acc;
+            }
+        }
+        F2 Ub[NB / 2], Wb[NB / 2];
+#pragma unroll
+        for (int q = 0; q < NB / 2; ++q) {
+            Ub[q] = EL::cvt2(U[2 * q], U[2 * q + 1]);
+            Wb[q] = EL::cvt2(U[2 * q] * ld4(ge + 32 * q + 4 * g4), U[2 * q + 1] * ld4(ge + 32 * q + 16 + 4 * g4));
+        }
+
+        // ---- phase 3: O^T = scale G (.) OT + U~^T A^T, stored directly;
+        //      S <- Gc S + (K*Gend)^T U~ -----------------------------------------
 #pragma unroll
         for (int I = 0; I < NB; ++I) {
-            f32x4 OT = {0.f, 0.f, 0.f, 0.f};
+            OT[I] *= p.scale * gs[16 * I + r16];
 #pragma unroll
-            for (int kt = 0; kt < NKB; kt += 2)
-                OT = mfma_kb2(Sb[kt], ld_frag<E>(Qst + SK::at(16 * I + r16, 16 * kt + 4 * g4)),
-                              Sb[kt + 1], ld_frag<E>(Qst + SK::at(16 * I + r16, 16 * kt + 16 + 4 * g4)), OT);
-            OT *= p.scale * gs[16 * I + r16];
-            OT = contract(OT, I + 1, [&](int kb) { return Ub[kb]; },
-                          [&](int kb) { return ld_frag<E>(Aqs + frag_pos<NB>(I, kb, ln)); });
-            // convert before the lane-dependent store condition: the accumulator
-            // is read in straight-line code, not behind an exec-skip branch
-            const F ob = EL::cvt(OT);
-            pin_v(ob);
-            const int row = 16 * I + r16;
-            if (row < clen) *reinterpret_cast<F *>(og + (t0 + row) * sv) = ob;
+            for (int q = 0; 2 * q <= I; ++q)
+                OT[I] = mfma_pair(Ub[q], ld_pair<E>(Aqs + frag_pair_pos<NB>(I, q, 0)), OT[I]);
         }
-
-        // ---- S <- Gc S + (K*Gend)^T U~  (independent chains per key block) --
-        F Wb[NB];
-#pragma unroll
-        for (int I = 0; I < NB; ++I) Wb[I] = EL::cvt(U[I] * ld4(ge + 16 * I + 4 * g4));
         const float gc = gs[CH - 1];
 #pragma unroll
         for (int kt = 0; kt < NKB; ++kt) S[kt] *= gc;
 #pragma unroll
-        for (int kb = 0; kb < NB; kb += 2) {
-            F a0[NKB], a1[NKB];
+        for (int q = 0; q < NB / 2; ++q)
 #pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) {
-                a0[kt] = ld_tr<E>(Kst + SK::at(16 * kb + 4 * g4 + (r16 >> 2), 16 * kt + 4 * (r16 & 3)));
-                a1[kt] = ld_tr<E>(Kst + SK::at(16 * kb + 16 + 4 * g4 + (r16 >> 2), 16 * kt + 4 * (r16 & 3)));
-            }
+            for (int kt = 0; kt < NKB; ++kt)
+                S[kt] = mfma_pair(ld_tr_pair<E>(Ktr + 32 * q * PK + KQ::col(16 * kt),
+                                                Ktr + (32 * q + 16) * PK + KQ::col(16 * kt)), Wb[q], S[kt]);
 #pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) S[kt] = mfma_kb2(a0[kt], Wb[kb], a1[kt], Wb[kb + 1], S[kt]);
+        for (int I = 0; I < NB; ++I) {
+            // convert before the lane-dependent store condition: the accumulator
+            // is read in straight-line code, not behind an exec-skip branch
+            const typename EL::frag ob = EL::cvt(OT[I]);
+            pin_v(ob);
+            const int row = 16 * I + r16;
+            if (row < clen) *reinterpret_cast<typename EL::frag *>(og + (t0 + row) * sv) = ob;
         }
     }
 
@@ -1085,13 +1172,13 @@ __global__ void __launch_bounds__(64 * (NW + NP)) chunk_state_tr_kernel(const Ch
 template <int DK, int CH, typename E, int GATE, bool DELTA>
 static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hipStream_t stream) {
     if constexpr (sizeof(E) == 2 && GATE != 2) {
-        // 16-bit elements, scalar gate or none: the transpose-read kernel, 4 producer waves
+        // 16-bit elements, scalar gate or none: the transpose-read kernel, 8 waves in all
         if (nw == 4)
             hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, DELTA>), dim3((unsigned)state_blocks),
                                dim3(64 * 8), 0, stream, p);
         else
-            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 4, E, DELTA>), dim3((unsigned)state_blocks),
-                               dim3(64 * 6), 0, stream, p);
+            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 6, E, DELTA>), dim3((unsigned)state_blocks),
+                               dim3(64 * 8), 0, stream, p);
         return;
     }
     if constexpr (StateLayout<DK, CH, 4, E, GATE>::FITS) {

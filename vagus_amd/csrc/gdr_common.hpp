@@ -49,6 +49,7 @@ template <> struct Elem<float> {
 
 template <> struct Elem<__bf16> {
     using frag = bf16x4;
+    using frag2 = bf16x8;                     // both k-blocks of one 16x16x32 MFMA
     static constexpr int pad = 4;
     static constexpr float gate_range = 60.f;
     __device__ static __forceinline__ float to_f(__bf16 x) { return (float)x; }
@@ -59,10 +60,15 @@ template <> struct Elem<__bf16> {
     __device__ static __forceinline__ f32x4 tof(frag x) {
         return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
     }
+    __device__ static __forceinline__ frag2 cvt2(f32x4 a, f32x4 b) {
+        return frag2{(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
+                     (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
+    }
 };
 
 template <> struct Elem<_Float16> {
     using frag = f16x4;
+    using frag2 = f16x8;
     static constexpr int pad = 4;
     static constexpr float gate_range = 8.f;  // fp16 overflows past e^11
     __device__ static __forceinline__ float to_f(_Float16 x) { return (float)x; }
@@ -72,6 +78,10 @@ template <> struct Elem<_Float16> {
     }
     __device__ static __forceinline__ f32x4 tof(frag x) {
         return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+    }
+    __device__ static __forceinline__ frag2 cvt2(f32x4 a, f32x4 b) {
+        return frag2{(_Float16)a[0], (_Float16)a[1], (_Float16)a[2], (_Float16)a[3],
+                     (_Float16)b[0], (_Float16)b[1], (_Float16)b[2], (_Float16)b[3]};
     }
 };
 
@@ -107,6 +117,14 @@ __device__ __forceinline__ f32x4 mfma_kb2(f16x4 a0, f16x4 b0, f16x4 a1, f16x4 b1
 __device__ __forceinline__ f32x4 mfma_kb1(f16x4 a, f16x4 b, f32x4 c) {
     const f16x4 z = {};
     return mfma_kb2(a, b, z, z, c);
+}
+
+// one 16x16x32 MFMA on operands that already hold both k-blocks (frag2)
+__device__ __forceinline__ f32x4 mfma_pair(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma_pair(f16x8 a, f16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 // c += sum over k-blocks kb in [0, n) of A(kb) * B(kb); fa / fb return the
