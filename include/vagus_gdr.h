@@ -76,11 +76,12 @@ const char *vgdr_last_error(void);
  * positive multiple of 16.
  *
  * The caller provides `workspace` (16-byte aligned device memory of at least
- * vgdr_chunk_workspace_size(...) bytes, contents irrelevant): it holds the
- * per-chunk intermediate products and, for a packed batch, the segment table
- * (see vgdr_varlen_prepare).  Calls sharing one workspace must not overlap.
+ * vgdr_chunk_workspace_size(...) bytes for the same dtype, gate_kind, sizes
+ * and chunk_size; contents irrelevant): it holds the per-chunk intermediate
+ * products and, for a packed batch, the segment table (see
+ * vgdr_varlen_prepare).  Calls sharing one workspace must not overlap.
  */
-int64_t vgdr_chunk_workspace_size(int dtype, int64_t B, int64_t T, int64_t H, int64_t dk,
+int64_t vgdr_chunk_workspace_size(int dtype, int gate_kind, int64_t B, int64_t T, int64_t H, int64_t dk,
                                   int64_t n_seqs, int varlen, int chunk_size);
 
 int vgdr_chunk_fwd(int dtype, int gate_kind, int use_delta,

@@ -21,7 +21,7 @@ _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 SIGNATURES = {
     'vgdr_version': (_I, []),
     'vgdr_last_error': (ctypes.c_char_p, []),
-    'vgdr_chunk_workspace_size': (_L, [_I, _L, _L, _L, _L, _L, _I, _I]),
+    'vgdr_chunk_workspace_size': (_L, [_I, _I, _L, _L, _L, _L, _L, _I, _I]),
     'vgdr_chunk_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                             _L, _L, _L, _L, _L, _L, _F, _I, _P]),
     'vgdr_chunk_prep': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,

@@ -75,7 +75,8 @@ struct ChunkWs {
     int64_t total;        // bytes
 };
 
-ChunkWs chunk_layout(int dtype, int chunk, int64_t B, int64_t T, int64_t H, int64_t n_seqs, bool varlen) {
+ChunkWs chunk_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int64_t H, int64_t dk,
+                     int64_t n_seqs, bool varlen) {
     ChunkWs w{};
     if (varlen) {
         w.slots = (B * T + chunk - 1) / chunk + n_seqs;     // each segment adds at most one partial chunk
@@ -84,7 +85,7 @@ ChunkWs chunk_layout(int dtype, int chunk, int64_t B, int64_t T, int64_t H, int6
         w.slots = B * ((T + chunk - 1) / chunk);
         w.blocks_off = 0;
     }
-    w.total = w.blocks_off + vgdr::chunk_blocks_bytes(dtype, chunk, w.slots, H);
+    w.total = w.blocks_off + vgdr::chunk_blocks_bytes(dtype, chunk, w.slots, H, dk, gate_kind == VGDR_GATE_VECTOR);
     if (w.slots == 0) w.total = varlen ? w.blocks_off : 0;
     return w;
 }
@@ -103,7 +104,7 @@ int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_del
         return fail(VGDR_ERR_UNSUPPORTED, "%s: dv=%lld (must be a positive multiple of 16)", fn, (long long)dv);
     if (!aligned16(o)) return fail(VGDR_ERR_INVALID, "%s: o must be 16-byte aligned", fn);
     const int chunk = effective_chunk(dtype, dk, chunk_size);
-    const ChunkWs ws = chunk_layout(dtype, chunk, B, T, H, n_seqs, cu_seqlens != nullptr);
+    const ChunkWs ws = chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, cu_seqlens != nullptr);
     if (ws.total > 0 && (!workspace || workspace_bytes < ws.total || !aligned16(workspace)))
         return fail(VGDR_ERR_INVALID, "%s: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)", fn,
                     (long long)ws.total, (long long)workspace_bytes, workspace);
@@ -155,11 +156,11 @@ int vgdr_version(void) { return 100; }
 
 const char *vgdr_last_error(void) { return g_err; }
 
-int64_t vgdr_chunk_workspace_size(int dtype, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t n_seqs,
-                                   int varlen, int chunk_size) {
+int64_t vgdr_chunk_workspace_size(int dtype, int gate_kind, int64_t B, int64_t T, int64_t H, int64_t dk,
+                                  int64_t n_seqs, int varlen, int chunk_size) {
     if (B < 0 || T < 0 || H <= 0 || n_seqs < 0) return 0;
     const int chunk = effective_chunk(dtype, dk, chunk_size);
-    return chunk_layout(dtype, chunk, B, T, H, n_seqs, varlen).total;
+    return chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, varlen).total;
 }
 
 #define VGDR_CHUNK_ARGS                                                                                    \

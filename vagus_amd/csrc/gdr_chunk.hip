@@ -53,16 +53,23 @@ __device__ __forceinline__ int frag_pos(int I, int kb, int lane) {
 }
 
 // The per-(chunk slot, head) block chunk_prep leaves in the workspace: TE and
-// A (CH x CH each, element type, fragment order), then for the scalar gate
-// G_t = exp(gamma_t) and Gend_t = exp(gamma_C - gamma_t) (CH floats each;
-// gamma is constant past a partial chunk's end, so G[CH - 1] is the chunk's
-// total decay).  Blocks are 16-byte multiples.
-template <typename E, int CH>
+// A (CH x CH each, element type, tile-pair fragment order), then
+//   scalar gate (or none): G_t = exp(gamma_t) and Gend_t = exp(gamma_C - gamma_t)
+//       (CH floats each; gamma is constant past a partial chunk's end, so
+//       G[CH - 1] is the chunk's total decay);
+//   per-channel gate, 16-bit elements (VEC): the gated tiles K*G, scale Q*G and
+//       K*Gend (CH x DK each, element type, rows in the paired-column order of
+//       KQRows, unpadded), then Gc = exp(gamma_C) (DK floats).
+// Blocks are 16-byte multiples.
+template <typename E, int CH, int DK, int GATE>
 struct ChunkBlock {
+    static constexpr bool VEC = GATE == 2 && sizeof(E) == 2;
     static constexpr int TEA = 2 * CH * CH;                                   // elements of TE and A
-    static constexpr int GOFF = TEA * (int)sizeof(E);                         // byte offset of G, Gend
-    static constexpr int BYTES = GOFF + 2 * CH * 4;
-    static_assert(BYTES % 16 == 0, "blocks are copied in 16-byte units");
+    static constexpr int TILES = VEC ? 3 * CH * DK : 0;                       // elements of the gated tiles
+    static constexpr int GOFF = (TEA + TILES) * (int)sizeof(E);               // byte offset of the floats
+    static constexpr int FLOATS = VEC ? DK : 2 * CH;
+    static constexpr int BYTES = GOFF + FLOATS * 4;
+    static_assert(BYTES % 16 == 0 && GOFF % 16 == 0, "blocks are copied in 16-byte units");
 };
 
 __device__ __forceinline__ void seq_bounds(const SeqGeom &g, int seq, int64_t &bos, int64_t &eos) {
@@ -249,7 +256,8 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     const int64_t sqk = (int64_t)H * DK;
     const E *kg = reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK;
     const E *qg = reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK;
-    char *blk_base = reinterpret_cast<char *>(p.blocks) + (slot * H + h) * ChunkBlock<E, CH>::BYTES;
+    using CB = ChunkBlock<E, CH, DK, GATE>;
+    char *blk_base = reinterpret_cast<char *>(p.blocks) + (slot * H + h) * CB::BYTES;
     E *blk = reinterpret_cast<E *>(blk_base);                                    // TE, then A
 
     // ---- stage K, Q rows; cumulative decay; beta --------------------------
@@ -293,7 +301,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             const float last = __shfl(x, CH - 1);
             if (lane < CH) {
                 gam[lane] = x;
-                float *gblk = reinterpret_cast<float *>(blk_base + ChunkBlock<E, CH>::GOFF);
+                float *gblk = reinterpret_cast<float *>(blk_base + CB::GOFF);
                 gblk[lane] = __expf(x);
                 gblk[CH + lane] = __expf(last - x);
             }
@@ -381,6 +389,29 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         }
         res_q[s] = aq;
         res_k[s] = mk;
+    }
+    if constexpr (CB::VEC) {
+        // gated tiles for chunk_state_tr_kernel: K*G, scale Q*G, K*Gend, rows in
+        // paired-column order (16-byte unit pu = 4 q + g holds columns 32 q + 4 g
+        // .. + 3 and 32 q + 16 + 4 g .. + 3), then Gc = exp(gamma_C)
+        using F2 = typename EL::frag2;
+        E *tg = reinterpret_cast<E *>(blk_base) + CB::TEA;
+        constexpr int UPR = DK / 8;
+        for (int it = tid; it < CH * UPR; it += NT) {
+            const int t = it / UPR, pu = it % UPR;
+            const int c0 = 32 * (pu >> 2) + 4 * (pu & 3), c1 = c0 + 16;
+            const f32x4 gt0 = ld4(gam + t * PG + c0), gt1 = ld4(gam + t * PG + c1);
+            const f32x4 gl0 = ld4(gam + (CH - 1) * PG + c0), gl1 = ld4(gam + (CH - 1) * PG + c1);
+            const f32x4 e0 = exp4(gt0), e1 = exp4(gt1), d0 = exp4(gl0 - gt0), d1 = exp4(gl1 - gt1);
+            const f32x4 k0 = EL::tof(ld_frag<E>(Kst + SK::at(t, c0))), k1 = EL::tof(ld_frag<E>(Kst + SK::at(t, c1)));
+            const f32x4 q0 = EL::tof(ld_frag<E>(Qst + SK::at(t, c0))), q1 = EL::tof(ld_frag<E>(Qst + SK::at(t, c1)));
+            E *row = tg + t * DK + 8 * pu;
+            *reinterpret_cast<F2 *>(row) = EL::cvt2(k0 * e0, k1 * e1);
+            *reinterpret_cast<F2 *>(row + CH * DK) = EL::cvt2(q0 * e0 * p.scale, q1 * e1 * p.scale);
+            *reinterpret_cast<F2 *>(row + 2 * CH * DK) = EL::cvt2(k0 * d0, k1 * d1);
+        }
+        float *gcb = reinterpret_cast<float *>(blk_base + CB::GOFF);
+        for (int cc = tid; cc < DK; cc += NT) gcb[cc] = __expf(gam[(CH - 1) * PG + cc]);
     }
     __syncthreads();                                           // K, Q reads done: M, T reuse the stage
 #pragma unroll
@@ -499,7 +530,7 @@ __device__ __forceinline__ void state_issue(const StateSlot<DK, CH, NW, E, GATE>
     dma_rows<E, CH, DK, L::NT>(sl.K, kg + t0 * sqk, sqk, clen, DK, tid);
     dma_rows<E, CH, DK, L::NT>(sl.Q, qg + t0 * sqk, sqk, clen, DK, tid);
     dma_rows<E, CH, L::DVT, L::NT>(sl.V, vg + t0 * sv, sv, clen, p.DV - col0, tid);
-    const char *bk = reinterpret_cast<const char *>(blocks) + ((cbase + c) * H + h) * ChunkBlock<E, CH>::BYTES;
+    const char *bk = reinterpret_cast<const char *>(blocks) + ((cbase + c) * H + h) * ChunkBlock<E, CH, DK, GATE>::BYTES;
     dma_flat<E, 2 * CH * CH * L::ES / 16, L::NT>(sl.B, reinterpret_cast<const E *>(bk), tid);
     if constexpr (GATE != 2) {
         const int wave = tid >> 6, lane = tid & 63;
@@ -963,26 +994,31 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 // One workgroup barrier per chunk: the double-buffer hand-over.
 // One workgroup per CU (LDS-limited) of NW + NP <= 8 waves: at most two waves per
 // SIMD, so the compiler may use up to 256 registers per wave for lookahead.
-template <int DK, int CH, int NW, int NP, typename E, bool DELTA>
+template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA>
 __global__ void __launch_bounds__(64 * (NW + NP)) __attribute__((amdgpu_waves_per_eu(1, 2)))
 chunk_state_tr_kernel(const ChunkParams p) {
     static_assert(sizeof(E) == 2, "transpose reads take 16-bit elements");
     using EL = Elem<E>;
     using F2 = typename EL::frag2;
-    using CB = ChunkBlock<E, CH>;
+    using CB = ChunkBlock<E, CH, DK, VEC ? 2 : 1>;
     using KQ = KQRows<DK>;
     constexpr int NB = CH / 16, NKB = DK / 16, DVT = 16 * NW, NPT = 64 * NP;
     constexpr int PK = KQ::PITCH, PV = DVT + 8;
+    constexpr int TEAB = CB::TEA * (int)sizeof(E);              // bytes of TE + A in a slot
+    constexpr int BSLOT = TEAB + CB::FLOATS * 4;                 // TE, A, then G, Gend | Gc
     static_assert(NB % 2 == 0 && NKB % 2 == 0, "k-blocks are consumed in pairs");
 
+    // K, Q hold K*G and scale Q*G for a per-channel gate (VEC), KE then K*Gend
     __shared__ __attribute__((aligned(16))) E K0[CH * PK];
     __shared__ __attribute__((aligned(16))) E K1[CH * PK];
     __shared__ __attribute__((aligned(16))) E Q0[CH * PK];
     __shared__ __attribute__((aligned(16))) E Q1[CH * PK];
+    __shared__ __attribute__((aligned(16))) E KE0[VEC ? CH * PK : 8];
+    __shared__ __attribute__((aligned(16))) E KE1[VEC ? CH * PK : 8];
     __shared__ __attribute__((aligned(16))) E V0[CH * PV];
     __shared__ __attribute__((aligned(16))) E V1[CH * PV];
-    __shared__ __attribute__((aligned(16))) char B0[CB::BYTES];     // TE, A, G, Gend
-    __shared__ __attribute__((aligned(16))) char B1[CB::BYTES];
+    __shared__ __attribute__((aligned(16))) char B0[BSLOT];
+    __shared__ __attribute__((aligned(16))) char B1[BSLOT];
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int H = p.H, DV = p.DV;
@@ -1011,25 +1047,40 @@ chunk_state_tr_kernel(const ChunkParams p) {
     const int64_t len = eos - bos;
     const int nchunks = (int)((len + CH - 1) / CH);
 
-    // producer: one chunk's operands (K, Q, V rows, the block) in registers.
-    // load(c) may run ahead of the slot hand-over; store(c) writes slot c & 1.
-    RowCopy<E, CH, DK, NPT, true> ck, cq;
+    // producer: one chunk's operands in registers.  load(c) may run ahead of
+    // the slot hand-over; store(c) writes slot c & 1.  K and Q come from q and
+    // k (scalar gate), or already gated and paired from chunk_prep (VEC).
+    RowCopy<E, CH, DK, NPT, !VEC> ck, cq;
+    RowCopy<E, CH, DK, NPT, false> ce;
     RowCopy<E, CH, DVT, NPT, false> cv;
-    FlatCopy<CB::BYTES / 16, NPT> cb;
+    FlatCopy<TEAB / 16, NPT> cb;
+    FlatCopy<CB::FLOATS * 4 / 16, NPT> cf;
     auto load = [&](int c, int pt) {
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
-        cb.load(blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES, pt);
-        ck.load(kg + t0 * sqk, sqk, clen, DK, pt);
-        cv.load(vg + t0 * sv, sv, clen, DV - col0, pt);
-        cq.load(qg + t0 * sqk, sqk, clen, DK, pt);
+        const char *bk = blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES;
+        cb.load(bk, pt);
+        cf.load(bk + CB::GOFF, pt);
+        if constexpr (VEC) {
+            const E *tiles = reinterpret_cast<const E *>(bk) + CB::TEA;
+            ck.load(tiles, DK, CH, DK, pt);
+            cv.load(vg + t0 * sv, sv, clen, DV - col0, pt);
+            cq.load(tiles + CH * DK, DK, CH, DK, pt);
+            ce.load(tiles + 2 * CH * DK, DK, CH, DK, pt);
+        } else {
+            ck.load(kg + t0 * sqk, sqk, clen, DK, pt);
+            cv.load(vg + t0 * sv, sv, clen, DV - col0, pt);
+            cq.load(qg + t0 * sqk, sqk, clen, DK, pt);
+        }
     };
     auto store = [&](int c, int z, int pt) {
         const bool odd = c & 1;
         cb.store((odd ? B1 : B0) + z, pt);
+        cf.store((odd ? B1 : B0) + z + TEAB, pt);
         ck.store((odd ? K1 : K0) + z, pt);
         cv.store((odd ? V1 : V0) + z, pt);
         cq.store((odd ? Q1 : Q0) + z, pt);
+        if constexpr (VEC) ce.store((odd ? KE1 : KE0) + z, pt);
     };
 
     // ---- entry state (C layout: S[kt][j] = S[16kt + 4g + j][col0 + wcol + r]) --
@@ -1067,11 +1118,11 @@ chunk_state_tr_kernel(const ChunkParams p) {
         // per-lane bases; every fragment below is base + a compile-time offset
         const E *Krow = (odd ? K1 : K0) + z + r16 * PK + 8 * g4;                 // row r, unit g
         const E *Qrow = (odd ? Q1 : Q0) + z + r16 * PK + 8 * g4;
-        const E *Ktr = (odd ? K1 : K0) + z + (4 * g4 + (r16 >> 2)) * PK + 8 * (r16 & 3);
+        const E *Ktr = (VEC ? (odd ? KE1 : KE0) : (odd ? K1 : K0)) + z + (4 * g4 + (r16 >> 2)) * PK + 8 * (r16 & 3);
         const E *Vtr = (odd ? V1 : V0) + z + (4 * g4 + (r16 >> 2)) * PV + wcol + 4 * (r16 & 3);
         const char *Bst = (odd ? B1 : B0) + z;
         const E *TEs = reinterpret_cast<const E *>(Bst) + 8 * ln, *Aqs = TEs + CH * CH;
-        const float *gs = reinterpret_cast<const float *>(Bst + CB::GOFF), *ge = gs + CH;
+        const float *gs = reinterpret_cast<const float *>(Bst + TEAB), *ge = gs + CH;       // G, Gend | Gc
         E *og = reinterpret_cast<E *>(p.o) + (int64_t)h * DV + col0 + wcol + 4 * g4;
 
         F2 Sb[NKB / 2];
@@ -1102,9 +1153,11 @@ chunk_state_tr_kernel(const ChunkParams p) {
         if constexpr (DELTA) {
             F2 Xb[NB / 2];
 #pragma unroll
-            for (int q = 0; q < NB / 2; ++q)
-                Xb[q] = EL::cvt2(U[2 * q] - P[2 * q] * ld4(gs + 32 * q + 4 * g4),
-                                 U[2 * q + 1] - P[2 * q + 1] * ld4(gs + 32 * q + 16 + 4 * g4));
+            for (int q = 0; q < NB / 2; ++q) {
+                if constexpr (VEC) Xb[q] = EL::cvt2(U[2 * q] - P[2 * q], U[2 * q + 1] - P[2 * q + 1]);
+                else Xb[q] = EL::cvt2(U[2 * q] - P[2 * q] * ld4(gs + 32 * q + 4 * g4),
+                                      U[2 * q + 1] - P[2 * q + 1] * ld4(gs + 32 * q + 16 + 4 * g4));
+            }
 #pragma unroll
             for (int I = 0; I < NB; ++I) {
                 f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -1118,21 +1171,27 @@ chunk_state_tr_kernel(const ChunkParams p) {
 #pragma unroll
         for (int q = 0; q < NB / 2; ++q) {
             Ub[q] = EL::cvt2(U[2 * q], U[2 * q + 1]);
-            Wb[q] = EL::cvt2(U[2 * q] * ld4(ge + 32 * q + 4 * g4), U[2 * q + 1] * ld4(ge + 32 * q + 16 + 4 * g4));
+            if constexpr (VEC) Wb[q] = Ub[q];                   // Gend is in the K*Gend tile
+            else Wb[q] = EL::cvt2(U[2 * q] * ld4(ge + 32 * q + 4 * g4), U[2 * q + 1] * ld4(ge + 32 * q + 16 + 4 * g4));
         }
 
         // ---- phase 3: O^T = scale G (.) OT + U~^T A^T, stored directly;
         //      S <- Gc S + (K*Gend)^T U~ -----------------------------------------
 #pragma unroll
         for (int I = 0; I < NB; ++I) {
-            OT[I] *= p.scale * gs[16 * I + r16];
+            if constexpr (!VEC) OT[I] *= p.scale * gs[16 * I + r16];    // VEC: scale and G are in Q*G
 #pragma unroll
             for (int q = 0; 2 * q <= I; ++q)
                 OT[I] = mfma_pair(Ub[q], ld_pair<E>(Aqs + frag_pair_pos<NB>(I, q, 0)), OT[I]);
         }
-        const float gc = gs[CH - 1];
+        if constexpr (VEC) {
 #pragma unroll
-        for (int kt = 0; kt < NKB; ++kt) S[kt] *= gc;
+            for (int kt = 0; kt < NKB; ++kt) S[kt] *= ld4(gs + 16 * kt + 4 * g4);    // Gc per key channel
+        } else {
+            const float gc = gs[CH - 1];
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt) S[kt] *= gc;
+        }
 #pragma unroll
         for (int q = 0; q < NB / 2; ++q)
 #pragma unroll
@@ -1171,16 +1230,17 @@ chunk_state_tr_kernel(const ChunkParams p) {
 // such read.
 template <int DK, int CH, typename E, int GATE, bool DELTA>
 static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hipStream_t stream) {
-    if constexpr (sizeof(E) == 2 && GATE != 2) {
-        // 16-bit elements, scalar gate or none: the transpose-read kernel, 8 waves in all
+    if constexpr (sizeof(E) == 2) {
+        // 16-bit elements: the transpose-read kernel, 8 waves in all
+        constexpr bool VEC = GATE == 2;
         if (nw == 4)
-            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, DELTA>), dim3((unsigned)state_blocks),
+            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, VEC, DELTA>), dim3((unsigned)state_blocks),
                                dim3(64 * 8), 0, stream, p);
         else
-            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 6, E, DELTA>), dim3((unsigned)state_blocks),
+            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 6, E, VEC, DELTA>), dim3((unsigned)state_blocks),
                                dim3(64 * 8), 0, stream, p);
         return;
-    }
+    } else {
     if constexpr (StateLayout<DK, CH, 4, E, GATE>::FITS) {
         if (nw == 4) {
             hipLaunchKernelGGL((chunk_state_kernel<DK, CH, 4, E, GATE, DELTA>), dim3((unsigned)state_blocks),
@@ -1190,6 +1250,7 @@ static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hip
     }
     hipLaunchKernelGGL((chunk_state_kernel<DK, CH, 2, E, GATE, DELTA>), dim3((unsigned)state_blocks), dim3(128), 0,
                        stream, p);
+    }
 }
 
 template <int DK, int CH, typename E, int GATE>
@@ -1210,13 +1271,16 @@ static hipError_t launch_chunk(const ChunkParams &p, int nw, int phases, hipStre
 template <int DK, int CH, typename E, int GATE>
 static int state_waves(int64_t units, int dv, int cus) {
     // 64-column tiles once the (sequence, head) pairs fill the chip and the tile fits LDS
-    if (!StateLayout<DK, CH, 4, E, GATE>::FITS) return 2;
+    // (the 16-bit kernel's tiles always fit)
+    if (sizeof(E) == 4 && !StateLayout<DK, CH, 4, E, GATE>::FITS) return 2;
     return units * ((dv + 63) / 64) >= cus ? 4 : 2;
 }
 
-int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H) {
+int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H, int64_t dk, int gate_vector) {
     const int64_t es = dtype == 0 ? 4 : 2;
-    return chunk_slots * H * (2 * chunk * chunk * es + 2 * chunk * 4);     // ChunkBlock<E, chunk>::BYTES
+    const bool vec = gate_vector && dtype != 0;                            // ChunkBlock<E, chunk, dk, gate>::BYTES
+    const int64_t per = 2 * chunk * chunk * es + (vec ? 3 * chunk * dk * es + dk * 4 : 2 * chunk * 4);
+    return chunk_slots * H * per;
 }
 
 template <int DK, int CH, typename E, int GATE>

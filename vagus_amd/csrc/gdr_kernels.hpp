@@ -57,7 +57,7 @@ struct RecParams {
 enum { CHUNK_PREP = 1, CHUNK_STATE = 2 };
 hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table, int phases,
                      hipStream_t stream);
-int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H);
+int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H, int64_t dk, int gate_vector);
 
 hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
                          hipStream_t stream);

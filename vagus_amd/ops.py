@@ -166,7 +166,7 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
     S = c.new_state() if output_final_state else None
     L = _lib.load()
     varlen = c.cu is not None
-    nbytes = L.vgdr_chunk_workspace_size(_DTYPES[c.dtype], c.B, c.T, c.H, c.dkp, c.N, int(varlen),
+    nbytes = L.vgdr_chunk_workspace_size(_DTYPES[c.dtype], c.gate_kind, c.B, c.T, c.H, c.dkp, c.N, int(varlen),
                                          int(chunk_size))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
     with torch.cuda.device(c.device):
