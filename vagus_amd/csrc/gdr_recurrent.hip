@@ -11,7 +11,9 @@
 //     u  = beta (v - kS)   (v without the delta rule)
 //     o  = scale (qS + qk u)                          = scale q^T (S' + k u^T)
 //     S  = S' + k u^T
-// so S is read once and written once per call regardless of T.
+// so S is read once and written once per call regardless of T.  The state
+// streams through once per call, so it is read and written non-temporally
+// (measured: 30.7 -> 25.5 us per decode step at B=64 H=16 dk=dv=128).
 #include "gdr_common.hpp"
 #include "gdr_kernels.hpp"
 
@@ -60,7 +62,9 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
     f32x4 S[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; ++i)
-        S[i] = p.h0 ? ld4(p.h0 + sbase + (int64_t)(rg + NRG * i) * DV + 4 * cg) : f32x4{0.f, 0.f, 0.f, 0.f};
+        S[i] = p.h0 ? __builtin_nontemporal_load(
+                          reinterpret_cast<const f32x4 *>(p.h0 + sbase + (int64_t)(rg + NRG * i) * DV + 4 * cg))
+                    : f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int64_t t = bos; t < eos; ++t) {
         // token operands -> LDS (fp32)
@@ -128,7 +132,8 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
 
     if (p.ht) {
 #pragma unroll
-        for (int i = 0; i < RPT; ++i) st4(p.ht + sbase + (int64_t)(rg + NRG * i) * DV + 4 * cg, S[i]);
+        for (int i = 0; i < RPT; ++i)
+            __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(p.ht + sbase + (int64_t)(rg + NRG * i) * DV + 4 * cg));
     }
 }
 
