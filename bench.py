@@ -183,7 +183,7 @@ def cpu_baseline(torch, workloads):
 
 
 def measured_traffic(workload, kernel):
-    """HBM bytes per launch of `kernel` ('chunk_state' / 'chunk_prep') on
+    """HBM bytes per launch of `kernel` ('chunk_state' / 'chunk_prep' / 'recurrent') on
     `workload`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
     (profiles/traffic.json), if one exists."""
     path = os.path.join(ROOT, 'profiles', 'traffic.json')
@@ -240,7 +240,8 @@ def main():
         extra['decode'] = {'workload': 'gdn decode step B64 H16 dk=dv=128, 24 layer states, graph-replayed',
                            'us_per_step': round(dec['avg_us'], 2), 'achieved_GBs': round(dec['GBs'], 1),
                            'peak_GBs': PEAK_HBM_GBS, 'frac': round(dec['GBs'] / PEAK_HBM_GBS, 4),
-                           'bytes_per_step': dec['bytes']}
+                           'bytes_per_step': dec['bytes'],
+                           'traffic': measured_traffic('decode_b64_h16', 'recurrent')}
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
             r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))
@@ -277,11 +278,11 @@ def main():
         'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS,
                      'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_BF16_TFLOPS, 5),
                      'traffic': measured_traffic('gdn_340m', 'chunk_state'),
-                     'kernel': 'chunk_state_kernel', 'kernel_avg_ms': round(pre['state_ms'], 4),
+                     'kernel': 'chunk_state_tr_kernel', 'kernel_avg_ms': round(pre['state_ms'], 4),
                      'flop_per_launch': tokens * H * STATE_FLOP_PER_TOKEN_HEAD,
                      'algorithmic_bytes_per_launch': tokens * H * STATE_BYTES_PER_TOKEN_HEAD,
                      'hbm_algorithmic_GBs': round(state_gbs, 1)},
-        'path': {'kernels': 'chunk_prep_kernel + chunk_state_kernel', 'op_ms': round(pre['op_ms'], 4),
+        'path': {'kernels': 'chunk_prep_kernel + chunk_state_tr_kernel', 'op_ms': round(pre['op_ms'], 4),
                  'prep_ms': round(pre['prep_ms'], 4), 'state_ms': round(pre['state_ms'], 4),
                  'achieved_tflops': round(pre['path_tflops'], 2),
                  'frac_mfma': round(pre['path_tflops'] / PEAK_BF16_TFLOPS, 5),
