@@ -887,20 +887,18 @@ struct RowCopy {
     static constexpr int PER = (UNITS + NPT - 1) / NPT, PITCH = NCOL + 8;
     Vec16 r[PER];
     __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        unroll<PER>([&](auto i) {
             const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
             const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * VE < valid_cols;
             r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * VE)
                       : Vec16{{0u, 0u, 0u, 0u}};
-        }
+        });
     }
     __device__ __forceinline__ void store(E *lds, int pt) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        unroll<PER>([&](auto i) {
             const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
             if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + row * PITCH + cu * VE) = r[i];
-        }
+        });
     }
 };
 
@@ -921,48 +919,46 @@ struct RowCopy<E, CH, NCOL, NPT, true> {
     static_assert(UPR % 4 == 0 && NPT % 64 == 0, "quads of lanes hold whole 32-column groups");
     Vec16 r[PER];
     __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        unroll<PER>([&](auto i) {
             const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
             const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * VE < valid_cols;
             r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * VE)
                       : Vec16{{0u, 0u, 0u, 0u}};
-        }
+        });
     }
     __device__ __forceinline__ void store(E *lds, int pt) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        unroll<PER>([&](auto i) {
             const int u = pt + NPT * i, row = u / UPR, cu = u % UPR, a = cu & 3;
             Vec16 o;                                           // unit cu ^ 2, from lane ^ 2
-#pragma unroll
-            for (int k = 0; k < 4; ++k) o.w[k] = from_lane_xor2(r[i].w[k]);
+            unroll<4>([&](auto k) { o.w[k] = from_lane_xor2(r[i].w[k]); });
             const bool lo = a < 2;
             const Vec16 d = lo ? Vec16{{r[i].w[0], r[i].w[1], o.w[0], o.w[1]}}
                                : Vec16{{o.w[2], o.w[3], r[i].w[2], r[i].w[3]}};
             const int off = row * PITCH + 32 * (cu >> 2) + (lo ? 16 * a : 16 * (a - 2) + 8);
             if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + off) = d;
-        }
+        });
     }
 };
 
-// Contiguous 16-byte units (the chunk_prep block).
+// Contiguous 16-byte units (the chunk_prep block).  The units are a vector
+// type: a conditional copy of a 16-byte struct becomes a memcpy into a stack
+// slot, which the alloca promotion pass then places in LDS or scratch.
 template <int UNITS, int NPT>
 struct FlatCopy {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     static constexpr int PER = (UNITS + NPT - 1) / NPT;
-    Vec16 r[PER];
+    u32x4 r[PER];
     __device__ __forceinline__ void load(const void *src, int pt) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        unroll<PER>([&](auto i) {
             const int u = pt + NPT * i;
-            if (UNITS % NPT == 0 || u < UNITS) r[i] = reinterpret_cast<const Vec16 *>(src)[u];
-        }
+            if (UNITS % NPT == 0 || u < UNITS) r[i] = reinterpret_cast<const u32x4 *>(src)[u];
+        });
     }
     __device__ __forceinline__ void store(void *lds, int pt) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
+        unroll<PER>([&](auto i) {
             const int u = pt + NPT * i;
-            if (UNITS % NPT == 0 || u < UNITS) reinterpret_cast<Vec16 *>(lds)[u] = r[i];
-        }
+            if (UNITS % NPT == 0 || u < UNITS) reinterpret_cast<u32x4 *>(lds)[u] = r[i];
+        });
     }
 };
 
@@ -1055,7 +1051,7 @@ chunk_state_tr_kernel(const ChunkParams p) {
     RowCopy<E, CH, DVT, NPT, false> cv;
     FlatCopy<TEAB / 16, NPT> cb;
     FlatCopy<CB::FLOATS * 4 / 16, NPT> cf;
-    auto load = [&](int c, int pt) {
+    auto load = [&](int c, int pt) __attribute__((always_inline)) {
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
         const char *bk = blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES;
@@ -1073,7 +1069,7 @@ chunk_state_tr_kernel(const ChunkParams p) {
             cq.load(qg + t0 * sqk, sqk, clen, DK, pt);
         }
     };
-    auto store = [&](int c, int z, int pt) {
+    auto store = [&](int c, int z, int pt) __attribute__((always_inline)) {
         const bool odd = c & 1;
         cb.store((odd ? B1 : B0) + z, pt);
         cf.store((odd ? B1 : B0) + z + TEAB, pt);

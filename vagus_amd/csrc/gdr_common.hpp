@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace vgdr {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -159,5 +161,18 @@ template <typename T> __host__ __device__ constexpr T cmax(T a, T b) { return a 
 
 // 16-byte global access
 struct alignas(16) Vec16 { uint32_t w[4]; };
+
+// f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}).
+// Register arrays indexed inside f are indexed by constants from the start:
+// a `#pragma unroll` loop is unrolled only after the alloca promotion pass,
+// which places a dynamically indexed array in LDS or scratch instead.
+template <typename F, int... I>
+__device__ __forceinline__ void unroll_seq(F &&f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll(F &&f) {
+    unroll_seq(f, std::make_integer_sequence<int, N>{});
+}
 
 }  // namespace vgdr
