@@ -881,23 +881,48 @@ struct KQRows {
 // far lower than from L2.  Rows [0, CH) x columns [0, NCOL) of a token-major
 // matrix; rows >= valid_rows and columns >= valid_cols read as zeros.
 // PAIRED: K/Q layout above; else rows of pitch NCOL + 8, natural column order.
-template <typename E, int CH, int NCOL, int NPT, bool PAIRED>
-struct RowCopy {
+//
+// Every load is issued unconditionally, from unit 0 (always inside the tile)
+// where the unit itself is out of range, and zeros are selected when the
+// registers are stored (a select next to the load would wait for it).  Loads
+// under a per-lane branch made the wait-count insertion put a full vmcnt(0)
+// wait in front of each following load, which serialised them.
+// The registers are a vector type: a 16-byte struct copied under a condition
+// becomes a memcpy through a stack slot, which the alloca promotion pass then
+// moves to LDS or scratch.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename E, int CH, int NCOL, int NPT>
+struct RowLoads {
     static constexpr int VE = 16 / (int)sizeof(E), UPR = NCOL / VE, UNITS = CH * UPR;
-    static constexpr int PER = (UNITS + NPT - 1) / NPT, PITCH = NCOL + 8;
-    Vec16 r[PER];
+    static constexpr int PER = (UNITS + NPT - 1) / NPT;
+    static_assert(PER <= 32, "one valid bit per unit");
+    u32x4 r[PER];
+    uint32_t valid;                                           // bit i: unit i lies inside the tile
     __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
+        valid = 0;
         unroll<PER>([&](auto i) {
             const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
             const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * VE < valid_cols;
-            r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * VE)
-                      : Vec16{{0u, 0u, 0u, 0u}};
+            r[i] = *reinterpret_cast<const u32x4 *>(src + (ok ? (int64_t)row * stride + cu * VE : 0));
+            valid |= (uint32_t)ok << (int)i;
         });
     }
+    // unit i of the last load, zero outside the tile
+    __device__ __forceinline__ u32x4 get(int i) const {
+        return (valid >> i) & 1u ? r[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+    __device__ static __forceinline__ bool live(int u) { return UNITS % NPT == 0 || u < UNITS; }
+};
+
+template <typename E, int CH, int NCOL, int NPT, bool PAIRED>
+struct RowCopy : RowLoads<E, CH, NCOL, NPT> {
+    using B = RowLoads<E, CH, NCOL, NPT>;
+    static constexpr int PITCH = NCOL + 8;
     __device__ __forceinline__ void store(E *lds, int pt) const {
-        unroll<PER>([&](auto i) {
-            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
-            if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + row * PITCH + cu * VE) = r[i];
+        unroll<B::PER>([&](auto i) {
+            const int u = pt + NPT * i, row = u / B::UPR, cu = u % B::UPR;
+            if (B::live(u)) *reinterpret_cast<u32x4 *>(lds + row * PITCH + cu * B::VE) = this->get(i);
         });
     }
 };
@@ -913,45 +938,33 @@ __device__ __forceinline__ uint32_t from_lane_xor2(uint32_t x) {
 // writes one whole paired unit: 4 q + 2 a from units 4 q + a, 4 q + a + 2 (the
 // lower halves) or 4 q + 2 a + 1 (the upper halves).
 template <typename E, int CH, int NCOL, int NPT>
-struct RowCopy<E, CH, NCOL, NPT, true> {
-    static constexpr int VE = 16 / (int)sizeof(E), UPR = NCOL / VE, UNITS = CH * UPR;
-    static constexpr int PER = (UNITS + NPT - 1) / NPT, PITCH = KQRows<NCOL>::PITCH;
-    static_assert(UPR % 4 == 0 && NPT % 64 == 0, "quads of lanes hold whole 32-column groups");
-    Vec16 r[PER];
-    __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
-        unroll<PER>([&](auto i) {
-            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
-            const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * VE < valid_cols;
-            r[i] = ok ? *reinterpret_cast<const Vec16 *>(src + (int64_t)row * stride + cu * VE)
-                      : Vec16{{0u, 0u, 0u, 0u}};
-        });
-    }
+struct RowCopy<E, CH, NCOL, NPT, true> : RowLoads<E, CH, NCOL, NPT> {
+    using B = RowLoads<E, CH, NCOL, NPT>;
+    static constexpr int PITCH = KQRows<NCOL>::PITCH;
+    static_assert(B::UPR % 4 == 0 && NPT % 64 == 0, "quads of lanes hold whole 32-column groups");
     __device__ __forceinline__ void store(E *lds, int pt) const {
-        unroll<PER>([&](auto i) {
-            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR, a = cu & 3;
-            Vec16 o;                                           // unit cu ^ 2, from lane ^ 2
-            unroll<4>([&](auto k) { o.w[k] = from_lane_xor2(r[i].w[k]); });
+        unroll<B::PER>([&](auto i) {
+            const int u = pt + NPT * i, row = u / B::UPR, cu = u % B::UPR, a = cu & 3;
+            const u32x4 x = this->get(i);
+            u32x4 o;                                           // unit cu ^ 2, from lane ^ 2
+            unroll<4>([&](auto k) { o[(int)k] = from_lane_xor2(x[(int)k]); });
             const bool lo = a < 2;
-            const Vec16 d = lo ? Vec16{{r[i].w[0], r[i].w[1], o.w[0], o.w[1]}}
-                               : Vec16{{o.w[2], o.w[3], r[i].w[2], r[i].w[3]}};
+            const u32x4 d = lo ? u32x4{x[0], x[1], o[0], o[1]} : u32x4{o[2], o[3], x[2], x[3]};
             const int off = row * PITCH + 32 * (cu >> 2) + (lo ? 16 * a : 16 * (a - 2) + 8);
-            if (UNITS % NPT == 0 || u < UNITS) *reinterpret_cast<Vec16 *>(lds + off) = d;
+            if (B::live(u)) *reinterpret_cast<u32x4 *>(lds + off) = d;
         });
     }
 };
 
-// Contiguous 16-byte units (the chunk_prep block).  The units are a vector
-// type: a conditional copy of a 16-byte struct becomes a memcpy into a stack
-// slot, which the alloca promotion pass then places in LDS or scratch.
+// Contiguous 16-byte units (the chunk_prep block), loaded as above.
 template <int UNITS, int NPT>
 struct FlatCopy {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
     static constexpr int PER = (UNITS + NPT - 1) / NPT;
     u32x4 r[PER];
     __device__ __forceinline__ void load(const void *src, int pt) {
         unroll<PER>([&](auto i) {
             const int u = pt + NPT * i;
-            if (UNITS % NPT == 0 || u < UNITS) r[i] = reinterpret_cast<const u32x4 *>(src)[u];
+            r[i] = reinterpret_cast<const u32x4 *>(src)[UNITS % NPT == 0 || u < UNITS ? u : 0];
         });
     }
     __device__ __forceinline__ void store(void *lds, int pt) const {
@@ -1091,20 +1104,28 @@ chunk_state_tr_kernel(const ChunkParams p) {
                 S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
     }
 
-    if (producer && nchunks > 0) {
-        load(0, tid - 64 * NW);
-        store(0, 0, tid - 64 * NW);
-        if (nchunks > 1) load(1, tid - 64 * NW);              // in flight across the first hand-over
-    }
-    for (int c = 0; c < nchunks; ++c) {
-        const int z = opaque_s(0);
-        lds_barrier();                                        // chunk c in place; chunk c-1 fully consumed
-        if (producer) {
+    // Producers and compute waves run separate loops with the same barriers:
+    // in one shared loop the wait-count insertion merged the producers'
+    // in-flight loads into the compute path and made it wait for all of its
+    // own stores at every chunk.
+    if (producer) {
+        if (nchunks > 0) {
+            load(0, tid - 64 * NW);
+            store(0, 0, tid - 64 * NW);
+            if (nchunks > 1) load(1, tid - 64 * NW);          // in flight across the first hand-over
+        }
+        for (int c = 0; c < nchunks; ++c) {
+            const int z = opaque_s(0);
+            lds_barrier();                                    // chunk c in place; chunk c-1 fully consumed
             const int pt = opaque_v(tid - 64 * NW);
             if (c + 1 < nchunks) store(c + 1, z, pt);         // into the slot chunk c-1 used
             if (c + 2 < nchunks) load(c + 2, pt);             // lands while chunk c computes
-            continue;
         }
+        return;
+    }
+    for (int c = 0; c < nchunks; ++c) {
+        const int z = opaque_s(0);
+        lds_barrier();                                        // the hand-over, as above
         if (!wvalid) continue;
         const int ln = opaque_v(lane);
         const int g4 = ln >> 4, r16 = ln & 15;
