@@ -860,16 +860,19 @@ __device__ __forceinline__ int opaque_s(int x) { asm volatile("" : "+s"(x)); ret
 // the value is computed at this point in program order
 template <typename T> __device__ __forceinline__ void pin_v(const T &x) { asm volatile("" ::"v"(x)); }
 
-// LDS layout of chunk_state_tr_kernel.  Rows are padded by 16 bytes (the
-// fragment reads of 16 consecutive rows then hit distinct banks) and every
-// fragment address is a per-lane base plus a compile-time offset.  K and Q
+// LDS layout of chunk_state_tr_kernel.  Rows are padded by 32 bytes and every
+// fragment address is a per-lane base plus a compile-time offset.  Measured on
+// gfx950 (8 waves on one CU): the 16-byte fragment reads of 16 rows and the
+// transpose reads of 4 rows x 4 lanes both run conflict-free at a 288-byte
+// row pitch (3.9 cycles per wave instruction) and take twice as long at 272
+// bytes; the LDS serves 256 bytes per clock to conflict-free 16-byte reads.  K and Q
 // rows hold their columns in paired order: the 16-byte unit 4 q + g of a row
 // holds columns 32 q + 4 g .. + 3 and 32 q + 16 + 4 g .. + 3, the eight
 // elements lane group g contributes to one 16x16x32 MFMA over k-blocks
 // (2 q, 2 q + 1) -- one 16-byte read per MFMA operand.
 template <int DK>
 struct KQRows {
-    static constexpr int PITCH = DK + 8;                               // elements
+    static constexpr int PITCH = DK + 16;                              // elements
     // element offset of column c (a multiple of 4) within a row
     __host__ __device__ static constexpr int col(int c) { return (c / 32) * 32 + ((c % 16) / 4) * 8 + ((c % 32) / 16) * 4; }
 };
@@ -880,7 +883,8 @@ struct KQRows {
 // times more bytes per CU than global_load_lds, whose throughput from HBM is
 // far lower than from L2.  Rows [0, CH) x columns [0, NCOL) of a token-major
 // matrix; rows >= valid_rows and columns >= valid_cols read as zeros.
-// PAIRED: K/Q layout above; else rows of pitch NCOL + 8, natural column order.
+// PAIRED: the K/Q column order above; else the source order.  PITCH: LDS row
+// pitch in elements.
 //
 // Every load is issued unconditionally, from unit 0 (always inside the tile)
 // where the unit itself is out of range, and zeros are selected when the
@@ -915,10 +919,9 @@ struct RowLoads {
     __device__ static __forceinline__ bool live(int u) { return UNITS % NPT == 0 || u < UNITS; }
 };
 
-template <typename E, int CH, int NCOL, int NPT, bool PAIRED>
+template <typename E, int CH, int NCOL, int NPT, bool PAIRED, int PITCH>
 struct RowCopy : RowLoads<E, CH, NCOL, NPT> {
     using B = RowLoads<E, CH, NCOL, NPT>;
-    static constexpr int PITCH = NCOL + 8;
     __device__ __forceinline__ void store(E *lds, int pt) const {
         unroll<B::PER>([&](auto i) {
             const int u = pt + NPT * i, row = u / B::UPR, cu = u % B::UPR;
@@ -937,10 +940,9 @@ __device__ __forceinline__ uint32_t from_lane_xor2(uint32_t x) {
 // units u and u ^ 2 of one 32-column group, swap halves through DPP, and each
 // writes one whole paired unit: 4 q + 2 a from units 4 q + a, 4 q + a + 2 (the
 // lower halves) or 4 q + 2 a + 1 (the upper halves).
-template <typename E, int CH, int NCOL, int NPT>
-struct RowCopy<E, CH, NCOL, NPT, true> : RowLoads<E, CH, NCOL, NPT> {
+template <typename E, int CH, int NCOL, int NPT, int PITCH>
+struct RowCopy<E, CH, NCOL, NPT, true, PITCH> : RowLoads<E, CH, NCOL, NPT> {
     using B = RowLoads<E, CH, NCOL, NPT>;
-    static constexpr int PITCH = KQRows<NCOL>::PITCH;
     static_assert(B::UPR % 4 == 0 && NPT % 64 == 0, "quads of lanes hold whole 32-column groups");
     __device__ __forceinline__ void store(E *lds, int pt) const {
         unroll<B::PER>([&](auto i) {
@@ -1012,7 +1014,10 @@ chunk_state_tr_kernel(const ChunkParams p) {
     using CB = ChunkBlock<E, CH, DK, VEC ? 2 : 1>;
     using KQ = KQRows<DK>;
     constexpr int NB = CH / 16, NKB = DK / 16, DVT = 16 * NW, NPT = 64 * NP;
-    constexpr int PK = KQ::PITCH, PV = DVT + 8;
+    // V rows: 2.4 cycles per transpose read at a pitch of DVT + 16 elements,
+    // 3.8 at DVT + 8 (which the per-channel-gate layout with 64 columns needs
+    // to stay within 160 KiB)
+    constexpr int PK = KQ::PITCH, PV = (VEC && NW == 4) ? DVT + 8 : DVT + 16;
     constexpr int TEAB = CB::TEA * (int)sizeof(E);              // bytes of TE + A in a slot
     constexpr int BSLOT = TEAB + CB::FLOATS * 4;                 // TE, A, then G, Gend | Gc
     static_assert(NB % 2 == 0 && NKB % 2 == 0, "k-blocks are consumed in pairs");
@@ -1059,9 +1064,9 @@ chunk_state_tr_kernel(const ChunkParams p) {
     // producer: one chunk's operands in registers.  load(c) may run ahead of
     // the slot hand-over; store(c) writes slot c & 1.  K and Q come from q and
     // k (scalar gate), or already gated and paired from chunk_prep (VEC).
-    RowCopy<E, CH, DK, NPT, !VEC> ck, cq;
-    RowCopy<E, CH, DK, NPT, false> ce;
-    RowCopy<E, CH, DVT, NPT, false> cv;
+    RowCopy<E, CH, DK, NPT, !VEC, PK> ck, cq;
+    RowCopy<E, CH, DK, NPT, false, PK> ce;
+    RowCopy<E, CH, DVT, NPT, false, PV> cv;
     FlatCopy<TEAB / 16, NPT> cb;
     FlatCopy<CB::FLOATS * 4 / 16, NPT> cf;
     auto load = [&](int c, int pt) __attribute__((always_inline)) {
