@@ -896,64 +896,67 @@ struct KQRows {
 // moves to LDS or scratch.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-template <typename E, int CH, int NCOL, int NPT>
-struct RowLoads {
-    static constexpr int VE = 16 / (int)sizeof(E), UPR = NCOL / VE, UNITS = CH * UPR;
-    static constexpr int PER = (UNITS + NPT - 1) / NPT;
-    static_assert(PER <= 32, "one valid bit per unit");
-    u32x4 r[PER];
-    uint32_t valid;                                           // bit i: unit i lies inside the tile
-    __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int pt) {
-        valid = 0;
-        unroll<PER>([&](auto i) {
-            const int u = pt + NPT * i, row = u / UPR, cu = u % UPR;
-            const bool ok = (UNITS % NPT == 0 || u < UNITS) && row < valid_rows && cu * VE < valid_cols;
-            r[i] = *reinterpret_cast<const u32x4 *>(src + (ok ? (int64_t)row * stride + cu * VE : 0));
-            valid |= (uint32_t)ok << (int)i;
-        });
-    }
-    // unit i of the last load, zero outside the tile
-    __device__ __forceinline__ u32x4 get(int i) const {
-        return (valid >> i) & 1u ? r[i] : u32x4{0u, 0u, 0u, 0u};
-    }
-    __device__ static __forceinline__ bool live(int u) { return UNITS % NPT == 0 || u < UNITS; }
-};
-
-template <typename E, int CH, int NCOL, int NPT, bool PAIRED, int PITCH>
-struct RowCopy : RowLoads<E, CH, NCOL, NPT> {
-    using B = RowLoads<E, CH, NCOL, NPT>;
-    __device__ __forceinline__ void store(E *lds, int pt) const {
-        unroll<B::PER>([&](auto i) {
-            const int u = pt + NPT * i, row = u / B::UPR, cu = u % B::UPR;
-            if (B::live(u)) *reinterpret_cast<u32x4 *>(lds + row * PITCH + cu * B::VE) = this->get(i);
-        });
-    }
-};
-
 // lane l receives x from lane l ^ 2 (DPP quad_perm [2, 3, 0, 1]; register only)
 __device__ __forceinline__ uint32_t from_lane_xor2(uint32_t x) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x4E, 0xF, 0xF, false);
 }
 
-// K / Q rows into the paired-column layout (KQRows).  Loads are the plain
-// contiguous ones (lane l: unit l of its row group); lanes l and l ^ 2 hold
-// units u and u ^ 2 of one 32-column group, swap halves through DPP, and each
-// writes one whole paired unit: 4 q + 2 a from units 4 q + a, 4 q + a + 2 (the
-// lower halves) or 4 q + 2 a + 1 (the upper halves).
-template <typename E, int CH, int NCOL, int NPT, int PITCH>
-struct RowCopy<E, CH, NCOL, NPT, true, PITCH> : RowLoads<E, CH, NCOL, NPT> {
-    using B = RowLoads<E, CH, NCOL, NPT>;
-    static_assert(B::UPR % 4 == 0 && NPT % 64 == 0, "quads of lanes hold whole 32-column groups");
-    __device__ __forceinline__ void store(E *lds, int pt) const {
-        unroll<B::PER>([&](auto i) {
-            const int u = pt + NPT * i, row = u / B::UPR, cu = u % B::UPR, a = cu & 3;
-            const u32x4 x = this->get(i);
-            u32x4 o;                                           // unit cu ^ 2, from lane ^ 2
-            unroll<4>([&](auto k) { o[(int)k] = from_lane_xor2(x[(int)k]); });
-            const bool lo = a < 2;
-            const u32x4 d = lo ? u32x4{x[0], x[1], o[0], o[1]} : u32x4{o[2], o[3], x[2], x[3]};
-            const int off = row * PITCH + 32 * (cu >> 2) + (lo ? 16 * a : 16 * (a - 2) + 8);
-            if (B::live(u)) *reinterpret_cast<u32x4 *>(lds + off) = d;
+// PAIRED (the K/Q layout): loads are the plain contiguous ones (lane l: unit l
+// of its row group); lanes l and l ^ 2 hold units u and u ^ 2 of one
+// 32-column group, swap halves through DPP, and each writes one whole paired
+// unit: 4 q + 2 a from units 4 q + a, 4 q + a + 2 (the lower halves) or
+// 4 q + 2 a + 1 (the upper halves).
+//
+// Which units a lane moves, and where they sit in global memory relative to
+// the chunk's first row and in LDS, is the same for every chunk: Plan holds
+// it, computed once; a chunk then costs one 64-bit add per load.
+template <typename E, int CH, int NCOL, int NPT, bool PAIRED, int PITCH>
+struct RowCopy {
+    static constexpr int VE = 16 / (int)sizeof(E), UPR = NCOL / VE, UNITS = CH * UPR;
+    static constexpr int PER = (UNITS + NPT - 1) / NPT;
+    static_assert(PER <= 32, "one bit per unit");
+    static_assert(!PAIRED || (UPR % 4 == 0 && NPT % 64 == 0), "quads of lanes hold whole 32-column groups");
+    struct Plan {
+        int64_t goff[PER];                                   // elements from the chunk's first row
+        int row[PER];
+        int loff[PER];                                       // LDS elements
+        uint32_t exists = 0, cols = 0, lo = 0;               // unit < UNITS; columns < valid_cols; PAIRED half
+    };
+    __device__ static __forceinline__ Plan plan(int64_t stride, int valid_cols, int pt) {
+        Plan pl;
+        unroll<PER>([&](auto i) {
+            const int u0 = pt + NPT * i;
+            const bool ex = UNITS % NPT == 0 || u0 < UNITS;
+            const int u = ex ? u0 : 0, row = u / UPR, cu = u % UPR, a = cu & 3;
+            pl.goff[i] = (int64_t)row * stride + cu * VE;
+            pl.row[i] = row;
+            pl.loff[i] = row * PITCH + (PAIRED ? 32 * (cu >> 2) + (a < 2 ? 16 * a : 16 * (a - 2) + 8) : cu * VE);
+            pl.exists |= (uint32_t)ex << (int)i;
+            pl.cols |= (uint32_t)(cu * VE < valid_cols) << (int)i;
+            pl.lo |= (uint32_t)(a < 2) << (int)i;
+        });
+        return pl;
+    }
+    u32x4 r[PER];
+    uint32_t valid;                                           // bit i: unit i lies inside the tile
+    __device__ __forceinline__ void load(const E *src, const Plan &pl, int valid_rows) {
+        valid = 0;
+        unroll<PER>([&](auto i) {
+            const bool ok = (pl.exists & pl.cols) >> (int)i & 1u && pl.row[i] < valid_rows;
+            r[i] = *reinterpret_cast<const u32x4 *>(src + (ok ? pl.goff[i] : 0));
+            valid |= (uint32_t)ok << (int)i;
+        });
+    }
+    __device__ __forceinline__ void store(E *lds, const Plan &pl) const {
+        unroll<PER>([&](auto i) {
+            const u32x4 x = (valid >> (int)i) & 1u ? r[i] : u32x4{0u, 0u, 0u, 0u};
+            u32x4 d = x;
+            if constexpr (PAIRED) {
+                u32x4 o;                                       // unit cu ^ 2, from lane ^ 2
+                unroll<4>([&](auto k) { o[(int)k] = from_lane_xor2(x[(int)k]); });
+                d = (pl.lo >> (int)i) & 1u ? u32x4{x[0], x[1], o[0], o[1]} : u32x4{o[2], o[3], x[2], x[3]};
+            }
+            if ((pl.exists >> (int)i) & 1u) *reinterpret_cast<u32x4 *>(lds + pl.loff[i]) = d;
         });
     }
 };
@@ -1061,40 +1064,50 @@ chunk_state_tr_kernel(const ChunkParams p) {
     const int64_t len = eos - bos;
     const int nchunks = (int)((len + CH - 1) / CH);
 
-    // producer: one chunk's operands in registers.  load(c) may run ahead of
-    // the slot hand-over; store(c) writes slot c & 1.  K and Q come from q and
-    // k (scalar gate), or already gated and paired from chunk_prep (VEC).
-    RowCopy<E, CH, DK, NPT, !VEC, PK> ck, cq;
-    RowCopy<E, CH, DK, NPT, false, PK> ce;
-    RowCopy<E, CH, DVT, NPT, false, PV> cv;
-    FlatCopy<TEAB / 16, NPT> cb;
-    FlatCopy<CB::FLOATS * 4 / 16, NPT> cf;
-    auto load = [&](int c, int pt) __attribute__((always_inline)) {
+    // producer: one chunk's operands in registers.  load(st, c) may run ahead
+    // of the slot hand-over; store(st, c) writes slot c & 1.  K and Q come
+    // from q and k (scalar gate), or already gated and paired from chunk_prep
+    // (VEC).  A chunk index past the end loads the last chunk again (every
+    // address stays inside the tensors).
+    using CK = RowCopy<E, CH, DK, NPT, !VEC, PK>;            // K, Q (VEC: K*G, scale Q*G, K*Gend)
+    using CV = RowCopy<E, CH, DVT, NPT, false, PV>;
+    struct Staged {
+        CK k, q, e;
+        CV v;
+        FlatCopy<TEAB / 16, NPT> b;
+        FlatCopy<CB::FLOATS * 4 / 16, NPT> f;
+    };
+    struct Plans {
+        typename CK::Plan k;
+        typename CV::Plan v;
+    };
+    auto load = [&](Staged &st, const Plans &pl, int c, int pt) __attribute__((always_inline)) {
+        c = c < nchunks ? c : nchunks - 1;
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
         const char *bk = blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES;
-        cb.load(bk, pt);
-        cf.load(bk + CB::GOFF, pt);
+        st.b.load(bk, pt);
+        st.f.load(bk + CB::GOFF, pt);
         if constexpr (VEC) {
             const E *tiles = reinterpret_cast<const E *>(bk) + CB::TEA;
-            ck.load(tiles, DK, CH, DK, pt);
-            cv.load(vg + t0 * sv, sv, clen, DV - col0, pt);
-            cq.load(tiles + CH * DK, DK, CH, DK, pt);
-            ce.load(tiles + 2 * CH * DK, DK, CH, DK, pt);
+            st.k.load(tiles, pl.k, CH);
+            st.v.load(vg + t0 * sv, pl.v, clen);
+            st.q.load(tiles + CH * DK, pl.k, CH);
+            st.e.load(tiles + 2 * CH * DK, pl.k, CH);
         } else {
-            ck.load(kg + t0 * sqk, sqk, clen, DK, pt);
-            cv.load(vg + t0 * sv, sv, clen, DV - col0, pt);
-            cq.load(qg + t0 * sqk, sqk, clen, DK, pt);
+            st.k.load(kg + t0 * sqk, pl.k, clen);
+            st.v.load(vg + t0 * sv, pl.v, clen);
+            st.q.load(qg + t0 * sqk, pl.k, clen);
         }
     };
-    auto store = [&](int c, int z, int pt) __attribute__((always_inline)) {
+    auto store = [&](const Staged &st, const Plans &pl, int c, int z, int pt) __attribute__((always_inline)) {
         const bool odd = c & 1;
-        cb.store((odd ? B1 : B0) + z, pt);
-        cf.store((odd ? B1 : B0) + z + TEAB, pt);
-        ck.store((odd ? K1 : K0) + z, pt);
-        cv.store((odd ? V1 : V0) + z, pt);
-        cq.store((odd ? Q1 : Q0) + z, pt);
-        if constexpr (VEC) ce.store((odd ? KE1 : KE0) + z, pt);
+        st.b.store((odd ? B1 : B0) + z, pt);
+        st.f.store((odd ? B1 : B0) + z + TEAB, pt);
+        st.k.store((odd ? K1 : K0) + z, pl.k);
+        st.v.store((odd ? V1 : V0) + z, pl.v);
+        st.q.store((odd ? Q1 : Q0) + z, pl.k);
+        if constexpr (VEC) st.e.store((odd ? KE1 : KE0) + z, pl.k);
     };
 
     // ---- entry state (C layout: S[kt][j] = S[16kt + 4g + j][col0 + wcol + r]) --
@@ -1113,18 +1126,35 @@ chunk_state_tr_kernel(const ChunkParams p) {
     // in one shared loop the wait-count insertion merged the producers'
     // in-flight loads into the compute path and made it wait for all of its
     // own stores at every chunk.
+    //
+    // Two register sets: when chunk c + 1 is stored (after hand-over c), chunk
+    // c + 2 is already in flight in the other set and chunk c + 3 is issued
+    // into the set just emptied, so every load has a whole chunk step to land.
+    // The loop body is unrolled over the two sets and free of per-chunk
+    // branches; a store past the last chunk goes to the idle slot, which no
+    // compute wave reads again.
     if (producer) {
         if (nchunks > 0) {
-            load(0, tid - 64 * NW);
-            store(0, 0, tid - 64 * NW);
-            if (nchunks > 1) load(1, tid - 64 * NW);          // in flight across the first hand-over
-        }
-        for (int c = 0; c < nchunks; ++c) {
-            const int z = opaque_s(0);
-            lds_barrier();                                    // chunk c in place; chunk c-1 fully consumed
-            const int pt = opaque_v(tid - 64 * NW);
-            if (c + 1 < nchunks) store(c + 1, z, pt);         // into the slot chunk c-1 used
-            if (c + 2 < nchunks) load(c + 2, pt);             // lands while chunk c computes
+            const int pt = tid - 64 * NW;
+            const Plans pl{CK::plan(VEC ? DK : sqk, DK, pt), CV::plan(sv, DV - col0, pt)};
+            Staged s0, s1;
+            load(s0, pl, 0, pt);
+            store(s0, pl, 0, 0, pt);
+            load(s1, pl, 1, pt);
+            load(s0, pl, 2, pt);
+            int c = 0;
+            for (; c + 1 < nchunks; c += 2) {
+                int z = opaque_s(0);
+                lds_barrier();                                // chunk c in place; chunk c-1 fully consumed
+                store(s1, pl, c + 1, z, pt);                  // into the slot chunk c-1 used
+                load(s1, pl, c + 3, pt);
+                z = opaque_s(0);
+                lds_barrier();                                // hand-over c + 1
+                store(s0, pl, c + 2, z, pt);
+                load(s0, pl, c + 4, pt);
+            }
+            if (c < nchunks) lds_barrier();                   // hand-over of the last (even) chunk
+            __builtin_amdgcn_s_waitcnt(0);                    // no load left in flight at exit
         }
         return;
     }
@@ -1220,14 +1250,14 @@ chunk_state_tr_kernel(const ChunkParams p) {
             for (int kt = 0; kt < NKB; ++kt)
                 S[kt] = mfma_pair(ld_tr_pair<E>(Ktr + 32 * q * PK + KQ::col(16 * kt),
                                                 Ktr + (32 * q + 16) * PK + KQ::col(16 * kt)), Wb[q], S[kt]);
+        E *orow = og + (t0 + r16) * sv;                          // token t0 + 16 I + r: orow + 16 I sv
 #pragma unroll
         for (int I = 0; I < NB; ++I) {
             // convert before the lane-dependent store condition: the accumulator
             // is read in straight-line code, not behind an exec-skip branch
             const typename EL::frag ob = EL::cvt(OT[I]);
             pin_v(ob);
-            const int row = 16 * I + r16;
-            if (row < clen) *reinterpret_cast<typename EL::frag *>(og + (t0 + row) * sv) = ob;
+            if (16 * I + r16 < clen) *reinterpret_cast<typename EL::frag *>(orow + (int64_t)(16 * I) * sv) = ob;
         }
     }
 
