@@ -303,7 +303,10 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
                 gam[lane] = x;
                 float *gblk = reinterpret_cast<float *>(blk_base + CB::GOFF);
                 gblk[lane] = __expf(x);
-                gblk[CH + lane] = __expf(last - x);
+                // zero past the end of the sequence: the state update scales
+                // those rows of U~ (or V without the delta rule) by it, and the
+                // state kernel leaves K and V rows there unzeroed
+                gblk[CH + lane] = lane < clen ? __expf(last - x) : 0.f;
             }
         }
     }
@@ -882,15 +885,21 @@ struct KQRows {
 // MI355X with all CUs streaming data not yet cached, this path moves several
 // times more bytes per CU than global_load_lds, whose throughput from HBM is
 // far lower than from L2.  Rows [0, CH) x columns [0, NCOL) of a token-major
-// matrix; rows >= valid_rows and columns >= valid_cols read as zeros.
+// matrix; rows >= valid_rows and columns >= valid_cols hold some other finite
+// element of the tile (see below).
 // PAIRED: the K/Q column order above; else the source order.  PITCH: LDS row
 // pitch in elements.
 //
 // Every load is issued unconditionally, from unit 0 (always inside the tile)
-// where the unit itself is out of range, and zeros are selected when the
-// registers are stored (a select next to the load would wait for it).  Loads
-// under a per-lane branch made the wait-count insertion put a full vmcnt(0)
-// wait in front of each following load, which serialised them.
+// where the unit itself is out of range: loads under a per-lane branch made
+// the wait-count insertion put a full vmcnt(0) wait in front of each following
+// load, which serialised them.  Such a unit is not zeroed either: a row past
+// the end of a sequence has beta = 0 and zero k, q in chunk_prep, so its
+// columns of TE and A are exactly zero, and its decay Gend (which scales its
+// row of U~, or of V without the delta rule, in the state update) is written
+// as zero; per-channel gates zero its K*Gend row instead.  Any finite value
+// in its K, Q or V row then contributes nothing, and its output row is not
+// stored.  Columns past dv belong to 16-column strips no compute wave uses.
 // The registers are a vector type: a 16-byte struct copied under a condition
 // becomes a memcpy through a stack slot, which the alloca promotion pass then
 // moves to LDS or scratch.
@@ -938,18 +947,15 @@ struct RowCopy {
         return pl;
     }
     u32x4 r[PER];
-    uint32_t valid;                                           // bit i: unit i lies inside the tile
     __device__ __forceinline__ void load(const E *src, const Plan &pl, int valid_rows) {
-        valid = 0;
         unroll<PER>([&](auto i) {
             const bool ok = (pl.exists & pl.cols) >> (int)i & 1u && pl.row[i] < valid_rows;
             r[i] = *reinterpret_cast<const u32x4 *>(src + (ok ? pl.goff[i] : 0));
-            valid |= (uint32_t)ok << (int)i;
         });
     }
     __device__ __forceinline__ void store(E *lds, const Plan &pl) const {
         unroll<PER>([&](auto i) {
-            const u32x4 x = (valid >> (int)i) & 1u ? r[i] : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 x = r[i];
             u32x4 d = x;
             if constexpr (PAIRED) {
                 u32x4 o;                                       // unit cu ^ 2, from lane ^ 2
