@@ -173,6 +173,39 @@ __device__ __forceinline__ void dma_rows(E *lds, const E *src, int64_t stride, i
     }
 }
 
+// The same copy through registers: load() issues every 16-byte load of the
+// tile at once (unconditionally, from a clamped address: a load under a
+// per-lane branch gets a full wait in front of the next one), store() writes
+// the swizzled LDS tile, zeros outside [valid_rows, valid_cols).  Measured on
+// MI355X with every CU streaming, plain loads move several times more bytes
+// per CU than global_load_lds.
+template <typename E, int CH, int NCOL, int NT>
+struct RegRows {
+    using S = Swz<E, NCOL>;
+    static constexpr int UNITS = CH * S::UPR, PER = UNITS / NT, NWV = NT / 64;
+    static_assert(UNITS % NT == 0 && PER <= 32, "tile does not split evenly over the workgroup");
+    u32x4 r[PER];
+    uint32_t ok;
+    __device__ __forceinline__ void load(const E *src, int64_t stride, int valid_rows, int valid_cols, int tid) {
+        const int wave = tid >> 6, lane = tid & 63;
+        ok = 0;
+        unroll<PER>([&](auto i) {
+            const int u = (wave + NWV * (int)i) * 64 + lane;
+            const int row = u / S::UPR, pp = u % S::UPR, c = pp ^ (row & (S::UPR - 1));
+            const bool in = row < valid_rows && c * S::VE < valid_cols;
+            r[i] = *reinterpret_cast<const u32x4 *>(src + (in ? (int64_t)row * stride + c * S::VE : 0));
+            ok |= (uint32_t)in << (int)i;
+        });
+    }
+    __device__ __forceinline__ void store(E *lds, int tid) const {
+        const int wave = tid >> 6, lane = tid & 63;
+        unroll<PER>([&](auto i) {
+            const int u = (wave + NWV * (int)i) * 64 + lane;
+            *reinterpret_cast<u32x4 *>(lds + u * S::VE) = (ok >> (int)i) & 1u ? r[i] : u32x4{0u, 0u, 0u, 0u};
+        });
+    }
+};
+
 // contiguous copy of n16 16-byte units (identity layout)
 template <typename E, int NUNITS, int NT>
 __device__ __forceinline__ void dma_flat(E *lds, const E *src, int tid) {
@@ -260,31 +293,48 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     char *blk_base = reinterpret_cast<char *>(p.blocks) + (slot * H + h) * CB::BYTES;
     E *blk = reinterpret_cast<E *>(blk_base);                                    // TE, then A
 
-    // ---- stage K, Q rows; cumulative decay; beta --------------------------
-    dma_rows<E, CH, DK, NT>(Kst, kg, sqk, clen, DK, tid);
-    dma_rows<E, CH, DK, NT>(Qst, qg, sqk, clen, DK, tid);
-    if (tid < CH) bet[tid] = (p.use_delta && tid < clen) ? p.beta[(t0 + tid) * H + h] : 0.f;
+    // ---- stage: gate and beta first (the scans wait for them), then K, Q rows
+    // Every load is unconditional, from a clamped row, and all are in flight
+    // together; rows past the end are zeroed afterwards.
+    float beta_v = 0.f, g_v = 0.f;
+    if (wave == 0) {
+        const int row = lane < clen ? lane : 0;
+        if (p.use_delta) beta_v = p.beta[(t0 + row) * H + h];
+        if constexpr (GATE != 2)
+            if (p.g) g_v = p.g[(t0 + row) * H + h];
+    }
+    // per-channel gate: thread (sg, cg) holds channels 4 cg .. + 3 of rows
+    // RPS sg .. + RPS - 1
+    constexpr int CG = DK / 4, SGN = NT / CG, RPS = CH / SGN;
+    static_assert(GATE != 2 || (SGN * CG == NT && RPS * SGN == CH), "gate tile does not split over the workgroup");
+    const int cg = tid % CG, sg = tid / CG;
+    f32x4 gv[GATE == 2 ? RPS : 1];
     if constexpr (GATE == 2) {
-        for (int vi = tid; vi < CH * DK / 4; vi += NT) {
-            const int row = vi / (DK / 4), col = (vi % (DK / 4)) * 4;
-            st4(gam + row * PG + col,
-                row < clen ? ld4(p.g + ((t0 + row) * H + h) * DK + col) : f32x4{0.f, 0.f, 0.f, 0.f});
-        }
+        unroll<RPS>([&](auto i) {
+            const int row = sg * RPS + (int)i, rr = row < clen ? row : 0;
+            gv[i] = ld4(p.g + ((t0 + rr) * H + h) * DK + 4 * cg);
+        });
+    }
+    RegRows<E, CH, DK, NT> rk, rq;
+    rk.load(kg, sqk, clen, DK, tid);
+    rq.load(qg, sqk, clen, DK, tid);
+    if (wave == 0 && lane < CH) bet[lane] = lane < clen ? beta_v : 0.f;
+    if constexpr (GATE == 2) {
+        // inclusive cumulative sum over rows: within the thread's rows in
+        // registers, then the totals of the preceding row segments from LDS
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        unroll<RPS>([&](auto i) {
+            if (sg * RPS + (int)i < clen) acc += gv[i];
+            gv[i] = acc;
+        });
+        // segment totals in the K stage, free until K and Q are stored below
+        f32x4 *gtot = reinterpret_cast<f32x4 *>(Kst);
+        gtot[sg * CG + cg] = acc;
         if (tid < 4) flag[tid] = 0;
         __syncthreads();
-        constexpr int NP = NT / DK, SEG = CH / NP;
-        const int cc = tid % DK, part = tid / DK;
-        float acc = 0.f;
-        for (int t = part * SEG; t < (part + 1) * SEG; ++t) {
-            acc += gam[t * PG + cc];
-            gam[t * PG + cc] = acc;
-        }
-        __syncthreads();
-        float off = 0.f;
-        for (int q2 = 0; q2 < part; ++q2) off += gam[((q2 + 1) * SEG - 1) * PG + cc];
-        __syncthreads();
-        if (part > 0)
-            for (int t = part * SEG; t < (part + 1) * SEG; ++t) gam[t * PG + cc] += off;
+        f32x4 off = {0.f, 0.f, 0.f, 0.f};
+        for (int s2 = 0; s2 < sg; ++s2) off += gtot[s2 * CG + cg];
+        unroll<RPS>([&](auto i) { st4(gam + (sg * RPS + (int)i) * PG + 4 * cg, gv[i] + off); });
         __syncthreads();
         for (int it = tid; it < NB * DK; it += NT) {
             const int b = it / DK, c2 = it % DK;
@@ -292,7 +342,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         }
     } else {
         if (wave == 0) {
-            float x = (p.g && lane < clen) ? p.g[(t0 + lane) * H + h] : 0.f;
+            float x = lane < clen ? g_v : 0.f;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
                 const float y = __shfl_up(x, o);
@@ -310,7 +360,8 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             }
         }
     }
-    dma_wait();
+    rk.store(Kst, tid);
+    rq.store(Qst, tid);
     __syncthreads();
 
     // ---- K K^T (-> M) and Q K^T (-> A), lower tile pairs -----------------

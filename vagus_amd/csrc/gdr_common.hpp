@@ -161,6 +161,7 @@ template <typename T> __host__ __device__ constexpr T cmax(T a, T b) { return a 
 
 // 16-byte global access
 struct alignas(16) Vec16 { uint32_t w[4]; };
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // f(std::integral_constant<int, 0>{}) ... f(std::integral_constant<int, N - 1>{}).
 // Register arrays indexed inside f are indexed by constants from the start:
