@@ -58,6 +58,29 @@ enum vgdr_gate {
     VGDR_GATE_VECTOR = 2       /* g [n_tokens, H, dk]: per key channel  — Kimi Delta Attn (KDA)  */
 };
 
+/*
+ * Producer fusions: elementwise work on the scan's operands that a caller
+ * would otherwise do in separate passes, applied where the kernels read those
+ * operands.  These are the flags the reference hands to its fla call,
+ * linear_attention.py:457-497 (use_qk_l2norm_in_kernel,
+ * use_beta_sigmoid_in_kernel, use_gate_in_kernel with A_log / dt_bias and
+ * safe_gate / lower_bound), with the reference's own activations
+ * (:703-706, :719-736).  A NULL vgdr_fusion pointer means none.
+ */
+typedef struct vgdr_fusion {
+    int qk_l2norm;          /* q, k un-normalised: x rsqrt(sum_c x_c^2 + 1e-6) per (token, head), rounded
+                               to q's type (needs use_delta) */
+    int beta_sigmoid;       /* beta holds logits: sigmoid(beta) (needs use_delta) */
+    int gate_activation;    /* gate_kind 2 only: g holds the pre-activation f [n_tokens, H, dk] and
+                               g = lower_bound_set ? lower_bound * sigmoid(exp(A_log[h]) (f + dt_bias[h dk + c]))
+                                                   : -exp(A_log[h]) softplus(f + dt_bias[h dk + c]) */
+    int gate_dtype;         /* element type of f: VGDR_F32, or the dtype of q */
+    const float *A_log;     /* [H] fp32 */
+    const float *dt_bias;   /* [H * dk] fp32 */
+    int lower_bound_set;
+    float lower_bound;
+} vgdr_fusion;
+
 /* Library version (major * 10000 + minor * 100 + patch). */
 int vgdr_version(void);
 
@@ -118,6 +141,27 @@ int vgdr_chunk_state(int dtype, int gate_kind, int use_delta,
                      float scale, int chunk_size, hipStream_t stream);
 
 /*
+ * vgdr_chunk_fwd / vgdr_chunk_prep with producer fusions (vgdr_fusion above;
+ * 16-bit dtypes).  The state phase reads only what the prep phase wrote, so
+ * vgdr_chunk_state is the same for fused and unfused calls.  Replaces the
+ * fla call at linear_attention.py:474-497 with its *_in_kernel flags set.
+ */
+int vgdr_chunk_fwd_fused(int dtype, int gate_kind, int use_delta,
+                         const void *q, const void *k, const void *v,
+                         const float *g, const float *beta,
+                         void *o, const float *initial_state, float *final_state,
+                         const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                         int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                         float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
+int vgdr_chunk_prep_fused(int dtype, int gate_kind, int use_delta,
+                          const void *q, const void *k, const void *v,
+                          const float *g, const float *beta,
+                          void *o, const float *initial_state, float *final_state,
+                          const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                          int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                          float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
+
+/*
  * Token-by-token recurrence.  The decode step is T = 1 with
  * initial_state == final_state (in place), replacing recurrent_scan at
  * linear_attention.py:945-947 and the state.copy_ at :950.  Any T works (the
@@ -130,6 +174,18 @@ int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta,
                        const int32_t *cu_seqlens,
                        int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
                        float scale, hipStream_t stream);
+
+/* vgdr_recurrent_fwd with producer fusions (vgdr_fusion; any dtype).  No
+ * reference counterpart (the reference normalises and activates in torch
+ * before recurrent_scan, linear_attention.py:698-753); a decode step that
+ * takes raw projections. */
+int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta,
+                             const void *q, const void *k, const void *v,
+                             const float *g, const float *beta,
+                             void *o, const float *initial_state, float *final_state,
+                             const int32_t *cu_seqlens,
+                             int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                             float scale, const vgdr_fusion *fusion, hipStream_t stream);
 
 /*
  * Packed-batch schedule.  No reference counterpart (the reference has no

@@ -21,6 +21,9 @@ Functions and the reference lines they follow:
     varlen          (no reference counterpart)    per-segment loop over cu_seqlens
     chunk_table     (no reference counterpart)    integer chunk / schedule table
     chunk_scan_flops linear_attention.py:128-143  FLOPs per token per head
+    l2norm          linear_attention.py:703-706   the q, k producer (fused by the kernels' qk_l2norm)
+    gate_activation linear_attention.py:722-734   per-channel gate from its pre-activation
+    beta_sigmoid    linear_attention.py:735-736   beta from its logits
 
 Layouts follow the reference (linear_attention.py:146-154): q, k (B, L, H, dk),
 v (B, L, H, dv), g (B, L, H) or (B, L, H, dk), beta (B, L, H), S0 (B, H, dk, dv).
@@ -33,7 +36,9 @@ delta-rule overwrite identity) and against an independent dense-matrix
 statement of the update above; the chunk forms against ``recurrent`` at
 1e-12 in fp64, chunk-size / padding invariance and the scalar == constant
 vector-gate reduction; ``varlen`` by segment isolation; ``chunk_table`` by
-brute-force enumeration; ``chunk_scan_flops`` by the reference's known answers.
+brute-force enumeration; ``chunk_scan_flops`` by the reference's known answers;
+the producers by their defining properties (unit norms and scale invariance,
+softplus / sigmoid identities and limits, the bounded gate's range).
 """
 from __future__ import annotations
 
@@ -293,3 +298,37 @@ def chunk_scan_flops(dk: int, dv: int, chunk: int, delta: bool) -> float:
     state = (6 if delta else 4) * dk * dv
     intra = 2 * chunk * ((3 * dk + 2 * dv) if delta else (dk + dv))
     return 3.0 * (state + intra)
+
+
+# ---------------------------------------------------------------------------
+# the producers the kernels can fuse (vgdr_fusion)
+# ---------------------------------------------------------------------------
+
+def _hi(x):
+    """At least fp32 (linear_attention.py:700-702)."""
+    return x.to(torch.promote_types(x.dtype, torch.float32))
+
+
+def l2norm(x, eps: float = 1e-6):
+    """x rsqrt(sum over the last dim of x^2 + eps), computed in at least fp32 and
+    returned in x's dtype (linear_attention.py:703-706)."""
+    h = _hi(x)
+    return (h * torch.rsqrt(h.pow(2).sum(-1, keepdim=True) + eps)).to(x.dtype)
+
+
+def gate_activation(f, A_log, dt_bias, lower_bound=None):
+    """Per-channel log-decay from the pre-activation f (B, L, H, dk), with A_log
+    (H,) and dt_bias (H * dk,) (linear_attention.py:722-734):
+    -exp(A_log) softplus(f + dt_bias), or lower_bound * sigmoid(exp(A_log)
+    (f + dt_bias)) when lower_bound is given.  fp32 (at least)."""
+    H, dk = f.shape[-2], f.shape[-1]
+    z = _hi(f) + _hi(dt_bias).reshape(H, dk)
+    a = _hi(A_log).exp()[:, None]
+    if lower_bound is not None:
+        return lower_bound * torch.sigmoid(a * z)
+    return -a * torch.nn.functional.softplus(z)
+
+
+def beta_sigmoid(b):
+    """beta from its logits (linear_attention.py:735-736)."""
+    return torch.sigmoid(_hi(b))

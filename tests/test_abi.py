@@ -62,17 +62,18 @@ def test_argument_checks_return_status_codes():
     assert _chunk_call(T=4, q=17, k=32, v=48, o=64, g=80, beta=96) == _lib.VGDR_ERR_INVALID  # alignment
     # the workspace must be present and large enough
     need = L.vgdr_chunk_workspace_size(1, 1, 2, 64, 4, 128, 2, 0, 64)
-    # per (chunk, head): TE and A (2 C^2 elements), then G and Gend (2 C floats)
-    assert need == 2 * 4 * (2 * 64 * 64 * 2 + 2 * 64 * 4)
+    # per (chunk, head): TE and A (2 C^2 elements), then the row factors GX, GO,
+    # GE (3 C floats), Gc and three floats of padding
+    assert need == 2 * 4 * (2 * 64 * 64 * 2 + (3 * 64 + 4) * 4)
     assert _chunk_call(T=64, q=16, k=32, v=48, o=64, g=80, beta=96, ws=None) == _lib.VGDR_ERR_INVALID
     assert _chunk_call(T=64, q=16, k=32, v=48, o=64, g=80, beta=96, ws=4096, nbytes=need - 1) == _lib.VGDR_ERR_INVALID
     assert b'workspace' in L.vgdr_last_error()
     # fp32 with 128-wide keys runs 32-token chunks; packed batches add the segment table
-    assert L.vgdr_chunk_workspace_size(0, 1, 1, 64, 1, 128, 1, 0, 64) == 2 * (2 * 32 * 32 * 4 + 2 * 32 * 4)
-    assert L.vgdr_chunk_workspace_size(1, 1, 1, 100, 2, 64, 3, 1, 64) == 256 + (2 + 3) * 2 * (2 * 64 * 64 * 2 + 2 * 64 * 4)
+    assert L.vgdr_chunk_workspace_size(0, 1, 1, 64, 1, 128, 1, 0, 64) == 2 * (2 * 32 * 32 * 4 + (3 * 32 + 4) * 4)
+    assert L.vgdr_chunk_workspace_size(1, 1, 1, 100, 2, 64, 3, 1, 64) == 256 + (2 + 3) * 2 * (2 * 64 * 64 * 2 + (3 * 64 + 4) * 4)
     # a per-channel gate (16-bit) adds the gated K, Q, K*Gend tiles and Gc per (chunk, head)
     assert L.vgdr_chunk_workspace_size(1, 2, 1, 64, 1, 128, 1, 0, 64) == 2 * 64 * 64 * 2 + 3 * 64 * 128 * 2 + 128 * 4
-    assert L.vgdr_chunk_workspace_size(0, 2, 1, 64, 1, 128, 1, 0, 64) == 2 * (2 * 32 * 32 * 4 + 2 * 32 * 4)
+    assert L.vgdr_chunk_workspace_size(0, 2, 1, 64, 1, 128, 1, 0, 64) == 2 * (2 * 32 * 32 * 4 + (3 * 32 + 4) * 4)
     rc = L.vgdr_recurrent_fwd(1, 1, 1, None, None, None, None, None, None, None, None, None,
                               1, 0, 4, 128, 256, 1, 1.0, None)
     assert rc == _lib.VGDR_ERR_UNSUPPORTED

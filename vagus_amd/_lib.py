@@ -16,8 +16,18 @@ VGDR_OK, VGDR_ERR_INVALID, VGDR_ERR_UNSUPPORTED, VGDR_ERR_HIP = 0, 1, 2, 3
 VGDR_F32, VGDR_BF16, VGDR_F16 = 0, 1, 2
 VGDR_GATE_NONE, VGDR_GATE_SCALAR, VGDR_GATE_VECTOR = 0, 1, 2
 
+
+
+class Fusion(ctypes.Structure):
+    """struct vgdr_fusion: the producer fusions of a scan call."""
+    _fields_ = [('qk_l2norm', ctypes.c_int), ('beta_sigmoid', ctypes.c_int), ('gate_activation', ctypes.c_int),
+                ('gate_dtype', ctypes.c_int), ('A_log', ctypes.c_void_p), ('dt_bias', ctypes.c_void_p),
+                ('lower_bound_set', ctypes.c_int), ('lower_bound', ctypes.c_float)]
+
+
 # every symbol the header declares, with its ctypes signature
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+_FZ = ctypes.POINTER(Fusion)
 SIGNATURES = {
     'vgdr_version': (_I, []),
     'vgdr_last_error': (ctypes.c_char_p, []),
@@ -28,8 +38,14 @@ SIGNATURES = {
                              _L, _L, _L, _L, _L, _L, _F, _I, _P]),
     'vgdr_chunk_state': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                               _L, _L, _L, _L, _L, _L, _F, _I, _P]),
+    'vgdr_chunk_fwd_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
+                                  _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
+    'vgdr_chunk_prep_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
+                                   _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
     'vgdr_recurrent_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                 _L, _L, _L, _L, _L, _L, _F, _P]),
+    'vgdr_recurrent_fwd_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                      _L, _L, _L, _L, _L, _L, _F, _FZ, _P]),
     'vgdr_varlen_workspace_size': (_L, [_L]),
     'vgdr_varlen_prepare': (_I, [_P, _L, _L, _I, _P, _P]),
 }

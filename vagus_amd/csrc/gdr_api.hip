@@ -61,6 +61,36 @@ int check_common(const char *fn, int dtype, int gate_kind, int use_delta, const 
     return VGDR_OK;
 }
 
+// the producer fusions a call asks for, checked against the scan's settings
+int check_fusion(const char *fn, const vgdr_fusion *fz, int dtype, int gate_kind, int use_delta, bool chunked,
+                 vgdr::Fusion &out) {
+    out = vgdr::Fusion{};
+    if (!fz) return VGDR_OK;
+    const bool any = fz->qk_l2norm || fz->beta_sigmoid || fz->gate_activation;
+    if (!any) return VGDR_OK;
+    if (chunked && dtype == VGDR_F32)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: producer fusions take 16-bit q, k, v", fn);
+    if ((fz->qk_l2norm || fz->beta_sigmoid) && !use_delta)
+        return fail(VGDR_ERR_INVALID, "%s: the fused L2 norm and beta sigmoid need the delta rule", fn);
+    if (fz->gate_activation) {
+        if (gate_kind != VGDR_GATE_VECTOR)
+            return fail(VGDR_ERR_INVALID, "%s: the fused gate activation is for the per-channel gate", fn);
+        if (!fz->A_log || !fz->dt_bias)
+            return fail(VGDR_ERR_INVALID, "%s: the fused gate activation needs A_log and dt_bias", fn);
+        if (fz->gate_dtype != VGDR_F32 && fz->gate_dtype != dtype)
+            return fail(VGDR_ERR_INVALID, "%s: gate_dtype must be VGDR_F32 or the dtype of q", fn);
+    }
+    out.qk_l2norm = fz->qk_l2norm ? 1 : 0;
+    out.beta_sigmoid = fz->beta_sigmoid ? 1 : 0;
+    out.gate_act = fz->gate_activation ? 1 : 0;
+    out.gate_16 = fz->gate_activation && fz->gate_dtype != VGDR_F32 ? 1 : 0;
+    out.A_log = fz->A_log;
+    out.dt_bias = fz->dt_bias;
+    out.lb_set = fz->lower_bound_set ? 1 : 0;
+    out.lb = fz->lower_bound;
+    return VGDR_OK;
+}
+
 // chunk length the kernels use: 32 when asked for <= 32, else 64; fp32 always
 // uses 32 (its double-buffered 64-token tiles overflow LDS)
 int effective_chunk(int dtype, int64_t dk, int chunk_size) {
@@ -95,10 +125,13 @@ int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_del
                const void *v, const float *g, const float *beta, void *o, const float *initial_state,
                float *final_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B,
                int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
-               hipStream_t stream) {
+               const vgdr_fusion *fusion, hipStream_t stream) {
     g_err[0] = 0;
     int rc = check_common(fn, dtype, gate_kind, use_delta, q, k, v, g, beta, o, cu_seqlens,
                           B, T, H, dk, dv, n_seqs);
+    if (rc) return rc;
+    vgdr::Fusion fz;
+    rc = check_fusion(fn, fusion, dtype, gate_kind, use_delta, true, fz);
     if (rc) return rc;
     if (dv <= 0 || dv % 16)
         return fail(VGDR_ERR_UNSUPPORTED, "%s: dv=%lld (must be a positive multiple of 16)", fn, (long long)dv);
@@ -128,6 +161,7 @@ int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_del
     p.n_chunk_slots = (int)ws.slots;
     p.use_delta = use_delta ? 1 : 0;
     p.scale = scale;
+    p.fz = fz;
     int32_t *table = cu_seqlens ? static_cast<int32_t *>(workspace) : nullptr;
     return hip_status(vgdr::chunk_fwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, p, table, phases, stream),
                       fn);
@@ -168,25 +202,49 @@ int64_t vgdr_chunk_workspace_size(int dtype, int gate_kind, int64_t B, int64_t T
         const float *beta, void *o, const float *initial_state, float *final_state, const int32_t *cu_seqlens, \
         void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,     \
         int64_t n_seqs, float scale, int chunk_size, hipStream_t stream
-#define VGDR_CHUNK_PASS                                                                                    \
+#define VGDR_CHUNK_ARGS_FUSED                                                                              \
+    int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v, const float *g,     \
+        const float *beta, void *o, const float *initial_state, float *final_state, const int32_t *cu_seqlens, \
+        void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,     \
+        int64_t n_seqs, float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream
+#define VGDR_CHUNK_PASS_NOFUSION                                                                           \
     dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state, final_state, cu_seqlens, workspace,      \
-        workspace_bytes, B, T, H, dk, dv, n_seqs, scale, chunk_size, stream
+        workspace_bytes, B, T, H, dk, dv, n_seqs, scale, chunk_size, nullptr, stream
+#define VGDR_CHUNK_PASS_FUSED                                                                              \
+    dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state, final_state, cu_seqlens, workspace,      \
+        workspace_bytes, B, T, H, dk, dv, n_seqs, scale, chunk_size, fusion, stream
 
 int vgdr_chunk_fwd(VGDR_CHUNK_ARGS) {
-    return chunk_call("vgdr_chunk_fwd", vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, VGDR_CHUNK_PASS);
+    return chunk_call("vgdr_chunk_fwd", vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, VGDR_CHUNK_PASS_NOFUSION);
 }
-int vgdr_chunk_prep(VGDR_CHUNK_ARGS) { return chunk_call("vgdr_chunk_prep", vgdr::CHUNK_PREP, VGDR_CHUNK_PASS); }
-int vgdr_chunk_state(VGDR_CHUNK_ARGS) { return chunk_call("vgdr_chunk_state", vgdr::CHUNK_STATE, VGDR_CHUNK_PASS); }
+int vgdr_chunk_prep(VGDR_CHUNK_ARGS) {
+    return chunk_call("vgdr_chunk_prep", vgdr::CHUNK_PREP, VGDR_CHUNK_PASS_NOFUSION);
+}
+int vgdr_chunk_state(VGDR_CHUNK_ARGS) {
+    return chunk_call("vgdr_chunk_state", vgdr::CHUNK_STATE, VGDR_CHUNK_PASS_NOFUSION);
+}
+int vgdr_chunk_fwd_fused(VGDR_CHUNK_ARGS_FUSED) {
+    return chunk_call("vgdr_chunk_fwd_fused", vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, VGDR_CHUNK_PASS_FUSED);
+}
+int vgdr_chunk_prep_fused(VGDR_CHUNK_ARGS_FUSED) {
+    return chunk_call("vgdr_chunk_prep_fused", vgdr::CHUNK_PREP, VGDR_CHUNK_PASS_FUSED);
+}
 #undef VGDR_CHUNK_ARGS
-#undef VGDR_CHUNK_PASS
+#undef VGDR_CHUNK_ARGS_FUSED
+#undef VGDR_CHUNK_PASS_NOFUSION
+#undef VGDR_CHUNK_PASS_FUSED
 
-int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
-                       const float *g, const float *beta, void *o, const float *initial_state,
-                       float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H,
-                       int64_t dk, int64_t dv, int64_t n_seqs, float scale, hipStream_t stream) {
+int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta, const void *q, const void *k,
+                             const void *v, const float *g, const float *beta, void *o,
+                             const float *initial_state, float *final_state, const int32_t *cu_seqlens,
+                             int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
+                             const vgdr_fusion *fusion, hipStream_t stream) {
     g_err[0] = 0;
     int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o,
                           cu_seqlens, B, T, H, dk, dv, n_seqs);
+    if (rc) return rc;
+    vgdr::Fusion fz;
+    rc = check_fusion("vgdr_recurrent_fwd", fusion, dtype, gate_kind, use_delta, false, fz);
     if (rc) return rc;
     if (dv != 64 && dv != 128)
         return fail(VGDR_ERR_UNSUPPORTED, "vgdr_recurrent_fwd: dv=%lld (supported: 64, 128)", (long long)dv);
@@ -206,8 +264,17 @@ int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, c
     p.n_seqs = (int)n_seqs;
     p.use_delta = use_delta ? 1 : 0;
     p.scale = scale;
+    p.fz = fz;
     return hip_status(vgdr::recurrent_fwd(dtype, (int)dk, (int)dv, gate_kind == VGDR_GATE_VECTOR, p, stream),
                       "vgdr_recurrent_fwd launch");
+}
+
+int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                       const float *g, const float *beta, void *o, const float *initial_state,
+                       float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H,
+                       int64_t dk, int64_t dv, int64_t n_seqs, float scale, hipStream_t stream) {
+    return vgdr_recurrent_fwd_fused(dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state, final_state,
+                                    cu_seqlens, B, T, H, dk, dv, n_seqs, scale, nullptr, stream);
 }
 
 int64_t vgdr_varlen_workspace_size(int64_t n_seqs) {

@@ -54,9 +54,11 @@ __device__ __forceinline__ int frag_pos(int I, int kb, int lane) {
 
 // The per-(chunk slot, head) block chunk_prep leaves in the workspace: TE and
 // A (CH x CH each, element type, tile-pair fragment order), then
-//   scalar gate (or none): G_t = exp(gamma_t) and Gend_t = exp(gamma_C - gamma_t)
-//       (CH floats each; gamma is constant past a partial chunk's end, so
-//       G[CH - 1] is the chunk's total decay);
+//   scalar gate (or none), with G_t = exp(gamma_t), Gend_t = exp(gamma_C - gamma_t)
+//       and the rows' L2-norm factors rk_t, rq_t (1 unless the norm is fused):
+//       GX_t = G_t rk_t (for X), GO_t = scale G_t rq_t (for O), GE_t = Gend_t rk_t
+//       (for the state update; 0 past a partial chunk's end), CH floats each,
+//       then Gc = exp(gamma_C) and three floats of padding;
 //   per-channel gate, 16-bit elements (VEC): the gated tiles K*G, scale Q*G and
 //       K*Gend (CH x DK each, element type, rows in the paired-column order of
 //       KQRows, unpadded), then Gc = exp(gamma_C) (DK floats).
@@ -67,7 +69,7 @@ struct ChunkBlock {
     static constexpr int TEA = 2 * CH * CH;                                   // elements of TE and A
     static constexpr int TILES = VEC ? 3 * CH * DK : 0;                       // elements of the gated tiles
     static constexpr int GOFF = (TEA + TILES) * (int)sizeof(E);               // byte offset of the floats
-    static constexpr int FLOATS = VEC ? DK : 2 * CH;
+    static constexpr int FLOATS = VEC ? DK : 3 * CH + 4;
     static constexpr int BYTES = GOFF + FLOATS * 4;
     static_assert(BYTES % 16 == 0 && GOFF % 16 == 0, "blocks are copied in 16-byte units");
 };
@@ -204,6 +206,28 @@ struct RegRows {
             *reinterpret_cast<u32x4 *>(lds + u * S::VE) = (ok >> (int)i) & 1u ? r[i] : u32x4{0u, 0u, 0u, 0u};
         });
     }
+    // Scales every row to unit L2 norm, x rsqrt(sum x^2 + 1e-6) rounded to E
+    // (linear_attention.py:703-706), and writes each row's factor to rf[row].
+    // A row's UPR units sit in UPR consecutive lanes of one load.
+    __device__ __forceinline__ void l2norm_rows(float *rf, int tid) {
+        static_assert(sizeof(E) == 2 && 64 % S::UPR == 0, "rows of 16-bit elements within one wavefront");
+        using V8 = typename Elem<E>::frag2;
+        const int wave = tid >> 6, lane = tid & 63;
+        unroll<PER>([&](auto i) {
+            V8 x = __builtin_bit_cast(V8, r[i]);
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += (float)x[e] * (float)x[e];
+#pragma unroll
+            for (int off = 1; off < S::UPR; off <<= 1) ss += __shfl_xor(ss, off);
+            const float f = rsqrtf(ss + 1e-6f);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x[e] = (E)((float)x[e] * f);
+            r[i] = __builtin_bit_cast(u32x4, x);
+            const int u = (wave + NWV * (int)i) * 64 + lane;
+            if (u % S::UPR == 0) rf[u / S::UPR] = f;
+        });
+    }
 };
 
 // contiguous copy of n16 16-byte units (identity layout)
@@ -252,6 +276,8 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     __shared__ __attribute__((aligned(16))) char smem[L::UNION];
     __shared__ __attribute__((aligned(16))) float gam[GATE == 2 ? CH * PG : CH];
     __shared__ __attribute__((aligned(16))) float bet[CH];
+    __shared__ __attribute__((aligned(16))) float rkf[CH];     // rows' L2-norm factors (fused norm)
+    __shared__ __attribute__((aligned(16))) float rqf[CH];
     __shared__ int flag[4];
     E *Kst = reinterpret_cast<E *>(smem);
     E *Qst = Kst + CH * DK;
@@ -303,6 +329,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         if constexpr (GATE != 2)
             if (p.g) g_v = p.g[(t0 + row) * H + h];
     }
+    const Fusion &fz = p.fz;
     // per-channel gate: thread (sg, cg) holds channels 4 cg .. + 3 of rows
     // RPS sg .. + RPS - 1
     constexpr int CG = DK / 4, SGN = NT / CG, RPS = CH / SGN;
@@ -312,14 +339,32 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     if constexpr (GATE == 2) {
         unroll<RPS>([&](auto i) {
             const int row = sg * RPS + (int)i, rr = row < clen ? row : 0;
-            gv[i] = ld4(p.g + ((t0 + rr) * H + h) * DK + 4 * cg);
+            const int64_t off = ((t0 + rr) * H + h) * DK + 4 * cg;
+            if constexpr (sizeof(E) == 2) {
+                if (fz.gate_16) {                               // pre-activation f in the element type
+                    const uint2 raw = *reinterpret_cast<const uint2 *>(reinterpret_cast<const E *>(p.g) + off);
+                    gv[i] = EL::tof(__builtin_bit_cast(F, raw));
+                } else {
+                    gv[i] = ld4(p.g + off);
+                }
+            } else {
+                gv[i] = ld4(p.g + off);
+            }
         });
     }
     RegRows<E, CH, DK, NT> rk, rq;
     rk.load(kg, sqk, clen, DK, tid);
     rq.load(qg, sqk, clen, DK, tid);
-    if (wave == 0 && lane < CH) bet[lane] = lane < clen ? beta_v : 0.f;
+    if (wave == 0 && lane < CH) bet[lane] = lane < clen ? (fz.beta_sigmoid ? sigmoidf_(beta_v) : beta_v) : 0.f;
     if constexpr (GATE == 2) {
+        if (fz.gate_act) {                                      // g = act(f + dt_bias) per channel
+            const float a_log = fz.A_log[h];
+            const f32x4 dt = ld4(fz.dt_bias + (int64_t)h * DK + 4 * cg);
+            unroll<RPS>([&](auto i) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) gv[i][e] = gate_activation(gv[i][e], a_log, dt[e], fz.lb_set, fz.lb);
+            });
+        }
         // inclusive cumulative sum over rows: within the thread's rows in
         // registers, then the totals of the preceding row segments from LDS
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -348,21 +393,35 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
                 const float y = __shfl_up(x, o);
                 if (lane >= o) x += y;
             }
-            const float last = __shfl(x, CH - 1);
-            if (lane < CH) {
-                gam[lane] = x;
-                float *gblk = reinterpret_cast<float *>(blk_base + CB::GOFF);
-                gblk[lane] = __expf(x);
-                // zero past the end of the sequence: the state update scales
-                // those rows of U~ (or V without the delta rule) by it, and the
-                // state kernel leaves K and V rows there unzeroed
-                gblk[CH + lane] = lane < clen ? __expf(last - x) : 0.f;
-            }
+            if (lane < CH) gam[lane] = x;
+        }
+    }
+    if constexpr (sizeof(E) == 2) {
+        if (fz.qk_l2norm) {                                     // normalised rows, factors in rkf / rqf
+            rk.l2norm_rows(rkf, tid);
+            rq.l2norm_rows(rqf, tid);
         }
     }
     rk.store(Kst, tid);
     rq.store(Qst, tid);
     __syncthreads();
+    if constexpr (GATE != 2) {
+        // the state kernel's row factors (ChunkBlock)
+        if (wave == 0 && lane < CH) {
+            const float x = gam[lane], last = gam[CH - 1];
+            const bool nrm = sizeof(E) == 2 && fz.qk_l2norm;
+            const float fk = nrm ? rkf[lane] : 1.f, fq = nrm ? rqf[lane] : 1.f;
+            const float gx = __expf(x);
+            float *gblk = reinterpret_cast<float *>(blk_base + CB::GOFF);
+            gblk[lane] = gx * fk;
+            gblk[CH + lane] = p.scale * gx * fq;
+            // zero past the end of the sequence: the state update scales those
+            // rows of U~ (or V without the delta rule) by it, and the state
+            // kernel leaves K and V rows there unzeroed
+            gblk[2 * CH + lane] = lane < clen ? __expf(last - x) * fk : 0.f;
+            if (lane < 4) gblk[3 * CH + lane] = lane == 0 ? __expf(last) : 0.f;
+        }
+    }
 
     // ---- K K^T (-> M) and Q K^T (-> A), lower tile pairs -----------------
     // Job (I, J) computes X = K_J Y_I^T for Y in {K, Q}; the C layout then
@@ -1231,7 +1290,8 @@ chunk_state_tr_kernel(const ChunkParams p) {
         const E *Vtr = (odd ? V1 : V0) + z + (4 * g4 + (r16 >> 2)) * PV + wcol + 4 * (r16 & 3);
         const char *Bst = (odd ? B1 : B0) + z;
         const E *TEs = reinterpret_cast<const E *>(Bst) + 8 * ln, *Aqs = TEs + CH * CH;
-        const float *gs = reinterpret_cast<const float *>(Bst + TEAB), *ge = gs + CH;       // G, Gend | Gc
+        // scalar gate: GX, GO, GE, Gc (ChunkBlock); VEC: Gc per key channel
+        const float *gs = reinterpret_cast<const float *>(Bst + TEAB), *go = gs + CH, *ge = gs + 2 * CH;
         E *og = reinterpret_cast<E *>(p.o) + (int64_t)h * DV + col0 + wcol + 4 * g4;
 
         F2 Sb[NKB / 2];
@@ -1288,7 +1348,7 @@ chunk_state_tr_kernel(const ChunkParams p) {
         //      S <- Gc S + (K*Gend)^T U~ -----------------------------------------
 #pragma unroll
         for (int I = 0; I < NB; ++I) {
-            if constexpr (!VEC) OT[I] *= p.scale * gs[16 * I + r16];    // VEC: scale and G are in Q*G
+            if constexpr (!VEC) OT[I] *= go[16 * I + r16];              // VEC: scale and G are in Q*G
 #pragma unroll
             for (int q = 0; 2 * q <= I; ++q)
                 OT[I] = mfma_pair(Ub[q], ld_pair<E>(Aqs + frag_pair_pos<NB>(I, q, 0)), OT[I]);
@@ -1297,7 +1357,7 @@ chunk_state_tr_kernel(const ChunkParams p) {
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) S[kt] *= ld4(gs + 16 * kt + 4 * g4);    // Gc per key channel
         } else {
-            const float gc = gs[CH - 1];
+            const float gc = gs[3 * CH];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) S[kt] *= gc;
         }
@@ -1388,7 +1448,7 @@ static int state_waves(int64_t units, int dv, int cus) {
 int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H, int64_t dk, int gate_vector) {
     const int64_t es = dtype == 0 ? 4 : 2;
     const bool vec = gate_vector && dtype != 0;                            // ChunkBlock<E, chunk, dk, gate>::BYTES
-    const int64_t per = 2 * chunk * chunk * es + (vec ? 3 * chunk * dk * es + dk * 4 : 2 * chunk * 4);
+    const int64_t per = 2 * chunk * chunk * es + (vec ? 3 * chunk * dk * es + dk * 4 : (3 * chunk + 4) * 4);
     return chunk_slots * H * per;
 }
 

@@ -159,6 +159,16 @@ __device__ __forceinline__ f32x4 exp4(f32x4 x) {
 
 template <typename T> __host__ __device__ constexpr T cmax(T a, T b) { return a > b ? a : b; }
 
+// the reference's producer activations (linear_attention.py:703-706, :719-736)
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+// torch.nn.functional.softplus (beta 1, threshold 20)
+__device__ __forceinline__ float softplusf_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+// gate activation of the per-channel gate from its pre-activation f
+__device__ __forceinline__ float gate_activation(float f, float a_log, float dt, int lb_set, float lb) {
+    const float a = __expf(a_log), z = f + dt;
+    return lb_set ? lb * sigmoidf_(a * z) : -a * softplusf_(z);
+}
+
 // 16-byte global access
 struct alignas(16) Vec16 { uint32_t w[4]; };
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));

@@ -19,6 +19,19 @@ struct SeqGeom {
     int chunks_per_seq;           // dense: ceil(T / CH)
 };
 
+// Producer fusions (the flags of the reference's fla call): work a caller
+// would otherwise do in elementwise passes over q, k, g and beta before the scan.
+struct Fusion {
+    int qk_l2norm;                // q, k un-normalised: x rsqrt(sum x^2 + 1e-6) per (token, head)
+    int beta_sigmoid;             // beta holds logits
+    int gate_act;                 // per-channel gate: g holds the pre-activation f
+    int gate_16;                  // f is in q's 16-bit type (else fp32)
+    const float *A_log;           // [H]
+    const float *dt_bias;         // [H * dk]
+    int lb_set;                   // g = lb sigmoid(exp(A_log) (f + dt_bias)), else -exp(A_log) softplus(f + dt_bias)
+    float lb;
+};
+
 struct ChunkParams {
     SeqGeom geo;
     const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
@@ -33,6 +46,7 @@ struct ChunkParams {
     int n_chunk_slots;            // chunk-prep grid size / H (upper bound of chunks)
     int use_delta;
     float scale;
+    Fusion fz;
 };
 
 struct RecParams {
@@ -48,6 +62,7 @@ struct RecParams {
     int H, n_seqs;
     int use_delta;
     float scale;
+    Fusion fz;
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.

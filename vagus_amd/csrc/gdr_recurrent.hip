@@ -35,6 +35,7 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
     __shared__ __attribute__((aligned(16))) float gv[GATE == 2 ? DK : 1];
     __shared__ __attribute__((aligned(16))) float red[NWV][2][DV];
     __shared__ float redqk[NWV];
+    __shared__ float nrm[NWV][2];           // fused L2 norm: per-wave sums of q^2, k^2
     __shared__ float sc[2];                 // decay (scalar gate), beta
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -67,17 +68,51 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
                     : f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (int64_t t = bos; t < eos; ++t) {
-        // token operands -> LDS (fp32)
+        // token operands -> LDS (fp32); thread i < DK owns q_i, k_i (and g_i)
         const int64_t qo = (t * H + h) * DK, vo = (t * H + h) * DV;
-        for (int i = tid; i < DK; i += NT) {
-            qs[i] = EL::to_f(qg[qo + i]) * p.scale;
-            ks[i] = EL::to_f(kg[qo + i]);
-            if constexpr (GATE == 2) gv[i] = __expf(p.g[qo + i]);
+        const bool own = tid < DK;
+        float qv = own ? EL::to_f(qg[qo + tid]) : 0.f, kv = own ? EL::to_f(kg[qo + tid]) : 0.f;
+        if (p.fz.qk_l2norm) {
+            // fused producer (linear_attention.py:703-706): x rsqrt(sum x^2 + 1e-6), rounded to E
+            float sq = qv * qv, sk = kv * kv;
+#pragma unroll
+            for (int off = 32; off >= 1; off >>= 1) {
+                sq += __shfl_xor(sq, off);
+                sk += __shfl_xor(sk, off);
+            }
+            if (lane == 0) {
+                nrm[wave][0] = sq;
+                nrm[wave][1] = sk;
+            }
+            __syncthreads();
+            sq = sk = 0.f;
+#pragma unroll
+            for (int w = 0; w < NWV; ++w) {
+                sq += nrm[w][0];
+                sk += nrm[w][1];
+            }
+            qv = EL::to_f(EL::from_f(qv * rsqrtf(sq + 1e-6f)));
+            kv = EL::to_f(EL::from_f(kv * rsqrtf(sk + 1e-6f)));
+        }
+        if (own) {
+            qs[tid] = qv * p.scale;
+            ks[tid] = kv;
+            if constexpr (GATE == 2) {
+                float gl;
+                if (p.fz.gate_act) {                       // fused gate activation from the pre-activation f
+                    const float f = p.fz.gate_16 ? EL::to_f(reinterpret_cast<const E *>(p.g)[qo + tid]) : p.g[qo + tid];
+                    gl = gate_activation(f, p.fz.A_log[h], p.fz.dt_bias[(int64_t)h * DK + tid], p.fz.lb_set, p.fz.lb);
+                } else {
+                    gl = p.g[qo + tid];
+                }
+                gv[tid] = __expf(gl);
+            }
         }
         for (int i = tid; i < DV; i += NT) vs[i] = EL::to_f(vg[vo + i]);
         if (tid == 0) {
             sc[0] = (GATE == 1 && p.g) ? __expf(p.g[t * H + h]) : 1.f;
-            sc[1] = p.use_delta ? p.beta[t * H + h] : 0.f;
+            const float b = p.use_delta ? p.beta[t * H + h] : 0.f;
+            sc[1] = p.use_delta && p.fz.beta_sigmoid ? sigmoidf_(b) : b;
         }
         __syncthreads();
 

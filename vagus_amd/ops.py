@@ -13,11 +13,19 @@ and final state per segment).
 Layouts: q, k (B, T, H, dk); v (B, T, H, dv); g (B, T, H) scalar log-decay
 (GDN) or (B, T, H, dk) per-channel (KDA), fp32 in the kernel; beta (B, T, H);
 states (N, H, dk, dv) fp32 with N = B (dense) or the segment count.  o comes
-back in q's dtype.  Every call runs the HIP kernels of libvagus_gdr.so on the
+back in q's dtype.
+
+The fla flags use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel and (KDA)
+use_gate_in_kernel with A_log / dt_bias / lower_bound move the producers'
+elementwise work into the kernels (struct vgdr_fusion): q, k arrive
+un-normalised, beta as logits, g as the gate pre-activation (in q's dtype or
+fp32).  They need 16-bit q, k, v for the chunked scan, as fla does.  Every call runs the HIP kernels of libvagus_gdr.so on the
 current stream; there is no CPU path and no autograd (backward is out of
 scope: inputs that require grad raise NotImplementedError).
 """
 from __future__ import annotations
+
+import ctypes
 
 import torch
 import torch.nn.functional as F
@@ -81,11 +89,45 @@ def _check_grad(*ts):
         raise NotImplementedError('vagus_amd implements the forward pass only (no backward)')
 
 
+class _Fusion:
+    """The producer fusions of one call (linear_attention.py:457-497 flags)."""
+
+    def __init__(self, *, l2norm=False, beta=False, gate=False, A_log=None, dt_bias=None, lower_bound=None):
+        self.l2norm, self.beta, self.gate = bool(l2norm), bool(beta), bool(gate)
+        self.A_log, self.dt_bias, self.lower_bound = A_log, dt_bias, lower_bound
+        if self.gate:
+            assert A_log is not None and dt_bias is not None, 'use_gate_in_kernel needs A_log and dt_bias'
+        else:
+            assert lower_bound is None, 'lower_bound belongs to the fused gate activation'
+
+    @property
+    def any(self):
+        return self.l2norm or self.beta or self.gate
+
+    def struct(self, c):
+        """(the C struct, tensors it points into) for the padded operands of call c."""
+        keep = []
+        fz = _lib.Fusion(int(self.l2norm), int(self.beta), int(self.gate), _lib.VGDR_F32, None, None, 0, 0.0)
+        if self.gate:
+            a_log = self.A_log.detach().float().reshape(c.H).contiguous()
+            dt = self.dt_bias.detach().float().reshape(c.H, c.dk)
+            dt = _aligned(_pad_to(dt, {1: c.dkp}))
+            keep += [a_log, dt]
+            fz.A_log, fz.dt_bias = a_log.data_ptr(), dt.data_ptr()
+            fz.gate_dtype = _DTYPES[c.g.dtype]
+            if self.lower_bound is not None:
+                fz.lower_bound_set, fz.lower_bound = 1, float(self.lower_bound)
+        return fz, keep
+
+
+_NO_FUSION = _Fusion()
+
+
 class _Call:
     """Validated, padded, contiguous operands of one kernel call."""
 
     def __init__(self, q, k, v, g, beta, initial_state, cu_seqlens, *, gate: str, delta: bool,
-                 dv_to):
+                 dv_to, fusion: _Fusion = _NO_FUSION):
         _check_device(q, k, v, g, beta, initial_state, cu_seqlens)
         _check_grad(q, k, v, g, beta, initial_state)
         assert q.dim() == 4 and k.shape == q.shape and v.dim() == 4 and v.shape[:3] == q.shape[:3], \
@@ -126,7 +168,9 @@ class _Call:
         if gate == 'none' or g is None:
             self.g, self.gate_kind = None, _lib.VGDR_GATE_NONE
         elif gate == 'vector':
-            self.g, self.gate_kind = _aligned(_pad_to(g.float(), {1: dkp})), _lib.VGDR_GATE_VECTOR
+            # a fused gate pre-activation stays in q's 16-bit type (no fp32 copy)
+            gk = g if (fusion.gate and g.dtype == q.dtype and q.dtype != torch.float32) else g.float()
+            self.g, self.gate_kind = _aligned(_pad_to(gk, {1: dkp})), _lib.VGDR_GATE_VECTOR
         else:
             self.g, self.gate_kind = g.float().contiguous(), _lib.VGDR_GATE_SCALAR
         self.beta = beta.float().contiguous() if delta else None
@@ -151,16 +195,17 @@ class _Call:
 
 
 def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None, output_final_state=False,
-               cu_seqlens=None, chunk_size=64, phase_event=None):
+               cu_seqlens=None, chunk_size=64, phase_event=None, fusion: _Fusion = _NO_FUSION):
     """Chunkwise prefill, the general form behind chunk_gated_delta_rule,
     chunk_kda and chunk_simple_gla: gate in {'none', 'scalar', 'vector'},
     delta selects the delta rule.  Returns (o, final_state or None).
 
     phase_event: optional torch.cuda.Event recorded on the current stream
     between the chunk-prep and the chunk-state kernels (the same two launches
-    either way), so that a caller can time the two phases separately."""
+    either way), so that a caller can time the two phases separately.
+    fusion: the producer fusions (_Fusion)."""
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=gate, delta=delta,
-              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     o = c.new_output()
     S = c.new_state() if output_final_state else None
@@ -170,10 +215,21 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
                                          int(chunk_size))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
     with torch.cuda.device(c.device):
-        args = (_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
+        head = (_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
                 _ptr(c.beta), _ptr(o), _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws), nbytes,
-                c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size), _stream(c.device))
-        if phase_event is None:
+                c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size))
+        args = head + (_stream(c.device),)
+        if fusion.any:
+            fz, keep = fusion.struct(c)
+            fargs = head + (ctypes.byref(fz), _stream(c.device))
+            if phase_event is None:
+                _lib.check(L.vgdr_chunk_fwd_fused(*fargs))
+            else:
+                _lib.check(L.vgdr_chunk_prep_fused(*fargs))
+                phase_event.record(torch.cuda.current_stream(c.device))
+                _lib.check(L.vgdr_chunk_state(*args))
+            del keep
+        elif phase_event is None:
             _lib.check(L.vgdr_chunk_fwd(*args))
         else:
             _lib.check(L.vgdr_chunk_prep(*args))
@@ -182,11 +238,15 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
     return c.unpad_o(o), c.unpad_state(S)
 
 
-def _unsupported(**flags):
-    on = [k for k, v in flags.items() if v]
-    if on:
-        raise NotImplementedError(f'vagus_amd does not implement {on} yet (pass the activated '
-                                  'inputs, as the unfused reference path does)')
+def _kda_fusion(use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
+                safe_gate, lower_bound) -> _Fusion:
+    # safe_gate / lower_bound select the bounded activation lower_bound *
+    # sigmoid(exp(A_log) (f + dt_bias)) of the fused gate (the reference passes
+    # them only together with use_gate_in_kernel, linear_attention.py:465-471)
+    if safe_gate:
+        assert lower_bound is not None, 'safe_gate needs lower_bound'
+    return _Fusion(l2norm=use_qk_l2norm_in_kernel, beta=use_beta_sigmoid_in_kernel, gate=use_gate_in_kernel,
+                   A_log=A_log, dt_bias=dt_bias, lower_bound=lower_bound if use_gate_in_kernel else None)
 
 
 def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
@@ -195,12 +255,12 @@ def chunk_gated_delta_rule(q, k, v, g, beta, scale=None, initial_state=None,
     """GDN chunkwise prefill (the call at linear_attention.py:487-491).
 
     g: (B, T, H) log-decay (None for DeltaNet, a = 1).  Returns (o, final_state),
-    final_state None unless output_final_state."""
-    _unsupported(use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
-                 use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel)
+    final_state None unless output_final_state.  use_qk_l2norm_in_kernel: q, k
+    arrive un-normalised; use_beta_sigmoid_in_kernel: beta arrives as logits."""
+    fz = _Fusion(l2norm=use_qk_l2norm_in_kernel, beta=use_beta_sigmoid_in_kernel)
     return chunk_scan(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True,
                   scale=scale, initial_state=initial_state, output_final_state=output_final_state,
-                  cu_seqlens=cu_seqlens, chunk_size=chunk_size)
+                  cu_seqlens=cu_seqlens, chunk_size=chunk_size, fusion=fz)
 
 
 def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
@@ -209,15 +269,16 @@ def chunk_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_sta
               safe_gate=False, lower_bound=None, disable_recompute=False):
     """KDA chunkwise prefill (the call at linear_attention.py:474-479).
 
-    g: (B, T, H, dk) per-channel log-decay.  disable_recompute only concerns a
-    backward pass and is accepted and ignored; safe_gate / lower_bound belong to
-    the fused gate activation."""
-    _unsupported(use_qk_l2norm_in_kernel=use_qk_l2norm_in_kernel,
-                 use_beta_sigmoid_in_kernel=use_beta_sigmoid_in_kernel,
-                 use_gate_in_kernel=use_gate_in_kernel, safe_gate=safe_gate)
+    g: (B, T, H, dk) per-channel log-decay, or with use_gate_in_kernel the gate
+    pre-activation f (q's dtype or fp32) with A_log (H,) and dt_bias (H*dk,):
+    g = -exp(A_log) softplus(f + dt_bias), or lower_bound * sigmoid(exp(A_log)
+    (f + dt_bias)) with lower_bound (linear_attention.py:719-734).
+    disable_recompute only concerns a backward pass and is accepted and ignored."""
+    fz = _kda_fusion(use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
+                     safe_gate, lower_bound)
     return chunk_scan(q, k, v, g, beta, gate='vector', delta=True, scale=scale,
                   initial_state=initial_state, output_final_state=output_final_state,
-                  cu_seqlens=cu_seqlens, chunk_size=chunk_size)
+                  cu_seqlens=cu_seqlens, chunk_size=chunk_size, fusion=fz)
 
 
 def chunk_simple_gla(q, k, v, g, scale=None, initial_state=None, output_final_state=False,
@@ -230,7 +291,7 @@ def chunk_simple_gla(q, k, v, g, scale=None, initial_state=None, output_final_st
 
 
 def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state,
-               cu_seqlens, inplace_final_state=False):
+               cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION):
     dv = v.shape[-1]
     if dv > max(_REC_DVS):
         # the recurrence is column-separable: independent 128-wide column blocks
@@ -240,7 +301,7 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
             s0 = None if initial_state is None else initial_state[..., sl]
             o_, s_ = _recurrent(q, k, v[..., sl], g, beta, gate=gate, delta=delta, scale=scale,
                                 initial_state=s0, output_final_state=output_final_state,
-                                cu_seqlens=cu_seqlens)
+                                cu_seqlens=cu_seqlens, fusion=fusion)
             outs.append(o_)
             states.append(s_)
         S = torch.cat(states, -1) if output_final_state else None
@@ -249,7 +310,7 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
             S = initial_state
         return torch.cat(outs, -1), S
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=gate, delta=delta,
-              dv_to=lambda d: next(x for x in _REC_DVS if x >= d))
+              dv_to=lambda d: next(x for x in _REC_DVS if x >= d), fusion=fusion)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     o = c.new_output()
     in_place = (inplace_final_state and initial_state is not None and not c.padded
@@ -262,10 +323,14 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
         h0 = c.h0
     L = _lib.load()
     with torch.cuda.device(c.device):
-        _lib.check(L.vgdr_recurrent_fwd(
-            _DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
-            _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), _ptr(c.cu), c.B, c.T, c.H, c.dkp, c.dvp, c.N,
-            scale, _stream(c.device)))
+        head = (_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
+                _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), _ptr(c.cu), c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale)
+        if fusion.any:
+            fz, keep = fusion.struct(c)
+            _lib.check(L.vgdr_recurrent_fwd_fused(*head, ctypes.byref(fz), _stream(c.device)))
+            del keep
+        else:
+            _lib.check(L.vgdr_recurrent_fwd(*head, _stream(c.device)))
     if in_place:
         return c.unpad_o(o), S
     S = c.unpad_state(S)
@@ -277,20 +342,28 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
 
 def fused_recurrent_gated_delta_rule(q, k, v, g=None, beta=None, scale=None, initial_state=None,
                                      output_final_state=False, cu_seqlens=None,
-                                     inplace_final_state=False):
+                                     inplace_final_state=False, use_qk_l2norm_in_kernel=False,
+                                     use_beta_sigmoid_in_kernel=False):
     """Token-by-token GDN (decode: T = 1).  inplace_final_state writes the new
-    state into initial_state (the decode step's state.copy_, linear_attention.py:950)."""
+    state into initial_state (the decode step's state.copy_, linear_attention.py:950).
+    The fusion flags are those of chunk_gated_delta_rule."""
+    fz = _Fusion(l2norm=use_qk_l2norm_in_kernel, beta=use_beta_sigmoid_in_kernel)
     return _recurrent(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True,
                       scale=scale, initial_state=initial_state, output_final_state=output_final_state,
-                      cu_seqlens=cu_seqlens, inplace_final_state=inplace_final_state)
+                      cu_seqlens=cu_seqlens, inplace_final_state=inplace_final_state, fusion=fz)
 
 
 def fused_recurrent_kda(q, k, v, g, beta, scale=None, initial_state=None, output_final_state=False,
-                        cu_seqlens=None, inplace_final_state=False):
-    """Token-by-token KDA (per-channel decay g (B, T, H, dk))."""
+                        cu_seqlens=None, inplace_final_state=False, use_qk_l2norm_in_kernel=False,
+                        use_beta_sigmoid_in_kernel=False, use_gate_in_kernel=False, A_log=None,
+                        dt_bias=None, safe_gate=False, lower_bound=None):
+    """Token-by-token KDA (per-channel decay g (B, T, H, dk)); the fusion flags
+    are those of chunk_kda."""
+    fz = _kda_fusion(use_qk_l2norm_in_kernel, use_beta_sigmoid_in_kernel, use_gate_in_kernel, A_log, dt_bias,
+                     safe_gate, lower_bound)
     return _recurrent(q, k, v, g, beta, gate='vector', delta=True, scale=scale,
                       initial_state=initial_state, output_final_state=output_final_state,
-                      cu_seqlens=cu_seqlens, inplace_final_state=inplace_final_state)
+                      cu_seqlens=cu_seqlens, inplace_final_state=inplace_final_state, fusion=fz)
 
 
 def _gate_of(g) -> str:
@@ -300,13 +373,24 @@ def _gate_of(g) -> str:
 
 
 def hip_scan(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_size: int = 64,
+             l2norm_in_kernel: bool = False, gate_in_kernel: bool = False, beta_in_kernel: bool = False,
+             A_log=None, dt_bias=None, disable_recompute: bool = False, lower_bound: float | None = None,
              cu_seqlens=None):
-    """The contract of fla_scan (linear_attention.py:428-498): chunked scan from
-    entry state S0 (or zeros), always returning (o in q.dtype, final S fp32).
-    g: None, (B, L, H) or (B, L, H, dk)."""
-    return chunk_scan(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale,
+    """The contract of fla_scan (linear_attention.py:428-498), flags included:
+    chunked scan from entry state S0 (or zeros), always returning (o in
+    q.dtype, final S fp32).  g: None, (B, L, H) or (B, L, H, dk) (with
+    gate_in_kernel the per-channel pre-activation).  The *_in_kernel flags are
+    fused into the kernels; disable_recompute concerns a backward pass only."""
+    gate = _gate_of(g)
+    if gate_in_kernel:
+        assert gate == 'vector', 'the fused gate activation is a KDA (vector-gate) kernel'
+    if not delta:
+        assert not l2norm_in_kernel and not beta_in_kernel, 'simple_gla takes no fused l2norm / beta'
+    fz = _Fusion(l2norm=l2norm_in_kernel, beta=beta_in_kernel, gate=gate_in_kernel, A_log=A_log,
+                 dt_bias=dt_bias, lower_bound=lower_bound if gate_in_kernel else None)
+    return chunk_scan(q, k, v, g, beta, gate=gate, delta=delta, scale=scale,
                   initial_state=S0, output_final_state=True, cu_seqlens=cu_seqlens,
-                  chunk_size=chunk_size)
+                  chunk_size=chunk_size, fusion=fz)
 
 
 def hip_recurrent(q, k, v, g, beta, S0, *, scale: float, delta: bool, cu_seqlens=None,
