@@ -81,6 +81,20 @@ typedef struct vgdr_fusion {
     float lower_bound;
 } vgdr_fusion;
 
+/*
+ * Output epilogue of the layer: per (token, head), RMSNorm of o over dv with
+ * weight gamma, times SiLU of the output gate (linear_attention.py:814-825,
+ * norm_layer.py:15-24; fla's rms_norm_gated with activation 'swish', :820-823):
+ *     out = x rsqrt(mean_c x_c^2 + eps) gamma * gate sigmoid(gate),   x = o rounded to dtype
+ * computed in fp32 and rounded once to dtype.
+ */
+typedef struct vgdr_epilogue {
+    const void *gate;       /* [n_tokens, H, dv] in dtype (the W_g x projection), 16-byte aligned */
+    const void *gamma;      /* [dv] RMSNorm weight */
+    int gamma_dtype;        /* VGDR_F32 or dtype */
+    float eps;              /* > 0 */
+} vgdr_epilogue;
+
 /* Library version (major * 10000 + minor * 100 + patch). */
 int vgdr_version(void);
 
@@ -186,6 +200,29 @@ int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta,
                              const int32_t *cu_seqlens,
                              int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
                              float scale, const vgdr_fusion *fusion, hipStream_t stream);
+
+/* vgdr_recurrent_fwd_fused whose o receives the layer's output epilogue
+ * (vgdr_epilogue; NULL = plain o) instead of the raw scan output: the decode
+ * step of GatedDeltaNet.decode_step through _output, up to W_o
+ * (linear_attention.py:945-952 and :814-825), in one kernel.  The workgroup of
+ * a (sequence, head) holds the whole dv row, so the norm needs no extra pass. */
+int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta,
+                                const void *q, const void *k, const void *v,
+                                const float *g, const float *beta,
+                                void *o, const float *initial_state, float *final_state,
+                                const int32_t *cu_seqlens,
+                                int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                                float scale, const vgdr_fusion *fusion, const vgdr_epilogue *epilogue,
+                                hipStream_t stream);
+
+/* The output epilogue as one pass over n_rows rows of dv elements (a row per
+ * (token, head)): out = epilogue(o, gate).  Replaces rms_norm_gated / the
+ * RMSNorm x SiLU expression at linear_attention.py:820-825 after a chunked
+ * prefill (the chunk kernels split dv across workgroups).  out may equal o.
+ * dv = 8 x a power of two up to 512 (16-bit), 4 x a power of two up to 256
+ * (fp32); o, out 16-byte aligned. */
+int vgdr_norm_gate(int dtype, const void *o, const vgdr_epilogue *epilogue, void *out, int64_t n_rows,
+                   int64_t dv, hipStream_t stream);
 
 /*
  * Packed-batch schedule.  No reference counterpart (the reference has no

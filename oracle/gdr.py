@@ -24,6 +24,8 @@ Functions and the reference lines they follow:
     l2norm          linear_attention.py:703-706   the q, k producer (fused by the kernels' qk_l2norm)
     gate_activation linear_attention.py:722-734   per-channel gate from its pre-activation
     beta_sigmoid    linear_attention.py:735-736   beta from its logits
+    norm_gate       linear_attention.py:814-825   output epilogue RMSNorm(o) * SiLU(gate)
+                    norm_layer.py:15-24           (fused by the kernels' vgdr_epilogue)
 
 Layouts follow the reference (linear_attention.py:146-154): q, k (B, L, H, dk),
 v (B, L, H, dv), g (B, L, H) or (B, L, H, dk), beta (B, L, H), S0 (B, H, dk, dv).
@@ -38,7 +40,9 @@ statement of the update above; the chunk forms against ``recurrent`` at
 vector-gate reduction; ``varlen`` by segment isolation; ``chunk_table`` by
 brute-force enumeration; ``chunk_scan_flops`` by the reference's known answers;
 the producers by their defining properties (unit norms and scale invariance,
-softplus / sigmoid identities and limits, the bounded gate's range).
+softplus / sigmoid identities and limits, the bounded gate's range);
+``norm_gate`` against torch's own ``F.rms_norm`` x ``F.silu`` in fp64, a
+constant row's closed form and scale invariance.
 """
 from __future__ import annotations
 
@@ -332,3 +336,18 @@ def gate_activation(f, A_log, dt_bias, lower_bound=None):
 def beta_sigmoid(b):
     """beta from its logits (linear_attention.py:735-736)."""
     return torch.sigmoid(_hi(b))
+
+
+# ---------------------------------------------------------------------------
+# the output epilogue the kernels can fuse (vgdr_epilogue)
+# ---------------------------------------------------------------------------
+
+def norm_gate(o, gate, gamma, eps: float = 1e-6):
+    """The layer's output epilogue before W_o (linear_attention.py:825):
+    RMSNorm(o.to(gate.dtype)) * SiLU(gate), RMSNorm per norm_layer.py:15-24:
+    statistics in at least fp32, the normalised row cast back to the input
+    dtype, then scaled by gamma.  Shapes (..., dv); gamma (dv,)."""
+    x = o.to(gate.dtype)
+    h = _hi(x)
+    y = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * gamma
+    return y * torch.nn.functional.silu(gate)

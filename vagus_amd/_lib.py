@@ -25,9 +25,16 @@ class Fusion(ctypes.Structure):
                 ('lower_bound_set', ctypes.c_int), ('lower_bound', ctypes.c_float)]
 
 
+class Epilogue(ctypes.Structure):
+    """struct vgdr_epilogue: the layer's RMSNorm x SiLU(gate) output epilogue."""
+    _fields_ = [('gate', ctypes.c_void_p), ('gamma', ctypes.c_void_p), ('gamma_dtype', ctypes.c_int),
+                ('eps', ctypes.c_float)]
+
+
 # every symbol the header declares, with its ctypes signature
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 _FZ = ctypes.POINTER(Fusion)
+_EP = ctypes.POINTER(Epilogue)
 SIGNATURES = {
     'vgdr_version': (_I, []),
     'vgdr_last_error': (ctypes.c_char_p, []),
@@ -46,6 +53,9 @@ SIGNATURES = {
                                 _L, _L, _L, _L, _L, _L, _F, _P]),
     'vgdr_recurrent_fwd_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                       _L, _L, _L, _L, _L, _L, _F, _FZ, _P]),
+    'vgdr_recurrent_fwd_epilogue': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                         _L, _L, _L, _L, _L, _L, _F, _FZ, _EP, _P]),
+    'vgdr_norm_gate': (_I, [_I, _P, _EP, _P, _L, _L, _P]),
     'vgdr_varlen_workspace_size': (_L, [_L]),
     'vgdr_varlen_prepare': (_I, [_P, _L, _L, _I, _P, _P]),
 }

@@ -91,6 +91,23 @@ int check_fusion(const char *fn, const vgdr_fusion *fz, int dtype, int gate_kind
     return VGDR_OK;
 }
 
+// the output epilogue a call asks for; `elems` = 16 / element size (the
+// standalone pass reads rows in 16-byte units)
+int check_epilogue(const char *fn, const vgdr_epilogue *ep, int dtype, vgdr::Epilogue &out) {
+    out = vgdr::Epilogue{};
+    if (!ep) return VGDR_OK;
+    if (!ep->gate || !ep->gamma) return fail(VGDR_ERR_INVALID, "%s: the epilogue needs gate and gamma", fn);
+    if (!aligned16(ep->gate)) return fail(VGDR_ERR_INVALID, "%s: the epilogue gate must be 16-byte aligned", fn);
+    if (ep->gamma_dtype != VGDR_F32 && ep->gamma_dtype != dtype)
+        return fail(VGDR_ERR_INVALID, "%s: gamma_dtype must be VGDR_F32 or the dtype of o", fn);
+    if (!(ep->eps > 0.f)) return fail(VGDR_ERR_INVALID, "%s: the RMSNorm eps must be positive", fn);
+    out.gate = ep->gate;
+    out.gamma = ep->gamma;
+    out.gamma_f32 = ep->gamma_dtype == VGDR_F32 ? 1 : 0;
+    out.eps = ep->eps;
+    return VGDR_OK;
+}
+
 // chunk length the kernels use: 32 when asked for <= 32, else 64; fp32 always
 // uses 32 (its double-buffered 64-token tiles overflow LDS)
 int effective_chunk(int dtype, int64_t dk, int chunk_size) {
@@ -234,17 +251,20 @@ int vgdr_chunk_prep_fused(VGDR_CHUNK_ARGS_FUSED) {
 #undef VGDR_CHUNK_PASS_NOFUSION
 #undef VGDR_CHUNK_PASS_FUSED
 
-int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta, const void *q, const void *k,
-                             const void *v, const float *g, const float *beta, void *o,
-                             const float *initial_state, float *final_state, const int32_t *cu_seqlens,
-                             int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
-                             const vgdr_fusion *fusion, hipStream_t stream) {
+int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta, const void *q, const void *k,
+                                const void *v, const float *g, const float *beta, void *o,
+                                const float *initial_state, float *final_state, const int32_t *cu_seqlens,
+                                int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
+                                const vgdr_fusion *fusion, const vgdr_epilogue *epilogue, hipStream_t stream) {
     g_err[0] = 0;
     int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o,
                           cu_seqlens, B, T, H, dk, dv, n_seqs);
     if (rc) return rc;
     vgdr::Fusion fz;
     rc = check_fusion("vgdr_recurrent_fwd", fusion, dtype, gate_kind, use_delta, false, fz);
+    if (rc) return rc;
+    vgdr::Epilogue ep;
+    rc = check_epilogue("vgdr_recurrent_fwd", epilogue, dtype, ep);
     if (rc) return rc;
     if (dv != 64 && dv != 128)
         return fail(VGDR_ERR_UNSUPPORTED, "vgdr_recurrent_fwd: dv=%lld (supported: 64, 128)", (long long)dv);
@@ -265,8 +285,40 @@ int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta, const void
     p.use_delta = use_delta ? 1 : 0;
     p.scale = scale;
     p.fz = fz;
+    p.ep = ep;
     return hip_status(vgdr::recurrent_fwd(dtype, (int)dk, (int)dv, gate_kind == VGDR_GATE_VECTOR, p, stream),
                       "vgdr_recurrent_fwd launch");
+}
+
+int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta, const void *q, const void *k,
+                             const void *v, const float *g, const float *beta, void *o,
+                             const float *initial_state, float *final_state, const int32_t *cu_seqlens,
+                             int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
+                             const vgdr_fusion *fusion, hipStream_t stream) {
+    return vgdr_recurrent_fwd_epilogue(dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state,
+                                       final_state, cu_seqlens, B, T, H, dk, dv, n_seqs, scale, fusion, nullptr,
+                                       stream);
+}
+
+int vgdr_norm_gate(int dtype, const void *o, const vgdr_epilogue *epilogue, void *out, int64_t n_rows, int64_t dv,
+                   hipStream_t stream) {
+    g_err[0] = 0;
+    if (dtype != VGDR_F32 && dtype != VGDR_BF16 && dtype != VGDR_F16)
+        return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: unknown dtype %d", dtype);
+    if (!epilogue) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: the epilogue is required");
+    vgdr::Epilogue ep;
+    int rc = check_epilogue("vgdr_norm_gate", epilogue, dtype, ep);
+    if (rc) return rc;
+    if (n_rows < 0) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: n_rows=%lld", (long long)n_rows);
+    const int64_t ve = dtype == VGDR_F32 ? 4 : 8, lpr = dv / ve;
+    if (dv <= 0 || dv % ve || lpr > 64 || (lpr & (lpr - 1)))
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_norm_gate: dv=%lld (supported: %lld x a power of two, at most %lld)",
+                    (long long)dv, (long long)ve, (long long)(64 * ve));
+    if (n_rows == 0) return VGDR_OK;
+    if (!o || !out) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: o and out are required");
+    if (!aligned16(o) || !aligned16(out)) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: o and out must be 16-byte aligned");
+    if (n_rows > (int64_t)0xffffffffLL * 256 / lpr) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: too many rows");
+    return hip_status(vgdr::norm_gate(dtype, o, ep, out, n_rows, (int)dv, stream), "vgdr_norm_gate launch");
 }
 
 int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,

@@ -1,0 +1,78 @@
+// The layer's output epilogue, RMSNorm(o) x SiLU(gate) over the value head
+// dim (linear_attention.py:814-825, norm_layer.py:15-24), as one HBM pass.
+//
+// Rows of dv elements (one per (token, head)) are cut into 16-byte units; a
+// group of LPR = dv / VE consecutive lanes owns one row, so a wavefront covers
+// 64 / LPR rows and every global access is one coalesced 16-byte load or
+// store.  The sum of squares is reduced across the group with xor shuffles.
+// The decode step applies the same epilogue inside recurrent_kernel, where a
+// workgroup holds a whole row; the chunk kernels tile dv across workgroups,
+// so prefill runs this pass after the scan.
+#include "gdr_common.hpp"
+#include "gdr_kernels.hpp"
+
+namespace vgdr {
+
+__device__ __forceinline__ float silu_(float x) { return x * sigmoidf_(x); }
+
+template <typename E, int LPR>
+__global__ void __launch_bounds__(256) norm_gate_kernel(const E *o, const E *__restrict__ gate,
+                                                        const void *__restrict__ gamma, int gamma_f32, float eps,
+                                                        E *out, int64_t n_rows) {
+    constexpr int VE = 16 / (int)sizeof(E), DV = LPR * VE;
+    typedef E V __attribute__((ext_vector_type(VE)));
+    const int64_t gt = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = gt / LPR;
+    const int part = (int)(gt % LPR);
+    const bool live = row < n_rows;
+    const int64_t off = (live ? row : n_rows - 1) * DV + part * VE;      // groups past the end re-read the last row
+    const V xv = *reinterpret_cast<const V *>(o + off);
+    const V gv = *reinterpret_cast<const V *>(gate + off);
+    float x[VE], w[VE];
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+        x[e] = (float)xv[e];
+        ss += x[e] * x[e];
+        w[e] = gamma_f32 ? reinterpret_cast<const float *>(gamma)[part * VE + e]
+                         : (float)reinterpret_cast<const E *>(gamma)[part * VE + e];
+    }
+#pragma unroll
+    for (int m = 1; m < LPR; m <<= 1) ss += __shfl_xor(ss, m);
+    const float r = rsqrtf(ss * (1.f / DV) + eps);
+    V y;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) y[e] = (E)(x[e] * r * w[e] * silu_((float)gv[e]));
+    if (live) *reinterpret_cast<V *>(out + off) = y;
+}
+
+template <typename E>
+static hipError_t norm_gate_t(const void *o, const Epilogue &ep, void *out, int64_t n_rows, int dv,
+                              hipStream_t stream) {
+    constexpr int VE = 16 / (int)sizeof(E);
+    const int lpr = dv / VE;
+    const int64_t blocks = (n_rows * lpr + 255) / 256;
+    if (blocks == 0) return hipSuccess;
+    const E *x = reinterpret_cast<const E *>(o), *g = reinterpret_cast<const E *>(ep.gate);
+    E *y = reinterpret_cast<E *>(out);
+#define VGDR_NG(L)                                                                                             \
+    case L:                                                                                                     \
+        hipLaunchKernelGGL((norm_gate_kernel<E, L>), dim3((unsigned)blocks), dim3(256), 0, stream, x, g, ep.gamma, \
+                           ep.gamma_f32, ep.eps, y, n_rows);                                                    \
+        break;
+    switch (lpr) {
+        VGDR_NG(1) VGDR_NG(2) VGDR_NG(4) VGDR_NG(8) VGDR_NG(16) VGDR_NG(32) VGDR_NG(64)
+        default: return hipErrorInvalidValue;
+    }
+#undef VGDR_NG
+    return hipGetLastError();
+}
+
+hipError_t norm_gate(int dtype, const void *o, const Epilogue &ep, void *out, int64_t n_rows, int dv,
+                     hipStream_t stream) {
+    if (dtype == 1) return norm_gate_t<__bf16>(o, ep, out, n_rows, dv, stream);
+    if (dtype == 2) return norm_gate_t<_Float16>(o, ep, out, n_rows, dv, stream);
+    return norm_gate_t<float>(o, ep, out, n_rows, dv, stream);
+}
+
+}  // namespace vgdr

@@ -32,6 +32,17 @@ struct Fusion {
     float lb;
 };
 
+// Output epilogue of the layer (linear_attention.py:814-825): per (token,
+// head), RMSNorm over dv with weight gamma, times SiLU of the output gate:
+//     out = x rsqrt(mean_c x_c^2 + eps) gamma * gate sigmoid(gate),  x = o in q's type
+// computed in fp32 and rounded once.
+struct Epilogue {
+    const void *gate;             // [n_tokens, H, dv] in the element type; NULL = no epilogue
+    const void *gamma;            // [dv], fp32 (gamma_f32) or the element type
+    int gamma_f32;
+    float eps;
+};
+
 struct ChunkParams {
     SeqGeom geo;
     const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
@@ -63,6 +74,7 @@ struct RecParams {
     int use_delta;
     float scale;
     Fusion fz;
+    Epilogue ep;                  // applied to o before it is stored
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.
@@ -76,6 +88,12 @@ int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H,
 
 hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
                          hipStream_t stream);
+
+// The epilogue as its own pass: out[r, :] from o[r, :] and gate[r, :] for
+// n_rows rows of dv elements (out may alias o).  dv / (16 / sizeof(E)) must be
+// a power of two <= 64.
+hipError_t norm_gate(int dtype, const void *o, const Epilogue &ep, void *out, int64_t n_rows, int dv,
+                     hipStream_t stream);
 
 hipError_t varlen_prepare(const int32_t *cu, int n_seqs, int64_t n_tokens, int chunk,
                           int32_t *ws, hipStream_t stream);

@@ -19,7 +19,7 @@
 
 namespace vgdr {
 
-template <int DK, int DV, typename E, int GATE>
+template <int DK, int DV, typename E, int GATE, bool EPI>
 __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
     constexpr int NT = 256;
     constexpr int NCG = DV / 4;             // column groups (float4 each)
@@ -37,6 +37,8 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
     __shared__ float redqk[NWV];
     __shared__ float nrm[NWV][2];           // fused L2 norm: per-wave sums of q^2, k^2
     __shared__ float sc[2];                 // decay (scalar gate), beta
+    __shared__ __attribute__((aligned(16))) float gts[EPI ? DV : 4];   // epilogue: output gate of the token
+    __shared__ __attribute__((aligned(16))) float gms[EPI ? DV : 4];   // epilogue: RMSNorm weight
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int cg = tid % NCG, rg = tid / NCG;
@@ -58,6 +60,12 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
     const E *vg = reinterpret_cast<const E *>(p.v);
     E *og = reinterpret_cast<E *>(p.o);
     const int H = p.H;
+
+    if constexpr (EPI) {
+        for (int i = tid; i < DV; i += NT)
+            gms[i] = p.ep.gamma_f32 ? reinterpret_cast<const float *>(p.ep.gamma)[i]
+                                    : EL::to_f(reinterpret_cast<const E *>(p.ep.gamma)[i]);
+    }
 
     const int64_t sbase = ((int64_t)seq * H + h) * DK * DV;
     f32x4 S[RPT];
@@ -108,7 +116,10 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
                 gv[tid] = __expf(gl);
             }
         }
-        for (int i = tid; i < DV; i += NT) vs[i] = EL::to_f(vg[vo + i]);
+        for (int i = tid; i < DV; i += NT) {
+            vs[i] = EL::to_f(vg[vo + i]);
+            if constexpr (EPI) gts[i] = EL::to_f(reinterpret_cast<const E *>(p.ep.gate)[vo + i]);
+        }
         if (tid == 0) {
             sc[0] = (GATE == 1 && p.g) ? __expf(p.g[t * H + h]) : 1.f;
             const float b = p.use_delta ? p.beta[t * H + h] : 0.f;
@@ -156,7 +167,30 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
         const f32x4 v4 = ld4(&vs[4 * cg]);
         const f32x4 u = p.use_delta ? sc[1] * (v4 - kS) : v4;
         const f32x4 o = qS + qk * u;                     // q was pre-scaled
-        if (rg == 0) {
+        if constexpr (EPI) {
+            // the layer's output epilogue (linear_attention.py:814-825) on the row this
+            // workgroup holds: x = o in E, out = x rsqrt(mean x^2 + eps) gamma silu(gate).
+            // Wave 0 holds every column (lanes cg of each NCG-lane group).
+            if (wave == 0) {
+                // the gate and gamma were staged in LDS with v (loads issued early, no
+                // registers held across the step)
+                float x[4], ss = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    x[e] = EL::to_f(EL::from_f(o[e]));
+                    ss += x[e] * x[e];
+                }
+#pragma unroll
+                for (int m = 1; m < NCG; m <<= 1) ss += __shfl_xor(ss, m);
+                const float r = rsqrtf(ss * (1.f / DV) + p.ep.eps);
+                if (rg == 0) {
+                    const f32x4 gt = ld4(&gts[4 * cg]), gm = ld4(&gms[4 * cg]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        og[vo + 4 * cg + e] = EL::from_f(x[e] * r * gm[e] * (gt[e] * sigmoidf_(gt[e])));
+                }
+            }
+        } else if (rg == 0) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) og[vo + 4 * cg + e] = EL::from_f(o[e]);
         }
@@ -176,8 +210,12 @@ template <int DK, int DV, typename E, int GATE>
 static hipError_t launch_rec(const RecParams &p, hipStream_t stream) {
     const int64_t blocks = (int64_t)p.n_seqs * p.H;
     if (blocks == 0) return hipSuccess;
-    hipLaunchKernelGGL((recurrent_kernel<DK, DV, E, GATE>), dim3((unsigned)blocks), dim3(256), 0,
-                       stream, p);
+    if (p.ep.gate)
+        hipLaunchKernelGGL((recurrent_kernel<DK, DV, E, GATE, true>), dim3((unsigned)blocks), dim3(256), 0,
+                           stream, p);
+    else
+        hipLaunchKernelGGL((recurrent_kernel<DK, DV, E, GATE, false>), dim3((unsigned)blocks), dim3(256), 0,
+                           stream, p);
     return hipGetLastError();
 }
 

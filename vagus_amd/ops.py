@@ -290,9 +290,67 @@ def chunk_simple_gla(q, k, v, g, scale=None, initial_state=None, output_final_st
                   cu_seqlens=cu_seqlens, chunk_size=chunk_size)
 
 
+class _Epilogue:
+    """The layer's output epilogue (linear_attention.py:814-825): RMSNorm of o
+    over dv with weight gamma, times SiLU(gate)."""
+
+    def __init__(self, gate, gamma, eps):
+        assert gate is not None and gamma is not None, 'the output epilogue needs the gate and the norm weight'
+        assert gamma.dim() == 1 and gate.shape[-1] == gamma.shape[0], \
+            f'gamma is (dv,) and gate (..., dv); got {tuple(gamma.shape)}, {tuple(gate.shape)}'
+        assert eps > 0, 'the RMSNorm eps must be positive'
+        _check_device(gate, gamma)
+        self.gate, self.gamma, self.eps = gate, gamma, float(eps)
+
+    def struct(self, dtype):
+        """(vgdr_epilogue, tensors to keep alive) for o in `dtype`."""
+        if self.gate.dtype != dtype:
+            raise NotImplementedError(f'the epilogue gate must have o\'s dtype {dtype}; got {self.gate.dtype}')
+        gate = _aligned(self.gate)
+        gamma = self.gamma.contiguous() if self.gamma.dtype in (torch.float32, dtype) else self.gamma.float()
+        ep = _lib.Epilogue(gate=_ptr(gate), gamma=_ptr(gamma), gamma_dtype=_DTYPES[gamma.dtype], eps=self.eps)
+        return ep, (gate, gamma)
+
+
+def _norm_gate(o, ep: _Epilogue):
+    """One HIP pass: ep applied to o (..., dv), returned in o's dtype."""
+    assert o.shape == ep.gate.shape, f'o {tuple(o.shape)} and gate {tuple(ep.gate.shape)} differ'
+    if o.dtype not in _DTYPES:
+        raise NotImplementedError(f'o must be one of {list(_DTYPES)}; got {o.dtype}')
+    x = _aligned(o)
+    out = torch.empty_like(x)
+    e, keep = ep.struct(x.dtype)
+    dv = x.shape[-1]
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().vgdr_norm_gate(_DTYPES[x.dtype], _ptr(x), ctypes.byref(e), _ptr(out),
+                                              x.numel() // max(dv, 1), dv, _stream(x.device)))
+    del keep
+    return out
+
+
+def rms_norm_gated(x, g, weight, bias=None, activation='swish', residual=None, prenorm=False,
+                   residual_in_fp32=False, eps=1e-6):
+    """RMSNorm(x) * weight * SiLU(g) over the last dim in one HIP pass: fla's
+    rms_norm_gated as the reference calls it (linear_attention.py:820-823,
+    bias None, activation 'swish'), equal to the torch expression at :825
+    (norm_layer.py:15-24) up to rounding.  x, g: (..., D) in one dtype;
+    weight: (D,) fp32 or x's dtype."""
+    if bias is not None or residual is not None or prenorm or activation not in ('swish', 'silu'):
+        raise NotImplementedError('rms_norm_gated: only bias=None, residual=None, prenorm=False and the '
+                                  'swish / silu activation (the reference\'s call) are implemented')
+    _check_grad(x, g, weight)
+    return _norm_gate(x, _Epilogue(g, weight, eps))
+
+
 def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state,
-               cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION):
+               cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION, epilogue=None):
     dv = v.shape[-1]
+    if epilogue is not None and dv not in _REC_DVS:
+        # the fused epilogue needs the kernel's whole, unpadded dv row: apply it as its own pass
+        o, S = _recurrent(q, k, v, g, beta, gate=gate, delta=delta, scale=scale, initial_state=initial_state,
+                          output_final_state=output_final_state, cu_seqlens=cu_seqlens,
+                          inplace_final_state=inplace_final_state, fusion=fusion)
+        return _norm_gate(o, epilogue), S
     if dv > max(_REC_DVS):
         # the recurrence is column-separable: independent 128-wide column blocks
         outs, states = [], []
@@ -325,7 +383,15 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
     with torch.cuda.device(c.device):
         head = (_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
                 _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), _ptr(c.cu), c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale)
-        if fusion.any:
+        if epilogue is not None:
+            assert epilogue.gate.shape == (c.B, c.T, c.H, c.dv), \
+                f'the epilogue gate must be {(c.B, c.T, c.H, c.dv)}; got {tuple(epilogue.gate.shape)}'
+            fz, keep = fusion.struct(c) if fusion.any else (None, None)
+            ep, keep_ep = epilogue.struct(c.dtype)
+            _lib.check(L.vgdr_recurrent_fwd_epilogue(*head, None if fz is None else ctypes.byref(fz),
+                                                     ctypes.byref(ep), _stream(c.device)))
+            del keep, keep_ep
+        elif fusion.any:
             fz, keep = fusion.struct(c)
             _lib.check(L.vgdr_recurrent_fwd_fused(*head, ctypes.byref(fz), _stream(c.device)))
             del keep
@@ -394,9 +460,17 @@ def hip_scan(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_size: int
 
 
 def hip_recurrent(q, k, v, g, beta, S0, *, scale: float, delta: bool, cu_seqlens=None,
-                  inplace: bool = False):
+                  inplace: bool = False, out_gate=None, out_norm_weight=None, out_norm_eps: float = 1e-6):
     """The contract of recurrent_scan (linear_attention.py:161-195) on the GPU:
-    token-by-token from S0, returning (o, S).  inplace=True updates S0 itself."""
+    token-by-token from S0, returning (o, S).  inplace=True updates S0 itself.
+
+    With out_gate (B, T, H, dv) (the W_g x projection, o's dtype) and
+    out_norm_weight (dv,) (o_norm's gamma), o is returned through the layer's
+    output epilogue RMSNorm(o) * SiLU(out_gate) (GatedDeltaNet._output before
+    W_o, :814-825), computed by the same kernel: the decode step up to W_o."""
+    ep = None
+    if out_gate is not None or out_norm_weight is not None:
+        ep = _Epilogue(out_gate, out_norm_weight, out_norm_eps)
     return _recurrent(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale,
                       initial_state=S0, output_final_state=True, cu_seqlens=cu_seqlens,
-                      inplace_final_state=inplace)
+                      inplace_final_state=inplace, epilogue=ep)
