@@ -198,8 +198,8 @@ def measured_traffic(workload, kernel):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=30)
-    ap.add_argument('--warmup', type=int, default=6)
+    ap.add_argument('--steps', type=int, default=60)
+    ap.add_argument('--warmup', type=int, default=100)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--prefill-only', action='store_true', help='only the headline prefill (for profiling)')
     ap.add_argument('--decode-only', action='store_true', help='only the decode step (for profiling)')
