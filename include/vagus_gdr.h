@@ -69,8 +69,8 @@ enum vgdr_gate {
  */
 typedef struct vgdr_fusion {
     int qk_l2norm;          /* q, k un-normalised: x rsqrt(sum_c x_c^2 + 1e-6) per (token, head), rounded
-                               to q's type (needs use_delta) */
-    int beta_sigmoid;       /* beta holds logits: sigmoid(beta) (needs use_delta) */
+                               to q's type (the chunked scan: needs use_delta, as fla) */
+    int beta_sigmoid;       /* beta holds logits: sigmoid(beta) (the chunked scan: needs use_delta) */
     int gate_activation;    /* gate_kind 2 only: g holds the pre-activation f [n_tokens, H, dk] and
                                g = lower_bound_set ? lower_bound * sigmoid(exp(A_log[h]) (f + dt_bias[h dk + c]))
                                                    : -exp(A_log[h]) softplus(f + dt_bias[h dk + c]) */
@@ -94,6 +94,26 @@ typedef struct vgdr_epilogue {
     int gamma_dtype;        /* VGDR_F32 or dtype */
     float eps;              /* > 0 */
 } vgdr_epilogue;
+
+/*
+ * The layer's short causal convolution + SiLU on the q, k, v projections
+ * (ShortConv, opt.py:15-93, applied at linear_attention.py:741-745), with the
+ * decode-time conv cache (:929-941): channel c of token t is
+ *     SiLU( sum_j w[c][j] x[t - K + 1 + j][c] ),
+ * the inputs before a sequence's first token taken from its cache, which holds
+ * the sequence's last K inputs and is advanced in place.  The convolution's and
+ * the SiLU's results are rounded to dtype, as the module computes them.
+ */
+typedef struct vgdr_short_conv {
+    const void *weight_q;   /* [H * dk, K]: nn.Conv1d's (D, 1, K) weight, squeezed */
+    const void *weight_k;   /* [H * dk, K] */
+    const void *weight_v;   /* [H * dv, K] */
+    void *cache_q;          /* [n_seqs, K, H * dk] in dtype (the module's qp_cache) */
+    void *cache_k;          /* [n_seqs, K, H * dk] */
+    void *cache_v;          /* [n_seqs, K, H * dv] */
+    int kernel_size;        /* K, 1..8 */
+    int weight_dtype;       /* VGDR_F32 or dtype */
+} vgdr_short_conv;
 
 /* Library version (major * 10000 + minor * 100 + patch). */
 int vgdr_version(void);
@@ -214,6 +234,23 @@ int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta,
                                 int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
                                 float scale, const vgdr_fusion *fusion, const vgdr_epilogue *epilogue,
                                 hipStream_t stream);
+
+/* The decode step of GatedDeltaNet.decode_step from the projections to the
+ * input of W_o (linear_attention.py:918-952 with _heads :737-747 and _output
+ * :814-825), in one kernel per call: with `conv` (NULL = none), q, k, v are
+ * the raw projections qp, kp, vp [n_tokens, H, d] and go through the short
+ * conv + SiLU (advancing its caches), then the producer fusions (the q, k L2
+ * norm, beta sigmoid, KDA gate activation), the recurrence from
+ * initial_state, and with `epilogue` the RMSNorm x SiLU(gate) output.
+ * dk, dv in {64, 128}. */
+int vgdr_decode_step(int dtype, int gate_kind, int use_delta,
+                     const void *q, const void *k, const void *v,
+                     const float *g, const float *beta,
+                     void *o, const float *initial_state, float *final_state,
+                     const int32_t *cu_seqlens,
+                     int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                     float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
+                     const vgdr_epilogue *epilogue, hipStream_t stream);
 
 /* The output epilogue as one pass over n_rows rows of dv elements (a row per
  * (token, head)): out = epilogue(o, gate).  Replaces rms_norm_gated / the

@@ -26,6 +26,9 @@ Functions and the reference lines they follow:
     beta_sigmoid    linear_attention.py:735-736   beta from its logits
     norm_gate       linear_attention.py:814-825   output epilogue RMSNorm(o) * SiLU(gate)
                     norm_layer.py:15-24           (fused by the kernels' vgdr_epilogue)
+    short_conv      opt.py:15-100                 causal depthwise conv + SiLU, decode cache
+                    linear_attention.py:929-941   (fused by the decode kernel's vgdr_short_conv)
+    decode_step     linear_attention.py:929-947   conv, L2 norm, recurrence of one decode call
 
 Layouts follow the reference (linear_attention.py:146-154): q, k (B, L, H, dk),
 v (B, L, H, dv), g (B, L, H) or (B, L, H, dk), beta (B, L, H), S0 (B, H, dk, dv).
@@ -42,7 +45,10 @@ brute-force enumeration; ``chunk_scan_flops`` by the reference's known answers;
 the producers by their defining properties (unit norms and scale invariance,
 softplus / sigmoid identities and limits, the bounded gate's range);
 ``norm_gate`` against torch's own ``F.rms_norm`` x ``F.silu`` in fp64, a
-constant row's closed form and scale invariance.
+constant row's closed form and scale invariance; ``short_conv`` against
+torch's ``F.conv1d`` on the left-padded transpose (nn.Conv1d, the module's
+'conv1d' path), a unit impulse returning the reversed kernel, and streaming
+(token-by-token calls threading the cache equal one call).
 """
 from __future__ import annotations
 
@@ -351,3 +357,44 @@ def norm_gate(o, gate, gamma, eps: float = 1e-6):
     h = _hi(x)
     y = (h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * gamma
     return y * torch.nn.functional.silu(gate)
+
+
+# ---------------------------------------------------------------------------
+# the decode step's producers (vgdr_short_conv, vgdr_decode_step)
+# ---------------------------------------------------------------------------
+
+def short_conv(x, weight, cache=None, activation: str | None = 'silu'):
+    """Depthwise causal 1-D conv over the sequence (ShortConv, opt.py:15-93):
+    y[t][c] = sum_j w[c][j] x[t - K + 1 + j][c], with the inputs before t = 0
+    taken from `cache` (B, K, D), the previous call's last K inputs
+    (linear_attention.py:929-941), or zero.  x (B, L, D); weight (D, 1, K) or
+    (D, K).  The sum runs in at least fp32 and is returned in x's dtype, then
+    SiLU in that dtype (opt.py:96-100).  Returns (y, new cache = the last K
+    inputs of cache ++ x)."""
+    B, L, D = x.shape
+    K = weight.shape[-1]
+    w = _hi(weight.reshape(D, K))
+    prev = torch.zeros(B, K, D, dtype=x.dtype) if cache is None else cache.to(x.dtype)
+    xs = torch.cat([prev, x], 1)
+    h = _hi(xs)
+    y = sum(w[:, j] * h[:, 1 + j:1 + j + L] for j in range(K))
+    y = y.to(x.dtype)
+    if activation is not None:
+        y = torch.nn.functional.silu(y)
+    return y, xs[:, -K:].clone()
+
+
+def decode_step(qp, kp, vp, g, beta, S0, conv_weights, conv_cache, *, scale: float, delta: bool = True,
+                l2norm_qk: bool = True):
+    """GatedDeltaNet.decode_step's data path up to _output (linear_attention.py:
+    929-947): short conv + SiLU of the projections (advancing the caches),
+    per-head view, q, k L2 norm, then the recurrence from S0.  qp, kp
+    (B, L, H*dk), vp (B, L, H*dv); returns (o, S, (new caches))."""
+    B, L = qp.shape[0], qp.shape[1]
+    H, dk, dv = S0.shape[1], S0.shape[2], S0.shape[3]
+    (q, cq), (k, ck), (v, cv) = (short_conv(x, w, c) for x, w, c in zip((qp, kp, vp), conv_weights, conv_cache))
+    q, k, v = q.view(B, L, H, dk), k.view(B, L, H, dk), v.view(B, L, H, dv)
+    if l2norm_qk:
+        q, k = l2norm(q), l2norm(k)
+    o, S = recurrent(q, k, v, g, beta, S0, scale=scale, delta=delta)
+    return o, S, (cq, ck, cv)

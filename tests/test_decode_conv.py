@@ -1,0 +1,200 @@
+"""The decode step with the short conv fused (vgdr_decode_step,
+vgdr_short_conv; linear_attention.py:918-952, opt.py:15-100).
+
+CPU: the oracle's short_conv pinned against torch's F.conv1d on the
+left-padded transpose (nn.Conv1d, the module's 'conv1d' path), a unit
+impulse, and streaming (token-by-token calls threading the cache equal one
+call); the oracle's decode_step against itself token by token; the C ABI's
+argument checks (no launch).
+GPU: hip_decode_step against the oracle's decode_step (fp64 recurrence fed
+the oracle's producers) at rel_l2 <= 2e-2 for bf16 and 1e-5 for fp32, and the
+advanced conv caches bit-exact (they are copies of inputs).
+"""
+import ctypes
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import gdr
+from vagus_amd import _lib
+
+TOL = 2e-2
+
+
+def _rel(x, ref):
+    x, ref = x.double().cpu(), ref.double().cpu()
+    return ((x - ref).norm() / ref.norm().clamp_min(1e-30)).item()
+
+
+# --- the oracle (CPU) --------------------------------------------------------
+
+def test_short_conv_equals_conv1d_on_left_padded_input():
+    g = torch.Generator().manual_seed(0)
+    B, L, D, K = 2, 11, 6, 4
+    x = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    w = torch.randn(D, 1, K, generator=g, dtype=torch.float64)
+    y, cache = gdr.short_conv(x, w, None, activation=None)
+    ref = F.conv1d(F.pad(x.transpose(1, 2), (K - 1, 0)), w, groups=D).transpose(1, 2)
+    assert torch.allclose(y, ref, rtol=1e-12, atol=1e-12)
+    assert torch.equal(cache, x[:, -K:])
+    ys, _ = gdr.short_conv(x, w, None)
+    assert torch.allclose(ys, F.silu(ref), rtol=1e-12, atol=1e-12)
+
+
+def test_short_conv_impulse_returns_reversed_kernel():
+    D, K = 3, 4
+    w = torch.arange(1.0, D * K + 1, dtype=torch.float64).reshape(D, K)
+    x = torch.zeros(1, 6, D, dtype=torch.float64)
+    x[0, 0] = 1.0
+    y, _ = gdr.short_conv(x, w, None, activation=None)
+    for t in range(K):
+        assert torch.equal(y[0, t], w[:, K - 1 - t])
+    assert torch.equal(y[0, K:], torch.zeros(6 - K, D, dtype=torch.float64))
+
+
+@pytest.mark.parametrize('K', [1, 2, 4])
+def test_short_conv_streams_through_its_cache(K):
+    g = torch.Generator().manual_seed(K)
+    B, L, D = 2, 9, 5
+    x = torch.randn(B, L, D, generator=g, dtype=torch.float64)
+    w = torch.randn(D, K, generator=g, dtype=torch.float64)
+    c0 = torch.randn(B, K, D, generator=g, dtype=torch.float64)
+    y_all, c_all = gdr.short_conv(x, w, c0)
+    c, ys = c0, []
+    for sl in (slice(0, 1), slice(1, 3), slice(3, 4), slice(4, 9)):      # calls shorter and longer than K
+        y, c = gdr.short_conv(x[:, sl], w, c)
+        ys.append(y)
+    assert torch.allclose(torch.cat(ys, 1), y_all, rtol=1e-12, atol=1e-12)
+    assert torch.equal(c, c_all)
+    assert torch.equal(c_all, torch.cat([c0, x], 1)[:, -K:])
+
+
+def _decode_inputs(B, L, H, dk, dv, K, gate, dtype, seed, w_dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    qp = torch.randn(B, L, H * dk, generator=g).to(dtype)
+    kp = torch.randn(B, L, H * dk, generator=g).to(dtype)
+    vp = torch.randn(B, L, H * dv, generator=g).to(dtype)
+    ws = tuple((0.5 * torch.randn(d, 1, K, generator=g)).to(w_dtype) for d in (H * dk, H * dk, H * dv))
+    cs = tuple(torch.randn(B, K, d, generator=g).to(dtype) for d in (H * dk, H * dk, H * dv))
+    beta = torch.sigmoid(torch.randn(B, L, H, generator=g))
+    gl = F.logsigmoid(torch.randn(*((B, L, H, dk) if gate == 'vector' else (B, L, H)), generator=g) + 4.0)
+    S0 = 0.1 * torch.randn(B, H, dk, dv, generator=g)
+    return qp, kp, vp, ws, cs, gl, beta, S0
+
+
+def test_oracle_decode_step_is_token_by_token_consistent():
+    qp, kp, vp, ws, cs, gl, beta, S0 = _decode_inputs(2, 5, 2, 8, 4, 3, 'scalar', torch.float64, seed=1,
+                                                      w_dtype=torch.float64)
+    o_all, S_all, c_all = gdr.decode_step(qp, kp, vp, gl, beta.double(), S0.double(), ws, cs, scale=0.3)
+    S, c, os_ = S0.double(), cs, []
+    for t in range(5):
+        o, S, c = gdr.decode_step(qp[:, t:t + 1], kp[:, t:t + 1], vp[:, t:t + 1], gl[:, t:t + 1],
+                                  beta[:, t:t + 1].double(), S, ws, c, scale=0.3)
+        os_.append(o)
+    assert torch.allclose(torch.cat(os_, 1), o_all, rtol=1e-12, atol=1e-12)
+    assert torch.allclose(S, S_all, rtol=1e-12, atol=1e-12)
+    assert all(torch.equal(a, b) for a, b in zip(c, c_all))
+
+
+# --- C ABI argument checks (no launch) --------------------------------------
+
+def test_short_conv_argument_checks():
+    L = _lib.load()
+
+    def call(sc):
+        return L.vgdr_decode_step(1, 1, 1, 16, 32, 48, 64, 80, 96, None, None, None,
+                                  1, 1, 4, 128, 128, 1, 1.0, None, ctypes.byref(sc), None, None)
+    good = dict(weight_q=256, weight_k=512, weight_v=768, cache_q=1024, cache_k=1280, cache_v=1536,
+                kernel_size=4, weight_dtype=_lib.VGDR_F32)
+    for k_, v_ in (('kernel_size', 0), ('kernel_size', 9)):
+        assert call(_lib.ShortConv(**{**good, k_: v_})) == _lib.VGDR_ERR_UNSUPPORTED
+    assert b'kernel_size' in L.vgdr_last_error()
+    assert call(_lib.ShortConv(**{**good, 'cache_v': None})) == _lib.VGDR_ERR_INVALID
+    assert call(_lib.ShortConv(**{**good, 'weight_dtype': _lib.VGDR_F16})) == _lib.VGDR_ERR_INVALID
+
+
+# --- GPU ----------------------------------------------------------------------
+
+def _run(gate, dtype, K, L, epilogue, w_dtype, seed, B=4, H=2, dk=128, dv=64):
+    from vagus_amd import ops
+    qp, kp, vp, ws, cs, gl, beta, S0 = _decode_inputs(B, L, H, dk, dv, K, gate, dtype, seed, w_dtype)
+    g = torch.Generator().manual_seed(seed + 100)
+    og = torch.randn(B, L, H, dv, generator=g).to(dtype)
+    gamma = torch.rand(dv, generator=g) + 0.5
+    print(f'\n[case] decode conv gate={gate} dtype={dtype} K={K} L={L} epilogue={epilogue} w={w_dtype}', flush=True)
+    o_ref, S_ref, c_ref = gdr.decode_step(qp, kp, vp, gl.double(), beta.double(), S0.double(), ws, cs,
+                                          scale=dk ** -0.5)
+    if epilogue:
+        o_ref = gdr.norm_gate(o_ref.to(dtype).double(), og.double(), gamma.double(), 1e-6)
+    dev = lambda t: t.cuda()
+    S = dev(S0.clone())
+    caches = tuple(dev(c.clone()) for c in cs)
+    o = ops.hip_decode_step(dev(qp), dev(kp), dev(vp), dev(gl), dev(beta), S, scale=dk ** -0.5,
+                            conv_weights=tuple(dev(w) for w in ws), conv_cache=caches,
+                            out_gate=dev(og) if epilogue else None, out_norm_weight=dev(gamma) if epilogue else None)
+    tol = 1e-5 if dtype == torch.float32 else TOL
+    eo, es = _rel(o, o_ref), _rel(S, S_ref)
+    exact = all(torch.equal(a.cpu(), b) for a, b in zip(caches, c_ref))
+    print(f'[parity] decode conv o={eo:.3e} S={es:.3e} caches exact={exact} (tol {tol:g})', flush=True)
+    assert eo <= tol and es <= tol and exact
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('L', [1, 3, 6])
+@pytest.mark.parametrize('K', [4, 2])
+def test_decode_step_conv_matches_oracle(dtype, L, K):
+    _run('scalar', dtype, K, L, epilogue=False, w_dtype=torch.float32, seed=L * 10 + K)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('gate', ['scalar', 'vector'])
+def test_decode_step_conv_with_epilogue(gate):
+    _run(gate, torch.bfloat16, 4, 1, epilogue=True, w_dtype=torch.bfloat16, seed=7)
+
+
+@pytest.mark.gpu
+def test_decode_step_conv_varlen():
+    from vagus_amd import ops
+    H, dk, dv, K = 2, 64, 128, 4
+    cu = torch.tensor([0, 1, 1, 3, 8], dtype=torch.int32)      # lengths 1, 0, 2, 5
+    N, T = 4, 8
+    qp, kp, vp, ws, _, gl, beta, _ = _decode_inputs(1, T, H, dk, dv, K, 'scalar', torch.bfloat16, seed=21)
+    g = torch.Generator().manual_seed(22)
+    cs = tuple(torch.randn(N, K, d, generator=g).bfloat16() for d in (H * dk, H * dk, H * dv))
+    S0 = 0.1 * torch.randn(N, H, dk, dv, generator=g)
+    print('\n[case] decode conv varlen', flush=True)
+    os_, Ss, cref = [], [], [[], [], []]
+    for n in range(N):
+        a, b = int(cu[n]), int(cu[n + 1])
+        o, S, c = gdr.decode_step(qp[:, a:b], kp[:, a:b], vp[:, a:b], gl[:, a:b].double(), beta[:, a:b].double(),
+                                  S0[n:n + 1].double(), ws, tuple(x[n:n + 1] for x in cs), scale=dk ** -0.5)
+        os_.append(o)
+        Ss.append(S)
+        for i in range(3):
+            cref[i].append(c[i])
+    o_ref, S_ref = torch.cat(os_, 1), torch.cat(Ss, 0)
+    dev = lambda t: t.cuda()
+    S = dev(S0.clone())
+    caches = tuple(dev(c.clone()) for c in cs)
+    o = ops.hip_decode_step(dev(qp), dev(kp), dev(vp), dev(gl), dev(beta), S, scale=dk ** -0.5,
+                            conv_weights=tuple(dev(w) for w in ws), conv_cache=caches, cu_seqlens=dev(cu))
+    eo, es = _rel(o, o_ref), _rel(S, S_ref)
+    exact = all(torch.equal(a.cpu(), torch.cat(b, 0)) for a, b in zip(caches, cref))
+    print(f'[parity] decode conv varlen o={eo:.3e} S={es:.3e} caches exact={exact}', flush=True)
+    assert eo <= TOL and es <= TOL and exact
+
+
+@pytest.mark.gpu
+def test_decode_step_conv_misuse():
+    from vagus_amd import ops
+    qp, kp, vp, ws, cs, gl, beta, S0 = _decode_inputs(2, 1, 2, 96, 64, 4, 'scalar', torch.bfloat16, seed=3)
+    dev = lambda t: t.cuda()
+    with pytest.raises(NotImplementedError):                 # dk = 96 would need padding
+        ops.hip_decode_step(dev(qp), dev(kp), dev(vp), dev(gl), dev(beta), dev(S0), scale=0.1,
+                            conv_weights=tuple(dev(w) for w in ws), conv_cache=tuple(dev(c) for c in cs))
+    qp, kp, vp, ws, cs, gl, beta, S0 = _decode_inputs(2, 1, 2, 64, 64, 4, 'scalar', torch.bfloat16, seed=3)
+    with pytest.raises(AssertionError):                      # caches are updated in place: q's dtype
+        ops.hip_decode_step(dev(qp), dev(kp), dev(vp), dev(gl), dev(beta), dev(S0), scale=0.1,
+                            conv_weights=tuple(dev(w) for w in ws), conv_cache=tuple(dev(c.float()) for c in cs))

@@ -31,10 +31,18 @@ class Epilogue(ctypes.Structure):
                 ('eps', ctypes.c_float)]
 
 
+class ShortConv(ctypes.Structure):
+    """struct vgdr_short_conv: the q, k, v short conv + SiLU and its decode caches."""
+    _fields_ = [('weight_q', ctypes.c_void_p), ('weight_k', ctypes.c_void_p), ('weight_v', ctypes.c_void_p),
+                ('cache_q', ctypes.c_void_p), ('cache_k', ctypes.c_void_p), ('cache_v', ctypes.c_void_p),
+                ('kernel_size', ctypes.c_int), ('weight_dtype', ctypes.c_int)]
+
+
 # every symbol the header declares, with its ctypes signature
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 _FZ = ctypes.POINTER(Fusion)
 _EP = ctypes.POINTER(Epilogue)
+_SC = ctypes.POINTER(ShortConv)
 SIGNATURES = {
     'vgdr_version': (_I, []),
     'vgdr_last_error': (ctypes.c_char_p, []),
@@ -56,6 +64,8 @@ SIGNATURES = {
     'vgdr_recurrent_fwd_epilogue': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                          _L, _L, _L, _L, _L, _L, _F, _FZ, _EP, _P]),
     'vgdr_norm_gate': (_I, [_I, _P, _EP, _P, _L, _L, _P]),
+    'vgdr_decode_step': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                              _L, _L, _L, _L, _L, _L, _F, _FZ, _SC, _EP, _P]),
     'vgdr_varlen_workspace_size': (_L, [_L]),
     'vgdr_varlen_prepare': (_I, [_P, _L, _L, _I, _P, _P]),
 }

@@ -70,7 +70,7 @@ int check_fusion(const char *fn, const vgdr_fusion *fz, int dtype, int gate_kind
     if (!any) return VGDR_OK;
     if (chunked && dtype == VGDR_F32)
         return fail(VGDR_ERR_UNSUPPORTED, "%s: producer fusions take 16-bit q, k, v", fn);
-    if ((fz->qk_l2norm || fz->beta_sigmoid) && !use_delta)
+    if (chunked && (fz->qk_l2norm || fz->beta_sigmoid) && !use_delta)
         return fail(VGDR_ERR_INVALID, "%s: the fused L2 norm and beta sigmoid need the delta rule", fn);
     if (fz->gate_activation) {
         if (gate_kind != VGDR_GATE_VECTOR)
@@ -105,6 +105,27 @@ int check_epilogue(const char *fn, const vgdr_epilogue *ep, int dtype, vgdr::Epi
     out.gamma = ep->gamma;
     out.gamma_f32 = ep->gamma_dtype == VGDR_F32 ? 1 : 0;
     out.eps = ep->eps;
+    return VGDR_OK;
+}
+
+// the short conv a decode call asks for
+int check_conv(const char *fn, const vgdr_short_conv *cv, int dtype, vgdr::ShortConv &out) {
+    out = vgdr::ShortConv{};
+    if (!cv) return VGDR_OK;
+    if (cv->kernel_size < 1 || cv->kernel_size > 8)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: short conv kernel_size=%d (supported: 1..8)", fn, cv->kernel_size);
+    if (!cv->weight_q || !cv->weight_k || !cv->weight_v || !cv->cache_q || !cv->cache_k || !cv->cache_v)
+        return fail(VGDR_ERR_INVALID, "%s: the short conv needs its three weights and three caches", fn);
+    if (cv->weight_dtype != VGDR_F32 && cv->weight_dtype != dtype)
+        return fail(VGDR_ERR_INVALID, "%s: the conv weight_dtype must be VGDR_F32 or the dtype of q", fn);
+    out.wq = cv->weight_q;
+    out.wk = cv->weight_k;
+    out.wv = cv->weight_v;
+    out.cq = cv->cache_q;
+    out.ck = cv->cache_k;
+    out.cv = cv->cache_v;
+    out.K = cv->kernel_size;
+    out.w_f32 = cv->weight_dtype == VGDR_F32 ? 1 : 0;
     return VGDR_OK;
 }
 
@@ -251,11 +272,11 @@ int vgdr_chunk_prep_fused(VGDR_CHUNK_ARGS_FUSED) {
 #undef VGDR_CHUNK_PASS_NOFUSION
 #undef VGDR_CHUNK_PASS_FUSED
 
-int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta, const void *q, const void *k,
-                                const void *v, const float *g, const float *beta, void *o,
-                                const float *initial_state, float *final_state, const int32_t *cu_seqlens,
-                                int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
-                                const vgdr_fusion *fusion, const vgdr_epilogue *epilogue, hipStream_t stream) {
+int vgdr_decode_step(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                     const float *g, const float *beta, void *o, const float *initial_state, float *final_state,
+                     const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                     int64_t n_seqs, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
+                     const vgdr_epilogue *epilogue, hipStream_t stream) {
     g_err[0] = 0;
     int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o,
                           cu_seqlens, B, T, H, dk, dv, n_seqs);
@@ -265,6 +286,9 @@ int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta, const v
     if (rc) return rc;
     vgdr::Epilogue ep;
     rc = check_epilogue("vgdr_recurrent_fwd", epilogue, dtype, ep);
+    if (rc) return rc;
+    vgdr::ShortConv cv;
+    rc = check_conv("vgdr_recurrent_fwd", conv, dtype, cv);
     if (rc) return rc;
     if (dv != 64 && dv != 128)
         return fail(VGDR_ERR_UNSUPPORTED, "vgdr_recurrent_fwd: dv=%lld (supported: 64, 128)", (long long)dv);
@@ -286,8 +310,18 @@ int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta, const v
     p.scale = scale;
     p.fz = fz;
     p.ep = ep;
+    p.cv = cv;
     return hip_status(vgdr::recurrent_fwd(dtype, (int)dk, (int)dv, gate_kind == VGDR_GATE_VECTOR, p, stream),
                       "vgdr_recurrent_fwd launch");
+}
+
+int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta, const void *q, const void *k,
+                                const void *v, const float *g, const float *beta, void *o,
+                                const float *initial_state, float *final_state, const int32_t *cu_seqlens,
+                                int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
+                                const vgdr_fusion *fusion, const vgdr_epilogue *epilogue, hipStream_t stream) {
+    return vgdr_decode_step(dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state, final_state,
+                            cu_seqlens, B, T, H, dk, dv, n_seqs, scale, fusion, nullptr, epilogue, stream);
 }
 
 int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta, const void *q, const void *k,
@@ -295,9 +329,8 @@ int vgdr_recurrent_fwd_fused(int dtype, int gate_kind, int use_delta, const void
                              const float *initial_state, float *final_state, const int32_t *cu_seqlens,
                              int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
                              const vgdr_fusion *fusion, hipStream_t stream) {
-    return vgdr_recurrent_fwd_epilogue(dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state,
-                                       final_state, cu_seqlens, B, T, H, dk, dv, n_seqs, scale, fusion, nullptr,
-                                       stream);
+    return vgdr_decode_step(dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state, final_state,
+                            cu_seqlens, B, T, H, dk, dv, n_seqs, scale, fusion, nullptr, nullptr, stream);
 }
 
 int vgdr_norm_gate(int dtype, const void *o, const vgdr_epilogue *epilogue, void *out, int64_t n_rows, int64_t dv,

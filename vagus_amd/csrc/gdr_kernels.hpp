@@ -43,6 +43,19 @@ struct Epilogue {
     float eps;
 };
 
+// The layer's short causal convolution + SiLU on the q, k, v projections
+// (opt.py:15-93, linear_attention.py:741-745), for the token-by-token kernel:
+// channel c of token t is SiLU(sum_j w[c][j] x[t - K + 1 + j][c]), where inputs
+// before the sequence's first token come from its conv cache (the last K
+// inputs of the previous call, linear_attention.py:929-941), which the kernel
+// then advances in place.
+struct ShortConv {
+    const void *wq, *wk, *wv;     // [H * dk, K], [H * dk, K], [H * dv, K]: fp32 (w_f32) or the element type
+    void *cq, *ck, *cv;           // [n_seqs, K, H * dk | H * dv] in the element type
+    int K;                        // 1..8; 0 = inputs arrive convolved and activated
+    int w_f32;
+};
+
 struct ChunkParams {
     SeqGeom geo;
     const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
@@ -75,6 +88,7 @@ struct RecParams {
     float scale;
     Fusion fz;
     Epilogue ep;                  // applied to o before it is stored
+    ShortConv cv;                 // applied to q, k, v where they are read
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.

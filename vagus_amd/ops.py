@@ -342,9 +342,46 @@ def rms_norm_gated(x, g, weight, bias=None, activation='swish', residual=None, p
     return _norm_gate(x, _Epilogue(g, weight, eps))
 
 
+class _ShortConv:
+    """The q, k, v short conv + SiLU (opt.py:15-93) and its decode caches
+    (linear_attention.py:929-941) for one decode call."""
+
+    def __init__(self, weights, caches):
+        assert weights is not None and caches is not None and len(weights) == 3 and len(caches) == 3, \
+            'the short conv takes (w_q, w_k, w_v) and (qp_cache, kp_cache, vp_cache)'
+        _check_device(*weights, *caches)
+        self.K = weights[0].shape[-1]
+        self.weights = [w.reshape(w.shape[0], self.K) for w in weights]
+        for w in self.weights:
+            assert w.shape[-1] == self.K, 'the three conv weights share one kernel size'
+        self.caches = caches
+
+    def struct(self, c):
+        """(vgdr_short_conv, tensors to keep alive) for the validated call c."""
+        if c.padded:
+            raise NotImplementedError(f'the fused short conv needs dk, dv in {_REC_DVS} (no padding); '
+                                      f'got dk={c.dk}, dv={c.dv}')
+        D = (c.H * c.dk, c.H * c.dk, c.H * c.dv)
+        for w, d in zip(self.weights, D):
+            assert w.shape == (d, self.K), f'conv weight must be ({d}, {self.K}) or ({d}, 1, {self.K}); got {tuple(w.shape)}'
+        for x, d in zip(self.caches, D):
+            assert x.shape == (c.N, self.K, d), f'conv cache must be {(c.N, self.K, d)}; got {tuple(x.shape)}'
+            assert x.dtype == c.dtype and x.is_contiguous() and x.data_ptr() % 16 == 0, \
+                'conv caches are updated in place: contiguous, aligned, in q\'s dtype'
+        wdt = torch.float32 if all(w.dtype == torch.float32 for w in self.weights) else c.dtype
+        ws = [w.to(wdt).contiguous() for w in self.weights]
+        sc = _lib.ShortConv(weight_q=_ptr(ws[0]), weight_k=_ptr(ws[1]), weight_v=_ptr(ws[2]),
+                            cache_q=_ptr(self.caches[0]), cache_k=_ptr(self.caches[1]),
+                            cache_v=_ptr(self.caches[2]), kernel_size=self.K, weight_dtype=_DTYPES[wdt])
+        return sc, ws
+
+
 def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state,
-               cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION, epilogue=None):
+               cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION, epilogue=None,
+               conv: _ShortConv | None = None):
     dv = v.shape[-1]
+    if conv is not None and (dv not in _REC_DVS or q.shape[-1] not in _REC_DVS):
+        raise NotImplementedError(f'the fused short conv needs dk, dv in {_REC_DVS}; got dk={q.shape[-1]}, dv={dv}')
     if epilogue is not None and dv not in _REC_DVS:
         # the fused epilogue needs the kernel's whole, unpadded dv row: apply it as its own pass
         o, S = _recurrent(q, k, v, g, beta, gate=gate, delta=delta, scale=scale, initial_state=initial_state,
@@ -383,7 +420,18 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
     with torch.cuda.device(c.device):
         head = (_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
                 _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), _ptr(c.cu), c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale)
-        if epilogue is not None:
+        if conv is not None:
+            fz, keep = fusion.struct(c) if fusion.any else (None, None)
+            ep, keep_ep = (None, None)
+            if epilogue is not None:
+                assert epilogue.gate.shape == (c.B, c.T, c.H, c.dv), \
+                    f'the epilogue gate must be {(c.B, c.T, c.H, c.dv)}; got {tuple(epilogue.gate.shape)}'
+                ep, keep_ep = epilogue.struct(c.dtype)
+            sc, keep_sc = conv.struct(c)
+            _lib.check(L.vgdr_decode_step(*head, None if fz is None else ctypes.byref(fz), ctypes.byref(sc),
+                                          None if ep is None else ctypes.byref(ep), _stream(c.device)))
+            del keep, keep_ep, keep_sc
+        elif epilogue is not None:
             assert epilogue.gate.shape == (c.B, c.T, c.H, c.dv), \
                 f'the epilogue gate must be {(c.B, c.T, c.H, c.dv)}; got {tuple(epilogue.gate.shape)}'
             fz, keep = fusion.struct(c) if fusion.any else (None, None)
@@ -474,3 +522,41 @@ def hip_recurrent(q, k, v, g, beta, S0, *, scale: float, delta: bool, cu_seqlens
     return _recurrent(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale,
                       initial_state=S0, output_final_state=True, cu_seqlens=cu_seqlens,
                       inplace_final_state=inplace, epilogue=ep)
+
+
+def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = True, conv_weights=None,
+                    conv_cache=None, l2norm: bool = True, beta_logits: bool = False, gate_in_kernel: bool = False,
+                    A_log=None, dt_bias=None, lower_bound: float | None = None, out_gate=None,
+                    out_norm_weight=None, out_norm_eps: float = 1e-6, cu_seqlens=None):
+    """GatedDeltaNet.decode_step (linear_attention.py:918-952) from the
+    projections to the input of W_o, in one kernel.
+
+    qp, kp: (B, L, H*dk) or (B, L, H, dk), vp: (B, L, H*dv) or (B, L, H, dv), the
+    raw projections W_q x, W_k x, W_v x.  conv_weights (w_q, w_k, w_v): the
+    ShortConv weights, (D, 1, K) or (D, K); conv_cache (qp_cache, kp_cache,
+    vp_cache): (N, K, D) in q's dtype, advanced in place (:929-941).  The
+    kernel applies the conv and SiLU (:741-745), the q, k L2 norm unless
+    l2norm=False (:746-747), sigmoid to beta logits with beta_logits, the KDA
+    gate activation with gate_in_kernel (g is then the pre-activation), the
+    recurrence from `state`, which it updates in place (:945-950), and with
+    out_gate / out_norm_weight the RMSNorm x SiLU(gate) epilogue (:814-825).
+    Returns o (B, L, H, dv) in q's dtype.  dk, dv in {64, 128}."""
+    B, L = qp.shape[0], qp.shape[1]
+    H = state.shape[1]
+    dk, dv = state.shape[2], state.shape[3]
+    q = qp.reshape(B, L, H, dk)
+    k = kp.reshape(B, L, H, dk)
+    v = vp.reshape(B, L, H, dv)
+    gate = _gate_of(g)
+    if gate_in_kernel:
+        assert gate == 'vector', 'the fused gate activation is a KDA (vector-gate) kernel'
+    fz = _Fusion(l2norm=l2norm, beta=beta_logits, gate=gate_in_kernel, A_log=A_log, dt_bias=dt_bias,
+                 lower_bound=lower_bound if gate_in_kernel else None)
+    ep = None
+    if out_gate is not None or out_norm_weight is not None:
+        ep = _Epilogue(out_gate.reshape(B, L, H, dv) if out_gate is not None else None, out_norm_weight,
+                       out_norm_eps)
+    o, _ = _recurrent(q, k, v, g, beta, gate=gate, delta=delta, scale=scale, initial_state=state,
+                      output_final_state=True, cu_seqlens=cu_seqlens, inplace_final_state=True, fusion=fz,
+                      epilogue=ep, conv=_ShortConv(conv_weights, conv_cache))
+    return o
