@@ -252,12 +252,27 @@ int vgdr_decode_step(int dtype, int gate_kind, int use_delta,
                      float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
                      const vgdr_epilogue *epilogue, hipStream_t stream);
 
+/* The short conv + SiLU (vgdr_short_conv's semantics) over a whole call's
+ * tokens, for prefill: y[t] from x[t - K + 1 .. t] of the same sequence.
+ * Replaces the module's ShortConv (opt.py:15-100; fla's causal_conv1d as the
+ * reference calls it, :73-77) and, with caches, the cached conv of a
+ * multi-token decode_step (:929-941).  x, y [n_tokens, D] (the q, k or v
+ * projection, D = H * d); weight [D, K] (fp32 or dtype); initial_state /
+ * final_state: [n_seqs, K, D] conv caches in dtype, NULL = zeros / not
+ * written, and may alias.  activation: 0 none, 1 SiLU.  The convolution's and
+ * the SiLU's results are rounded to dtype.  Sequences as in the scans
+ * (dense B x T, or packed with cu_seqlens and B = 1). */
+int vgdr_causal_conv1d(int dtype, const void *x, const void *weight, int weight_dtype,
+                       const void *initial_state, void *y, void *final_state,
+                       const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t D, int64_t n_seqs,
+                       int kernel_size, int activation, hipStream_t stream);
+
 /* The output epilogue as one pass over n_rows rows of dv elements (a row per
  * (token, head)): out = epilogue(o, gate).  Replaces rms_norm_gated / the
  * RMSNorm x SiLU expression at linear_attention.py:820-825 after a chunked
  * prefill (the chunk kernels split dv across workgroups).  out may equal o.
  * dv = 8 x a power of two up to 512 (16-bit), 4 x a power of two up to 256
- * (fp32); o, out 16-byte aligned. */
+ * (fp32); o, out and gamma 16-byte aligned. */
 int vgdr_norm_gate(int dtype, const void *o, const vgdr_epilogue *epilogue, void *out, int64_t n_rows,
                    int64_t dv, hipStream_t stream);
 

@@ -349,7 +349,8 @@ int vgdr_norm_gate(int dtype, const void *o, const vgdr_epilogue *epilogue, void
                     (long long)dv, (long long)ve, (long long)(64 * ve));
     if (n_rows == 0) return VGDR_OK;
     if (!o || !out) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: o and out are required");
-    if (!aligned16(o) || !aligned16(out)) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: o and out must be 16-byte aligned");
+    if (!aligned16(o) || !aligned16(out) || !aligned16(ep.gamma))
+        return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: o, out and gamma must be 16-byte aligned");
     if (n_rows > (int64_t)0xffffffffLL * 256 / lpr) return fail(VGDR_ERR_INVALID, "vgdr_norm_gate: too many rows");
     return hip_status(vgdr::norm_gate(dtype, o, ep, out, n_rows, (int)dv, stream), "vgdr_norm_gate launch");
 }
@@ -360,6 +361,50 @@ int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, c
                        int64_t dk, int64_t dv, int64_t n_seqs, float scale, hipStream_t stream) {
     return vgdr_recurrent_fwd_fused(dtype, gate_kind, use_delta, q, k, v, g, beta, o, initial_state, final_state,
                                     cu_seqlens, B, T, H, dk, dv, n_seqs, scale, nullptr, stream);
+}
+
+int vgdr_causal_conv1d(int dtype, const void *x, const void *weight, int weight_dtype, const void *initial_state,
+                       void *y, void *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t D,
+                       int64_t n_seqs, int kernel_size, int activation, hipStream_t stream) {
+    g_err[0] = 0;
+    const char *fn = "vgdr_causal_conv1d";
+    if (dtype != VGDR_F32 && dtype != VGDR_BF16 && dtype != VGDR_F16)
+        return fail(VGDR_ERR_INVALID, "%s: unknown dtype %d", fn, dtype);
+    if (weight_dtype != VGDR_F32 && weight_dtype != dtype)
+        return fail(VGDR_ERR_INVALID, "%s: weight_dtype must be VGDR_F32 or dtype", fn);
+    if (kernel_size < 1 || kernel_size > 8)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: kernel_size=%d (supported: 1..8)", fn, kernel_size);
+    if (activation != 0 && activation != 1) return fail(VGDR_ERR_INVALID, "%s: activation %d (0 none, 1 silu)", fn, activation);
+    if (B < 0 || T < 0 || D <= 0 || n_seqs < 0 || n_seqs > 0x7fffffffLL)
+        return fail(VGDR_ERR_INVALID, "%s: bad sizes", fn);
+    const int64_t ve = dtype == VGDR_F32 ? 4 : 8;
+    if (D % ve) return fail(VGDR_ERR_UNSUPPORTED, "%s: D=%lld (must be a multiple of %lld)", fn, (long long)D, (long long)ve);
+    if (cu_seqlens) {
+        if (B != 1) return fail(VGDR_ERR_INVALID, "%s: a packed batch (cu_seqlens) needs B == 1", fn);
+    } else if (n_seqs != B) {
+        return fail(VGDR_ERR_INVALID, "%s: n_seqs must equal B for a dense batch", fn);
+    }
+    if (B * T > 0 && (!x || !weight || !y)) return fail(VGDR_ERR_INVALID, "%s: x, weight and y are required", fn);
+    if (!aligned16(x) || !aligned16(y) || !aligned16(initial_state) || !aligned16(final_state))
+        return fail(VGDR_ERR_INVALID, "%s: x, y and the caches must be 16-byte aligned", fn);
+    if (B * T > 0 && x == y) return fail(VGDR_ERR_INVALID, "%s: y must not alias x (outputs read earlier inputs)", fn);
+    if (n_seqs > 0 && !weight) return fail(VGDR_ERR_INVALID, "%s: weight is required", fn);
+    vgdr::ConvParams p{};
+    p.x = x;
+    p.w = weight;
+    p.state_in = initial_state;
+    p.y = y;
+    p.state_out = final_state;
+    p.cu = cu_seqlens;
+    p.T = T;
+    p.n_tokens = B * T;
+    p.D = D;
+    p.n_seqs = (int)n_seqs;
+    p.K = kernel_size;
+    p.w_f32 = weight_dtype == VGDR_F32 ? 1 : 0;
+    p.silu = activation;
+    if (p.n_tokens == 0 && (!final_state || n_seqs == 0)) return VGDR_OK;
+    return hip_status(vgdr::causal_conv(dtype, p, stream), "vgdr_causal_conv1d launch");
 }
 
 int64_t vgdr_varlen_workspace_size(int64_t n_seqs) {

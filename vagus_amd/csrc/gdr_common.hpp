@@ -160,7 +160,10 @@ __device__ __forceinline__ f32x4 exp4(f32x4 x) {
 template <typename T> __host__ __device__ constexpr T cmax(T a, T b) { return a > b ? a : b; }
 
 // the reference's producer activations (linear_attention.py:703-706, :719-736)
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + __expf(-x)); }
+// 1 / (1 + e^-x) with the hardware reciprocal (v_rcp_f32, about 1 ulp): an IEEE
+// division costs a dozen instructions, which made the SiLU of the streaming
+// conv and epilogue kernels bound by the vector ALU rather than by HBM
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 // torch.nn.functional.softplus (beta 1, threshold 20)
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
 // gate activation of the per-channel gate from its pre-activation f

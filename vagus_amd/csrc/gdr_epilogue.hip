@@ -26,16 +26,29 @@ __global__ void __launch_bounds__(256) norm_gate_kernel(const E *o, const E *__r
     const int part = (int)(gt % LPR);
     const bool live = row < n_rows;
     const int64_t off = (live ? row : n_rows - 1) * DV + part * VE;      // groups past the end re-read the last row
-    const V xv = *reinterpret_cast<const V *>(o + off);
-    const V gv = *reinterpret_cast<const V *>(gate + off);
+    // o and the gate stream through once: nontemporal
+    const V xv = __builtin_nontemporal_load(reinterpret_cast<const V *>(o + off));
+    const V gv = __builtin_nontemporal_load(reinterpret_cast<const V *>(gate + off));
     float x[VE], w[VE];
     float ss = 0.f;
+    if (gamma_f32) {
+        // VE fp32 values: one or two 16-byte loads (gamma is 16-byte aligned)
+        const f32x4 *gp = reinterpret_cast<const f32x4 *>(reinterpret_cast<const float *>(gamma) + part * VE);
+#pragma unroll
+        for (int q = 0; q < VE / 4; ++q) {
+            const f32x4 g4 = gp[q];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) w[4 * q + e] = g4[e];
+        }
+    } else {
+        const V g = *reinterpret_cast<const V *>(reinterpret_cast<const E *>(gamma) + part * VE);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) w[e] = (float)g[e];
+    }
 #pragma unroll
     for (int e = 0; e < VE; ++e) {
         x[e] = (float)xv[e];
         ss += x[e] * x[e];
-        w[e] = gamma_f32 ? reinterpret_cast<const float *>(gamma)[part * VE + e]
-                         : (float)reinterpret_cast<const E *>(gamma)[part * VE + e];
     }
 #pragma unroll
     for (int m = 1; m < LPR; m <<= 1) ss += __shfl_xor(ss, m);
@@ -43,7 +56,7 @@ __global__ void __launch_bounds__(256) norm_gate_kernel(const E *o, const E *__r
     V y;
 #pragma unroll
     for (int e = 0; e < VE; ++e) y[e] = (E)(x[e] * r * w[e] * silu_((float)gv[e]));
-    if (live) *reinterpret_cast<V *>(out + off) = y;
+    if (live) __builtin_nontemporal_store(y, reinterpret_cast<V *>(out + off));
 }
 
 template <typename E>

@@ -56,6 +56,20 @@ struct ShortConv {
     int w_f32;
 };
 
+// The short conv over a whole call (prefill): x, y [n_tokens, D]; w [D, K];
+// conv caches [n_seqs, K, D] (state_in may be NULL = zeros, state_out NULL =
+// not written; they may alias).
+struct ConvParams {
+    const void *x;
+    const void *w;
+    const void *state_in;
+    void *y;
+    void *state_out;
+    const int32_t *cu;            // [n_seqs + 1] or NULL (dense: n_seqs sequences of T tokens)
+    int64_t T, n_tokens, D;
+    int n_seqs, K, w_f32, silu;
+};
+
 struct ChunkParams {
     SeqGeom geo;
     const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
@@ -108,6 +122,8 @@ hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecPa
 // a power of two <= 64.
 hipError_t norm_gate(int dtype, const void *o, const Epilogue &ep, void *out, int64_t n_rows, int dv,
                      hipStream_t stream);
+
+hipError_t causal_conv(int dtype, const ConvParams &p, hipStream_t stream);
 
 hipError_t varlen_prepare(const int32_t *cu, int n_seqs, int64_t n_tokens, int chunk,
                           int32_t *ws, hipStream_t stream);

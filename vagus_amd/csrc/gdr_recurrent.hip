@@ -22,49 +22,48 @@ namespace vgdr {
 // Producer of one channel with the short conv: SiLU(sum_j w[c][j] x[t - K + 1 + j][c])
 // for the token t of a sequence starting at bos; x is [n_tokens, HD] (HD = H * d), the
 // cache [K, HD] holds the sequence's K inputs before bos.  The convolution's and the
-// SiLU's results are rounded to E, as the module computes them in its dtype.
+// SiLU's results are rounded to E, as the module computes them in its dtype.  At the
+// sequence's last token (last = true) the K inputs just read are exactly the cache's
+// next contents, and are written back to it here: the owner thread of a channel is
+// its only reader, and it has read its last old value in this call.
 template <typename E>
-__device__ __forceinline__ float conv_silu(const E *x, const E *cache, const void *w, int w_f32, int64_t HD,
-                                           int64_t c, int K, int64_t t, int64_t bos) {
+__device__ __forceinline__ float conv_silu(const E *x, E *cache, const void *w, int w_f32, int64_t HD, int64_t c,
+                                           int K, int64_t t, int64_t bos, bool last) {
     using EL = Elem<E>;
     // c passes through an empty asm: the weight loads then stay in the token step
     // instead of being hoisted out of the token loop into registers held across it
     asm volatile("" : "+v"(c));
+    // all K (<= 8) input and weight loads are issued together (predicated), not one
+    // dependent load per tap
+    E xs[8];
+    float wt[8];
+    unroll<8>([&](auto j) __attribute__((always_inline)) {
+        xs[j] = EL::from_f(0.f);
+        wt[j] = 0.f;
+        if (j < K) {
+            const int64_t pos = t - (K - 1) + j;
+            xs[j] = pos >= bos ? x[pos * HD + c] : cache[(K + (pos - bos)) * HD + c];
+            wt[j] = w_f32 ? reinterpret_cast<const float *>(w)[c * K + j]
+                          : EL::to_f(reinterpret_cast<const E *>(w)[c * K + j]);
+        }
+    });
     float acc = 0.f;
-    for (int j = 0; j < K; ++j) {
-        const int64_t pos = t - (K - 1) + j;
-        const float xv = pos >= bos ? EL::to_f(x[pos * HD + c]) : EL::to_f(cache[(K + (pos - bos)) * HD + c]);
-        const float wv = w_f32 ? reinterpret_cast<const float *>(w)[c * K + j]
-                               : EL::to_f(reinterpret_cast<const E *>(w)[c * K + j]);
-        acc += wv * xv;
+    unroll<8>([&](auto j) __attribute__((always_inline)) { acc += wt[j] * EL::to_f(xs[j]); });
+    if (last) {
+        unroll<8>([&](auto j) __attribute__((always_inline)) {
+            if (j < K) cache[(int64_t)j * HD + c] = xs[j];
+        });
     }
     const float y = EL::to_f(EL::from_f(acc));
     return EL::to_f(EL::from_f(y * sigmoidf_(y)));
-}
-
-// Advance a sequence's conv cache of channel c past its tokens [bos, eos): the
-// last K inputs of (cache, x[bos..eos)).  Every old value is read before any is
-// written (the shift reads slot j + T for slot j).
-template <typename E>
-__device__ __forceinline__ void conv_advance(const E *x, E *cache, int64_t HD, int64_t c, int K, int64_t bos,
-                                             int64_t eos) {
-    E nv[8];
-    unroll<8>([&](auto j) {
-        if (j < K) {
-            const int64_t pos = eos - K + j;
-            nv[j] = pos >= bos ? x[pos * HD + c] : cache[(K + (pos - bos)) * HD + c];
-        }
-    });
-    unroll<8>([&](auto j) {
-        if (j < K) cache[(int64_t)j * HD + c] = nv[j];
-    });
 }
 
 // MODE bit 0: the output epilogue; bit 1: the short conv.  Both are template
 // choices: as run-time branches they add registers to every variant (the GDN
 // kernel fills the chip in one pass only within 128 VGPRs).
 template <int DK, int DV, typename E, int GATE, int MODE>
-__global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATE == 2 ? 1 : 4)))
+recurrent_kernel(const RecParams p) {
     constexpr bool EPI = MODE & 1, CONV = MODE & 2;
     constexpr int NT = 256;
     constexpr int NCG = DV / 4;             // column groups (float4 each)
@@ -128,11 +127,12 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
         if constexpr (CONV) {
             // fused short conv + SiLU of the q, k projections (linear_attention.py:741-745, :929-941)
             const int64_t HDK = (int64_t)H * DK, c = (int64_t)h * DK + tid, cb = (int64_t)seq * p.cv.K * HDK;
-            qv = own ? conv_silu<E>(qg, reinterpret_cast<const E *>(p.cv.cq) + cb, p.cv.wq, p.cv.w_f32, HDK, c,
-                                    p.cv.K, t, bos)
+            const bool last = t == eos - 1;
+            qv = own ? conv_silu<E>(qg, reinterpret_cast<E *>(p.cv.cq) + cb, p.cv.wq, p.cv.w_f32, HDK, c, p.cv.K, t,
+                                    bos, last)
                      : 0.f;
-            kv = own ? conv_silu<E>(kg, reinterpret_cast<const E *>(p.cv.ck) + cb, p.cv.wk, p.cv.w_f32, HDK, c,
-                                    p.cv.K, t, bos)
+            kv = own ? conv_silu<E>(kg, reinterpret_cast<E *>(p.cv.ck) + cb, p.cv.wk, p.cv.w_f32, HDK, c, p.cv.K, t,
+                                    bos, last)
                      : 0.f;
         } else {
             qv = own ? EL::to_f(qg[qo + tid]) : 0.f;
@@ -177,8 +177,8 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
         for (int i = tid; i < DV; i += NT) {
             if constexpr (CONV) {
                 const int64_t HDV = (int64_t)H * DV;
-                vs[i] = conv_silu<E>(vg, reinterpret_cast<const E *>(p.cv.cv) + (int64_t)seq * p.cv.K * HDV, p.cv.wv,
-                                     p.cv.w_f32, HDV, (int64_t)h * DV + i, p.cv.K, t, bos);
+                vs[i] = conv_silu<E>(vg, reinterpret_cast<E *>(p.cv.cv) + (int64_t)seq * p.cv.K * HDV, p.cv.wv,
+                                     p.cv.w_f32, HDV, (int64_t)h * DV + i, p.cv.K, t, bos, t == eos - 1);
             } else {
                 vs[i] = EL::to_f(vg[vo + i]);
             }
@@ -268,19 +268,8 @@ __global__ void __launch_bounds__(256) recurrent_kernel(const RecParams p) {
         for (int i = 0; i < RPT; ++i)
             __builtin_nontemporal_store(S[i], reinterpret_cast<f32x4 *>(p.ht + sbase + (int64_t)(rg + NRG * i) * DV + 4 * cg));
     }
-    if constexpr (CONV) {
-        // the conv caches move past this call's tokens; each thread owns its channels, and
-        // read them (in conv_silu) only in its own earlier steps
-        const int64_t HDK = (int64_t)H * DK, HDV = (int64_t)H * DV;
-        if (tid < DK) {
-            const int64_t c = (int64_t)h * DK + tid, cb = (int64_t)seq * p.cv.K * HDK;
-            conv_advance<E>(qg, reinterpret_cast<E *>(p.cv.cq) + cb, HDK, c, p.cv.K, bos, eos);
-            conv_advance<E>(kg, reinterpret_cast<E *>(p.cv.ck) + cb, HDK, c, p.cv.K, bos, eos);
-        }
-        for (int i = tid; i < DV; i += NT)
-            conv_advance<E>(vg, reinterpret_cast<E *>(p.cv.cv) + (int64_t)seq * p.cv.K * HDV, HDV,
-                            (int64_t)h * DV + i, p.cv.K, bos, eos);
-    }
+    // (the conv caches were advanced in the last token's step; an empty segment leaves
+    // its cache as it was)
 }
 
 template <int DK, int DV, typename E, int GATE>

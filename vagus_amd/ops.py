@@ -307,7 +307,7 @@ class _Epilogue:
         if self.gate.dtype != dtype:
             raise NotImplementedError(f'the epilogue gate must have o\'s dtype {dtype}; got {self.gate.dtype}')
         gate = _aligned(self.gate)
-        gamma = self.gamma.contiguous() if self.gamma.dtype in (torch.float32, dtype) else self.gamma.float()
+        gamma = _aligned(self.gamma if self.gamma.dtype in (torch.float32, dtype) else self.gamma.float())
         ep = _lib.Epilogue(gate=_ptr(gate), gamma=_ptr(gamma), gamma_dtype=_DTYPES[gamma.dtype], eps=self.eps)
         return ep, (gate, gamma)
 
@@ -560,3 +560,54 @@ def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = T
                       output_final_state=True, cu_seqlens=cu_seqlens, inplace_final_state=True, fusion=fz,
                       epilogue=ep, conv=_ShortConv(conv_weights, conv_cache))
     return o
+
+
+def causal_conv1d(x, weight, bias=None, residual=None, initial_state=None, output_final_state=False,
+                  activation=None, cu_seqlens=None, conv_cache=None):
+    """The short causal depthwise conv over the sequence, with the activation
+    (opt.py:15-100): fla's causal_conv1d as the reference calls it
+    (opt.py:73-77, ``causal_conv1d(x, w, activation='silu')``), one HIP pass.
+
+    x: (B, T, D) (B = 1 with cu_seqlens); weight: (D, K) or (D, 1, K), K <= 8;
+    activation: None, 'silu' or 'swish'.  Returns (y, final_state).
+    conv_cache: (N, K, D) in x's dtype, the module's decode cache layout
+    (linear_attention.py:929-941): the conv continues from it, and it is
+    advanced in place to the last K inputs (the cached conv of a multi-token
+    decode_step).  output_final_state without conv_cache returns a new
+    (N, K, D) cache; with it, the advanced conv_cache itself.  fla's own
+    initial_state layout (N, D, K), bias and residual are not implemented."""
+    if bias is not None or residual is not None or initial_state is not None:
+        raise NotImplementedError('causal_conv1d: bias, residual and fla-layout initial_state are not '
+                                  'implemented (pass the (N, K, D) cache as conv_cache)')
+    if activation not in (None, 'silu', 'swish'):
+        raise NotImplementedError(f'causal_conv1d: activation {activation!r} (None, silu, swish)')
+    _check_device(x, weight, cu_seqlens, conv_cache)
+    _check_grad(x, weight)
+    assert x.dim() == 3, f'x must be (B, T, D); got {tuple(x.shape)}'
+    if x.dtype not in _DTYPES:
+        raise NotImplementedError(f'x must be one of {list(_DTYPES)}; got {x.dtype}')
+    B, T, D = x.shape
+    K = weight.shape[-1]
+    w = weight.reshape(D, K)
+    w = w.contiguous() if w.dtype in (torch.float32, x.dtype) else w.float().contiguous()
+    if cu_seqlens is not None:
+        assert B == 1, f'packed varlen input (cu_seqlens) has batch 1, got {B}'
+        cu = cu_seqlens.to(torch.int32).contiguous()
+        N = cu.numel() - 1
+    else:
+        cu, N = None, B
+    xa = _aligned(x)
+    y = torch.empty_like(xa)
+    st_in = st_out = None
+    if conv_cache is not None:
+        assert conv_cache.shape == (N, K, D), f'conv_cache must be {(N, K, D)}; got {tuple(conv_cache.shape)}'
+        assert conv_cache.dtype == x.dtype and conv_cache.is_contiguous() and conv_cache.data_ptr() % 16 == 0, \
+            'conv_cache is advanced in place: contiguous, aligned, in x\'s dtype'
+        st_in = st_out = conv_cache
+    elif output_final_state:
+        st_out = torch.empty(N, K, D, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(x.device):
+        _lib.check(_lib.load().vgdr_causal_conv1d(_DTYPES[x.dtype], _ptr(xa), _ptr(w), _DTYPES[w.dtype], _ptr(st_in),
+                                                  _ptr(y), _ptr(st_out), _ptr(cu), B, T, D, N, K,
+                                                  0 if activation is None else 1, _stream(x.device)))
+    return y, (st_out if output_final_state else None)
