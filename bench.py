@@ -30,6 +30,11 @@ Also reported on the same line:
                 dk=dv=128) for each of 24 layer states (1.5 GB), the 24 launches
                 replayed from a HIP graph; per-layer time in algorithmic GB/s
                 (132,104 B per sequence-head) over 8 TB/s
+  layer_kernels the layer's other kernels: the short conv + SiLU over one
+                projection and the RMSNorm x SiLU(gate) output epilogue at the
+                340M prefill shape (GB/s over HBM peak), and the fully fused
+                decode step (conv + caches, L2 norm, beta sigmoid, recurrence,
+                epilogue) at the decode shape
   kda, varlen   KDA prefill (B=4 T=8192 H=8) and packed GDN prefill (32
                 segments U[128, 8192], H=16) tokens/s and TFLOP/s
   cpu_baseline  the oracle's torch fp32 chunk form (the reference's CPU path)
@@ -152,6 +157,85 @@ def bench_decode(torch, ops, workloads, steps, warmup, B=64, H=16, layers=24):
     return dict(avg_us=per_layer_ms * 1e3, GBs=byts / (per_layer_ms * 1e-3) / 1e9, bytes=byts)
 
 
+def _event_us(torch, fn, steps, warmup):
+    """Mean event-timed microseconds of fn() over `steps` back-to-back calls."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for i in range(steps):
+        fn(i)
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps * 1e3
+
+
+def bench_layer_kernels(torch, ops, workloads, steps, warmup):
+    """The layer's other kernels at the 340M shape (B8 T4096 H8 dk=dv=128):
+    the short conv + SiLU over one projection (D = 1024, K = 4) and the
+    RMSNorm x SiLU(gate) output epilogue, each over three rotating input
+    copies; and the fused decode step (conv + SiLU with its caches, L2 norm,
+    beta sigmoid, recurrence, epilogue) at the decode shape (B64 H16), 24
+    rotating layers replayed from a HIP graph."""
+    import torch.nn.functional as F
+    g = torch.Generator(device='cpu').manual_seed(11)
+    B, T, H, D, K = 8, 4096, 8, 128, 4
+    xs = [torch.randn(B, T, H * D, generator=g).bfloat16().cuda() for _ in range(3)]
+    w = (0.5 * torch.randn(H * D, 1, K, generator=g)).cuda()
+    conv_us = _event_us(torch, lambda i: ops.causal_conv1d(xs[i % 3], w, activation='silu'), steps, warmup)
+    conv_bytes = 2 * B * T * H * D * 2
+    os_ = [torch.randn(B, T, H, D, generator=g).bfloat16().cuda() for _ in range(3)]
+    gs = [torch.randn(B, T, H, D, generator=g).bfloat16().cuda() for _ in range(3)]
+    gamma = (torch.rand(D, generator=g) + 0.5).bfloat16().cuda()
+    ng_us = _event_us(torch, lambda i: ops.rms_norm_gated(os_[i % 3], gs[i % 3], gamma), steps, warmup)
+    ng_bytes = 3 * B * T * H * D * 2
+    del xs, os_, gs
+    # decode: every producer and the epilogue fused, 24 layers
+    Bd, Hd, layers = 64, 16, 24
+    Dd = Hd * D
+    states = [torch.randn(Bd, Hd, D, D, generator=g).cuda() for _ in range(layers)]
+    caches = [[torch.randn(Bd, K, Dd, generator=g).bfloat16().cuda() for _ in range(3)] for _ in range(layers)]
+    cw = [(0.5 * torch.randn(Dd, 1, K, generator=g)).cuda() for _ in range(3)]
+    qp, kp, vp = (torch.randn(Bd, 1, Dd, generator=g).bfloat16().cuda() for _ in range(3))
+    gl = F.logsigmoid(torch.randn(Bd, 1, Hd, generator=g) + 4.0).cuda()
+    bl = torch.randn(Bd, 1, Hd, generator=g).cuda()
+    og = [torch.randn(Bd, 1, Hd, D, generator=g).bfloat16().cuda() for _ in range(layers)]
+
+    def step_all():
+        for i in range(layers):
+            ops.hip_decode_step(qp, kp, vp, gl, bl, states[i], scale=D ** -0.5, conv_weights=cw,
+                                conv_cache=caches[i], beta_logits=True, out_gate=og[i], out_norm_weight=gamma)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step_all()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step_all()
+    _, ms = time_steps(torch, lambda i: graph.replay(), max(3, steps // 3), max(2, warmup // 2), 1)
+    dec_us = statistics.mean(ms) / layers * 1e3
+    # per (sequence, head): the plain step's bytes (state read and written, q k v o, g, beta), the three
+    # conv caches read and written (K rows of the head's channels each), the epilogue gate row
+    dec_bytes = Bd * Hd * (DECODE_BYTES_PER_SEQ_HEAD + 3 * 2 * K * D * 2 + D * 2)
+    del graph, states, caches
+    return {
+        'short_conv': {'workload': 'causal_conv1d + SiLU, B8 T4096 D1024 K4 bf16', 'us': round(conv_us, 2),
+                       'achieved_GBs': round(conv_bytes / conv_us / 1e3, 1),
+                       'frac_hbm': round(conv_bytes / conv_us / 1e3 / PEAK_HBM_GBS, 4)},
+        'output_epilogue': {'workload': 'rms_norm_gated, B8 T4096 H8 dv128 bf16', 'us': round(ng_us, 2),
+                            'achieved_GBs': round(ng_bytes / ng_us / 1e3, 1),
+                            'frac_hbm': round(ng_bytes / ng_us / 1e3 / PEAK_HBM_GBS, 4)},
+        'decode_step_fused': {'workload': 'vgdr_decode_step (conv + caches, L2 norm, beta sigmoid, recurrence, '
+                                          'epilogue) B64 H16 dk=dv=128 K4, 24 layers graph-replayed',
+                              'us_per_step': round(dec_us, 2), 'achieved_GBs': round(dec_bytes / dec_us / 1e3, 1),
+                              'frac_hbm': round(dec_bytes / dec_us / 1e3 / PEAK_HBM_GBS, 4)},
+    }
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's torch fp32 chunk form over the full headline workload."""
     from oracle import gdr
@@ -203,6 +287,8 @@ def main():
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--prefill-only', action='store_true', help='only the headline prefill (for profiling)')
     ap.add_argument('--decode-only', action='store_true', help='only the decode step (for profiling)')
+    ap.add_argument('--layer-only', action='store_true',
+                    help='only the short conv, output epilogue and fused decode step (for profiling)')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a plain 1 GiB device copy (x5): the reference point that scales '
                          'rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes')
@@ -226,6 +312,9 @@ def main():
         print(json.dumps({'calibrate_copy_bytes': src.numel() * 4, 'launches': 5}), flush=True)
         return
 
+    if args.layer_only:
+        print(json.dumps(bench_layer_kernels(torch, ops, workloads, args.steps, args.warmup)), flush=True)
+        return
     if args.decode_only:
         dec = bench_decode(torch, ops, workloads, args.steps, args.warmup)
         print(json.dumps({'decode_us_per_layer': round(dec['avg_us'], 2), 'achieved_GBs': round(dec['GBs'], 1)}),
@@ -242,6 +331,8 @@ def main():
                            'peak_GBs': PEAK_HBM_GBS, 'frac': round(dec['GBs'] / PEAK_HBM_GBS, 4),
                            'bytes_per_step': dec['bytes'],
                            'traffic': measured_traffic('decode_b64_h16', 'recurrent')}
+        log('[bench] layer kernels: short conv, output epilogue, fused decode step')
+        extra['layer_kernels'] = bench_layer_kernels(torch, ops, workloads, args.steps, args.warmup)
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
             r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))
