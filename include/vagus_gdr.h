@@ -235,6 +235,19 @@ int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta,
                                 float scale, const vgdr_fusion *fusion, const vgdr_epilogue *epilogue,
                                 hipStream_t stream);
 
+/* vgdr_recurrent_fwd with an explicit write vector w [n_tokens, H, dk] (dtype)
+ * in place of beta_t k_t: the asymmetric delta rule
+ *     S_t = Diag(a_t) S_{t-1} + w_t (v_t - k_t^T Diag(a_t) S_{t-1})^T
+ * of recurrent_scan(..., w=w) (linear_attention.py:161-170, :185-188; the
+ * write a Kalman gain produces, KalmanDeltaNet).  No beta; fusion as in
+ * vgdr_recurrent_fwd_fused (the q, k L2 norm, the KDA gate activation). */
+int vgdr_recurrent_fwd_w(int dtype, int gate_kind,
+                         const void *q, const void *k, const void *v, const void *w,
+                         const float *g, void *o, const float *initial_state, float *final_state,
+                         const int32_t *cu_seqlens,
+                         int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                         float scale, const vgdr_fusion *fusion, hipStream_t stream);
+
 /* The decode step of GatedDeltaNet.decode_step from the projections to the
  * input of W_o (linear_attention.py:918-952 with _heads :737-747 and _output
  * :814-825), in one kernel per call: with `conv` (NULL = none), q, k, v are

@@ -14,9 +14,9 @@ beta_t (linear_attention.py:8-11):
 
 Functions and the reference lines they follow:
 
-    recurrent       linear_attention.py:161-195   the definition
+    recurrent       linear_attention.py:161-195   the definition (with the asymmetric write w)
     chunk_scalar    linear_attention.py:237-309   WY chunk form, scalar / no gate
-    chunk_vector    linear_attention.py:312-425   WY chunk form, per-channel gate
+    chunk_vector    linear_attention.py:312-425   WY chunk form, per-channel gate (and w)
     chunk           linear_attention.py:251-252   dispatch on g.dim()
     varlen          (no reference counterpart)    per-segment loop over cu_seqlens
     chunk_table     (no reference counterpart)    integer chunk / schedule table
@@ -68,14 +68,17 @@ def compute_dtype(x: torch.Tensor) -> torch.dtype:
 # the definition
 # ---------------------------------------------------------------------------
 
-def recurrent(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True):
+def recurrent(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True, w=None):
     """Token-by-token recurrence (linear_attention.py:161-195).
 
     Per step: decay the key rows of S (scalar or per channel), read what S
     returns for k_t, write beta_t k_t (v_t - k_t^T S)^T (or k_t v_t^T without
     the delta rule), then read out o_t = scale q_t^T S *after* the write.
+    w (B, L, H, dk): explicit write vectors in place of beta_t k_t, the
+    asymmetric delta rule S <- S + w_t (v_t - k_t^T S)^T (:164-170, :185-188).
     L == 0 returns an empty o and S0 unchanged (as a copy in compute dtype).
     """
+    assert w is None or delta, 'an explicit write vector needs the delta rule'
     B, L, H, dk = q.shape
     dv = v.shape[-1]
     ct = compute_dtype(q)
@@ -93,7 +96,7 @@ def recurrent(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True):
         kt, vt = kc[:, t], vc[:, t]                # (B, H, dk), (B, H, dv)
         if delta:
             read = torch.matmul(kt.unsqueeze(-2), S).squeeze(-2)          # k_t^T S  (B, H, dv)
-            wt = kt * beta[:, t].to(ct).unsqueeze(-1)
+            wt = kt * beta[:, t].to(ct).unsqueeze(-1) if w is None else w[:, t].to(ct)
             S = S + wt.unsqueeze(-1) * (vt - read).unsqueeze(-2)
         else:
             S = S + kt.unsqueeze(-1) * vt.unsqueeze(-2)
@@ -184,7 +187,7 @@ def chunk_scalar(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
 
 
 def chunk_vector(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
-                 chunk_size: int = 64):
+                 chunk_size: int = 64, w=None):
     """WY chunk form for a per-channel gate g (B, L, H, dk) (linear_attention.py:312-425).
 
     Every inner product becomes a gated one,
@@ -196,7 +199,13 @@ def chunk_vector(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
         S' <- G_C (.) S + (K * G_C / G_j)^T U~     (G_C scales the key rows of S)
     Without the delta rule U~ = V.  The pairwise exponent tensor is built one
     chunk at a time.
+
+    w (B, L, H, dk): explicit write vectors (the asymmetric delta rule,
+    :340-353, :389-396): k stays in the reading slot and w takes the writing
+    slot, M_ij = <k_i, w_j>_g (j < i), (I + M) W = K * G, (I + M) U = V,
+    A_ij = <q_i, w_j>_g, and the state update writes with W * G_C / G_j.
     """
+    assert w is None or delta, 'an explicit write vector needs the delta rule'
     B, L, H, dk = q.shape
     dv = v.shape[-1]
     C = chunk_size
@@ -207,8 +216,9 @@ def chunk_vector(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
     kc = _blocks(_pad_tokens(k.to(ct), pad), N, C)
     vc = _blocks(_pad_tokens(v.to(ct), pad), N, C)
     gam = _blocks(_pad_tokens(g.to(ct), pad), N, C).cumsum(3)              # (B, H, N, C, dk)
-    if delta:
+    if delta and w is None:
         bt = _blocks(_pad_tokens(beta.to(ct), pad), N, C)
+    wc = None if w is None else _blocks(_pad_tokens(w.to(ct), pad), N, C)
     lower = torch.ones(C, C, dtype=torch.bool).tril()
     strict = lower.tril(-1)
     eye = torch.eye(C, dtype=ct)
@@ -225,8 +235,14 @@ def chunk_vector(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
         def gated(x, y):
             return torch.einsum('bhic,bhijc,bhjc->bhij', x, E, y)
 
-        A = gated(Qn, Kn)
-        if delta:
+        Wr = Kn if wc is None else wc[:, :, n]                             # the writing slot
+        A = gated(Qn, Wr)
+        if wc is not None:
+            M = gated(Kn, Wr) * strict
+            W = torch.linalg.solve_triangular(eye + M, Kn * G, upper=False, unitriangular=True)
+            U = torch.linalg.solve_triangular(eye + M, Vn, upper=False, unitriangular=True)
+            Ut = U - torch.matmul(W, S)
+        elif delta:
             bn = bt[:, :, n].unsqueeze(-1)
             M = bn * gated(Kn, Kn) * strict
             W = torch.linalg.solve_triangular(eye + M, bn * (Kn * G), upper=False, unitriangular=True)
@@ -235,7 +251,7 @@ def chunk_vector(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True,
         else:
             Ut = Vn
         out.append(torch.matmul(Qn * G, S) + torch.matmul(A, Ut))
-        S = G[:, :, -1, :, None] * S + torch.matmul((Kn * Gtail).transpose(-1, -2), Ut)
+        S = G[:, :, -1, :, None] * S + torch.matmul((Wr * Gtail).transpose(-1, -2), Ut)
     o = torch.stack(out, dim=2) if N else torch.zeros(B, H, 0, C, dv, dtype=ct)
     o = o.permute(0, 2, 3, 1, 4).reshape(B, N * C, H, dv)[:, :L]
     return o.to(q.dtype), S

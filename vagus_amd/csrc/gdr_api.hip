@@ -272,15 +272,20 @@ int vgdr_chunk_prep_fused(VGDR_CHUNK_ARGS_FUSED) {
 #undef VGDR_CHUNK_PASS_NOFUSION
 #undef VGDR_CHUNK_PASS_FUSED
 
-int vgdr_decode_step(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
-                     const float *g, const float *beta, void *o, const float *initial_state, float *final_state,
-                     const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
-                     int64_t n_seqs, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
-                     const vgdr_epilogue *epilogue, hipStream_t stream) {
+namespace {
+
+// every token-by-token entry point: validation, then one recurrent_kernel launch
+int recurrent_call(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                   const void *w, const float *g, const float *beta, void *o, const float *initial_state,
+                   float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H, int64_t dk,
+                   int64_t dv, int64_t n_seqs, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
+                   const vgdr_epilogue *epilogue, hipStream_t stream) {
     g_err[0] = 0;
-    int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, use_delta, q, k, v, g, beta, o,
+    // with an explicit write vector, beta is not read
+    int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, w ? 0 : use_delta, q, k, v, g, beta, o,
                           cu_seqlens, B, T, H, dk, dv, n_seqs);
     if (rc) return rc;
+    if (w && !use_delta) return fail(VGDR_ERR_INVALID, "vgdr_recurrent_fwd: an explicit write vector needs the delta rule");
     vgdr::Fusion fz;
     rc = check_fusion("vgdr_recurrent_fwd", fusion, dtype, gate_kind, use_delta, false, fz);
     if (rc) return rc;
@@ -311,8 +316,37 @@ int vgdr_decode_step(int dtype, int gate_kind, int use_delta, const void *q, con
     p.fz = fz;
     p.ep = ep;
     p.cv = cv;
+    p.w = w;
     return hip_status(vgdr::recurrent_fwd(dtype, (int)dk, (int)dv, gate_kind == VGDR_GATE_VECTOR, p, stream),
                       "vgdr_recurrent_fwd launch");
+}
+
+}  // namespace
+
+int vgdr_decode_step(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                     const float *g, const float *beta, void *o, const float *initial_state, float *final_state,
+                     const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                     int64_t n_seqs, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
+                     const vgdr_epilogue *epilogue, hipStream_t stream) {
+    return recurrent_call(dtype, gate_kind, use_delta, q, k, v, nullptr, g, beta, o, initial_state, final_state,
+                          cu_seqlens, B, T, H, dk, dv, n_seqs, scale, fusion, conv, epilogue, stream);
+}
+
+int vgdr_recurrent_fwd_w(int dtype, int gate_kind, const void *q, const void *k, const void *v, const void *w,
+                         const float *g, void *o, const float *initial_state, float *final_state,
+                         const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                         int64_t n_seqs, float scale, const vgdr_fusion *fusion, hipStream_t stream) {
+    if (B * T > 0 && !w) {
+        g_err[0] = 0;
+        return fail(VGDR_ERR_INVALID, "vgdr_recurrent_fwd_w: w is required");
+    }
+    if (fusion && fusion->beta_sigmoid) {
+        g_err[0] = 0;
+        return fail(VGDR_ERR_INVALID, "vgdr_recurrent_fwd_w: there is no beta to activate with an explicit w");
+    }
+    static const char dummy = 0;           // w for an empty call: never read
+    return recurrent_call(dtype, gate_kind, 1, q, k, v, w ? w : &dummy, g, nullptr, o, initial_state, final_state,
+                          cu_seqlens, B, T, H, dk, dv, n_seqs, scale, fusion, nullptr, nullptr, stream);
 }
 
 int vgdr_recurrent_fwd_epilogue(int dtype, int gate_kind, int use_delta, const void *q, const void *k,

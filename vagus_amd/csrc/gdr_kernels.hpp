@@ -103,6 +103,7 @@ struct RecParams {
     Fusion fz;
     Epilogue ep;                  // applied to o before it is stored
     ShortConv cv;                 // applied to q, k, v where they are read
+    const void *w;                // [n_tokens, H, dk] write vectors in place of beta k, or NULL
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.

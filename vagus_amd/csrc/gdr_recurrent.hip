@@ -58,13 +58,15 @@ __device__ __forceinline__ float conv_silu(const E *x, E *cache, const void *w, 
     return EL::to_f(EL::from_f(y * sigmoidf_(y)));
 }
 
-// MODE bit 0: the output epilogue; bit 1: the short conv.  Both are template
-// choices: as run-time branches they add registers to every variant (the GDN
-// kernel fills the chip in one pass only within 128 VGPRs).
+// MODE bit 0: the output epilogue; bit 1: the short conv; bit 2: an explicit
+// write vector w_t in place of beta_t k_t (the asymmetric delta rule,
+// linear_attention.py:161-170, :185-188).  All are template choices: as
+// run-time branches they add registers to every variant (the GDN kernel fills
+// the chip in one pass only within 128 VGPRs).
 template <int DK, int DV, typename E, int GATE, int MODE>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATE == 2 ? 1 : 4)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATE == 2 || (MODE & 4) ? 1 : 4)))
 recurrent_kernel(const RecParams p) {
-    constexpr bool EPI = MODE & 1, CONV = MODE & 2;
+    constexpr bool EPI = MODE & 1, CONV = MODE & 2, WR = MODE & 4;
     constexpr int NT = 256;
     constexpr int NCG = DV / 4;             // column groups (float4 each)
     constexpr int NRG = NT / NCG;           // row groups
@@ -81,6 +83,7 @@ recurrent_kernel(const RecParams p) {
     __shared__ float redqk[NWV];
     __shared__ float nrm[NWV][2];           // fused L2 norm: per-wave sums of q^2, k^2
     __shared__ float sc[2];                 // decay (scalar gate), beta
+    __shared__ __attribute__((aligned(16))) float wsv[WR ? DK : 4];    // the write vector w_t
     __shared__ __attribute__((aligned(16))) float gts[EPI ? DV : 4];   // epilogue: output gate of the token
     __shared__ __attribute__((aligned(16))) float gms[EPI ? DV : 4];   // epilogue: RMSNorm weight
 
@@ -163,6 +166,7 @@ recurrent_kernel(const RecParams p) {
         if (own) {
             qs[tid] = qv * p.scale;
             ks[tid] = kv;
+            if constexpr (WR) wsv[tid] = EL::to_f(reinterpret_cast<const E *>(p.w)[qo + tid]);
             if constexpr (GATE == 2) {
                 float gl;
                 if (p.fz.gate_act) {                       // fused gate activation from the pre-activation f
@@ -186,8 +190,8 @@ recurrent_kernel(const RecParams p) {
         }
         if (tid == 0) {
             sc[0] = (GATE == 1 && p.g) ? __expf(p.g[t * H + h]) : 1.f;
-            const float b = p.use_delta ? p.beta[t * H + h] : 0.f;
-            sc[1] = p.use_delta && p.fz.beta_sigmoid ? sigmoidf_(b) : b;
+            const float b = (!WR && p.use_delta) ? p.beta[t * H + h] : 0.f;     // beta may be NULL with w
+            sc[1] = WR ? 1.f : (p.use_delta && p.fz.beta_sigmoid ? sigmoidf_(b) : b);   // w carries the strength
         }
         __syncthreads();
 
@@ -201,7 +205,7 @@ recurrent_kernel(const RecParams p) {
             S[i] *= a;
             kS += ks[r] * S[i];
             qS += qs[r] * S[i];
-            qk += qs[r] * ks[r];
+            qk += qs[r] * (WR ? wsv[r] : ks[r]);
         }
         // reduce over the row groups of this wave (lanes NCG apart share columns)
 #pragma unroll
@@ -259,7 +263,7 @@ recurrent_kernel(const RecParams p) {
             for (int e = 0; e < 4; ++e) og[vo + 4 * cg + e] = EL::from_f(o[e]);
         }
 #pragma unroll
-        for (int i = 0; i < RPT; ++i) S[i] += ks[rg + NRG * i] * u;
+        for (int i = 0; i < RPT; ++i) S[i] += (WR ? wsv[rg + NRG * i] : ks[rg + NRG * i]) * u;
         __syncthreads();                                 // LDS reused by the next token
     }
 
@@ -276,12 +280,12 @@ template <int DK, int DV, typename E, int GATE>
 static hipError_t launch_rec(const RecParams &p, hipStream_t stream) {
     const int64_t blocks = (int64_t)p.n_seqs * p.H;
     if (blocks == 0) return hipSuccess;
-    const int mode = (p.ep.gate ? 1 : 0) | (p.cv.K ? 2 : 0);
+    const int mode = (p.ep.gate ? 1 : 0) | (p.cv.K ? 2 : 0) | (p.w ? 4 : 0);
 #define VGDR_REC(M)                                                                                           \
     case M:                                                                                                    \
         hipLaunchKernelGGL((recurrent_kernel<DK, DV, E, GATE, M>), dim3((unsigned)blocks), dim3(256), 0, stream, p); \
         break;
-    switch (mode) { VGDR_REC(0) VGDR_REC(1) VGDR_REC(2) VGDR_REC(3) }
+    switch (mode) { VGDR_REC(0) VGDR_REC(1) VGDR_REC(2) VGDR_REC(3) VGDR_REC(4) VGDR_REC(5) VGDR_REC(6) VGDR_REC(7) }
 #undef VGDR_REC
     return hipGetLastError();
 }

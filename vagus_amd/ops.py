@@ -378,8 +378,13 @@ class _ShortConv:
 
 def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state,
                cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION, epilogue=None,
-               conv: _ShortConv | None = None):
+               conv: _ShortConv | None = None, w=None):
     dv = v.shape[-1]
+    if w is not None:
+        assert delta, 'an explicit write vector needs the delta rule'
+        assert w.shape == q.shape, f'w must be {tuple(q.shape)} (B, T, H, dk); got {tuple(w.shape)}'
+        if conv is not None or epilogue is not None:
+            raise NotImplementedError('the explicit write vector runs without the short conv and the epilogue')
     if conv is not None and (dv not in _REC_DVS or q.shape[-1] not in _REC_DVS):
         raise NotImplementedError(f'the fused short conv needs dk, dv in {_REC_DVS}; got dk={q.shape[-1]}, dv={dv}')
     if epilogue is not None and dv not in _REC_DVS:
@@ -396,7 +401,7 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
             s0 = None if initial_state is None else initial_state[..., sl]
             o_, s_ = _recurrent(q, k, v[..., sl], g, beta, gate=gate, delta=delta, scale=scale,
                                 initial_state=s0, output_final_state=output_final_state,
-                                cu_seqlens=cu_seqlens, fusion=fusion)
+                                cu_seqlens=cu_seqlens, fusion=fusion, w=w)
             outs.append(o_)
             states.append(s_)
         S = torch.cat(states, -1) if output_final_state else None
@@ -404,8 +409,9 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
             initial_state.copy_(S)
             S = initial_state
         return torch.cat(outs, -1), S
-    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=gate, delta=delta,
-              dv_to=lambda d: next(x for x in _REC_DVS if x >= d), fusion=fusion)
+    # with w the delta rule's strength is in w: no beta is validated or passed
+    c = _Call(q, k, v, g, None if w is not None else beta, initial_state, cu_seqlens, gate=gate,
+              delta=delta and w is None, dv_to=lambda d: next(x for x in _REC_DVS if x >= d), fusion=fusion)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     o = c.new_output()
     in_place = (inplace_final_state and initial_state is not None and not c.padded
@@ -420,7 +426,15 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
     with torch.cuda.device(c.device):
         head = (_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
                 _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), _ptr(c.cu), c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale)
-        if conv is not None:
+        if w is not None:
+            wk = _aligned(_pad_to(w.to(c.dtype), {1: c.dkp}))
+            fz, keep = fusion.struct(c) if fusion.any else (None, None)
+            _lib.check(L.vgdr_recurrent_fwd_w(_DTYPES[c.dtype], c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v),
+                                              _ptr(wk), _ptr(c.g), _ptr(o), _ptr(h0), _ptr(S), _ptr(c.cu), c.B, c.T,
+                                              c.H, c.dkp, c.dvp, c.N, scale,
+                                              None if fz is None else ctypes.byref(fz), _stream(c.device)))
+            del keep
+        elif conv is not None:
             fz, keep = fusion.struct(c) if fusion.any else (None, None)
             ep, keep_ep = (None, None)
             if epilogue is not None:
@@ -508,20 +522,23 @@ def hip_scan(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_size: int
 
 
 def hip_recurrent(q, k, v, g, beta, S0, *, scale: float, delta: bool, cu_seqlens=None,
-                  inplace: bool = False, out_gate=None, out_norm_weight=None, out_norm_eps: float = 1e-6):
+                  inplace: bool = False, out_gate=None, out_norm_weight=None, out_norm_eps: float = 1e-6, w=None):
     """The contract of recurrent_scan (linear_attention.py:161-195) on the GPU:
     token-by-token from S0, returning (o, S).  inplace=True updates S0 itself.
 
     With out_gate (B, T, H, dv) (the W_g x projection, o's dtype) and
     out_norm_weight (dv,) (o_norm's gamma), o is returned through the layer's
     output epilogue RMSNorm(o) * SiLU(out_gate) (GatedDeltaNet._output before
-    W_o, :814-825), computed by the same kernel: the decode step up to W_o."""
+    W_o, :814-825), computed by the same kernel: the decode step up to W_o.
+
+    w (B, T, H, dk): explicit write vectors in place of beta_t k_t (the
+    asymmetric delta rule, recurrent_scan's w, :161-170); beta is then unused."""
     ep = None
     if out_gate is not None or out_norm_weight is not None:
         ep = _Epilogue(out_gate, out_norm_weight, out_norm_eps)
     return _recurrent(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale,
                       initial_state=S0, output_final_state=True, cu_seqlens=cu_seqlens,
-                      inplace_final_state=inplace, epilogue=ep)
+                      inplace_final_state=inplace, epilogue=ep, w=w)
 
 
 def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = True, conv_weights=None,
