@@ -196,6 +196,20 @@ int vgdr_chunk_prep_fused(int dtype, int gate_kind, int use_delta,
                           float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
 
 /*
+ * vgdr_chunk_fwd with an explicit write vector w [n_tokens, H, dk] (16-bit,
+ * 16-byte aligned) in place of beta_t k_t: the asymmetric delta rule of
+ * chunk_scan_vec(..., w=w) (linear_attention.py:312-425, :340-353,
+ * :389-396), on the per-channel-gate path: g [n_tokens, H, dk] fp32 log-decay
+ * (zeros for none).  No beta.  The workspace is vgdr_chunk_workspace_size's
+ * for gate_kind 2.  fusion: the q, k L2 norm and the KDA gate activation.
+ */
+int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, const void *w,
+                     const float *g, void *o, const float *initial_state, float *final_state,
+                     const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                     int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                     float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
+
+/*
  * Token-by-token recurrence.  The decode step is T = 1 with
  * initial_state == final_state (in place), replacing recurrent_scan at
  * linear_attention.py:945-947 and the state.copy_ at :950.  Any T works (the

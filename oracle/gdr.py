@@ -270,8 +270,10 @@ def chunk(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True, chunk_
 def varlen(fn, q, k, v, g, beta, S0, cu_seqlens, **kw):
     """Run `fn` (recurrent / chunk) on each segment [cu[n], cu[n+1]) of a packed
     (1, T, H, d) stream with its own entry state S0[n] (or zeros).  Returns the
-    packed o (1, T, H, dv) and the stacked final states (N, H, dk, dv)."""
+    packed o (1, T, H, dv) and the stacked final states (N, H, dk, dv).  A
+    per-token keyword (w) is cut per segment like q."""
     cu = [int(x) for x in torch.as_tensor(cu_seqlens).tolist()]
+    w = kw.pop('w', None)
     assert q.shape[0] == 1, 'packed varlen input has batch 1'
     N = len(cu) - 1
     ct = compute_dtype(q)
@@ -284,7 +286,8 @@ def varlen(fn, q, k, v, g, beta, S0, cu_seqlens, **kw):
         gn = None if g is None else g[:, sl]
         bn = None if beta is None else beta[:, sl]
         if e > s:
-            o, S = fn(q[:, sl], k[:, sl], v[:, sl], gn, bn, s0, **kw)
+            extra = {} if w is None else {'w': w[:, sl]}
+            o, S = fn(q[:, sl], k[:, sl], v[:, sl], gn, bn, s0, **kw, **extra)
         else:
             o = q.new_zeros(1, 0, H, dv)
             S = torch.zeros(1, H, dk, dv, dtype=ct) if s0 is None else s0.to(ct).clone()

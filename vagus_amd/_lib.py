@@ -57,6 +57,8 @@ SIGNATURES = {
                                   _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
     'vgdr_chunk_prep_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                                    _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
+    'vgdr_chunk_fwd_w': (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
+                              _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
     'vgdr_recurrent_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                 _L, _L, _L, _L, _L, _L, _F, _P]),
     'vgdr_recurrent_fwd_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,

@@ -163,11 +163,21 @@ int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_del
                const void *v, const float *g, const float *beta, void *o, const float *initial_state,
                float *final_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B,
                int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
-               const vgdr_fusion *fusion, hipStream_t stream) {
+               const vgdr_fusion *fusion, hipStream_t stream, const void *w = nullptr) {
     g_err[0] = 0;
-    int rc = check_common(fn, dtype, gate_kind, use_delta, q, k, v, g, beta, o, cu_seqlens,
+    // with an explicit write vector, beta is not read
+    int rc = check_common(fn, dtype, gate_kind, w ? 0 : use_delta, q, k, v, g, beta, o, cu_seqlens,
                           B, T, H, dk, dv, n_seqs);
     if (rc) return rc;
+    if (w) {
+        if (dtype == VGDR_F32)
+            return fail(VGDR_ERR_UNSUPPORTED, "%s: the chunked explicit write takes 16-bit q, k, v, w", fn);
+        if (gate_kind != VGDR_GATE_VECTOR)
+            return fail(VGDR_ERR_INVALID, "%s: the chunked explicit write runs with a per-channel g", fn);
+        if (!aligned16(w)) return fail(VGDR_ERR_INVALID, "%s: w must be 16-byte aligned", fn);
+        if (fusion && fusion->beta_sigmoid)
+            return fail(VGDR_ERR_INVALID, "%s: there is no beta to activate with an explicit w", fn);
+    }
     vgdr::Fusion fz;
     rc = check_fusion(fn, fusion, dtype, gate_kind, use_delta, true, fz);
     if (rc) return rc;
@@ -200,6 +210,7 @@ int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_del
     p.use_delta = use_delta ? 1 : 0;
     p.scale = scale;
     p.fz = fz;
+    p.w = w;
     int32_t *table = cu_seqlens ? static_cast<int32_t *>(workspace) : nullptr;
     return hip_status(vgdr::chunk_fwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, p, table, phases, stream),
                       fn);
@@ -266,6 +277,19 @@ int vgdr_chunk_fwd_fused(VGDR_CHUNK_ARGS_FUSED) {
 }
 int vgdr_chunk_prep_fused(VGDR_CHUNK_ARGS_FUSED) {
     return chunk_call("vgdr_chunk_prep_fused", vgdr::CHUNK_PREP, VGDR_CHUNK_PASS_FUSED);
+}
+int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, const void *w, const float *g, void *o,
+                     const float *initial_state, float *final_state, const int32_t *cu_seqlens, void *workspace,
+                     int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                     float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream) {
+    if (B * T > 0 && !w) {
+        g_err[0] = 0;
+        return fail(VGDR_ERR_INVALID, "vgdr_chunk_fwd_w: w is required");
+    }
+    static const char dummy[16] __attribute__((aligned(16))) = {};     // w for an empty call: never read
+    return chunk_call("vgdr_chunk_fwd_w", vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, dtype, VGDR_GATE_VECTOR, 1, q, k, v,
+                      g, nullptr, o, initial_state, final_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk,
+                      dv, n_seqs, scale, chunk_size, fusion, stream, w ? w : dummy);
 }
 #undef VGDR_CHUNK_ARGS
 #undef VGDR_CHUNK_ARGS_FUSED

@@ -255,19 +255,25 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // ===========================================================================
 // chunk_prep_kernel: per (chunk, head) TE and A
 // ===========================================================================
-template <int DK, int CH, typename E, int GATE>
+template <int DK, int CH, typename E, int GATE, bool WR = false>
 struct PrepLayout {
     static constexpr int PF = CH + 4, PG = DK + 4;
-    static constexpr int STAGE = 2 * CH * DK * (int)sizeof(E);    // K, Q rows (swizzled)
+    static constexpr int STAGE = (WR ? 3 : 2) * CH * DK * (int)sizeof(E);    // K, Q (and W) rows (swizzled)
     static constexpr int SOLVE = 2 * CH * PF * 4;                  // M, T (reuse the stage)
     static constexpr int UNION = cmax(STAGE, SOLVE);
 };
 
-template <int DK, int CH, typename E, int GATE>
+// WR: an explicit write vector w_t in place of beta_t k_t (the asymmetric
+// delta rule, linear_attention.py:340-353, :389-396), per-channel gate only.
+// W rows take the writing slot: M_ij = <k_i, w_j>_g, A_ij = scale <q_i, w_j>_g,
+// TE = (I + M)^-1 (no beta), and the third gated tile is W * Gend; the state
+// kernel is the per-channel one, unchanged.
+template <int DK, int CH, typename E, int GATE, bool WR = false>
 __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
+    static_assert(!WR || GATE == 2, "the explicit write runs on the per-channel-gate path");
     using EL = Elem<E>;
     using F = typename EL::frag;
-    using L = PrepLayout<DK, CH, E, GATE>;
+    using L = PrepLayout<DK, CH, E, GATE, WR>;
     using SK = Swz<E, DK>;
     constexpr int NT = 256, NW = 4, NB = CH / 16, NKB = DK / 16, PF = L::PF, PG = L::PG;
     constexpr int NL = NB * (NB + 1) / 2;
@@ -281,6 +287,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     __shared__ int flag[4];
     E *Kst = reinterpret_cast<E *>(smem);
     E *Qst = Kst + CH * DK;
+    E *Wst = WR ? Qst + CH * DK : Kst;                          // the writing slot: W rows, or K
     float *Mf = reinterpret_cast<float *>(smem);                // after the products are done
     float *Tf = Mf + CH * PF;
 
@@ -325,7 +332,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     float beta_v = 0.f, g_v = 0.f;
     if (wave == 0) {
         const int row = lane < clen ? lane : 0;
-        if (p.use_delta) beta_v = p.beta[(t0 + row) * H + h];
+        if (!WR && p.use_delta) beta_v = p.beta[(t0 + row) * H + h];
         if constexpr (GATE != 2)
             if (p.g) g_v = p.g[(t0 + row) * H + h];
     }
@@ -353,9 +360,13 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         });
     }
     RegRows<E, CH, DK, NT> rk, rq;
+    RegRows<E, CH, DK, NT> rw;                                  // W rows (WR only)
     rk.load(kg, sqk, clen, DK, tid);
+    if constexpr (WR)
+        rw.load(reinterpret_cast<const E *>(p.w) + t0 * sqk + (int64_t)h * DK, sqk, clen, DK, tid);
     rq.load(qg, sqk, clen, DK, tid);
-    if (wave == 0 && lane < CH) bet[lane] = lane < clen ? (fz.beta_sigmoid ? sigmoidf_(beta_v) : beta_v) : 0.f;
+    if (wave == 0 && lane < CH)
+        bet[lane] = lane < clen ? (WR ? 1.f : (fz.beta_sigmoid ? sigmoidf_(beta_v) : beta_v)) : 0.f;
     if constexpr (GATE == 2) {
         if (fz.gate_act) {                                      // g = act(f + dt_bias) per channel
             const float a_log = fz.A_log[h];
@@ -404,6 +415,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     }
     rk.store(Kst, tid);
     rq.store(Qst, tid);
+    if constexpr (WR) rw.store(Wst, tid);
     __syncthreads();
     if constexpr (GATE != 2) {
         // the state kernel's row factors (ChunkBlock)
@@ -440,7 +452,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
 #pragma unroll
         for (int kt = 0; kt < NKB; ++kt) {
             const int cc = 16 * kt + 4 * g4;
-            a[kt] = ld_frag<E>(Kst + SK::at(jrow, cc));
+            a[kt] = ld_frag<E>(Wst + SK::at(jrow, cc));           // the j side: the writing slot
             bq[kt] = ld_frag<E>(Qst + SK::at(irow, cc));
             bk[kt] = ld_frag<E>(Kst + SK::at(irow, cc));
         }
@@ -475,7 +487,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
                 if (jt <= irow) {
                     for (int cc = 0; cc < DK; cc += 4) {
                         const f32x4 e = exp4(ld4(gam + irow * PG + cc) - ld4(gam + jt * PG + cc));
-                        const f32x4 kj = EL::tof(ld_frag<E>(Kst + SK::at(jt, cc))) * e;
+                        const f32x4 kj = EL::tof(ld_frag<E>(Wst + SK::at(jt, cc))) * e;
                         const f32x4 yq = EL::tof(ld_frag<E>(Qst + SK::at(irow, cc))) * kj;
                         const f32x4 yk = EL::tof(ld_frag<E>(Kst + SK::at(irow, cc))) * kj;
                         sq += yq[0] + yq[1] + yq[2] + yq[3];
@@ -521,7 +533,12 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             E *row = tg + t * DK + 8 * pu;
             *reinterpret_cast<F2 *>(row) = EL::cvt2(k0 * e0, k1 * e1);
             *reinterpret_cast<F2 *>(row + CH * DK) = EL::cvt2(q0 * e0 * p.scale, q1 * e1 * p.scale);
-            *reinterpret_cast<F2 *>(row + 2 * CH * DK) = EL::cvt2(k0 * d0, k1 * d1);
+            if constexpr (WR) {                                  // the state update writes with W * Gend
+                const f32x4 w0 = EL::tof(ld_frag<E>(Wst + SK::at(t, c0))), w1 = EL::tof(ld_frag<E>(Wst + SK::at(t, c1)));
+                *reinterpret_cast<F2 *>(row + 2 * CH * DK) = EL::cvt2(w0 * d0, w1 * d1);
+            } else {
+                *reinterpret_cast<F2 *>(row + 2 * CH * DK) = EL::cvt2(k0 * d0, k1 * d1);
+            }
         }
         float *gcb = reinterpret_cast<float *>(blk_base + CB::GOFF);
         for (int cc = tid; cc < DK; cc += NT) gcb[cc] = __expf(gam[(CH - 1) * PG + cc]);
@@ -1425,9 +1442,21 @@ static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hip
 template <int DK, int CH, typename E, int GATE>
 static hipError_t launch_chunk(const ChunkParams &p, int nw, int phases, hipStream_t stream) {
     const int64_t prep_blocks = (int64_t)p.n_chunk_slots * p.H;
-    if ((phases & CHUNK_PREP) && prep_blocks > 0)
-        hipLaunchKernelGGL((chunk_prep_kernel<DK, CH, E, GATE>), dim3((unsigned)prep_blocks), dim3(256), 0,
-                           stream, p);
+    if ((phases & CHUNK_PREP) && prep_blocks > 0) {
+        bool done = false;
+        if constexpr (GATE == 2 && sizeof(E) == 2) {
+            if (p.w) {
+                hipLaunchKernelGGL((chunk_prep_kernel<DK, CH, E, GATE, true>), dim3((unsigned)prep_blocks), dim3(256),
+                                   0, stream, p);
+                done = true;
+            }
+        }
+        if (!done) {
+            if (p.w) return hipErrorInvalidValue;             // the API admits w only on the 16-bit per-channel path
+            hipLaunchKernelGGL((chunk_prep_kernel<DK, CH, E, GATE>), dim3((unsigned)prep_blocks), dim3(256), 0,
+                               stream, p);
+        }
+    }
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
     const int64_t state_blocks = (units + 7) / 8 * 8 * p.n_tiles;
     if ((phases & CHUNK_STATE) && state_blocks > 0) {

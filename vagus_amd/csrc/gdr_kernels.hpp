@@ -85,6 +85,7 @@ struct ChunkParams {
     int use_delta;
     float scale;
     Fusion fz;
+    const void *w;                // [n_tokens, H, dk] write vectors in place of beta k (per-channel gate), or NULL
 };
 
 struct RecParams {

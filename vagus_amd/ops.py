@@ -628,3 +628,44 @@ def causal_conv1d(x, weight, bias=None, residual=None, initial_state=None, outpu
                                                   _ptr(y), _ptr(st_out), _ptr(cu), B, T, D, N, K,
                                                   0 if activation is None else 1, _stream(x.device)))
     return y, (st_out if output_final_state else None)
+
+
+def chunk_scan_vec(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_size: int = 64, w=None,
+                   cu_seqlens=None):
+    """The reference's chunk_scan_vec (linear_attention.py:312-425) on the GPU,
+    including its explicit write vectors: returns (o in q's dtype, final S fp32).
+
+    g: (B, T, H, dk) per-channel log-decay; a (B, T, H) scalar gate or None is
+    taken as the same decay on every channel.  w (B, T, H, dk): write vectors
+    in place of beta_t k_t (the asymmetric delta rule, :340-353, :389-396;
+    beta unused), run chunkwise with 16-bit q, k, v and token by token (the
+    same rule, vgdr_recurrent_fwd_w) in fp32.  Without w it is chunk_kda."""
+    B, T, H, dk = q.shape
+    if g is None:
+        g = torch.zeros(B, T, H, dk, dtype=torch.float32, device=q.device)
+    elif g.dim() == 3:
+        g = g.float().unsqueeze(-1).expand(B, T, H, dk)
+    if w is None:
+        return chunk_scan(q, k, v, g, beta, gate='vector', delta=delta, scale=scale, initial_state=S0,
+                          output_final_state=True, cu_seqlens=cu_seqlens, chunk_size=chunk_size)
+    assert delta, 'an explicit write vector needs the delta rule'
+    assert w.shape == q.shape, f'w must be {tuple(q.shape)} (B, T, H, dk); got {tuple(w.shape)}'
+    if q.dtype == torch.float32:
+        return _recurrent(q, k, v, g, None, gate='vector', delta=True, scale=scale, initial_state=S0,
+                          output_final_state=True, cu_seqlens=cu_seqlens, w=w)
+    c = _Call(q, k, v, g, None, S0, cu_seqlens, gate='vector', delta=False,
+              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+    scale = c.dk ** -0.5 if scale is None else float(scale)
+    wk = _aligned(_pad_to(w.to(c.dtype), {1: c.dkp}))
+    o = c.new_output()
+    S = c.new_state()
+    L = _lib.load()
+    varlen = c.cu is not None
+    nbytes = L.vgdr_chunk_workspace_size(_DTYPES[c.dtype], _lib.VGDR_GATE_VECTOR, c.B, c.T, c.H, c.dkp, c.N,
+                                         int(varlen), int(chunk_size))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+    with torch.cuda.device(c.device):
+        _lib.check(L.vgdr_chunk_fwd_w(_DTYPES[c.dtype], _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(wk), _ptr(c.g), _ptr(o),
+                                      _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws), nbytes, c.B, c.T, c.H, c.dkp, c.dvp,
+                                      c.N, scale, int(chunk_size), None, _stream(c.device)))
+    return c.unpad_o(o), c.unpad_state(S)
