@@ -277,7 +277,13 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     using SK = Swz<E, DK>;
     constexpr int NT = 256, NW = 4, NB = CH / 16, NKB = DK / 16, PF = L::PF, PG = L::PG;
     constexpr int NL = NB * (NB + 1) / 2;
-    constexpr int JPW = (NL + NW - 1) / NW;                    // tile jobs per wave
+    // tile jobs (I, J), J <= I.  With one row block per wave (CH = 64), wave w
+    // takes row block I = w and its tiles J = 0..w: it reads its Q_I, K_I
+    // fragments once instead of once per tile, which cuts the LDS reads of
+    // the products by 40% (they bound this phase when four workgroups share
+    // a CU).  Otherwise the NL tiles go round-robin over the waves.
+    constexpr bool RB = NB == NW;
+    constexpr int JPW = RB ? NB : (NL + NW - 1) / NW;           // tile jobs per wave
 
     __shared__ __attribute__((aligned(16))) char smem[L::UNION];
     __shared__ __attribute__((aligned(16))) float gam[GATE == 2 ? CH * PG : CH];
@@ -439,22 +445,48 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     // Job (I, J) computes X = K_J Y_I^T for Y in {K, Q}; the C layout then
     // holds X[4g + jj][r] = <y_i, k_j> for i = 16I + r, j = 16J + 4g + jj, four
     // consecutive j of row i: exactly the fragment (I, J) of A / M.
+    // job s of this wave -> tile (I, J); false past the wave's last job
+    auto job_ij = [&](int s, int &I, int &J) __attribute__((always_inline)) {
+        if constexpr (RB) {
+            I = wave;
+            J = s;
+            return s <= wave;
+        } else {
+            const int job = wave + NW * s;
+            I = 0;
+            J = job;
+            while (J > I) { J -= I + 1; ++I; }
+            return job < NL;
+        }
+    };
+    F bq_rb[RB ? NKB : 1], bk_rb[RB ? NKB : 1];                 // row block I = wave, read once
+    if constexpr (RB) {
+#pragma unroll
+        for (int kt = 0; kt < NKB; ++kt) {
+            const int cc = 16 * kt + 4 * g4, irow = 16 * wave + r16;
+            bq_rb[kt] = ld_frag<E>(Qst + SK::at(irow, cc));
+            bk_rb[kt] = ld_frag<E>(Kst + SK::at(irow, cc));
+        }
+    }
     f32x4 res_q[JPW], res_k[JPW];
 #pragma unroll
     for (int s = 0; s < JPW; ++s) {
-        const int job = wave + NW * s;
         res_q[s] = res_k[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (job >= NL) continue;
-        int I = 0, J = job;
-        while (J > I) { J -= I + 1; ++I; }
+        int I, J;
+        if (!job_ij(s, I, J)) continue;
         const int jrow = 16 * J + r16, irow = 16 * I + r16;
         F a[NKB], bq[NKB], bk[NKB];
 #pragma unroll
         for (int kt = 0; kt < NKB; ++kt) {
             const int cc = 16 * kt + 4 * g4;
             a[kt] = ld_frag<E>(Wst + SK::at(jrow, cc));           // the j side: the writing slot
-            bq[kt] = ld_frag<E>(Qst + SK::at(irow, cc));
-            bk[kt] = ld_frag<E>(Kst + SK::at(irow, cc));
+            if constexpr (RB) {
+                bq[kt] = bq_rb[kt];
+                bk[kt] = bk_rb[kt];
+            } else {
+                bq[kt] = ld_frag<E>(Qst + SK::at(irow, cc));
+                bk[kt] = ld_frag<E>(Kst + SK::at(irow, cc));
+            }
         }
         bool pairwise = false;
         if constexpr (GATE == 2) {
@@ -546,10 +578,8 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     __syncthreads();                                           // K, Q reads done: M, T reuse the stage
 #pragma unroll
     for (int s = 0; s < JPW; ++s) {
-        const int job = wave + NW * s;
-        if (job >= NL) continue;
-        int I = 0, J = job;
-        while (J > I) { J -= I + 1; ++I; }
+        int I, J;
+        if (!job_ij(s, I, J)) continue;
         st_frag<E>(blk + CH * CH + frag_pos<NB>(I, J, lane), EL::cvt(res_q[s]));
         if (p.use_delta) st4(Mf + (16 * I + r16) * PF + 16 * J + 4 * g4, res_k[s]);
     }
