@@ -277,12 +277,14 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     using SK = Swz<E, DK>;
     constexpr int NT = 256, NW = 4, NB = CH / 16, NKB = DK / 16, PF = L::PF, PG = L::PG;
     constexpr int NL = NB * (NB + 1) / 2;
-    // tile jobs (I, J), J <= I.  With one row block per wave (CH = 64), wave w
-    // takes row block I = w and its tiles J = 0..w: it reads its Q_I, K_I
-    // fragments once instead of once per tile, which cuts the LDS reads of
-    // the products by 40% (they bound this phase when four workgroups share
-    // a CU).  Otherwise the NL tiles go round-robin over the waves.
-    constexpr bool RB = NB == NW;
+    // tile jobs (I, J), J <= I.  With one row block per wave (CH = 64, scalar
+    // gate), wave w takes row block I = w and its tiles J = 0..w: it reads its
+    // Q_I, K_I fragments once instead of once per tile (40% fewer LDS reads in
+    // the products).  The per-channel gate keeps the round-robin: its tiles
+    // carry per-element exponentials, and the 4-tile wave of the row-block
+    // split lengthened the phase (measured: 16k -> 18k cycles, plus the others'
+    // wait at the barrier).  Otherwise the NL tiles go round-robin over the waves.
+    constexpr bool RB = NB == NW && GATE != 2;
     constexpr int JPW = RB ? NB : (NL + NW - 1) / NW;           // tile jobs per wave
 
     __shared__ __attribute__((aligned(16))) char smem[L::UNION];
