@@ -210,6 +210,34 @@ int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, con
                      float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
 
 /*
+ * Backward of the chunked scan, scalar gate (gate_kind 1) or none (0), delta
+ * rule: the gradients the reference's training takes through chunk_scan
+ * (linear_attention.py:237-309, autograd) or fla's chunk_gated_delta_rule
+ * backward (the call at :487-491 with grads enabled).  Inputs as the forward
+ * call had them (q, k already normalised; beta in [0, 1]; initial_state
+ * nullable), plus grad_o [n_tokens, H, dv] in dtype and grad_final_state
+ * [n_seqs, H, dk, dv] fp32 (nullable: zero).  Outputs: grad_q, grad_k
+ * [n_tokens, H, dk], grad_v [n_tokens, H, dv] in dtype; grad_g, grad_beta
+ * [n_tokens, H] fp32 (grad_g unused and nullable without a gate);
+ * grad_initial_state [n_seqs, H, dk, dv] fp32 (nullable: not computed).
+ * The gradients must not alias the inputs.  workspace:
+ * vgdr_chunk_bwd_workspace_size(...) bytes, 16-byte aligned; it holds the
+ * chunk blocks (rebuilt from q, k, g, beta), each chunk's entry state and the
+ * gradient of its exit state.  Same dk, dv, chunk_size and packed-batch
+ * rules as vgdr_chunk_fwd.
+ */
+int64_t vgdr_chunk_bwd_workspace_size(int dtype, int gate_kind, int64_t B, int64_t T, int64_t H, int64_t dk,
+                                      int64_t dv, int64_t n_seqs, int varlen, int chunk_size);
+int vgdr_chunk_bwd(int dtype, int gate_kind,
+                   const void *q, const void *k, const void *v, const float *g, const float *beta,
+                   const float *initial_state, const void *grad_o, const float *grad_final_state,
+                   void *grad_q, void *grad_k, void *grad_v, float *grad_g, float *grad_beta,
+                   float *grad_initial_state,
+                   const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                   int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                   float scale, int chunk_size, hipStream_t stream);
+
+/*
  * Token-by-token recurrence.  The decode step is T = 1 with
  * initial_state == final_state (in place), replacing recurrent_scan at
  * linear_attention.py:945-947 and the state.copy_ at :950.  Any T works (the

@@ -15,6 +15,7 @@ beta_t (linear_attention.py:8-11):
 Functions and the reference lines they follow:
 
     recurrent       linear_attention.py:161-195   the definition (with the asymmetric write w)
+    recurrent_grads linear_attention.py:237-309   gradients of the scan (autograd of the fp64 recurrence)
     chunk_scalar    linear_attention.py:237-309   WY chunk form, scalar / no gate
     chunk_vector    linear_attention.py:312-425   WY chunk form, per-channel gate (and w)
     chunk           linear_attention.py:251-252   dispatch on g.dim()
@@ -35,7 +36,10 @@ v (B, L, H, dv), g (B, L, H) or (B, L, H, dk), beta (B, L, H), S0 (B, H, dk, dv)
 Computation is fp64 when q is fp64, else fp32 (linear_attention.py:157-158);
 o is returned in q.dtype and S in the compute dtype.
 
-How each function is pinned (tests/test_oracle.py): ``recurrent`` against
+How each function is pinned (tests/test_oracle.py): ``recurrent_grads``
+against central finite differences of ``recurrent`` (torch.autograd.gradcheck
+in fp64) and against reverse-mode through the independent chunk form
+``chunk_scalar``; ``recurrent`` against
 closed forms (causal linear attention, pure decay, one-token write, the
 delta-rule overwrite identity) and against an independent dense-matrix
 statement of the update above; the chunk forms against ``recurrent`` at
@@ -102,6 +106,35 @@ def recurrent(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True, w=
             S = S + kt.unsqueeze(-1) * vt.unsqueeze(-2)
         o[:, t] = torch.matmul(qs[:, t].unsqueeze(-2), S).squeeze(-2)
     return o.to(q.dtype), S
+
+
+def recurrent_grads(q, k, v, g, beta, S0, do, dST=None, *, scale: float, delta: bool = True):
+    """Gradients of ``recurrent``'s (o, final S) under the cotangents do (and
+    dST, the final state's; None = zero), by reverse-mode differentiation of
+    the fp64 recurrence: the gradients the reference's training takes through
+    chunk_scan's autograd (linear_attention.py:237-309), which computes the
+    same function.  Returns (dq, dk, dv, dg, dbeta, dS0) in fp64; None for
+    absent inputs (g, beta without the delta rule, S0)."""
+    leaves = [None if x is None else x.detach().double().requires_grad_(True) for x in (q, k, v, g, beta, S0)]
+    o, S = recurrent(*leaves, scale=scale, delta=delta)
+    outs, cots = [o], [do.double()]
+    if dST is not None:
+        outs.append(S)
+        cots.append(dST.double())
+    pairs = [(y, c) for y, c in zip(outs, cots) if y.requires_grad]      # an empty o has no graph
+    inputs = [x for x in leaves if x is not None]
+    if pairs:
+        grads = iter(torch.autograd.grad([y for y, _ in pairs], inputs, [c for _, c in pairs], allow_unused=True))
+    else:
+        grads = iter([None] * len(inputs))
+    res = []
+    for x in leaves:
+        if x is None:
+            res.append(None)
+        else:
+            gx = next(grads)
+            res.append(torch.zeros_like(x) if gx is None else gx)
+    return tuple(res)
 
 
 # ---------------------------------------------------------------------------

@@ -235,3 +235,49 @@ def test_flop_formula_known_answers():
     # the forward third at the benchmark shapes
     assert gdr.chunk_scan_flops(128, 128, 64, True) / 3 == 180224
     assert gdr.chunk_scan_flops(64, 64, 64, True) / 3 == 65536
+
+
+# ---------------------------------------------------------------------------
+# the backward (recurrent_grads)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize('gate', ['none', 'scalar'])
+def test_recurrent_grads_match_finite_differences(gate):
+    """Reverse-mode through the recurrence equals central differences of the
+    forward (gradcheck, fp64) for every input, with an initial state and a
+    cotangent on the final state: a dropped term in any gradient fails."""
+    q, k, v, g, beta, S0 = inputs(B=1, L=6, H=1, dk=3, dv=2, seed=11, gate=gate)
+    gen = torch.Generator().manual_seed(12)
+    do = torch.randn(1, 6, 1, 2, generator=gen, dtype=torch.float64)
+    dST = torch.randn(1, 1, 3, 2, generator=gen, dtype=torch.float64)
+    dq, dk_, dv_, dg, db, dS0 = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=0.7)
+
+    def loss(*xs):
+        qq, kk, vv, bb, ss = xs[:5]
+        gg = xs[5] if gate != 'none' else None
+        o, S = gdr.recurrent(qq, kk, vv, gg, bb, ss, scale=0.7)
+        return (o * do).sum() + (S * dST).sum()
+
+    leaves = [x.clone().requires_grad_(True) for x in (q, k, v, beta, S0) + ((g,) if gate != 'none' else ())]
+    assert torch.autograd.gradcheck(loss, leaves, eps=1e-6, atol=1e-7, rtol=1e-6)
+    # and the function's own gradients are those of that loss
+    ref = torch.autograd.grad(loss(*leaves), leaves)
+    mine = (dq, dk_, dv_, db, dS0) + ((dg,) if gate != 'none' else ())
+    for a, b in zip(mine, ref):
+        assert torch.allclose(a, b, rtol=1e-12, atol=1e-12)
+
+
+@pytest.mark.parametrize('gate', ['none', 'scalar'])
+def test_recurrent_grads_match_chunk_form_gradients(gate):
+    """The same gradients through the independent WY chunk form (triangular
+    solves, decay masks), partial last chunk included."""
+    q, k, v, g, beta, S0 = inputs(B=2, L=37, H=2, dk=8, dv=12, seed=13, gate=gate)
+    gen = torch.Generator().manual_seed(14)
+    do = torch.randn(2, 37, 2, 12, generator=gen, dtype=torch.float64)
+    dST = torch.randn(2, 2, 8, 12, generator=gen, dtype=torch.float64)
+    ref = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=0.5)
+    leaves = [None if x is None else x.clone().requires_grad_(True) for x in (q, k, v, g, beta, S0)]
+    o, S = gdr.chunk_scalar(*leaves, scale=0.5, chunk_size=16)
+    got = torch.autograd.grad([o, S], [x for x in leaves if x is not None], [do, dST])
+    for a, b in zip([x for x in ref if x is not None], got):
+        assert torch.allclose(a, b, rtol=1e-9, atol=1e-10)

@@ -291,6 +291,98 @@ int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, con
                       g, nullptr, o, initial_state, final_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk,
                       dv, n_seqs, scale, chunk_size, fusion, stream, w ? w : dummy);
 }
+
+namespace {
+// workspace of the backward: the forward's (table, blocks), then each chunk's
+// entry state and exit-state gradient (fp32, dk x dv per (chunk, head))
+struct BwdWs {
+    ChunkWs fwd;
+    int64_t hs_off, dhs_off, total;
+};
+BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                 int64_t n_seqs, bool varlen) {
+    BwdWs w{};
+    w.fwd = chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, varlen);
+    const int64_t states = w.fwd.slots * H * dk * dv * 4;
+    w.hs_off = (w.fwd.total + 255) / 256 * 256;
+    w.dhs_off = w.hs_off + (states + 255) / 256 * 256;
+    w.total = states > 0 ? w.dhs_off + states : w.fwd.total;
+    return w;
+}
+}  // namespace
+
+int64_t vgdr_chunk_bwd_workspace_size(int dtype, int gate_kind, int64_t B, int64_t T, int64_t H, int64_t dk,
+                                      int64_t dv, int64_t n_seqs, int varlen, int chunk_size) {
+    if (B < 0 || T < 0 || H <= 0 || n_seqs < 0 || dv < 0) return 0;
+    const int chunk = effective_chunk(dtype, dk, chunk_size);
+    return bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, varlen).total;
+}
+
+int vgdr_chunk_bwd(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
+                   const float *beta, const float *initial_state, const void *grad_o, const float *grad_final_state,
+                   void *grad_q, void *grad_k, void *grad_v, float *grad_g, float *grad_beta,
+                   float *grad_initial_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                   int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
+                   int chunk_size, hipStream_t stream) {
+    const char *fn = "vgdr_chunk_bwd";
+    g_err[0] = 0;
+    int rc = check_common(fn, dtype, gate_kind, 1, q, k, v, g, beta, grad_o, cu_seqlens, B, T, H, dk, dv, n_seqs);
+    if (rc) return rc;
+    if (gate_kind == VGDR_GATE_VECTOR)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: the backward covers the scalar gate and no gate", fn);
+    if (dv <= 0 || dv % 16)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: dv=%lld (must be a positive multiple of 16)", fn, (long long)dv);
+    if (B * T > 0 && (!grad_q || !grad_k || !grad_v || !grad_beta))
+        return fail(VGDR_ERR_INVALID, "%s: grad_q, grad_k, grad_v and grad_beta are required", fn);
+    if (grad_v == v || grad_q == q || grad_k == k)
+        return fail(VGDR_ERR_INVALID, "%s: the gradients must not alias the inputs", fn);
+    const int chunk = effective_chunk(dtype, dk, chunk_size);
+    const BwdWs ws = bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, cu_seqlens != nullptr);
+    if (ws.total > 0 && (!workspace || workspace_bytes < ws.total || !aligned16(workspace)))
+        return fail(VGDR_ERR_INVALID, "%s: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)", fn,
+                    (long long)ws.total, (long long)workspace_bytes, workspace);
+    if (ws.fwd.slots * H > 0x7fffffffLL || (n_seqs * H + 7) / 8 * 8 * ((dv + 31) / 32) > 0x7fffffffLL)
+        return fail(VGDR_ERR_INVALID, "%s: grid too large", fn);
+    char *wsb = static_cast<char *>(workspace);
+    vgdr::ChunkParams f{};
+    f.geo.cu = cu_seqlens;
+    f.geo.T = T;
+    f.geo.n_tokens = B * T;
+    f.geo.n_seqs = (int)n_seqs;
+    f.geo.chunks_per_seq = (int)((T + chunk - 1) / chunk);
+    f.q = q; f.k = k; f.v = v;
+    f.g = gate_kind == VGDR_GATE_NONE ? nullptr : g;
+    f.beta = beta;
+    f.blocks = wsb + ws.fwd.blocks_off;
+    f.H = (int)H;
+    f.DV = (int)dv;
+    f.n_chunk_slots = (int)ws.fwd.slots;
+    f.use_delta = 1;
+    f.scale = scale;
+    vgdr::ChunkBwdParams p{};
+    p.geo = f.geo;
+    p.q = q; p.k = k; p.v = v;
+    p.g = f.g;
+    p.beta = beta;
+    p.dout = grad_o;
+    p.h0 = initial_state;
+    p.dht = grad_final_state;
+    p.dq = grad_q; p.dk = grad_k; p.dv = grad_v;
+    p.dg = f.g ? grad_g : nullptr;
+    p.dbeta = grad_beta;
+    p.dh0 = grad_initial_state;
+    p.blocks = f.blocks;
+    p.hs = reinterpret_cast<float *>(wsb + ws.hs_off);
+    p.dhs = reinterpret_cast<float *>(wsb + ws.dhs_off);
+    p.H = (int)H;
+    p.DV = (int)dv;
+    p.n_chunk_slots = (int)ws.fwd.slots;
+    p.scale = scale;
+    int32_t *table = cu_seqlens ? reinterpret_cast<int32_t *>(wsb) : nullptr;
+    if (f.geo.n_seqs == 0) return VGDR_OK;
+    return hip_status(vgdr::chunk_bwd(dtype, (int)dk, chunk, f, p, table, stream), fn);
+}
+
 #undef VGDR_CHUNK_ARGS
 #undef VGDR_CHUNK_ARGS_FUSED
 #undef VGDR_CHUNK_PASS_NOFUSION

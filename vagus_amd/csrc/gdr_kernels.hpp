@@ -88,6 +88,30 @@ struct ChunkParams {
     const void *w;                // [n_tokens, H, dk] write vectors in place of beta k (per-channel gate), or NULL
 };
 
+// Backward of the chunked scan (scalar gate or none, delta rule).  q, k are the
+// normalised inputs the forward scanned; the gradients come back in the
+// element type (dq, dk, dv) or fp32 (dg, dbeta, dh0).
+struct ChunkBwdParams {
+    SeqGeom geo;
+    const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
+    const float *g;               // [n_tokens, H] or NULL (no gate)
+    const float *beta;            // [n_tokens, H]
+    const void *dout;             // [n_tokens, H, dv] gradient of o
+    const float *h0;              // [n_seqs, H, dk, dv] or NULL
+    const float *dht;             // [n_seqs, H, dk, dv] gradient of the final state, or NULL
+    void *dq, *dk, *dv;           // [n_tokens, H, dk|dv]
+    float *dg;                    // [n_tokens, H] (NULL without a gate)
+    float *dbeta;                 // [n_tokens, H]
+    float *dh0;                   // [n_seqs, H, dk, dv] or NULL
+    const void *blocks;           // chunk_prep's per-(chunk, head) blocks
+    float *hs;                    // [chunk slots, H, dk, dv] each chunk's entry state
+    float *dhs;                   // [chunk slots, H, dk, dv] gradient of each chunk's exit state
+    int H, DV;
+    int n_tiles;                  // dv tiles of the walk kernels (set by the launcher)
+    int n_chunk_slots;
+    float scale;
+};
+
 struct RecParams {
     const void *q, *k, *v;
     const float *g;
@@ -115,6 +139,12 @@ enum { CHUNK_PREP = 1, CHUNK_STATE = 2 };
 hipError_t chunk_fwd(int dtype, int dk, int chunk, int gate_vector, ChunkParams p, int32_t *table, int phases,
                      hipStream_t stream);
 int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H, int64_t dk, int gate_vector);
+
+// The backward: chunk prep (with `fwd`, the same call's forward parameters,
+// writing the blocks p.blocks points at), then the walks and the per-chunk
+// gradients.  table: the packed-batch schedule (as chunk_fwd).
+hipError_t chunk_bwd(int dtype, int dk, int chunk, const ChunkParams &fwd, ChunkBwdParams p, int32_t *table,
+                     hipStream_t stream);
 
 hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
                          hipStream_t stream);

@@ -20,8 +20,10 @@ use_gate_in_kernel with A_log / dt_bias / lower_bound move the producers'
 elementwise work into the kernels (struct vgdr_fusion): q, k arrive
 un-normalised, beta as logits, g as the gate pre-activation (in q's dtype or
 fp32).  They need 16-bit q, k, v for the chunked scan, as fla does.  Every call runs the HIP kernels of libvagus_gdr.so on the
-current stream; there is no CPU path and no autograd (backward is out of
-scope: inputs that require grad raise NotImplementedError).
+current stream; there is no CPU path.  The chunked delta rule with a scalar
+gate or none (chunk_gated_delta_rule, hip_scan with such a g) is
+differentiable: its backward runs vgdr_chunk_bwd.  Other calls with inputs
+that require grad raise NotImplementedError.
 """
 from __future__ import annotations
 
@@ -84,9 +86,21 @@ def _check_device(*ts):
                                f'{t.device} (there is no CPU implementation)')
 
 
+def _wants_grad(*ts):
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
+
+
 def _check_grad(*ts):
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts):
-        raise NotImplementedError('vagus_amd implements the forward pass only (no backward)')
+    if _wants_grad(*ts):
+        raise NotImplementedError('vagus_amd has a backward for the chunked delta rule with a scalar gate or none '
+                                  '(chunk_gated_delta_rule); this call has no backward')
+
+
+def _l2norm_rows(x):
+    """x rsqrt(sum x^2 + 1e-6) per (token, head) in >= fp32, cast back
+    (linear_attention.py:703-706): the q, k producer, differentiable in torch."""
+    xf = x if x.dtype == torch.float64 else x.float()
+    return (xf * torch.rsqrt((xf * xf).sum(-1, keepdim=True) + 1e-6)).to(x.dtype)
 
 
 class _Fusion:
@@ -194,6 +208,55 @@ class _Call:
         return S[:, :, :self.dk, :self.dv].contiguous()
 
 
+class _ChunkDeltaRule(torch.autograd.Function):
+    """The chunked delta rule with a scalar gate or none, differentiable:
+    forward vgdr_chunk_fwd, backward vgdr_chunk_bwd (the gradients the
+    reference's training takes through chunk_scan, linear_attention.py:237-309,
+    or fla's chunk backward).  q, k arrive normalised, beta in [0, 1]."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, S0, scale, cu, chunk_size):
+        o, S = chunk_scan(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True, scale=scale,
+                          initial_state=S0, output_final_state=True, cu_seqlens=cu, chunk_size=chunk_size)
+        ctx.save_for_backward(q, k, v, g, beta, S0, cu)
+        ctx.scale, ctx.chunk_size = scale, chunk_size
+        return o, S
+
+    @staticmethod
+    def backward(ctx, do, dS):
+        q, k, v, g, beta, S0, cu = ctx.saved_tensors
+        c = _Call(q, k, v, g, beta, S0, cu, gate='scalar' if g is not None else 'none', delta=True,
+                  dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+        if do is None:
+            do = torch.zeros(c.B, c.T, c.H, c.dv, dtype=c.dtype, device=c.device)
+        dop = _aligned(_pad_to(do.to(c.dtype), {1: c.dvp}))
+        dSp = None if dS is None else _aligned(_pad_to(dS.float(), {1: c.dvp, 2: c.dkp}))
+        new = lambda *shape, dt=torch.float32: torch.empty(*shape, dtype=dt, device=c.device)
+        dq, dk = new(c.B, c.T, c.H, c.dkp, dt=c.dtype), new(c.B, c.T, c.H, c.dkp, dt=c.dtype)
+        dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
+        dg = new(c.B, c.T, c.H) if g is not None else None
+        db = new(c.B, c.T, c.H)
+        dS0 = new(c.N, c.H, c.dkp, c.dvp) if S0 is not None else None
+        L = _lib.load()
+        dtype = _DTYPES[c.dtype]
+        nbytes = L.vgdr_chunk_bwd_workspace_size(dtype, c.gate_kind, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
+                                                 int(c.cu is not None), int(ctx.chunk_size))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+        with torch.cuda.device(c.device):
+            _lib.check(L.vgdr_chunk_bwd(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
+                                        _ptr(c.beta), _ptr(c.h0), _ptr(dop), _ptr(dSp), _ptr(dq), _ptr(dk),
+                                        _ptr(dv), _ptr(dg), _ptr(db), _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes,
+                                        c.B, c.T, c.H, c.dkp, c.dvp, c.N, float(ctx.scale), int(ctx.chunk_size),
+                                        _stream(c.device)))
+        if c.dkp != c.dk:
+            dq, dk = dq[..., :c.dk], dk[..., :c.dk]
+        if c.dvp != c.dv:
+            dv = dv[..., :c.dv]
+        if dS0 is not None:
+            dS0 = c.unpad_state(dS0).to(S0.dtype)
+        return (dq, dk, dv, None if dg is None else dg.to(g.dtype), db.to(beta.dtype), dS0, None, None, None)
+
+
 def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None, output_final_state=False,
                cu_seqlens=None, chunk_size=64, phase_event=None, fusion: _Fusion = _NO_FUSION):
     """Chunkwise prefill, the general form behind chunk_gated_delta_rule,
@@ -203,7 +266,24 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
     phase_event: optional torch.cuda.Event recorded on the current stream
     between the chunk-prep and the chunk-state kernels (the same two launches
     either way), so that a caller can time the two phases separately.
-    fusion: the producer fusions (_Fusion)."""
+    fusion: the producer fusions (_Fusion).
+
+    With grads enabled and an input that requires grad, the delta rule with a
+    scalar gate or none runs through _ChunkDeltaRule (the fused L2 norm and
+    beta sigmoid then run in torch, differentiably, before it); other
+    combinations raise NotImplementedError."""
+    if _wants_grad(q, k, v, g, beta, initial_state):
+        if gate == 'vector' or not delta or fusion.gate:
+            raise NotImplementedError('vagus_amd has a backward for the chunked delta rule with a scalar gate '
+                                      f'or none; this call has gate={gate!r}, delta={delta}')
+        if fusion.l2norm:
+            q, k = _l2norm_rows(q), _l2norm_rows(k)
+        if fusion.beta:
+            beta = torch.sigmoid(beta.float())
+        scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
+        o, S = _ChunkDeltaRule.apply(q, k, v, g if gate == 'scalar' else None, beta, initial_state, scale,
+                                     cu_seqlens, chunk_size)
+        return o, (S if output_final_state else None)
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=gate, delta=delta,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
     scale = c.dk ** -0.5 if scale is None else float(scale)
