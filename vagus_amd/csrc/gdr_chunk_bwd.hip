@@ -46,47 +46,80 @@ namespace vgdr {
 
 namespace {
 
-// CH rows x DK columns of a token-major matrix (row t at src + t * stride) into
-// LDS, row-major at rm (pitch prm) and/or transposed at tr (pitch ptr); rows
-// >= clen are zero.  Both pitches keep 16-byte rows aligned.
+// Rows [0, CH) x columns [0, DK) of a token-major matrix (row t at src + t *
+// stride), held in registers between load() and store().  load() issues every
+// 16-byte load at once, unconditionally, from clamped rows (a load under a
+// per-lane branch waits for the ones before it); store() writes row-major
+// (rm, pitch prm) and/or transposed (tr, pitch ptr) LDS copies with rows >=
+// clen zeroed.  Pitches keep 16-byte rows aligned.
 template <typename E, int CH, int DK, int NT>
-__device__ __forceinline__ void stage_rows(E *rm, int prm, E *tr, int ptr, const E *src, int64_t stride, int clen,
-                                           int tid) {
-    constexpr int VE = 16 / (int)sizeof(E);
+struct RowRegs {
+    static constexpr int VE = 16 / (int)sizeof(E), UPR = DK / VE, UNITS = CH * UPR, N = (UNITS + NT - 1) / NT;
     typedef E V __attribute__((ext_vector_type(VE)));
-    constexpr int UPR = DK / VE;
-    for (int u = tid; u < CH * UPR; u += NT) {
-        const int row = u / UPR, c0 = (u % UPR) * VE;
-        V x = {};
-        if (row < clen) x = *reinterpret_cast<const V *>(src + row * stride + c0);
-        if (rm) *reinterpret_cast<V *>(rm + row * prm + c0) = x;
-        if (tr) {
-#pragma unroll
-            for (int e = 0; e < VE; ++e) tr[(c0 + e) * ptr + row] = x[e];
-        }
+    V x[N];
+    __device__ __forceinline__ void load(const E *src, int64_t stride, int clen, int tid) {
+        unroll<N>([&](auto i) __attribute__((always_inline)) {
+            const int u = tid + (int)i * NT;
+            const int row = u / UPR, c0 = (u % UPR) * VE;
+            const int rr = (u < UNITS && row < clen) ? row : 0;
+            x[i] = *reinterpret_cast<const V *>(src + rr * stride + (u < UNITS ? c0 : 0));
+        });
     }
-}
+    __device__ __forceinline__ void store(E *rm, int prm, E *tr, int ptr, int clen, int tid) const {
+        unroll<N>([&](auto i) __attribute__((always_inline)) {
+            const int u = tid + (int)i * NT;
+            if (u < UNITS) {
+                const int row = u / UPR, c0 = (u % UPR) * VE;
+                const V v = row < clen ? x[i] : V{};
+                if (rm) *reinterpret_cast<V *>(rm + row * prm + c0) = v;
+                if (tr) {
+#pragma unroll
+                    for (int e = 0; e < VE; ++e) tr[(c0 + e) * ptr + row] = v[e];
+                }
+            }
+        });
+    }
+};
+
+// A fragment-order CH x CH block (TE or A: lower triangle with the diagonal)
+// in registers, 16-byte units read in order; store() writes it as a plain LDS
+// matrix dst[row][col] (dst[col][row] when TRANS) with zeros above the diagonal.
+template <typename E, int CH, int NT>
+struct BlockRegs {
+    static constexpr int VE = 16 / (int)sizeof(E), UNITS = CH * CH / VE, N = (UNITS + NT - 1) / NT;
+    static constexpr int NB = CH / 16;
+    typedef E V __attribute__((ext_vector_type(VE)));
+    V x[N];
+    __device__ __forceinline__ void load(const E *blk, int tid) {
+        unroll<N>([&](auto i) __attribute__((always_inline)) {
+            const int u = tid + (int)i * NT;
+            x[i] = *reinterpret_cast<const V *>(blk + (u < UNITS ? u : 0) * VE);
+        });
+    }
+    template <bool TRANS, typename T>
+    __device__ __forceinline__ void store(T *dst, int pitch, int tid) const {
+        unroll<N>([&](auto i) __attribute__((always_inline)) {
+            const int u = tid + (int)i * NT;
+            if (u < UNITS) {
+#pragma unroll
+                for (int e = 0; e < VE; ++e) {
+                    const int p = u * VE + e;
+                    const int e8 = p & 7, ln = (p >> 3) & 63, pr = p >> 9;   // pr = I (NB / 2) + q
+                    const int I = pr / (NB / 2), q = pr % (NB / 2);
+                    const int row = 16 * I + (ln & 15), col = 16 * (2 * q + (e8 >> 2)) + 4 * (ln >> 4) + (e8 & 3);
+                    const T v = col <= row ? (T)(float)x[i][e] : (T)0.f;
+                    if (TRANS) dst[col * pitch + row] = v;
+                    else dst[row * pitch + col] = v;
+                }
+            }
+        });
+    }
+};
 
 // position of element (row, col) of a fragment-order CH x CH block (frag_pos)
 template <int NB>
 __device__ __forceinline__ int blk_pos(int row, int col) {
     return frag_pos<NB>(row >> 4, col >> 4, 16 * ((col & 15) >> 2) + (row & 15)) + (col & 3);
-}
-
-// A fragment-order CH x CH block (TE or A, lower triangle with the diagonal)
-// as a plain LDS matrix: dst[row][col] (or dst[col][row] when TRANS), zeros
-// above the diagonal.  The block is read in order (coalesced).
-template <typename E, typename T, int CH, bool TRANS, int NT>
-__device__ __forceinline__ void unpack_block(T *dst, int pitch, const E *blk, int tid) {
-    constexpr int NB = CH / 16;
-    for (int p = tid; p < CH * CH; p += NT) {
-        const int e8 = p & 7, ln = (p >> 3) & 63, pr = p >> 9;   // pr = I (NB / 2) + q
-        const int I = pr / (NB / 2), q = pr % (NB / 2);
-        const int row = 16 * I + (ln & 15), col = 16 * (2 * q + (e8 >> 2)) + 4 * (ln >> 4) + (e8 & 3);
-        const float x = col <= row ? (float)blk[p] : 0.f;
-        if (TRANS) dst[col * pitch + row] = (T)x;
-        else dst[row * pitch + col] = (T)x;
-    }
 }
 
 // four consecutive rows k0 .. k0 + 3 of column c of a row-major fp32 matrix
@@ -150,6 +183,9 @@ __device__ __forceinline__ bool locate_chunk(const SeqGeom &g, int64_t slot, int
 // ===========================================================================
 // chunk_hs_kernel: entry state of every chunk
 // ===========================================================================
+// Each chunk's operands are loaded into registers one chunk ahead: the loads
+// of chunk c + 1 are in flight while chunk c computes, and reach LDS after
+// the next barrier.
 template <int DK, int CH, int NW, typename E>
 __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
@@ -168,8 +204,9 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
     WalkUnit u;
     if (!walk_unit(p, u)) return;
     const int H = p.H, DV = p.DV, h = u.h;
-    const int col = u.tile * 16 * NW + 16 * wave + r16;
-    const bool wvalid = u.tile * 16 * NW + 16 * wave < DV;     // DV % 16 == 0
+    const int colw = u.tile * 16 * NW + 16 * wave;
+    const bool wvalid = colw < DV;                             // DV % 16 == 0
+    const int col = wvalid ? colw + r16 : r16;                 // in bounds for the unconditional loads
     const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
     const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
     const E *vg = reinterpret_cast<const E *>(p.v) + (int64_t)h * DV + col;
@@ -183,6 +220,31 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
             S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
 
     const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
+    RowRegs<E, CH, DK, NT> rk;
+    f32x4 vn[NB];                                              // V rows of the fetched chunk (C layout)
+    float gxn = 0.f, gen = 0.f, gcn = 0.f;
+    int clen_n = 0;
+    auto fetch = [&](int c) __attribute__((always_inline)) {
+        const int64_t t0 = u.bos + (int64_t)c * CH;
+        clen_n = (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
+        rk.load(kg + t0 * sqk, sqk, clen_n, tid);
+        const float *gf =
+            reinterpret_cast<const float *>(reinterpret_cast<const char *>(p.blocks) +
+                                            ((u.cbase + c) * H + h) * CB::BYTES + CB::GOFF);
+        const int tc = tid < CH ? tid : 0;
+        gxn = gf[tc];
+        gen = gf[2 * CH + tc];
+        gcn = gf[3 * CH];
+#pragma unroll
+        for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = 16 * I + 4 * g4 + j;
+                vn[I][j] = EL::to_f(vg[(t0 + (row < clen_n ? row : 0)) * sv]);
+                if (row >= clen_n) vn[I][j] = 0.f;
+            }
+    };
+    if (nchunks > 1) fetch(0);
     for (int c = 0; c < nchunks; ++c) {
         const int64_t slot = u.cbase + c;
         if (wvalid) {
@@ -193,19 +255,19 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
                 for (int j = 0; j < 4; ++j) hs[(int64_t)(16 * kt + 4 * g4 + j) * DV] = S[kt][j];
         }
         if (c + 1 == nchunks) break;                           // the last exit state is not needed
-        const int64_t t0 = u.bos + (int64_t)c * CH;
-        const int clen = (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
-        const char *blkb = reinterpret_cast<const char *>(p.blocks) + (slot * H + h) * CB::BYTES;
-        const E *TEb = reinterpret_cast<const E *>(blkb);
-        const float *gf = reinterpret_cast<const float *>(blkb + CB::GOFF);
+        const E *TEb = reinterpret_cast<const E *>(reinterpret_cast<const char *>(p.blocks) + (slot * H + h) * CB::BYTES);
         __syncthreads();                                       // the previous chunk's LDS reads are done
-        stage_rows<E, CH, DK, NT>(Ks, PK, KT, PT, kg + t0 * sqk, sqk, clen, tid);
+        rk.store(Ks, PK, KT, PT, clen_n, tid);
         if (tid < CH) {
-            gx[tid] = gf[tid];
-            ge[tid] = gf[2 * CH + tid];
+            gx[tid] = gxn;
+            ge[tid] = gen;
         }
-        if (tid == 0) gcs[0] = gf[3 * CH];
+        if (tid == 0) gcs[0] = gcn;
+        f32x4 V[NB];
+#pragma unroll
+        for (int I = 0; I < NB; ++I) V[I] = vn[I];
         __syncthreads();
+        if (c + 2 < nchunks) fetch(c + 1);
         if (wvalid) {
             F Sb[NKB];
 #pragma unroll
@@ -216,14 +278,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
                 const f32x4 P = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return Sb[kt]; });
-                f32x4 X;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = 16 * I + 4 * g4 + j;
-                    const float v = row < clen ? EL::to_f(vg[(t0 + row) * sv]) : 0.f;
-                    X[j] = v - gx[row] * P[j];
-                }
-                Xb[I] = EL::cvt(X);
+                Xb[I] = EL::cvt(V[I] - ld4(gx + 16 * I + 4 * g4) * P);
             }
             F Wb[NB];
 #pragma unroll
@@ -268,8 +323,9 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
     WalkUnit u;
     if (!walk_unit(p, u)) return;
     const int H = p.H, DV = p.DV, h = u.h;
-    const int col = u.tile * 16 * NW + 16 * wave + r16;
-    const bool wvalid = u.tile * 16 * NW + 16 * wave < DV;
+    const int colw = u.tile * 16 * NW + 16 * wave;
+    const bool wvalid = colw < DV;
+    const int col = wvalid ? colw + r16 : r16;
     const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
     const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
     const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
@@ -285,6 +341,35 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
             dS[kt][j] = (p.dht && wvalid) ? p.dht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
 
     const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
+    RowRegs<E, CH, DK, NT> rk, rq;
+    BlockRegs<E, CH, NT> rte, ra;
+    f32x4 don[NB];                                             // dO rows of the fetched chunk (C layout)
+    float gxn = 0.f, gon = 0.f, gen = 0.f, gcn = 0.f;
+    int clen_n = 0;
+    auto fetch = [&](int c) __attribute__((always_inline)) {
+        const int64_t t0 = u.bos + (int64_t)c * CH;
+        clen_n = (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
+        rk.load(kg + t0 * sqk, sqk, clen_n, tid);
+        rq.load(qg + t0 * sqk, sqk, clen_n, tid);
+        const char *blkb = reinterpret_cast<const char *>(p.blocks) + ((u.cbase + c) * H + h) * CB::BYTES;
+        rte.load(reinterpret_cast<const E *>(blkb), tid);
+        ra.load(reinterpret_cast<const E *>(blkb) + CH * CH, tid);
+        const float *gf = reinterpret_cast<const float *>(blkb + CB::GOFF);
+        const int tc = tid < CH ? tid : 0;
+        gxn = gf[tc];
+        gon = gf[CH + tc];
+        gen = gf[2 * CH + tc];
+        gcn = gf[3 * CH];
+#pragma unroll
+        for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = 16 * I + 4 * g4 + j;
+                don[I][j] = EL::to_f(dog[(t0 + (row < clen_n ? row : 0)) * sv]);
+                if (row >= clen_n) don[I][j] = 0.f;
+            }
+    };
+    if (nchunks > 0) fetch(nchunks - 1);
     for (int c = nchunks - 1; c >= 0; --c) {
         const int64_t slot = u.cbase + c;
         if (wvalid) {
@@ -295,31 +380,24 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
                 for (int j = 0; j < 4; ++j) dhs[(int64_t)(16 * kt + 4 * g4 + j) * DV] = dS[kt][j];
         }
         const int64_t t0 = u.bos + (int64_t)c * CH;
-        const int clen = (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
-        const char *blkb = reinterpret_cast<const char *>(p.blocks) + (slot * H + h) * CB::BYTES;
-        const E *TEb = reinterpret_cast<const E *>(blkb);
-        const float *gf = reinterpret_cast<const float *>(blkb + CB::GOFF);
+        const int clen = clen_n;
         __syncthreads();
-        stage_rows<E, CH, DK, NT>(Ks, PK, KT, PT, kg + t0 * sqk, sqk, clen, tid);
-        stage_rows<E, CH, DK, NT>(nullptr, 0, QT, PT, qg + t0 * sqk, sqk, clen, tid);
-        unpack_block<E, E, CH, true, NT>(TEt, PT, TEb, tid);
-        unpack_block<E, E, CH, true, NT>(At, PT, TEb + CH * CH, tid);
+        rk.store(Ks, PK, KT, PT, clen, tid);
+        rq.store(nullptr, 0, QT, PT, clen, tid);
+        rte.template store<true>(TEt, PT, tid);
+        ra.template store<true>(At, PT, tid);
         if (tid < CH) {
-            gx[tid] = gf[tid];
-            go[tid] = gf[CH + tid];
-            ge[tid] = gf[2 * CH + tid];
+            gx[tid] = gxn;
+            go[tid] = gon;
+            ge[tid] = gen;
         }
-        if (tid == 0) gcs[0] = gf[3 * CH];
+        if (tid == 0) gcs[0] = gcn;
+        f32x4 dO[NB];
+#pragma unroll
+        for (int I = 0; I < NB; ++I) dO[I] = don[I];
         __syncthreads();
+        if (c > 0) fetch(c - 1);
         if (wvalid) {
-            f32x4 dO[NB];
-#pragma unroll
-            for (int I = 0; I < NB; ++I)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = 16 * I + 4 * g4 + j;
-                    dO[I][j] = row < clen ? EL::to_f(dog[(t0 + row) * sv]) : 0.f;
-                }
             F dOb[NB], dSb[NKB];
 #pragma unroll
             for (int I = 0; I < NB; ++I) dOb[I] = EL::cvt(dO[I]);
@@ -457,26 +535,58 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     const float *hsb = p.hs + (slot * H + h) * DK * DV;
     const float *dhsb = p.dhs + (slot * H + h) * DK * DV;
 
-    // ---- stage ------------------------------------------------------------
-    stage_rows<E, CH, DK, NT>(Ks, PK, KT, PT, reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk,
-                              clen, tid);
-    stage_rows<E, CH, DK, NT>(nullptr, 0, QT, PT, reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK,
-                              sqk, clen, tid);
-    unpack_block<E, E, CH, true, NT>(At, PT, Ab, tid);
+    // ---- stage: every load of the chunk issued at once --------------------
+    RowRegs<E, CH, DK, NT> rk, rq;
+    BlockRegs<E, CH, NT> ra, rte;                              // A (-> A^T now), TE (-> fp32 later)
+    rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+    rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+    ra.load(Ab, tid);
+    rte.load(TEb, tid);
+    const int tc = tid < CH ? tid : 0, tg = tc < clen ? tc : 0;
+    const float gx_v = gf[tc], go_v = gf[CH + tc], ge_v = gf[2 * CH + tc], gc_v = gf[3 * CH];
+    const float be_v = p.beta[(t0 + tg) * H + h];
+    const float g_v = p.g ? p.g[(t0 + (lane < clen ? lane : 0)) * H + h] : 0.f;
+    const int Iw = wave % NB, J0 = (wave / NB) * JPW;          // this wave's C x DK tiles (Iw, J0 + s)
+    auto tile_of = [&](int l, int &I, int &J) __attribute__((always_inline)) {
+        I = 0;
+        J = l;
+        while (J > I) { J -= I + 1; ++I; }
+    };
+    // A at this wave's dA elements (the A terms of dgamma), and the TE fragments of U = TE X
+    float aval[LPW][4];
+#pragma unroll
+    for (int s = 0; s < LPW; ++s) {
+        const int l = wave + NW * s;
+        int I = 0, J = 0;
+        if (l < NL) tile_of(l, I, J);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = 16 * I + 4 * g4 + j, jj = 16 * J + r16;
+            aval[s][j] = EL::to_f(Ab[blk_pos<NB>(i, jj <= i ? jj : i)]);
+        }
+    }
+    F tef[NB * NB];
+#pragma unroll
+    for (int I = 0; I < NB; ++I)
+#pragma unroll
+        for (int kb = 0; kb <= I; ++kb) tef[I * NB + kb] = gfrag<E>(TEb + frag_pos<NB>(I, kb, lane));
+    rk.store(Ks, PK, KT, PT, clen, tid);
+    rq.store(nullptr, 0, QT, PT, clen, tid);
+    ra.template store<true>(At, PT, tid);
     if (tid < CH) {
-        gx[tid] = gf[tid];
-        go[tid] = gf[CH + tid];
-        ge[tid] = gf[2 * CH + tid];
-        bet[tid] = tid < clen ? p.beta[(t0 + tid) * H + h] : 0.f;
+        gx[tid] = gx_v;
+        go[tid] = go_v;
+        ge[tid] = ge_v;
+        bet[tid] = tid < clen ? be_v : 0.f;
         dgam[tid] = 0.f;
         dbet[tid] = 0.f;
     }
     if (tid == 0) {
-        misc[0] = gf[3 * CH];
+        misc[0] = gc_v;
         misc[1] = 0.f;
     }
     if (wave == 0) {                                           // gamma: in-chunk inclusive sum of g
-        float x = (p.g && lane < clen) ? p.g[(t0 + lane) * H + h] : 0.f;
+        float x = lane < clen ? g_v : 0.f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
             const float y = __shfl_up(x, o);
@@ -490,18 +600,12 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     // wave w < NCW computes X, U, dU (and loads S, dS', dO, dX) for columns
     // 16 w .. 16 w + 15 of the block; then every wave accumulates its tiles of
     // the products that contract over dv.
-    const int Iw = wave % NB, J0 = (wave / NB) * JPW;          // this wave's C x DK tiles (Iw, J0 + s)
     f32x4 aQ[JPW], aX[JPW], aE[JPW];                           // dO S^T, dX S^T, U dS'^T
     f32x4 aA[LPW], aT[LPW];                                    // dO U^T, dU X^T (lower tiles)
 #pragma unroll
     for (int s = 0; s < JPW; ++s) aQ[s] = aX[s] = aE[s] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < LPW; ++s) aA[s] = aT[s] = f32x4{0.f, 0.f, 0.f, 0.f};
-    auto tile_of = [&](int l, int &I, int &J) __attribute__((always_inline)) {
-        I = 0;
-        J = l;
-        while (J > I) { J -= I + 1; ++I; }
-    };
     float gcacc = 0.f;
     const int ndb = (DV + DVB - 1) / DVB;
     for (int db = 0; db < ndb; ++db) {
@@ -511,15 +615,30 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             const int cw = 16 * wave + r16;                      // column within the block
             const int col = cb + cw;
             const bool cv = cb + 16 * wave < DV;
-            f32x4 S[NKB], dSx[NKB];
+            const int colc = cv ? col : r16;                     // in bounds for the unconditional loads
+            f32x4 S[NKB], dSx[NKB], Vr[NB], dOr[NB], dXr[NB];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt)
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int64_t off = (int64_t)(16 * kt + 4 * g4 + j) * DV + col;
-                    S[kt][j] = cv ? hsb[off] : 0.f;
-                    dSx[kt][j] = cv ? dhsb[off] : 0.f;
+                    const int64_t off = (int64_t)(16 * kt + 4 * g4 + j) * DV + colc;
+                    S[kt][j] = hsb[off];
+                    dSx[kt][j] = dhsb[off];
                 }
+#pragma unroll
+            for (int I = 0; I < NB; ++I)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int row = 16 * I + 4 * g4 + j;
+                    const int64_t off = (t0 + (row < clen ? row : 0)) * sv + (int64_t)h * DV + colc;
+                    Vr[I][j] = EL::to_f(reinterpret_cast<const E *>(p.v)[off]);
+                    dOr[I][j] = EL::to_f(reinterpret_cast<const E *>(p.dout)[off]);
+                    dXr[I][j] = EL::to_f(reinterpret_cast<const E *>(p.dv)[off]);
+                }
+            if (!cv) {
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt) S[kt] = dSx[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
             F Sb[NKB], dSb[NKB];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) {
@@ -548,10 +667,9 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 for (int j = 0; j < 4; ++j) {
                     const int row = 16 * I + 4 * g4 + j;
                     const bool ok = cv && row < clen;
-                    const int64_t off = (t0 + row) * sv + (int64_t)h * DV + col;
-                    const float v = ok ? EL::to_f(reinterpret_cast<const E *>(p.v)[off]) : 0.f;
-                    dO[j] = ok ? EL::to_f(reinterpret_cast<const E *>(p.dout)[off]) : 0.f;
-                    const float dx = ok ? EL::to_f(reinterpret_cast<const E *>(p.dv)[off]) : 0.f;
+                    const float v = ok ? Vr[I][j] : 0.f;
+                    dO[j] = ok ? dOr[I][j] : 0.f;
+                    const float dx = ok ? dXr[I][j] : 0.f;
                     X[I][j] = v - gx[row] * P[j];
                     Y[I][j] = ge[row] * P2[j];
                     Xs[row * PD + cw] = EL::from_f(X[I][j]);
@@ -565,7 +683,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             for (int I = 0; I < NB; ++I) {
                 // U = TE X ;  dU = A^T dO + diag(GE) K dS'
                 const f32x4 U = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
-                    [&](int kb) { return gfrag<E>(TEb + frag_pos<NB>(I, kb, lane)); },
+                    [&](int kb) { return tef[I * NB + kb]; },
                     [&](int kb) { return Xb[kb]; });
                 Y[I] = contract(Y[I], NB,
                     [&](int kb) { return ld_frag<E>(At + (16 * I + r16) * PT + 16 * kb + 4 * g4); },
@@ -613,7 +731,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     // ---- CH x CH phase ----------------------------------------------------
     for (int i = tid; i < 3 * CH * PF; i += NT) Fn[i] = 0.f;   // N, dTE, T0 (written by lower tiles)
     for (int i = tid; i < 3 * CH * PT; i += NT) WA[i] = EL::from_f(0.f);
-    unpack_block<E, float, CH, false, NT>(Fte, PF, TEb, tid);
+    rte.template store<false>(Fte, PF, tid);
     {
         const float t = sum64(gcacc);
         if (lane == 0 && wave < NCW) atomicAdd(&misc[1], misc[0] * t);     // Gc <S, dS'>
@@ -636,7 +754,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 const bool low = jj <= i;
                 const float D = low ? __expf(gam[i] - gam[jj]) : 0.f;
                 const float da = low ? aA[s][j] : 0.f;
-                const float v = low ? da * EL::to_f(Ab[blk_pos<NB>(i, jj)]) : 0.f;
+                const float v = low ? da * aval[s][j] : 0.f;
                 if (low) {
                     atomicAdd(&dgam[i], v);
                     atomicAdd(&dgam[jj], -v);
