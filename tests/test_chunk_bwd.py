@@ -47,8 +47,8 @@ def test_chunk_bwd_argument_checks():
     assert call(beta=None) == _lib.VGDR_ERR_INVALID
     assert call(B=0, N=0, T=0) == _lib.VGDR_OK
     need = L.vgdr_chunk_bwd_workspace_size(1, 1, 2, 64, 2, 64, 64, 2, 0, 64)
-    # forward blocks plus two fp32 states per (chunk, head)
-    assert need >= 2 * 2 * 2 * 64 * 64 * 4 + L.vgdr_chunk_workspace_size(1, 1, 2, 64, 2, 64, 2, 0, 64)
+    # forward blocks plus two bf16 states per (chunk, head)
+    assert need >= 2 * 2 * 2 * 64 * 64 * 2 + L.vgdr_chunk_workspace_size(1, 1, 2, 64, 2, 64, 2, 0, 64)
 
 
 def test_calls_without_a_backward_raise():

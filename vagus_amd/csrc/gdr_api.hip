@@ -294,7 +294,7 @@ int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, con
 
 namespace {
 // workspace of the backward: the forward's (table, blocks), then each chunk's
-// entry state and exit-state gradient (fp32, dk x dv per (chunk, head))
+// entry state and exit-state gradient (dk x dv per (chunk, head) in the element type)
 struct BwdWs {
     ChunkWs fwd;
     int64_t hs_off, dhs_off, total;
@@ -303,7 +303,7 @@ BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int6
                  int64_t n_seqs, bool varlen) {
     BwdWs w{};
     w.fwd = chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, varlen);
-    const int64_t states = w.fwd.slots * H * dk * dv * 4;
+    const int64_t states = w.fwd.slots * H * dk * dv * (dtype == VGDR_F32 ? 4 : 2);
     w.hs_off = (w.fwd.total + 255) / 256 * 256;
     w.dhs_off = w.hs_off + (states + 255) / 256 * 256;
     w.total = states > 0 ? w.dhs_off + states : w.fwd.total;
@@ -372,8 +372,8 @@ int vgdr_chunk_bwd(int dtype, int gate_kind, const void *q, const void *k, const
     p.dbeta = grad_beta;
     p.dh0 = grad_initial_state;
     p.blocks = f.blocks;
-    p.hs = reinterpret_cast<float *>(wsb + ws.hs_off);
-    p.dhs = reinterpret_cast<float *>(wsb + ws.dhs_off);
+    p.hs = wsb + ws.hs_off;
+    p.dhs = wsb + ws.dhs_off;
     p.H = (int)H;
     p.DV = (int)dv;
     p.n_chunk_slots = (int)ws.fwd.slots;

@@ -938,22 +938,6 @@ __global__ void __launch_bounds__(64 * NW) chunk_state_kernel(const ChunkParams 
 // chunk_state_tr_kernel: the chunk recurrence for 16-bit elements with a
 // scalar gate or none, on LDS transpose reads
 // ===========================================================================
-// gfx950 ds_read_b64_tr_b16: within each 16-lane group, source lane s gives the
-// address of 4 consecutive 16-bit elements, and result lane d receives element
-// d % 4 of source lanes d / 4 + 4 i (i = 0..3).  With source lane s pointing at
-// row k0 + s / 4, columns c0 + 4 (s % 4) of a row-major tile, lane d receives
-// rows k0 .. k0 + 3 of column c0 + d: the C-layout / B-operand fragment of the
-// tile, or the A-operand fragment of its transpose, read straight from
-// row-major storage.
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ s16x4 lds_tr16(const void *p) {
-    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)const_cast<void *>(p));
-}
-template <typename E>
-__device__ __forceinline__ typename Elem<E>::frag ld_tr(const E *p) {
-    return __builtin_bit_cast(typename Elem<E>::frag, lds_tr16(p));
-}
-
 // Values the compiler must treat as unknown where they are produced.  Address
 // arithmetic derived from them is redone next to each use instead of being
 // hoisted out of the chunk loop, which would pin one register per fragment

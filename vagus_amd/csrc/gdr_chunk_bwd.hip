@@ -116,10 +116,39 @@ struct BlockRegs {
     }
 };
 
+// four consecutive elements to global memory (aligned to their size)
+template <typename E>
+__device__ __forceinline__ void st_gfrag(E *p, typename Elem<E>::frag x) {
+    *reinterpret_cast<typename Elem<E>::frag *>(p) = x;
+}
+
 // position of element (row, col) of a fragment-order CH x CH block (frag_pos)
 template <int NB>
 __device__ __forceinline__ int blk_pos(int row, int col) {
     return frag_pos<NB>(row >> 4, col >> 4, 16 * ((col & 15) >> 2) + (row & 15)) + (col & 3);
+}
+
+// LDS row pitch (elements) of an N-column matrix: 288-byte rows for N = 128 in
+// a 16-bit type, at which both the 8-byte fragment reads of 16 rows and the
+// transpose reads run conflict-free on gfx950
+template <typename E, int N>
+struct Pitch {
+    static constexpr int value = N + (sizeof(E) == 2 ? 16 : 4);
+};
+
+// Lane (g, r) gets M[k0 + 4 g + j][c0 + r], j = 0..3, of a row-major LDS
+// matrix M (pitch pm): the A-operand fragment of M^T at row c0 + r, or the
+// B-operand fragment of M at column c0 + r, over the k-block of rows k0 ..
+// k0 + 15.  16-bit types use the transpose read; fp32 reads four rows.
+template <typename E>
+__device__ __forceinline__ typename Elem<E>::frag ld_colfrag(const E *M, int pm, int k0, int c0, int lane) {
+    const int g = lane >> 4, s = lane & 15;
+    if constexpr (sizeof(E) == 2) {
+        return ld_tr<E>(M + (k0 + 4 * g + (s >> 2)) * pm + c0 + 4 * (s & 3));
+    } else {
+        const E *b = M + (k0 + 4 * g) * pm + c0 + s;
+        return typename Elem<E>::frag{b[0], b[pm], b[2 * pm], b[3 * pm]};
+    }
 }
 
 // four consecutive rows k0 .. k0 + 3 of column c of a row-major fp32 matrix
@@ -192,9 +221,8 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
     using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, 1>;
     constexpr int NT = 64 * NW, NB = CH / 16, NKB = DK / 16, VE = 16 / (int)sizeof(E);
-    constexpr int PK = DK + VE, PT = CH + VE;
+    constexpr int PK = Pitch<E, DK>::value;
     __shared__ __attribute__((aligned(16))) E Ks[CH * PK];
-    __shared__ __attribute__((aligned(16))) E KT[DK * PT];
     __shared__ __attribute__((aligned(16))) float gx[CH];
     __shared__ __attribute__((aligned(16))) float ge[CH];
     __shared__ float gcs[4];
@@ -222,6 +250,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
     const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
     RowRegs<E, CH, DK, NT> rk;
     f32x4 vn[NB];                                              // V rows of the fetched chunk (C layout)
+    F ten[NB * NB];                                            // its TE fragments (lower tiles)
     float gxn = 0.f, gen = 0.f, gcn = 0.f;
     int clen_n = 0;
     auto fetch = [&](int c) __attribute__((always_inline)) {
@@ -235,6 +264,12 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
         gxn = gf[tc];
         gen = gf[2 * CH + tc];
         gcn = gf[3 * CH];
+        const E *TEb = reinterpret_cast<const E *>(reinterpret_cast<const char *>(p.blocks) +
+                                                   ((u.cbase + c) * H + h) * CB::BYTES);
+#pragma unroll
+        for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int kb = 0; kb <= I; ++kb) ten[I * NB + kb] = gfrag<E>(TEb + frag_pos<NB>(I, kb, lane));
 #pragma unroll
         for (int I = 0; I < NB; ++I)
 #pragma unroll
@@ -248,24 +283,26 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
     for (int c = 0; c < nchunks; ++c) {
         const int64_t slot = u.cbase + c;
         if (wvalid) {
-            float *hs = p.hs + (slot * H + h) * DK * DV + col;
+            E *hs = reinterpret_cast<E *>(p.hs) + ((slot * H + h) * DV + col) * DK + 4 * g4;
 #pragma unroll
-            for (int kt = 0; kt < NKB; ++kt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) hs[(int64_t)(16 * kt + 4 * g4 + j) * DV] = S[kt][j];
+            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(hs + 16 * kt, EL::cvt(S[kt]));
         }
         if (c + 1 == nchunks) break;                           // the last exit state is not needed
-        const E *TEb = reinterpret_cast<const E *>(reinterpret_cast<const char *>(p.blocks) + (slot * H + h) * CB::BYTES);
         __syncthreads();                                       // the previous chunk's LDS reads are done
-        rk.store(Ks, PK, KT, PT, clen_n, tid);
+        rk.store(Ks, PK, nullptr, 0, clen_n, tid);
         if (tid < CH) {
             gx[tid] = gxn;
             ge[tid] = gen;
         }
         if (tid == 0) gcs[0] = gcn;
         f32x4 V[NB];
+        F TEf[NB * NB];
 #pragma unroll
-        for (int I = 0; I < NB; ++I) V[I] = vn[I];
+        for (int I = 0; I < NB; ++I) {
+            V[I] = vn[I];
+#pragma unroll
+            for (int kb = 0; kb <= I; ++kb) TEf[I * NB + kb] = ten[I * NB + kb];
+        }
         __syncthreads();
         if (c + 2 < nchunks) fetch(c + 1);
         if (wvalid) {
@@ -284,7 +321,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
 #pragma unroll
             for (int I = 0; I < NB; ++I) {
                 const f32x4 U = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
-                    [&](int kb) { return gfrag<E>(TEb + frag_pos<NB>(I, kb, lane)); },
+                    [&](int kb) { return TEf[I * NB + kb]; },
                     [&](int kb) { return Xb[kb]; });
                 Wb[I] = EL::cvt(U * ld4(ge + 16 * I + 4 * g4));
             }
@@ -292,7 +329,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt)
                 S[kt] = contract(S[kt] * gc, NB,
-                    [&](int kb) { return ld_frag<E>(KT + (16 * kt + r16) * PT + 16 * kb + 4 * g4); },
+                    [&](int kb) { return ld_colfrag<E>(Ks, PK, 16 * kb, 16 * kt, lane); },
                     [&](int kb) { return Wb[kb]; });
         }
     }
@@ -307,12 +344,11 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
     using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, 1>;
     constexpr int NT = 64 * NW, NB = CH / 16, NKB = DK / 16, VE = 16 / (int)sizeof(E);
-    constexpr int PK = DK + VE, PT = CH + VE;
+    constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value;
     __shared__ __attribute__((aligned(16))) E Ks[CH * PK];
-    __shared__ __attribute__((aligned(16))) E KT[DK * PT];
-    __shared__ __attribute__((aligned(16))) E QT[DK * PT];
-    __shared__ __attribute__((aligned(16))) E TEt[CH * PT];   // TE^T
-    __shared__ __attribute__((aligned(16))) E At[CH * PT];    // A^T
+    __shared__ __attribute__((aligned(16))) E Qs[CH * PK];
+    __shared__ __attribute__((aligned(16))) E TEm[CH * PT];
+    __shared__ __attribute__((aligned(16))) E Am[CH * PT];
     __shared__ __attribute__((aligned(16))) float gx[CH];
     __shared__ __attribute__((aligned(16))) float go[CH];
     __shared__ __attribute__((aligned(16))) float ge[CH];
@@ -373,19 +409,17 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
     for (int c = nchunks - 1; c >= 0; --c) {
         const int64_t slot = u.cbase + c;
         if (wvalid) {
-            float *dhs = p.dhs + (slot * H + h) * DK * DV + col;
+            E *dhs = reinterpret_cast<E *>(p.dhs) + ((slot * H + h) * DV + col) * DK + 4 * g4;
 #pragma unroll
-            for (int kt = 0; kt < NKB; ++kt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) dhs[(int64_t)(16 * kt + 4 * g4 + j) * DV] = dS[kt][j];
+            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(dhs + 16 * kt, EL::cvt(dS[kt]));
         }
         const int64_t t0 = u.bos + (int64_t)c * CH;
         const int clen = clen_n;
         __syncthreads();
-        rk.store(Ks, PK, KT, PT, clen, tid);
-        rq.store(nullptr, 0, QT, PT, clen, tid);
-        rte.template store<true>(TEt, PT, tid);
-        ra.template store<true>(At, PT, tid);
+        rk.store(Ks, PK, nullptr, 0, clen, tid);
+        rq.store(Qs, PK, nullptr, 0, clen, tid);
+        rte.template store<false>(TEm, PT, tid);
+        ra.template store<false>(Am, PT, tid);
         if (tid < CH) {
             gx[tid] = gxn;
             go[tid] = gon;
@@ -411,7 +445,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return dSb[kt]; });
                 Y *= ld4(ge + 16 * I + 4 * g4);
-                Y = contract(Y, NB, [&](int kb) { return ld_frag<E>(At + (16 * I + r16) * PT + 16 * kb + 4 * g4); },
+                Y = contract(Y, NB, [&](int kb) { return ld_colfrag<E>(Am, PT, 16 * kb, 16 * I, lane); },
                              [&](int kb) { return dOb[kb]; });
                 Yb[I] = EL::cvt(Y);
             }
@@ -420,7 +454,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
 #pragma unroll
             for (int I = 0; I < NB; ++I) {
                 const f32x4 dX = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NB,
-                    [&](int kb) { return ld_frag<E>(TEt + (16 * I + r16) * PT + 16 * kb + 4 * g4); },
+                    [&](int kb) { return ld_colfrag<E>(TEm, PT, 16 * kb, 16 * I, lane); },
                     [&](int kb) { return Yb[kb]; });
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -435,10 +469,10 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) {
                 f32x4 s = contract(dS[kt] * gc, NB,
-                    [&](int kb) { return ld_frag<E>(QT + (16 * kt + r16) * PT + 16 * kb + 4 * g4); },
+                    [&](int kb) { return ld_colfrag<E>(Qs, PK, 16 * kb, 16 * kt, lane); },
                     [&](int kb) { return Ob[kb]; });
                 dS[kt] = contract(s, NB,
-                    [&](int kb) { return ld_frag<E>(KT + (16 * kt + r16) * PT + 16 * kb + 4 * g4); },
+                    [&](int kb) { return ld_colfrag<E>(Ks, PK, 16 * kb, 16 * kt, lane); },
                     [&](int kb) { return Xb[kb]; });
             }
         }
@@ -459,13 +493,13 @@ struct GradLayout {
     static constexpr int ES = sizeof(E), VE = 16 / ES;
     static constexpr int NCW = ES == 2 ? 4 : 2;               // waves of the column phase
     static constexpr int DVB = 16 * NCW;                      // dv columns per block
-    static constexpr int PK = DK + VE, PT = CH + VE, PD = DVB + VE, PF = CH + 4;
-    // K rows, K^T and Q^T for the whole kernel
-    static constexpr int PERS = (CH * PK + 2 * DK * PT) * ES;
-    // column phase: A^T; X, U, dU, dO, dX rows of the block; S, dS' rows of the block
+    static constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value, PD = DVB + VE, PF = CH + 4;
+    // K and Q rows for the whole kernel
+    static constexpr int PERS = 2 * CH * PK * ES;
+    // column phase: A; X, U, dU, dO, dX rows of the block; S, dS' rows of the block
     static constexpr int COLS = (CH * PT + 5 * CH * PD + 2 * DK * PD) * ES;
-    // CH x CH phase: four fp32 matrices; W_A, W_A^T, W_N + W_N^T in the element type
-    static constexpr int SQ = 4 * CH * PF * 4 + 3 * CH * PT * ES;
+    // CH x CH phase: four fp32 matrices; W_A and W_N + W_N^T in the element type
+    static constexpr int SQ = 4 * CH * PF * 4 + 2 * CH * PT * ES;
     static constexpr int REGION = cmax(COLS, SQ);
     static constexpr int SMALL = 8 * CH * 4 + 64;
     static constexpr int BYTES = PERS + REGION + SMALL;
@@ -490,12 +524,11 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     E *Ks = reinterpret_cast<E *>(smem);
-    E *KT = Ks + CH * PK;
-    E *QT = KT + DK * PT;
+    E *Qs = Ks + CH * PK;
     char *R = smem + L::PERS;
     // column phase
-    E *At = reinterpret_cast<E *>(R);
-    E *Xs = At + CH * PT;
+    E *Am = reinterpret_cast<E *>(R);
+    E *Xs = Am + CH * PT;
     E *Us = Xs + CH * PD;
     E *Ys = Us + CH * PD;
     E *dOs = Ys + CH * PD;
@@ -508,8 +541,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     float *Fdte = Fn + CH * PF;
     float *Ft0 = Fdte + CH * PF;                  // T0, then Z
     E *WA = reinterpret_cast<E *>(Ft0 + CH * PF);
-    E *WAt = WA + CH * PT;
-    E *WS = WAt + CH * PT;
+    E *WS = WA + CH * PT;
     float *sm = reinterpret_cast<float *>(R + L::REGION);
     float *gam = sm, *bet = sm + CH, *gx = sm + 2 * CH, *go = sm + 3 * CH, *ge = sm + 4 * CH;
     float *dgam = sm + 5 * CH, *dbet = sm + 6 * CH;
@@ -532,12 +564,12 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     const E *TEb = reinterpret_cast<const E *>(blkb);
     const E *Ab = TEb + CH * CH;
     const float *gf = reinterpret_cast<const float *>(blkb + CB::GOFF);
-    const float *hsb = p.hs + (slot * H + h) * DK * DV;
-    const float *dhsb = p.dhs + (slot * H + h) * DK * DV;
+    const E *hsb = reinterpret_cast<const E *>(p.hs) + (slot * H + h) * DK * DV;
+    const E *dhsb = reinterpret_cast<const E *>(p.dhs) + (slot * H + h) * DK * DV;
 
     // ---- stage: every load of the chunk issued at once --------------------
     RowRegs<E, CH, DK, NT> rk, rq;
-    BlockRegs<E, CH, NT> ra, rte;                              // A (-> A^T now), TE (-> fp32 later)
+    BlockRegs<E, CH, NT> ra, rte;                              // A (-> LDS now), TE (-> fp32 later)
     rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
     rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
     ra.load(Ab, tid);
@@ -570,9 +602,9 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     for (int I = 0; I < NB; ++I)
 #pragma unroll
         for (int kb = 0; kb <= I; ++kb) tef[I * NB + kb] = gfrag<E>(TEb + frag_pos<NB>(I, kb, lane));
-    rk.store(Ks, PK, KT, PT, clen, tid);
-    rq.store(nullptr, 0, QT, PT, clen, tid);
-    ra.template store<true>(At, PT, tid);
+    rk.store(Ks, PK, nullptr, 0, clen, tid);
+    rq.store(Qs, PK, nullptr, 0, clen, tid);
+    ra.template store<false>(Am, PT, tid);
     if (tid < CH) {
         gx[tid] = gx_v;
         go[tid] = go_v;
@@ -618,13 +650,11 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             const int colc = cv ? col : r16;                     // in bounds for the unconditional loads
             f32x4 S[NKB], dSx[NKB], Vr[NB], dOr[NB], dXr[NB];
 #pragma unroll
-            for (int kt = 0; kt < NKB; ++kt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int64_t off = (int64_t)(16 * kt + 4 * g4 + j) * DV + colc;
-                    S[kt][j] = hsb[off];
-                    dSx[kt][j] = dhsb[off];
-                }
+            for (int kt = 0; kt < NKB; ++kt) {
+                const int64_t off = (int64_t)colc * DK + 16 * kt + 4 * g4;     // states are stored [dv][dk]
+                S[kt] = EL::tof(gfrag<E>(hsb + off));
+                dSx[kt] = EL::tof(gfrag<E>(dhsb + off));
+            }
 #pragma unroll
             for (int I = 0; I < NB; ++I)
 #pragma unroll
@@ -686,7 +716,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                     [&](int kb) { return tef[I * NB + kb]; },
                     [&](int kb) { return Xb[kb]; });
                 Y[I] = contract(Y[I], NB,
-                    [&](int kb) { return ld_frag<E>(At + (16 * I + r16) * PT + 16 * kb + 4 * g4); },
+                    [&](int kb) { return ld_colfrag<E>(Am, PT, 16 * kb, 16 * I, lane); },
                     [&](int kb) { return dOb[kb]; });
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -730,7 +760,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 
     // ---- CH x CH phase ----------------------------------------------------
     for (int i = tid; i < 3 * CH * PF; i += NT) Fn[i] = 0.f;   // N, dTE, T0 (written by lower tiles)
-    for (int i = tid; i < 3 * CH * PT; i += NT) WA[i] = EL::from_f(0.f);
+    for (int i = tid; i < 2 * CH * PT; i += NT) WA[i] = EL::from_f(0.f);
     rte.template store<false>(Fte, PF, tid);
     {
         const float t = sum64(gcacc);
@@ -818,7 +848,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         }
     }
     __syncthreads();
-    // dM = -strict_lower(Z TE^T): the M terms of dbeta and dgamma, W_N + W_N^T -> WS; W_A -> WA, WA^T
+    // dM = -strict_lower(Z TE^T): the M terms of dbeta and dgamma, W_N + W_N^T -> WS; W_A -> WA
 #pragma unroll
     for (int s = 0; s < LPW; ++s) {
         const int l = wave + NW * s;
@@ -847,7 +877,6 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 if (jj <= i) {
                     const E wa = EL::from_f(aA[s][j]);
                     WA[i * PT + jj] = wa;
-                    WAt[jj * PT + i] = wa;
                 }
             }
         }
@@ -863,7 +892,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int i = 16 * Iw + 4 * g4 + j;
-                const float qv = EL::to_f(QT[d * PT + i]), kv = EL::to_f(Ks[i * PK + d]);
+                const float qv = EL::to_f(Qs[i * PK + d]), kv = EL::to_f(Ks[i * PK + d]);
                 rq[j] += qv * aQ[s][j];
                 rx[j] += kv * aX[s][j];
                 re[j] += kv * aE[s][j];
@@ -887,13 +916,13 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         const int J = J0 + s;
         f32x4 q = contract(aQ[s] * GOr, NB,
             [&](int kb) { return ld_frag<E>(WA + (16 * Iw + r16) * PT + 16 * kb + 4 * g4); },
-            [&](int kb) { return ld_frag<E>(KT + (16 * J + r16) * PT + 16 * kb + 4 * g4); });
+            [&](int kb) { return ld_colfrag<E>(Ks, PK, 16 * kb, 16 * J, lane); });
         f32x4 k = contract(aE[s] * GEr - aX[s] * GXr, NB,
-            [&](int kb) { return ld_frag<E>(WAt + (16 * Iw + r16) * PT + 16 * kb + 4 * g4); },
-            [&](int kb) { return ld_frag<E>(QT + (16 * J + r16) * PT + 16 * kb + 4 * g4); });
+            [&](int kb) { return ld_colfrag<E>(WA, PT, 16 * kb, 16 * Iw, lane); },
+            [&](int kb) { return ld_colfrag<E>(Qs, PK, 16 * kb, 16 * J, lane); });
         k = contract(k, NB,
             [&](int kb) { return ld_frag<E>(WS + (16 * Iw + r16) * PT + 16 * kb + 4 * g4); },
-            [&](int kb) { return ld_frag<E>(KT + (16 * J + r16) * PT + 16 * kb + 4 * g4); });
+            [&](int kb) { return ld_colfrag<E>(Ks, PK, 16 * kb, 16 * J, lane); });
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int i = 16 * Iw + 4 * g4 + j;

@@ -1,6 +1,7 @@
 // Layout of the per-(chunk, head) blocks chunk_prep_kernel leaves in the
-// workspace, and the sequence geometry helpers, shared by the forward chunk
-// kernels (gdr_chunk.hip) and the backward ones (gdr_chunk_bwd.hip).
+// workspace, the sequence geometry helpers and the LDS transpose read, shared
+// by the forward chunk kernels (gdr_chunk.hip) and the backward ones
+// (gdr_chunk_bwd.hip).
 #pragma once
 
 #include "gdr_common.hpp"
@@ -66,6 +67,22 @@ __device__ __forceinline__ int64_t chunk_base(const SeqGeom &g, int seq) {
 template <typename E>
 __device__ __forceinline__ typename Elem<E>::frag gfrag(const E *p) {
     return *reinterpret_cast<const typename Elem<E>::frag *>(p);
+}
+
+// gfx950 ds_read_b64_tr_b16: within each 16-lane group, source lane s gives the
+// address of 4 consecutive 16-bit elements, and result lane d receives element
+// d % 4 of source lanes d / 4 + 4 i (i = 0..3).  With source lane s pointing at
+// row k0 + s / 4, columns c0 + 4 (s % 4) of a row-major tile, lane d receives
+// rows k0 .. k0 + 3 of column c0 + d: the C-layout / B-operand fragment of the
+// tile, or the A-operand fragment of its transpose, read straight from
+// row-major storage.
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s16x4 lds_tr16(const void *p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)const_cast<void *>(p));
+}
+template <typename E>
+__device__ __forceinline__ typename Elem<E>::frag ld_tr(const E *p) {
+    return __builtin_bit_cast(typename Elem<E>::frag, lds_tr16(p));
 }
 
 }  // namespace vgdr

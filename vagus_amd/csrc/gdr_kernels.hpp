@@ -104,8 +104,8 @@ struct ChunkBwdParams {
     float *dbeta;                 // [n_tokens, H]
     float *dh0;                   // [n_seqs, H, dk, dv] or NULL
     const void *blocks;           // chunk_prep's per-(chunk, head) blocks
-    float *hs;                    // [chunk slots, H, dk, dv] each chunk's entry state
-    float *dhs;                   // [chunk slots, H, dk, dv] gradient of each chunk's exit state
+    void *hs;                     // [chunk slots, H, dv, dk] each chunk's entry state (element type, transposed)
+    void *dhs;                    // [chunk slots, H, dv, dk] gradient of each chunk's exit state (same)
     int H, DV;
     int n_tiles;                  // dv tiles of the walk kernels (set by the launcher)
     int n_chunk_slots;
