@@ -498,8 +498,8 @@ struct GradLayout {
     static constexpr int PERS = 2 * CH * PK * ES;
     // column phase: A; X, U, dU, dO, dX rows of the block; S, dS' rows of the block
     static constexpr int COLS = (CH * PT + 5 * CH * PD + 2 * DK * PD) * ES;
-    // CH x CH phase: four fp32 matrices; W_A and W_N + W_N^T in the element type
-    static constexpr int SQ = 4 * CH * PF * 4 + 2 * CH * PT * ES;
+    // CH x CH phase: N, dTE, T0 (then Z) in fp32; W_A, W_N + W_N^T and TE in the element type
+    static constexpr int SQ = 3 * CH * PF * 4 + 3 * CH * PT * ES;
     static constexpr int REGION = cmax(COLS, SQ);
     static constexpr int SMALL = 8 * CH * 4 + 64;
     static constexpr int BYTES = PERS + REGION + SMALL;
@@ -536,12 +536,12 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     E *Ss = dXs + CH * PD;
     E *dSs = Ss + DK * PD;
     // CH x CH phase
-    float *Fte = reinterpret_cast<float *>(R);
-    float *Fn = Fte + CH * PF;
+    float *Fn = reinterpret_cast<float *>(R);
     float *Fdte = Fn + CH * PF;
     float *Ft0 = Fdte + CH * PF;                  // T0, then Z
     E *WA = reinterpret_cast<E *>(Ft0 + CH * PF);
     E *WS = WA + CH * PT;
+    E *TEs = WS + CH * PT;                        // TE rows (lower tiles)
     float *sm = reinterpret_cast<float *>(R + L::REGION);
     float *gam = sm, *bet = sm + CH, *gx = sm + 2 * CH, *go = sm + 3 * CH, *ge = sm + 4 * CH;
     float *dgam = sm + 5 * CH, *dbet = sm + 6 * CH;
@@ -569,11 +569,10 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 
     // ---- stage: every load of the chunk issued at once --------------------
     RowRegs<E, CH, DK, NT> rk, rq;
-    BlockRegs<E, CH, NT> ra, rte;                              // A (-> LDS now), TE (-> fp32 later)
+    BlockRegs<E, CH, NT> ra;                                   // A
     rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
     rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
     ra.load(Ab, tid);
-    rte.load(TEb, tid);
     const int tc = tid < CH ? tid : 0, tg = tc < clen ? tc : 0;
     const float gx_v = gf[tc], go_v = gf[CH + tc], ge_v = gf[2 * CH + tc], gc_v = gf[3 * CH];
     const float be_v = p.beta[(t0 + tg) * H + h];
@@ -584,7 +583,9 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         J = l;
         while (J > I) { J -= I + 1; ++I; }
     };
-    // A at this wave's dA elements (the A terms of dgamma), and the TE fragments of U = TE X
+    // A at this wave's dA elements (the A terms of dgamma), and the TE fragments
+    // of U = TE X (lower tiles), later stored as TE rows for T0 = I - TE N and
+    // dM = -Z TE^T
     float aval[LPW][4];
 #pragma unroll
     for (int s = 0; s < LPW; ++s) {
@@ -759,9 +760,16 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     __syncthreads();                                           // the region now holds the CH x CH phase
 
     // ---- CH x CH phase ----------------------------------------------------
-    for (int i = tid; i < 3 * CH * PF; i += NT) Fn[i] = 0.f;   // N, dTE, T0 (written by lower tiles)
-    for (int i = tid; i < 2 * CH * PT; i += NT) WA[i] = EL::from_f(0.f);
-    rte.template store<false>(Fte, PF, tid);
+    // Every matrix is written tile by tile over the lower tiles (W_A and WS
+    // also over their mirror images) before it is read, and reads stay in the
+    // tiles written: no zero fill.  Row and column sums go through shuffles
+    // first, so each LDS atomic has distinct addresses across its lanes.
+    if (wave == 0) {
+#pragma unroll
+        for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int kb = 0; kb <= I; ++kb) st_frag<E>(TEs + (16 * I + r16) * PT + 16 * kb + 4 * g4, tef[I * NB + kb]);
+    }
     {
         const float t = sum64(gcacc);
         if (lane == 0 && wave < NCW) atomicAdd(&misc[1], misc[0] * t);     // Gc <S, dS'>
@@ -778,21 +786,28 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             const f32x4 kk = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
                 [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                 [&](int kt) { return ld_frag<E>(Ks + (16 * J + r16) * PK + 16 * kt + 4 * g4); });
+            float rs[4], cs = 0.f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int i = 16 * I + 4 * g4 + j;
                 const bool low = jj <= i;
                 const float D = low ? __expf(gam[i] - gam[jj]) : 0.f;
                 const float da = low ? aA[s][j] : 0.f;
-                const float v = low ? da * aval[s][j] : 0.f;
-                if (low) {
-                    atomicAdd(&dgam[i], v);
-                    atomicAdd(&dgam[jj], -v);
-                }
+                rs[j] = da * aval[s][j];
+                cs += rs[j];
                 aA[s][j] = p.scale * da * D;
                 Fdte[i * PF + jj] = low ? aT[s][j] : 0.f;
                 Fn[i * PF + jj] = jj < i ? kk[j] * D : 0.f;
             }
+            cs += __shfl_xor(cs, 16);
+            cs += __shfl_xor(cs, 32);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rs[j] = sum16(rs[j]);
+            if (r16 == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) atomicAdd(&dgam[16 * I + 4 * g4 + j], rs[j]);
+            }
+            if (g4 == 0) atomicAdd(&dgam[jj], -cs);
         }
     }
     __syncthreads();
@@ -805,7 +820,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             tile_of(l, I, J);
             f32x4 t = {0.f, 0.f, 0.f, 0.f};
             for (int kb = J; kb <= I; ++kb)
-                t = mfma_kb1(ld4(Fte + (16 * I + r16) * PF + 16 * kb + 4 * g4),
+                t = mfma_kb1(EL::tof(ld_frag<E>(TEs + (16 * I + r16) * PT + 16 * kb + 4 * g4)),
                              col4(Fn, PF, 16 * kb + 4 * g4, 16 * J + r16), t);
             const int jj = 16 * J + r16;
 #pragma unroll
@@ -858,27 +873,43 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             f32x4 m = {0.f, 0.f, 0.f, 0.f};
             for (int kb = 0; kb <= J; ++kb)
                 m = mfma_kb1(ld4(Fz + (16 * I + r16) * PF + 16 * kb + 4 * g4),
-                             ld4(Fte + (16 * J + r16) * PF + 16 * kb + 4 * g4), m);
+                             EL::tof(ld_frag<E>(TEs + (16 * J + r16) * PT + 16 * kb + 4 * g4)), m);
             const int jj = 16 * J + r16;
+            float rb[4], rg[4], cg = 0.f;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int i = 16 * I + 4 * g4 + j;
-                if (jj < i) {
-                    const float dm = -m[j];
-                    const float n = Fn[i * PF + jj];
-                    atomicAdd(&dbet[i], dm * n);
-                    const float dn = bet[i] * dm;
-                    atomicAdd(&dgam[i], dn * n);
-                    atomicAdd(&dgam[jj], -dn * n);
+                const bool strict = jj < i;
+                const float dm = strict ? -m[j] : 0.f;
+                const float n = Fn[i * PF + jj];                 // 0 off the strict lower triangle
+                const float dn = bet[i] * dm;
+                rb[j] = dm * n;
+                rg[j] = dn * n;
+                cg += dn * n;
+                if (strict) {
                     const E wn = EL::from_f(dn * __expf(gam[i] - gam[jj]));
                     WS[i * PT + jj] = wn;
                     WS[jj * PT + i] = wn;
                 }
-                if (jj <= i) {
-                    const E wa = EL::from_f(aA[s][j]);
-                    WA[i * PT + jj] = wa;
+                if (jj == i) WS[i * PT + i] = EL::from_f(0.f);
+                WA[i * PT + jj] = EL::from_f(jj <= i ? aA[s][j] : 0.f);
+                if (jj < i) WA[jj * PT + i] = EL::from_f(0.f);      // the upper tiles
+            }
+            cg += __shfl_xor(cg, 16);
+            cg += __shfl_xor(cg, 32);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                rb[j] = sum16(rb[j]);
+                rg[j] = sum16(rg[j]);
+            }
+            if (r16 == 0) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    atomicAdd(&dbet[16 * I + 4 * g4 + j], rb[j]);
+                    atomicAdd(&dgam[16 * I + 4 * g4 + j], rg[j]);
                 }
             }
+            if (g4 == 0) atomicAdd(&dgam[jj], -cg);
         }
     }
     __syncthreads();
