@@ -493,13 +493,14 @@ struct GradLayout {
     static constexpr int ES = sizeof(E), VE = 16 / ES;
     static constexpr int NCW = ES == 2 ? 4 : 2;               // waves of the column phase
     static constexpr int DVB = 16 * NCW;                      // dv columns per block
-    static constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value, PD = DVB + VE, PF = CH + 4;
-    // K and Q rows for the whole kernel
-    static constexpr int PERS = 2 * CH * PK * ES;
-    // column phase: A; X, U, dU, dO, dX rows of the block; S, dS' rows of the block
-    static constexpr int COLS = (CH * PT + 5 * CH * PD + 2 * DK * PD) * ES;
-    // CH x CH phase: N, dTE, T0 (then Z) in fp32; W_A, W_N + W_N^T and TE in the element type
-    static constexpr int SQ = 3 * CH * PF * 4 + 3 * CH * PT * ES;
+    static constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value, PF = CH + 4;
+    // K and Q rows, and TE rows (lower tiles), for the whole kernel
+    static constexpr int PERS = (2 * CH * PK + CH * PT) * ES;
+    // column phase: A; the block's columns of X, U, dU, dO, dX (CH tokens each)
+    // and of S, dS' (DK key channels each), stored column by column
+    static constexpr int COLS = (CH * PT + 5 * DVB * PT + 2 * DVB * PK) * ES;
+    // CH x CH phase: N, dTE, T0 (then Z) in fp32; W_A and W_N + W_N^T in the element type
+    static constexpr int SQ = 3 * CH * PF * 4 + 2 * CH * PT * ES;
     static constexpr int REGION = cmax(COLS, SQ);
     static constexpr int SMALL = 8 * CH * 4 + 64;
     static constexpr int BYTES = PERS + REGION + SMALL;
@@ -507,17 +508,20 @@ struct GradLayout {
     static constexpr bool FITS = BYTES <= 160 * 1024;
 };
 
+// Eight waves, two per SIMD: the kernel's phases are chains of short products
+// with LDS round trips in between, and a second wave on each SIMD covers them
+// (one workgroup per CU: its LDS is above half of the CU's).
 template <int DK, int CH, typename E>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 chunk_grad_kernel(const ChunkBwdParams p) {
     using L = GradLayout<DK, CH, E>;
     static_assert(L::FITS, "LDS budget exceeded");
     using EL = Elem<E>;
     using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, 1>;
-    constexpr int NT = 256, NW = 4, NB = CH / 16, NKB = DK / 16;
+    constexpr int NT = 512, NW = 8, NB = CH / 16, NKB = DK / 16, NBH = NB / 2;
     constexpr int NCW = L::NCW, DVB = L::DVB, NKD = DVB / 16;
-    constexpr int PK = L::PK, PT = L::PT, PD = L::PD, PF = L::PF;
+    constexpr int PK = L::PK, PT = L::PT, PF = L::PF;
     constexpr int NL = NB * (NB + 1) / 2, LPW = (NL + NW - 1) / NW;   // lower CH x CH tiles, per wave
     static_assert(NW % NB == 0, "a row block is split over whole waves");
     constexpr int JPW = NB * NKB / NW;                                 // CH x DK tiles per wave
@@ -525,23 +529,23 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     __shared__ __attribute__((aligned(16))) char smem[L::BYTES];
     E *Ks = reinterpret_cast<E *>(smem);
     E *Qs = Ks + CH * PK;
+    E *TEs = Qs + CH * PK;                        // TE rows (zero above the diagonal)
     char *R = smem + L::PERS;
     // column phase
     E *Am = reinterpret_cast<E *>(R);
-    E *Xs = Am + CH * PT;
-    E *Us = Xs + CH * PD;
-    E *Ys = Us + CH * PD;
-    E *dOs = Ys + CH * PD;
-    E *dXs = dOs + CH * PD;
-    E *Ss = dXs + CH * PD;
-    E *dSs = Ss + DK * PD;
+    E *Xs = Am + CH * PT;                         // Xs[c][t] = X[t][c], c a column of the block
+    E *Us = Xs + DVB * PT;
+    E *Ys = Us + DVB * PT;
+    E *dOs = Ys + DVB * PT;
+    E *dXs = dOs + DVB * PT;
+    E *Ss = dXs + DVB * PT;                       // Ss[c][d] = S[d][c]
+    E *dSs = Ss + DVB * PK;
     // CH x CH phase
     float *Fn = reinterpret_cast<float *>(R);
     float *Fdte = Fn + CH * PF;
     float *Ft0 = Fdte + CH * PF;                  // T0, then Z
     E *WA = reinterpret_cast<E *>(Ft0 + CH * PF);
     E *WS = WA + CH * PT;
-    E *TEs = WS + CH * PT;                        // TE rows (lower tiles)
     float *sm = reinterpret_cast<float *>(R + L::REGION);
     float *gam = sm, *bet = sm + CH, *gx = sm + 2 * CH, *go = sm + 3 * CH, *ge = sm + 4 * CH;
     float *dgam = sm + 5 * CH, *dbet = sm + 6 * CH;
@@ -569,10 +573,11 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 
     // ---- stage: every load of the chunk issued at once --------------------
     RowRegs<E, CH, DK, NT> rk, rq;
-    BlockRegs<E, CH, NT> ra;                                   // A
+    BlockRegs<E, CH, NT> ra, rte;                              // A, TE
     rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
     rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
     ra.load(Ab, tid);
+    rte.load(TEb, tid);
     const int tc = tid < CH ? tid : 0, tg = tc < clen ? tc : 0;
     const float gx_v = gf[tc], go_v = gf[CH + tc], ge_v = gf[2 * CH + tc], gc_v = gf[3 * CH];
     const float be_v = p.beta[(t0 + tg) * H + h];
@@ -583,9 +588,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         J = l;
         while (J > I) { J -= I + 1; ++I; }
     };
-    // A at this wave's dA elements (the A terms of dgamma), and the TE fragments
-    // of U = TE X (lower tiles), later stored as TE rows for T0 = I - TE N and
-    // dM = -Z TE^T
+    // A at this wave's dA elements (the A terms of dgamma)
     float aval[LPW][4];
 #pragma unroll
     for (int s = 0; s < LPW; ++s) {
@@ -598,14 +601,41 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             aval[s][j] = EL::to_f(Ab[blk_pos<NB>(i, jj <= i ? jj : i)]);
         }
     }
-    F tef[NB * NB];
+    // Column block c (16 columns of a dv block, c < NCW) belongs to waves c
+    // and c + 4: both hold its S, dS' columns; wave c + 4 h computes X, U, dU
+    // for token blocks h NBH .. h NBH + NBH - 1.  Their global operands are
+    // loaded a dv block ahead: block 0 with the staging loads, block db + 1
+    // during block db's products.
+    const int cwave = wave & 3, half = wave >> 2;
+    const bool colw_ok = cwave < NCW;
+    F cS[NKB], cdS[NKB];
+    E cV[NBH][4], cdO[NBH][4], cdX[NBH][4];
+    auto colload = [&](int db) __attribute__((always_inline)) {
+        if (!colw_ok) return;
+        const int colw = db * DVB + 16 * cwave;
+        const int colc = colw < DV ? colw + r16 : r16;         // in bounds for the unconditional loads
 #pragma unroll
-    for (int I = 0; I < NB; ++I)
+        for (int kt = 0; kt < NKB; ++kt) {
+            const int64_t off = (int64_t)colc * DK + 16 * kt + 4 * g4;         // states are stored [dv][dk]
+            cS[kt] = gfrag<E>(hsb + off);
+            cdS[kt] = gfrag<E>(dhsb + off);
+        }
 #pragma unroll
-        for (int kb = 0; kb <= I; ++kb) tef[I * NB + kb] = gfrag<E>(TEb + frag_pos<NB>(I, kb, lane));
+        for (int ii = 0; ii < NBH; ++ii)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int row = 16 * (half * NBH + ii) + 4 * g4 + j;
+                const int64_t off = (t0 + (row < clen ? row : 0)) * sv + (int64_t)h * DV + colc;
+                cV[ii][j] = reinterpret_cast<const E *>(p.v)[off];
+                cdO[ii][j] = reinterpret_cast<const E *>(p.dout)[off];
+                cdX[ii][j] = reinterpret_cast<const E *>(p.dv)[off];
+            }
+    };
+    colload(0);
     rk.store(Ks, PK, nullptr, 0, clen, tid);
     rq.store(Qs, PK, nullptr, 0, clen, tid);
     ra.template store<false>(Am, PT, tid);
+    rte.template store<false>(TEs, PT, tid);
     if (tid < CH) {
         gx[tid] = gx_v;
         go[tid] = go_v;
@@ -630,9 +660,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     __syncthreads();
 
     // ---- column phase: dv blocks of DVB columns ---------------------------
-    // wave w < NCW computes X, U, dU (and loads S, dS', dO, dX) for columns
-    // 16 w .. 16 w + 15 of the block; then every wave accumulates its tiles of
-    // the products that contract over dv.
+    // then every wave accumulates its tiles of the products that contract over dv
     f32x4 aQ[JPW], aX[JPW], aE[JPW];                           // dO S^T, dX S^T, U dS'^T
     f32x4 aA[LPW], aT[LPW];                                    // dO U^T, dU X^T (lower tiles)
 #pragma unroll
@@ -641,106 +669,78 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     for (int s = 0; s < LPW; ++s) aA[s] = aT[s] = f32x4{0.f, 0.f, 0.f, 0.f};
     float gcacc = 0.f;
     const int ndb = (DV + DVB - 1) / DVB;
+    const int cw = 16 * cwave + r16;                           // column within the block
     for (int db = 0; db < ndb; ++db) {
-        const int cb = db * DVB;
         if (db > 0) __syncthreads();                           // the previous block's reads are done
-        if (wave < NCW) {
-            const int cw = 16 * wave + r16;                      // column within the block
-            const int col = cb + cw;
-            const bool cv = cb + 16 * wave < DV;
-            const int colc = cv ? col : r16;                     // in bounds for the unconditional loads
-            f32x4 S[NKB], dSx[NKB], Vr[NB], dOr[NB], dXr[NB];
-#pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) {
-                const int64_t off = (int64_t)colc * DK + 16 * kt + 4 * g4;     // states are stored [dv][dk]
-                S[kt] = EL::tof(gfrag<E>(hsb + off));
-                dSx[kt] = EL::tof(gfrag<E>(dhsb + off));
-            }
-#pragma unroll
-            for (int I = 0; I < NB; ++I)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = 16 * I + 4 * g4 + j;
-                    const int64_t off = (t0 + (row < clen ? row : 0)) * sv + (int64_t)h * DV + colc;
-                    Vr[I][j] = EL::to_f(reinterpret_cast<const E *>(p.v)[off]);
-                    dOr[I][j] = EL::to_f(reinterpret_cast<const E *>(p.dout)[off]);
-                    dXr[I][j] = EL::to_f(reinterpret_cast<const E *>(p.dv)[off]);
-                }
-            if (!cv) {
-#pragma unroll
-                for (int kt = 0; kt < NKB; ++kt) S[kt] = dSx[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
+        f32x4 Y0[NBH];
+        if (colw_ok) {
+            const bool cv = db * DVB + 16 * cwave < DV;
             F Sb[NKB], dSb[NKB];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) {
-                gcacc += S[kt][0] * dSx[kt][0] + S[kt][1] * dSx[kt][1] + S[kt][2] * dSx[kt][2] +
-                         S[kt][3] * dSx[kt][3];
-                Sb[kt] = EL::cvt(S[kt]);
-                dSb[kt] = EL::cvt(dSx[kt]);
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    Ss[(16 * kt + 4 * g4 + j) * PD + cw] = EL::from_f(S[kt][j]);
-                    dSs[(16 * kt + 4 * g4 + j) * PD + cw] = EL::from_f(dSx[kt][j]);
+                Sb[kt] = cv ? cS[kt] : F{};
+                dSb[kt] = cv ? cdS[kt] : F{};
+                if (half == 0) {
+                    const f32x4 a = EL::tof(Sb[kt]), b = EL::tof(dSb[kt]);
+                    gcacc += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+                }
+                if (kt / (NKB / 2) == half) {                  // this half's key rows of the S, dS' columns
+                    st_frag<E>(Ss + cw * PK + 16 * kt + 4 * g4, Sb[kt]);
+                    st_frag<E>(dSs + cw * PK + 16 * kt + 4 * g4, dSb[kt]);
                 }
             }
-            F Xb[NB], dOb[NB];
-            f32x4 X[NB], Y[NB];
 #pragma unroll
-            for (int I = 0; I < NB; ++I) {
+            for (int ii = 0; ii < NBH; ++ii) {
+                const int I = half * NBH + ii;
                 const f32x4 P = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return Sb[kt]; });
                 const f32x4 P2 = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return dSb[kt]; });
-                f32x4 dO;
+                f32x4 X, dO, dx;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int row = 16 * I + 4 * g4 + j;
                     const bool ok = cv && row < clen;
-                    const float v = ok ? Vr[I][j] : 0.f;
-                    dO[j] = ok ? dOr[I][j] : 0.f;
-                    const float dx = ok ? dXr[I][j] : 0.f;
-                    X[I][j] = v - gx[row] * P[j];
-                    Y[I][j] = ge[row] * P2[j];
-                    Xs[row * PD + cw] = EL::from_f(X[I][j]);
-                    dOs[row * PD + cw] = EL::from_f(dO[j]);
-                    dXs[row * PD + cw] = EL::from_f(dx);
+                    dO[j] = ok ? EL::to_f(cdO[ii][j]) : 0.f;
+                    dx[j] = ok ? EL::to_f(cdX[ii][j]) : 0.f;
+                    X[j] = (ok ? EL::to_f(cV[ii][j]) : 0.f) - gx[row] * P[j];
+                    Y0[ii][j] = ge[row] * P2[j];
                 }
-                Xb[I] = EL::cvt(X[I]);
-                dOb[I] = EL::cvt(dO);
-            }
-#pragma unroll
-            for (int I = 0; I < NB; ++I) {
-                // U = TE X ;  dU = A^T dO + diag(GE) K dS'
-                const f32x4 U = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
-                    [&](int kb) { return tef[I * NB + kb]; },
-                    [&](int kb) { return Xb[kb]; });
-                Y[I] = contract(Y[I], NB,
-                    [&](int kb) { return ld_colfrag<E>(Am, PT, 16 * kb, 16 * I, lane); },
-                    [&](int kb) { return dOb[kb]; });
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = 16 * I + 4 * g4 + j;
-                    Us[row * PD + cw] = EL::from_f(U[j]);
-                    Ys[row * PD + cw] = EL::from_f(Y[I][j]);
-                }
+                st_frag<E>(Xs + cw * PT + 16 * I + 4 * g4, EL::cvt(X));
+                st_frag<E>(dOs + cw * PT + 16 * I + 4 * g4, EL::cvt(dO));
+                st_frag<E>(dXs + cw * PT + 16 * I + 4 * g4, EL::cvt(dx));
             }
         }
+        __syncthreads();                                       // X and dO of both halves in LDS
+        if (colw_ok) {
+#pragma unroll
+            for (int ii = 0; ii < NBH; ++ii) {
+                // U = TE X ;  dU = A^T dO + diag(GE) K dS'
+                const int I = half * NBH + ii;
+                const f32x4 U = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
+                    [&](int kb) { return ld_frag<E>(TEs + (16 * I + r16) * PT + 16 * kb + 4 * g4); },
+                    [&](int kb) { return ld_frag<E>(Xs + cw * PT + 16 * kb + 4 * g4); });
+                const f32x4 Y = contract(Y0[ii], NB,
+                    [&](int kb) { return ld_colfrag<E>(Am, PT, 16 * kb, 16 * I, lane); },
+                    [&](int kb) { return ld_frag<E>(dOs + cw * PT + 16 * kb + 4 * g4); });
+                st_frag<E>(Us + cw * PT + 16 * I + 4 * g4, EL::cvt(U));
+                st_frag<E>(Ys + cw * PT + 16 * I + 4 * g4, EL::cvt(Y));
+            }
+        }
+        if (db + 1 < ndb) colload(db + 1);
         __syncthreads();
         // products contracting over the block's columns
 #pragma unroll
         for (int s = 0; s < JPW; ++s) {
             const int J = J0 + s;
-            aQ[s] = contract(aQ[s], NKD,
-                [&](int kb) { return ld_frag<E>(dOs + (16 * Iw + r16) * PD + 16 * kb + 4 * g4); },
-                [&](int kb) { return ld_frag<E>(Ss + (16 * J + r16) * PD + 16 * kb + 4 * g4); });
-            aX[s] = contract(aX[s], NKD,
-                [&](int kb) { return ld_frag<E>(dXs + (16 * Iw + r16) * PD + 16 * kb + 4 * g4); },
-                [&](int kb) { return ld_frag<E>(Ss + (16 * J + r16) * PD + 16 * kb + 4 * g4); });
-            aE[s] = contract(aE[s], NKD,
-                [&](int kb) { return ld_frag<E>(Us + (16 * Iw + r16) * PD + 16 * kb + 4 * g4); },
-                [&](int kb) { return ld_frag<E>(dSs + (16 * J + r16) * PD + 16 * kb + 4 * g4); });
+            aQ[s] = contract(aQ[s], NKD, [&](int kb) { return ld_colfrag<E>(dOs, PT, 16 * kb, 16 * Iw, lane); },
+                             [&](int kb) { return ld_colfrag<E>(Ss, PK, 16 * kb, 16 * J, lane); });
+            aX[s] = contract(aX[s], NKD, [&](int kb) { return ld_colfrag<E>(dXs, PT, 16 * kb, 16 * Iw, lane); },
+                             [&](int kb) { return ld_colfrag<E>(Ss, PK, 16 * kb, 16 * J, lane); });
+            aE[s] = contract(aE[s], NKD, [&](int kb) { return ld_colfrag<E>(Us, PT, 16 * kb, 16 * Iw, lane); },
+                             [&](int kb) { return ld_colfrag<E>(dSs, PK, 16 * kb, 16 * J, lane); });
         }
 #pragma unroll
         for (int s = 0; s < LPW; ++s) {
@@ -748,12 +748,10 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             if (l < NL) {
                 int I, J;
                 tile_of(l, I, J);
-                aA[s] = contract(aA[s], NKD,
-                    [&](int kb) { return ld_frag<E>(dOs + (16 * I + r16) * PD + 16 * kb + 4 * g4); },
-                    [&](int kb) { return ld_frag<E>(Us + (16 * J + r16) * PD + 16 * kb + 4 * g4); });
-                aT[s] = contract(aT[s], NKD,
-                    [&](int kb) { return ld_frag<E>(Ys + (16 * I + r16) * PD + 16 * kb + 4 * g4); },
-                    [&](int kb) { return ld_frag<E>(Xs + (16 * J + r16) * PD + 16 * kb + 4 * g4); });
+                aA[s] = contract(aA[s], NKD, [&](int kb) { return ld_colfrag<E>(dOs, PT, 16 * kb, 16 * I, lane); },
+                                 [&](int kb) { return ld_colfrag<E>(Us, PT, 16 * kb, 16 * J, lane); });
+                aT[s] = contract(aT[s], NKD, [&](int kb) { return ld_colfrag<E>(Ys, PT, 16 * kb, 16 * I, lane); },
+                                 [&](int kb) { return ld_colfrag<E>(Xs, PT, 16 * kb, 16 * J, lane); });
             }
         }
     }
@@ -764,12 +762,6 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     // also over their mirror images) before it is read, and reads stay in the
     // tiles written: no zero fill.  Row and column sums go through shuffles
     // first, so each LDS atomic has distinct addresses across its lanes.
-    if (wave == 0) {
-#pragma unroll
-        for (int I = 0; I < NB; ++I)
-#pragma unroll
-            for (int kb = 0; kb <= I; ++kb) st_frag<E>(TEs + (16 * I + r16) * PT + 16 * kb + 4 * g4, tef[I * NB + kb]);
-    }
     {
         const float t = sum64(gcacc);
         if (lane == 0 && wave < NCW) atomicAdd(&misc[1], misc[0] * t);     // Gc <S, dS'>
@@ -999,7 +991,7 @@ static hipError_t run_bwd(ChunkBwdParams p, hipStream_t stream) {
     }
     const int64_t grad_blocks = (int64_t)p.n_chunk_slots * p.H;
     if (grad_blocks > 0)
-        hipLaunchKernelGGL((chunk_grad_kernel<DK, CH, E>), dim3((unsigned)grad_blocks), dim3(256), 0, stream, p);
+        hipLaunchKernelGGL((chunk_grad_kernel<DK, CH, E>), dim3((unsigned)grad_blocks), dim3(512), 0, stream, p);
     return hipGetLastError();
 }
 
