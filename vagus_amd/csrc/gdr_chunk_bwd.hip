@@ -978,16 +978,19 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 template <int DK, int CH, typename E>
 static hipError_t run_bwd(ChunkBwdParams p, hipStream_t stream) {
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
-    // four waves per workgroup: the walks stage K, Q, TE and A through
-    // registers one chunk ahead, and at two waves that buffer pushed the
-    // dS walk into register spills (measured 1.86 ms vs 1.51 ms at B8 T4096 H8 d128)
-    constexpr int nw = 4;
-    p.n_tiles = (p.DV + 16 * nw - 1) / (16 * nw);
-    const int64_t walk_blocks = (units + 7) / 8 * 8 * p.n_tiles;
-    if (walk_blocks > 0) {
-        hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, nw, E>), dim3((unsigned)walk_blocks), dim3(64 * nw), 0, stream, p);
-        hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, nw, E>), dim3((unsigned)walk_blocks), dim3(64 * nw), 0, stream,
-                           p);
+    // The entry-state walk runs two waves (32-column tiles: 256 workgroups at
+    // B = 8, H = 8, dv = 128) and the dS walk four: the dS walk's one-chunk-ahead
+    // buffers of K, Q, TE and A spill at two waves (measured at B8 T4096 H8
+    // d128: dS walk 1.86 -> 1.51 ms whole backward with four; entry walk 243 ->
+    // 202 us with two).
+    if (units > 0) {
+        ChunkBwdParams ph = p;
+        ph.n_tiles = (p.DV + 31) / 32;
+        hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * ph.n_tiles)),
+                           dim3(128), 0, stream, ph);
+        p.n_tiles = (p.DV + 63) / 64;
+        hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 4, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
+                           dim3(256), 0, stream, p);
     }
     const int64_t grad_blocks = (int64_t)p.n_chunk_slots * p.H;
     if (grad_blocks > 0)
