@@ -35,6 +35,10 @@ Also reported on the same line:
                 340M prefill shape (GB/s over HBM peak), and the fully fused
                 decode step (conv + caches, L2 norm, beta sigmoid, recurrence,
                 epilogue) at the decode shape
+  backward      the chunked backward at the headline shape (all six
+                gradients), against the reference's count for the backward:
+                2 x 180,224 FLOP per token-head (chunk_scan_flops counts
+                forward + backward as 3 x the forward)
   kda, varlen   KDA prefill (B=4 T=8192 H=8) and packed GDN prefill (32
                 segments U[128, 8192], H=16) tokens/s and TFLOP/s
   cpu_baseline  the oracle's torch fp32 chunk form (the reference's CPU path)
@@ -236,6 +240,32 @@ def bench_layer_kernels(torch, ops, workloads, steps, warmup):
     }
 
 
+def bench_backward(torch, ops, workloads, steps, warmup):
+    """The chunked backward (vgdr_chunk_bwd through ops.chunk_gated_delta_rule_bwd)
+    at the headline shape: gradients of o and the final state with respect to
+    q, k, v, g, beta and the entry state, two rotating input copies."""
+    g = torch.Generator(device='cpu').manual_seed(12)
+    xs = [workloads.workload('gdn_340m', device='cuda') for _ in range(2)]
+    dos = [torch.randn(*x.v.shape, generator=g).bfloat16().cuda() for x in xs]
+    dST = torch.randn(*xs[0].initial_state.shape, generator=g).cuda()
+
+    def step(i):
+        x = xs[i % 2]
+        ops.chunk_gated_delta_rule_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, dos[i % 2], dST,
+                                       scale=DK ** -0.5)
+
+    us = _event_us(torch, step, steps, warmup)
+    x0 = xs[0]
+    th = x0.q.shape[0] * x0.q.shape[1] * x0.q.shape[2]
+    del xs, dos
+    tflops = th * 2 * FLOP_PER_TOKEN_HEAD / (us * 1e-6) / 1e12
+    return {'workload': 'gdn_340m backward: dq, dk, dv, dg, dbeta, dh0 from do and dht, B8 T4096 H8 dk=dv=128 bf16',
+            'kernels': 'chunk_prep_kernel + chunk_hs_kernel + chunk_dhs_kernel + chunk_grad_kernel',
+            'us': round(us, 1), 'tok_s': round(x0.q.shape[0] * x0.q.shape[1] / (us * 1e-6), 1),
+            'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
+            'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5)}
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's torch fp32 chunk form over the full headline workload."""
     from oracle import gdr
@@ -289,6 +319,7 @@ def main():
     ap.add_argument('--decode-only', action='store_true', help='only the decode step (for profiling)')
     ap.add_argument('--layer-only', action='store_true',
                     help='only the short conv, output epilogue and fused decode step (for profiling)')
+    ap.add_argument('--backward-only', action='store_true', help='only the chunked backward (for profiling)')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a plain 1 GiB device copy (x5): the reference point that scales '
                          'rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes')
@@ -312,6 +343,9 @@ def main():
         print(json.dumps({'calibrate_copy_bytes': src.numel() * 4, 'launches': 5}), flush=True)
         return
 
+    if args.backward_only:
+        print(json.dumps(bench_backward(torch, ops, workloads, args.steps, args.warmup)), flush=True)
+        return
     if args.layer_only:
         print(json.dumps(bench_layer_kernels(torch, ops, workloads, args.steps, args.warmup)), flush=True)
         return
@@ -333,6 +367,8 @@ def main():
                            'traffic': measured_traffic('decode_b64_h16', 'recurrent')}
         log('[bench] layer kernels: short conv, output epilogue, fused decode step')
         extra['layer_kernels'] = bench_layer_kernels(torch, ops, workloads, args.steps, args.warmup)
+        log('[bench] backward gdn_340m')
+        extra['backward'] = bench_backward(torch, ops, workloads, max(5, args.steps // 4), max(3, args.warmup // 10))
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
             r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))

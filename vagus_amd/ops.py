@@ -208,11 +208,52 @@ class _Call:
         return S[:, :, :self.dk, :self.dv].contiguous()
 
 
+def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, cu_seqlens=None,
+                               chunk_size=64):
+    """Backward of chunk_gated_delta_rule without autograd (vgdr_chunk_bwd):
+    the gradients of (o, final_state) under the cotangents do (and dht, None =
+    zero) with respect to q, k, v, g, beta and initial_state, for the delta
+    rule with a scalar gate (g (B, T, H)) or none (g None).  q, k as the
+    forward scanned them (normalised), beta in [0, 1].  Returns (dq, dk, dv,
+    dg, dbeta, dh0) in the inputs' dtypes; dg is None without a gate and dh0
+    None without an initial state.  The gradients the reference's training
+    takes through chunk_scan (linear_attention.py:237-309) or fla's backward."""
+    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate='scalar' if g is not None else 'none', delta=True,
+              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+    scale = c.dk ** -0.5 if scale is None else float(scale)
+    assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
+    _check_device(do, dht)
+    dop = _aligned(_pad_to(do.to(c.dtype), {1: c.dvp}))
+    dSp = None if dht is None else _aligned(_pad_to(dht.float(), {1: c.dvp, 2: c.dkp}))
+    new = lambda *shape, dt=torch.float32: torch.empty(*shape, dtype=dt, device=c.device)
+    dq, dk = new(c.B, c.T, c.H, c.dkp, dt=c.dtype), new(c.B, c.T, c.H, c.dkp, dt=c.dtype)
+    dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
+    dg = new(c.B, c.T, c.H) if g is not None else None
+    db = new(c.B, c.T, c.H)
+    dS0 = new(c.N, c.H, c.dkp, c.dvp) if initial_state is not None else None
+    L = _lib.load()
+    dtype = _DTYPES[c.dtype]
+    nbytes = L.vgdr_chunk_bwd_workspace_size(dtype, c.gate_kind, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
+                                             int(c.cu is not None), int(chunk_size))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+    with torch.cuda.device(c.device):
+        _lib.check(L.vgdr_chunk_bwd(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g), _ptr(c.beta),
+                                    _ptr(c.h0), _ptr(dop), _ptr(dSp), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg),
+                                    _ptr(db), _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes, c.B, c.T, c.H, c.dkp, c.dvp,
+                                    c.N, scale, int(chunk_size), _stream(c.device)))
+    if c.dkp != c.dk:
+        dq, dk = dq[..., :c.dk], dk[..., :c.dk]
+    if c.dvp != c.dv:
+        dv = dv[..., :c.dv]
+    if dS0 is not None:
+        dS0 = c.unpad_state(dS0).to(initial_state.dtype)
+    return dq, dk, dv, None if dg is None else dg.to(g.dtype), db.to(beta.dtype), dS0
+
+
 class _ChunkDeltaRule(torch.autograd.Function):
     """The chunked delta rule with a scalar gate or none, differentiable:
-    forward vgdr_chunk_fwd, backward vgdr_chunk_bwd (the gradients the
-    reference's training takes through chunk_scan, linear_attention.py:237-309,
-    or fla's chunk backward).  q, k arrive normalised, beta in [0, 1]."""
+    forward vgdr_chunk_fwd, backward vgdr_chunk_bwd.  q, k arrive normalised,
+    beta in [0, 1]."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, S0, scale, cu, chunk_size):
@@ -225,36 +266,11 @@ class _ChunkDeltaRule(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do, dS):
         q, k, v, g, beta, S0, cu = ctx.saved_tensors
-        c = _Call(q, k, v, g, beta, S0, cu, gate='scalar' if g is not None else 'none', delta=True,
-                  dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
         if do is None:
-            do = torch.zeros(c.B, c.T, c.H, c.dv, dtype=c.dtype, device=c.device)
-        dop = _aligned(_pad_to(do.to(c.dtype), {1: c.dvp}))
-        dSp = None if dS is None else _aligned(_pad_to(dS.float(), {1: c.dvp, 2: c.dkp}))
-        new = lambda *shape, dt=torch.float32: torch.empty(*shape, dtype=dt, device=c.device)
-        dq, dk = new(c.B, c.T, c.H, c.dkp, dt=c.dtype), new(c.B, c.T, c.H, c.dkp, dt=c.dtype)
-        dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
-        dg = new(c.B, c.T, c.H) if g is not None else None
-        db = new(c.B, c.T, c.H)
-        dS0 = new(c.N, c.H, c.dkp, c.dvp) if S0 is not None else None
-        L = _lib.load()
-        dtype = _DTYPES[c.dtype]
-        nbytes = L.vgdr_chunk_bwd_workspace_size(dtype, c.gate_kind, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
-                                                 int(c.cu is not None), int(ctx.chunk_size))
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
-        with torch.cuda.device(c.device):
-            _lib.check(L.vgdr_chunk_bwd(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
-                                        _ptr(c.beta), _ptr(c.h0), _ptr(dop), _ptr(dSp), _ptr(dq), _ptr(dk),
-                                        _ptr(dv), _ptr(dg), _ptr(db), _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes,
-                                        c.B, c.T, c.H, c.dkp, c.dvp, c.N, float(ctx.scale), int(ctx.chunk_size),
-                                        _stream(c.device)))
-        if c.dkp != c.dk:
-            dq, dk = dq[..., :c.dk], dk[..., :c.dk]
-        if c.dvp != c.dv:
-            dv = dv[..., :c.dv]
-        if dS0 is not None:
-            dS0 = c.unpad_state(dS0).to(S0.dtype)
-        return (dq, dk, dv, None if dg is None else dg.to(g.dtype), db.to(beta.dtype), dS0, None, None, None)
+            do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
+        grads = chunk_gated_delta_rule_bwd(q, k, v, g, beta, S0, do, dS, scale=ctx.scale, cu_seqlens=cu,
+                                           chunk_size=ctx.chunk_size)
+        return grads + (None, None, None)
 
 
 def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None, output_final_state=False,
