@@ -9,7 +9,8 @@ combinations without a backward.
 GPU: every gradient (dq, dk, dv, dg, dbeta, dS0) at rel_l2 <= 1e-5 (fp32)
 or 2e-2 (bf16; the kernels round intermediates to bf16 as the forward does),
 dense with a partial last chunk, a padded head (dk = 100, dv = 48), a packed
-batch (empty, one-token and multi-chunk segments) and the fused producers
+batch (empty, one-token and multi-chunk segments), fp16 and 32-token chunks,
+no initial state, the fla_scan contract (hip_scan) and the fused producers
 (L2 norm and beta sigmoid, differentiated in torch before the kernels).
 """
 import pytest
@@ -162,3 +163,54 @@ def test_chunk_bwd_with_fused_producers():
         err = _rel(a, b)
         print(f'[parity] fused {name} rel_l2={err:.3e}', flush=True)
         assert err <= 2e-2, name
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('dtype,chunk', [(torch.float16, 64), (torch.bfloat16, 32), (torch.float16, 32)])
+def test_chunk_bwd_fp16_and_32_token_chunks(dtype, chunk):
+    """fp16 and the 32-token chunk variants, dk = 64 with dv = 128, no initial
+    state and no final-state cotangent (dS0 is then not asked for)."""
+    B, T, H, dk, dv = 2, 77, 2, 64, 128
+    print(f'\n[case] chunk_bwd dtype={dtype} chunk={chunk}', flush=True)
+    q, k, v, g, beta, _, do, _ = _inputs(B, T, H, dk, dv, dtype, seed=31 + chunk, s0=False)
+    scale = dk ** -0.5
+    ref = gdr.recurrent_grads(q, k, v, g, beta, None, do, None, scale=scale)
+    leaves = [x.cuda().requires_grad_(True) for x in (q, k, v, g, beta)]
+    o, _ = ops.chunk_gated_delta_rule(*leaves, scale=scale, chunk_size=chunk)
+    o.backward(do.cuda())
+    _compare([x.grad for x in leaves] + [None], ref, 2e-2, f'{dtype} chunk={chunk}')
+
+
+@pytest.mark.gpu
+def test_hip_scan_is_differentiable():
+    """hip_scan (the fla_scan contract: o and the final state) with grads, the
+    route a training module takes, against the oracle."""
+    B, T, H, dk, dv = 1, 90, 2, 128, 64
+    print('\n[case] hip_scan backward', flush=True)
+    q, k, v, g, beta, S0, do, dST = _inputs(B, T, H, dk, dv, torch.bfloat16, seed=41)
+    ref = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=dk ** -0.5)
+    leaves = [x.cuda().requires_grad_(True) for x in (q, k, v, g, beta, S0)]
+    o, S = ops.hip_scan(*leaves, scale=dk ** -0.5, delta=True)
+    torch.autograd.backward([o, S], [do.cuda(), dST.cuda()])
+    _compare([x.grad for x in leaves], ref, 2e-2, 'hip_scan')
+
+
+@pytest.mark.gpu
+def test_explicit_backward_matches_autograd():
+    """ops.chunk_gated_delta_rule_bwd (no autograd) returns what autograd
+    accumulates through chunk_gated_delta_rule: bit for bit for dq, dk, dv,
+    dS0 (same kernels); dg and dbeta sum their row and column terms through
+    LDS atomics, whose order varies, so they agree to rounding."""
+    B, T, H, dk, dv = 2, 64, 2, 64, 64
+    q, k, v, g, beta, S0, do, dST = (None if x is None else x.cuda()
+                                     for x in _inputs(B, T, H, dk, dv, torch.bfloat16, seed=51))
+    print('\n[case] explicit backward vs autograd', flush=True)
+    got = ops.chunk_gated_delta_rule_bwd(q, k, v, g, beta, S0, do, dST, scale=0.125)
+    leaves = [x.clone().requires_grad_(True) for x in (q, k, v, g, beta, S0)]
+    o, S = ops.chunk_gated_delta_rule(*leaves[:5], scale=0.125, initial_state=leaves[5], output_final_state=True)
+    torch.autograd.backward([o, S], [do, dST])
+    for name, a, b in zip(NAMES, got, [x.grad for x in leaves]):
+        if name in ('dg', 'dbeta'):
+            assert _rel(a, b) <= 1e-6, name
+        else:
+            assert torch.equal(a, b), name
