@@ -82,8 +82,11 @@ struct RowRegs {
 };
 
 // A fragment-order CH x CH block (TE or A: lower triangle with the diagonal)
-// in registers, 16-byte units read in order; store() writes it as a plain LDS
-// matrix dst[row][col] (dst[col][row] when TRANS) with zeros above the diagonal.
+// in registers, 16-byte units read in order; store() writes it as a plain
+// row-major LDS matrix.  A fragment is four consecutive columns of one row,
+// so each is one 8-byte (16-bit types) or 16-byte (fp32) store.  Tiles above
+// the diagonal are written as zeros (chunk_prep leaves them unwritten, except
+// the partner of a diagonal tile pair, and zeros inside the diagonal tiles).
 template <typename E, int CH, int NT>
 struct BlockRegs {
     static constexpr int VE = 16 / (int)sizeof(E), UNITS = CH * CH / VE, N = (UNITS + NT - 1) / NT;
@@ -96,20 +99,22 @@ struct BlockRegs {
             x[i] = *reinterpret_cast<const V *>(blk + (u < UNITS ? u : 0) * VE);
         });
     }
-    template <bool TRANS, typename T>
-    __device__ __forceinline__ void store(T *dst, int pitch, int tid) const {
+    __device__ __forceinline__ void store(E *dst, int pitch, int tid) const {
+        using F = typename Elem<E>::frag;
         unroll<N>([&](auto i) __attribute__((always_inline)) {
             const int u = tid + (int)i * NT;
             if (u < UNITS) {
+                const int p = u * VE;                              // first element of the unit
+                const int ln = (p >> 3) & 63, pr = p >> 9;         // pr = I (NB / 2) + q
+                const int I = pr / (NB / 2), q = pr % (NB / 2);
+                const int row = 16 * I + (ln & 15);
 #pragma unroll
-                for (int e = 0; e < VE; ++e) {
-                    const int p = u * VE + e;
-                    const int e8 = p & 7, ln = (p >> 3) & 63, pr = p >> 9;   // pr = I (NB / 2) + q
-                    const int I = pr / (NB / 2), q = pr % (NB / 2);
-                    const int row = 16 * I + (ln & 15), col = 16 * (2 * q + (e8 >> 2)) + 4 * (ln >> 4) + (e8 & 3);
-                    const T v = col <= row ? (T)(float)x[i][e] : (T)0.f;
-                    if (TRANS) dst[col * pitch + row] = v;
-                    else dst[row * pitch + col] = v;
+                for (int h = 0; h < VE / 4; ++h) {                 // the unit's fragments (two for 16-bit types)
+                    const int kb = 2 * q + ((p >> 2) & 1) + h;
+                    F f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) f[e] = kb <= I ? x[i][4 * h + e] : E(0.f);
+                    *reinterpret_cast<F *>(dst + row * pitch + 16 * kb + 4 * (ln >> 4)) = f;
                 }
             }
         });
@@ -418,8 +423,8 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
         __syncthreads();
         rk.store(Ks, PK, nullptr, 0, clen, tid);
         rq.store(Qs, PK, nullptr, 0, clen, tid);
-        rte.template store<false>(TEm, PT, tid);
-        ra.template store<false>(Am, PT, tid);
+        rte.store(TEm, PT, tid);
+        ra.store(Am, PT, tid);
         if (tid < CH) {
             gx[tid] = gxn;
             go[tid] = gon;
@@ -634,8 +639,8 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     colload(0);
     rk.store(Ks, PK, nullptr, 0, clen, tid);
     rq.store(Qs, PK, nullptr, 0, clen, tid);
-    ra.template store<false>(Am, PT, tid);
-    rte.template store<false>(TEs, PT, tid);
+    ra.store(Am, PT, tid);
+    rte.store(TEs, PT, tid);
     if (tid < CH) {
         gx[tid] = gx_v;
         go[tid] = go_v;
