@@ -254,7 +254,10 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
 
     const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
     RowRegs<E, CH, DK, NT> rk;
-    f32x4 vn[NB];                                              // V rows of the fetched chunk (C layout)
+    // V rows of the fetched chunk (C layout), kept in the element type: a
+    // conversion right after the load would wait for it, and with it for every
+    // load issued before (the wait counter is in order)
+    E vn[NB][4];
     F ten[NB * NB];                                            // its TE fragments (lower tiles)
     float gxn = 0.f, gen = 0.f, gcn = 0.f;
     int clen_n = 0;
@@ -280,8 +283,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = 16 * I + 4 * g4 + j;
-                vn[I][j] = EL::to_f(vg[(t0 + (row < clen_n ? row : 0)) * sv]);
-                if (row >= clen_n) vn[I][j] = 0.f;
+                vn[I][j] = vg[(t0 + (row < clen_n ? row : 0)) * sv];
             }
     };
     if (nchunks > 1) fetch(0);
@@ -304,7 +306,8 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
         F TEf[NB * NB];
 #pragma unroll
         for (int I = 0; I < NB; ++I) {
-            V[I] = vn[I];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) V[I][j] = 16 * I + 4 * g4 + j < clen_n ? EL::to_f(vn[I][j]) : 0.f;
 #pragma unroll
             for (int kb = 0; kb <= I; ++kb) TEf[I * NB + kb] = ten[I * NB + kb];
         }
@@ -343,36 +346,105 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
 // ===========================================================================
 // chunk_dhs_kernel: the reverse recurrence for dS; dV = dX
 // ===========================================================================
-template <int DK, int CH, int NW, typename E>
-__global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams p) {
+template <int V_> struct SlotTag { static constexpr int value = V_; };
+
+// NWC compute waves (16 state columns each) and NWC producer waves.  The
+// producers load each chunk's K, Q rows, TE and A blocks and gate factors
+// into registers and stage them into the idle half of a double-buffered LDS
+// slot while the compute waves work on the other half; one barrier per chunk
+// hands a slot over.  The two roles run separate loops with the same barrier
+// count.  The compute waves load their own dO rows one chunk ahead.
+template <int DK, int CH, int NWC, typename E>
+__global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
     using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, 1>;
-    constexpr int NT = 64 * NW, NB = CH / 16, NKB = DK / 16, VE = 16 / (int)sizeof(E);
+    constexpr int NTP = 64 * NWC, NB = CH / 16, NKB = DK / 16;
     constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value;
-    __shared__ __attribute__((aligned(16))) E Ks[CH * PK];
-    __shared__ __attribute__((aligned(16))) E Qs[CH * PK];
-    __shared__ __attribute__((aligned(16))) E TEm[CH * PT];
-    __shared__ __attribute__((aligned(16))) E Am[CH * PT];
-    __shared__ __attribute__((aligned(16))) float gx[CH];
-    __shared__ __attribute__((aligned(16))) float go[CH];
-    __shared__ __attribute__((aligned(16))) float ge[CH];
-    __shared__ float gcs[4];
+    __shared__ __attribute__((aligned(16))) E Ks0[CH * PK];
+    __shared__ __attribute__((aligned(16))) E Ks1[CH * PK];
+    __shared__ __attribute__((aligned(16))) E Qs0[CH * PK];
+    __shared__ __attribute__((aligned(16))) E Qs1[CH * PK];
+    __shared__ __attribute__((aligned(16))) E TE0[CH * PT];
+    __shared__ __attribute__((aligned(16))) E TE1[CH * PT];
+    __shared__ __attribute__((aligned(16))) E Am0[CH * PT];
+    __shared__ __attribute__((aligned(16))) E Am1[CH * PT];
+    __shared__ __attribute__((aligned(16))) float gt0[3 * CH + 4];   // GX, GO, GE, then Gc
+    __shared__ __attribute__((aligned(16))) float gt1[3 * CH + 4];
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g4 = lane >> 4, r16 = lane & 15;
     WalkUnit u;
     if (!walk_unit(p, u)) return;
     const int H = p.H, DV = p.DV, h = u.h;
-    const int colw = u.tile * 16 * NW + 16 * wave;
+    const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
+    const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
+    auto clen_of = [&](int c) __attribute__((always_inline)) {
+        const int64_t t0 = u.bos + (int64_t)c * CH;
+        return (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
+    };
+
+    if (wave >= NWC) {
+        // ---- producers ----------------------------------------------------
+        const int ptid = tid - 64 * NWC;
+        const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
+        const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
+        RowRegs<E, CH, DK, NTP> rk, rq;
+        BlockRegs<E, CH, NTP> rte, ra;
+        constexpr int NG = 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
+        float gv[GPT];
+        auto fetch = [&](int c) __attribute__((always_inline)) {
+            const int64_t t0 = u.bos + (int64_t)c * CH;
+            const int clen = clen_of(c);
+            rk.load(kg + t0 * sqk, sqk, clen, ptid);
+            rq.load(qg + t0 * sqk, sqk, clen, ptid);
+            const char *blkb = reinterpret_cast<const char *>(p.blocks) + ((u.cbase + c) * H + h) * CB::BYTES;
+            rte.load(reinterpret_cast<const E *>(blkb), ptid);
+            ra.load(reinterpret_cast<const E *>(blkb) + CH * CH, ptid);
+#pragma unroll
+            for (int i = 0; i < GPT; ++i) {
+                const int gi = ptid + i * NTP;
+                gv[i] = reinterpret_cast<const float *>(blkb + CB::GOFF)[gi < NG ? gi : 0];
+            }
+        };
+        auto put = [&](auto tag, int c) __attribute__((always_inline)) {
+            constexpr int SL = decltype(tag)::value;
+            const int clen = clen_of(c);
+            rk.store(SL ? Ks1 : Ks0, PK, nullptr, 0, clen, ptid);
+            rq.store(SL ? Qs1 : Qs0, PK, nullptr, 0, clen, ptid);
+            rte.store(SL ? TE1 : TE0, PT, ptid);
+            ra.store(SL ? Am1 : Am0, PT, ptid);
+#pragma unroll
+            for (int i = 0; i < GPT; ++i)
+                if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = gv[i];
+        };
+        if (nchunks == 0) return;
+        fetch(nchunks - 1);
+        put(SlotTag<0>{}, nchunks - 1);
+        __syncthreads();
+        for (int k = 0; k < nchunks; k += 2) {
+            if (k + 1 < nchunks) {                             // step k reads slot 0: fill slot 1
+                fetch(nchunks - 2 - k);
+                put(SlotTag<1>{}, nchunks - 2 - k);
+            }
+            __syncthreads();
+            if (k + 1 < nchunks) {
+                if (k + 2 < nchunks) {                         // step k + 1 reads slot 1: fill slot 0
+                    fetch(nchunks - 3 - k);
+                    put(SlotTag<0>{}, nchunks - 3 - k);
+                }
+                __syncthreads();
+            }
+        }
+        return;
+    }
+
+    // ---- compute waves ------------------------------------------------------
+    const int colw = u.tile * 16 * NWC + 16 * wave;
     const bool wvalid = colw < DV;
     const int col = wvalid ? colw + r16 : r16;
-    const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
-    const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
-    const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
     const E *dog = reinterpret_cast<const E *>(p.dout) + (int64_t)h * DV + col;
     E *dvg = reinterpret_cast<E *>(p.dv) + (int64_t)h * DV + col;
-
     f32x4 dS[NKB];
     const int64_t sbase = ((int64_t)u.seq * H + h) * DK * DV + col;
 #pragma unroll
@@ -380,62 +452,40 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             dS[kt][j] = (p.dht && wvalid) ? p.dht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
-
-    const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
-    RowRegs<E, CH, DK, NT> rk, rq;
-    BlockRegs<E, CH, NT> rte, ra;
-    f32x4 don[NB];                                             // dO rows of the fetched chunk (C layout)
-    float gxn = 0.f, gon = 0.f, gen = 0.f, gcn = 0.f;
-    int clen_n = 0;
-    auto fetch = [&](int c) __attribute__((always_inline)) {
+    E don[NB][4];                                              // dO rows of the next chunk (C layout, raw)
+    auto fetch_do = [&](int c) __attribute__((always_inline)) {
         const int64_t t0 = u.bos + (int64_t)c * CH;
-        clen_n = (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
-        rk.load(kg + t0 * sqk, sqk, clen_n, tid);
-        rq.load(qg + t0 * sqk, sqk, clen_n, tid);
-        const char *blkb = reinterpret_cast<const char *>(p.blocks) + ((u.cbase + c) * H + h) * CB::BYTES;
-        rte.load(reinterpret_cast<const E *>(blkb), tid);
-        ra.load(reinterpret_cast<const E *>(blkb) + CH * CH, tid);
-        const float *gf = reinterpret_cast<const float *>(blkb + CB::GOFF);
-        const int tc = tid < CH ? tid : 0;
-        gxn = gf[tc];
-        gon = gf[CH + tc];
-        gen = gf[2 * CH + tc];
-        gcn = gf[3 * CH];
+        const int clen = clen_of(c);
 #pragma unroll
         for (int I = 0; I < NB; ++I)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = 16 * I + 4 * g4 + j;
-                don[I][j] = EL::to_f(dog[(t0 + (row < clen_n ? row : 0)) * sv]);
-                if (row >= clen_n) don[I][j] = 0.f;
+                don[I][j] = dog[(t0 + (row < clen ? row : 0)) * sv];
             }
     };
-    if (nchunks > 0) fetch(nchunks - 1);
-    for (int c = nchunks - 1; c >= 0; --c) {
+    auto step = [&](auto tag, int k) __attribute__((always_inline)) {
+        constexpr int SL = decltype(tag)::value;
+        const E *Ks = SL ? Ks1 : Ks0;
+        const E *Qs = SL ? Qs1 : Qs0;
+        const E *TEm = SL ? TE1 : TE0;
+        const E *Am = SL ? Am1 : Am0;
+        const float *gt = SL ? gt1 : gt0;
+        const int c = nchunks - 1 - k;
         const int64_t slot = u.cbase + c;
+        const int64_t t0 = u.bos + (int64_t)c * CH;
+        const int clen = clen_of(c);
         if (wvalid) {
             E *dhs = reinterpret_cast<E *>(p.dhs) + ((slot * H + h) * DV + col) * DK + 4 * g4;
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(dhs + 16 * kt, EL::cvt(dS[kt]));
         }
-        const int64_t t0 = u.bos + (int64_t)c * CH;
-        const int clen = clen_n;
-        __syncthreads();
-        rk.store(Ks, PK, nullptr, 0, clen, tid);
-        rq.store(Qs, PK, nullptr, 0, clen, tid);
-        rte.store(TEm, PT, tid);
-        ra.store(Am, PT, tid);
-        if (tid < CH) {
-            gx[tid] = gxn;
-            go[tid] = gon;
-            ge[tid] = gen;
-        }
-        if (tid == 0) gcs[0] = gcn;
         f32x4 dO[NB];
 #pragma unroll
-        for (int I = 0; I < NB; ++I) dO[I] = don[I];
-        __syncthreads();
-        if (c > 0) fetch(c - 1);
+        for (int I = 0; I < NB; ++I)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) dO[I][j] = 16 * I + 4 * g4 + j < clen ? EL::to_f(don[I][j]) : 0.f;
+        if (c > 0) fetch_do(c - 1);
         if (wvalid) {
             F dOb[NB], dSb[NKB];
 #pragma unroll
@@ -449,7 +499,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
                 f32x4 Y = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return dSb[kt]; });
-                Y *= ld4(ge + 16 * I + 4 * g4);
+                Y *= ld4(gt + 2 * CH + 16 * I + 4 * g4);
                 Y = contract(Y, NB, [&](int kb) { return ld_colfrag<E>(Am, PT, 16 * kb, 16 * I, lane); },
                              [&](int kb) { return dOb[kb]; });
                 Yb[I] = EL::cvt(Y);
@@ -466,11 +516,11 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
                     const int row = 16 * I + 4 * g4 + j;
                     if (row < clen) dvg[(t0 + row) * sv] = EL::from_f(dX[j]);
                 }
-                Ob[I] = EL::cvt(dO[I] * ld4(go + 16 * I + 4 * g4));
-                Xb[I] = EL::cvt(-dX * ld4(gx + 16 * I + 4 * g4));
+                Ob[I] = EL::cvt(dO[I] * ld4(gt + CH + 16 * I + 4 * g4));
+                Xb[I] = EL::cvt(-dX * ld4(gt + 16 * I + 4 * g4));
             }
             // dS = Gc dS' + Q^T diag(GO) dO - K^T diag(GX) dX
-            const float gc = gcs[0];
+            const float gc = gt[3 * CH];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) {
                 f32x4 s = contract(dS[kt] * gc, NB,
@@ -480,6 +530,18 @@ __global__ void __launch_bounds__(64 * NW) chunk_dhs_kernel(const ChunkBwdParams
                     [&](int kb) { return ld_colfrag<E>(Ks, PK, 16 * kb, 16 * kt, lane); },
                     [&](int kb) { return Xb[kb]; });
             }
+        }
+    };
+    if (nchunks > 0) {
+        fetch_do(nchunks - 1);
+        __syncthreads();                                       // slot 0 holds the last chunk
+    }
+    for (int k = 0; k < nchunks; k += 2) {
+        step(SlotTag<0>{}, k);
+        __syncthreads();
+        if (k + 1 < nchunks) {
+            step(SlotTag<1>{}, k + 1);
+            __syncthreads();
         }
     }
     if (p.dh0 && wvalid) {
@@ -594,7 +656,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         while (J > I) { J -= I + 1; ++I; }
     };
     // A at this wave's dA elements (the A terms of dgamma)
-    float aval[LPW][4];
+    E aval[LPW][4];                                            // raw: converted where used
 #pragma unroll
     for (int s = 0; s < LPW; ++s) {
         const int l = wave + NW * s;
@@ -603,7 +665,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int i = 16 * I + 4 * g4 + j, jj = 16 * J + r16;
-            aval[s][j] = EL::to_f(Ab[blk_pos<NB>(i, jj <= i ? jj : i)]);
+            aval[s][j] = Ab[blk_pos<NB>(i, jj <= i ? jj : i)];
         }
     }
     // Column block c (16 columns of a dv block, c < NCW) belongs to waves c
@@ -790,7 +852,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 const bool low = jj <= i;
                 const float D = low ? __expf(gam[i] - gam[jj]) : 0.f;
                 const float da = low ? aA[s][j] : 0.f;
-                rs[j] = da * aval[s][j];
+                rs[j] = da * EL::to_f(aval[s][j]);
                 cs += rs[j];
                 aA[s][j] = p.scale * da * D;
                 Fdte[i * PF + jj] = low ? aT[s][j] : 0.f;
@@ -983,18 +1045,18 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 template <int DK, int CH, typename E>
 static hipError_t run_bwd(ChunkBwdParams p, hipStream_t stream) {
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
-    // The entry-state walk runs two waves (32-column tiles: 256 workgroups at
-    // B = 8, H = 8, dv = 128) and the dS walk four: the dS walk's one-chunk-ahead
-    // buffers of K, Q, TE and A spill at two waves (measured at B8 T4096 H8
-    // d128: dS walk 1.86 -> 1.51 ms whole backward with four; entry walk 243 ->
-    // 202 us with two).
+    // Both walks take 32-column tiles (256 workgroups at B = 8, H = 8, dv = 128):
+    // the entry-state walk with two waves, the dS walk with two compute and two
+    // producer waves (measured at B8 T4096 H8 d128, whole backward: 1.13 ms with
+    // the dS walk's compute waves staging their own operands, 1.00 ms with
+    // producers; 1.02 ms with 64-column tiles).
     if (units > 0) {
         ChunkBwdParams ph = p;
         ph.n_tiles = (p.DV + 31) / 32;
         hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * ph.n_tiles)),
                            dim3(128), 0, stream, ph);
-        p.n_tiles = (p.DV + 63) / 64;
-        hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 4, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
+        p.n_tiles = (p.DV + 31) / 32;
+        hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
                            dim3(256), 0, stream, p);
     }
     const int64_t grad_blocks = (int64_t)p.n_chunk_slots * p.H;
