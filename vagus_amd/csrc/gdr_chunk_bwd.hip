@@ -217,33 +217,89 @@ __device__ __forceinline__ bool locate_chunk(const SeqGeom &g, int64_t slot, int
 // ===========================================================================
 // chunk_hs_kernel: entry state of every chunk
 // ===========================================================================
-// Each chunk's operands are loaded into registers one chunk ahead: the loads
-// of chunk c + 1 are in flight while chunk c computes, and reach LDS after
-// the next barrier.
-template <int DK, int CH, int NW, typename E>
-__global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams p) {
+template <int V_> struct SlotTag { static constexpr int value = V_; };
+
+// NWC compute waves (16 state columns each) re-run the forward recurrence and
+// store each chunk's entry state; NWC producer waves stage each chunk's K rows
+// and gate factors into the idle half of a double-buffered LDS slot (one
+// barrier per chunk hands a slot over; separate loops, equal barrier counts).
+// The compute waves load their own V rows and TE fragments one chunk ahead.
+template <int DK, int CH, int NWC, typename E>
+__global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
     using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, 1>;
-    constexpr int NT = 64 * NW, NB = CH / 16, NKB = DK / 16, VE = 16 / (int)sizeof(E);
+    constexpr int NTP = 64 * NWC, NB = CH / 16, NKB = DK / 16;
     constexpr int PK = Pitch<E, DK>::value;
-    __shared__ __attribute__((aligned(16))) E Ks[CH * PK];
-    __shared__ __attribute__((aligned(16))) float gx[CH];
-    __shared__ __attribute__((aligned(16))) float ge[CH];
-    __shared__ float gcs[4];
+    __shared__ __attribute__((aligned(16))) E Ks0[CH * PK];
+    __shared__ __attribute__((aligned(16))) E Ks1[CH * PK];
+    __shared__ __attribute__((aligned(16))) float gt0[3 * CH + 4];   // GX, GO, GE, then Gc
+    __shared__ __attribute__((aligned(16))) float gt1[3 * CH + 4];
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g4 = lane >> 4, r16 = lane & 15;
     WalkUnit u;
     if (!walk_unit(p, u)) return;
     const int H = p.H, DV = p.DV, h = u.h;
-    const int colw = u.tile * 16 * NW + 16 * wave;
+    const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
+    const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
+    const int nsteps = nchunks > 0 ? nchunks - 1 : 0;          // the last chunk's exit state is not needed
+    auto clen_of = [&](int c) __attribute__((always_inline)) {
+        const int64_t t0 = u.bos + (int64_t)c * CH;
+        return (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
+    };
+    auto blk_of = [&](int c) __attribute__((always_inline)) {
+        return reinterpret_cast<const char *>(p.blocks) + ((u.cbase + c) * H + h) * CB::BYTES;
+    };
+
+    if (wave >= NWC) {
+        // ---- producers ----------------------------------------------------
+        const int ptid = tid - 64 * NWC;
+        const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
+        constexpr int NG = 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
+        RowRegs<E, CH, DK, NTP> rk;
+        float gv[GPT];
+        auto fetch = [&](int c) __attribute__((always_inline)) {
+            rk.load(kg + (u.bos + (int64_t)c * CH) * sqk, sqk, clen_of(c), ptid);
+#pragma unroll
+            for (int i = 0; i < GPT; ++i) {
+                const int gi = ptid + i * NTP;
+                gv[i] = reinterpret_cast<const float *>(blk_of(c) + CB::GOFF)[gi < NG ? gi : 0];
+            }
+        };
+        auto put = [&](auto tag, int c) __attribute__((always_inline)) {
+            constexpr int SL = decltype(tag)::value;
+            rk.store(SL ? Ks1 : Ks0, PK, nullptr, 0, clen_of(c), ptid);
+#pragma unroll
+            for (int i = 0; i < GPT; ++i)
+                if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = gv[i];
+        };
+        if (nsteps == 0) return;
+        fetch(0);
+        put(SlotTag<0>{}, 0);
+        __syncthreads();
+        for (int k = 0; k < nsteps; k += 2) {
+            if (k + 1 < nsteps) {                              // step k reads slot 0: fill slot 1
+                fetch(k + 1);
+                put(SlotTag<1>{}, k + 1);
+            }
+            __syncthreads();
+            if (k + 1 < nsteps) {
+                if (k + 2 < nsteps) {                          // step k + 1 reads slot 1: fill slot 0
+                    fetch(k + 2);
+                    put(SlotTag<0>{}, k + 2);
+                }
+                __syncthreads();
+            }
+        }
+        return;
+    }
+
+    // ---- compute waves ------------------------------------------------------
+    const int colw = u.tile * 16 * NWC + 16 * wave;
     const bool wvalid = colw < DV;                             // DV % 16 == 0
     const int col = wvalid ? colw + r16 : r16;                 // in bounds for the unconditional loads
-    const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
-    const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
     const E *vg = reinterpret_cast<const E *>(p.v) + (int64_t)h * DV + col;
-
     f32x4 S[NKB];
     const int64_t sbase = ((int64_t)u.seq * H + h) * DK * DV + col;
 #pragma unroll
@@ -251,29 +307,21 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
-
-    const int nchunks = (int)((u.eos - u.bos + CH - 1) / CH);
-    RowRegs<E, CH, DK, NT> rk;
-    // V rows of the fetched chunk (C layout), kept in the element type: a
-    // conversion right after the load would wait for it, and with it for every
-    // load issued before (the wait counter is in order)
+    auto store_state = [&](int c) __attribute__((always_inline)) {
+        if (wvalid) {
+            E *hs = reinterpret_cast<E *>(p.hs) + (((u.cbase + c) * H + h) * DV + col) * DK + 4 * g4;
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(hs + 16 * kt, EL::cvt(S[kt]));
+        }
+    };
+    // V rows (C layout) and TE fragments (lower tiles) of the next chunk, raw:
+    // a conversion next to its load would wait for every load before it
     E vn[NB][4];
-    F ten[NB * NB];                                            // its TE fragments (lower tiles)
-    float gxn = 0.f, gen = 0.f, gcn = 0.f;
-    int clen_n = 0;
-    auto fetch = [&](int c) __attribute__((always_inline)) {
+    F ten[NB * NB];
+    auto fetch_own = [&](int c) __attribute__((always_inline)) {
         const int64_t t0 = u.bos + (int64_t)c * CH;
-        clen_n = (int)(u.eos - t0 < CH ? u.eos - t0 : CH);
-        rk.load(kg + t0 * sqk, sqk, clen_n, tid);
-        const float *gf =
-            reinterpret_cast<const float *>(reinterpret_cast<const char *>(p.blocks) +
-                                            ((u.cbase + c) * H + h) * CB::BYTES + CB::GOFF);
-        const int tc = tid < CH ? tid : 0;
-        gxn = gf[tc];
-        gen = gf[2 * CH + tc];
-        gcn = gf[3 * CH];
-        const E *TEb = reinterpret_cast<const E *>(reinterpret_cast<const char *>(p.blocks) +
-                                                   ((u.cbase + c) * H + h) * CB::BYTES);
+        const int clen = clen_of(c);
+        const E *TEb = reinterpret_cast<const E *>(blk_of(c));
 #pragma unroll
         for (int I = 0; I < NB; ++I)
 #pragma unroll
@@ -283,36 +331,25 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int row = 16 * I + 4 * g4 + j;
-                vn[I][j] = vg[(t0 + (row < clen_n ? row : 0)) * sv];
+                vn[I][j] = vg[(t0 + (row < clen ? row : 0)) * sv];
             }
     };
-    if (nchunks > 1) fetch(0);
-    for (int c = 0; c < nchunks; ++c) {
-        const int64_t slot = u.cbase + c;
-        if (wvalid) {
-            E *hs = reinterpret_cast<E *>(p.hs) + ((slot * H + h) * DV + col) * DK + 4 * g4;
-#pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(hs + 16 * kt, EL::cvt(S[kt]));
-        }
-        if (c + 1 == nchunks) break;                           // the last exit state is not needed
-        __syncthreads();                                       // the previous chunk's LDS reads are done
-        rk.store(Ks, PK, nullptr, 0, clen_n, tid);
-        if (tid < CH) {
-            gx[tid] = gxn;
-            ge[tid] = gen;
-        }
-        if (tid == 0) gcs[0] = gcn;
+    auto step = [&](auto tag, int c) __attribute__((always_inline)) {
+        constexpr int SL = decltype(tag)::value;
+        const E *Ks = SL ? Ks1 : Ks0;
+        const float *gt = SL ? gt1 : gt0;
+        store_state(c);
+        const int clen = clen_of(c);
         f32x4 V[NB];
         F TEf[NB * NB];
 #pragma unroll
         for (int I = 0; I < NB; ++I) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) V[I][j] = 16 * I + 4 * g4 + j < clen_n ? EL::to_f(vn[I][j]) : 0.f;
+            for (int j = 0; j < 4; ++j) V[I][j] = 16 * I + 4 * g4 + j < clen ? EL::to_f(vn[I][j]) : 0.f;
 #pragma unroll
             for (int kb = 0; kb <= I; ++kb) TEf[I * NB + kb] = ten[I * NB + kb];
         }
-        __syncthreads();
-        if (c + 2 < nchunks) fetch(c + 1);
+        if (c + 1 < nsteps) fetch_own(c + 1);
         if (wvalid) {
             F Sb[NKB];
 #pragma unroll
@@ -323,7 +360,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
                 const f32x4 P = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return Sb[kt]; });
-                Xb[I] = EL::cvt(V[I] - ld4(gx + 16 * I + 4 * g4) * P);
+                Xb[I] = EL::cvt(V[I] - ld4(gt + 16 * I + 4 * g4) * P);
             }
             F Wb[NB];
 #pragma unroll
@@ -331,22 +368,34 @@ __global__ void __launch_bounds__(64 * NW) chunk_hs_kernel(const ChunkBwdParams 
                 const f32x4 U = contract(f32x4{0.f, 0.f, 0.f, 0.f}, I + 1,
                     [&](int kb) { return TEf[I * NB + kb]; },
                     [&](int kb) { return Xb[kb]; });
-                Wb[I] = EL::cvt(U * ld4(ge + 16 * I + 4 * g4));
+                Wb[I] = EL::cvt(U * ld4(gt + 2 * CH + 16 * I + 4 * g4));
             }
-            const float gc = gcs[0];
+            const float gc = gt[3 * CH];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt)
                 S[kt] = contract(S[kt] * gc, NB,
                     [&](int kb) { return ld_colfrag<E>(Ks, PK, 16 * kb, 16 * kt, lane); },
                     [&](int kb) { return Wb[kb]; });
         }
+    };
+    if (nsteps > 0) {
+        fetch_own(0);
+        __syncthreads();                                       // slot 0 holds chunk 0
     }
+    for (int k = 0; k < nsteps; k += 2) {
+        step(SlotTag<0>{}, k);
+        __syncthreads();
+        if (k + 1 < nsteps) {
+            step(SlotTag<1>{}, k + 1);
+            __syncthreads();
+        }
+    }
+    if (nchunks > 0) store_state(nchunks - 1);
 }
 
 // ===========================================================================
 // chunk_dhs_kernel: the reverse recurrence for dS; dV = dX
 // ===========================================================================
-template <int V_> struct SlotTag { static constexpr int value = V_; };
 
 // NWC compute waves (16 state columns each) and NWC producer waves.  The
 // producers load each chunk's K, Q rows, TE and A blocks and gate factors
@@ -1045,17 +1094,14 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 template <int DK, int CH, typename E>
 static hipError_t run_bwd(ChunkBwdParams p, hipStream_t stream) {
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
-    // Both walks take 32-column tiles (256 workgroups at B = 8, H = 8, dv = 128):
-    // the entry-state walk with two waves, the dS walk with two compute and two
-    // producer waves (measured at B8 T4096 H8 d128, whole backward: 1.13 ms with
-    // the dS walk's compute waves staging their own operands, 1.00 ms with
-    // producers; 1.02 ms with 64-column tiles).
+    // Both walks take 32-column tiles (256 workgroups at B = 8, H = 8, dv =
+    // 128) with two compute and two producer waves (measured at B8 T4096 H8
+    // d128, whole backward: 1.13 ms with the dS walk's compute waves staging
+    // their own operands, 1.00 ms with producers; 1.02 ms with 64-column tiles).
     if (units > 0) {
-        ChunkBwdParams ph = p;
-        ph.n_tiles = (p.DV + 31) / 32;
-        hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * ph.n_tiles)),
-                           dim3(128), 0, stream, ph);
         p.n_tiles = (p.DV + 31) / 32;
+        hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
+                           dim3(256), 0, stream, p);
         hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
                            dim3(256), 0, stream, p);
     }
