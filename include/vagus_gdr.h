@@ -220,7 +220,8 @@ int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, con
  * [n_tokens, H, dk], grad_v [n_tokens, H, dv] in dtype; grad_g, grad_beta
  * [n_tokens, H] fp32 (grad_g unused and nullable without a gate);
  * grad_initial_state [n_seqs, H, dk, dv] fp32 (nullable: not computed).
- * The gradients must not alias the inputs.  workspace:
+ * The gradients must not alias the inputs; grad_o and grad_v are 16-byte
+ * aligned (q, k, v as in vgdr_chunk_fwd).  workspace:
  * vgdr_chunk_bwd_workspace_size(...) bytes, 16-byte aligned; it holds the
  * chunk blocks (rebuilt from q, k, g, beta), each chunk's entry state and the
  * gradient of its exit state.  Same dk, dv, chunk_size and packed-batch

@@ -43,6 +43,7 @@ def test_chunk_bwd_argument_checks():
     assert call(db=None) == _lib.VGDR_ERR_INVALID
     assert call(dv=12288) == _lib.VGDR_ERR_INVALID                   # grad_v aliasing v
     assert b'alias' in L.vgdr_last_error()
+    assert call(do=24578) == _lib.VGDR_ERR_INVALID                  # grad_o alignment
     assert call(ws=None) == _lib.VGDR_ERR_INVALID
     assert call(wsb=16) == _lib.VGDR_ERR_INVALID
     assert call(beta=None) == _lib.VGDR_ERR_INVALID

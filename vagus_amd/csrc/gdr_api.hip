@@ -336,6 +336,8 @@ int vgdr_chunk_bwd(int dtype, int gate_kind, const void *q, const void *k, const
         return fail(VGDR_ERR_INVALID, "%s: grad_q, grad_k, grad_v and grad_beta are required", fn);
     if (grad_v == v || grad_q == q || grad_k == k)
         return fail(VGDR_ERR_INVALID, "%s: the gradients must not alias the inputs", fn);
+    if (!aligned16(grad_o) || !aligned16(grad_v))
+        return fail(VGDR_ERR_INVALID, "%s: grad_o and grad_v must be 16-byte aligned", fn);
     const int chunk = effective_chunk(dtype, dk, chunk_size);
     const BwdWs ws = bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, cu_seqlens != nullptr);
     if (ws.total > 0 && (!workspace || workspace_bytes < ws.total || !aligned16(workspace)))

@@ -46,36 +46,31 @@ namespace vgdr {
 
 namespace {
 
-// Rows [0, CH) x columns [0, DK) of a token-major matrix (row t at src + t *
+// Rows [0, CH) x columns [0, DK) of a row-major matrix (row t at src + t *
 // stride), held in registers between load() and store().  load() issues every
-// 16-byte load at once, unconditionally, from clamped rows (a load under a
-// per-lane branch waits for the ones before it); store() writes row-major
-// (rm, pitch prm) and/or transposed (tr, pitch ptr) LDS copies with rows >=
-// clen zeroed.  Pitches keep 16-byte rows aligned.
+// 16-byte load at once, unconditionally, from clamped addresses (a load under
+// a per-lane branch waits for the ones before it); store() writes the rows to
+// LDS (pitch keeps 16-byte rows aligned) with rows >= `rows` and columns >=
+// `cols` zeroed.
 template <typename E, int CH, int DK, int NT>
 struct RowRegs {
     static constexpr int VE = 16 / (int)sizeof(E), UPR = DK / VE, UNITS = CH * UPR, N = (UNITS + NT - 1) / NT;
     typedef E V __attribute__((ext_vector_type(VE)));
     V x[N];
-    __device__ __forceinline__ void load(const E *src, int64_t stride, int clen, int tid) {
+    __device__ __forceinline__ void load(const E *src, int64_t stride, int rows, int tid, int cols = DK) {
         unroll<N>([&](auto i) __attribute__((always_inline)) {
             const int u = tid + (int)i * NT;
             const int row = u / UPR, c0 = (u % UPR) * VE;
-            const int rr = (u < UNITS && row < clen) ? row : 0;
-            x[i] = *reinterpret_cast<const V *>(src + rr * stride + (u < UNITS ? c0 : 0));
+            const bool ok = u < UNITS && row < rows && c0 < cols;
+            x[i] = *reinterpret_cast<const V *>(src + (ok ? row * stride + c0 : 0));
         });
     }
-    __device__ __forceinline__ void store(E *rm, int prm, E *tr, int ptr, int clen, int tid) const {
+    __device__ __forceinline__ void store(E *dst, int pitch, int rows, int tid, int cols = DK) const {
         unroll<N>([&](auto i) __attribute__((always_inline)) {
             const int u = tid + (int)i * NT;
             if (u < UNITS) {
                 const int row = u / UPR, c0 = (u % UPR) * VE;
-                const V v = row < clen ? x[i] : V{};
-                if (rm) *reinterpret_cast<V *>(rm + row * prm + c0) = v;
-                if (tr) {
-#pragma unroll
-                    for (int e = 0; e < VE; ++e) tr[(c0 + e) * ptr + row] = v[e];
-                }
+                *reinterpret_cast<V *>(dst + row * pitch + c0) = (row < rows && c0 < cols) ? x[i] : V{};
             }
         });
     }
@@ -269,7 +264,7 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
         };
         auto put = [&](auto tag, int c) __attribute__((always_inline)) {
             constexpr int SL = decltype(tag)::value;
-            rk.store(SL ? Ks1 : Ks0, PK, nullptr, 0, clen_of(c), ptid);
+            rk.store(SL ? Ks1 : Ks0, PK, clen_of(c), ptid);
 #pragma unroll
             for (int i = 0; i < GPT; ++i)
                 if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = gv[i];
@@ -459,8 +454,8 @@ __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdPara
         auto put = [&](auto tag, int c) __attribute__((always_inline)) {
             constexpr int SL = decltype(tag)::value;
             const int clen = clen_of(c);
-            rk.store(SL ? Ks1 : Ks0, PK, nullptr, 0, clen, ptid);
-            rq.store(SL ? Qs1 : Qs0, PK, nullptr, 0, clen, ptid);
+            rk.store(SL ? Ks1 : Ks0, PK, clen, ptid);
+            rq.store(SL ? Qs1 : Qs0, PK, clen, ptid);
             rte.store(SL ? TE1 : TE0, PT, ptid);
             ra.store(SL ? Am1 : Am0, PT, ptid);
 #pragma unroll
@@ -609,12 +604,14 @@ struct GradLayout {
     static constexpr int ES = sizeof(E), VE = 16 / ES;
     static constexpr int NCW = ES == 2 ? 4 : 2;               // waves of the column phase
     static constexpr int DVB = 16 * NCW;                      // dv columns per block
-    static constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value, PF = CH + 4;
+    static constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value, PV = Pitch<E, DVB>::value;
+    static constexpr int PF = CH + 4;
     // K and Q rows, and TE rows (lower tiles), for the whole kernel
     static constexpr int PERS = (2 * CH * PK + CH * PT) * ES;
-    // column phase: A; the block's columns of X, U, dU, dO, dX (CH tokens each)
-    // and of S, dS' (DK key channels each), stored column by column
-    static constexpr int COLS = (CH * PT + 5 * DVB * PT + 2 * DVB * PK) * ES;
+    // column phase: A; the block's V, dO, dX rows (CH tokens, row-major); its
+    // columns of X, U, dU (CH tokens each) and of S, dS' (DK key channels
+    // each, the workspace's [dv][dk] order), stored column by column
+    static constexpr int COLS = (CH * PT + 3 * CH * PV + 3 * DVB * PT + 2 * DVB * PK) * ES;
     // CH x CH phase: N, dTE, T0 (then Z) in fp32; W_A and W_N + W_N^T in the element type
     static constexpr int SQ = 3 * CH * PF * 4 + 2 * CH * PT * ES;
     static constexpr int REGION = cmax(COLS, SQ);
@@ -637,7 +634,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     using CB = ChunkBlock<E, CH, DK, 1>;
     constexpr int NT = 512, NW = 8, NB = CH / 16, NKB = DK / 16, NBH = NB / 2;
     constexpr int NCW = L::NCW, DVB = L::DVB, NKD = DVB / 16;
-    constexpr int PK = L::PK, PT = L::PT, PF = L::PF;
+    constexpr int PK = L::PK, PT = L::PT, PV = L::PV, PF = L::PF;
     constexpr int NL = NB * (NB + 1) / 2, LPW = (NL + NW - 1) / NW;   // lower CH x CH tiles, per wave
     static_assert(NW % NB == 0, "a row block is split over whole waves");
     constexpr int JPW = NB * NKB / NW;                                 // CH x DK tiles per wave
@@ -649,12 +646,13 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     char *R = smem + L::PERS;
     // column phase
     E *Am = reinterpret_cast<E *>(R);
-    E *Xs = Am + CH * PT;                         // Xs[c][t] = X[t][c], c a column of the block
+    E *Vs = Am + CH * PT;                         // V, dO, dX rows of the block
+    E *dOs = Vs + CH * PV;
+    E *dXs = dOs + CH * PV;
+    E *Xs = dXs + CH * PV;                        // Xs[c][t] = X[t][c], c a column of the block
     E *Us = Xs + DVB * PT;
     E *Ys = Us + DVB * PT;
-    E *dOs = Ys + DVB * PT;
-    E *dXs = dOs + DVB * PT;
-    E *Ss = dXs + DVB * PT;                       // Ss[c][d] = S[d][c]
+    E *Ss = Ys + DVB * PT;                        // Ss[c][d] = S[d][c]
     E *dSs = Ss + DVB * PK;
     // CH x CH phase
     float *Fn = reinterpret_cast<float *>(R);
@@ -717,39 +715,34 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             aval[s][j] = Ab[blk_pos<NB>(i, jj <= i ? jj : i)];
         }
     }
-    // Column block c (16 columns of a dv block, c < NCW) belongs to waves c
-    // and c + 4: both hold its S, dS' columns; wave c + 4 h computes X, U, dU
-    // for token blocks h NBH .. h NBH + NBH - 1.  Their global operands are
-    // loaded a dv block ahead: block 0 with the staging loads, block db + 1
-    // during block db's products.
+    // The column phase's global operands of one dv block, as whole 16-byte
+    // rows: S and dS' columns (the workspace's [dv][dk] rows), and the V, dO,
+    // dX rows.  Loaded a dv block ahead: block 0 with the staging loads, block
+    // db + 1 during block db's products.
     const int cwave = wave & 3, half = wave >> 2;
     const bool colw_ok = cwave < NCW;
-    F cS[NKB], cdS[NKB];
-    E cV[NBH][4], cdO[NBH][4], cdX[NBH][4];
+    RowRegs<E, DVB, DK, NT> cS, cdS;
+    RowRegs<E, CH, DVB, NT> cV, cdO, cdX;
     auto colload = [&](int db) __attribute__((always_inline)) {
-        if (!colw_ok) return;
-        const int colw = db * DVB + 16 * cwave;
-        const int colc = colw < DV ? colw + r16 : r16;         // in bounds for the unconditional loads
-#pragma unroll
-        for (int kt = 0; kt < NKB; ++kt) {
-            const int64_t off = (int64_t)colc * DK + 16 * kt + 4 * g4;         // states are stored [dv][dk]
-            cS[kt] = gfrag<E>(hsb + off);
-            cdS[kt] = gfrag<E>(dhsb + off);
-        }
-#pragma unroll
-        for (int ii = 0; ii < NBH; ++ii)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int row = 16 * (half * NBH + ii) + 4 * g4 + j;
-                const int64_t off = (t0 + (row < clen ? row : 0)) * sv + (int64_t)h * DV + colc;
-                cV[ii][j] = reinterpret_cast<const E *>(p.v)[off];
-                cdO[ii][j] = reinterpret_cast<const E *>(p.dout)[off];
-                cdX[ii][j] = reinterpret_cast<const E *>(p.dv)[off];
-            }
+        const int cb = db * DVB, ncol = DV - cb < DVB ? DV - cb : DVB;
+        cS.load(hsb + (int64_t)cb * DK, DK, ncol, tid);
+        cdS.load(dhsb + (int64_t)cb * DK, DK, ncol, tid);
+        const int64_t rb = t0 * sv + (int64_t)h * DV + cb;
+        cV.load(reinterpret_cast<const E *>(p.v) + rb, sv, clen, tid, ncol);
+        cdO.load(reinterpret_cast<const E *>(p.dout) + rb, sv, clen, tid, ncol);
+        cdX.load(reinterpret_cast<const E *>(p.dv) + rb, sv, clen, tid, ncol);
+    };
+    auto colstore = [&](int db) __attribute__((always_inline)) {
+        const int cb = db * DVB, ncol = DV - cb < DVB ? DV - cb : DVB;
+        cS.store(Ss, PK, ncol, tid);
+        cdS.store(dSs, PK, ncol, tid);
+        cV.store(Vs, PV, clen, tid, ncol);
+        cdO.store(dOs, PV, clen, tid, ncol);
+        cdX.store(dXs, PV, clen, tid, ncol);
     };
     colload(0);
-    rk.store(Ks, PK, nullptr, 0, clen, tid);
-    rq.store(Qs, PK, nullptr, 0, clen, tid);
+    rk.store(Ks, PK, clen, tid);
+    rq.store(Qs, PK, clen, tid);
     ra.store(Am, PT, tid);
     rte.store(TEs, PT, tid);
     if (tid < CH) {
@@ -788,21 +781,18 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     const int cw = 16 * cwave + r16;                           // column within the block
     for (int db = 0; db < ndb; ++db) {
         if (db > 0) __syncthreads();                           // the previous block's reads are done
+        colstore(db);
+        __syncthreads();
         f32x4 Y0[NBH];
         if (colw_ok) {
-            const bool cv = db * DVB + 16 * cwave < DV;
             F Sb[NKB], dSb[NKB];
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) {
-                Sb[kt] = cv ? cS[kt] : F{};
-                dSb[kt] = cv ? cdS[kt] : F{};
+                Sb[kt] = ld_frag<E>(Ss + cw * PK + 16 * kt + 4 * g4);
+                dSb[kt] = ld_frag<E>(dSs + cw * PK + 16 * kt + 4 * g4);
                 if (half == 0) {
                     const f32x4 a = EL::tof(Sb[kt]), b = EL::tof(dSb[kt]);
                     gcacc += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
-                }
-                if (kt / (NKB / 2) == half) {                  // this half's key rows of the S, dS' columns
-                    st_frag<E>(Ss + cw * PK + 16 * kt + 4 * g4, Sb[kt]);
-                    st_frag<E>(dSs + cw * PK + 16 * kt + 4 * g4, dSb[kt]);
                 }
             }
 #pragma unroll
@@ -814,22 +804,12 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 const f32x4 P2 = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return dSb[kt]; });
-                f32x4 X, dO, dx;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = 16 * I + 4 * g4 + j;
-                    const bool ok = cv && row < clen;
-                    dO[j] = ok ? EL::to_f(cdO[ii][j]) : 0.f;
-                    dx[j] = ok ? EL::to_f(cdX[ii][j]) : 0.f;
-                    X[j] = (ok ? EL::to_f(cV[ii][j]) : 0.f) - gx[row] * P[j];
-                    Y0[ii][j] = ge[row] * P2[j];
-                }
-                st_frag<E>(Xs + cw * PT + 16 * I + 4 * g4, EL::cvt(X));
-                st_frag<E>(dOs + cw * PT + 16 * I + 4 * g4, EL::cvt(dO));
-                st_frag<E>(dXs + cw * PT + 16 * I + 4 * g4, EL::cvt(dx));
+                const f32x4 V = EL::tof(ld_colfrag<E>(Vs, PV, 16 * I, 16 * cwave, lane));
+                st_frag<E>(Xs + cw * PT + 16 * I + 4 * g4, EL::cvt(V - ld4(gx + 16 * I + 4 * g4) * P));
+                Y0[ii] = ld4(ge + 16 * I + 4 * g4) * P2;
             }
         }
-        __syncthreads();                                       // X and dO of both halves in LDS
+        __syncthreads();                                       // X of both halves in LDS
         if (colw_ok) {
 #pragma unroll
             for (int ii = 0; ii < NBH; ++ii) {
@@ -840,7 +820,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                     [&](int kb) { return ld_frag<E>(Xs + cw * PT + 16 * kb + 4 * g4); });
                 const f32x4 Y = contract(Y0[ii], NB,
                     [&](int kb) { return ld_colfrag<E>(Am, PT, 16 * kb, 16 * I, lane); },
-                    [&](int kb) { return ld_frag<E>(dOs + cw * PT + 16 * kb + 4 * g4); });
+                    [&](int kb) { return ld_colfrag<E>(dOs, PV, 16 * kb, 16 * cwave, lane); });
                 st_frag<E>(Us + cw * PT + 16 * I + 4 * g4, EL::cvt(U));
                 st_frag<E>(Ys + cw * PT + 16 * I + 4 * g4, EL::cvt(Y));
             }
@@ -851,9 +831,11 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 #pragma unroll
         for (int s = 0; s < JPW; ++s) {
             const int J = J0 + s;
-            aQ[s] = contract(aQ[s], NKD, [&](int kb) { return ld_colfrag<E>(dOs, PT, 16 * kb, 16 * Iw, lane); },
+            aQ[s] = contract(aQ[s], NKD,
+                             [&](int kb) { return ld_frag<E>(dOs + (16 * Iw + r16) * PV + 16 * kb + 4 * g4); },
                              [&](int kb) { return ld_colfrag<E>(Ss, PK, 16 * kb, 16 * J, lane); });
-            aX[s] = contract(aX[s], NKD, [&](int kb) { return ld_colfrag<E>(dXs, PT, 16 * kb, 16 * Iw, lane); },
+            aX[s] = contract(aX[s], NKD,
+                             [&](int kb) { return ld_frag<E>(dXs + (16 * Iw + r16) * PV + 16 * kb + 4 * g4); },
                              [&](int kb) { return ld_colfrag<E>(Ss, PK, 16 * kb, 16 * J, lane); });
             aE[s] = contract(aE[s], NKD, [&](int kb) { return ld_colfrag<E>(Us, PT, 16 * kb, 16 * Iw, lane); },
                              [&](int kb) { return ld_colfrag<E>(dSs, PK, 16 * kb, 16 * J, lane); });
@@ -864,7 +846,8 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             if (l < NL) {
                 int I, J;
                 tile_of(l, I, J);
-                aA[s] = contract(aA[s], NKD, [&](int kb) { return ld_colfrag<E>(dOs, PT, 16 * kb, 16 * I, lane); },
+                aA[s] = contract(aA[s], NKD,
+                                 [&](int kb) { return ld_frag<E>(dOs + (16 * I + r16) * PV + 16 * kb + 4 * g4); },
                                  [&](int kb) { return ld_colfrag<E>(Us, PT, 16 * kb, 16 * J, lane); });
                 aT[s] = contract(aT[s], NKD, [&](int kb) { return ld_colfrag<E>(Ys, PT, 16 * kb, 16 * I, lane); },
                                  [&](int kb) { return ld_colfrag<E>(Xs, PT, 16 * kb, 16 * J, lane); });
