@@ -11,7 +11,10 @@ or 2e-2 (bf16; the kernels round intermediates to bf16 as the forward does),
 dense with a partial last chunk, a padded head (dk = 100, dv = 48), a packed
 batch (empty, one-token and multi-chunk segments), fp16 and 32-token chunks,
 no initial state, the fla_scan contract (hip_scan) and the fused producers
-(L2 norm and beta sigmoid, differentiated in torch before the kernels).
+(L2 norm and beta sigmoid, differentiated in torch before the kernels).  At
+the full 340M shape, where the oracle is too slow, the gradients' directional
+derivative against Richardson-extrapolated central differences of the
+forward kernel (fp32, relative 1e-3).
 """
 import pytest
 import torch
@@ -215,3 +218,46 @@ def test_explicit_backward_matches_autograd():
             assert _rel(a, b) <= 1e-6, name
         else:
             assert torch.equal(a, b), name
+
+
+@pytest.mark.gpu
+def test_chunk_bwd_full_size_directional_derivative():
+    """At the 340M shape (B8 T4096 H8 dk=dv=128, fp32), where the fp64 oracle is
+    too slow: the backward's directional derivative sum_x <grad_x, delta_x> of
+    L = <o, do> + <S_T, dST> equals central differences of the forward kernel
+    along delta, for every input (q, k, v, g, beta, S0) at once."""
+    B, T, H, dk, dv = 8, 4096, 8, 128, 128
+    print('\n[case] chunk_bwd full-size directional derivative', flush=True)
+    g0 = torch.Generator(device='cpu').manual_seed(61)
+    r = lambda *s: torch.randn(*s, generator=g0).cuda()
+    q = F.normalize(r(B, T, H, dk), dim=-1)
+    k = F.normalize(r(B, T, H, dk), dim=-1)
+    v = r(B, T, H, dv)
+    g = F.logsigmoid(r(B, T, H) + 4.0)
+    beta = torch.sigmoid(r(B, T, H))
+    S0 = 0.1 * r(B, H, dk, dv)
+    do, dST = r(B, T, H, dv), r(B, H, dk, dv)
+    xs = [q, k, v, g, beta, S0]
+    # small directions that keep g <= 0 and beta in (0, 1) under +-eps
+    ds = [0.01 * r(*x.shape) for x in xs]
+    ds[3] = -0.01 * torch.rand(*g.shape, generator=g0).cuda()
+    ds[4] = 0.01 * r(*beta.shape) * beta * (1 - beta)
+    scale = dk ** -0.5
+
+    def loss(ys):
+        o, S = ops.chunk_gated_delta_rule(*ys[:5], scale=scale, initial_state=ys[5], output_final_state=True)
+        return (o.double() * do.double()).sum().item() + (S.double() * dST.double()).sum().item()
+
+    grads = ops.chunk_gated_delta_rule_bwd(q, k, v, g, beta, S0, do, dST, scale=scale)
+    ana = sum((gx.double() * d.double()).sum().item() for gx, d in zip(grads, ds))
+    def cd(eps):                                               # central difference along the directions
+        return (loss([x + eps * d for x, d in zip(xs, ds)]) - loss([x - eps * d for x, d in zip(xs, ds)])) / (2 * eps)
+
+    # Richardson extrapolation of two step sizes cancels the O(eps^2) term (the
+    # decays compound over each chunk, so the curvature along g is not small)
+    c1, c2 = cd(0.5), cd(0.25)
+    fd = (4 * c2 - c1) / 3
+    err = abs(ana - fd) / max(abs(fd), 1e-30)
+    print(f'[parity] full-size directional derivative: backward {ana:.6e} central differences {c1:.6e} '
+          f'(eps 0.5) {c2:.6e} (eps 0.25) extrapolated {fd:.6e} rel {err:.2e}', flush=True)
+    assert err <= 1e-3
