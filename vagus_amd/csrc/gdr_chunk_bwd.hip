@@ -29,11 +29,16 @@
 // Kernels, launched after chunk_prep_kernel has rebuilt TE, A and the gate
 // factors of every chunk (the forward's workspace blocks):
 //   chunk_hs_kernel   (sequence, head, dv tile): the forward recurrence again,
-//                     storing each chunk's entry state S (fp32) in the workspace;
+//                     storing each chunk's entry state S in the workspace;
 //   chunk_dhs_kernel  (sequence, head, dv tile): the reverse recurrence for dS,
 //                     writing dV = dX, each chunk's exit-state gradient and dS0;
 //   chunk_grad_kernel (chunk, head), all chunks in parallel: dQ, dK, dbeta, dg
 //                     from the chunk's S, dS', dO, dX.
+// The workspace states are stored in the element type, transposed ([dv][dk]
+// per (chunk, head)): the gradient kernel rounds them to that type for its
+// products anyway, and a lane's four consecutive key rows are one store.  The
+// two walks run compute waves beside producer waves that stage each chunk's
+// operands into a double-buffered LDS slot.
 // Products run on the MFMA units in the C-layout convention of gdr_common.hpp:
 // element-type operands (bf16 / fp16 / fp32) with fp32 accumulation, and fp32
 // operands for the small CH x CH chain (T0, Z, dM), where cancellation makes
