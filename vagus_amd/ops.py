@@ -222,6 +222,8 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
+    assert dht is None or dht.shape == (c.N, c.H, c.dk, c.dv), \
+        f'dht must be {(c.N, c.H, c.dk, c.dv)}, got {tuple(dht.shape)}'
     _check_device(do, dht)
     dop = _aligned(_pad_to(do.to(c.dtype), {1: c.dvp}))
     dSp = None if dht is None else _aligned(_pad_to(dht.float(), {1: c.dvp, 2: c.dkp}))
