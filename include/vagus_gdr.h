@@ -239,6 +239,32 @@ int vgdr_chunk_bwd(int dtype, int gate_kind,
                    float scale, int chunk_size, hipStream_t stream);
 
 /*
+ * The same pair with the forward's intermediates kept instead of recomputed
+ * (no reference counterpart as an entry point; fla's disable_recompute,
+ * linear_attention.py:463-471, is the same trade of memory for time).
+ * vgdr_chunk_fwd_saving is vgdr_chunk_fwd (16-bit dtypes, gate_kind 0/1,
+ * delta rule, no fusion) run in the backward's workspace
+ * (vgdr_chunk_bwd_workspace_size bytes, same dv): besides o and final_state it
+ * leaves there the packed-batch schedule, the chunk blocks and every chunk's
+ * entry state.  vgdr_chunk_bwd_saved, called with the same inputs and that
+ * workspace untouched in between, is vgdr_chunk_bwd without rebuilding them
+ * (it skips the chunk prep and the forward re-walk).
+ */
+int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k, const void *v,
+                          const float *g, const float *beta, void *o, const float *initial_state,
+                          float *final_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                          int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                          float scale, int chunk_size, hipStream_t stream);
+int vgdr_chunk_bwd_saved(int dtype, int gate_kind,
+                         const void *q, const void *k, const void *v, const float *g, const float *beta,
+                         const float *initial_state, const void *grad_o, const float *grad_final_state,
+                         void *grad_q, void *grad_k, void *grad_v, float *grad_g, float *grad_beta,
+                         float *grad_initial_state,
+                         const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                         int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                         float scale, int chunk_size, hipStream_t stream);
+
+/*
  * Token-by-token recurrence.  The decode step is T = 1 with
  * initial_state == final_state (in place), replacing recurrent_scan at
  * linear_attention.py:945-947 and the state.copy_ at :950.  Any T works (the

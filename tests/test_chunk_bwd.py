@@ -51,6 +51,12 @@ def test_chunk_bwd_argument_checks():
     assert call(wsb=16) == _lib.VGDR_ERR_INVALID
     assert call(beta=None) == _lib.VGDR_ERR_INVALID
     assert call(B=0, N=0, T=0) == _lib.VGDR_OK
+    # the saving forward and saved backward: 16-bit, scalar gate or none
+    fwd_saving = lambda dtype, gate: L.vgdr_chunk_fwd_saving(dtype, gate, 4096, 8192, 12288, 16384, 20480, 24576,
+                                                             None, None, None, 49152, 1 << 40, 2, 64, 2, 64, 64, 2,
+                                                             0.125, 64, None)
+    assert fwd_saving(0, 1) == _lib.VGDR_ERR_UNSUPPORTED
+    assert fwd_saving(1, 2) == _lib.VGDR_ERR_UNSUPPORTED
     need = L.vgdr_chunk_bwd_workspace_size(1, 1, 2, 64, 2, 64, 64, 2, 0, 64)
     # forward blocks plus two bf16 states per (chunk, head)
     assert need >= 2 * 2 * 2 * 64 * 64 * 2 + L.vgdr_chunk_workspace_size(1, 1, 2, 64, 2, 64, 2, 0, 64)
@@ -200,11 +206,12 @@ def test_hip_scan_is_differentiable():
 
 
 @pytest.mark.gpu
-def test_explicit_backward_matches_autograd():
-    """ops.chunk_gated_delta_rule_bwd (no autograd) returns what autograd
-    accumulates through chunk_gated_delta_rule: bit for bit for dq, dk, dv,
-    dS0 (same kernels); dg and dbeta sum their row and column terms through
-    LDS atomics, whose order varies, so they agree to rounding."""
+def test_saved_and_recomputed_backward_agree():
+    """Autograd through chunk_gated_delta_rule (16-bit: the saving forward and
+    vgdr_chunk_bwd_saved, which read the entry states the forward kernel
+    stored) against ops.chunk_gated_delta_rule_bwd (vgdr_chunk_bwd, which
+    re-walks the recurrence for them): the same gradients up to the rounding
+    of the two state computations (the oracle bar itself is checked above)."""
     B, T, H, dk, dv = 2, 64, 2, 64, 64
     q, k, v, g, beta, S0, do, dST = (None if x is None else x.cuda()
                                      for x in _inputs(B, T, H, dk, dv, torch.bfloat16, seed=51))
@@ -214,10 +221,9 @@ def test_explicit_backward_matches_autograd():
     o, S = ops.chunk_gated_delta_rule(*leaves[:5], scale=0.125, initial_state=leaves[5], output_final_state=True)
     torch.autograd.backward([o, S], [do, dST])
     for name, a, b in zip(NAMES, got, [x.grad for x in leaves]):
-        if name in ('dg', 'dbeta'):
-            assert _rel(a, b) <= 1e-6, name
-        else:
-            assert torch.equal(a, b), name
+        err = _rel(a, b)
+        print(f'[parity] saved vs recomputed {name} rel_l2={err:.3e}', flush=True)
+        assert err <= 5e-3, name
 
 
 @pytest.mark.gpu

@@ -62,6 +62,10 @@ SIGNATURES = {
     'vgdr_chunk_bwd_workspace_size': (_L, [_I, _I, _L, _L, _L, _L, _L, _L, _I, _I]),
     'vgdr_chunk_bwd': (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                             _L, _L, _L, _L, _L, _L, _F, _I, _P]),
+    'vgdr_chunk_bwd_saved': (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
+                                  _L, _L, _L, _L, _L, _L, _F, _I, _P]),
+    'vgdr_chunk_fwd_saving': (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
+                                   _L, _L, _L, _L, _L, _L, _F, _I, _P]),
     'vgdr_recurrent_fwd': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                 _L, _L, _L, _L, _L, _L, _F, _P]),
     'vgdr_recurrent_fwd_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,

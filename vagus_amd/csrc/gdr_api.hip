@@ -158,12 +158,29 @@ ChunkWs chunk_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, 
     return w;
 }
 
+// workspace of the backward: the forward's (table, blocks), then each chunk's
+// entry state and exit-state gradient (dk x dv per (chunk, head) in the element type)
+struct BwdWs {
+    ChunkWs fwd;
+    int64_t hs_off, dhs_off, total;
+};
+BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                 int64_t n_seqs, bool varlen) {
+    BwdWs w{};
+    w.fwd = chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, varlen);
+    const int64_t states = w.fwd.slots * H * dk * dv * (dtype == VGDR_F32 ? 4 : 2);
+    w.hs_off = (w.fwd.total + 255) / 256 * 256;
+    w.dhs_off = w.hs_off + (states + 255) / 256 * 256;
+    w.total = states > 0 ? w.dhs_off + states : w.fwd.total;
+    return w;
+}
+
 // the three chunk entry points: validation, workspace layout, then the phases asked for
 int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_delta, const void *q, const void *k,
                const void *v, const float *g, const float *beta, void *o, const float *initial_state,
                float *final_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B,
                int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
-               const vgdr_fusion *fusion, hipStream_t stream, const void *w = nullptr) {
+               const vgdr_fusion *fusion, hipStream_t stream, const void *w = nullptr, void *bwd_ws = nullptr) {
     g_err[0] = 0;
     // with an explicit write vector, beta is not read
     int rc = check_common(fn, dtype, gate_kind, w ? 0 : use_delta, q, k, v, g, beta, o, cu_seqlens,
@@ -186,12 +203,18 @@ int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_del
     if (!aligned16(o)) return fail(VGDR_ERR_INVALID, "%s: o must be 16-byte aligned", fn);
     const int chunk = effective_chunk(dtype, dk, chunk_size);
     const ChunkWs ws = chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, cu_seqlens != nullptr);
-    if (ws.total > 0 && (!workspace || workspace_bytes < ws.total || !aligned16(workspace)))
+    // a saving forward runs in the backward's workspace (its prefix is this layout)
+    const int64_t need =
+        bwd_ws ? bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, cu_seqlens != nullptr).total : ws.total;
+    if (need > 0 && (!workspace || workspace_bytes < need || !aligned16(workspace)))
         return fail(VGDR_ERR_INVALID, "%s: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)", fn,
-                    (long long)ws.total, (long long)workspace_bytes, workspace);
+                    (long long)need, (long long)workspace_bytes, workspace);
     if (ws.slots * H > 0x7fffffffLL || (n_seqs * H + 7) / 8 * 8 * ((dv + 31) / 32) > 0x7fffffffLL)
         return fail(VGDR_ERR_INVALID, "%s: grid too large", fn);
     vgdr::ChunkParams p{};
+    p.hs = bwd_ws ? static_cast<char *>(workspace) +
+                        bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, cu_seqlens != nullptr).hs_off
+                  : nullptr;
     p.geo.cu = cu_seqlens;
     p.geo.T = T;
     p.geo.n_tokens = B * T;
@@ -292,24 +315,6 @@ int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, con
                       dv, n_seqs, scale, chunk_size, fusion, stream, w ? w : dummy);
 }
 
-namespace {
-// workspace of the backward: the forward's (table, blocks), then each chunk's
-// entry state and exit-state gradient (dk x dv per (chunk, head) in the element type)
-struct BwdWs {
-    ChunkWs fwd;
-    int64_t hs_off, dhs_off, total;
-};
-BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
-                 int64_t n_seqs, bool varlen) {
-    BwdWs w{};
-    w.fwd = chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, varlen);
-    const int64_t states = w.fwd.slots * H * dk * dv * (dtype == VGDR_F32 ? 4 : 2);
-    w.hs_off = (w.fwd.total + 255) / 256 * 256;
-    w.dhs_off = w.hs_off + (states + 255) / 256 * 256;
-    w.total = states > 0 ? w.dhs_off + states : w.fwd.total;
-    return w;
-}
-}  // namespace
 
 int64_t vgdr_chunk_bwd_workspace_size(int dtype, int gate_kind, int64_t B, int64_t T, int64_t H, int64_t dk,
                                       int64_t dv, int64_t n_seqs, int varlen, int chunk_size) {
@@ -318,13 +323,20 @@ int64_t vgdr_chunk_bwd_workspace_size(int dtype, int gate_kind, int64_t B, int64
     return bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, varlen).total;
 }
 
-int vgdr_chunk_bwd(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
-                   const float *beta, const float *initial_state, const void *grad_o, const float *grad_final_state,
-                   void *grad_q, void *grad_k, void *grad_v, float *grad_g, float *grad_beta,
-                   float *grad_initial_state, const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
-                   int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale,
-                   int chunk_size, hipStream_t stream) {
-    const char *fn = "vgdr_chunk_bwd";
+#define VGDR_BWD_ARGS                                                                                        \
+    int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g, const float *beta,   \
+        const float *initial_state, const void *grad_o, const float *grad_final_state, void *grad_q,            \
+        void *grad_k, void *grad_v, float *grad_g, float *grad_beta, float *grad_initial_state,                 \
+        const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H,    \
+        int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size, hipStream_t stream
+#define VGDR_BWD_PASS                                                                                        \
+    dtype, gate_kind, q, k, v, g, beta, initial_state, grad_o, grad_final_state, grad_q, grad_k, grad_v,        \
+        grad_g, grad_beta, grad_initial_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk, dv, n_seqs, \
+        scale, chunk_size, stream
+
+namespace {
+// both backward entry points; saved: the workspace holds what a saving forward left
+int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS) {
     g_err[0] = 0;
     int rc = check_common(fn, dtype, gate_kind, 1, q, k, v, g, beta, grad_o, cu_seqlens, B, T, H, dk, dv, n_seqs);
     if (rc) return rc;
@@ -382,7 +394,30 @@ int vgdr_chunk_bwd(int dtype, int gate_kind, const void *q, const void *k, const
     p.scale = scale;
     int32_t *table = cu_seqlens ? reinterpret_cast<int32_t *>(wsb) : nullptr;
     if (f.geo.n_seqs == 0) return VGDR_OK;
-    return hip_status(vgdr::chunk_bwd(dtype, (int)dk, chunk, f, p, table, stream), fn);
+    if (saved && dtype == VGDR_F32)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: saved states come from the 16-bit forward kernel", fn);
+    return hip_status(vgdr::chunk_bwd(dtype, (int)dk, chunk, f, p, table, saved, stream), fn);
+}
+}  // namespace
+
+int vgdr_chunk_bwd(VGDR_BWD_ARGS) { return bwd_call("vgdr_chunk_bwd", false, VGDR_BWD_PASS); }
+int vgdr_chunk_bwd_saved(VGDR_BWD_ARGS) { return bwd_call("vgdr_chunk_bwd_saved", true, VGDR_BWD_PASS); }
+#undef VGDR_BWD_ARGS
+#undef VGDR_BWD_PASS
+
+int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
+                          const float *beta, void *o, const float *initial_state, float *final_state,
+                          const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T,
+                          int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
+                          hipStream_t stream) {
+    const char *fn = "vgdr_chunk_fwd_saving";
+    if (dtype == VGDR_F32 || gate_kind == VGDR_GATE_VECTOR) {
+        g_err[0] = 0;
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: saving runs the 16-bit kernel, scalar gate or none", fn);
+    }
+    return chunk_call(fn, vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, dtype, gate_kind, 1, q, k, v, g, beta, o,
+                      initial_state, final_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk, dv, n_seqs,
+                      scale, chunk_size, nullptr, stream, nullptr, workspace);
 }
 
 #undef VGDR_CHUNK_ARGS

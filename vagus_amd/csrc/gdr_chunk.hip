@@ -1098,7 +1098,10 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 // One workgroup barrier per chunk: the double-buffer hand-over.
 // One workgroup per CU (LDS-limited) of NW + NP <= 8 waves: at most two waves per
 // SIMD, so the compiler may use up to 256 registers per wave for lookahead.
-template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA>
+// HS: also store each chunk's entry state (the element-type copy the products
+// use) to p.hs, transposed ([chunk slot, H, dv, dk]): the states the chunked
+// backward reads, saved by a training forward instead of recomputed.
+template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA, bool HS = false>
 __global__ void __launch_bounds__(64 * (NW + NP)) __attribute__((amdgpu_waves_per_eu(1, 2)))
 chunk_state_tr_kernel(const ChunkParams p) {
     static_assert(sizeof(E) == 2, "transpose reads take 16-bit elements");
@@ -1271,6 +1274,17 @@ chunk_state_tr_kernel(const ChunkParams p) {
         F2 Sb[NKB / 2];
 #pragma unroll
         for (int q = 0; q < NKB / 2; ++q) Sb[q] = EL::cvt2(S[2 * q], S[2 * q + 1]);
+        if constexpr (HS) {
+            // lane (g, r) holds rows 16 kt + 4 g .. + 3 of column col0 + wcol + r
+            E *hs = reinterpret_cast<E *>(p.hs) + (((cbase + c) * H + h) * (int64_t)DV + col0 + wcol + r16) * DK +
+                    4 * g4;
+#pragma unroll
+            for (int q = 0; q < NKB / 2; ++q) {
+                typedef E E4 __attribute__((ext_vector_type(4)));
+                *reinterpret_cast<E4 *>(hs + 32 * q) = __builtin_shufflevector(Sb[q], Sb[q], 0, 1, 2, 3);
+                *reinterpret_cast<E4 *>(hs + 32 * q + 16) = __builtin_shufflevector(Sb[q], Sb[q], 4, 5, 6, 7);
+            }
+        }
         // V rows in C layout: U[I][j] = V[16 I + 4 g + j][wcol + r]
         f32x4 U[NB];
 #pragma unroll
@@ -1376,6 +1390,17 @@ static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hip
     if constexpr (sizeof(E) == 2) {
         // 16-bit elements: the transpose-read kernel, 8 waves in all
         constexpr bool VEC = GATE == 2;
+        if constexpr (!VEC && DELTA) {
+            if (p.hs) {                                       // a training forward: entry states saved
+                if (nw == 4)
+                    hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, false, true, true>),
+                                       dim3((unsigned)state_blocks), dim3(64 * 8), 0, stream, p);
+                else
+                    hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 6, E, false, true, true>),
+                                       dim3((unsigned)state_blocks), dim3(64 * 8), 0, stream, p);
+                return;
+            }
+        }
         if (nw == 4)
             hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, VEC, DELTA>), dim3((unsigned)state_blocks),
                                dim3(64 * 8), 0, stream, p);

@@ -1080,7 +1080,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 // launch
 // ===========================================================================
 template <int DK, int CH, typename E>
-static hipError_t run_bwd(ChunkBwdParams p, hipStream_t stream) {
+static hipError_t run_bwd(ChunkBwdParams p, bool saved, hipStream_t stream) {
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
     // Both walks take 32-column tiles (256 workgroups at B = 8, H = 8, dv =
     // 128) with two compute and two producer waves (measured at B8 T4096 H8
@@ -1088,8 +1088,9 @@ static hipError_t run_bwd(ChunkBwdParams p, hipStream_t stream) {
     // their own operands, 1.00 ms with producers; 1.02 ms with 64-column tiles).
     if (units > 0) {
         p.n_tiles = (p.DV + 31) / 32;
-        hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
-                           dim3(256), 0, stream, p);
+        if (!saved)                                            // else a training forward stored the states
+            hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
+                               dim3(256), 0, stream, p);
         hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
                            dim3(256), 0, stream, p);
     }
@@ -1100,16 +1101,19 @@ static hipError_t run_bwd(ChunkBwdParams p, hipStream_t stream) {
 }
 
 hipError_t chunk_bwd(int dtype, int dk, int chunk, const ChunkParams &fwd, ChunkBwdParams p, int32_t *table,
-                     hipStream_t stream) {
+                     bool saved, hipStream_t stream) {
     if (p.geo.n_seqs == 0) return hipSuccess;
     // TE, A and the gate factors of every chunk, as the forward built them
-    hipError_t e = chunk_fwd(dtype, dk, chunk, 0, fwd, table, CHUNK_PREP, stream);
-    if (e != hipSuccess) return e;
+    // (already in the workspace after a saving forward)
+    if (!saved) {
+        hipError_t e = chunk_fwd(dtype, dk, chunk, 0, fwd, table, CHUNK_PREP, stream);
+        if (e != hipSuccess) return e;
+    }
     if (p.geo.cu) {
         p.geo.chunk_offs = table + 2 * p.geo.n_seqs;
         p.geo.order = table + 3 * p.geo.n_seqs + 1;
     }
-#define VGDR_BWD(DK_, CH_, E_) return run_bwd<DK_, CH_, E_>(p, stream);
+#define VGDR_BWD(DK_, CH_, E_) return run_bwd<DK_, CH_, E_>(p, saved, stream);
     if (dtype == 1) {
         if (dk == 64) { if (chunk == 32) { VGDR_BWD(64, 32, __bf16) } VGDR_BWD(64, 64, __bf16) }
         if (chunk == 32) { VGDR_BWD(128, 32, __bf16) } VGDR_BWD(128, 64, __bf16)

@@ -86,6 +86,7 @@ struct ChunkParams {
     float scale;
     Fusion fz;
     const void *w;                // [n_tokens, H, dk] write vectors in place of beta k (per-channel gate), or NULL
+    void *hs;                     // [chunk slots, H, dv, dk] entry states for the backward (16-bit, scalar gate), or NULL
 };
 
 // Backward of the chunked scan (scalar gate or none, delta rule).  q, k are the
@@ -142,9 +143,11 @@ int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H,
 
 // The backward: chunk prep (with `fwd`, the same call's forward parameters,
 // writing the blocks p.blocks points at), then the walks and the per-chunk
-// gradients.  table: the packed-batch schedule (as chunk_fwd).
+// gradients.  table: the packed-batch schedule (as chunk_fwd).  saved: a
+// forward with ChunkParams::hs = p.hs already left the schedule, the blocks
+// and the entry states in the workspace; the prep and the entry walk are skipped.
 hipError_t chunk_bwd(int dtype, int dk, int chunk, const ChunkParams &fwd, ChunkBwdParams p, int32_t *table,
-                     hipStream_t stream);
+                     bool saved, hipStream_t stream);
 
 hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
                          hipStream_t stream);

@@ -209,7 +209,7 @@ class _Call:
 
 
 def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, cu_seqlens=None,
-                               chunk_size=64):
+                               chunk_size=64, saved_workspace=None):
     """Backward of chunk_gated_delta_rule without autograd (vgdr_chunk_bwd):
     the gradients of (o, final_state) under the cotangents do (and dht, None =
     zero) with respect to q, k, v, g, beta and initial_state, for the delta
@@ -217,7 +217,10 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     forward scanned them (normalised), beta in [0, 1].  Returns (dq, dk, dv,
     dg, dbeta, dh0) in the inputs' dtypes; dg is None without a gate and dh0
     None without an initial state.  The gradients the reference's training
-    takes through chunk_scan (linear_attention.py:237-309) or fla's backward."""
+    takes through chunk_scan (linear_attention.py:237-309) or fla's backward.
+    saved_workspace: the workspace a saving forward (_chunk_fwd_saving, same
+    inputs) filled; the backward then skips rebuilding the chunk blocks and
+    the per-chunk entry states."""
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate='scalar' if g is not None else 'none', delta=True,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
     scale = c.dk ** -0.5 if scale is None else float(scale)
@@ -237,9 +240,13 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     dtype = _DTYPES[c.dtype]
     nbytes = L.vgdr_chunk_bwd_workspace_size(dtype, c.gate_kind, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
                                              int(c.cu is not None), int(chunk_size))
-    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+    if saved_workspace is not None:
+        assert saved_workspace.numel() >= nbytes, 'saved_workspace is smaller than this backward needs'
+        ws, fn = saved_workspace, L.vgdr_chunk_bwd_saved
+    else:
+        ws, fn = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device), L.vgdr_chunk_bwd
     with torch.cuda.device(c.device):
-        _lib.check(L.vgdr_chunk_bwd(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g), _ptr(c.beta),
+        _lib.check(fn(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g), _ptr(c.beta),
                                     _ptr(c.h0), _ptr(dop), _ptr(dSp), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg),
                                     _ptr(db), _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes, c.B, c.T, c.H, c.dkp, c.dvp,
                                     c.N, scale, int(chunk_size), _stream(c.device)))
@@ -252,15 +259,46 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     return dq, dk, dv, None if dg is None else dg.to(g.dtype), db.to(beta.dtype), dS0
 
 
+def _chunk_fwd_saving(q, k, v, g, beta, initial_state, *, scale, cu_seqlens, chunk_size):
+    """vgdr_chunk_fwd_saving: the chunked forward (16-bit, scalar gate or none,
+    delta rule) run in a backward workspace, which keeps the chunk blocks and
+    every chunk's entry state for vgdr_chunk_bwd_saved.  Returns (o,
+    final_state, workspace)."""
+    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate='scalar' if g is not None else 'none', delta=True,
+              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+    o, S = c.new_output(), c.new_state()
+    L = _lib.load()
+    dtype = _DTYPES[c.dtype]
+    nbytes = L.vgdr_chunk_bwd_workspace_size(dtype, c.gate_kind, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
+                                             int(c.cu is not None), int(chunk_size))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+    with torch.cuda.device(c.device):
+        _lib.check(L.vgdr_chunk_fwd_saving(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
+                                           _ptr(c.beta), _ptr(o), _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws), nbytes,
+                                           c.B, c.T, c.H, c.dkp, c.dvp, c.N, float(scale), int(chunk_size),
+                                           _stream(c.device)))
+    return c.unpad_o(o), c.unpad_state(S), ws
+
+
 class _ChunkDeltaRule(torch.autograd.Function):
-    """The chunked delta rule with a scalar gate or none, differentiable:
-    forward vgdr_chunk_fwd, backward vgdr_chunk_bwd.  q, k arrive normalised,
-    beta in [0, 1]."""
+    """The chunked delta rule with a scalar gate or none, differentiable.
+    16-bit inputs: forward vgdr_chunk_fwd_saving, which keeps the chunk blocks
+    and the per-chunk entry states in the backward's workspace, and backward
+    vgdr_chunk_bwd_saved (fla's disable_recompute trade: about 2 dk dv bytes
+    per chunk and head of device memory held from forward to backward for
+    skipping two of the backward's kernels).  fp32: forward vgdr_chunk_fwd,
+    backward vgdr_chunk_bwd.  q, k arrive normalised, beta in [0, 1]."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, beta, S0, scale, cu, chunk_size):
-        o, S = chunk_scan(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True, scale=scale,
-                          initial_state=S0, output_final_state=True, cu_seqlens=cu, chunk_size=chunk_size)
+        ctx.ws = None
+        if q.dtype != torch.float32:
+            o, S, ctx.ws = _chunk_fwd_saving(q, k, v, g, beta, S0, scale=scale, cu_seqlens=cu,
+                                             chunk_size=chunk_size)
+        else:
+            o, S = chunk_scan(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True,
+                              scale=scale, initial_state=S0, output_final_state=True, cu_seqlens=cu,
+                              chunk_size=chunk_size)
         ctx.save_for_backward(q, k, v, g, beta, S0, cu)
         ctx.scale, ctx.chunk_size = scale, chunk_size
         return o, S
@@ -271,7 +309,8 @@ class _ChunkDeltaRule(torch.autograd.Function):
         if do is None:
             do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
         grads = chunk_gated_delta_rule_bwd(q, k, v, g, beta, S0, do, dS, scale=ctx.scale, cu_seqlens=cu,
-                                           chunk_size=ctx.chunk_size)
+                                           chunk_size=ctx.chunk_size, saved_workspace=ctx.ws)
+        ctx.ws = None
         return grads + (None, None, None)
 
 
