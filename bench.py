@@ -38,7 +38,8 @@ Also reported on the same line:
   backward      the chunked backward at the headline shape (all six
                 gradients), against the reference's count for the backward:
                 2 x 180,224 FLOP per token-head (chunk_scan_flops counts
-                forward + backward as 3 x the forward)
+                forward + backward as 3 x the forward); and the training pair
+                (saving forward + saved backward) against 3 x 180,224
   kda, varlen   KDA prefill (B=4 T=8192 H=8) and packed GDN prefill (32
                 segments U[128, 8192], H=16) tokens/s and TFLOP/s
   cpu_baseline  the oracle's torch fp32 chunk form (the reference's CPU path)
@@ -255,6 +256,17 @@ def bench_backward(torch, ops, workloads, steps, warmup):
                                        scale=DK ** -0.5)
 
     us = _event_us(torch, step, steps, warmup)
+
+    # the training pair autograd runs for 16-bit inputs: the saving forward, then
+    # the backward that reads the states and blocks it left
+    def pair(i):
+        x = xs[i % 2]
+        o, S, ws = ops._chunk_fwd_saving(x.q, x.k, x.v, x.g, x.beta, x.initial_state, scale=DK ** -0.5,
+                                         cu_seqlens=None, chunk_size=CHUNK)
+        ops.chunk_gated_delta_rule_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, dos[i % 2], dST,
+                                       scale=DK ** -0.5, saved_workspace=ws)
+
+    pair_us = _event_us(torch, pair, steps, warmup)
     x0 = xs[0]
     th = x0.q.shape[0] * x0.q.shape[1] * x0.q.shape[2]
     del xs, dos
@@ -263,7 +275,11 @@ def bench_backward(torch, ops, workloads, steps, warmup):
             'kernels': 'chunk_prep_kernel + chunk_hs_kernel + chunk_dhs_kernel + chunk_grad_kernel',
             'us': round(us, 1), 'tok_s': round(x0.q.shape[0] * x0.q.shape[1] / (us * 1e-6), 1),
             'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
-            'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5)}
+            'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5),
+            'train_pair_us': round(pair_us, 1),
+            'train_pair': 'vgdr_chunk_fwd_saving + vgdr_chunk_bwd_saved (what autograd runs for 16-bit inputs): '
+                          'forward and backward with the entry states kept, not recomputed',
+            'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2)}
 
 
 def cpu_baseline(torch, workloads):
