@@ -1099,8 +1099,8 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 // One workgroup per CU (LDS-limited) of NW + NP <= 8 waves: at most two waves per
 // SIMD, so the compiler may use up to 256 registers per wave for lookahead.
 // HS: also store each chunk's entry state (the element-type copy the products
-// use) to p.hs, transposed ([chunk slot, H, dv, dk]): the states the chunked
-// backward reads, saved by a training forward instead of recomputed.
+// use) to p.hs ([chunk slot, H] checkpoints in ckpt_pos order): the states the
+// chunked backward reads, saved by a training forward instead of recomputed.
 template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA, bool HS = false>
 __global__ void __launch_bounds__(64 * (NW + NP)) __attribute__((amdgpu_waves_per_eu(1, 2)))
 chunk_state_tr_kernel(const ChunkParams p) {
@@ -1275,14 +1275,16 @@ chunk_state_tr_kernel(const ChunkParams p) {
 #pragma unroll
         for (int q = 0; q < NKB / 2; ++q) Sb[q] = EL::cvt2(S[2 * q], S[2 * q + 1]);
         if constexpr (HS) {
-            // lane (g, r) holds rows 16 kt + 4 g .. + 3 of column col0 + wcol + r
-            E *hs = reinterpret_cast<E *>(p.hs) + (((cbase + c) * H + h) * (int64_t)DV + col0 + wcol + r16) * DK +
-                    4 * g4;
+            // lane (g, r) holds rows 16 kt + 4 g .. + 3 of column col0 + wcol + r: the
+            // checkpoint's fragment order, one contiguous run per key block
+            E *hs = reinterpret_cast<E *>(p.hs) + ((cbase + c) * H + h) * (int64_t)DK * DV;
+            const int cb = (col0 + wcol) >> 4;
 #pragma unroll
             for (int q = 0; q < NKB / 2; ++q) {
                 typedef E E4 __attribute__((ext_vector_type(4)));
-                *reinterpret_cast<E4 *>(hs + 32 * q) = __builtin_shufflevector(Sb[q], Sb[q], 0, 1, 2, 3);
-                *reinterpret_cast<E4 *>(hs + 32 * q + 16) = __builtin_shufflevector(Sb[q], Sb[q], 4, 5, 6, 7);
+                *reinterpret_cast<E4 *>(hs + ckpt_pos<DK>(cb, 2 * q, ln)) = __builtin_shufflevector(Sb[q], Sb[q], 0, 1, 2, 3);
+                *reinterpret_cast<E4 *>(hs + ckpt_pos<DK>(cb, 2 * q + 1, ln)) =
+                    __builtin_shufflevector(Sb[q], Sb[q], 4, 5, 6, 7);
             }
         }
         // V rows in C layout: U[I][j] = V[16 I + 4 g + j][wcol + r]

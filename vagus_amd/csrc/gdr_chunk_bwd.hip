@@ -34,9 +34,10 @@
 //                     writing dV = dX, each chunk's exit-state gradient and dS0;
 //   chunk_grad_kernel (chunk, head), all chunks in parallel: dQ, dK, dbeta, dg
 //                     from the chunk's S, dS', dO, dX.
-// The workspace states are stored in the element type, transposed ([dv][dk]
-// per (chunk, head)): the gradient kernel rounds them to that type for its
-// products anyway, and a lane's four consecutive key rows are one store.  The
+// The workspace states are stored in the element type, in the C-layout
+// fragment order of ckpt_pos: the gradient kernel rounds them to that type for
+// its products anyway, and a wavefront's 16 columns are one contiguous store
+// per key block.  The
 // two walks run compute waves beside producer waves that stage each chunk's
 // operands into a double-buffered LDS slot.
 // Products run on the MFMA units in the C-layout convention of gdr_common.hpp:
@@ -76,6 +77,42 @@ struct RowRegs {
             if (u < UNITS) {
                 const int row = u / UPR, c0 = (u % UPR) * VE;
                 *reinterpret_cast<V *>(dst + row * pitch + c0) = (row < rows && c0 < cols) ? x[i] : V{};
+            }
+        });
+    }
+};
+
+// NCB column blocks (16 columns each) of a state checkpoint (ckpt_pos order, a
+// contiguous run) in registers; store() writes them as an LDS matrix
+// dst[c][d] (column c of the blocks, key row d; pitch keeps 8-byte fragments
+// aligned), column blocks >= `ncb` zeroed.
+template <typename E, int DK, int NCB, int NT>
+struct CkptRegs {
+    static constexpr int VE = 16 / (int)sizeof(E), UNITS = NCB * DK * 16 / VE, N = (UNITS + NT - 1) / NT;
+    static constexpr int NKB = DK / 16;
+    typedef E V __attribute__((ext_vector_type(VE)));
+    V x[N];
+    __device__ __forceinline__ void load(const E *src, int ncb, int tid) {
+        unroll<N>([&](auto i) __attribute__((always_inline)) {
+            const int u = tid + (int)i * NT;
+            const bool ok = u < UNITS && u * VE / (DK * 16) < ncb;
+            x[i] = *reinterpret_cast<const V *>(src + (ok ? u * VE : 0));
+        });
+    }
+    __device__ __forceinline__ void store(E *dst, int pitch, int ncb, int tid) const {
+        using F = typename Elem<E>::frag;
+        unroll<N>([&](auto i) __attribute__((always_inline)) {
+            const int u = tid + (int)i * NT;
+            if (u < UNITS) {
+#pragma unroll
+                for (int hh = 0; hh < VE / 4; ++hh) {
+                    const int e0 = u * VE + 4 * hh;               // ckpt_pos(cb, kt, l) of these four
+                    const int l = (e0 >> 2) & 63, kt = (e0 >> 8) % NKB, cb = e0 / (256 * NKB);
+                    F f;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) f[e] = cb < ncb ? x[i][4 * hh + e] : E(0.f);
+                    *reinterpret_cast<F *>(dst + (16 * cb + (l & 15)) * pitch + 16 * kt + 4 * (l >> 4)) = f;
+                }
             }
         });
     }
@@ -309,9 +346,9 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
             S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
     auto store_state = [&](int c) __attribute__((always_inline)) {
         if (wvalid) {
-            E *hs = reinterpret_cast<E *>(p.hs) + (((u.cbase + c) * H + h) * DV + col) * DK + 4 * g4;
+            E *hs = reinterpret_cast<E *>(p.hs) + ((u.cbase + c) * H + h) * (int64_t)DK * DV;
 #pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(hs + 16 * kt, EL::cvt(S[kt]));
+            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(hs + ckpt_pos<DK>(colw >> 4, kt, lane), EL::cvt(S[kt]));
         }
     };
     // V rows (C layout) and TE fragments (lower tiles) of the next chunk, raw:
@@ -525,9 +562,9 @@ __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdPara
         const int64_t t0 = u.bos + (int64_t)c * CH;
         const int clen = clen_of(c);
         if (wvalid) {
-            E *dhs = reinterpret_cast<E *>(p.dhs) + ((slot * H + h) * DV + col) * DK + 4 * g4;
+            E *dhs = reinterpret_cast<E *>(p.dhs) + (slot * H + h) * (int64_t)DK * DV;
 #pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(dhs + 16 * kt, EL::cvt(dS[kt]));
+            for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(dhs + ckpt_pos<DK>(colw >> 4, kt, lane), EL::cvt(dS[kt]));
         }
         f32x4 dO[NB];
 #pragma unroll
@@ -615,7 +652,7 @@ struct GradLayout {
     static constexpr int PERS = (2 * CH * PK + CH * PT) * ES;
     // column phase: A; the block's V, dO, dX rows (CH tokens, row-major); its
     // columns of X, U, dU (CH tokens each) and of S, dS' (DK key channels
-    // each, the workspace's [dv][dk] order), stored column by column
+    // each), stored column by column
     static constexpr int COLS = (CH * PT + 3 * CH * PV + 3 * DVB * PT + 2 * DVB * PK) * ES;
     // CH x CH phase: N, dTE, T0 (then Z) in fp32; W_A and W_N + W_N^T in the element type
     static constexpr int SQ = 3 * CH * PF * 4 + 2 * CH * PT * ES;
@@ -721,17 +758,17 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         }
     }
     // The column phase's global operands of one dv block, as whole 16-byte
-    // rows: S and dS' columns (the workspace's [dv][dk] rows), and the V, dO,
+    // units: S and dS' columns (the checkpoints' contiguous runs), and the V, dO,
     // dX rows.  Loaded a dv block ahead: block 0 with the staging loads, block
     // db + 1 during block db's products.
     const int cwave = wave & 3, half = wave >> 2;
     const bool colw_ok = cwave < NCW;
-    RowRegs<E, DVB, DK, NT> cS, cdS;
+    CkptRegs<E, DK, NCW, NT> cS, cdS;
     RowRegs<E, CH, DVB, NT> cV, cdO, cdX;
     auto colload = [&](int db) __attribute__((always_inline)) {
         const int cb = db * DVB, ncol = DV - cb < DVB ? DV - cb : DVB;
-        cS.load(hsb + (int64_t)cb * DK, DK, ncol, tid);
-        cdS.load(dhsb + (int64_t)cb * DK, DK, ncol, tid);
+        cS.load(hsb + (int64_t)cb * DK, ncol >> 4, tid);        // ckpt_pos(cb / 16, 0, 0) = cb DK
+        cdS.load(dhsb + (int64_t)cb * DK, ncol >> 4, tid);
         const int64_t rb = t0 * sv + (int64_t)h * DV + cb;
         cV.load(reinterpret_cast<const E *>(p.v) + rb, sv, clen, tid, ncol);
         cdO.load(reinterpret_cast<const E *>(p.dout) + rb, sv, clen, tid, ncol);
@@ -739,8 +776,8 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     };
     auto colstore = [&](int db) __attribute__((always_inline)) {
         const int cb = db * DVB, ncol = DV - cb < DVB ? DV - cb : DVB;
-        cS.store(Ss, PK, ncol, tid);
-        cdS.store(dSs, PK, ncol, tid);
+        cS.store(Ss, PK, ncol >> 4, tid);
+        cdS.store(dSs, PK, ncol >> 4, tid);
         cV.store(Vs, PV, clen, tid, ncol);
         cdO.store(dOs, PV, clen, tid, ncol);
         cdX.store(dXs, PV, clen, tid, ncol);

@@ -69,6 +69,17 @@ __device__ __forceinline__ typename Elem<E>::frag gfrag(const E *p) {
     return *reinterpret_cast<const typename Elem<E>::frag *>(p);
 }
 
+// The chunked backward's per-(chunk, head) state checkpoints (dk x dv in the
+// element type) are stored in C-layout fragment order: for column block cb
+// (columns 16 cb .. 16 cb + 15) and key block kt, lane l = 16 g + r holds rows
+// 16 kt + 4 g .. + 3 of column 16 cb + r, the four entries at ckpt_pos(cb, kt,
+// l).  A wavefront that owns a column block writes one contiguous 512-element
+// run per key block, and the column blocks of a dv range are contiguous.
+template <int DK>
+__device__ __forceinline__ int64_t ckpt_pos(int cb, int kt, int lane) {
+    return ((int64_t)(cb * (DK / 16) + kt) * 64 + lane) * 4;
+}
+
 // gfx950 ds_read_b64_tr_b16: within each 16-lane group, source lane s gives the
 // address of 4 consecutive 16-bit elements, and result lane d receives element
 // d % 4 of source lanes d / 4 + 4 i (i = 0..3).  With source lane s pointing at
