@@ -265,6 +265,32 @@ int vgdr_chunk_bwd_saved(int dtype, int gate_kind,
                          float scale, int chunk_size, hipStream_t stream);
 
 /*
+ * Backward of every scan form: the per-channel (KDA) gate, the explicit write
+ * vector w (the asymmetric delta rule) and the plain recurrence without the
+ * delta rule, besides the scalar gate and no gate.  Replaces the autograd of
+ * chunk_scan_vec (linear_attention.py:312-425, the KDA and w path) and of
+ * recurrent_scan / chunk_scan for use_delta = 0 (:161-195, :237-309).
+ * Inputs as vgdr_recurrent_fwd_w (w != NULL) or vgdr_recurrent_fwd; beta is
+ * read only for the delta rule without w.  Gradients: grad_q, grad_k, grad_v
+ * (and grad_w with w) in dtype; grad_g (the gate's shape, gate_kind != 0),
+ * grad_beta (delta rule without w) and grad_initial_state (may be NULL) in
+ * fp32.  grad_final_state may be NULL (zero).  dk in {64, 128}; dv a positive
+ * multiple of 16.  Workspace: vgdr_scan_bwd_workspace_size(...) bytes,
+ * 16-byte aligned (state checkpoints every 8 tokens in fp32, u_t per token,
+ * per-column-tile partial sums).
+ */
+int64_t vgdr_scan_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs);
+int vgdr_scan_bwd(int dtype, int gate_kind, int use_delta,
+                  const void *q, const void *k, const void *v, const void *w,
+                  const float *g, const float *beta, const float *initial_state,
+                  const void *grad_o, const float *grad_final_state,
+                  void *grad_q, void *grad_k, void *grad_v, void *grad_w,
+                  float *grad_g, float *grad_beta, float *grad_initial_state,
+                  const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                  int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                  float scale, hipStream_t stream);
+
+/*
  * Token-by-token recurrence.  The decode step is T = 1 with
  * initial_state == final_state (in place), replacing recurrent_scan at
  * linear_attention.py:945-947 and the state.copy_ at :950.  Any T works (the

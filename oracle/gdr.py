@@ -15,7 +15,7 @@ beta_t (linear_attention.py:8-11):
 Functions and the reference lines they follow:
 
     recurrent       linear_attention.py:161-195   the definition (with the asymmetric write w)
-    recurrent_grads linear_attention.py:237-309   gradients of the scan (autograd of the fp64 recurrence)
+    recurrent_grads linear_attention.py:237-425   gradients of the scans (autograd of the fp64 recurrence)
     chunk_scalar    linear_attention.py:237-309   WY chunk form, scalar / no gate
     chunk_vector    linear_attention.py:312-425   WY chunk form, per-channel gate (and w)
     chunk           linear_attention.py:251-252   dispatch on g.dim()
@@ -108,15 +108,16 @@ def recurrent(q, k, v, g, beta, S0=None, *, scale: float, delta: bool = True, w=
     return o.to(q.dtype), S
 
 
-def recurrent_grads(q, k, v, g, beta, S0, do, dST=None, *, scale: float, delta: bool = True):
+def recurrent_grads(q, k, v, g, beta, S0, do, dST=None, *, scale: float, delta: bool = True, w=None):
     """Gradients of ``recurrent``'s (o, final S) under the cotangents do (and
     dST, the final state's; None = zero), by reverse-mode differentiation of
     the fp64 recurrence: the gradients the reference's training takes through
-    chunk_scan's autograd (linear_attention.py:237-309), which computes the
-    same function.  Returns (dq, dk, dv, dg, dbeta, dS0) in fp64; None for
-    absent inputs (g, beta without the delta rule, S0)."""
-    leaves = [None if x is None else x.detach().double().requires_grad_(True) for x in (q, k, v, g, beta, S0)]
-    o, S = recurrent(*leaves, scale=scale, delta=delta)
+    chunk_scan / chunk_scan_vec's autograd (linear_attention.py:237-309,
+    :312-425), which computes the same function.  Returns (dq, dk, dv, dg,
+    dbeta, dS0) in fp64, with dw appended when an explicit write w is given
+    (beta is then unused and its gradient zero); None for absent inputs."""
+    leaves = [None if x is None else x.detach().double().requires_grad_(True) for x in (q, k, v, g, beta, S0, w)]
+    o, S = recurrent(*leaves[:6], scale=scale, delta=delta, w=leaves[6])
     outs, cots = [o], [do.double()]
     if dST is not None:
         outs.append(S)
@@ -134,7 +135,7 @@ def recurrent_grads(q, k, v, g, beta, S0, do, dST=None, *, scale: float, delta: 
         else:
             gx = next(grads)
             res.append(torch.zeros_like(x) if gx is None else gx)
-    return tuple(res)
+    return tuple(res) if w is not None else tuple(res[:6])
 
 
 # ---------------------------------------------------------------------------

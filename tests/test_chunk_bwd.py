@@ -4,8 +4,7 @@ recurrent_grads (reverse-mode through the fp64 recurrence, pinned in
 tests/test_oracle.py by finite differences and by the chunk form's own
 gradients).
 
-CPU: the C ABI's argument checks (no launch) and the NotImplementedError of
-combinations without a backward.
+CPU: the C ABI's argument checks (no launch); CPU tensors fail loudly.
 GPU: every gradient (dq, dk, dv, dg, dbeta, dS0) at rel_l2 <= 1e-5 (fp32)
 or 2e-2 (bf16; the kernels round intermediates to bf16 as the forward does),
 dense with a partial last chunk, a padded head (dk = 100, dv = 48), a packed
@@ -62,13 +61,9 @@ def test_chunk_bwd_argument_checks():
     assert need >= 2 * 2 * 2 * 64 * 64 * 2 + L.vgdr_chunk_workspace_size(1, 1, 2, 64, 2, 64, 2, 0, 64)
 
 
-def test_calls_without_a_backward_raise():
+def test_cpu_tensors_with_grad_fail_loudly():
     q = torch.randn(1, 4, 2, 64, requires_grad=True)
-    with pytest.raises(NotImplementedError):
-        ops.chunk_kda(q, q, q, torch.zeros(1, 4, 2, 64), torch.ones(1, 4, 2))
-    with pytest.raises(NotImplementedError):
-        ops.chunk_simple_gla(q, q, q, torch.zeros(1, 4, 2))
-    with pytest.raises(RuntimeError, match='ROCm GPU'):                 # a CPU tensor still fails loudly
+    with pytest.raises(RuntimeError, match='ROCm GPU'):                 # no CPU path, with or without grad
         ops.chunk_gated_delta_rule(q, q, q, torch.zeros(1, 4, 2), torch.ones(1, 4, 2))
 
 

@@ -281,3 +281,55 @@ def test_recurrent_grads_match_chunk_form_gradients(gate):
     got = torch.autograd.grad([o, S], [x for x in leaves if x is not None], [do, dST])
     for a, b in zip([x for x in ref if x is not None], got):
         assert torch.allclose(a, b, rtol=1e-9, atol=1e-10)
+
+
+@pytest.mark.parametrize('mode', ['vector', 'vector_w', 'vector_nodelta', 'scalar_w', 'none_nodelta'])
+def test_recurrent_grads_other_forms_match_finite_differences(mode):
+    """gradcheck of the per-channel gate, the explicit write w and the plain
+    (no delta rule) recurrence, each with an initial state and a final-state
+    cotangent; dw must be the gradient of w and dbeta zero when w replaces
+    beta k."""
+    gate = mode.split('_')[0]
+    delta = not mode.endswith('nodelta')
+    q, k, v, g, beta, S0 = inputs(B=1, L=6, H=1, dk=3, dv=2, seed=21, gate=gate)
+    gen = torch.Generator().manual_seed(22)
+    w = 0.5 * torch.randn(1, 6, 1, 3, generator=gen, dtype=torch.float64) if mode.endswith('_w') else None
+    do = torch.randn(1, 6, 1, 2, generator=gen, dtype=torch.float64)
+    dST = torch.randn(1, 1, 3, 2, generator=gen, dtype=torch.float64)
+    got = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=0.7, delta=delta, w=w)
+    names = ['q', 'k', 'v', 'g', 'beta', 'S0', 'w']
+    vals = dict(zip(names, (q, k, v, g, beta, S0, w)))
+    live = [n for n in names if vals[n] is not None and not (n == 'beta' and (w is not None or not delta))]
+
+    def loss(*xs):
+        d = dict(vals, **dict(zip(live, xs)))
+        o, S = gdr.recurrent(d['q'], d['k'], d['v'], d['g'], d['beta'], d['S0'], scale=0.7, delta=delta, w=d['w'])
+        return (o * do).sum() + (S * dST).sum()
+
+    leaves = [vals[n].clone().requires_grad_(True) for n in live]
+    assert torch.autograd.gradcheck(loss, leaves, eps=1e-6, atol=1e-7, rtol=1e-6)
+    ref = dict(zip(live, torch.autograd.grad(loss(*leaves), leaves)))
+    mine = dict(zip(names, got))
+    for n in live:
+        assert torch.allclose(mine[n], ref[n], rtol=1e-12, atol=1e-12), n
+    if w is not None or not delta:
+        assert mine['beta'] is None or float(mine['beta'].abs().max()) == 0.0
+
+
+@pytest.mark.parametrize('with_w', [False, True])
+def test_recurrent_grads_match_vector_chunk_form_gradients(with_w):
+    """Per-channel gate: the same gradients through the independent gated
+    chunk form (gated inner products, triangular solves), partial last chunk
+    and the explicit write included."""
+    q, k, v, g, beta, S0 = inputs(B=2, L=37, H=2, dk=8, dv=12, seed=23, gate='vector')
+    gen = torch.Generator().manual_seed(24)
+    w = 0.3 * torch.randn(2, 37, 2, 8, generator=gen, dtype=torch.float64) if with_w else None
+    do = torch.randn(2, 37, 2, 12, generator=gen, dtype=torch.float64)
+    dST = torch.randn(2, 2, 8, 12, generator=gen, dtype=torch.float64)
+    ref = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=0.5, w=w)
+    leaves = [None if x is None else x.clone().requires_grad_(True) for x in (q, k, v, g, beta, S0, w)]
+    o, S = gdr.chunk_vector(*leaves[:6], scale=0.5, chunk_size=16, w=leaves[6])
+    live = [i for i, x in enumerate(leaves) if x is not None and not (i == 4 and with_w)]
+    got = torch.autograd.grad([o, S], [leaves[i] for i in live], [do, dST])
+    for i, b in zip(live, got):
+        assert torch.allclose(ref[i], b, rtol=1e-9, atol=1e-10), i

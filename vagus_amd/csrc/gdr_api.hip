@@ -420,6 +420,93 @@ int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k
                       scale, chunk_size, nullptr, stream, nullptr, workspace);
 }
 
+namespace {
+struct ScanBwdWs {
+    int64_t hs_off, u_off, part_off, total;
+    int tw, n_tiles;
+};
+ScanBwdWs scan_bwd_layout(int64_t n_tokens, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs) {
+    ScanBwdWs w{};
+    w.tw = dv % 32 == 0 ? 32 : 16;
+    w.n_tiles = (int)(dv / w.tw);
+    auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
+    const int64_t slots = vgdr::scan_bwd_ckpt_slots(n_tokens, n_seqs);
+    w.hs_off = 0;
+    w.u_off = up(slots * H * dk * dv * 4);
+    w.part_off = w.u_off + up(n_tokens * H * dv * 4);
+    w.total = w.part_off + up(4 * (int64_t)w.n_tiles * n_tokens * H * dk * 4);
+    return w;
+}
+}  // namespace
+
+int64_t vgdr_scan_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs) {
+    if (B < 0 || T < 0 || H <= 0 || n_seqs < 0 || dk <= 0 || dv <= 0) return 0;
+    return scan_bwd_layout(B * T, H, dk, dv, n_seqs).total;
+}
+
+int vgdr_scan_bwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                  const void *w, const float *g, const float *beta, const float *initial_state, const void *grad_o,
+                  const float *grad_final_state, void *grad_q, void *grad_k, void *grad_v, void *grad_w,
+                  float *grad_g, float *grad_beta, float *grad_initial_state, const int32_t *cu_seqlens,
+                  void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk,
+                  int64_t dv, int64_t n_seqs, float scale, hipStream_t stream) {
+    const char *fn = "vgdr_scan_bwd";
+    g_err[0] = 0;
+    if (w && !use_delta) return fail(VGDR_ERR_INVALID, "%s: an explicit write vector needs the delta rule", fn);
+    const int mode = !use_delta ? 2 : (w ? 1 : 0);
+    int rc = check_common(fn, dtype, gate_kind, mode == 0, q, k, v, g, beta, grad_o, cu_seqlens, B, T, H, dk, dv,
+                          n_seqs);
+    if (rc) return rc;
+    if (dv <= 0 || dv % 16)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: dv=%lld (must be a positive multiple of 16)", fn, (long long)dv);
+    const bool any = B * T > 0;
+    if (any && (!grad_q || !grad_k || !grad_v))
+        return fail(VGDR_ERR_INVALID, "%s: grad_q, grad_k and grad_v are required", fn);
+    if (any && mode == 1 && !grad_w) return fail(VGDR_ERR_INVALID, "%s: w needs grad_w", fn);
+    if (any && mode == 0 && !grad_beta) return fail(VGDR_ERR_INVALID, "%s: the delta rule needs grad_beta", fn);
+    if (any && gate_kind != VGDR_GATE_NONE && !grad_g) return fail(VGDR_ERR_INVALID, "%s: a gate needs grad_g", fn);
+    if (grad_v == v || grad_q == q || grad_k == k || (w && grad_w == w))
+        return fail(VGDR_ERR_INVALID, "%s: the gradients must not alias the inputs", fn);
+    if (!aligned16(grad_o) || !aligned16(grad_v) || (w && !aligned16(w)))
+        return fail(VGDR_ERR_INVALID, "%s: grad_o, grad_v and w must be 16-byte aligned", fn);
+    if (!aligned16(initial_state) || !aligned16(grad_final_state) || !aligned16(grad_initial_state))
+        return fail(VGDR_ERR_INVALID, "%s: the state tensors must be 16-byte aligned", fn);
+    const ScanBwdWs ws = scan_bwd_layout(B * T, H, dk, dv, n_seqs);
+    if (!workspace || workspace_bytes < ws.total || !aligned16(workspace))
+        return fail(VGDR_ERR_INVALID, "%s: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)", fn,
+                    (long long)ws.total, (long long)workspace_bytes, workspace);
+    if (n_seqs * H * ws.n_tiles > 0x7fffffffLL || (B * T * H + 3) / 4 > 0x7fffffffLL)
+        return fail(VGDR_ERR_INVALID, "%s: grid too large", fn);
+    if (n_seqs == 0) return VGDR_OK;
+    char *wsb = static_cast<char *>(workspace);
+    vgdr::ScanBwdParams p{};
+    p.geo.cu = cu_seqlens;
+    p.geo.T = T;
+    p.geo.n_tokens = B * T;
+    p.geo.n_seqs = (int)n_seqs;
+    p.q = q; p.k = k; p.v = v; p.w = mode == 1 ? w : nullptr;
+    p.g = gate_kind == VGDR_GATE_NONE ? nullptr : g;
+    p.beta = mode == 0 ? beta : nullptr;
+    p.dout = grad_o;
+    p.h0 = initial_state;
+    p.dht = grad_final_state;
+    p.dq = grad_q; p.dk = grad_k; p.dv = grad_v; p.dw = mode == 1 ? grad_w : nullptr;
+    p.dg = gate_kind == VGDR_GATE_NONE ? nullptr : grad_g;
+    p.dbeta = mode == 0 ? grad_beta : nullptr;
+    p.dh0 = grad_initial_state;
+    p.hs = reinterpret_cast<float *>(wsb + ws.hs_off);
+    p.u = reinterpret_cast<float *>(wsb + ws.u_off);
+    p.part = reinterpret_cast<float *>(wsb + ws.part_off);
+    p.H = (int)H;
+    p.DV = (int)dv;
+    p.TW = ws.tw;
+    p.n_tiles = ws.n_tiles;
+    p.gate = gate_kind;
+    p.mode = mode;
+    p.scale = scale;
+    return hip_status(vgdr::scan_bwd(dtype, (int)dk, p, stream), fn);
+}
+
 #undef VGDR_CHUNK_ARGS
 #undef VGDR_CHUNK_ARGS_FUSED
 #undef VGDR_CHUNK_PASS_NOFUSION

@@ -113,6 +113,29 @@ struct ChunkBwdParams {
     float scale;
 };
 
+// Backward of the token recurrence (any gate; write vector beta k, an explicit
+// w, or none without the delta rule).  Gradients come back in the element type
+// (dq, dk, dv, dw) or fp32 (dg, dbeta, dh0).
+struct ScanBwdParams {
+    SeqGeom geo;                  // cu / T / n_tokens / n_seqs (chunk fields unused)
+    const void *q, *k, *v, *w;    // [n_tokens, H, dk|dv]; w NULL unless mode 1
+    const float *g;               // [n_tokens, H] (gate 1) or [n_tokens, H, dk] (gate 2) or NULL
+    const float *beta;            // [n_tokens, H] (mode 0)
+    const void *dout;             // [n_tokens, H, dv]
+    const float *h0, *dht;        // [n_seqs, H, dk, dv] or NULL
+    void *dq, *dk, *dv, *dw;      // dw: mode 1 only
+    float *dg, *dbeta, *dh0;      // dg: gate != 0; dbeta: mode 0; dh0 may be NULL
+    float *hs;                    // [ckpt slots, H, n_tiles, dk * TW] state checkpoints
+    float *u;                     // [n_tokens, H, dv] u_t of every token (delta rule)
+    float *part;                  // [4, n_tiles, n_tokens, H, dk] per-tile sums over columns
+    int H, DV;
+    int TW;                       // columns per workgroup (4 per wave): 32 or 16
+    int n_tiles;                  // DV / TW
+    int gate;                     // 0 none, 1 scalar, 2 per key channel
+    int mode;                     // 0: x = beta k; 1: x = w; 2: no delta rule (x = k, u = v)
+    float scale;
+};
+
 struct RecParams {
     const void *q, *k, *v;
     const float *g;
@@ -148,6 +171,12 @@ int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H,
 // and the entry states in the workspace; the prep and the entry walk are skipped.
 hipError_t chunk_bwd(int dtype, int dk, int chunk, const ChunkParams &fwd, ChunkBwdParams p, int32_t *table,
                      bool saved, hipStream_t stream);
+
+// the token-recurrence backward: one forward-then-backward walk per (sequence,
+// head, column tile), then the per-(token, head) finish; slots: checkpoint
+// slots the workspace must hold
+hipError_t scan_bwd(int dtype, int dk, const ScanBwdParams &p, hipStream_t stream);
+int64_t scan_bwd_ckpt_slots(int64_t n_tokens, int64_t n_seqs);
 
 hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecParams &p,
                          hipStream_t stream);

@@ -1,0 +1,369 @@
+// Backward of the token recurrence for every scan form the chunked backward
+// does not take: the per-channel (KDA) gate, the explicit write vector w (the
+// asymmetric delta rule) and the plain, no-delta recurrence.  The scalar gate
+// and no gate run here too.
+//
+// Per head, with a_t = exp(g_t) (scalar or per key row) and the write vector
+// x_t = beta_t k_t, or w_t, or (no delta rule) k_t (linear_attention.py:161-195):
+//     S~_t = Diag(a_t) S_{t-1}
+//     u_t  = v_t - S~_t^T k_t            (u_t = v_t without the delta rule)
+//     S_t  = S~_t + x_t u_t^T
+//     o_t  = scale S_t^T q_t
+// and, walking back with dS the gradient of S_t (dht at the end):
+//     dS   += scale q_t do_t^T
+//     dq_t  = scale S_t do_t
+//     dx_t  = dS u_t                      (no delta: this is dk_t)
+//     du_t  = dS^T x_t   = dv_t
+//     dS~   = dS - k_t du_t^T             (no delta: dS~ = dS)
+//     dk_t  = -S~_t du_t                  (+ beta_t dx_t for x = beta k; dbeta_t = k_t . dx_t)
+//     dg_t  = rowsum(dS~ o S~_t)          (summed over rows for a scalar gate)
+//     dS    = Diag(a_t) dS~               (dh0 at the start)
+//
+// The state's columns evolve independently, so one workgroup owns one
+// (sequence, head, tile of TW = 4 * waves columns) and each of its waves four
+// of those columns over all DK rows (lane l: rows l*RPL .. l*RPL + RPL - 1),
+// with no barrier in either walk: the only reductions, over the key rows
+// (S~^T k and dS^T x), stay inside the wave (DPP row rotations and row
+// broadcasts, then one readlane).
+//
+// scan_bwd_kernel first walks forward, storing S at the entry of every block
+// of CT tokens and u_t for every token; then it walks back block by block,
+// recomputes the block's states from its checkpoint and u (two FMAs per
+// element, no reduction), and takes the backward steps.  The sums over the
+// columns (dq, dk, dx, dg) add into a per-workgroup LDS buffer and leave as one
+// fp32 partial per (tile, token, head, row); scan_bwd_finish_kernel adds the
+// tiles and applies the write vector's chain rule.
+#include "gdr_common.hpp"
+#include "gdr_chunk_layout.hpp"
+#include "gdr_kernels.hpp"
+
+namespace vgdr {
+
+namespace {
+
+constexpr int SB_CT = 8;   // tokens per checkpoint block
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_src(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK,
+                                                                 0xf, false));
+}
+
+// the sum of x over the wave's 64 lanes, returned to every lane: rotations
+// within each 16-lane row leave the row's sum in all its lanes, the two row
+// broadcasts carry rows 0..2 into row 3, and lane 63's value is read out
+__device__ __forceinline__ float wave_sum(float x) {
+    x += dpp_src<0x128>(x);          // row_ror:8
+    x += dpp_src<0x124>(x);          // row_ror:4
+    x += dpp_src<0x122>(x);          // row_ror:2
+    x += dpp_src<0x121>(x);          // row_ror:1
+    x += dpp_src<0x142, 0xa>(x);     // row_bcast:15 into rows 1 and 3
+    x += dpp_src<0x143, 0xc>(x);     // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+template <typename E, int N>
+__device__ __forceinline__ void load_f(const E *__restrict__ p, float (&x)[N]) {
+    unroll<N>([&](auto i) __attribute__((always_inline)) { x[i] = Elem<E>::to_f(p[i]); });
+}
+
+// one token's per-row inputs for a lane: the decay a and the write vector x
+template <int RPL, typename E>
+__device__ __forceinline__ void row_inputs(const ScanBwdParams &p, int64_t th, int row0, float (&a)[RPL],
+                                           float (&x)[RPL], float (&kk)[RPL]) {
+    const int DK = RPL * 64;
+    load_f(reinterpret_cast<const E *>(p.k) + th * DK + row0, kk);
+    if (p.gate == 2) {
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) { a[r] = __expf(p.g[th * DK + row0 + r]); });
+    } else {
+        const float as = p.gate == 1 ? __expf(p.g[th]) : 1.f;
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) { a[r] = as; });
+    }
+    if (p.mode == 1) {
+        load_f(reinterpret_cast<const E *>(p.w) + th * DK + row0, x);
+    } else if (p.mode == 0) {
+        const float b = p.beta[th];
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) { x[r] = kk[r] * b; });
+    } else {
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) { x[r] = kk[r]; });
+    }
+}
+
+template <int DK, typename E>
+__global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
+    constexpr int RPL = DK / 64;
+    constexpr int CT = SB_CT;
+    using EL = Elem<E>;
+    __shared__ float acc[CT][4][DK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nthr = blockDim.x;
+    const int tile = blockIdx.x % p.n_tiles;
+    const int pair = blockIdx.x / p.n_tiles;
+    const int s = pair / p.H, h = pair % p.H;
+    const int H = p.H, DV = p.DV;
+    int64_t bos, eos;
+    seq_bounds(p.geo, s, bos, eos);
+    const int64_t L = eos - bos;
+    const int col0 = tile * p.TW + wv * 4;
+    const int row0 = lane * RPL;
+    const bool delta = p.mode != 2;
+
+    for (int i = tid; i < CT * 4 * DK; i += nthr) (&acc[0][0][0])[i] = 0.f;
+
+    // state tiles [n_seqs, H, DK, DV]: rows row0 + r, columns col0 .. col0 + 3
+    const int64_t soff = ((int64_t)s * H + h) * DK * DV + (int64_t)row0 * DV + col0;
+    float S[RPL][4];
+    unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+        const f32x4 x = p.h0 ? ld4(p.h0 + soff + (int64_t)r * DV) : f32x4{0.f, 0.f, 0.f, 0.f};
+        unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] = x[(int)j]; });
+    });
+
+    // checkpoints: per (slot, head, tile) one run of DK * TW floats, each lane's
+    // RPL * 4 values contiguous; a sequence's blocks take slots bos / CT + s + b
+    const int64_t slot0 = bos / CT + s;
+    auto ckpt = [&](int64_t b) {
+        return p.hs + (((slot0 + b) * H + h) * p.n_tiles + tile) * (int64_t)(DK * p.TW) +
+               (int64_t)(wv * 64 + lane) * (RPL * 4);
+    };
+    const E *__restrict__ vp = reinterpret_cast<const E *>(p.v);
+
+    // ---- forward walk: checkpoints and u ----
+    for (int64_t t = 0; t < L; ++t) {
+        const int64_t tok = bos + t;
+        const int64_t th = tok * H + h;
+        if (t % CT == 0) {
+            float *c = ckpt(t / CT);
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                st4(c + r * 4, f32x4{S[r][0], S[r][1], S[r][2], S[r][3]});
+            });
+        }
+        float a[RPL], x[RPL], kk[RPL], vv[4];
+        row_inputs<RPL, E>(p, th, row0, a, x, kk);
+        load_f(vp + th * DV + col0, vv);
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+            unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] *= a[r]; });
+        });
+        float u[4];
+        if (delta) {
+            unroll<4>([&](auto j) __attribute__((always_inline)) {
+                float pj = 0.f;
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) { pj += S[r][j] * kk[r]; });
+                u[j] = vv[j] - wave_sum(pj);
+            });
+            if (lane == 0) st4(p.u + th * DV + col0, f32x4{u[0], u[1], u[2], u[3]});
+        } else {
+            unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = vv[j]; });
+        }
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+            unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] += x[r] * u[j]; });
+        });
+    }
+    // the backward walk reads what this walk stored (same workgroup)
+    __threadfence();
+    __syncthreads();
+
+    // ---- backward walk ----
+    float dS[RPL][4];
+    unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+        const f32x4 x = p.dht ? ld4(p.dht + soff + (int64_t)r * DV) : f32x4{0.f, 0.f, 0.f, 0.f};
+        unroll<4>([&](auto j) __attribute__((always_inline)) { dS[r][j] = x[(int)j]; });
+    });
+    const E *__restrict__ qp = reinterpret_cast<const E *>(p.q);
+    const E *__restrict__ dop = reinterpret_cast<const E *>(p.dout);
+    E *__restrict__ dvp = reinterpret_cast<E *>(p.dv);
+    const int64_t nblk = (L + CT - 1) / CT;
+    const int64_t plane = (int64_t)p.geo.n_tokens * H * DK;      // one (quantity, tile) partial
+    for (int64_t b = nblk - 1; b >= 0; --b) {
+        const int64_t t0 = b * CT;
+        const int n = (int)(L - t0 < CT ? L - t0 : CT);
+        float S0[RPL][4];
+        {
+            const float *c = ckpt(b);
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                const f32x4 x = ld4(c + r * 4);
+                unroll<4>([&](auto j) __attribute__((always_inline)) { S0[r][j] = x[(int)j]; });
+            });
+        }
+        // the block's states S_t, recomputed from the checkpoint and u
+        float st[CT][RPL][4];
+        unroll<CT>([&](auto i) __attribute__((always_inline)) {
+            if (i < n) {
+                const int64_t tok = bos + t0 + i;
+                const int64_t th = tok * H + h;
+                float a[RPL], x[RPL], kk[RPL], u[4];
+                row_inputs<RPL, E>(p, th, row0, a, x, kk);
+                if (delta) {
+                    const f32x4 uv = ld4(p.u + th * DV + col0);
+                    unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = uv[(int)j]; });
+                } else {
+                    load_f(vp + th * DV + col0, u);
+                }
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                    unroll<4>([&](auto j) __attribute__((always_inline)) {
+                        const float prev = i == 0 ? S0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
+                        st[i][r][j] = prev * a[r] + x[r] * u[j];
+                    });
+                });
+            }
+        });
+        unroll<CT>([&](auto ii) __attribute__((always_inline)) {
+            constexpr int i = CT - 1 - decltype(ii)::value;
+            if (i < n) {
+                const int64_t tok = bos + t0 + i;
+                const int64_t th = tok * H + h;
+                float a[RPL], x[RPL], kk[RPL], u[4], qq[RPL], dout[4];
+                row_inputs<RPL, E>(p, th, row0, a, x, kk);
+                if (delta) {
+                    const f32x4 uv = ld4(p.u + th * DV + col0);
+                    unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = uv[(int)j]; });
+                } else {
+                    load_f(vp + th * DV + col0, u);
+                }
+                load_f(qp + th * DK + row0, qq);
+                load_f(dop + th * DV + col0, dout);
+                float pdq[RPL], pdk[RPL], pdx[RPL], pdg[RPL];
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                    const float sq = p.scale * qq[r];
+                    float aq = 0.f, ax = 0.f;
+                    unroll<4>([&](auto j) __attribute__((always_inline)) {
+                        dS[r][j] += sq * dout[j];
+                        aq += st[i][r][j] * dout[j];
+                        ax += dS[r][j] * u[j];
+                    });
+                    pdq[r] = p.scale * aq;
+                    pdx[r] = ax;
+                });
+                float du[4];
+                unroll<4>([&](auto j) __attribute__((always_inline)) {
+                    float y = 0.f;
+                    unroll<RPL>([&](auto r) __attribute__((always_inline)) { y += dS[r][j] * x[r]; });
+                    du[j] = wave_sum(y);
+                });
+                if (lane == 0) {
+                    unroll<4>([&](auto j) __attribute__((always_inline)) {
+                        dvp[th * DV + col0 + j] = EL::from_f(du[j]);
+                    });
+                }
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                    float ak = 0.f, ag = 0.f;
+                    unroll<4>([&](auto j) __attribute__((always_inline)) {
+                        const float prev = i == 0 ? S0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
+                        const float sb = prev * a[r];
+                        if (delta) {
+                            dS[r][j] -= kk[r] * du[j];
+                            ak -= sb * du[j];
+                        }
+                        ag += dS[r][j] * sb;
+                        dS[r][j] *= a[r];
+                    });
+                    pdk[r] = ak;
+                    pdg[r] = ag;
+                });
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                    atomicAdd(&acc[i][0][row0 + r], pdq[r]);
+                    atomicAdd(&acc[i][1][row0 + r], pdk[r]);
+                    atomicAdd(&acc[i][2][row0 + r], pdx[r]);
+                    if (p.gate) atomicAdd(&acc[i][3][row0 + r], pdg[r]);
+                });
+            }
+        });
+        __syncthreads();
+        for (int idx = tid; idx < n * 4 * DK; idx += nthr) {
+            const int i = idx / (4 * DK), qn = (idx / DK) & 3, row = idx % DK;
+            float *a = &acc[i][qn][row];
+            p.part[(int64_t)(qn * p.n_tiles + tile) * plane + ((bos + t0 + i) * H + h) * DK + row] = *a;
+            *a = 0.f;
+        }
+        __syncthreads();
+    }
+    if (p.dh0) {
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+            st4(p.dh0 + soff + (int64_t)r * DV, f32x4{dS[r][0], dS[r][1], dS[r][2], dS[r][3]});
+        });
+    }
+}
+
+// one wave per (token, head): the tiles' partials summed, then
+//   dq = P_q;  w given: dk = P_k, dw = P_x;  x = beta k: dk = P_k + beta P_x,
+//   dbeta = k . P_x;  no delta: dk = P_x;  dg = P_g (per row) or its row sum
+template <int DK, typename E>
+__global__ void __launch_bounds__(256) scan_bwd_finish_kernel(ScanBwdParams p) {
+    constexpr int RPL = DK / 64;
+    using EL = Elem<E>;
+    const int lane = threadIdx.x & 63;
+    const int64_t rowi = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);     // token * H + head
+    const int64_t nrows = p.geo.n_tokens * p.H;
+    if (rowi >= nrows) return;
+    const int64_t plane = nrows * DK;
+    const int64_t off = rowi * DK + lane * RPL;
+    float P[4][RPL];
+    unroll<4>([&](auto qn) __attribute__((always_inline)) {
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) { P[qn][r] = 0.f; });
+        for (int t = 0; t < p.n_tiles; ++t) {
+            const float *src = p.part + (int64_t)(qn * p.n_tiles + t) * plane + off;
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) { P[qn][r] += src[r]; });
+        }
+    });
+    E *dq = reinterpret_cast<E *>(p.dq) + off;
+    E *dk = reinterpret_cast<E *>(p.dk) + off;
+    float kk[RPL];
+    load_f(reinterpret_cast<const E *>(p.k) + off, kk);
+    const float b = p.mode == 0 ? p.beta[rowi] : 0.f;
+    float db = 0.f, gs = 0.f;
+    unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+        dq[r] = EL::from_f(P[0][r]);
+        if (p.mode == 1) {
+            dk[r] = EL::from_f(P[1][r]);
+            reinterpret_cast<E *>(p.dw)[off + r] = EL::from_f(P[2][r]);
+        } else if (p.mode == 0) {
+            dk[r] = EL::from_f(P[1][r] + b * P[2][r]);
+            db += kk[r] * P[2][r];
+        } else {
+            dk[r] = EL::from_f(P[2][r]);
+        }
+        if (p.gate == 2) p.dg[off + r] = P[3][r];
+        gs += P[3][r];
+    });
+    if (p.mode == 0) {
+        db = wave_sum(db);
+        if (lane == 0) p.dbeta[rowi] = db;
+    }
+    if (p.gate == 1) {
+        gs = wave_sum(gs);
+        if (lane == 0) p.dg[rowi] = gs;
+    }
+}
+
+template <int DK, typename E>
+hipError_t launch(const ScanBwdParams &p, hipStream_t stream) {
+    const int64_t pairs = (int64_t)p.geo.n_seqs * p.H;
+    if (pairs > 0) {
+        scan_bwd_kernel<DK, E><<<dim3((unsigned)(pairs * p.n_tiles)), dim3(64 * (p.TW / 4)), 0, stream>>>(p);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const int64_t nrows = p.geo.n_tokens * p.H;
+    if (nrows > 0) {
+        scan_bwd_finish_kernel<DK, E><<<dim3((unsigned)((nrows + 3) / 4)), dim3(256), 0, stream>>>(p);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+}  // namespace
+
+int64_t scan_bwd_ckpt_slots(int64_t n_tokens, int64_t n_seqs) { return n_tokens / SB_CT + n_seqs + 1; }
+
+hipError_t scan_bwd(int dtype, int dk, const ScanBwdParams &p, hipStream_t stream) {
+    if (dk == 128) {
+        if (dtype == 0) return launch<128, float>(p, stream);
+        if (dtype == 1) return launch<128, __bf16>(p, stream);
+        return launch<128, _Float16>(p, stream);
+    }
+    if (dtype == 0) return launch<64, float>(p, stream);
+    if (dtype == 1) return launch<64, __bf16>(p, stream);
+    return launch<64, _Float16>(p, stream);
+}
+
+}  // namespace vgdr

@@ -20,10 +20,13 @@ use_gate_in_kernel with A_log / dt_bias / lower_bound move the producers'
 elementwise work into the kernels (struct vgdr_fusion): q, k arrive
 un-normalised, beta as logits, g as the gate pre-activation (in q's dtype or
 fp32).  They need 16-bit q, k, v for the chunked scan, as fla does.  Every call runs the HIP kernels of libvagus_gdr.so on the
-current stream; there is no CPU path.  The chunked delta rule with a scalar
-gate or none (chunk_gated_delta_rule, hip_scan with such a g) is
-differentiable: its backward runs vgdr_chunk_bwd.  Other calls with inputs
-that require grad raise NotImplementedError.
+current stream; there is no CPU path.  The chunked scans are differentiable:
+the delta rule with a scalar gate or none (chunk_gated_delta_rule, hip_scan
+with such a g) through vgdr_chunk_bwd, every other form (chunk_kda's
+per-channel gate, chunk_simple_gla's plain recurrence, chunk_scan_vec's
+explicit write vector w) through vgdr_scan_bwd.  The token-by-token calls
+(fused_recurrent_*, hip_recurrent, the decode step) raise NotImplementedError
+for inputs that require grad.
 """
 from __future__ import annotations
 
@@ -92,8 +95,20 @@ def _wants_grad(*ts):
 
 def _check_grad(*ts):
     if _wants_grad(*ts):
-        raise NotImplementedError('vagus_amd has a backward for the chunked delta rule with a scalar gate or none '
-                                  '(chunk_gated_delta_rule); this call has no backward')
+        raise NotImplementedError('vagus_amd differentiates the chunked scans (chunk_gated_delta_rule, chunk_kda, '
+                                  'chunk_simple_gla, hip_scan, chunk_scan_vec); this call has no backward')
+
+
+def _gate_activation_rows(f, fz):
+    """The per-channel gate from its pre-activation f (B, T, H, dk) in fp32
+    (linear_attention.py:722-734): -exp(A_log) softplus(f + dt_bias), or
+    lower_bound sigmoid(exp(A_log) (f + dt_bias)); differentiable in torch."""
+    H, dk = f.shape[2], f.shape[3]
+    x = f.float() + fz.dt_bias.float().reshape(H, dk)
+    a = fz.A_log.float().reshape(H, 1).exp()
+    if fz.lower_bound is not None:
+        return fz.lower_bound * torch.sigmoid(a * x)
+    return -a * F.softplus(x)
 
 
 def _l2norm_rows(x):
@@ -280,6 +295,86 @@ def _chunk_fwd_saving(q, k, v, g, beta, initial_state, *, scale, cu_seqlens, chu
     return c.unpad_o(o), c.unpad_state(S), ws
 
 
+def scan_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, delta=True, w=None, cu_seqlens=None):
+    """Backward of every scan form without autograd (vgdr_scan_bwd): the
+    gradients of (o, final_state) under do (and dht, None = zero) for g None,
+    (B, T, H) or (B, T, H, dk), the delta rule with beta_t k_t or an explicit
+    write w (B, T, H, dk), or (delta=False) the plain recurrence.  Returns
+    (dq, dk, dv, dg, dbeta, dh0), with dw appended when w is given; dg is None
+    without a gate, dbeta None unless the delta rule writes beta_t k_t, dh0
+    None without an initial state.  The gradients the reference's training
+    takes through chunk_scan_vec / chunk_scan / recurrent_scan
+    (linear_attention.py:161-425)."""
+    gate = _gate_of(g)
+    writes_beta = delta and w is None
+    c = _Call(q, k, v, g, beta if writes_beta else None, initial_state, cu_seqlens, gate=gate,
+              delta=writes_beta, dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+    scale = c.dk ** -0.5 if scale is None else float(scale)
+    assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
+    assert dht is None or dht.shape == (c.N, c.H, c.dk, c.dv), \
+        f'dht must be {(c.N, c.H, c.dk, c.dv)}, got {tuple(dht.shape)}'
+    if w is not None:
+        assert delta, 'an explicit write vector needs the delta rule'
+        assert w.shape == q.shape, f'w must be {tuple(q.shape)} (B, T, H, dk); got {tuple(w.shape)}'
+    _check_device(do, dht, w)
+    wk = None if w is None else _aligned(_pad_to(w.to(c.dtype), {1: c.dkp}))
+    dop = _aligned(_pad_to(do.to(c.dtype), {1: c.dvp}))
+    dSp = None if dht is None else _aligned(_pad_to(dht.float(), {1: c.dvp, 2: c.dkp}))
+    new = lambda *shape, dt=torch.float32: torch.empty(*shape, dtype=dt, device=c.device)
+    dq, dk = new(c.B, c.T, c.H, c.dkp, dt=c.dtype), new(c.B, c.T, c.H, c.dkp, dt=c.dtype)
+    dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
+    dw = new(c.B, c.T, c.H, c.dkp, dt=c.dtype) if w is not None else None
+    dg = None if gate == 'none' else (new(c.B, c.T, c.H, c.dkp) if gate == 'vector' else new(c.B, c.T, c.H))
+    db = new(c.B, c.T, c.H) if writes_beta else None
+    dS0 = new(c.N, c.H, c.dkp, c.dvp) if initial_state is not None else None
+    L = _lib.load()
+    nbytes = L.vgdr_scan_bwd_workspace_size(c.B, c.T, c.H, c.dkp, c.dvp, c.N)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+    with torch.cuda.device(c.device):
+        _lib.check(L.vgdr_scan_bwd(_DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v),
+                                   _ptr(wk), _ptr(c.g), _ptr(c.beta), _ptr(c.h0), _ptr(dop), _ptr(dSp), _ptr(dq),
+                                   _ptr(dk), _ptr(dv), _ptr(dw), _ptr(dg), _ptr(db), _ptr(dS0), _ptr(c.cu),
+                                   _ptr(ws), nbytes, c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, _stream(c.device)))
+    if c.dkp != c.dk:
+        dq, dk = dq[..., :c.dk], dk[..., :c.dk]
+        dw = None if dw is None else dw[..., :c.dk]
+        dg = dg[..., :c.dk] if gate == 'vector' else dg
+    if c.dvp != c.dv:
+        dv = dv[..., :c.dv]
+    if dS0 is not None:
+        dS0 = c.unpad_state(dS0).to(initial_state.dtype)
+    res = (dq, dk, dv, None if dg is None else dg.to(g.dtype), None if db is None else db.to(beta.dtype), dS0)
+    return res + ((dw,) if w is not None else ())
+
+
+class _ScanRule(torch.autograd.Function):
+    """Every chunked form the scalar-gate chunk backward does not take,
+    differentiable: the per-channel gate, the plain recurrence (delta=False)
+    and the explicit write w.  Forward: the chunked kernels (chunk_scan, or
+    chunk_scan_vec with w); backward: vgdr_scan_bwd, which rebuilds the states
+    it needs from q, k, v, g, beta (w) and the entry state."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, S0, w, scale, cu, chunk_size, delta):
+        if w is None:
+            o, S = chunk_scan(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale, initial_state=S0,
+                              output_final_state=True, cu_seqlens=cu, chunk_size=chunk_size)
+        else:
+            o, S = chunk_scan_vec(q, k, v, g, None, S0, scale=scale, delta=True, chunk_size=chunk_size, w=w,
+                                  cu_seqlens=cu)
+        ctx.save_for_backward(q, k, v, g, beta, S0, w, cu)
+        ctx.scale, ctx.delta = scale, delta
+        return o, S
+
+    @staticmethod
+    def backward(ctx, do, dS):
+        q, k, v, g, beta, S0, w, cu = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
+        r = scan_bwd(q, k, v, g, beta, S0, do, dS, scale=ctx.scale, delta=ctx.delta, w=w, cu_seqlens=cu)
+        return r[:6] + (r[6] if w is not None else None, None, None, None, None)
+
+
 class _ChunkDeltaRule(torch.autograd.Function):
     """The chunked delta rule with a scalar gate or none, differentiable.
     16-bit inputs: forward vgdr_chunk_fwd_saving, which keeps the chunk blocks
@@ -325,21 +420,24 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
     either way), so that a caller can time the two phases separately.
     fusion: the producer fusions (_Fusion).
 
-    With grads enabled and an input that requires grad, the delta rule with a
-    scalar gate or none runs through _ChunkDeltaRule (the fused L2 norm and
-    beta sigmoid then run in torch, differentiably, before it); other
-    combinations raise NotImplementedError."""
+    With grads enabled and an input that requires grad, the fused producers
+    (L2 norm, beta sigmoid, gate activation) run in torch, differentiably, and
+    the scan through _ChunkDeltaRule (delta rule, scalar gate or none) or
+    _ScanRule (every other form)."""
     if _wants_grad(q, k, v, g, beta, initial_state):
-        if gate == 'vector' or not delta or fusion.gate:
-            raise NotImplementedError('vagus_amd has a backward for the chunked delta rule with a scalar gate '
-                                      f'or none; this call has gate={gate!r}, delta={delta}')
         if fusion.l2norm:
             q, k = _l2norm_rows(q), _l2norm_rows(k)
         if fusion.beta:
             beta = torch.sigmoid(beta.float())
+        if fusion.gate:
+            g = _gate_activation_rows(g, fusion)
         scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
-        o, S = _ChunkDeltaRule.apply(q, k, v, g if gate == 'scalar' else None, beta, initial_state, scale,
-                                     cu_seqlens, chunk_size)
+        gk = None if gate == 'none' else g
+        if gate == 'vector' or not delta:
+            o, S = _ScanRule.apply(q, k, v, gk, beta if delta else None, initial_state, None, scale, cu_seqlens,
+                                   chunk_size, delta)
+        else:
+            o, S = _ChunkDeltaRule.apply(q, k, v, gk, beta, initial_state, scale, cu_seqlens, chunk_size)
         return o, (S if output_final_state else None)
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=gate, delta=delta,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
@@ -776,8 +874,13 @@ def chunk_scan_vec(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_siz
     taken as the same decay on every channel.  w (B, T, H, dk): write vectors
     in place of beta_t k_t (the asymmetric delta rule, :340-353, :389-396;
     beta unused), run chunkwise with 16-bit q, k, v and token by token (the
-    same rule, vgdr_recurrent_fwd_w) in fp32.  Without w it is chunk_kda."""
+    same rule, vgdr_recurrent_fwd_w) in fp32.  Without w it is chunk_kda.
+    Differentiable (vgdr_scan_bwd) when an input requires grad."""
     B, T, H, dk = q.shape
+    if w is not None and _wants_grad(q, k, v, g, beta, S0, w):
+        assert delta, 'an explicit write vector needs the delta rule'
+        scale = dk ** -0.5 if scale is None else float(scale)
+        return _ScanRule.apply(q, k, v, g, None, S0, w, scale, cu_seqlens, chunk_size, True)
     if g is None:
         g = torch.zeros(B, T, H, dk, dtype=torch.float32, device=q.device)
     elif g.dim() == 3:
