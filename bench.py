@@ -282,6 +282,31 @@ def bench_backward(torch, ops, workloads, steps, warmup):
             'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2)}
 
 
+def bench_scan_backward(torch, ops, workloads, steps, warmup):
+    """The token-walk backward (vgdr_scan_bwd through ops.scan_bwd) at the KDA
+    prefill shape: gradients of o and the final state with respect to q, k, v,
+    the per-channel g, beta and the entry state."""
+    g = torch.Generator(device='cpu').manual_seed(13)
+    x = workloads.workload('kda_prefill', device='cuda')
+    do = torch.randn(*x.v.shape, generator=g).bfloat16().cuda()
+    B, T, H = x.q.shape[:3]
+    dST = torch.randn(B, H, x.q.shape[-1], x.v.shape[-1], generator=g).cuda()
+
+    def step(i):
+        ops.scan_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST, scale=DK ** -0.5)
+
+    us = _event_us(torch, step, steps, warmup)
+    th = B * T * H
+    del x, do
+    tflops = th * 2 * FLOP_PER_TOKEN_HEAD / (us * 1e-6) / 1e12
+    return {'workload': 'kda_prefill backward: dq, dk, dv, dg (per channel), dbeta, dh0 from do and dht, '
+                        'B4 T8192 H8 dk=dv=128 bf16',
+            'kernels': 'scan_bwd_kernel + scan_bwd_finish_kernel',
+            'us': round(us, 1), 'tok_s': round(B * T / (us * 1e-6), 1),
+            'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
+            'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5)}
+
+
 def cpu_baseline(torch, workloads):
     """The oracle's torch fp32 chunk form over the full headline workload."""
     from oracle import gdr
@@ -361,6 +386,8 @@ def main():
 
     if args.backward_only:
         print(json.dumps(bench_backward(torch, ops, workloads, args.steps, args.warmup)), flush=True)
+        print(json.dumps(bench_scan_backward(torch, ops, workloads, max(3, args.steps // 3), max(2, args.warmup // 3))),
+              flush=True)
         return
     if args.layer_only:
         print(json.dumps(bench_layer_kernels(torch, ops, workloads, args.steps, args.warmup)), flush=True)
@@ -385,6 +412,8 @@ def main():
         extra['layer_kernels'] = bench_layer_kernels(torch, ops, workloads, args.steps, args.warmup)
         log('[bench] backward gdn_340m')
         extra['backward'] = bench_backward(torch, ops, workloads, max(5, args.steps // 4), max(3, args.warmup // 10))
+        log('[bench] backward kda_prefill (token walk)')
+        extra['kda_backward'] = bench_scan_backward(torch, ops, workloads, 3, 1)
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
             r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))

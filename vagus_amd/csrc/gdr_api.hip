@@ -427,7 +427,7 @@ struct ScanBwdWs {
 };
 ScanBwdWs scan_bwd_layout(int64_t n_tokens, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs) {
     ScanBwdWs w{};
-    w.tw = dv % 32 == 0 ? 32 : 16;
+    w.tw = 16;
     w.n_tiles = (int)(dv / w.tw);
     auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
     const int64_t slots = vgdr::scan_bwd_ckpt_slots(n_tokens, n_seqs);

@@ -129,7 +129,7 @@ struct ScanBwdParams {
     float *u;                     // [n_tokens, H, dv] u_t of every token (delta rule)
     float *part;                  // [4, n_tiles, n_tokens, H, dk] per-tile sums over columns
     int H, DV;
-    int TW;                       // columns per workgroup (4 per wave): 32 or 16
+    int TW;                       // columns per workgroup (4 per wave)
     int n_tiles;                  // DV / TW
     int gate;                     // 0 none, 1 scalar, 2 per key channel
     int mode;                     // 0: x = beta k; 1: x = w; 2: no delta rule (x = k, u = v)

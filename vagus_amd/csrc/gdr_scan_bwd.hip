@@ -67,26 +67,81 @@ __device__ __forceinline__ void load_f(const E *__restrict__ p, float (&x)[N]) {
     unroll<N>([&](auto i) __attribute__((always_inline)) { x[i] = Elem<E>::to_f(p[i]); });
 }
 
-// one token's per-row inputs for a lane: the decay a and the write vector x
+// a lane's RPL consecutive row values as one load: RPL = 2 packs two 16-bit
+// elements into one register
+template <typename T, int RPL> struct RowVec { typedef T V __attribute__((ext_vector_type(RPL))); };
+template <typename T> struct RowVec<T, 1> { typedef T V; };
+template <typename T, int RPL>
+__device__ __forceinline__ typename RowVec<T, RPL>::V ld_row(const T *p) {
+    return *reinterpret_cast<const typename RowVec<T, RPL>::V *>(p);
+}
+template <typename T, int RPL>
+__device__ __forceinline__ float row_el(typename RowVec<T, RPL>::V x, int r) {
+    if constexpr (RPL == 1) return Elem<T>::to_f(x); else return Elem<T>::to_f(x[r]);
+}
+__device__ __forceinline__ float lane_val(float x, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+
+// One block of CT tokens as a lane holds it before use, fetched a block ahead
+// and left raw until then (a conversion would wait for the load).  Row data
+// per lane; the wave-uniform per-token values spread over lanes and read back
+// with readlane: lane 4i + j holds u (or v) of token i, column j, lane
+// 32 + 4i + j its do; lane i its scalar gate and beta.
 template <int RPL, typename E>
-__device__ __forceinline__ void row_inputs(const ScanBwdParams &p, int64_t th, int row0, float (&a)[RPL],
-                                           float (&x)[RPL], float (&kk)[RPL]) {
-    const int DK = RPL * 64;
-    load_f(reinterpret_cast<const E *>(p.k) + th * DK + row0, kk);
-    if (p.gate == 2) {
-        unroll<RPL>([&](auto r) __attribute__((always_inline)) { a[r] = __expf(p.g[th * DK + row0 + r]); });
-    } else {
-        const float as = p.gate == 1 ? __expf(p.g[th]) : 1.f;
-        unroll<RPL>([&](auto r) __attribute__((always_inline)) { a[r] = as; });
+struct Blk {
+    typename RowVec<E, RPL>::V q[SB_CT], k[SB_CT], w[SB_CT];
+    typename RowVec<float, RPL>::V g[SB_CT];
+    float s0[RPL][4];      // the block's entry state (backward)
+    float uf;              // u (delta rule, backward)
+    E vr, dr;              // v, do
+    float gs, bs;          // scalar gate, beta
+};
+
+template <int RPL, typename E>
+__device__ __forceinline__ void load_blk(const ScanBwdParams &p, Blk<RPL, E> &b, int64_t bos, int64_t L, int64_t t0,
+                                         int h, int row0, int lane, int col0, bool bwd, const float *ck) {
+    constexpr int DK = RPL * 64;
+    const int H = p.H, DV = p.DV;
+    auto th = [&](int64_t i) {
+        const int64_t t = t0 + i;
+        return (bos + (t < L ? t : L - 1)) * H + h;
+    };
+    const E *qp = reinterpret_cast<const E *>(p.q), *kp = reinterpret_cast<const E *>(p.k);
+    unroll<SB_CT>([&](auto i) __attribute__((always_inline)) {
+        const int64_t o = th(i) * DK + row0;
+        b.k[i] = ld_row<E, RPL>(kp + o);
+        if (bwd) b.q[i] = ld_row<E, RPL>(qp + o);
+        if (p.mode == 1) b.w[i] = ld_row<E, RPL>(reinterpret_cast<const E *>(p.w) + o);
+        if (p.gate == 2) b.g[i] = ld_row<float, RPL>(p.g + o);
+    });
+    const int li = lane & 31;
+    const int64_t tu = th(li >> 2) * DV + col0 + (li & 3);
+    if (bwd && p.mode != 2) b.uf = p.u[tu];
+    else b.vr = reinterpret_cast<const E *>(p.v)[tu];
+    if (bwd) b.dr = reinterpret_cast<const E *>(p.dout)[tu];
+    const int64_t ts = th(lane & (SB_CT - 1));
+    if (p.gate == 1) b.gs = p.g[ts];
+    if (p.mode == 0) b.bs = p.beta[ts];
+    if (ck) {
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+            const f32x4 x = ld4(ck + r * 4);
+            unroll<4>([&](auto j) __attribute__((always_inline)) { b.s0[r][j] = x[(int)j]; });
+        });
     }
-    if (p.mode == 1) {
-        load_f(reinterpret_cast<const E *>(p.w) + th * DK + row0, x);
-    } else if (p.mode == 0) {
-        const float b = p.beta[th];
-        unroll<RPL>([&](auto r) __attribute__((always_inline)) { x[r] = kk[r] * b; });
-    } else {
-        unroll<RPL>([&](auto r) __attribute__((always_inline)) { x[r] = kk[r]; });
-    }
+}
+
+// token i of a block: the decay, the write vector and k of the lane's rows
+template <int RPL, typename E>
+__device__ __forceinline__ void tok_rows(const ScanBwdParams &p, const Blk<RPL, E> &b, int i, float (&a)[RPL],
+                                         float (&x)[RPL], float (&kk)[RPL]) {
+    const float as = p.gate == 1 ? __expf(lane_val(b.gs, i)) : 1.f;
+    const float bt = p.mode == 0 ? lane_val(b.bs, i) : 0.f;
+    unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+        kk[r] = row_el<E, RPL>(b.k[i], r);
+        a[r] = p.gate == 2 ? __expf(row_el<float, RPL>(b.g[i], r)) : as;
+        x[r] = p.mode == 1 ? row_el<E, RPL>(b.w[i], r) : (p.mode == 0 ? kk[r] * bt : kk[r]);
+    });
 }
 
 template <int DK, typename E>
@@ -108,6 +163,7 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
     const int col0 = tile * p.TW + wv * 4;
     const int row0 = lane * RPL;
     const bool delta = p.mode != 2;
+    const int64_t nblk = (L + CT - 1) / CT;
 
     for (int i = tid; i < CT * 4 * DK; i += nthr) (&acc[0][0][0])[i] = 0.f;
 
@@ -126,38 +182,50 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
         return p.hs + (((slot0 + b) * H + h) * p.n_tiles + tile) * (int64_t)(DK * p.TW) +
                (int64_t)(wv * 64 + lane) * (RPL * 4);
     };
-    const E *__restrict__ vp = reinterpret_cast<const E *>(p.v);
 
     // ---- forward walk: checkpoints and u ----
-    for (int64_t t = 0; t < L; ++t) {
-        const int64_t tok = bos + t;
-        const int64_t th = tok * H + h;
-        if (t % CT == 0) {
-            float *c = ckpt(t / CT);
-            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                st4(c + r * 4, f32x4{S[r][0], S[r][1], S[r][2], S[r][3]});
-            });
-        }
-        float a[RPL], x[RPL], kk[RPL], vv[4];
-        row_inputs<RPL, E>(p, th, row0, a, x, kk);
-        load_f(vp + th * DV + col0, vv);
+    auto fwd_block = [&](const Blk<RPL, E> &bk, int64_t b) __attribute__((always_inline)) {
+        const int64_t t0 = b * CT;
+        const int n = (int)(L - t0 < CT ? L - t0 : CT);
+        float *c = ckpt(b);
         unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-            unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] *= a[r]; });
+            st4(c + r * 4, f32x4{S[r][0], S[r][1], S[r][2], S[r][3]});
         });
-        float u[4];
-        if (delta) {
-            unroll<4>([&](auto j) __attribute__((always_inline)) {
-                float pj = 0.f;
-                unroll<RPL>([&](auto r) __attribute__((always_inline)) { pj += S[r][j] * kk[r]; });
-                u[j] = vv[j] - wave_sum(pj);
-            });
-            if (lane == 0) st4(p.u + th * DV + col0, f32x4{u[0], u[1], u[2], u[3]});
-        } else {
-            unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = vv[j]; });
+        const float vl = EL::to_f(bk.vr);
+        unroll<CT>([&](auto i) __attribute__((always_inline)) {
+            if (i < n) {
+                float a[RPL], x[RPL], kk[RPL], u[4];
+                tok_rows<RPL, E>(p, bk, i, a, x, kk);
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                    unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] *= a[r]; });
+                });
+                unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = lane_val(vl, 4 * i + j); });
+                if (delta) {
+                    unroll<4>([&](auto j) __attribute__((always_inline)) {
+                        float pj = 0.f;
+                        unroll<RPL>([&](auto r) __attribute__((always_inline)) { pj += S[r][j] * kk[r]; });
+                        u[j] -= wave_sum(pj);
+                    });
+                    if (lane == 0)
+                        st4(p.u + ((bos + t0 + i) * H + h) * DV + col0, f32x4{u[0], u[1], u[2], u[3]});
+                }
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                    unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] += x[r] * u[j]; });
+                });
+            }
+        });
+    };
+    {
+        Blk<RPL, E> A, B;
+        if (nblk > 0) load_blk<RPL, E>(p, A, bos, L, 0, h, row0, lane, col0, false, nullptr);
+        for (int64_t b = 0; b < nblk; b += 2) {
+            load_blk<RPL, E>(p, B, bos, L, (b + 1) * CT, h, row0, lane, col0, false, nullptr);
+            fwd_block(A, b);
+            if (b + 1 < nblk) {
+                load_blk<RPL, E>(p, A, bos, L, (b + 2) * CT, h, row0, lane, col0, false, nullptr);
+                fwd_block(B, b + 1);
+            }
         }
-        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-            unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] += x[r] * u[j]; });
-        });
     }
     // the backward walk reads what this walk stored (same workgroup)
     __threadfence();
@@ -169,40 +237,23 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
         const f32x4 x = p.dht ? ld4(p.dht + soff + (int64_t)r * DV) : f32x4{0.f, 0.f, 0.f, 0.f};
         unroll<4>([&](auto j) __attribute__((always_inline)) { dS[r][j] = x[(int)j]; });
     });
-    const E *__restrict__ qp = reinterpret_cast<const E *>(p.q);
-    const E *__restrict__ dop = reinterpret_cast<const E *>(p.dout);
     E *__restrict__ dvp = reinterpret_cast<E *>(p.dv);
-    const int64_t nblk = (L + CT - 1) / CT;
     const int64_t plane = (int64_t)p.geo.n_tokens * H * DK;      // one (quantity, tile) partial
-    for (int64_t b = nblk - 1; b >= 0; --b) {
+    auto bwd_block = [&](const Blk<RPL, E> &bk, int64_t b) __attribute__((always_inline)) {
         const int64_t t0 = b * CT;
         const int n = (int)(L - t0 < CT ? L - t0 : CT);
-        float S0[RPL][4];
-        {
-            const float *c = ckpt(b);
-            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                const f32x4 x = ld4(c + r * 4);
-                unroll<4>([&](auto j) __attribute__((always_inline)) { S0[r][j] = x[(int)j]; });
-            });
-        }
+        const float ul = delta ? bk.uf : EL::to_f(bk.vr);
+        const float dl = EL::to_f(bk.dr);
         // the block's states S_t, recomputed from the checkpoint and u
         float st[CT][RPL][4];
         unroll<CT>([&](auto i) __attribute__((always_inline)) {
             if (i < n) {
-                const int64_t tok = bos + t0 + i;
-                const int64_t th = tok * H + h;
-                float a[RPL], x[RPL], kk[RPL], u[4];
-                row_inputs<RPL, E>(p, th, row0, a, x, kk);
-                if (delta) {
-                    const f32x4 uv = ld4(p.u + th * DV + col0);
-                    unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = uv[(int)j]; });
-                } else {
-                    load_f(vp + th * DV + col0, u);
-                }
+                float a[RPL], x[RPL], kk[RPL];
+                tok_rows<RPL, E>(p, bk, i, a, x, kk);
                 unroll<RPL>([&](auto r) __attribute__((always_inline)) {
                     unroll<4>([&](auto j) __attribute__((always_inline)) {
-                        const float prev = i == 0 ? S0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
-                        st[i][r][j] = prev * a[r] + x[r] * u[j];
+                        const float prev = i == 0 ? bk.s0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
+                        st[i][r][j] = prev * a[r] + x[r] * lane_val(ul, 4 * i + j);
                     });
                 });
             }
@@ -210,21 +261,15 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
         unroll<CT>([&](auto ii) __attribute__((always_inline)) {
             constexpr int i = CT - 1 - decltype(ii)::value;
             if (i < n) {
-                const int64_t tok = bos + t0 + i;
-                const int64_t th = tok * H + h;
-                float a[RPL], x[RPL], kk[RPL], u[4], qq[RPL], dout[4];
-                row_inputs<RPL, E>(p, th, row0, a, x, kk);
-                if (delta) {
-                    const f32x4 uv = ld4(p.u + th * DV + col0);
-                    unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = uv[(int)j]; });
-                } else {
-                    load_f(vp + th * DV + col0, u);
-                }
-                load_f(qp + th * DK + row0, qq);
-                load_f(dop + th * DV + col0, dout);
+                float a[RPL], x[RPL], kk[RPL], u[4], dout[4];
+                tok_rows<RPL, E>(p, bk, i, a, x, kk);
+                unroll<4>([&](auto j) __attribute__((always_inline)) {
+                    u[j] = lane_val(ul, 4 * i + j);
+                    dout[j] = lane_val(dl, 32 + 4 * i + j);
+                });
                 float pdq[RPL], pdk[RPL], pdx[RPL], pdg[RPL];
                 unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                    const float sq = p.scale * qq[r];
+                    const float sq = p.scale * row_el<E, RPL>(bk.q[i], r);
                     float aq = 0.f, ax = 0.f;
                     unroll<4>([&](auto j) __attribute__((always_inline)) {
                         dS[r][j] += sq * dout[j];
@@ -241,14 +286,13 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
                     du[j] = wave_sum(y);
                 });
                 if (lane == 0) {
-                    unroll<4>([&](auto j) __attribute__((always_inline)) {
-                        dvp[th * DV + col0 + j] = EL::from_f(du[j]);
-                    });
+                    const int64_t o = ((bos + t0 + i) * H + h) * DV + col0;
+                    unroll<4>([&](auto j) __attribute__((always_inline)) { dvp[o + j] = EL::from_f(du[j]); });
                 }
                 unroll<RPL>([&](auto r) __attribute__((always_inline)) {
                     float ak = 0.f, ag = 0.f;
                     unroll<4>([&](auto j) __attribute__((always_inline)) {
-                        const float prev = i == 0 ? S0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
+                        const float prev = i == 0 ? bk.s0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
                         const float sb = prev * a[r];
                         if (delta) {
                             dS[r][j] -= kk[r] * du[j];
@@ -276,6 +320,20 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
             *a = 0.f;
         }
         __syncthreads();
+    };
+    {
+        Blk<RPL, E> A, B;
+        if (nblk > 0) load_blk<RPL, E>(p, A, bos, L, (nblk - 1) * CT, h, row0, lane, col0, true, ckpt(nblk - 1));
+        for (int64_t b = nblk - 1; b >= 0; b -= 2) {
+            const int64_t bp = b > 0 ? b - 1 : 0;
+            load_blk<RPL, E>(p, B, bos, L, bp * CT, h, row0, lane, col0, true, ckpt(bp));
+            bwd_block(A, b);
+            if (b >= 1) {
+                const int64_t bq = b > 1 ? b - 2 : 0;
+                load_blk<RPL, E>(p, A, bos, L, bq * CT, h, row0, lane, col0, true, ckpt(bq));
+                bwd_block(B, b - 1);
+            }
+        }
     }
     if (p.dh0) {
         unroll<RPL>([&](auto r) __attribute__((always_inline)) {
