@@ -422,7 +422,7 @@ int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k
 
 namespace {
 struct ScanBwdWs {
-    int64_t hs_off, u_off, part_off, total;
+    int64_t hs_off, dhs_off, u_off, part_off, total;
     int tw, n_tiles;
 };
 ScanBwdWs scan_bwd_layout(int64_t n_tokens, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs) {
@@ -432,7 +432,8 @@ ScanBwdWs scan_bwd_layout(int64_t n_tokens, int64_t H, int64_t dk, int64_t dv, i
     auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
     const int64_t slots = vgdr::scan_bwd_ckpt_slots(n_tokens, n_seqs);
     w.hs_off = 0;
-    w.u_off = up(slots * H * dk * dv * 4);
+    w.dhs_off = up(slots * H * dk * dv * 4);
+    w.u_off = w.dhs_off + up(slots * H * dk * dv * 4);
     w.part_off = w.u_off + up(n_tokens * H * dv * 4);
     w.total = w.part_off + up(4 * (int64_t)w.n_tiles * n_tokens * H * dk * 4);
     return w;
@@ -475,7 +476,8 @@ int vgdr_scan_bwd(int dtype, int gate_kind, int use_delta, const void *q, const 
     if (!workspace || workspace_bytes < ws.total || !aligned16(workspace))
         return fail(VGDR_ERR_INVALID, "%s: workspace needs %lld bytes, 16-byte aligned (got %lld at %p)", fn,
                     (long long)ws.total, (long long)workspace_bytes, workspace);
-    if (n_seqs * H * ws.n_tiles > 0x7fffffffLL || (B * T * H + 3) / 4 > 0x7fffffffLL)
+    if (2 * n_seqs * H * ws.n_tiles > 0x7fffffffLL || (B * T * H + 3) / 4 > 0x7fffffffLL ||
+        vgdr::scan_bwd_ckpt_slots(B * T, n_seqs) * H * ws.n_tiles > 0x7fffffffLL)
         return fail(VGDR_ERR_INVALID, "%s: grid too large", fn);
     if (n_seqs == 0) return VGDR_OK;
     char *wsb = static_cast<char *>(workspace);
@@ -495,6 +497,7 @@ int vgdr_scan_bwd(int dtype, int gate_kind, int use_delta, const void *q, const 
     p.dbeta = mode == 0 ? grad_beta : nullptr;
     p.dh0 = grad_initial_state;
     p.hs = reinterpret_cast<float *>(wsb + ws.hs_off);
+    p.dhs = reinterpret_cast<float *>(wsb + ws.dhs_off);
     p.u = reinterpret_cast<float *>(wsb + ws.u_off);
     p.part = reinterpret_cast<float *>(wsb + ws.part_off);
     p.H = (int)H;

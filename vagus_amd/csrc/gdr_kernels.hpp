@@ -125,7 +125,8 @@ struct ScanBwdParams {
     const float *h0, *dht;        // [n_seqs, H, dk, dv] or NULL
     void *dq, *dk, *dv, *dw;      // dw: mode 1 only
     float *dg, *dbeta, *dh0;      // dg: gate != 0; dbeta: mode 0; dh0 may be NULL
-    float *hs;                    // [ckpt slots, H, n_tiles, dk * TW] state checkpoints
+    float *hs;                    // [ckpt slots, H, n_tiles, dk * TW] state at each block's entry
+    float *dhs;                   // same layout: gradient of the state at each block's exit
     float *u;                     // [n_tokens, H, dv] u_t of every token (delta rule)
     float *part;                  // [4, n_tiles, n_tokens, H, dk] per-tile sums over columns
     int H, DV;
@@ -172,9 +173,9 @@ int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H,
 hipError_t chunk_bwd(int dtype, int dk, int chunk, const ChunkParams &fwd, ChunkBwdParams p, int32_t *table,
                      bool saved, hipStream_t stream);
 
-// the token-recurrence backward: one forward-then-backward walk per (sequence,
-// head, column tile), then the per-(token, head) finish; slots: checkpoint
-// slots the workspace must hold
+// the token-recurrence backward: the forward and backward walks per (sequence,
+// head, column tile), the per-block gradients, then the per-(token, head)
+// finish; slots: checkpoint slots the workspace must hold
 hipError_t scan_bwd(int dtype, int dk, const ScanBwdParams &p, hipStream_t stream);
 int64_t scan_bwd_ckpt_slots(int64_t n_tokens, int64_t n_seqs);
 

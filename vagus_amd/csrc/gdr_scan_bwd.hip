@@ -26,22 +26,26 @@
 // (S~^T k and dS^T x), stay inside the wave (DPP row rotations and row
 // broadcasts, then one readlane).
 //
-// scan_bwd_kernel first walks forward, storing S at the entry of every block
-// of CT tokens and u_t for every token; then it walks back block by block,
-// recomputes the block's states from its checkpoint and u (two FMAs per
-// element, no reduction), and takes the backward steps.  The sums over the
-// columns (dq, dk, dx, dg) add into a per-workgroup LDS buffer and leave as one
-// fp32 partial per (tile, token, head, row); scan_bwd_finish_kernel adds the
-// tiles and applies the write vector's chain rule.
+// scan_walks_kernel runs the two sequential walks side by side: forward,
+// storing S at the entry of every block of CT tokens and u_t of every token;
+// and back, storing dS at every block's exit and writing dv (the dS recurrence
+// needs no state).  scan_grad_kernel then takes every block at once: it
+// recomputes the block's states from the entry checkpoint and u (two FMAs per
+// element, no reduction), walks the block back from its exit gradient, and
+// adds the sums over the columns (dq, dk, dx, dg) into LDS, leaving one fp32
+// partial per (tile, token, head, row); scan_bwd_finish_kernel adds the tiles
+// and applies the write vector's chain rule.
 #include "gdr_common.hpp"
 #include "gdr_chunk_layout.hpp"
 #include "gdr_kernels.hpp"
 
 namespace vgdr {
 
-namespace {
-
 constexpr int SB_CT = 8;   // tokens per checkpoint block
+
+int64_t scan_bwd_ckpt_slots(int64_t n_tokens, int64_t n_seqs) { return n_tokens / SB_CT + n_seqs + 1; }
+
+namespace {
 
 template <int CTRL, int ROW_MASK = 0xf>
 __device__ __forceinline__ float dpp_src(float x) {
@@ -60,6 +64,19 @@ __device__ __forceinline__ float wave_sum(float x) {
     x += dpp_src<0x142, 0xa>(x);     // row_bcast:15 into rows 1 and 3
     x += dpp_src<0x143, 0xc>(x);     // row_bcast:31 into rows 2 and 3
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
+// four wave sums at once, stage by stage, so that the four DPP chains overlap
+__device__ __forceinline__ void wave_sum4(float (&x)[4]) {
+    unroll<4>([&](auto j) __attribute__((always_inline)) { x[j] += dpp_src<0x128>(x[j]); });
+    unroll<4>([&](auto j) __attribute__((always_inline)) { x[j] += dpp_src<0x124>(x[j]); });
+    unroll<4>([&](auto j) __attribute__((always_inline)) { x[j] += dpp_src<0x122>(x[j]); });
+    unroll<4>([&](auto j) __attribute__((always_inline)) { x[j] += dpp_src<0x121>(x[j]); });
+    unroll<4>([&](auto j) __attribute__((always_inline)) { x[j] += dpp_src<0x142, 0xa>(x[j]); });
+    unroll<4>([&](auto j) __attribute__((always_inline)) { x[j] += dpp_src<0x143, 0xc>(x[j]); });
+    unroll<4>([&](auto j) __attribute__((always_inline)) {
+        x[j] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[j]), 63));
+    });
 }
 
 template <typename E, int N>
@@ -144,17 +161,29 @@ __device__ __forceinline__ void tok_rows(const ScanBwdParams &p, const Blk<RPL, 
     });
 }
 
+template <int DK>
+__device__ __forceinline__ float *ckpt_at(float *base, const ScanBwdParams &p, int64_t slot, int h, int tile,
+                                          int wv, int lane) {
+    return base + ((slot * p.H + h) * p.n_tiles + tile) * (int64_t)(DK * p.TW) + (int64_t)(wv * 64 + lane) * (DK / 16);
+}
+
+// The two walks, one launch: workgroups [0, pairs * n_tiles) walk forward
+// from h0, storing S at the entry of every block of CT tokens and u of every
+// token; the others walk back from dht, storing dS (the gradient of the state
+// at a block's exit) before each block, writing dv = dS^T x per token and dh0
+// at the start.  The backward recurrence of dS reads only q, k, the
+// write vector, the gate and do, so the two walks run side by side.
 template <int DK, typename E>
-__global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
+__global__ void __launch_bounds__(256) scan_walks_kernel(ScanBwdParams p) {
     constexpr int RPL = DK / 64;
     constexpr int CT = SB_CT;
     using EL = Elem<E>;
-    __shared__ float acc[CT][4][DK];
-
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int nthr = blockDim.x;
-    const int tile = blockIdx.x % p.n_tiles;
-    const int pair = blockIdx.x / p.n_tiles;
+    const int64_t per_walk = (int64_t)p.geo.n_seqs * p.H * p.n_tiles;
+    const bool back = blockIdx.x >= per_walk;
+    const int64_t wg = back ? blockIdx.x - per_walk : blockIdx.x;
+    const int tile = wg % p.n_tiles;
+    const int pair = wg / p.n_tiles;
     const int s = pair / p.H, h = pair % p.H;
     const int H = p.H, DV = p.DV;
     int64_t bos, eos;
@@ -164,58 +193,50 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
     const int row0 = lane * RPL;
     const bool delta = p.mode != 2;
     const int64_t nblk = (L + CT - 1) / CT;
-
-    for (int i = tid; i < CT * 4 * DK; i += nthr) (&acc[0][0][0])[i] = 0.f;
-
+    const int64_t slot0 = bos / CT + s;
     // state tiles [n_seqs, H, DK, DV]: rows row0 + r, columns col0 .. col0 + 3
     const int64_t soff = ((int64_t)s * H + h) * DK * DV + (int64_t)row0 * DV + col0;
     float S[RPL][4];
+    const float *init = back ? p.dht : p.h0;
     unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-        const f32x4 x = p.h0 ? ld4(p.h0 + soff + (int64_t)r * DV) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 x = init ? ld4(init + soff + (int64_t)r * DV) : f32x4{0.f, 0.f, 0.f, 0.f};
         unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] = x[(int)j]; });
     });
 
-    // checkpoints: per (slot, head, tile) one run of DK * TW floats, each lane's
-    // RPL * 4 values contiguous; a sequence's blocks take slots bos / CT + s + b
-    const int64_t slot0 = bos / CT + s;
-    auto ckpt = [&](int64_t b) {
-        return p.hs + (((slot0 + b) * H + h) * p.n_tiles + tile) * (int64_t)(DK * p.TW) +
-               (int64_t)(wv * 64 + lane) * (RPL * 4);
-    };
-
-    // ---- forward walk: checkpoints and u ----
-    auto fwd_block = [&](const Blk<RPL, E> &bk, int64_t b) __attribute__((always_inline)) {
-        const int64_t t0 = b * CT;
-        const int n = (int)(L - t0 < CT ? L - t0 : CT);
-        float *c = ckpt(b);
-        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-            st4(c + r * 4, f32x4{S[r][0], S[r][1], S[r][2], S[r][3]});
-        });
-        const float vl = EL::to_f(bk.vr);
-        unroll<CT>([&](auto i) __attribute__((always_inline)) {
-            if (i < n) {
-                float a[RPL], x[RPL], kk[RPL], u[4];
-                tok_rows<RPL, E>(p, bk, i, a, x, kk);
-                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                    unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] *= a[r]; });
-                });
-                unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = lane_val(vl, 4 * i + j); });
-                if (delta) {
-                    unroll<4>([&](auto j) __attribute__((always_inline)) {
-                        float pj = 0.f;
-                        unroll<RPL>([&](auto r) __attribute__((always_inline)) { pj += S[r][j] * kk[r]; });
-                        u[j] -= wave_sum(pj);
+    if (!back) {
+        auto fwd_block = [&](const Blk<RPL, E> &bk, int64_t b) __attribute__((always_inline)) {
+            const int64_t t0 = b * CT;
+            const int n = (int)(L - t0 < CT ? L - t0 : CT);
+            float *c = ckpt_at<DK>(p.hs, p, slot0 + b, h, tile, wv, lane);
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                st4(c + r * 4, f32x4{S[r][0], S[r][1], S[r][2], S[r][3]});
+            });
+            const float vl = EL::to_f(bk.vr);
+            unroll<CT>([&](auto i) __attribute__((always_inline)) {
+                if (i < n) {
+                    float a[RPL], x[RPL], kk[RPL], u[4];
+                    tok_rows<RPL, E>(p, bk, i, a, x, kk);
+                    unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                        unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] *= a[r]; });
                     });
-                    if (lane == 0)
-                        st4(p.u + ((bos + t0 + i) * H + h) * DV + col0, f32x4{u[0], u[1], u[2], u[3]});
+                    unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] = lane_val(vl, 4 * i + j); });
+                    if (delta) {
+                        float pj[4];
+                        unroll<4>([&](auto j) __attribute__((always_inline)) {
+                            pj[j] = 0.f;
+                            unroll<RPL>([&](auto r) __attribute__((always_inline)) { pj[j] += S[r][j] * kk[r]; });
+                        });
+                        wave_sum4(pj);
+                        unroll<4>([&](auto j) __attribute__((always_inline)) { u[j] -= pj[j]; });
+                        if (lane == 0)
+                            st4(p.u + ((bos + t0 + i) * H + h) * DV + col0, f32x4{u[0], u[1], u[2], u[3]});
+                    }
+                    unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                        unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] += x[r] * u[j]; });
+                    });
                 }
-                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                    unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] += x[r] * u[j]; });
-                });
-            }
-        });
-    };
-    {
+            });
+        };
         Blk<RPL, E> A, B;
         if (nblk > 0) load_blk<RPL, E>(p, A, bos, L, 0, h, row0, lane, col0, false, nullptr);
         for (int64_t b = 0; b < nblk; b += 2) {
@@ -226,119 +247,188 @@ __global__ void __launch_bounds__(512) scan_bwd_kernel(ScanBwdParams p) {
                 fwd_block(B, b + 1);
             }
         }
+        return;
     }
-    // the backward walk reads what this walk stored (same workgroup)
-    __threadfence();
-    __syncthreads();
 
-    // ---- backward walk ----
-    float dS[RPL][4];
-    unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-        const f32x4 x = p.dht ? ld4(p.dht + soff + (int64_t)r * DV) : f32x4{0.f, 0.f, 0.f, 0.f};
-        unroll<4>([&](auto j) __attribute__((always_inline)) { dS[r][j] = x[(int)j]; });
-    });
+    // the backward walk: S holds dS
     E *__restrict__ dvp = reinterpret_cast<E *>(p.dv);
-    const int64_t plane = (int64_t)p.geo.n_tokens * H * DK;      // one (quantity, tile) partial
-    auto bwd_block = [&](const Blk<RPL, E> &bk, int64_t b) __attribute__((always_inline)) {
+    auto back_block = [&](const Blk<RPL, E> &bk, int64_t b) __attribute__((always_inline)) {
         const int64_t t0 = b * CT;
         const int n = (int)(L - t0 < CT ? L - t0 : CT);
-        const float ul = delta ? bk.uf : EL::to_f(bk.vr);
-        const float dl = EL::to_f(bk.dr);
-        // the block's states S_t, recomputed from the checkpoint and u
-        float st[CT][RPL][4];
-        unroll<CT>([&](auto i) __attribute__((always_inline)) {
-            if (i < n) {
-                float a[RPL], x[RPL], kk[RPL];
-                tok_rows<RPL, E>(p, bk, i, a, x, kk);
-                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                    unroll<4>([&](auto j) __attribute__((always_inline)) {
-                        const float prev = i == 0 ? bk.s0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
-                        st[i][r][j] = prev * a[r] + x[r] * lane_val(ul, 4 * i + j);
-                    });
-                });
-            }
+        float *c = ckpt_at<DK>(p.dhs, p, slot0 + b, h, tile, wv, lane);
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+            st4(c + r * 4, f32x4{S[r][0], S[r][1], S[r][2], S[r][3]});
         });
+        const float dl = EL::to_f(bk.dr);
         unroll<CT>([&](auto ii) __attribute__((always_inline)) {
             constexpr int i = CT - 1 - decltype(ii)::value;
             if (i < n) {
-                float a[RPL], x[RPL], kk[RPL], u[4], dout[4];
+                float a[RPL], x[RPL], kk[RPL], dout[4], du[4];
                 tok_rows<RPL, E>(p, bk, i, a, x, kk);
-                unroll<4>([&](auto j) __attribute__((always_inline)) {
-                    u[j] = lane_val(ul, 4 * i + j);
-                    dout[j] = lane_val(dl, 32 + 4 * i + j);
-                });
-                float pdq[RPL], pdk[RPL], pdx[RPL], pdg[RPL];
+                unroll<4>([&](auto j) __attribute__((always_inline)) { dout[j] = lane_val(dl, 32 + 4 * i + j); });
                 unroll<RPL>([&](auto r) __attribute__((always_inline)) {
                     const float sq = p.scale * row_el<E, RPL>(bk.q[i], r);
-                    float aq = 0.f, ax = 0.f;
-                    unroll<4>([&](auto j) __attribute__((always_inline)) {
-                        dS[r][j] += sq * dout[j];
-                        aq += st[i][r][j] * dout[j];
-                        ax += dS[r][j] * u[j];
-                    });
-                    pdq[r] = p.scale * aq;
-                    pdx[r] = ax;
+                    unroll<4>([&](auto j) __attribute__((always_inline)) { S[r][j] += sq * dout[j]; });
                 });
-                float du[4];
                 unroll<4>([&](auto j) __attribute__((always_inline)) {
-                    float y = 0.f;
-                    unroll<RPL>([&](auto r) __attribute__((always_inline)) { y += dS[r][j] * x[r]; });
-                    du[j] = wave_sum(y);
+                    du[j] = 0.f;
+                    unroll<RPL>([&](auto r) __attribute__((always_inline)) { du[j] += S[r][j] * x[r]; });
                 });
+                wave_sum4(du);
                 if (lane == 0) {
                     const int64_t o = ((bos + t0 + i) * H + h) * DV + col0;
                     unroll<4>([&](auto j) __attribute__((always_inline)) { dvp[o + j] = EL::from_f(du[j]); });
                 }
                 unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                    float ak = 0.f, ag = 0.f;
                     unroll<4>([&](auto j) __attribute__((always_inline)) {
-                        const float prev = i == 0 ? bk.s0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
-                        const float sb = prev * a[r];
-                        if (delta) {
-                            dS[r][j] -= kk[r] * du[j];
-                            ak -= sb * du[j];
-                        }
-                        ag += dS[r][j] * sb;
-                        dS[r][j] *= a[r];
+                        if (delta) S[r][j] -= kk[r] * du[j];
+                        S[r][j] *= a[r];
                     });
-                    pdk[r] = ak;
-                    pdg[r] = ag;
-                });
-                unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                    atomicAdd(&acc[i][0][row0 + r], pdq[r]);
-                    atomicAdd(&acc[i][1][row0 + r], pdk[r]);
-                    atomicAdd(&acc[i][2][row0 + r], pdx[r]);
-                    if (p.gate) atomicAdd(&acc[i][3][row0 + r], pdg[r]);
                 });
             }
         });
-        __syncthreads();
-        for (int idx = tid; idx < n * 4 * DK; idx += nthr) {
-            const int i = idx / (4 * DK), qn = (idx / DK) & 3, row = idx % DK;
-            float *a = &acc[i][qn][row];
-            p.part[(int64_t)(qn * p.n_tiles + tile) * plane + ((bos + t0 + i) * H + h) * DK + row] = *a;
-            *a = 0.f;
-        }
-        __syncthreads();
     };
     {
         Blk<RPL, E> A, B;
-        if (nblk > 0) load_blk<RPL, E>(p, A, bos, L, (nblk - 1) * CT, h, row0, lane, col0, true, ckpt(nblk - 1));
+        if (nblk > 0) load_blk<RPL, E>(p, A, bos, L, (nblk - 1) * CT, h, row0, lane, col0, true, nullptr);
         for (int64_t b = nblk - 1; b >= 0; b -= 2) {
-            const int64_t bp = b > 0 ? b - 1 : 0;
-            load_blk<RPL, E>(p, B, bos, L, bp * CT, h, row0, lane, col0, true, ckpt(bp));
-            bwd_block(A, b);
+            load_blk<RPL, E>(p, B, bos, L, (b > 0 ? b - 1 : 0) * CT, h, row0, lane, col0, true, nullptr);
+            back_block(A, b);
             if (b >= 1) {
-                const int64_t bq = b > 1 ? b - 2 : 0;
-                load_blk<RPL, E>(p, A, bos, L, bq * CT, h, row0, lane, col0, true, ckpt(bq));
-                bwd_block(B, b - 1);
+                load_blk<RPL, E>(p, A, bos, L, (b > 1 ? b - 2 : 0) * CT, h, row0, lane, col0, true, nullptr);
+                back_block(B, b - 1);
             }
         }
     }
     if (p.dh0) {
         unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-            st4(p.dh0 + soff + (int64_t)r * DV, f32x4{dS[r][0], dS[r][1], dS[r][2], dS[r][3]});
+            st4(p.dh0 + soff + (int64_t)r * DV, f32x4{S[r][0], S[r][1], S[r][2], S[r][3]});
         });
+    }
+}
+
+// The gradients of one block of CT tokens, all blocks in parallel: one
+// workgroup per (checkpoint slot, head, tile).  It recomputes the block's
+// states from the entry checkpoint and u, then walks the block back from the
+// stored exit gradient, adding each token's column sums into LDS and writing
+// them out as the tile's partials.
+template <int DK, typename E>
+__global__ void __launch_bounds__(256) scan_grad_kernel(ScanBwdParams p) {
+    constexpr int RPL = DK / 64;
+    constexpr int CT = SB_CT;
+    using EL = Elem<E>;
+    __shared__ float acc[CT][4][DK];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int nthr = blockDim.x;
+    const int tile = blockIdx.x % p.n_tiles;
+    const int64_t rest = blockIdx.x / p.n_tiles;
+    const int h = (int)(rest % p.H);
+    const int64_t slot = rest / p.H;
+    const int H = p.H;
+    // the sequence whose blocks hold this slot: the last s with bos(s) / CT + s <= slot
+    int lo = 0, hi = p.geo.n_seqs - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        int64_t b0, e0;
+        seq_bounds(p.geo, mid, b0, e0);
+        if (b0 / CT + mid <= slot) lo = mid; else hi = mid - 1;
+    }
+    const int s = lo;
+    int64_t bos, eos;
+    seq_bounds(p.geo, s, bos, eos);
+    const int64_t L = eos - bos;
+    const int64_t b = slot - (bos / CT + s);
+    if (b < 0 || b * CT >= L) return;                 // a slot no block uses
+    const int64_t t0 = b * CT;
+    const int n = (int)(L - t0 < CT ? L - t0 : CT);
+    const int col0 = tile * p.TW + wv * 4;
+    const int row0 = lane * RPL;
+    const bool delta = p.mode != 2;
+
+    for (int i = tid; i < CT * 4 * DK; i += nthr) (&acc[0][0][0])[i] = 0.f;
+    Blk<RPL, E> bk;
+    load_blk<RPL, E>(p, bk, bos, L, t0, h, row0, lane, col0, true, ckpt_at<DK>(p.hs, p, slot, h, tile, wv, lane));
+    float dS[RPL][4];
+    {
+        const float *c = ckpt_at<DK>(p.dhs, p, slot, h, tile, wv, lane);
+        unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+            const f32x4 x = ld4(c + r * 4);
+            unroll<4>([&](auto j) __attribute__((always_inline)) { dS[r][j] = x[(int)j]; });
+        });
+    }
+    __syncthreads();
+
+    const float ul = delta ? bk.uf : EL::to_f(bk.vr);
+    const float dl = EL::to_f(bk.dr);
+    float st[CT][RPL][4];
+    unroll<CT>([&](auto i) __attribute__((always_inline)) {
+        if (i < n) {
+            float a[RPL], x[RPL], kk[RPL];
+            tok_rows<RPL, E>(p, bk, i, a, x, kk);
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                unroll<4>([&](auto j) __attribute__((always_inline)) {
+                    const float prev = i == 0 ? bk.s0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
+                    st[i][r][j] = prev * a[r] + x[r] * lane_val(ul, 4 * i + j);
+                });
+            });
+        }
+    });
+    unroll<CT>([&](auto ii) __attribute__((always_inline)) {
+        constexpr int i = CT - 1 - decltype(ii)::value;
+        if (i < n) {
+            float a[RPL], x[RPL], kk[RPL], u[4], dout[4];
+            tok_rows<RPL, E>(p, bk, i, a, x, kk);
+            unroll<4>([&](auto j) __attribute__((always_inline)) {
+                u[j] = lane_val(ul, 4 * i + j);
+                dout[j] = lane_val(dl, 32 + 4 * i + j);
+            });
+            float pdq[RPL], pdk[RPL], pdx[RPL], pdg[RPL];
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                const float sq = p.scale * row_el<E, RPL>(bk.q[i], r);
+                float aq = 0.f, ax = 0.f;
+                unroll<4>([&](auto j) __attribute__((always_inline)) {
+                    dS[r][j] += sq * dout[j];
+                    aq += st[i][r][j] * dout[j];
+                    ax += dS[r][j] * u[j];
+                });
+                pdq[r] = p.scale * aq;
+                pdx[r] = ax;
+            });
+            float du[4];
+            unroll<4>([&](auto j) __attribute__((always_inline)) {
+                du[j] = 0.f;
+                unroll<RPL>([&](auto r) __attribute__((always_inline)) { du[j] += dS[r][j] * x[r]; });
+            });
+            wave_sum4(du);
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                float ak = 0.f, ag = 0.f;
+                unroll<4>([&](auto j) __attribute__((always_inline)) {
+                    const float prev = i == 0 ? bk.s0[r][j] : st[i == 0 ? 0 : i - 1][r][j];
+                    const float sb = prev * a[r];
+                    if (delta) {
+                        dS[r][j] -= kk[r] * du[j];
+                        ak -= sb * du[j];
+                    }
+                    ag += dS[r][j] * sb;
+                    dS[r][j] *= a[r];
+                });
+                pdk[r] = ak;
+                pdg[r] = ag;
+            });
+            unroll<RPL>([&](auto r) __attribute__((always_inline)) {
+                atomicAdd(&acc[i][0][row0 + r], pdq[r]);
+                atomicAdd(&acc[i][1][row0 + r], pdk[r]);
+                atomicAdd(&acc[i][2][row0 + r], pdx[r]);
+                if (p.gate) atomicAdd(&acc[i][3][row0 + r], pdg[r]);
+            });
+        }
+    });
+    __syncthreads();
+    const int64_t plane = (int64_t)p.geo.n_tokens * H * DK;      // one (quantity, tile) partial
+    for (int idx = tid; idx < n * 4 * DK; idx += nthr) {
+        const int i = idx / (4 * DK), qn = (idx / DK) & 3, row = idx % DK;
+        p.part[(int64_t)(qn * p.n_tiles + tile) * plane + ((bos + t0 + i) * H + h) * DK + row] =
+            (&acc[0][0][0])[idx];
     }
 }
 
@@ -397,8 +487,13 @@ template <int DK, typename E>
 hipError_t launch(const ScanBwdParams &p, hipStream_t stream) {
     const int64_t pairs = (int64_t)p.geo.n_seqs * p.H;
     if (pairs > 0) {
-        scan_bwd_kernel<DK, E><<<dim3((unsigned)(pairs * p.n_tiles)), dim3(64 * (p.TW / 4)), 0, stream>>>(p);
+        const dim3 blk(64 * (p.TW / 4));
+        scan_walks_kernel<DK, E><<<dim3((unsigned)(2 * pairs * p.n_tiles)), blk, 0, stream>>>(p);
         hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        const int64_t slots = scan_bwd_ckpt_slots(p.geo.n_tokens, p.geo.n_seqs);
+        scan_grad_kernel<DK, E><<<dim3((unsigned)(slots * p.H * p.n_tiles)), blk, 0, stream>>>(p);
+        e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     const int64_t nrows = p.geo.n_tokens * p.H;
@@ -410,8 +505,6 @@ hipError_t launch(const ScanBwdParams &p, hipStream_t stream) {
 }
 
 }  // namespace
-
-int64_t scan_bwd_ckpt_slots(int64_t n_tokens, int64_t n_seqs) { return n_tokens / SB_CT + n_seqs + 1; }
 
 hipError_t scan_bwd(int dtype, int dk, const ScanBwdParams &p, hipStream_t stream) {
     if (dk == 128) {
