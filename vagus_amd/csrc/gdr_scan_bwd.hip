@@ -310,14 +310,16 @@ __global__ void __launch_bounds__(256) scan_walks_kernel(ScanBwdParams p) {
 // The gradients of one block of CT tokens, all blocks in parallel: one
 // workgroup per (checkpoint slot, head, tile).  It recomputes the block's
 // states from the entry checkpoint and u, then walks the block back from the
-// stored exit gradient, adding each token's column sums into LDS and writing
-// them out as the tile's partials.
+// stored exit gradient, storing each wave's column sums of every token in its
+// own LDS slice (no atomics: four waves adding to one row waited on the LDS),
+// and writes the four slices' sum out as the tile's partials.
 template <int DK, typename E>
 __global__ void __launch_bounds__(256) scan_grad_kernel(ScanBwdParams p) {
     constexpr int RPL = DK / 64;
     constexpr int CT = SB_CT;
     using EL = Elem<E>;
-    __shared__ float acc[CT][4][DK];
+    constexpr int NWG = 4;                            // waves per workgroup (16-column tiles)
+    __shared__ float red[NWG][CT][4][DK];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int nthr = blockDim.x;
     const int tile = blockIdx.x % p.n_tiles;
@@ -345,7 +347,6 @@ __global__ void __launch_bounds__(256) scan_grad_kernel(ScanBwdParams p) {
     const int row0 = lane * RPL;
     const bool delta = p.mode != 2;
 
-    for (int i = tid; i < CT * 4 * DK; i += nthr) (&acc[0][0][0])[i] = 0.f;
     Blk<RPL, E> bk;
     load_blk<RPL, E>(p, bk, bos, L, t0, h, row0, lane, col0, true, ckpt_at<DK>(p.hs, p, slot, h, tile, wv, lane));
     float dS[RPL][4];
@@ -356,7 +357,6 @@ __global__ void __launch_bounds__(256) scan_grad_kernel(ScanBwdParams p) {
             unroll<4>([&](auto j) __attribute__((always_inline)) { dS[r][j] = x[(int)j]; });
         });
     }
-    __syncthreads();
 
     const float ul = delta ? bk.uf : EL::to_f(bk.vr);
     const float dl = EL::to_f(bk.dr);
@@ -416,10 +416,10 @@ __global__ void __launch_bounds__(256) scan_grad_kernel(ScanBwdParams p) {
                 pdg[r] = ag;
             });
             unroll<RPL>([&](auto r) __attribute__((always_inline)) {
-                atomicAdd(&acc[i][0][row0 + r], pdq[r]);
-                atomicAdd(&acc[i][1][row0 + r], pdk[r]);
-                atomicAdd(&acc[i][2][row0 + r], pdx[r]);
-                if (p.gate) atomicAdd(&acc[i][3][row0 + r], pdg[r]);
+                red[wv][i][0][row0 + r] = pdq[r];
+                red[wv][i][1][row0 + r] = pdk[r];
+                red[wv][i][2][row0 + r] = pdx[r];
+                red[wv][i][3][row0 + r] = pdg[r];
             });
         }
     });
@@ -427,8 +427,9 @@ __global__ void __launch_bounds__(256) scan_grad_kernel(ScanBwdParams p) {
     const int64_t plane = (int64_t)p.geo.n_tokens * H * DK;      // one (quantity, tile) partial
     for (int idx = tid; idx < n * 4 * DK; idx += nthr) {
         const int i = idx / (4 * DK), qn = (idx / DK) & 3, row = idx % DK;
-        p.part[(int64_t)(qn * p.n_tiles + tile) * plane + ((bos + t0 + i) * H + h) * DK + row] =
-            (&acc[0][0][0])[idx];
+        float sum = 0.f;
+        unroll<NWG>([&](auto w) __attribute__((always_inline)) { sum += red[w][i][qn][row]; });
+        p.part[(int64_t)(qn * p.n_tiles + tile) * plane + ((bos + t0 + i) * H + h) * DK + row] = sum;
     }
 }
 
@@ -486,6 +487,7 @@ __global__ void __launch_bounds__(256) scan_bwd_finish_kernel(ScanBwdParams p) {
 template <int DK, typename E>
 hipError_t launch(const ScanBwdParams &p, hipStream_t stream) {
     const int64_t pairs = (int64_t)p.geo.n_seqs * p.H;
+    if (p.TW != 16) return hipErrorInvalidValue;               // the grad kernel's LDS holds 4 waves
     if (pairs > 0) {
         const dim3 blk(64 * (p.TW / 4));
         scan_walks_kernel<DK, E><<<dim3((unsigned)(2 * pairs * p.n_tiles)), blk, 0, stream>>>(p);
