@@ -276,8 +276,8 @@ int vgdr_chunk_bwd_saved(int dtype, int gate_kind,
  * grad_beta (delta rule without w) and grad_initial_state (may be NULL) in
  * fp32.  grad_final_state may be NULL (zero).  dk in {64, 128}; dv a positive
  * multiple of 16.  Workspace: vgdr_scan_bwd_workspace_size(...) bytes,
- * 16-byte aligned (state checkpoints every 8 tokens in fp32, u_t per token,
- * per-column-tile partial sums).
+ * 16-byte aligned (state and state-gradient checkpoints every 8 tokens in
+ * fp32, u_t per token, per-column-tile partial sums).
  */
 int64_t vgdr_scan_bwd_workspace_size(int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs);
 int vgdr_scan_bwd(int dtype, int gate_kind, int use_delta,
