@@ -1,7 +1,8 @@
 """Backward of every scan form the scalar-gate chunk backward does not take:
 vgdr_scan_bwd (per-channel KDA gate, explicit write vector w, the plain
 recurrence without the delta rule; the scalar gate and none too) and the
-autograd routes of ops.chunk_kda / chunk_simple_gla / chunk_scan_vec / hip_scan,
+autograd routes of ops.chunk_kda / chunk_simple_gla / chunk_scan_vec / hip_scan
+and of the token-by-token hip_recurrent,
 against the oracle's recurrent_grads (reverse-mode through the fp64
 recurrence, pinned in tests/test_oracle.py by finite differences for every
 form and by the per-channel chunk form's own gradients).
@@ -60,11 +61,11 @@ def test_scan_bwd_argument_checks():
     assert L.vgdr_scan_bwd_workspace_size(-1, 64, 2, 64, 64, 2) == 0
 
 
-def test_recurrent_calls_with_grad_still_raise():
+def test_cpu_tensors_with_grad_fail_loudly():
     q = torch.randn(1, 4, 2, 64, requires_grad=True)
-    with pytest.raises((NotImplementedError, RuntimeError)):
+    with pytest.raises(RuntimeError, match='ROCm GPU'):
         ops.fused_recurrent_gated_delta_rule(q, q, q, torch.zeros(1, 4, 2), torch.ones(1, 4, 2))
-    with pytest.raises(RuntimeError, match='ROCm GPU'):                 # a CPU tensor fails loudly
+    with pytest.raises(RuntimeError, match='ROCm GPU'):
         ops.chunk_kda(q, q, q, torch.zeros(1, 4, 2, 64), torch.ones(1, 4, 2))
 
 
@@ -224,3 +225,23 @@ def test_chunk_scan_vec_and_simple_gla_autograd():
                     (q, k, v, gs, S0), do, dST)
     r = gdr.recurrent_grads(q, k, v, gs, None, S0, do, dST, scale=0.2, delta=False)
     _compare(got[:4] + [None, got[4]], r, 2e-2, 'chunk_simple_gla')
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('mode', ['vector', 'scalar_w', 'none_nodelta'])
+def test_recurrent_autograd(mode):
+    """The token-by-token calls (hip_recurrent, the contract of recurrent_scan)
+    differentiated by autograd through vgdr_scan_bwd."""
+    gate = mode.split('_')[0]
+    delta = not mode.endswith('nodelta')
+    with_w = mode.endswith('_w')
+    B, T, H, dk, dv = 1, 29, 2, 64, 64
+    q, k, v, g, beta, w, S0, do, dST = _inputs(B, T, H, dk, dv, torch.float32, seed=41, gate=gate, with_w=with_w)
+    print(f'\n[case] hip_recurrent autograd mode={mode}', flush=True)
+    b = beta if (delta and not with_w) else None
+
+    def fn(q, k, v, g, b, S0, w):
+        return ops.hip_recurrent(q, k, v, g, b, S0, scale=0.3, delta=delta, w=w)
+    got = _autograd(fn, (q, k, v, g, b, S0, w), do, dST)
+    r = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=0.3, delta=delta, w=w)
+    _compare(got[:6] + [got[6]], r, 1e-5, f'hip_recurrent {mode}')

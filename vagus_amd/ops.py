@@ -24,9 +24,10 @@ current stream; there is no CPU path.  The chunked scans are differentiable:
 the delta rule with a scalar gate or none (chunk_gated_delta_rule, hip_scan
 with such a g) through vgdr_chunk_bwd, every other form (chunk_kda's
 per-channel gate, chunk_simple_gla's plain recurrence, chunk_scan_vec's
-explicit write vector w) through vgdr_scan_bwd.  The token-by-token calls
-(fused_recurrent_*, hip_recurrent, the decode step) raise NotImplementedError
-for inputs that require grad.
+explicit write vector w) through vgdr_scan_bwd, and so are the token-by-token
+calls (fused_recurrent_*, hip_recurrent) without the short conv or the output
+epilogue.  The decode step, the fused epilogue and in-place state updates
+raise NotImplementedError for inputs that require grad.
 """
 from __future__ import annotations
 
@@ -348,15 +349,19 @@ def scan_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, delta
 
 
 class _ScanRule(torch.autograd.Function):
-    """Every chunked form the scalar-gate chunk backward does not take,
-    differentiable: the per-channel gate, the plain recurrence (delta=False)
-    and the explicit write w.  Forward: the chunked kernels (chunk_scan, or
-    chunk_scan_vec with w); backward: vgdr_scan_bwd, which rebuilds the states
-    it needs from q, k, v, g, beta (w) and the entry state."""
+    """Every form the scalar-gate chunk backward does not take, differentiable:
+    the per-channel gate, the plain recurrence (delta=False) and the explicit
+    write w.  Forward: the chunked kernels (chunk_scan, or chunk_scan_vec with
+    w), or with token=True the token-by-token kernel; backward: vgdr_scan_bwd,
+    which rebuilds the states it needs from q, k, v, g, beta (w) and the entry
+    state."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, S0, w, scale, cu, chunk_size, delta):
-        if w is None:
+    def forward(ctx, q, k, v, g, beta, S0, w, scale, cu, chunk_size, delta, token=False):
+        if token:
+            o, S = _recurrent(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale, initial_state=S0,
+                              output_final_state=True, cu_seqlens=cu, w=w)
+        elif w is None:
             o, S = chunk_scan(q, k, v, g, beta, gate=_gate_of(g), delta=delta, scale=scale, initial_state=S0,
                               output_final_state=True, cu_seqlens=cu, chunk_size=chunk_size)
         else:
@@ -372,7 +377,7 @@ class _ScanRule(torch.autograd.Function):
         if do is None:
             do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
         r = scan_bwd(q, k, v, g, beta, S0, do, dS, scale=ctx.scale, delta=ctx.delta, w=w, cu_seqlens=cu)
-        return r[:6] + (r[6] if w is not None else None, None, None, None, None)
+        return r[:6] + (r[6] if w is not None else None, None, None, None, None, None)
 
 
 class _ChunkDeltaRule(torch.autograd.Function):
@@ -614,6 +619,19 @@ class _ShortConv:
 def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state,
                cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION, epilogue=None,
                conv: _ShortConv | None = None, w=None):
+    if (conv is None and epilogue is None and not inplace_final_state
+            and _wants_grad(q, k, v, g, beta, initial_state, w)):
+        # differentiable: the producers in torch, then the kernel with vgdr_scan_bwd as its backward
+        if fusion.l2norm:
+            q, k = _l2norm_rows(q), _l2norm_rows(k)
+        if fusion.beta:
+            beta = torch.sigmoid(beta.float())
+        if fusion.gate:
+            g = _gate_activation_rows(g, fusion)
+        scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
+        o, S = _ScanRule.apply(q, k, v, None if gate == 'none' else g, beta if (delta and w is None) else None,
+                               initial_state, w, scale, cu_seqlens, 64, delta, True)
+        return o, (S if output_final_state else None)
     dv = v.shape[-1]
     if w is not None:
         assert delta, 'an explicit write vector needs the delta rule'
