@@ -14,7 +14,10 @@ lengths that end inside a checkpoint block, a padded head (dk = 100, dv = 48),
 dv = 80 (16-column tiles), a packed batch (empty, one-token and long
 segments), no initial state, and the fused producers (L2 norm, beta sigmoid,
 the gate activation with and without its lower bound, differentiated in torch
-before the kernels).
+before the kernels).  At the full KDA prefill shape (B4 T8192 H8), where the
+oracle is too slow, the gradients' directional derivative against
+Richardson-extrapolated central differences of the chunked forward kernel
+(fp32, relative 1e-3).
 """
 import pytest
 import torch
@@ -245,3 +248,46 @@ def test_recurrent_autograd(mode):
     got = _autograd(fn, (q, k, v, g, b, S0, w), do, dST)
     r = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=0.3, delta=delta, w=w)
     _compare(got[:6] + [got[6]], r, 1e-5, f'hip_recurrent {mode}')
+
+
+@pytest.mark.gpu
+def test_scan_bwd_kda_full_size_directional_derivative():
+    """At the KDA prefill shape (B4 T8192 H8 dk=dv=128, fp32), where the fp64
+    oracle is too slow: the backward's directional derivative
+    sum_x <grad_x, delta_x> of L = <o, do> + <S_T, dST> equals central
+    differences of the chunked forward kernel along delta, for every input
+    (q, k, v, the per-channel g, beta, S0) at once (Richardson-extrapolated,
+    relative 1e-3)."""
+    B, T, H, dk, dv = 4, 8192, 8, 128, 128
+    print('\n[case] scan_bwd KDA full-size directional derivative', flush=True)
+    g0 = torch.Generator(device='cpu').manual_seed(71)
+    r = lambda *s: torch.randn(*s, generator=g0).cuda()
+    q = F.normalize(r(B, T, H, dk), dim=-1)
+    k = F.normalize(r(B, T, H, dk), dim=-1)
+    v = r(B, T, H, dv)
+    g = F.logsigmoid(r(B, T, H, dk) + 4.0)
+    beta = torch.sigmoid(r(B, T, H))
+    S0 = 0.1 * r(B, H, dk, dv)
+    do, dST = r(B, T, H, dv), r(B, H, dk, dv)
+    xs = [q, k, v, g, beta, S0]
+    ds = [0.01 * r(*x.shape) for x in xs]
+    ds[3] = -0.01 * torch.rand(*g.shape, generator=g0).cuda()
+    ds[4] = 0.01 * r(*beta.shape) * beta * (1 - beta)
+    scale = dk ** -0.5
+
+    def loss(ys):
+        o, S = ops.chunk_kda(*ys[:5], scale=scale, initial_state=ys[5], output_final_state=True)
+        return (o.double() * do.double()).sum().item() + (S.double() * dST.double()).sum().item()
+
+    grads = ops.scan_bwd(q, k, v, g, beta, S0, do, dST, scale=scale)
+    ana = sum((gx.double() * d.double()).sum().item() for gx, d in zip(grads, ds))
+
+    def cd(eps):
+        return (loss([x + eps * d for x, d in zip(xs, ds)]) - loss([x - eps * d for x, d in zip(xs, ds)])) / (2 * eps)
+
+    c1, c2 = cd(0.5), cd(0.25)
+    fd = (4 * c2 - c1) / 3
+    err = abs(ana - fd) / max(abs(fd), 1e-30)
+    print(f'[parity] KDA full-size directional derivative: backward {ana:.6e} extrapolated {fd:.6e} rel {err:.2e}',
+          flush=True)
+    assert err <= 1e-3
