@@ -22,8 +22,12 @@
  *   - Sequences: with cu_seqlens == NULL the batch is dense, B sequences of
  *     T tokens (sequence b owns tokens [b*T, (b+1)*T)).  Otherwise
  *     cu_seqlens is a device int32 array of n_seqs + 1 offsets into a packed
- *     stream of n_tokens = T tokens (B must be 1); each segment is clamped to
- *     [0, T], so a malformed table cannot address memory outside the tensors.
+ *     stream of n_tokens = T tokens (B must be 1).  The caller guarantees
+ *     cu[0] = 0, cu[n] <= cu[n+1] and cu[n_seqs] = T (the Python layer checks
+ *     it on the host); the kernels do not read the table back.  Each segment
+ *     is clamped to [0, T], so a malformed table cannot address memory
+ *     outside the tensors, but overlapping segments race on o and tokens no
+ *     segment covers are left unwritten.
  *   - States: initial_state / final_state are fp32 [n_seqs, H, dk, dv]
  *     (n_seqs = B for a dense batch), either may be NULL (zeros / not
  *     written).  They may alias (in-place update).

@@ -90,6 +90,27 @@ def _check_device(*ts):
                                f'{t.device} (there is no CPU implementation)')
 
 
+def _check_cu(cu_seqlens, n_tokens: int):
+    """The packed-batch contract, checked on the host: integer offsets,
+    cu[0] == 0, non-decreasing, cu[-1] == n_tokens, inside int32.  The
+    kernels only clamp each segment into [0, n_tokens] (memory safety);
+    overlapping or uncovered rows would otherwise race on o or be left
+    unwritten.  Reads the offsets back (one small device-to-host copy), except
+    inside HIP graph capture, where no copy may run and the caller vouches
+    for the table."""
+    assert cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 1, 'cu_seqlens is 1-D with N + 1 entries'
+    assert not cu_seqlens.is_floating_point() and cu_seqlens.dtype != torch.bool, \
+        'cu_seqlens holds integer offsets'
+    if cu_seqlens.is_cuda and torch.cuda.is_current_stream_capturing():
+        return
+    cu = cu_seqlens.detach().to('cpu', torch.int64)
+    assert int(cu[0]) == 0, f'cu_seqlens[0] must be 0, got {int(cu[0])}'
+    assert int(cu[-1]) == n_tokens, f'cu_seqlens[-1] must equal the {n_tokens} packed tokens, got {int(cu[-1])}'
+    assert n_tokens < 2 ** 31, f'{n_tokens} packed tokens exceed the int32 offsets'
+    if cu.numel() > 1:
+        assert bool((cu[1:] >= cu[:-1]).all()), 'cu_seqlens must be non-decreasing'
+
+
 def _wants_grad(*ts):
     return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in ts)
 
@@ -177,8 +198,7 @@ class _Call:
             assert beta is not None and beta.shape == (B, T, H), 'the delta rule needs beta (B, T, H)'
         if cu_seqlens is not None:
             assert B == 1, f'packed varlen input (cu_seqlens) has batch 1, got {B}'
-            assert cu_seqlens.dim() == 1 and cu_seqlens.numel() >= 1, 'cu_seqlens is 1-D with N + 1 entries'
-            assert not cu_seqlens.is_floating_point(), 'cu_seqlens holds integer offsets'
+            _check_cu(cu_seqlens, T)
             N = cu_seqlens.numel() - 1
             cu = cu_seqlens.to(torch.int32).contiguous()
         else:
@@ -862,6 +882,7 @@ def causal_conv1d(x, weight, bias=None, residual=None, initial_state=None, outpu
     w = w.contiguous() if w.dtype in (torch.float32, x.dtype) else w.float().contiguous()
     if cu_seqlens is not None:
         assert B == 1, f'packed varlen input (cu_seqlens) has batch 1, got {B}'
+        _check_cu(cu_seqlens, T)
         cu = cu_seqlens.to(torch.int32).contiguous()
         N = cu.numel() - 1
     else:
