@@ -200,6 +200,27 @@ int vgdr_chunk_prep_fused(int dtype, int gate_kind, int use_delta,
                           float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
 
 /*
+ * vgdr_chunk_fwd_fused without a workspace argument and without allocating
+ * (no reference counterpart: for callers that cannot allocate device memory,
+ * such as code under HIP graph capture or a serving loop that forbids
+ * hipMalloc).  The chunk workspace lives in a device array the library holds
+ * per GPU, VGDR_CHUNK_SCRATCH_BYTES long, from the first call on that GPU to
+ * the end of the process.  A call whose vgdr_chunk_workspace_size exceeds it
+ * returns VGDR_ERR_INVALID (use vgdr_chunk_fwd_fused with a workspace).
+ * Calls that overlap on one GPU (two streams, two threads) share that array
+ * and race; serialise them.  Otherwise the arguments, checks and results are
+ * those of vgdr_chunk_fwd_fused (fusion may be NULL).
+ */
+#define VGDR_CHUNK_SCRATCH_BYTES (64LL << 20)
+int vgdr_chunk_fwd_noalloc(int dtype, int gate_kind, int use_delta,
+                           const void *q, const void *k, const void *v,
+                           const float *g, const float *beta,
+                           void *o, const float *initial_state, float *final_state,
+                           const int32_t *cu_seqlens,
+                           int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                           float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
+
+/*
  * vgdr_chunk_fwd with an explicit write vector w [n_tokens, H, dk] (16-bit,
  * 16-byte aligned) in place of beta_t k_t: the asymmetric delta rule of
  * chunk_scan_vec(..., w=w) (linear_attention.py:312-425, :340-353,

@@ -123,3 +123,14 @@ def test_padding_helpers():
     p = ops._pad_to(t, {1: 16, 2: 8})
     assert p.shape == (2, 3, 8, 16) and p[..., :5, :7].eq(1).all() and p.sum() == t.sum()
     assert ops._pad_to(t, {1: 7}) is t
+
+
+def test_noalloc_entry_point_rejects_calls_beyond_its_scratch():
+    """vgdr_chunk_fwd_noalloc checks the workspace a call needs against the
+    library's per-GPU scratch before it touches a device."""
+    L = _lib.load()
+    limit = 64 << 20
+    assert L.vgdr_chunk_workspace_size(_lib.VGDR_BF16, 1, 64, 8192, 16, 128, 64, 0, 64) > limit
+    rc = L.vgdr_chunk_fwd_noalloc(_lib.VGDR_BF16, 1, 1, 4096, 8192, 12288, 16384, 20480, 24576, None, None, None,
+                                  64, 8192, 16, 128, 128, 64, 0.1, 64, None, None)
+    assert rc == _lib.VGDR_ERR_INVALID and b'scratch' in L.vgdr_last_error()

@@ -57,6 +57,8 @@ SIGNATURES = {
                                   _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
     'vgdr_chunk_prep_fused': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                                    _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
+    'vgdr_chunk_fwd_noalloc': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
+                                    _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
     'vgdr_chunk_fwd_w': (_I, [_I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _L,
                               _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P]),
     'vgdr_chunk_bwd_workspace_size': (_L, [_I, _I, _L, _L, _L, _L, _L, _L, _I, _I]),

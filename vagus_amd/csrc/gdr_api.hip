@@ -5,6 +5,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "../../include/vagus_gdr.h"
 #include "gdr_kernels.hpp"
 
@@ -404,6 +406,67 @@ int vgdr_chunk_bwd(VGDR_BWD_ARGS) { return bwd_call("vgdr_chunk_bwd", false, VGD
 int vgdr_chunk_bwd_saved(VGDR_BWD_ARGS) { return bwd_call("vgdr_chunk_bwd_saved", true, VGDR_BWD_PASS); }
 #undef VGDR_BWD_ARGS
 #undef VGDR_BWD_PASS
+
+}  // extern "C"
+
+namespace {
+// Scratch of vgdr_chunk_fwd_noalloc: the chunk workspace (segment table and
+// per-(chunk, head) blocks) in a file-scope device array, so that the call
+// allocates nothing.  Each GPU holds its own copy for the life of the
+// process; host code reaches it only through the address hipGetSymbolAddress
+// returns on that device (the array's name is a host-side stand-in).  Its
+// contents need no clearing: the prep phase writes every byte the state
+// phase reads.  Calls that overlap on one GPU share it and race.
+constexpr int64_t kScratchBytes = VGDR_CHUNK_SCRATCH_BYTES;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+
+// the current device's scratch address, looked up once per device with that device current
+int scratch_address(const char *fn, void **out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_status(e, fn);
+    if (dev < 0 || dev >= kMaxDevices) return fail(VGDR_ERR_UNSUPPORTED, "%s: device %d out of range", fn, dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_status(e, fn);
+        if (!p) return fail(VGDR_ERR_HIP, "%s: no device address for the scratch array", fn);
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return VGDR_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int vgdr_chunk_fwd_noalloc(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                           const float *g, const float *beta, void *o, const float *initial_state,
+                           float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H,
+                           int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
+                           const vgdr_fusion *fusion, hipStream_t stream) {
+    const char *fn = "vgdr_chunk_fwd_noalloc";
+    g_err[0] = 0;
+    if (B >= 0 && T >= 0 && H > 0 && n_seqs >= 0 && B * T > 0) {
+        const int chunk = effective_chunk(dtype, dk, chunk_size);
+        const int64_t need = chunk_layout(dtype, gate_kind, chunk, B, T, H, dk, n_seqs, cu_seqlens != nullptr).total;
+        if (need > kScratchBytes)
+            return fail(VGDR_ERR_INVALID, "%s: this call needs %lld bytes of scratch, more than the %lld the "
+                        "library holds per GPU (use vgdr_chunk_fwd_fused with a workspace)", fn, (long long)need,
+                        (long long)kScratchBytes);
+    }
+    void *ws = nullptr;
+    const int rc = scratch_address(fn, &ws);
+    if (rc) return rc;
+    return chunk_call(fn, vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, dtype, gate_kind, use_delta, q, k, v, g, beta, o,
+                      initial_state, final_state, cu_seqlens, ws, kScratchBytes, B, T, H, dk, dv, n_seqs, scale,
+                      chunk_size, fusion, stream);
+}
 
 int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
                           const float *beta, void *o, const float *initial_state, float *final_state,
