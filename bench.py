@@ -12,8 +12,9 @@ so that no step finds its operands in the 256 MB Infinity Cache.
 
 The prefill runs as two kernels per call: chunk_prep (every (chunk, head) in
 parallel: the intra-chunk Q K^T and K K^T products and the triangular
-inverse) and chunk_state (the sequential chunk recurrence per (sequence,
-head, dv tile)), the dominant one.  The timed steps issue them as
+inverse) and chunk_state (chunk_pipe_kernel: the sequential chunk recurrence
+per (sequence, head, dv tile), with the outputs computed one chunk behind by
+waves of their own), the dominant one.  The timed steps issue them as
 vgdr_chunk_prep + vgdr_chunk_state with an event in between (identical GPU
 work to vgdr_chunk_fwd), so each kernel has its own event-timed duration.
 
@@ -23,7 +24,8 @@ Also reported on the same line:
                 products and the two intra-chunk products with V) per launch,
                 over its event-timed average duration; `traffic` = its measured
                 HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE scaled
-                by a plain-copy calibration, profiles/traffic.json) when present
+                by a plain-copy calibration, profiles/traffic.json) when one was
+                measured on the current kernel sources, else null
   path          both kernels together against the reference's own count,
                 forward chunk_scan_flops / 3 = 180,224 FLOP per token-head
   decode        one recurrent decode step at the 1.3B layer shape (B=64 H=16
@@ -301,7 +303,7 @@ def bench_scan_backward(torch, ops, workloads, steps, warmup):
     tflops = th * 2 * FLOP_PER_TOKEN_HEAD / (us * 1e-6) / 1e12
     return {'workload': 'kda_prefill backward: dq, dk, dv, dg (per channel), dbeta, dh0 from do and dht, '
                         'B4 T8192 H8 dk=dv=128 bf16',
-            'kernels': 'scan_bwd_kernel + scan_bwd_finish_kernel',
+            'kernels': 'scan_walks_kernel + scan_grad_kernel + scan_bwd_finish_kernel',
             'us': round(us, 1), 'tok_s': round(B * T / (us * 1e-6), 1),
             'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
             'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5)}
@@ -337,17 +339,89 @@ def cpu_baseline(torch, workloads):
                       f'in fp32, median of 3 after 1 warmup, {med:.2f} s per run, {cpu}'}
 
 
+# kernel sources each measured traffic record depends on: a record whose
+# fingerprint differs from the current sources is stale and is not reported
+TRAFFIC_SOURCES = {
+    'chunk_state': ('gdr_chunk.hip', 'gdr_chunk_layout.hpp', 'gdr_common.hpp', 'gdr_kernels.hpp'),
+    'chunk_prep': ('gdr_chunk.hip', 'gdr_chunk_layout.hpp', 'gdr_common.hpp', 'gdr_kernels.hpp'),
+    'recurrent': ('gdr_recurrent.hip', 'gdr_common.hpp', 'gdr_kernels.hpp'),
+}
+# (workload, kernel) -> the kernel-name prefix rocprofv3 reports for it
+TRAFFIC_KERNELS = {
+    ('gdn_340m', 'chunk_state'): 'vgdr::chunk_pipe_kernel<128, 64, 2',
+    ('gdn_340m', 'chunk_prep'): 'vgdr::chunk_prep_kernel<128, 64',
+    ('decode_b64_h16', 'recurrent'): 'vgdr::recurrent_kernel<128, 128',
+}
+
+
+def sources_sha(kernel):
+    import hashlib
+    h = hashlib.sha256()
+    for name in TRAFFIC_SOURCES[kernel]:
+        with open(os.path.join(ROOT, 'vagus_amd', 'csrc', name), 'rb') as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(workload, kernel):
     """HBM bytes per launch of `kernel` ('chunk_state' / 'chunk_prep' / 'recurrent') on
     `workload`, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
-    (profiles/traffic.json), if one exists."""
+    (profiles/traffic.json), or None when there is none or it was measured on
+    other kernel sources."""
     path = os.path.join(ROOT, 'profiles', 'traffic.json')
     try:
         with open(path) as f:
             rec = json.load(f)[workload][kernel]
+        if rec.get('sources_sha') != sources_sha(kernel):
+            return None
         return int(rec['bytes_per_launch'])
     except (OSError, ValueError, KeyError, TypeError):
         return None
+
+
+def write_traffic(run_dir):
+    """profiles/traffic.json from rocprofv3 --pmc runs under run_dir: one
+    counter_collection.csv per directory prefill_FETCH_SIZE, prefill_WRITE_SIZE
+    (bench.py --prefill-only), decode_FETCH_SIZE, decode_WRITE_SIZE
+    (--decode-only) and copy_FETCH_SIZE, copy_WRITE_SIZE (--calibrate-copy).
+    Counters are in KiB per dispatch; a plain 1 GiB copy scales them to bytes."""
+    import csv
+    import glob
+
+    def per_kernel(sub, counter):
+        files = glob.glob(os.path.join(run_dir, f'{sub}_{counter}', '**', '*counter_collection.csv'), recursive=True)
+        if not files:
+            raise SystemExit(f'no counter_collection.csv under {run_dir}/{sub}_{counter}')
+        vals = {}
+        for row in csv.DictReader(open(files[0])):
+            if row['Counter_Name'] == counter:
+                vals.setdefault(row['Kernel_Name'], []).append(float(row['Counter_Value']))
+        return {k: sum(v) / len(v) for k, v in vals.items()}
+
+    def pick(table, prefix):
+        hits = [v for k, v in table.items() if k.startswith(prefix) or ('void ' + prefix) in k]
+        if not hits:
+            raise SystemExit(f'no kernel {prefix} in the counters')
+        return hits[0]
+
+    copy_bytes = 1 << 30
+    cf = max(per_kernel('copy', 'FETCH_SIZE').values())
+    cw = max(per_kernel('copy', 'WRITE_SIZE').values())
+    fs, ws = copy_bytes / 1024 / cf, copy_bytes / 1024 / cw
+    out = {'calibration': {'copy_fetch_KiB': cf, 'copy_write_KiB': cw, 'fetch_scale': round(fs, 4),
+                           'write_scale': round(ws, 4)}}
+    for (wl, kern), prefix in TRAFFIC_KERNELS.items():
+        sub = 'decode' if kern == 'recurrent' else 'prefill'
+        f_kib = pick(per_kernel(sub, 'FETCH_SIZE'), prefix)
+        w_kib = pick(per_kernel(sub, 'WRITE_SIZE'), prefix)
+        rd, wr = f_kib * 1024 * fs, w_kib * 1024 * ws
+        out.setdefault(wl, {})[kern] = {'bytes_per_launch': int(rd + wr), 'read_bytes': int(rd), 'write_bytes': int(wr),
+                                        'fetch_KiB': f_kib, 'write_KiB': w_kib, 'kernel': prefix,
+                                        'sources_sha': sources_sha(kern)}
+    path = os.path.join(ROOT, 'profiles', 'traffic.json')
+    with open(path, 'w') as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
 
 
 def main():
@@ -364,7 +438,13 @@ def main():
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a plain 1 GiB device copy (x5): the reference point that scales '
                          'rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes')
+    ap.add_argument('--write-traffic', metavar='RUN_DIR',
+                    help='write profiles/traffic.json from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs '
+                         '(see write_traffic) and exit; needs no GPU')
     args = ap.parse_args()
+    if args.write_traffic:
+        write_traffic(args.write_traffic)
+        return
     if args.gpus != 1:
         print(f'bench.py: this build measures one GPU only (the gated delta-rule core has no '
               f'cross-GPU path here); --gpus {args.gpus} is not supported', file=sys.stderr)
@@ -450,11 +530,11 @@ def main():
         'roofline': {'bound': 'mfma', 'achieved': round(achieved, 2), 'peak': PEAK_BF16_TFLOPS,
                      'unit': 'TFLOP/s', 'frac': round(achieved / PEAK_BF16_TFLOPS, 5),
                      'traffic': measured_traffic('gdn_340m', 'chunk_state'),
-                     'kernel': 'chunk_state_tr_kernel', 'kernel_avg_ms': round(pre['state_ms'], 4),
+                     'kernel': 'chunk_pipe_kernel', 'kernel_avg_ms': round(pre['state_ms'], 4),
                      'flop_per_launch': tokens * H * STATE_FLOP_PER_TOKEN_HEAD,
                      'algorithmic_bytes_per_launch': tokens * H * STATE_BYTES_PER_TOKEN_HEAD,
                      'hbm_algorithmic_GBs': round(state_gbs, 1)},
-        'path': {'kernels': 'chunk_prep_kernel + chunk_state_tr_kernel', 'op_ms': round(pre['op_ms'], 4),
+        'path': {'kernels': 'chunk_prep_kernel + chunk_pipe_kernel', 'op_ms': round(pre['op_ms'], 4),
                  'prep_ms': round(pre['prep_ms'], 4), 'state_ms': round(pre['state_ms'], 4),
                  'achieved_tflops': round(pre['path_tflops'], 2),
                  'frac_mfma': round(pre['path_tflops'] / PEAK_BF16_TFLOPS, 5),

@@ -491,9 +491,10 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         res_k[s] = mk;
     }
     if constexpr (CB::VEC) {
-        // gated tiles for chunk_state_tr_kernel: K*G, scale Q*G, K*Gend, rows in
+        // gated tiles for the state kernel: K*G and K*Gend with rows in
         // paired-column order (16-byte unit pu = 4 q + g holds columns 32 q + 4 g
-        // .. + 3 and 32 q + 16 + 4 g .. + 3), then Gc = exp(gamma_C)
+        // .. + 3 and 32 q + 16 + 4 g .. + 3), scale Q*G in natural column order,
+        // then Gc = exp(gamma_C)
         using F2 = typename EL::frag2;
         E *tg = reinterpret_cast<E *>(blk_base) + CB::TEA;
         constexpr int UPR = DK / 8;
@@ -507,7 +508,9 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             const f32x4 q0 = EL::tof(ld_frag<E>(Qst + SK::at(t, c0))), q1 = EL::tof(ld_frag<E>(Qst + SK::at(t, c1)));
             E *row = tg + t * DK + 8 * pu;
             *reinterpret_cast<F2 *>(row) = EL::cvt2(k0 * e0, k1 * e1);
-            *reinterpret_cast<F2 *>(row + CH * DK) = EL::cvt2(q0 * e0 * p.scale, q1 * e1 * p.scale);
+            E *qrow = tg + CH * DK + t * DK;
+            st_frag<E>(qrow + c0, EL::cvt(q0 * e0 * p.scale));
+            st_frag<E>(qrow + c1, EL::cvt(q1 * e1 * p.scale));
             if constexpr (WR) {                                  // the state update writes with W * Gend
                 const f32x4 w0 = EL::tof(ld_frag<E>(Wst + SK::at(t, c0))), w1 = EL::tof(ld_frag<E>(Wst + SK::at(t, c1)));
                 *reinterpret_cast<F2 *>(row + 2 * CH * DK) = EL::cvt2(w0 * d0, w1 * d1);
@@ -935,8 +938,7 @@ __global__ void __launch_bounds__(64 * NW) chunk_state_kernel(const ChunkParams 
 }
 
 // ===========================================================================
-// chunk_state_tr_kernel: the chunk recurrence for 16-bit elements with a
-// scalar gate or none, on LDS transpose reads
+// helpers of the 16-bit state kernel (LDS transpose reads, producer copies)
 // ===========================================================================
 // Values the compiler must treat as unknown where they are produced.  Address
 // arithmetic derived from them is redone next to each use instead of being
@@ -947,7 +949,7 @@ __device__ __forceinline__ int opaque_s(int x) { asm volatile("" : "+s"(x)); ret
 // the value is computed at this point in program order
 template <typename T> __device__ __forceinline__ void pin_v(const T &x) { asm volatile("" ::"v"(x)); }
 
-// LDS layout of chunk_state_tr_kernel.  Rows are padded by 32 bytes and every
+// LDS layout of the 16-bit state kernel's K rows.  Rows are padded by 32 bytes and every
 // fragment address is a per-lane base plus a compile-time offset.  Measured on
 // gfx950 (8 waves on one CU): the 16-byte fragment reads of 16 rows and the
 // transpose reads of 4 rows x 4 lanes both run conflict-free at a 288-byte
@@ -1081,58 +1083,75 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
     return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-// Differences from chunk_state_kernel, all to shorten the per-chunk chain:
-//   * NP producer waves (the last ones) copy the next chunk's operands into
-//     the other half of the double buffer while the NW compute waves work,
-//     issuing the loads of chunk c + 2 as soon as chunk c + 1 is stored;
-//   * the decay factors G, Gend come precomputed from chunk_prep;
-//   * every MFMA operand is one 16-byte LDS read or one register pair (the
-//     layouts above and the paired TE / A blocks), addresses fold into
-//     instruction offsets;
-//   * (K*Gend)^T for the state update and V in C layout come from transpose
-//     reads of the row-major K and V tiles: no transposed copy of K;
-//   * the output is computed transposed, O^T = S^T (scale Q*G)^T + U~^T A^T:
-//     S's and U~'s C-layout accumulators are the A operands, Q and A are read
-//     as for O, and each lane ends up holding four consecutive columns of one
-//     token, which it stores to global memory directly (no staging).
-// One workgroup barrier per chunk: the double-buffer hand-over.
-// One workgroup per CU (LDS-limited) of NW + NP <= 8 waves: at most two waves per
-// SIMD, so the compiler may use up to 256 registers per wave for lookahead.
-// HS: also store each chunk's entry state (the element-type copy the products
-// use) to p.hs ([chunk slot, H] checkpoints in ckpt_pos order): the states the
-// chunked backward reads, saved by a training forward instead of recomputed.
+// ===========================================================================
+// chunk_pipe_kernel: the chunk recurrence for 16-bit elements, with the
+// outputs computed one chunk behind by waves of their own
+// ===========================================================================
+// The recurrence S_c -> S_c+1 is the only sequential part of the prefill; the
+// outputs o_c = GO Q_c S_c + A_c U~_c hang off it.  One workgroup per
+// (sequence, head, 16 NW-column dv tile) splits its waves by role:
+//   chain waves   0 .. NW - 1     wave w owns columns col0 + 16 w .. + 15 of the
+//                                  state as fp32 C-layout accumulators for the whole
+//                                  sequence and runs only the recurrence:
+//                                  P = K S, X = V - GX P, U~ = TE X,
+//                                  S <- Gc S + (GE K)^T U~  (per-channel gate: K*G,
+//                                  K*Gend tiles and Gc per key channel).  For each
+//                                  chunk it leaves S_c (element type) and U~_c in LDS.
+//   output waves  NW .. 2 NW - 1   wave NW + w computes chunk c's O^T = S_c^T (GO Q)^T
+//                                  + U~_c^T A^T for the same columns while the chain
+//                                  runs chunk c + 1.  Q (or scale Q*G) and A come from
+//                                  global memory straight into registers, issued before
+//                                  the hand-over barrier and consumed after it.
+//   producers     2 NW ..          copy chunk c + 1's K (K*G and K*Gend), V, TE and gate
+//                                  factors into the idle half of the double buffer.
+// The chain waves thus issue 38 of the 60 MFMAs per chunk and column strip, and
+// the output products run on the other SIMDs (waves w and NW + w sit on
+// different SIMDs of the CU whenever NW <= 2).
+//
+// Barriers: b = 0 .. n (n chunks).  Barrier b hands operand slot b & 1 (chunk b)
+// to the chain waves and hand-over buffer (b - 1) & 1 (chunk b - 1) to the output
+// waves; every role passes all n + 1 of them.  Writes to a hand-over buffer
+// (chain, during step c) and its reads (output, during step c + 1) are separated
+// by barrier c + 1, and the next write to it (step c + 2) by barrier c + 2.
+//
+// Hand-over layout per chain wave and buffer:
+//   SH: the state in the element type, one row of DK + 8 elements per state
+//       column (natural key order), so the output wave reads eight consecutive
+//       keys per lane and its Q operand is a plain 16-byte load of a q row;
+//   UH: U~ in the MFMA A-operand order the chain wave holds it (lane-to-lane).
+// HS: the output waves also store each chunk's entry state to p.hs
+// ([chunk slot, H] checkpoints in ckpt_pos order), for the chunked backward.
 template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA, bool HS = false>
-__global__ void __launch_bounds__(64 * (NW + NP)) __attribute__((amdgpu_waves_per_eu(1, 2)))
-chunk_state_tr_kernel(const ChunkParams p) {
+__global__ void __launch_bounds__(64 * (NW + 2 + NP))
+__attribute__((amdgpu_waves_per_eu(1, (NW + 2 + NP + 3) / 4)))
+chunk_pipe_kernel(const ChunkParams p) {
     static_assert(sizeof(E) == 2, "transpose reads take 16-bit elements");
     using EL = Elem<E>;
     using F2 = typename EL::frag2;
+    typedef E E4 __attribute__((ext_vector_type(4)));
     using CB = ChunkBlock<E, CH, DK, VEC ? 2 : 1>;
     using KQ = KQRows<DK>;
     constexpr int NB = CH / 16, NKB = DK / 16, DVT = 16 * NW, NPT = 64 * NP;
-    // V rows: 2.4 cycles per transpose read at a pitch of DVT + 16 elements,
-    // 3.8 at DVT + 8 (which the per-channel-gate layout with 64 columns needs
-    // to stay within 160 KiB)
     constexpr int PK = KQ::PITCH, PV = (VEC && NW == 4) ? DVT + 8 : DVT + 16;
-    constexpr int TEAB = CB::TEA * (int)sizeof(E);              // bytes of TE + A in a slot
-    constexpr int BSLOT = TEAB + CB::FLOATS * 4;                 // TE, A, then G, Gend | Gc
+    constexpr int SP = DK + 8;                                   // hand-over state row pitch (elements)
+    constexpr int TEB = CH * CH * (int)sizeof(E);                // bytes of TE in a slot
+    constexpr int FB = CB::FLOATS * 4;                           // bytes of the gate factors
     static_assert(NB % 2 == 0 && NKB % 2 == 0, "k-blocks are consumed in pairs");
+    static_assert(TEB % 16 == 0 && FB % 16 == 0, "slots are copied in 16-byte units");
 
-    // K, Q hold K*G and scale Q*G for a per-channel gate (VEC), KE then K*Gend
     __shared__ __attribute__((aligned(16))) E K0[CH * PK];
     __shared__ __attribute__((aligned(16))) E K1[CH * PK];
-    __shared__ __attribute__((aligned(16))) E Q0[CH * PK];
-    __shared__ __attribute__((aligned(16))) E Q1[CH * PK];
     __shared__ __attribute__((aligned(16))) E KE0[VEC ? CH * PK : 8];
     __shared__ __attribute__((aligned(16))) E KE1[VEC ? CH * PK : 8];
     __shared__ __attribute__((aligned(16))) E V0[CH * PV];
     __shared__ __attribute__((aligned(16))) E V1[CH * PV];
-    __shared__ __attribute__((aligned(16))) char B0[BSLOT];
-    __shared__ __attribute__((aligned(16))) char B1[BSLOT];
+    __shared__ __attribute__((aligned(16))) char B0[TEB + FB];
+    __shared__ __attribute__((aligned(16))) char B1[TEB + FB];
+    __shared__ __attribute__((aligned(16))) E SH[2 * NW * 16 * SP];
+    __shared__ __attribute__((aligned(16))) E UH[2 * NW * (NB / 2) * 64 * 8];
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int H = p.H, DV = p.DV;
-    const bool producer = wave >= NW;
 
     // ---- work item: the dv tiles of one (sequence, head) share an XCD ------
     const int b = blockIdx.x;
@@ -1147,8 +1166,6 @@ chunk_state_tr_kernel(const ChunkParams p) {
     seq_bounds(p.geo, seq, bos, eos);
     const int64_t cbase = chunk_base(p.geo, seq);
     const int col0 = tile * DVT;
-    const int wcol = 16 * wave;                                  // within the tile
-    const bool wvalid = !producer && col0 + wcol < DV;           // DV % 16 == 0
     const int64_t sqk = (int64_t)H * DK, sv = (int64_t)H * DV;
     const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
     const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
@@ -1157,78 +1174,49 @@ chunk_state_tr_kernel(const ChunkParams p) {
     const int64_t len = eos - bos;
     const int nchunks = (int)((len + CH - 1) / CH);
 
-    // producer: one chunk's operands in registers.  load(st, c) may run ahead
-    // of the slot hand-over; store(st, c) writes slot c & 1.  K and Q come
-    // from q and k (scalar gate), or already gated and paired from chunk_prep
-    // (VEC).  A chunk index past the end loads the last chunk again (every
-    // address stays inside the tensors).
-    using CK = RowCopy<E, CH, DK, NPT, !VEC, PK>;            // K, Q (VEC: K*G, scale Q*G, K*Gend)
-    using CV = RowCopy<E, CH, DVT, NPT, false, PV>;
-    struct Staged {
-        CK k, q, e;
-        CV v;
-        FlatCopy<TEAB / 16, NPT> b;
-        FlatCopy<CB::FLOATS * 4 / 16, NPT> f;
-    };
-    struct Plans {
-        typename CK::Plan k;
-        typename CV::Plan v;
-    };
-    auto load = [&](Staged &st, const Plans &pl, int c, int pt) __attribute__((always_inline)) {
-        c = c < nchunks ? c : nchunks - 1;
-        const int64_t t0 = bos + (int64_t)c * CH;
-        const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
-        const char *bk = blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES;
-        st.b.load(bk, pt);
-        st.f.load(bk + CB::GOFF, pt);
-        if constexpr (VEC) {
-            const E *tiles = reinterpret_cast<const E *>(bk) + CB::TEA;
-            st.k.load(tiles, pl.k, CH);
-            st.v.load(vg + t0 * sv, pl.v, clen);
-            st.q.load(tiles + CH * DK, pl.k, CH);
-            st.e.load(tiles + 2 * CH * DK, pl.k, CH);
-        } else {
-            st.k.load(kg + t0 * sqk, pl.k, clen);
-            st.v.load(vg + t0 * sv, pl.v, clen);
-            st.q.load(qg + t0 * sqk, pl.k, clen);
-        }
-    };
-    auto store = [&](const Staged &st, const Plans &pl, int c, int z, int pt) __attribute__((always_inline)) {
-        const bool odd = c & 1;
-        st.b.store((odd ? B1 : B0) + z, pt);
-        st.f.store((odd ? B1 : B0) + z + TEAB, pt);
-        st.k.store((odd ? K1 : K0) + z, pl.k);
-        st.v.store((odd ? V1 : V0) + z, pl.v);
-        st.q.store((odd ? Q1 : Q0) + z, pl.k);
-        if constexpr (VEC) st.e.store((odd ? KE1 : KE0) + z, pl.k);
-    };
-
-    // ---- entry state (C layout: S[kt][j] = S[16kt + 4g + j][col0 + wcol + r]) --
-    f32x4 S[NKB];
-    {
-        const int g4 = lane >> 4, r16 = lane & 15;
-        const int64_t sbase = ((int64_t)seq * H + h) * DK * DV + col0 + wcol + r16;
-#pragma unroll
-        for (int kt = 0; kt < NKB; ++kt)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
-    }
-
-    // Producers and compute waves run separate loops with the same barriers:
-    // in one shared loop the wait-count insertion merged the producers'
-    // in-flight loads into the compute path and made it wait for all of its
-    // own stores at every chunk.
-    //
-    // Two register sets: when chunk c + 1 is stored (after hand-over c), chunk
-    // c + 2 is already in flight in the other set and chunk c + 3 is issued
-    // into the set just emptied, so every load has a whole chunk step to land.
-    // The loop body is unrolled over the two sets and free of per-chunk
-    // branches; a store past the last chunk goes to the idle slot, which no
-    // compute wave reads again.
-    if (producer) {
+    // ======================= producers ======================================
+    if (wave >= NW + 2) {
+        using CK = RowCopy<E, CH, DK, NPT, !VEC, PK>;            // K rows (VEC: K*G and K*Gend tiles)
+        using CV = RowCopy<E, CH, DVT, NPT, false, PV>;
+        struct Staged {
+            CK k, e;
+            CV v;
+            FlatCopy<TEB / 16, NPT> t;
+            FlatCopy<FB / 16, NPT> f;
+        };
+        struct Plans {
+            typename CK::Plan k;
+            typename CV::Plan v;
+        };
+        // a chunk index past the end loads the last chunk again (every address
+        // stays inside the tensors); store(st, c) writes slot c & 1
+        auto load = [&](Staged &st, const Plans &pl, int c, int pt) __attribute__((always_inline)) {
+            c = c < nchunks ? c : nchunks - 1;
+            const int64_t t0 = bos + (int64_t)c * CH;
+            const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+            const char *bk = blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES;
+            st.t.load(bk, pt);
+            st.f.load(bk + CB::GOFF, pt);
+            if constexpr (VEC) {
+                const E *tiles = reinterpret_cast<const E *>(bk) + CB::TEA;
+                st.k.load(tiles, pl.k, CH);
+                st.v.load(vg + t0 * sv, pl.v, clen);
+                st.e.load(tiles + 2 * CH * DK, pl.k, CH);
+            } else {
+                st.k.load(kg + t0 * sqk, pl.k, clen);
+                st.v.load(vg + t0 * sv, pl.v, clen);
+            }
+        };
+        auto store = [&](const Staged &st, const Plans &pl, int c, int z, int pt) __attribute__((always_inline)) {
+            const bool odd = c & 1;
+            st.t.store((odd ? B1 : B0) + z, pt);
+            st.f.store((odd ? B1 : B0) + z + TEB, pt);
+            st.k.store((odd ? K1 : K0) + z, pl.k);
+            st.v.store((odd ? V1 : V0) + z, pl.v);
+            if constexpr (VEC) st.e.store((odd ? KE1 : KE0) + z, pl.k);
+        };
         if (nchunks > 0) {
-            const int pt = tid - 64 * NW;
+            const int pt = tid - 64 * (NW + 2);
             const Plans pl{CK::plan(VEC ? DK : sqk, DK, pt), CV::plan(sv, DV - col0, pt)};
             Staged s0, s1;
             load(s0, pl, 0, pt);
@@ -1238,144 +1226,272 @@ chunk_state_tr_kernel(const ChunkParams p) {
             int c = 0;
             for (; c + 1 < nchunks; c += 2) {
                 int z = opaque_s(0);
-                lds_barrier();                                // chunk c in place; chunk c-1 fully consumed
+                lds_barrier();                                // barrier c: chunk c in place, chunk c-1 consumed
                 store(s1, pl, c + 1, z, pt);                  // into the slot chunk c-1 used
                 load(s1, pl, c + 3, pt);
                 z = opaque_s(0);
-                lds_barrier();                                // hand-over c + 1
+                lds_barrier();                                // barrier c + 1
                 store(s0, pl, c + 2, z, pt);
                 load(s0, pl, c + 4, pt);
             }
-            if (c < nchunks) lds_barrier();                   // hand-over of the last (even) chunk
+            if (c < nchunks) lds_barrier();                   // barrier n - 1 (n odd)
+            lds_barrier();                                    // barrier n: the last chunk's outputs
             __builtin_amdgcn_s_waitcnt(0);                    // no load left in flight at exit
         }
         return;
     }
-    for (int c = 0; c < nchunks; ++c) {
-        const int z = opaque_s(0);
-        lds_barrier();                                        // the hand-over, as above
-        if (!wvalid) continue;
-        const int ln = opaque_v(lane);
-        const int g4 = ln >> 4, r16 = ln & 15;
+
+    // ======================= chain waves ====================================
+    if (wave < NW) {
+        const int wcol = 16 * wave;
+        const bool wvalid = col0 + wcol < DV;                  // DV % 16 == 0
+        // entry state (C layout: S[kt][j] = S[16kt + 4g + j][col0 + wcol + r])
+        f32x4 S[NKB];
+        {
+            const int g4 = lane >> 4, r16 = lane & 15;
+            const int64_t sbase = ((int64_t)seq * H + h) * DK * DV + col0 + wcol + r16;
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
+        }
+        for (int c = 0; c < nchunks; ++c) {
+            const int z = opaque_s(0);
+            lds_barrier();                                    // barrier c
+            if (!wvalid) continue;
+            const int ln = opaque_v(lane);
+            const int g4 = ln >> 4, r16 = ln & 15;
+            const bool odd = c & 1;
+            // per-lane bases; every fragment below is base + a compile-time offset
+            const E *Krow = (odd ? K1 : K0) + z + r16 * PK + 8 * g4;                 // row r, unit g
+            const E *Ktr = (VEC ? (odd ? KE1 : KE0) : (odd ? K1 : K0)) + z + (4 * g4 + (r16 >> 2)) * PK + 8 * (r16 & 3);
+            const E *Vtr = (odd ? V1 : V0) + z + (4 * g4 + (r16 >> 2)) * PV + wcol + 4 * (r16 & 3);
+            const char *Bst = (odd ? B1 : B0) + z;
+            const E *TEs = reinterpret_cast<const E *>(Bst) + 8 * ln;
+            // scalar gate: GX, GO, GE, Gc (ChunkBlock); VEC: Gc per key channel
+            const float *gs = reinterpret_cast<const float *>(Bst + TEB), *ge = gs + 2 * CH;
+            E *sh = SH + ((odd ? NW : 0) + wave) * 16 * SP + z + r16 * SP + 4 * g4;
+            E *uh = UH + ((odd ? NW : 0) + wave) * (NB / 2) * 512 + z + 8 * ln;
+
+            // Operands that do not depend on the state are read first, in one
+            // batch (the scheduler would otherwise issue each next to its use,
+            // one LDS round trip apiece on the critical path): the gate factors,
+            // TE, the V rows.
+            f32x4 gx[NB], gev[NB], gcv[VEC ? NKB : 1];
+            float gc = 0.f;
+            F2 te[NB][NB / 2];
+            typename EL::frag vf[NB];
+            if constexpr (VEC) {
+                unroll<NKB>([&](auto kt) { gcv[kt] = ld4(gs + 16 * kt + 4 * g4); });     // Gc per key channel
+            } else {
+                unroll<NB>([&](auto I) {
+                    gx[I] = ld4(gs + 16 * I + 4 * g4);
+                    gev[I] = ld4(ge + 16 * I + 4 * g4);
+                });
+                gc = gs[3 * CH];
+            }
+            if constexpr (DELTA)
+                unroll<NB>([&](auto I) {
+                    unroll<NB / 2>([&](auto q) {
+                        if (2 * q <= I) te[I][q] = ld_pair<E>(TEs + frag_pair_pos<NB>(I, q, 0));
+                    });
+                });
+            // V rows in C layout: V[16 I + 4 g + j][wcol + r]
+            unroll<NB>([&](auto I) { vf[I] = ld_tr<E>(Vtr + 16 * I * PV); });
+            __builtin_amdgcn_sched_barrier(0);
+
+            F2 Sb[NKB / 2];
+#pragma unroll
+            for (int q = 0; q < NKB / 2; ++q) {
+                Sb[q] = EL::cvt2(S[2 * q], S[2 * q + 1]);
+                // rows 32 q + 4 g .. + 3 and 32 q + 16 + 4 g .. + 3 of column r
+                *reinterpret_cast<E4 *>(sh + 32 * q) = __builtin_shufflevector(Sb[q], Sb[q], 0, 1, 2, 3);
+                *reinterpret_cast<E4 *>(sh + 32 * q + 16) = __builtin_shufflevector(Sb[q], Sb[q], 4, 5, 6, 7);
+            }
+            f32x4 U[NB];
+            if constexpr (DELTA) {
+                // P = K S (C layout), NB independent accumulation chains
+                f32x4 P[NB];
+#pragma unroll
+                for (int I = 0; I < NB; ++I) P[I] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int q = 0; q < NKB / 2; ++q)
+#pragma unroll
+                    for (int I = 0; I < NB; ++I) P[I] = mfma_pair(ld_pair<E>(Krow + 16 * I * PK + 32 * q), Sb[q], P[I]);
+                // X = V - GX P ;  U~ = TE X
+                F2 Xb[NB / 2];
+#pragma unroll
+                for (int q = 0; q < NB / 2; ++q) {
+                    if constexpr (VEC) Xb[q] = EL::cvt2(EL::tof(vf[2 * q]) - P[2 * q], EL::tof(vf[2 * q + 1]) - P[2 * q + 1]);
+                    else Xb[q] = EL::cvt2(EL::tof(vf[2 * q]) - P[2 * q] * gx[2 * q],
+                                          EL::tof(vf[2 * q + 1]) - P[2 * q + 1] * gx[2 * q + 1]);
+                }
+#pragma unroll
+                for (int I = 0; I < NB; ++I) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                    for (int q = 0; 2 * q <= I; ++q) acc = mfma_pair(te[I][q], Xb[q], acc);
+                    U[I] = acc;
+                }
+            } else {
+                unroll<NB>([&](auto I) { U[I] = EL::tof(vf[I]); });
+            }
+            F2 Wb[NB / 2];
+#pragma unroll
+            for (int q = 0; q < NB / 2; ++q) {
+                const F2 ub = EL::cvt2(U[2 * q], U[2 * q + 1]);
+                *reinterpret_cast<F2 *>(uh + 512 * q) = ub;
+                if constexpr (VEC) Wb[q] = ub;                     // Gend is in the K*Gend tile
+                else Wb[q] = EL::cvt2(U[2 * q] * gev[2 * q], U[2 * q + 1] * gev[2 * q + 1]);
+            }
+            // S <- Gc S + (K*Gend)^T U~
+            if constexpr (VEC) {
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt) S[kt] *= gcv[kt];
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt) S[kt] *= gc;
+            }
+#pragma unroll
+            for (int q = 0; q < NB / 2; ++q)
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt)
+                    S[kt] = mfma_pair(ld_tr_pair<E>(Ktr + 32 * q * PK + KQ::col(16 * kt),
+                                                    Ktr + (32 * q + 16) * PK + KQ::col(16 * kt)), Wb[q], S[kt]);
+        }
+        if (nchunks > 0) lds_barrier();                       // barrier n
+        if (p.ht && wvalid) {
+            const int g4 = lane >> 4, r16 = lane & 15;
+            const int64_t sbase = ((int64_t)seq * H + h) * DK * DV + col0 + wcol + r16;
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) p.ht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] = S[kt][j];
+        }
+        return;
+    }
+
+    // ======================= output waves ===================================
+    // Output wave o covers token blocks rb(o, 0), rb(o, 1) ({0, 3} and {1, 2} at
+    // CH = 64, the same A tile pairs each) of every column strip of the tile.
+    // Three register sets of operands: chunk c + 2's loads are issued when chunk
+    // c's outputs start, two hand-overs before they are used.
+    constexpr int NR = NB / 2;                                 // token blocks per output wave
+    const int o = wave - NW;
+    auto rb = [&](int i) { return i == 0 ? o : NB - 1 - o; };
+    if (nchunks == 0) return;
+    const int g4 = lane >> 4, r16 = lane & 15;
+    struct Ops {
+        F2 q[NR][NKB / 2];                                     // Q rows 16 rb(i) + r, keys 32 k + 8 g .. + 7
+        F2 a[NR][NB / 2];                                      // A tile pairs (rb(i), k), 2 k <= rb(i)
+        float go[NR];
+    };
+    auto oload = [&](Ops &op, int c) __attribute__((always_inline)) {
+        c = c < nchunks ? c : nchunks - 1;                     // past the end: the last chunk again
+        const int64_t t0 = bos + (int64_t)c * CH;
+        const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+        const char *bk = blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES;
+        const E *Ab = reinterpret_cast<const E *>(bk) + CH * CH;
+        const float *gof = reinterpret_cast<const float *>(bk + CB::GOFF) + CH;
+        unroll<NR>([&](auto i) {
+            const int I = rb(i), row = 16 * I + r16;
+            // rows past the end of the sequence read its last row (not stored)
+            const E *qrow;
+            if constexpr (VEC) qrow = reinterpret_cast<const E *>(bk) + CB::TEA + CH * DK + row * DK;
+            else qrow = qg + (t0 + (row < clen ? row : clen - 1)) * sqk;
+            unroll<NKB / 2>([&](auto k) { op.q[i][k] = *reinterpret_cast<const F2 *>(qrow + 32 * k + 8 * g4); });
+            unroll<NB / 2>([&](auto k) {
+                if (2 * k <= I) op.a[i][k] = *reinterpret_cast<const F2 *>(Ab + frag_pair_pos<NB>(I, k, lane));
+            });
+            if constexpr (!VEC) op.go[i] = gof[row];
+        });
+    };
+    // O^T = S^T (GO Q)^T + U~^T A^T for chunk c: lane (g, r) ends with columns
+    // 16 s + 4 g .. + 3 of token 16 I + r.  The hand-over of every strip is read
+    // first; the NW x NR accumulators then advance together (independent MFMA
+    // chains, interleaved).
+    auto ocompute = [&](const Ops &op, int c, int z) __attribute__((always_inline)) {
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
         const bool odd = c & 1;
-        // per-lane bases; every fragment below is base + a compile-time offset
-        const E *Krow = (odd ? K1 : K0) + z + r16 * PK + 8 * g4;                 // row r, unit g
-        const E *Qrow = (odd ? Q1 : Q0) + z + r16 * PK + 8 * g4;
-        const E *Ktr = (VEC ? (odd ? KE1 : KE0) : (odd ? K1 : K0)) + z + (4 * g4 + (r16 >> 2)) * PK + 8 * (r16 & 3);
-        const E *Vtr = (odd ? V1 : V0) + z + (4 * g4 + (r16 >> 2)) * PV + wcol + 4 * (r16 & 3);
-        const char *Bst = (odd ? B1 : B0) + z;
-        const E *TEs = reinterpret_cast<const E *>(Bst) + 8 * ln, *Aqs = TEs + CH * CH;
-        // scalar gate: GX, GO, GE, Gc (ChunkBlock); VEC: Gc per key channel
-        const float *gs = reinterpret_cast<const float *>(Bst + TEAB), *go = gs + CH, *ge = gs + 2 * CH;
-        E *og = reinterpret_cast<E *>(p.o) + (int64_t)h * DV + col0 + wcol + 4 * g4;
-
-        F2 Sb[NKB / 2];
-#pragma unroll
-        for (int q = 0; q < NKB / 2; ++q) Sb[q] = EL::cvt2(S[2 * q], S[2 * q + 1]);
-        if constexpr (HS) {
-            // lane (g, r) holds rows 16 kt + 4 g .. + 3 of column col0 + wcol + r: the
-            // checkpoint's fragment order, one contiguous run per key block
-            E *hs = reinterpret_cast<E *>(p.hs) + ((cbase + c) * H + h) * (int64_t)DK * DV;
-            const int cb = (col0 + wcol) >> 4;
-#pragma unroll
-            for (int q = 0; q < NKB / 2; ++q) {
-                typedef E E4 __attribute__((ext_vector_type(4)));
-                *reinterpret_cast<E4 *>(hs + ckpt_pos<DK>(cb, 2 * q, ln)) = __builtin_shufflevector(Sb[q], Sb[q], 0, 1, 2, 3);
-                *reinterpret_cast<E4 *>(hs + ckpt_pos<DK>(cb, 2 * q + 1, ln)) =
-                    __builtin_shufflevector(Sb[q], Sb[q], 4, 5, 6, 7);
+        F2 Sn[NW][NKB / 2], Ub[NW][NB / 2];
+        unroll<NW>([&](auto s) {
+            const E *sh = SH + ((odd ? NW : 0) + s) * 16 * SP + z + r16 * SP;
+            const E *uh = UH + ((odd ? NW : 0) + s) * (NB / 2) * 512 + z + 8 * lane;
+            unroll<NKB / 2>([&](auto k) { Sn[s][k] = *reinterpret_cast<const F2 *>(sh + 32 * k + 8 * g4); });
+            unroll<NB / 2>([&](auto k) { Ub[s][k] = *reinterpret_cast<const F2 *>(uh + 512 * k); });
+        });
+        f32x4 ot[NW][NR];
+        unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] = f32x4{0.f, 0.f, 0.f, 0.f}; }); });
+        unroll<NKB / 2>([&](auto k) {
+            unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] = mfma_pair(Sn[s][k], op.q[i][k], ot[s][i]); }); });
+        });
+        if constexpr (!VEC)                                    // VEC: scale and G are in Q*G
+            unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] *= op.go[i]; }); });
+        unroll<NB / 2>([&](auto k) {
+            unroll<NW>([&](auto s) {
+                unroll<NR>([&](auto i) {
+                    if (2 * k <= rb(i)) ot[s][i] = mfma_pair(Ub[s][k], op.a[i][k], ot[s][i]);
+                });
+            });
+        });
+        unroll<NW>([&](auto s) {
+            if (col0 + 16 * s >= DV) return;
+            E *orow = reinterpret_cast<E *>(p.o) + (t0 + r16) * sv + (int64_t)h * DV + col0 + 16 * s + 4 * g4;
+            unroll<NR>([&](auto i) {
+                const int I = rb(i);
+                // convert before the lane-dependent store condition: the accumulator
+                // is read in straight-line code, not behind an exec-skip branch
+                const typename EL::frag ob = EL::cvt(ot[s][i]);
+                pin_v(ob);
+                if (16 * I + r16 < clen) *reinterpret_cast<typename EL::frag *>(orow + (int64_t)(16 * I) * sv) = ob;
+            });
+            if constexpr (HS) {
+                // the checkpoint's fragment order: lane (g, r) holds rows 16 kt + 4 g .. + 3
+                // of column 16 cb + r.  Output wave o stores key blocks o, o + 2, ..
+                const E *sh = SH + ((odd ? NW : 0) + s) * 16 * SP + z + r16 * SP;
+                E *hs = reinterpret_cast<E *>(p.hs) + ((cbase + c) * H + h) * (int64_t)DK * DV;
+                const int cb = (col0 >> 4) + s;
+                unroll<NKB / 2>([&](auto k) {
+                    const int kt = 2 * k + o;
+                    *reinterpret_cast<E4 *>(hs + ckpt_pos<DK>(cb, kt, lane)) =
+                        *reinterpret_cast<const E4 *>(sh + 16 * kt + 4 * g4);
+                });
             }
-        }
-        // V rows in C layout: U[I][j] = V[16 I + 4 g + j][wcol + r]
-        f32x4 U[NB];
-#pragma unroll
-        for (int I = 0; I < NB; ++I) U[I] = EL::tof(ld_tr<E>(Vtr + 16 * I * PV));
-
-        // ---- phase 1: everything that needs only the entry state, 2 NB independent
-        //      accumulation chains: P = K S (C layout) and OT = S^T Q^T, i.e. O^T
-        //      without its scale and intra-chunk term (lane (g, r): token 16 I + r,
-        //      columns wcol + 4 g .. + 3) -----------------------------------
-        f32x4 P[NB], OT[NB];
-#pragma unroll
-        for (int I = 0; I < NB; ++I) P[I] = OT[I] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int q = 0; q < NKB / 2; ++q) {
-#pragma unroll
-            for (int I = 0; I < NB; ++I) {
-                if constexpr (DELTA) P[I] = mfma_pair(ld_pair<E>(Krow + 16 * I * PK + 32 * q), Sb[q], P[I]);
-                OT[I] = mfma_pair(Sb[q], ld_pair<E>(Qrow + 16 * I * PK + 32 * q), OT[I]);
-            }
-        }
-
-        // ---- phase 2: X = V - (K*G) S ;  U~ = TE X ---------------------------
-        if constexpr (DELTA) {
-            F2 Xb[NB / 2];
-#pragma unroll
-            for (int q = 0; q < NB / 2; ++q) {
-                if constexpr (VEC) Xb[q] = EL::cvt2(U[2 * q] - P[2 * q], U[2 * q + 1] - P[2 * q + 1]);
-                else Xb[q] = EL::cvt2(U[2 * q] - P[2 * q] * ld4(gs + 32 * q + 4 * g4),
-                                      U[2 * q + 1] - P[2 * q + 1] * ld4(gs + 32 * q + 16 + 4 * g4));
-            }
-#pragma unroll
-            for (int I = 0; I < NB; ++I) {
-                f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int q = 0; 2 * q <= I; ++q)
-                    acc = mfma_pair(ld_pair<E>(TEs + frag_pair_pos<NB>(I, q, 0)), Xb[q], acc);
-                U[I] = acc;
-            }
-        }
-        F2 Ub[NB / 2], Wb[NB / 2];
-#pragma unroll
-        for (int q = 0; q < NB / 2; ++q) {
-            Ub[q] = EL::cvt2(U[2 * q], U[2 * q + 1]);
-            if constexpr (VEC) Wb[q] = Ub[q];                   // Gend is in the K*Gend tile
-            else Wb[q] = EL::cvt2(U[2 * q] * ld4(ge + 32 * q + 4 * g4), U[2 * q + 1] * ld4(ge + 32 * q + 16 + 4 * g4));
-        }
-
-        // ---- phase 3: O^T = scale G (.) OT + U~^T A^T, stored directly;
-        //      S <- Gc S + (K*Gend)^T U~ -----------------------------------------
-#pragma unroll
-        for (int I = 0; I < NB; ++I) {
-            if constexpr (!VEC) OT[I] *= go[16 * I + r16];              // VEC: scale and G are in Q*G
-#pragma unroll
-            for (int q = 0; 2 * q <= I; ++q)
-                OT[I] = mfma_pair(Ub[q], ld_pair<E>(Aqs + frag_pair_pos<NB>(I, q, 0)), OT[I]);
-        }
-        if constexpr (VEC) {
-#pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) S[kt] *= ld4(gs + 16 * kt + 4 * g4);    // Gc per key channel
-        } else {
-            const float gc = gs[3 * CH];
-#pragma unroll
-            for (int kt = 0; kt < NKB; ++kt) S[kt] *= gc;
-        }
-#pragma unroll
-        for (int q = 0; q < NB / 2; ++q)
-#pragma unroll
-            for (int kt = 0; kt < NKB; ++kt)
-                S[kt] = mfma_pair(ld_tr_pair<E>(Ktr + 32 * q * PK + KQ::col(16 * kt),
-                                                Ktr + (32 * q + 16) * PK + KQ::col(16 * kt)), Wb[q], S[kt]);
-        E *orow = og + (t0 + r16) * sv;                          // token t0 + 16 I + r: orow + 16 I sv
-#pragma unroll
-        for (int I = 0; I < NB; ++I) {
-            // convert before the lane-dependent store condition: the accumulator
-            // is read in straight-line code, not behind an exec-skip branch
-            const typename EL::frag ob = EL::cvt(OT[I]);
-            pin_v(ob);
-            if (16 * I + r16 < clen) *reinterpret_cast<typename EL::frag *>(orow + (int64_t)(16 * I) * sv) = ob;
-        }
+        });
+    };
+    Ops o0, o1, o2;
+    oload(o0, 0);
+    oload(o1, 1);
+    lds_barrier();                                            // barrier 0
+    int c = 0;
+    for (; c + 2 < nchunks; c += 3) {
+        int z;
+        oload(o2, c + 2);
+        z = opaque_s(0);
+        lds_barrier();                                        // barrier c + 1: chunk c's hand-over
+        ocompute(o0, c, z);
+        oload(o0, c + 3);
+        z = opaque_s(0);
+        lds_barrier();
+        ocompute(o1, c + 1, z);
+        oload(o1, c + 4);
+        z = opaque_s(0);
+        lds_barrier();
+        ocompute(o2, c + 2, z);
     }
-
-    if (p.ht && wvalid) {
-        const int g4 = lane >> 4, r16 = lane & 15;
-        const int64_t sbase = ((int64_t)seq * H + h) * DK * DV + col0 + wcol + r16;
-#pragma unroll
-        for (int kt = 0; kt < NKB; ++kt)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) p.ht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] = S[kt][j];
+    if (c < nchunks) {
+        const int z = opaque_s(0);
+        lds_barrier();
+        ocompute(o0, c, z);
     }
+    if (c + 1 < nchunks) {
+        const int z = opaque_s(0);
+        lds_barrier();
+        ocompute(o1, c + 1, z);
+    }
+    __builtin_amdgcn_s_waitcnt(0);                            // no load left in flight at exit
 }
 
 // ===========================================================================
@@ -1387,28 +1503,33 @@ chunk_state_tr_kernel(const ChunkParams p) {
 // then emitted reads of that MFMA's accumulators without the required wait
 // states (wrong outputs in token block 3).  Without the join there is no
 // such read.
+template <int DK, int CH, typename E, bool VEC, bool DELTA, bool HS>
+static void launch_pipe(const ChunkParams &p, int nw, int64_t state_blocks, hipStream_t stream) {
+    const dim3 grid((unsigned)state_blocks);
+    if constexpr (!VEC) {
+        if (nw == 4) {
+            hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 4, 2, E, VEC, DELTA, HS>), grid, dim3(64 * 8), 0, stream, p);
+            return;
+        }
+    }
+    if (nw == 2)
+        hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 2, 4, E, VEC, DELTA, HS>), grid, dim3(64 * 8), 0, stream, p);
+    else
+        hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 1, 4, E, VEC, DELTA, HS>), grid, dim3(64 * 7), 0, stream, p);
+}
+
 template <int DK, int CH, typename E, int GATE, bool DELTA>
 static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hipStream_t stream) {
     if constexpr (sizeof(E) == 2) {
-        // 16-bit elements: the transpose-read kernel, 8 waves in all
+        // 16-bit elements: the pipelined kernel (chain, output and producer waves)
         constexpr bool VEC = GATE == 2;
         if constexpr (!VEC && DELTA) {
             if (p.hs) {                                       // a training forward: entry states saved
-                if (nw == 4)
-                    hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, false, true, true>),
-                                       dim3((unsigned)state_blocks), dim3(64 * 8), 0, stream, p);
-                else
-                    hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 6, E, false, true, true>),
-                                       dim3((unsigned)state_blocks), dim3(64 * 8), 0, stream, p);
+                launch_pipe<DK, CH, E, false, true, true>(p, nw, state_blocks, stream);
                 return;
             }
         }
-        if (nw == 4)
-            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 4, 4, E, VEC, DELTA>), dim3((unsigned)state_blocks),
-                               dim3(64 * 8), 0, stream, p);
-        else
-            hipLaunchKernelGGL((chunk_state_tr_kernel<DK, CH, 2, 6, E, VEC, DELTA>), dim3((unsigned)state_blocks),
-                               dim3(64 * 8), 0, stream, p);
+        launch_pipe<DK, CH, E, VEC, DELTA, false>(p, nw, state_blocks, stream);
         return;
     } else {
     if constexpr (StateLayout<DK, CH, 4, E, GATE>::FITS) {
@@ -1452,10 +1573,16 @@ static hipError_t launch_chunk(const ChunkParams &p, int nw, int phases, hipStre
 
 template <int DK, int CH, typename E, int GATE>
 static int state_waves(int64_t units, int dv, int cus) {
-    // 64-column tiles once the (sequence, head) pairs fill the chip and the tile fits LDS
-    // (the 16-bit kernel's tiles always fit)
-    if (sizeof(E) == 4 && !StateLayout<DK, CH, 4, E, GATE>::FITS) return 2;
-    return units * ((dv + 63) / 64) >= cus ? 4 : 2;
+    if constexpr (sizeof(E) == 2) {
+        // the widest tile (16 nw columns) that still gives every CU a workgroup;
+        // 64-column tiles only with the scalar gate (the per-channel tiles overflow LDS)
+        if (GATE != 2 && units * ((dv + 63) / 64) >= cus) return 4;
+        return units * ((dv + 31) / 32) >= cus ? 2 : 1;
+    } else {
+        // fp32: 64-column tiles once the (sequence, head) pairs fill the chip and the tile fits LDS
+        if (!StateLayout<DK, CH, 4, E, GATE>::FITS) return 2;
+        return units * ((dv + 63) / 64) >= cus ? 4 : 2;
+    }
 }
 
 int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H, int64_t dk, int gate_vector) {

@@ -33,8 +33,9 @@ __device__ __forceinline__ int frag_pos(int I, int kb, int lane) {
 //       (for the state update; 0 past a partial chunk's end), CH floats each,
 //       then Gc = exp(gamma_C) and three floats of padding;
 //   per-channel gate, 16-bit elements (VEC): the gated tiles K*G, scale Q*G and
-//       K*Gend (CH x DK each, element type, rows in the paired-column order of
-//       KQRows, unpadded), then Gc = exp(gamma_C) (DK floats).
+//       K*Gend (CH x DK each, element type, unpadded rows; K*G and K*Gend in the
+//       paired-column order of KQRows, scale Q*G in natural column order), then
+//       Gc = exp(gamma_C) (DK floats).
 // Blocks are 16-byte multiples.
 template <typename E, int CH, int DK, int GATE>
 struct ChunkBlock {
