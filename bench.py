@@ -346,11 +346,12 @@ TRAFFIC_SOURCES = {
     'chunk_prep': ('gdr_chunk.hip', 'gdr_chunk_layout.hpp', 'gdr_common.hpp', 'gdr_kernels.hpp'),
     'recurrent': ('gdr_recurrent.hip', 'gdr_common.hpp', 'gdr_kernels.hpp'),
 }
-# (workload, kernel) -> the kernel-name prefix rocprofv3 reports for it
+# (workload, kernel) -> substrings of the name rocprofv3 reports for it
+# (demangled, or mangled where the demangler gives up on a __bf16 argument)
 TRAFFIC_KERNELS = {
-    ('gdn_340m', 'chunk_state'): 'vgdr::chunk_pipe_kernel<128, 64, 2',
-    ('gdn_340m', 'chunk_prep'): 'vgdr::chunk_prep_kernel<128, 64',
-    ('decode_b64_h16', 'recurrent'): 'vgdr::recurrent_kernel<128, 128',
+    ('gdn_340m', 'chunk_state'): ('vgdr::chunk_pipe_kernel<128, 64, 2,', 'chunk_pipe_kernelILi128ELi64ELi2E'),
+    ('gdn_340m', 'chunk_prep'): ('vgdr::chunk_prep_kernel<128, 64,', 'chunk_prep_kernelILi128ELi64E'),
+    ('decode_b64_h16', 'recurrent'): ('vgdr::recurrent_kernel<128, 128,', 'recurrent_kernelILi128ELi128E'),
 }
 
 
@@ -398,10 +399,10 @@ def write_traffic(run_dir):
                 vals.setdefault(row['Kernel_Name'], []).append(float(row['Counter_Value']))
         return {k: sum(v) / len(v) for k, v in vals.items()}
 
-    def pick(table, prefix):
-        hits = [v for k, v in table.items() if k.startswith(prefix) or ('void ' + prefix) in k]
+    def pick(table, names):
+        hits = [v for k, v in table.items() if any(n in k for n in names)]
         if not hits:
-            raise SystemExit(f'no kernel {prefix} in the counters')
+            raise SystemExit(f'no kernel {names[0]} in the counters')
         return hits[0]
 
     copy_bytes = 1 << 30
@@ -410,13 +411,13 @@ def write_traffic(run_dir):
     fs, ws = copy_bytes / 1024 / cf, copy_bytes / 1024 / cw
     out = {'calibration': {'copy_fetch_KiB': cf, 'copy_write_KiB': cw, 'fetch_scale': round(fs, 4),
                            'write_scale': round(ws, 4)}}
-    for (wl, kern), prefix in TRAFFIC_KERNELS.items():
+    for (wl, kern), names in TRAFFIC_KERNELS.items():
         sub = 'decode' if kern == 'recurrent' else 'prefill'
-        f_kib = pick(per_kernel(sub, 'FETCH_SIZE'), prefix)
-        w_kib = pick(per_kernel(sub, 'WRITE_SIZE'), prefix)
+        f_kib = pick(per_kernel(sub, 'FETCH_SIZE'), names)
+        w_kib = pick(per_kernel(sub, 'WRITE_SIZE'), names)
         rd, wr = f_kib * 1024 * fs, w_kib * 1024 * ws
         out.setdefault(wl, {})[kern] = {'bytes_per_launch': int(rd + wr), 'read_bytes': int(rd), 'write_bytes': int(wr),
-                                        'fetch_KiB': f_kib, 'write_KiB': w_kib, 'kernel': prefix,
+                                        'fetch_KiB': f_kib, 'write_KiB': w_kib, 'kernel': names[0],
                                         'sources_sha': sources_sha(kern)}
     path = os.path.join(ROOT, 'profiles', 'traffic.json')
     with open(path, 'w') as f:
@@ -430,7 +431,9 @@ def main():
     ap.add_argument('--steps', type=int, default=60)
     ap.add_argument('--warmup', type=int, default=100)
     ap.add_argument('--no-cpu-baseline', action='store_true')
-    ap.add_argument('--prefill-only', action='store_true', help='only the headline prefill (for profiling)')
+    ap.add_argument('--prefill-only', nargs='?', const='gdn_340m', default=None, metavar='WORKLOAD',
+                    help='only one prefill workload: gdn_340m (default, the headline line), kda_prefill or '
+                         'gdn_varlen (for profiling)')
     ap.add_argument('--decode-only', action='store_true', help='only the decode step (for profiling)')
     ap.add_argument('--layer-only', action='store_true',
                     help='only the short conv, output epilogue and fused decode step (for profiling)')
@@ -475,6 +478,13 @@ def main():
     if args.decode_only:
         dec = bench_decode(torch, ops, workloads, args.steps, args.warmup)
         print(json.dumps({'decode_us_per_layer': round(dec['avg_us'], 2), 'achieved_GBs': round(dec['GBs'], 1)}),
+              flush=True)
+        return
+    if args.prefill_only and args.prefill_only != 'gdn_340m':
+        r = bench_prefill(torch, ops, workloads, args.prefill_only, args.steps, args.warmup)
+        print(json.dumps({'workload': args.prefill_only, 'tok_s': round(r['tok_s'], 1),
+                          'prep_ms': round(r['prep_ms'], 4), 'state_ms': round(r['state_ms'], 4),
+                          'path_tflops': round(r['path_tflops'], 2), 'state_tflops': round(r['state_tflops'], 2)}),
               flush=True)
         return
     log('[bench] prefill gdn_340m')
