@@ -42,6 +42,11 @@ Also reported on the same line:
                 2 x 180,224 FLOP per token-head (chunk_scan_flops counts
                 forward + backward as 3 x the forward); and the training pair
                 (saving forward + saved backward) against 3 x 180,224
+  generation    the 1.3B-shape GDN LM (24 layers, d2048, vocab 32000, bf16):
+                ragged prefill of 64 prompts U[64, 2048], then 256 greedy
+                decode steps replayed from a HIP graph: prefill tok/s,
+                generated tok/s, per-step time and the step's bytes (states
+                132,104 B per sequence-head-layer, plus the weights) per second
   kda, varlen   KDA prefill (B=4 T=8192 H=8) and packed GDN prefill (32
                 segments U[128, 8192], H=16) tokens/s and TFLOP/s
   cpu_baseline  the oracle's torch fp32 chunk form (the reference's CPU path)
@@ -162,6 +167,53 @@ def bench_decode(torch, ops, workloads, steps, warmup, B=64, H=16, layers=24):
     byts = B * H * DECODE_BYTES_PER_SEQ_HEAD
     del graph, states
     return dict(avg_us=per_layer_ms * 1e3, GBs=byts / (per_layer_ms * 1e-3) / 1e9, bytes=byts)
+
+
+def bench_generate(torch, workloads, reps=2):
+    """The 1.3B-shape GDN language model (gdn_lm_1p3b: 24 layers, d2048, H16
+    dk=dv=128, vocab 32000, bf16, random init): ragged prefill of its 64
+    prompts (every prompt but its last token, one packed call per kernel),
+    then 256 greedy decode steps for all 64 streams, each step (embedding,
+    24 layers of projections, fused conv + recurrence + epilogue kernel and
+    FFN, the tied head, the argmax) replayed from one HIP graph.  Host-clock
+    timing around each phase, synchronised; the best of `reps` runs after a
+    warm-up run that records the graph."""
+    from vagus_amd.model import RaggedGenerator
+    m, prompts, new = workloads.lm_workload('gdn_lm_1p3b')
+    gen = RaggedGenerator(m)
+    gen.prefill(prompts)
+    gen.generate(4)
+    torch.cuda.synchronize()
+    best = None
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        gen.prefill(prompts)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        toks = gen.generate(new)
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        if best is None or t2 - t0 < best[2] - best[0]:
+            best = (t0, t1, t2)
+    t0, t1, t2 = best
+    c = m.config
+    N = len(prompts)
+    fed = sum(p.numel() - 1 for p in prompts)
+    step_s = (t2 - t1) / new
+    state_bytes = N * c['head_count'] * c['layer_count'] * DECODE_BYTES_PER_SEQ_HEAD
+    weight_bytes = sum(p.numel() * p.element_size() for p in m.parameters())
+    assert toks.shape == (N, new) and int(toks.min()) >= 0 and int(toks.max()) < c['vocab_size']
+    del gen, m
+    return {'workload': 'gdn_lm_1p3b: 24-layer GDN LM, d2048 H16 dk=dv=128, vocab 32000, bf16, random init; '
+                        f'{N} prompts U[64, 2048] ({fed + N} tokens), ragged prefill, {new} greedy steps',
+            'prefill_ms': round((t1 - t0) * 1e3, 2), 'prefill_tok_s': round(fed / (t1 - t0), 1),
+            'decode_ms': round((t2 - t1) * 1e3, 2), 'decode_step_ms': round(step_s * 1e3, 4),
+            'gen_tok_s': round(N * new / (t2 - t1), 1),
+            'decode_state_bytes_per_step': state_bytes, 'decode_weight_bytes_per_step': weight_bytes,
+            'decode_state_GBs': round(state_bytes / step_s / 1e9, 1),
+            'decode_total_GBs': round((state_bytes + weight_bytes) / step_s / 1e9, 1),
+            'decode_total_frac_hbm': round((state_bytes + weight_bytes) / step_s / 1e9 / PEAK_HBM_GBS, 4),
+            'end_to_end_s': round(t2 - t0, 4)}
 
 
 def _event_us(torch, fn, steps, warmup):
@@ -438,6 +490,8 @@ def main():
     ap.add_argument('--layer-only', action='store_true',
                     help='only the short conv, output epilogue and fused decode step (for profiling)')
     ap.add_argument('--backward-only', action='store_true', help='only the chunked backward (for profiling)')
+    ap.add_argument('--generate-only', action='store_true',
+                    help='only the 1.3B-shape LM generation (ragged prefill + 256 graph-replayed decode steps)')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a plain 1 GiB device copy (x5): the reference point that scales '
                          'rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes')
@@ -467,6 +521,9 @@ def main():
         print(json.dumps({'calibrate_copy_bytes': src.numel() * 4, 'launches': 5}), flush=True)
         return
 
+    if args.generate_only:
+        print(json.dumps(bench_generate(torch, workloads)), flush=True)
+        return
     if args.backward_only:
         print(json.dumps(bench_backward(torch, ops, workloads, args.steps, args.warmup)), flush=True)
         print(json.dumps(bench_scan_backward(torch, ops, workloads, max(3, args.steps // 3), max(2, args.warmup // 3))),
@@ -504,6 +561,8 @@ def main():
         extra['backward'] = bench_backward(torch, ops, workloads, max(5, args.steps // 4), max(3, args.warmup // 10))
         log('[bench] backward kda_prefill (token walk)')
         extra['kda_backward'] = bench_scan_backward(torch, ops, workloads, 3, 1)
+        log('[bench] generation gdn_lm_1p3b')
+        extra['generation'] = bench_generate(torch, workloads)
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
             r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))

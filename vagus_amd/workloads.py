@@ -9,6 +9,11 @@ The shapes and distributions are the benchmark's:
                 gate (B, T, H, dk), zero entry state, final states returned
     gdn_varlen  packed GDN prefill, bf16, 32 segments with lengths uniform in
                 [128, 8192], H=16 dk=dv=128, zero entry states
+    gdn_lm_1p3b greedy generation with the 1.3B-shape GDN language model
+                (24 layers, hidden 2048, H=16 dk=dv=128, vocab 32000, scalar
+                gate, bf16 weights, random init): 64 prompts with token ids
+                uniform over the vocabulary and lengths uniform in [64, 2048],
+                ragged prefill, then 256 decode steps (lm_workload)
 
 Distributions (all from one torch.Generator seeded with the workload's seed,
 drawn in the order below): q, k ~ N(0, 1) then L2-normalised per head;
@@ -34,6 +39,13 @@ WORKLOADS = {
                         s0_scale=None, seed=2),
     'gdn_varlen': dict(n_seqs=32, len_lo=128, len_hi=8192, H=16, dk=128, dv=128, gate='scalar',
                        dtype=torch.bfloat16, s0_scale=None, seed=3),
+}
+
+
+LM_WORKLOADS = {
+    'gdn_lm_1p3b': dict(model=dict(vocab_size=32000, dim=2048, layer_count=24, head_count=16, key_head_dim=128,
+                                   value_head_dim=128, gate='scalar', short_conv_size=4, chunk_size=64),
+                        dtype=torch.bfloat16, n_prompts=64, len_lo=64, len_hi=2048, new_tokens=256, seed=4),
 }
 
 
@@ -117,3 +129,25 @@ def workload(name: str, device='cpu') -> ScanInputs:
                                   s0_scale=w['s0_scale'], seed=w['seed'], device=device)
     return make_inputs(w['B'], w['T'], w['H'], w['dk'], w['dv'], gate=w['gate'], dtype=w['dtype'],
                        s0_scale=w['s0_scale'], seed=w['seed'], device=device)
+
+
+def lm_prompts(n: int, lo: int, hi: int, vocab: int, seed: int) -> list[torch.Tensor]:
+    """n prompts with lengths uniform in [lo, hi] and token ids uniform in
+    [0, vocab), from `seed` (CPU int64)."""
+    gen = torch.Generator('cpu').manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (n,), generator=gen).tolist()
+    return [torch.randint(0, vocab, (m,), generator=gen) for m in lens]
+
+
+def lm_workload(name: str, device='cuda'):
+    """(model, prompts, new_tokens) of a generation workload: the GDNLM built
+    on `device` from the workload's seed (random init, in its dtype, eval
+    mode) and its prompts."""
+    from .model import GDNLM
+    w = LM_WORKLOADS[name]
+    torch.manual_seed(w['seed'])
+    with torch.device(device):
+        m = GDNLM(**w['model'])
+    m = m.to(w['dtype']).eval()
+    prompts = lm_prompts(w['n_prompts'], w['len_lo'], w['len_hi'], w['model']['vocab_size'], w['seed'])
+    return m, prompts, w['new_tokens']
