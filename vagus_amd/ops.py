@@ -669,15 +669,16 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
     if dv > max(_REC_DVS):
         # the recurrence is column-separable: independent 128-wide column blocks
         outs, states = [], []
+        want_S = output_final_state or (inplace_final_state and initial_state is not None)
         for c0 in range(0, dv, 128):
             sl = slice(c0, min(dv, c0 + 128))
             s0 = None if initial_state is None else initial_state[..., sl]
             o_, s_ = _recurrent(q, k, v[..., sl], g, beta, gate=gate, delta=delta, scale=scale,
-                                initial_state=s0, output_final_state=output_final_state,
+                                initial_state=s0, output_final_state=want_S,
                                 cu_seqlens=cu_seqlens, fusion=fusion, w=w)
             outs.append(o_)
             states.append(s_)
-        S = torch.cat(states, -1) if output_final_state else None
+        S = torch.cat(states, -1) if want_S else None
         if inplace_final_state and initial_state is not None:
             initial_state.copy_(S)
             S = initial_state
