@@ -234,20 +234,41 @@ def bench_layer_kernels(torch, ops, workloads, steps, warmup):
     """The layer's other kernels at the 340M shape (B8 T4096 H8 dk=dv=128):
     the short conv + SiLU over one projection (D = 1024, K = 4) and the
     RMSNorm x SiLU(gate) output epilogue, each over three rotating input
-    copies; and the fused decode step (conv + SiLU with its caches, L2 norm,
+    copies, 24 calls replayed from a HIP graph; and the fused decode step (conv + SiLU with its caches, L2 norm,
     beta sigmoid, recurrence, epilogue) at the decode shape (B64 H16), 24
     rotating layers replayed from a HIP graph."""
     import torch.nn.functional as F
     g = torch.Generator(device='cpu').manual_seed(11)
     B, T, H, D, K = 8, 4096, 8, 128, 4
+
+    def graph_us(fn, calls):
+        # `calls` launches captured in one HIP graph and replayed: the kernels run back to
+        # back, without the host's per-call time (longer than these kernels) between them
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(calls):
+                fn(i)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(calls):
+                fn(i)
+        _, ms = time_steps(torch, lambda i: graph.replay(), max(3, steps // 3), max(2, warmup // 2), 1)
+        del graph
+        return statistics.mean(ms) / calls * 1e3
+
     xs = [torch.randn(B, T, H * D, generator=g).bfloat16().cuda() for _ in range(3)]
     w = (0.5 * torch.randn(H * D, 1, K, generator=g)).cuda()
-    conv_us = _event_us(torch, lambda i: ops.causal_conv1d(xs[i % 3], w, activation='silu'), steps, warmup)
+    # the weights in the module's dtype (a bf16 layer's ShortConv), and fp32 weights
+    wb = w.bfloat16()
+    conv_us = graph_us(lambda i: ops.causal_conv1d(xs[i % 3], wb, activation='silu'), 24)
+    conv32_us = graph_us(lambda i: ops.causal_conv1d(xs[i % 3], w, activation='silu'), 24)
     conv_bytes = 2 * B * T * H * D * 2
     os_ = [torch.randn(B, T, H, D, generator=g).bfloat16().cuda() for _ in range(3)]
     gs = [torch.randn(B, T, H, D, generator=g).bfloat16().cuda() for _ in range(3)]
     gamma = (torch.rand(D, generator=g) + 0.5).bfloat16().cuda()
-    ng_us = _event_us(torch, lambda i: ops.rms_norm_gated(os_[i % 3], gs[i % 3], gamma), steps, warmup)
+    ng_us = graph_us(lambda i: ops.rms_norm_gated(os_[i % 3], gs[i % 3], gamma), 24)
     ng_bytes = 3 * B * T * H * D * 2
     del xs, os_, gs
     # decode: every producer and the epilogue fused, 24 layers
@@ -282,9 +303,11 @@ def bench_layer_kernels(torch, ops, workloads, steps, warmup):
     dec_bytes = Bd * Hd * (DECODE_BYTES_PER_SEQ_HEAD + 3 * 2 * K * D * 2 + D * 2)
     del graph, states, caches
     return {
-        'short_conv': {'workload': 'causal_conv1d + SiLU, B8 T4096 D1024 K4 bf16', 'us': round(conv_us, 2),
+        'short_conv': {'workload': 'causal_conv1d + SiLU, B8 T4096 D1024 K4 bf16, bf16 weights', 'us': round(conv_us, 2),
                        'achieved_GBs': round(conv_bytes / conv_us / 1e3, 1),
-                       'frac_hbm': round(conv_bytes / conv_us / 1e3 / PEAK_HBM_GBS, 4)},
+                       'frac_hbm': round(conv_bytes / conv_us / 1e3 / PEAK_HBM_GBS, 4),
+                       'us_fp32_weights': round(conv32_us, 2),
+                       'frac_hbm_fp32_weights': round(conv_bytes / conv32_us / 1e3 / PEAK_HBM_GBS, 4)},
         'output_epilogue': {'workload': 'rms_norm_gated, B8 T4096 H8 dv128 bf16', 'us': round(ng_us, 2),
                             'achieved_GBs': round(ng_bytes / ng_us / 1e3, 1),
                             'frac_hbm': round(ng_bytes / ng_us / 1e3 / PEAK_HBM_GBS, 4)},

@@ -186,12 +186,6 @@ __device__ __forceinline__ void dma_flat(E *lds, const E *src, int tid) {
 
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
-// Workgroup barrier that orders LDS traffic only: waits for this wave's LDS
-// operations, then s_barrier.  Unlike __syncthreads() it does not wait for
-// outstanding global memory operations, so an asynchronous copy into the other
-// double-buffer slot keeps flowing across it.  The memory clobber stops the
-// compiler from moving memory accesses across the barrier.
-__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ===========================================================================
 // chunk_prep_kernel: per (chunk, head) TE and A

@@ -159,6 +159,31 @@ __device__ __forceinline__ f32x4 exp4(f32x4 x) {
 
 template <typename T> __host__ __device__ constexpr T cmax(T a, T b) { return a > b ? a : b; }
 
+// Workgroup barrier that orders LDS traffic only: waits for this wave's LDS
+// operations, then s_barrier.  Unlike __syncthreads() it does not wait for
+// outstanding global memory operations, so loads still in flight (an
+// asynchronous copy into the other double-buffer slot, a state tile) keep
+// flowing across it.  The memory clobber stops the compiler from moving memory
+// accesses across the barrier.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Buffer access to one contiguous block [base, base + bytes): a load or store
+// takes a 32-bit per-lane offset and a scalar offset instead of a 64-bit address
+// per lane (two VGPRs per access in flight), and an access outside the block
+// reads zeros or is dropped.  The resource's last word is the gfx9 format word;
+// CPOL_NT is the non-temporal bit of the cache policy (gfx94x, gfx950).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr int CPOL_NT = 2;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ f32x4 buffer_load_nt4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, CPOL_NT));
+}
+__device__ __forceinline__ void buffer_store_nt4(f32x4 x, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, (int)voff, (int)soff, CPOL_NT);
+}
+
 // the reference's producer activations (linear_attention.py:703-706, :719-736)
 // 1 / (1 + e^-x) with the hardware reciprocal (v_rcp_f32, about 1 ulp): an IEEE
 // division costs a dozen instructions, which made the SiLU of the streaming

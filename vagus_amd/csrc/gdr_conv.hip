@@ -4,13 +4,19 @@
 // token; here it is one HBM pass over x.
 //
 // A thread owns VE = 16 / sizeof(E) consecutive channels (one 16-byte unit)
-// for a run of RUN consecutive tokens, so a wavefront reads 64 neighbouring
-// units of one token row per load.  The K - 1 inputs before the current token
-// stay in registers as a sliding window: each input unit is loaded once per
-// run (plus K - 1 at the run's start).  Inputs before a sequence's first token
-// come from its conv cache [K, D] (the previous call's last K inputs,
-// linear_attention.py:929-941) or are zero; a run that crosses into the next
-// packed segment restarts its window there.
+// for a run of RUN = 8 consecutive tokens, so a wavefront reads 64 neighbouring
+// units of one token row per load.  The run's K - 1 + RUN input rows are all
+// loaded before any arithmetic and kept as loaded (16-bit values unconverted),
+// which keeps a thread within 128 VGPRs and so the whole grid of a 340M-shaped
+// projection (B8 T4096 D1024: 4096 waves) resident at once.  Each input unit is
+// loaded once per run plus K - 1 times at the run's start (those hit in cache).
+// Inputs before a sequence's first token come from its conv cache [K, D] (the
+// previous call's last K inputs, linear_attention.py:929-941) or are zero; a run
+// that crosses into the next packed segment goes token by token and restarts its
+// window there.  Measured at that shape: RUN 16 (occupancy 3) 25.2 us, RUN 8
+// 23.2 us, RUN 4 26.7 us; a plain copy of the same bytes 22.2 us.
+#include <type_traits>
+
 #include "gdr_common.hpp"
 #include "gdr_kernels.hpp"
 
@@ -18,23 +24,7 @@ namespace vgdr {
 
 namespace {
 
-constexpr int RUN = 16;
-
-template <typename E>
-struct Unit {
-    static constexpr int VE = 16 / (int)sizeof(E);
-    typedef E V __attribute__((ext_vector_type(VE)));
-    float f[VE];
-    __device__ __forceinline__ void load(const E *p) {
-        const V v = *reinterpret_cast<const V *>(p);
-#pragma unroll
-        for (int e = 0; e < VE; ++e) f[e] = (float)v[e];
-    }
-    __device__ __forceinline__ void zero() {
-#pragma unroll
-        for (int e = 0; e < VE; ++e) f[e] = 0.f;
-    }
-};
+constexpr int RUN = 8;
 
 __device__ __forceinline__ int64_t clamp_tok(int32_t c, int64_t n_tokens) {
     return c < 0 ? 0 : (c > n_tokens ? n_tokens : c);
@@ -50,15 +40,46 @@ __device__ __forceinline__ int seg_at(const int32_t *cu, int n, int64_t n_tokens
     return lo;
 }
 
+// the segment holding token t: its index and token range (dense: sequences of T
+// tokens; packed: the cu_seqlens entry, clamped; no segments: an empty range)
+struct Seg {
+    int seq;
+    int64_t bos, eos;
+};
+__device__ __forceinline__ Seg seg_of(const ConvParams &p, int64_t t) {
+    if (p.cu && p.n_seqs == 0) return Seg{0, 0, 0};
+    if (p.cu) {
+        const int s = seg_at(p.cu, p.n_seqs, p.n_tokens, t);
+        return Seg{s, clamp_tok(p.cu[s], p.n_tokens), clamp_tok(p.cu[s + 1], p.n_tokens)};
+    }
+    // (32-bit division where the tokens allow it: a 64-bit one is a long VALU sequence
+    // ahead of every load of the run)
+    const int s = p.n_tokens <= 0x7fffffff ? (int)((uint32_t)t / (uint32_t)p.T) : (int)(t / p.T);
+    return Seg{s, (int64_t)s * p.T, (int64_t)s * p.T + p.T};
+}
+
 }  // namespace
 
-template <typename E, int K>
+// WT: the weights' type (fp32 or E); WV: the weights are 16-byte aligned, so a
+// thread's VE x K block (contiguous, 16 * K or 32 * K bytes) is read with 16-byte loads
+template <typename E, typename WT, int K, bool WV>
 __global__ void __launch_bounds__(256) causal_conv_kernel(const ConvParams p) {
-    using U = Unit<E>;
-    constexpr int VE = U::VE;
+    constexpr int VE = 16 / (int)sizeof(E);
+    typedef E V __attribute__((ext_vector_type(VE)));
     const int64_t ncg = p.D / VE;
+    // (consecutive workgroups run on different XCDs, so about half of the window rows
+    // are fetched from HBM a second time; renumbering the workgroups so that each XCD
+    // streams one contiguous range measured slower, 24.5 against 23.3 us)
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    const int64_t cg = gid % ncg, run = gid / ncg;
+    int64_t cg, run;
+    if (gridDim.x <= (1u << 24)) {           // gid < 2^32: 32-bit division
+        const uint32_t g = (uint32_t)gid, n = (uint32_t)ncg;
+        cg = g % n;
+        run = g / n;
+    } else {
+        cg = gid % ncg;
+        run = gid / ncg;
+    }
     const int64_t t0 = run * RUN;
     if (t0 >= p.n_tokens) return;
     const int64_t c0 = cg * VE;
@@ -66,85 +87,85 @@ __global__ void __launch_bounds__(256) causal_conv_kernel(const ConvParams p) {
     const E *st = reinterpret_cast<const E *>(p.state_in);
     E *y = reinterpret_cast<E *>(p.y);
 
-    float w[K][VE];
-#pragma unroll
-    for (int e = 0; e < VE; ++e)
-#pragma unroll
-        for (int j = 0; j < K; ++j)
-            w[j][e] = p.w_f32 ? reinterpret_cast<const float *>(p.w)[(c0 + e) * K + j]
-                              : (float)reinterpret_cast<const E *>(p.w)[(c0 + e) * K + j];
+    // weights w[c][j] of channels c0..c0+VE-1 as loaded: wb[e * K + j]
+    WT wb[VE * K];
+    const WT *wsrc = reinterpret_cast<const WT *>(p.w) + c0 * K;
+    if constexpr (WV) {
+        typedef uint32_t U4 __attribute__((ext_vector_type(4)));
+        constexpr int N16 = VE * K * (int)sizeof(WT) / 16;
+        static_assert(VE * K * (int)sizeof(WT) % 16 == 0, "weight block");
+        unroll<N16>([&](auto i) __attribute__((always_inline)) {
+            const U4 u = reinterpret_cast<const U4 *>(wsrc)[decltype(i)::value];
+            __builtin_memcpy(reinterpret_cast<char *>(wb) + 16 * decltype(i)::value, &u, 16);
+        });
+    } else {
+        unroll<VE * K>([&](auto i) __attribute__((always_inline)) { wb[i] = wsrc[decltype(i)::value]; });
+    }
 
-    int seq = 0;
-    int64_t bos = 0, eos = 0;                // no segment located yet
-    auto locate = [&](int64_t t) __attribute__((always_inline)) {
-        if (p.cu && p.n_seqs == 0) {
-            bos = eos = 0;                   // no segments: every token is outside
-        } else if (p.cu) {
-            seq = seg_at(p.cu, p.n_seqs, p.n_tokens, t);
-            bos = clamp_tok(p.cu[seq], p.n_tokens);
-            eos = clamp_tok(p.cu[seq + 1], p.n_tokens);
-        } else {
-            seq = (int)(t / p.T);
-            bos = (int64_t)seq * p.T;
-            eos = bos + p.T;
-        }
+    // the input row at pos of segment sg (pos < bos: its cache, or zeros).  Branch-free:
+    // the load is from x, the cache or (for zeros) row bos of x, and the zeros are
+    // selected afterwards; a branch around each load would make the wave wait for it
+    // where the branches join.
+    auto row = [&](const Seg &sg, int64_t pos) __attribute__((always_inline)) -> V {
+        const bool in = pos >= sg.bos;
+        const E *src = in   ? x + pos * p.D + c0
+                       : st ? st + ((int64_t)sg.seq * K + (K + (pos - sg.bos))) * p.D + c0
+                            : x + sg.bos * p.D + c0;
+        const V v = *reinterpret_cast<const V *>(src);
+        return in || st ? v : V{};
     };
-    // window: win[j] = input at t - (K - 1) + j, j < K - 1 (filled only for bos <= t)
-    U win[K > 1 ? K - 1 : 1];
-    auto fill = [&](int64_t t) __attribute__((always_inline)) {
-#pragma unroll
-        for (int j = 0; j < K - 1; ++j) {
-            const int64_t pos = t - (K - 1) + j;
-            if (pos >= bos) win[j].load(x + pos * p.D + c0);
-            else if (st) win[j].load(st + ((int64_t)seq * K + (K + (pos - bos))) * p.D + c0);
-            else win[j].zero();
-        }
-    };
-    // one token: y[t] from the window and x[t], then the window moves on
-    auto step = [&](int64_t t, const typename U::V &xv) __attribute__((always_inline)) {
-        U cur;
-#pragma unroll
-        for (int e = 0; e < VE; ++e) cur.f[e] = (float)xv[e];
-        typename U::V out;
+    // y[t] from the K rows win[0..K-1] = inputs t - K + 1 .. t
+    auto out = [&](int64_t t, const V *win) __attribute__((always_inline)) {
+        V o;
 #pragma unroll
         for (int e = 0; e < VE; ++e) {
-            float acc = w[K - 1][e] * cur.f[e];
+            float acc = 0.f;
 #pragma unroll
-            for (int j = 0; j < K - 1; ++j) acc += w[j][e] * win[j].f[e];
+            for (int j = 0; j < K; ++j) acc += (float)wb[e * K + j] * (float)win[j][e];
             float r = (float)(E)acc;                         // the convolution's output in E
             if (p.silu) r = (float)(E)(r * sigmoidf_(r));
-            out[e] = (E)r;
+            o[e] = (E)r;
         }
-        __builtin_nontemporal_store(out, reinterpret_cast<typename U::V *>(y + t * p.D + c0));
-#pragma unroll
-        for (int j = 0; j + 1 < K - 1; ++j) win[j] = win[j + 1];
-        if constexpr (K > 1) win[K - 2] = cur;
+        __builtin_nontemporal_store(o, reinterpret_cast<V *>(y + t * p.D + c0));
     };
-    locate(t0);
-    if (bos <= t0 && t0 + RUN <= eos && t0 + RUN <= p.n_tokens) {
+    const Seg sg = seg_of(p, t0);
+    if (sg.bos <= t0 && t0 + RUN <= sg.eos && t0 + RUN <= p.n_tokens) {
         // the whole run inside one segment: every row in flight at once, then the math
-        fill(t0);
-        typename U::V rows[RUN];
+        V rows[K - 1 + RUN];
+        unroll<K - 1>([&](auto j) __attribute__((always_inline)) { rows[j] = row(sg, t0 - (K - 1) + j); });
         unroll<RUN>([&](auto i) __attribute__((always_inline)) {
-            rows[i] = *reinterpret_cast<const typename U::V *>(x + (t0 + i) * p.D + c0);
+            rows[K - 1 + i] = *reinterpret_cast<const V *>(x + (t0 + i) * p.D + c0);
         });
-        unroll<RUN>([&](auto i) __attribute__((always_inline)) { step(t0 + i, rows[i]); });
+        // (the scheduler would otherwise interleave the arithmetic with the loads and
+        // issue the last rows only after the first ones arrived)
+        __builtin_amdgcn_sched_barrier(0);
+        unroll<RUN>([&](auto i) __attribute__((always_inline)) { out(t0 + i, rows + decltype(i)::value); });
         return;
     }
-    // a run that meets a segment boundary or the end of the tokens: token by token
+    // a run that meets a segment boundary or the end of the tokens: token by token,
+    // win[] sliding
     const int64_t t1 = t0 + RUN < p.n_tokens ? t0 + RUN : p.n_tokens;
-    if (bos <= t0 && t0 < eos) fill(t0);
+    Seg cur = sg;
+    V win[K];
+    auto fill = [&](int64_t t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) win[j] = row(cur, t - (K - 1) + j);
+    };
+    if (cur.bos <= t0 && t0 < cur.eos) fill(t0);
 #pragma unroll 1
     for (int64_t t = t0; t < t1; ++t) {
-        if (t > t0 && t >= eos) {            // the run enters the next packed segment(s)
-            locate(t);
-            if (bos <= t && t < eos) fill(t);
+        if (t > t0 && t >= cur.eos) {        // the run enters the next packed segment(s)
+            cur = seg_of(p, t);
+            if (cur.bos <= t && t < cur.eos) fill(t);
         }
-        if (t < bos || t >= eos) {           // a token outside every segment (a malformed table)
-            *reinterpret_cast<typename U::V *>(y + t * p.D + c0) = typename U::V{};
+        if (t < cur.bos || t >= cur.eos) {   // a token outside every segment (a malformed table)
+            *reinterpret_cast<V *>(y + t * p.D + c0) = V{};
             continue;
         }
-        step(t, *reinterpret_cast<const typename U::V *>(x + t * p.D + c0));
+        win[K - 1] = *reinterpret_cast<const V *>(x + t * p.D + c0);
+        out(t, win);
+#pragma unroll
+        for (int j = 0; j < K - 1; ++j) win[j] = win[j + 1];
     }
 }
 
@@ -153,9 +174,8 @@ __global__ void __launch_bounds__(256) causal_conv_kernel(const ConvParams p) {
 // state_out may be state_in
 template <typename E, int K>
 __global__ void __launch_bounds__(256) conv_state_kernel(const ConvParams p) {
-    using U = Unit<E>;
-    constexpr int VE = U::VE;
-    typedef typename U::V V;
+    constexpr int VE = 16 / (int)sizeof(E);
+    typedef E V __attribute__((ext_vector_type(VE)));
     const int64_t ncg = p.D / VE;
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= (int64_t)p.n_seqs * ncg) return;
@@ -191,9 +211,17 @@ static hipError_t conv_k(const ConvParams &p, hipStream_t stream) {
     const int64_t ncg = p.D / VE;
     const int64_t runs = (p.n_tokens + RUN - 1) / RUN;
     const int64_t threads = runs * ncg;
-    if (threads > 0)
-        hipLaunchKernelGGL((causal_conv_kernel<E, K>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, stream,
-                           p);
+    if (threads > 0) {
+        const dim3 grid((unsigned)((threads + 255) / 256));
+        const bool wv = ((uintptr_t)p.w & 15) == 0;
+        if (p.w_f32 && !std::is_same<E, float>::value) {
+            if (wv) hipLaunchKernelGGL((causal_conv_kernel<E, float, K, true>), grid, dim3(256), 0, stream, p);
+            else hipLaunchKernelGGL((causal_conv_kernel<E, float, K, false>), grid, dim3(256), 0, stream, p);
+        } else {
+            if (wv) hipLaunchKernelGGL((causal_conv_kernel<E, E, K, true>), grid, dim3(256), 0, stream, p);
+            else hipLaunchKernelGGL((causal_conv_kernel<E, E, K, false>), grid, dim3(256), 0, stream, p);
+        }
+    }
     if (p.state_out && p.n_seqs > 0) {
         const int64_t st = (int64_t)p.n_seqs * ncg;
         hipLaunchKernelGGL((conv_state_kernel<E, K>), dim3((unsigned)((st + 255) / 256)), dim3(256), 0, stream, p);

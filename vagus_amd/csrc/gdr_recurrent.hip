@@ -14,10 +14,56 @@
 // so S is read once and written once per call regardless of T.  The state
 // streams through once per call, so it is read and written non-temporally
 // (measured: 30.7 -> 25.5 us per decode step at B=64 H=16 dk=dv=128).
+#include <type_traits>
+
 #include "gdr_common.hpp"
 #include "gdr_kernels.hpp"
 
 namespace vgdr {
+
+// an element of type E from its bits (a 16-bit type zero-extended into 32 bits)
+template <typename E>
+__device__ __forceinline__ float bits_to_f(uint32_t b) {
+    if constexpr (sizeof(E) == 2) return Elem<E>::to_f(__builtin_bit_cast(E, (uint16_t)b));
+    else return __uint_as_float(b);
+}
+
+// One channel of the four-tap short conv for one token of the decode step:
+// SiLU(sum_j w[c][j] x[t - 3 + j][c]) for the token t = bos of a sequence, x
+// [n_tokens, HD] (HD = H * d), the cache [4, HD] holding the sequence's 4 inputs
+// before bos.  load() only issues the loads (the taps, and the channel's weight row
+// as one aligned vector of WT), so that the caller decides what is in flight beside
+// them; apply() then does the arithmetic.  Loaded values are kept as loaded: a
+// conversion at load time would make the divergent owner branch wait for its loads
+// where it ends.  The convolution's and the SiLU's results are rounded to E, as the
+// module computes them in its dtype.  The 4 inputs read are exactly the cache's next
+// contents, and apply() writes them back: the owner thread of a channel is its only
+// reader, and it has read its last old value.
+template <typename E, typename WT>
+struct ConvTaps {
+    using EL = Elem<E>;
+    typedef WT WV __attribute__((ext_vector_type(4)));
+    E xs[4];
+    WV w4;
+    __device__ __forceinline__ void load(const E *x, const E *cache, const void *w, int64_t HD, int64_t c,
+                                         int64_t t) {
+        unroll<4>([&](auto j) __attribute__((always_inline)) {
+            xs[j] = j == 3 ? x[t * HD + c] : cache[(int64_t)(j + 1) * HD + c];
+        });
+        w4 = reinterpret_cast<const WV *>(w)[c];
+    }
+    __device__ __forceinline__ float apply(E *cache, int64_t HD, int64_t c) const {
+        float acc = 0.f;
+        unroll<4>([&](auto j) __attribute__((always_inline)) {
+            acc += (float)w4[decltype(j)::value] * EL::to_f(xs[j]);
+        });
+        // the cache row addresses are rebuilt here rather than kept from load()
+        asm volatile("" : "+v"(c));
+        unroll<4>([&](auto j) __attribute__((always_inline)) { cache[(int64_t)j * HD + c] = xs[j]; });
+        const float y = EL::to_f(EL::from_f(acc));
+        return EL::to_f(EL::from_f(y * sigmoidf_(y)));
+    }
+};
 
 // Producer of one channel with the short conv: SiLU(sum_j w[c][j] x[t - K + 1 + j][c])
 // for the token t of a sequence starting at bos; x is [n_tokens, HD] (HD = H * d), the
@@ -276,10 +322,259 @@ recurrent_kernel(const RecParams p) {
     // its cache as it was)
 }
 
+// The layer's decode step with the short conv (GatedDeltaNet.decode_step at L = 1,
+// linear_attention.py:918-952): one token per sequence, four conv taps with 16-byte
+// aligned weights of type WT (E or fp32), a state to read.  MODE: the EPI and WR bits
+// of recurrent_kernel (the conv is implied).  The layout is recurrent_kernel's; the
+// order of the work differs:
+//   * the state's loads are issued first thing (buffer loads: one lane offset for all
+//     rows), then the token's operand loads;
+//   * the producers (conv, SiLU, L2 norm, q . k) run on threads 0..dk-1 and stage
+//     their results in LDS behind barriers that order LDS only;
+//   * the state is read as loaded: the dot products take the decay from the staged
+//     q and k (per channel) or as one factor after the sum (scalar), and the update
+//     S <- diag(a) S + k u^T is one FMA per element.
+// Measured at B64 H16 dk=dv=128, bf16, 24 rotating layers: 29.2 us with the
+// producers waiting for the state (recurrent_kernel), 26.4 us with the operand
+// loads ahead of the state's, 25.7 us in this order before the decay folding.  A
+// producer wave of its own (5 waves per workgroup) needs more than 96 VGPRs and
+// spills: 31 us.
+template <int DK, int DV, typename E, int GATE, int MODE, typename WT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATE == 2 || (MODE & 4) ? 1 : 4)))
+decode_conv_kernel(const RecParams p) {
+    constexpr bool EPI = MODE & 1, WR = MODE & 4;
+    constexpr int NT = 256;
+    constexpr int NCG = DV / 4;
+    constexpr int NRG = NT / NCG;
+    constexpr int RPT = DK / NRG;
+    constexpr int NWV = NT / 64;
+    constexpr int K = 4;
+    static_assert(NT % NCG == 0 && DK % NRG == 0 && 64 % NCG == 0 && DK <= NT && DV <= NT, "thread layout");
+    using EL = Elem<E>;
+
+    // qs, ks: q (scaled) and k, times the per-channel decay with GATE 2; kr: k itself
+    __shared__ __attribute__((aligned(16))) float qs[DK];
+    __shared__ __attribute__((aligned(16))) float ks[DK];
+    __shared__ __attribute__((aligned(16))) float kr[GATE == 2 ? DK : 1];
+    __shared__ __attribute__((aligned(16))) float vs[DV];
+    __shared__ __attribute__((aligned(16))) float gv[GATE == 2 ? DK : 1];
+    __shared__ __attribute__((aligned(16))) float red[NWV][2][DV];
+    __shared__ float nrm[NWV][3];           // per-wave sums: q^2, k^2, then q . k (q . w)
+    __shared__ float sc[2];                 // decay (scalar gate), beta
+    __shared__ __attribute__((aligned(16))) float wsv[WR ? DK : 4];
+    __shared__ __attribute__((aligned(16))) float gts[EPI ? DV : 4];
+    __shared__ __attribute__((aligned(16))) float gms[EPI ? DV : 4];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int cg = tid % NCG, rg = tid / NCG;
+    const int H = p.H;
+    const int h = blockIdx.x % H;
+    const int seq = blockIdx.x / H;
+    const int64_t t = seq;                  // one token per sequence
+    const int64_t qo = (t * H + h) * DK, vo = (t * H + h) * DV;
+    const int64_t sbase = ((int64_t)seq * H + h) * DK * DV;
+    const bool own = tid < DK, vown = tid < DV;
+    E *og = reinterpret_cast<E *>(p.o);
+
+    // (1) the state
+    const __amdgpu_buffer_rsrc_t s_in = buffer_rsrc(p.h0 + sbase, DK * DV * 4);
+    const uint32_t so = (uint32_t)(rg * DV + 4 * cg) * 4;
+    f32x4 S[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) S[i] = buffer_load_nt4(s_in, so, (uint32_t)(NRG * i * DV * 4));
+
+    // (2) the token's operands
+    const int64_t HDK = (int64_t)H * DK, HDV = (int64_t)H * DV;
+    const int64_t cq = (int64_t)h * DK + tid, cvc = (int64_t)h * DV + tid;
+    E *cache_q = reinterpret_cast<E *>(p.cv.cq) + (int64_t)seq * K * HDK;
+    E *cache_k = reinterpret_cast<E *>(p.cv.ck) + (int64_t)seq * K * HDK;
+    E *cache_v = reinterpret_cast<E *>(p.cv.cv) + (int64_t)seq * K * HDV;
+    ConvTaps<E, WT> tq, tk, tv;
+    E wr = EL::from_f(0.f), gtr = EL::from_f(0.f);
+    uint32_t gr = 0;
+    float gsc = 0.f, bsc = 0.f, gmv = 0.f;
+    if (own) {
+        tq.load(reinterpret_cast<const E *>(p.q), cache_q, p.cv.wq, HDK, cq, t);
+        tk.load(reinterpret_cast<const E *>(p.k), cache_k, p.cv.wk, HDK, cq, t);
+        if constexpr (WR) wr = reinterpret_cast<const E *>(p.w)[qo + tid];
+        if constexpr (GATE == 2)
+            gr = p.fz.gate_act && p.fz.gate_16 && sizeof(E) == 2
+                     ? (uint32_t)reinterpret_cast<const uint16_t *>(p.g)[qo + tid]
+                     : reinterpret_cast<const uint32_t *>(p.g)[qo + tid];
+    }
+    if (vown) {
+        tv.load(reinterpret_cast<const E *>(p.v), cache_v, p.cv.wv, HDV, cvc, t);
+        if constexpr (EPI) {
+            gtr = reinterpret_cast<const E *>(p.ep.gate)[vo + tid];
+            gmv = p.ep.gamma_f32 ? reinterpret_cast<const float *>(p.ep.gamma)[tid]
+                                 : EL::to_f(reinterpret_cast<const E *>(p.ep.gamma)[tid]);
+        }
+    }
+    if (tid == 0) {
+        if (GATE == 1 && p.g) gsc = p.g[t * H + h];
+        if (!WR && p.use_delta) bsc = p.beta[t * H + h];
+    }
+
+    // (3) producers: conv + SiLU (linear_attention.py:741-745) advancing the caches
+    // (:929-941), the L2 norm (:703-706), q . k
+    float qv = 0.f, kv = 0.f;
+    if (own) {
+        qv = tq.apply(cache_q, HDK, cq);
+        kv = tk.apply(cache_k, HDK, cq);
+    }
+    if (p.fz.qk_l2norm) {
+        float sq = qv * qv, sk = kv * kv;
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) {
+            sq += __shfl_xor(sq, off);
+            sk += __shfl_xor(sk, off);
+        }
+        if (lane == 0) {
+            nrm[wave][0] = sq;
+            nrm[wave][1] = sk;
+        }
+        lds_barrier();
+        sq = sk = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) {
+            sq += nrm[w][0];
+            sk += nrm[w][1];
+        }
+        qv = EL::to_f(EL::from_f(qv * rsqrtf(sq + 1e-6f)));
+        kv = EL::to_f(EL::from_f(kv * rsqrtf(sk + 1e-6f)));
+    }
+    qv *= p.scale;
+    {
+        float qk = qv * (WR ? EL::to_f(wr) : kv);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) qk += __shfl_xor(qk, off);
+        if (lane == 0) nrm[wave][2] = qk;
+    }
+    if (own) {
+        float a = 1.f;
+        if constexpr (GATE == 2) {
+            const float gf = p.fz.gate_act && p.fz.gate_16 ? bits_to_f<E>(gr) : __uint_as_float(gr);
+            const float gl = p.fz.gate_act ? gate_activation(gf, p.fz.A_log[h], p.fz.dt_bias[(int64_t)h * DK + tid],
+                                                             p.fz.lb_set, p.fz.lb)
+                                           : gf;
+            a = __expf(gl);
+            gv[tid] = a;
+            kr[tid] = kv;
+        }
+        qs[tid] = qv * a;
+        ks[tid] = kv * a;
+        if constexpr (WR) wsv[tid] = EL::to_f(wr);
+    }
+    if (vown) {
+        vs[tid] = tv.apply(cache_v, HDV, cvc);
+        if constexpr (EPI) {
+            gts[tid] = EL::to_f(gtr);
+            gms[tid] = gmv;
+        }
+    }
+    if (tid == 0) {
+        sc[0] = (GATE == 1 && p.g) ? __expf(gsc) : 1.f;
+        sc[1] = WR ? 1.f : (p.use_delta && p.fz.beta_sigmoid ? sigmoidf_(bsc) : bsc);
+    }
+    lds_barrier();
+
+    // (4) the state math on the state as loaded
+    f32x4 kS = {0.f, 0.f, 0.f, 0.f}, qS = {0.f, 0.f, 0.f, 0.f};
+    const float a0 = sc[0];
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        const int r = rg + NRG * i;
+        kS += ks[r] * S[i];
+        qS += qs[r] * S[i];
+    }
+    if constexpr (GATE != 2) {
+        kS *= a0;
+        qS *= a0;
+    }
+#pragma unroll
+    for (int off = NCG; off < 64; off <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            kS[e] += __shfl_xor(kS[e], off);
+            qS[e] += __shfl_xor(qS[e], off);
+        }
+    }
+    if (lane < NCG) {
+        st4(&red[wave][0][4 * cg], kS);
+        st4(&red[wave][1][4 * cg], qS);
+    }
+    lds_barrier();
+    kS = ld4(&red[0][0][4 * cg]);
+    qS = ld4(&red[0][1][4 * cg]);
+    float qk = nrm[0][2];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) {
+        kS += ld4(&red[w][0][4 * cg]);
+        qS += ld4(&red[w][1][4 * cg]);
+        qk += nrm[w][2];
+    }
+    const f32x4 v4 = ld4(&vs[4 * cg]);
+    const f32x4 u = p.use_delta ? sc[1] * (v4 - kS) : v4;
+    const f32x4 o = qS + qk * u;                     // o = q^T (diag(a) S + k u^T)
+    if constexpr (EPI) {
+        // the output epilogue (linear_attention.py:814-825); wave 0 holds every column
+        if (wave == 0) {
+            float x[4], ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[e] = EL::to_f(EL::from_f(o[e]));
+                ss += x[e] * x[e];
+            }
+#pragma unroll
+            for (int m = 1; m < NCG; m <<= 1) ss += __shfl_xor(ss, m);
+            const float r = rsqrtf(ss * (1.f / DV) + p.ep.eps);
+            if (rg == 0) {
+                const f32x4 gt = ld4(&gts[4 * cg]), gm = ld4(&gms[4 * cg]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    og[vo + 4 * cg + e] = EL::from_f(x[e] * r * gm[e] * (gt[e] * sigmoidf_(gt[e])));
+            }
+        }
+    } else if (rg == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) og[vo + 4 * cg + e] = EL::from_f(o[e]);
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+        const int r = rg + NRG * i;
+        const float a = GATE == 2 ? gv[r] : a0;
+        S[i] = a * S[i] + (WR ? wsv[r] : GATE == 2 ? kr[r] : ks[r]) * u;
+    }
+    if (p.ht) {
+        const __amdgpu_buffer_rsrc_t s_out = buffer_rsrc(p.ht + sbase, DK * DV * 4);
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) buffer_store_nt4(S[i], s_out, so, (uint32_t)(NRG * i * DV * 4));
+    }
+}
+
 template <int DK, int DV, typename E, int GATE>
 static hipError_t launch_rec(const RecParams &p, hipStream_t stream) {
     const int64_t blocks = (int64_t)p.n_seqs * p.H;
     if (blocks == 0) return hipSuccess;
+    // the layer's decode step (one token per sequence, a state, the conv's usual four
+    // taps with 16-byte aligned weights) has its own kernel
+    const bool aligned = (((uintptr_t)p.cv.wq | (uintptr_t)p.cv.wk | (uintptr_t)p.cv.wv) & 15) == 0;
+    if (!p.cu && p.T == 1 && p.h0 && p.cv.K == 4 && aligned) {
+        const int m = (p.ep.gate ? 1 : 0) | (p.w ? 4 : 0);
+        const bool wf = p.cv.w_f32 && !std::is_same<E, float>::value;     // fp32 weights beside 16-bit inputs
+#define VGDR_DEC(M)                                                                                           \
+    case M:                                                                                                    \
+        if (wf)                                                                                                \
+            hipLaunchKernelGGL((decode_conv_kernel<DK, DV, E, GATE, M, float>), dim3((unsigned)blocks), dim3(256), 0, \
+                               stream, p);                                                                     \
+        else                                                                                                   \
+            hipLaunchKernelGGL((decode_conv_kernel<DK, DV, E, GATE, M, E>), dim3((unsigned)blocks), dim3(256), 0,  \
+                               stream, p);                                                                     \
+        break;
+        switch (m) { VGDR_DEC(0) VGDR_DEC(1) VGDR_DEC(4) VGDR_DEC(5) }
+#undef VGDR_DEC
+        return hipGetLastError();
+    }
     const int mode = (p.ep.gate ? 1 : 0) | (p.cv.K ? 2 : 0) | (p.w ? 4 : 0);
 #define VGDR_REC(M)                                                                                           \
     case M:                                                                                                    \
