@@ -41,7 +41,9 @@ Also reported on the same line:
                 gradients), against the reference's count for the backward:
                 2 x 180,224 FLOP per token-head (chunk_scan_flops counts
                 forward + backward as 3 x the forward); and the training pair
-                (saving forward + saved backward) against 3 x 180,224
+                (saving forward + saved backward) against 3 x 180,224; the
+                same for KDA (per-channel gate) at the KDA prefill shape, with
+                the token-walk backward timed beside it
   generation    the 1.3B-shape GDN LM (24 layers, d2048, vocab 32000, bf16):
                 ragged prefill of 64 prompts U[64, 2048], then 256 greedy
                 decode steps replayed from a HIP graph: prefill tok/s,
@@ -359,29 +361,53 @@ def bench_backward(torch, ops, workloads, steps, warmup):
             'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2)}
 
 
-def bench_scan_backward(torch, ops, workloads, steps, warmup):
-    """The token-walk backward (vgdr_scan_bwd through ops.scan_bwd) at the KDA
-    prefill shape: gradients of o and the final state with respect to q, k, v,
-    the per-channel g, beta and the entry state."""
+def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
+    """The KDA backward at the KDA prefill shape: gradients of o and the final
+    state with respect to q, k, v, the per-channel g, beta and the entry state.
+    The chunked backward (vgdr_chunk_bwd through
+    ops.chunk_gated_delta_rule_bwd), the training pair autograd runs (saving
+    forward + saved backward) and, for comparison, the token-walk backward
+    (vgdr_scan_bwd through ops.scan_bwd)."""
     g = torch.Generator(device='cpu').manual_seed(13)
     x = workloads.workload('kda_prefill', device='cuda')
     do = torch.randn(*x.v.shape, generator=g).bfloat16().cuda()
     B, T, H = x.q.shape[:3]
     dST = torch.randn(B, H, x.q.shape[-1], x.v.shape[-1], generator=g).cuda()
+    scale = DK ** -0.5
 
     def step(i):
-        ops.scan_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST, scale=DK ** -0.5)
+        ops.chunk_gated_delta_rule_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST, scale=scale)
 
     us = _event_us(torch, step, steps, warmup)
+
+    def pair(i):
+        o, S, ws = ops._chunk_fwd_saving(x.q, x.k, x.v, x.g, x.beta, x.initial_state, scale=scale,
+                                         cu_seqlens=None, chunk_size=CHUNK)
+        ops.chunk_gated_delta_rule_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST, scale=scale,
+                                       saved_workspace=ws)
+
+    pair_us = _event_us(torch, pair, steps, warmup)
+    walk_us = None
+    if token_walk:
+        walk_us = _event_us(torch, lambda i: ops.scan_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST,
+                                                          scale=scale), max(2, steps // 3), 1)
     th = B * T * H
     del x, do
     tflops = th * 2 * FLOP_PER_TOKEN_HEAD / (us * 1e-6) / 1e12
-    return {'workload': 'kda_prefill backward: dq, dk, dv, dg (per channel), dbeta, dh0 from do and dht, '
-                        'B4 T8192 H8 dk=dv=128 bf16',
-            'kernels': 'scan_walks_kernel + scan_grad_kernel + scan_bwd_finish_kernel',
-            'us': round(us, 1), 'tok_s': round(B * T / (us * 1e-6), 1),
-            'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
-            'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5)}
+    r = {'workload': 'kda_prefill backward: dq, dk, dv, dg (per channel), dbeta, dh0 from do and dht, '
+                     'B4 T8192 H8 dk=dv=128 bf16',
+         'kernels': 'chunk_prep_kernel + chunk_pipe_kernel (entry states) + chunk_dhs_kernel + chunk_grad_kernel '
+                    '+ chunk_grad_vec_kernel',
+         'us': round(us, 1), 'tok_s': round(B * T / (us * 1e-6), 1),
+         'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
+         'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5),
+         'train_pair_us': round(pair_us, 1),
+         'train_pair': 'vgdr_chunk_fwd_saving + vgdr_chunk_bwd_saved (what autograd runs for 16-bit inputs)',
+         'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2)}
+    if walk_us is not None:
+        r['token_walk_us'] = round(walk_us, 1)
+        r['token_walk'] = 'vgdr_scan_bwd (scan_walks_kernel + scan_grad_kernel + scan_bwd_finish_kernel)'
+    return r
 
 
 def cpu_baseline(torch, workloads):
@@ -549,7 +575,7 @@ def main():
         return
     if args.backward_only:
         print(json.dumps(bench_backward(torch, ops, workloads, args.steps, args.warmup)), flush=True)
-        print(json.dumps(bench_scan_backward(torch, ops, workloads, max(3, args.steps // 3), max(2, args.warmup // 3))),
+        print(json.dumps(bench_kda_backward(torch, ops, workloads, args.steps, args.warmup)),
               flush=True)
         return
     if args.layer_only:
@@ -582,8 +608,8 @@ def main():
         extra['layer_kernels'] = bench_layer_kernels(torch, ops, workloads, args.steps, args.warmup)
         log('[bench] backward gdn_340m')
         extra['backward'] = bench_backward(torch, ops, workloads, max(5, args.steps // 4), max(3, args.warmup // 10))
-        log('[bench] backward kda_prefill (token walk)')
-        extra['kda_backward'] = bench_scan_backward(torch, ops, workloads, 3, 1)
+        log('[bench] backward kda_prefill')
+        extra['kda_backward'] = bench_kda_backward(torch, ops, workloads, max(5, args.steps // 4), max(3, args.warmup // 10))
         log('[bench] generation gdn_lm_1p3b')
         extra['generation'] = bench_generate(torch, workloads)
         for name in ('kda_prefill', 'gdn_varlen'):

@@ -235,16 +235,19 @@ int vgdr_chunk_fwd_w(int dtype, const void *q, const void *k, const void *v, con
                      float scale, int chunk_size, const vgdr_fusion *fusion, hipStream_t stream);
 
 /*
- * Backward of the chunked scan, scalar gate (gate_kind 1) or none (0), delta
- * rule: the gradients the reference's training takes through chunk_scan
- * (linear_attention.py:237-309, autograd) or fla's chunk_gated_delta_rule
- * backward (the call at :487-491 with grads enabled).  Inputs as the forward
- * call had them (q, k already normalised; beta in [0, 1]; initial_state
- * nullable), plus grad_o [n_tokens, H, dv] in dtype and grad_final_state
- * [n_seqs, H, dk, dv] fp32 (nullable: zero).  Outputs: grad_q, grad_k
- * [n_tokens, H, dk], grad_v [n_tokens, H, dv] in dtype; grad_g, grad_beta
- * [n_tokens, H] fp32 (grad_g unused and nullable without a gate);
- * grad_initial_state [n_seqs, H, dk, dv] fp32 (nullable: not computed).
+ * Backward of the chunked scan, scalar gate (gate_kind 1), per-channel gate
+ * (2, 16-bit dtypes, 64-token chunks) or none (0), delta rule: the gradients
+ * the reference's training takes through chunk_scan and chunk_scan_vec
+ * (linear_attention.py:237-309, :312-425, autograd) or fla's
+ * chunk_gated_delta_rule / chunk_kda backward (the calls at :487-491 and
+ * :474-479 with grads enabled).  Inputs as the forward call had them (q, k
+ * already normalised; beta in [0, 1]; g the log-decay, [n_tokens, H] or
+ * [n_tokens, H, dk]; initial_state nullable), plus grad_o [n_tokens, H, dv]
+ * in dtype and grad_final_state [n_seqs, H, dk, dv] fp32 (nullable: zero).
+ * Outputs: grad_q, grad_k [n_tokens, H, dk], grad_v [n_tokens, H, dv] in
+ * dtype; grad_g fp32 shaped as g (unused and nullable without a gate);
+ * grad_beta [n_tokens, H] fp32; grad_initial_state [n_seqs, H, dk, dv] fp32
+ * (nullable: not computed).
  * The gradients must not alias the inputs; grad_o and grad_v are 16-byte
  * aligned (q, k, v as in vgdr_chunk_fwd).  workspace:
  * vgdr_chunk_bwd_workspace_size(...) bytes, 16-byte aligned; it holds the
@@ -267,8 +270,9 @@ int vgdr_chunk_bwd(int dtype, int gate_kind,
  * The same pair with the forward's intermediates kept instead of recomputed
  * (no reference counterpart as an entry point; fla's disable_recompute,
  * linear_attention.py:463-471, is the same trade of memory for time).
- * vgdr_chunk_fwd_saving is vgdr_chunk_fwd (16-bit dtypes, gate_kind 0/1,
- * delta rule, no fusion) run in the backward's workspace
+ * vgdr_chunk_fwd_saving is vgdr_chunk_fwd (16-bit dtypes, any gate_kind,
+ * 64-token chunks with the per-channel gate, delta rule, no fusion) run in
+ * the backward's workspace
  * (vgdr_chunk_bwd_workspace_size bytes, same dv): besides o and final_state it
  * leaves there the packed-batch schedule, the chunk blocks and every chunk's
  * entry state.  vgdr_chunk_bwd_saved, called with the same inputs and that

@@ -39,7 +39,7 @@ def test_chunk_bwd_argument_checks():
         return L.vgdr_chunk_bwd(a['dtype'], a['gate'], a['q'], a['k'], a['v'], a['g'], a['beta'], a['h0'], a['do'],
                                 a['dht'], a['dq'], a['dk'], a['dv'], a['dg'], a['db'], a['dh0'], a['cu'], a['ws'],
                                 a['wsb'], a['B'], a['T'], a['H'], a['dk_'], a['dv_'], a['N'], 0.125, 64, None)
-    assert call(gate=2) == _lib.VGDR_ERR_UNSUPPORTED                 # no per-channel backward
+    assert call(gate=2, dtype=0) == _lib.VGDR_ERR_UNSUPPORTED        # the per-channel backward is 16-bit
     assert call(dv_=40) == _lib.VGDR_ERR_UNSUPPORTED
     assert call(dk_=96) == _lib.VGDR_ERR_UNSUPPORTED
     assert call(db=None) == _lib.VGDR_ERR_INVALID
@@ -50,12 +50,11 @@ def test_chunk_bwd_argument_checks():
     assert call(wsb=16) == _lib.VGDR_ERR_INVALID
     assert call(beta=None) == _lib.VGDR_ERR_INVALID
     assert call(B=0, N=0, T=0) == _lib.VGDR_OK
-    # the saving forward and saved backward: 16-bit, scalar gate or none
+    # the saving forward and saved backward: 16-bit (64-token chunks with a per-channel gate)
     fwd_saving = lambda dtype, gate: L.vgdr_chunk_fwd_saving(dtype, gate, 4096, 8192, 12288, 16384, 20480, 24576,
                                                              None, None, None, 49152, 1 << 40, 2, 64, 2, 64, 64, 2,
                                                              0.125, 64, None)
     assert fwd_saving(0, 1) == _lib.VGDR_ERR_UNSUPPORTED
-    assert fwd_saving(1, 2) == _lib.VGDR_ERR_UNSUPPORTED
     need = L.vgdr_chunk_bwd_workspace_size(1, 1, 2, 64, 2, 64, 64, 2, 0, 64)
     # forward blocks plus two bf16 states per (chunk, head)
     assert need >= 2 * 2 * 2 * 64 * 64 * 2 + L.vgdr_chunk_workspace_size(1, 1, 2, 64, 2, 64, 2, 0, 64)

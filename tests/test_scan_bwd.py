@@ -182,7 +182,14 @@ def _autograd(fn, leaves, do, dST):
 def test_chunk_kda_autograd_with_fused_producers(lower_bound):
     """chunk_kda with q, k un-normalised, beta as logits and the gate as its
     pre-activation: the gradients of every input, A_log and dt_bias included,
-    equal those of the oracle's producers followed by its recurrence."""
+    equal those of the oracle's producers followed by its recurrence (with
+    grads, 16-bit chunk_kda runs the chunked backward, vgdr_chunk_bwd).
+    dA_log and ddt_bias are sums over tokens (and channels) of
+    dg * dg/dparam; their error is held to the bar relative to the L2 norm of
+    those summands, which is what rounding in dg bounds: with the lower bound
+    the sum for A_log is several times smaller than its summands' norm
+    (cancellation), and a relative bar on the sum would ask for more than the
+    16-bit per-token gradients carry."""
     B, T, H, dk, dv = 1, 50, 2, 64, 64
     gen = torch.Generator().manual_seed(9)
     r = lambda *s: torch.randn(*s, generator=gen)
@@ -203,10 +210,24 @@ def test_chunk_kda_autograd_with_fused_producers(lower_bound):
     qq, kk = gdr.l2norm(leaves[0]), gdr.l2norm(leaves[1])
     gg = gdr.gate_activation(leaves[3], leaves[6], leaves[7], lower_bound)
     o, S = gdr.recurrent(qq, kk, leaves[2], gg, gdr.beta_sigmoid(leaves[4]), leaves[5], scale=dk ** -0.5)
-    ref = torch.autograd.grad([o, S], leaves, [do.double(), dST.double()])
-    for name, a, b in zip(('q', 'k', 'v', 'f', 'beta', 'S0', 'A_log', 'dt_bias'), got, ref):
-        err = _rel(a, b)
-        print(f'[parity] chunk_kda fused d{name} rel_l2={err:.3e}', flush=True)
+    ref = torch.autograd.grad([o, S], leaves + [gg], [do.double(), dST.double()])
+    dg_ref = ref[-1]
+    # the summands of dA_log and ddt_bias: dg times the gate's derivative in
+    # that parameter (each gate element depends on one A_log and one dt_bias entry)
+    act = lambda a, d: gdr.gate_activation(f.double(), a, d, lower_bound)
+    A2, d2 = A_log.double(), dt_bias.double()
+    _, wA = torch.func.jvp(lambda a: act(a, d2), (A2,), (torch.ones_like(A2),))
+    _, wd = torch.func.jvp(lambda d: act(A2, d), (d2,), (torch.ones_like(d2),))
+    norms = {'A_log': (dg_ref * wA).pow(2).sum((0, 1, 3)).sqrt(),
+             'dt_bias': (dg_ref * wd).pow(2).sum((0, 1)).sqrt().reshape(-1)}
+    for name, a, b in zip(('q', 'k', 'v', 'f', 'beta', 'S0', 'A_log', 'dt_bias'), got, ref[:-1]):
+        if name in norms:
+            err = ((a.double().cpu() - b).norm() / norms[name].norm()).item()
+            print(f'[parity] chunk_kda fused d{name} rel_l2={_rel(a, b):.3e}, over its summands {err:.3e}',
+                  flush=True)
+        else:
+            err = _rel(a, b)
+            print(f'[parity] chunk_kda fused d{name} rel_l2={err:.3e}', flush=True)
         assert err <= 2e-2, f'd{name}: {err:.3e}'
 
 

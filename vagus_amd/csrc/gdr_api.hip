@@ -161,10 +161,12 @@ ChunkWs chunk_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, 
 }
 
 // workspace of the backward: the forward's (table, blocks), then each chunk's
-// entry state and exit-state gradient (dk x dv per (chunk, head) in the element type)
+// entry state and exit-state gradient (dk x dv per (chunk, head) in the element
+// type); with the per-channel gate also chunk prep's N (CH x CH fp32 per
+// (chunk, head)) and the column phase's sums (grad_vec_work_floats each)
 struct BwdWs {
     ChunkWs fwd;
-    int64_t hs_off, dhs_off, total;
+    int64_t hs_off, dhs_off, nbuf_off, gw_off, total;
 };
 BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
                  int64_t n_seqs, bool varlen) {
@@ -174,6 +176,14 @@ BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int6
     w.hs_off = (w.fwd.total + 255) / 256 * 256;
     w.dhs_off = w.hs_off + (states + 255) / 256 * 256;
     w.total = states > 0 ? w.dhs_off + states : w.fwd.total;
+    w.nbuf_off = w.gw_off = w.total;
+    if (gate_kind == VGDR_GATE_VECTOR && dtype != VGDR_F32 && states > 0) {
+        const int64_t nb = w.fwd.slots * H * chunk * chunk * 4;
+        const int64_t gw = w.fwd.slots * H * vgdr::grad_vec_work_floats(chunk, (int)dk) * 4;
+        w.nbuf_off = (w.total + 255) / 256 * 256;
+        w.gw_off = w.nbuf_off + (nb + 255) / 256 * 256;
+        w.total = w.gw_off + gw;
+    }
     return w;
 }
 
@@ -214,9 +224,12 @@ int chunk_call(const char *fn, int phases, int dtype, int gate_kind, int use_del
     if (ws.slots * H > 0x7fffffffLL || (n_seqs * H + 7) / 8 * 8 * ((dv + 31) / 32) > 0x7fffffffLL)
         return fail(VGDR_ERR_INVALID, "%s: grid too large", fn);
     vgdr::ChunkParams p{};
-    p.hs = bwd_ws ? static_cast<char *>(workspace) +
-                        bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, cu_seqlens != nullptr).hs_off
-                  : nullptr;
+    if (bwd_ws) {
+        const BwdWs bw = bwd_layout(dtype, gate_kind, chunk, B, T, H, dk, dv, n_seqs, cu_seqlens != nullptr);
+        p.hs = static_cast<char *>(workspace) + bw.hs_off;
+        if (gate_kind == VGDR_GATE_VECTOR)
+            p.nout = reinterpret_cast<float *>(static_cast<char *>(workspace) + bw.nbuf_off);
+    }
     p.geo.cu = cu_seqlens;
     p.geo.T = T;
     p.geo.n_tokens = B * T;
@@ -342,10 +355,11 @@ int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS) {
     g_err[0] = 0;
     int rc = check_common(fn, dtype, gate_kind, 1, q, k, v, g, beta, grad_o, cu_seqlens, B, T, H, dk, dv, n_seqs);
     if (rc) return rc;
-    if (gate_kind == VGDR_GATE_VECTOR)
-        return fail(VGDR_ERR_UNSUPPORTED, "%s: the backward covers the scalar gate and no gate", fn);
     if (dv <= 0 || dv % 16)
         return fail(VGDR_ERR_UNSUPPORTED, "%s: dv=%lld (must be a positive multiple of 16)", fn, (long long)dv);
+    if (gate_kind == VGDR_GATE_VECTOR && (dtype == VGDR_F32 || effective_chunk(dtype, dk, chunk_size) != 64))
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: the per-channel-gate backward runs 16-bit q, k, v in 64-token chunks",
+                    fn);
     if (B * T > 0 && (!grad_q || !grad_k || !grad_v || !grad_beta))
         return fail(VGDR_ERR_INVALID, "%s: grad_q, grad_k, grad_v and grad_beta are required", fn);
     if (grad_v == v || grad_q == q || grad_k == k)
@@ -394,11 +408,23 @@ int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS) {
     p.DV = (int)dv;
     p.n_chunk_slots = (int)ws.fwd.slots;
     p.scale = scale;
+    if (gate_kind == VGDR_GATE_VECTOR) {
+        p.nbuf = reinterpret_cast<const float *>(wsb + ws.nbuf_off);
+        p.gw = reinterpret_cast<float *>(wsb + ws.gw_off);
+        // the forward run for the entry states writes N and the states where
+        // the backward reads them; its output o goes to the exit-gradient
+        // region (n_tokens x dv <= chunk slots x CH x dv <= its dk x dv per
+        // slot), which the dS walk then overwrites
+        f.hs = p.hs;
+        f.nout = const_cast<float *>(p.nbuf);
+        f.o = p.dhs;
+        f.h0 = initial_state;
+    }
     int32_t *table = cu_seqlens ? reinterpret_cast<int32_t *>(wsb) : nullptr;
     if (f.geo.n_seqs == 0) return VGDR_OK;
     if (saved && dtype == VGDR_F32)
         return fail(VGDR_ERR_UNSUPPORTED, "%s: saved states come from the 16-bit forward kernel", fn);
-    return hip_status(vgdr::chunk_bwd(dtype, (int)dk, chunk, f, p, table, saved, stream), fn);
+    return hip_status(vgdr::chunk_bwd(dtype, (int)dk, chunk, gate_kind == VGDR_GATE_VECTOR, f, p, table, saved, stream), fn);
 }
 }  // namespace
 
@@ -474,9 +500,10 @@ int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k
                           int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
                           hipStream_t stream) {
     const char *fn = "vgdr_chunk_fwd_saving";
-    if (dtype == VGDR_F32 || gate_kind == VGDR_GATE_VECTOR) {
+    if (dtype == VGDR_F32 || (gate_kind == VGDR_GATE_VECTOR && effective_chunk(dtype, dk, chunk_size) != 64)) {
         g_err[0] = 0;
-        return fail(VGDR_ERR_UNSUPPORTED, "%s: saving runs the 16-bit kernel, scalar gate or none", fn);
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: saving runs the 16-bit kernel (64-token chunks with a per-channel g)",
+                    fn);
     }
     return chunk_call(fn, vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, dtype, gate_kind, 1, q, k, v, g, beta, o,
                       initial_state, final_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk, dv, n_seqs,

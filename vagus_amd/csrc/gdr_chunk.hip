@@ -481,6 +481,14 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             aq[jj] = (jt <= irow) ? p.scale * accq[jj] * d : 0.f;
             mk[jj] = (jt < irow) ? bet[irow] * acck[jj] * d : 0.f;
         }
+        if constexpr (GATE == 2 && !WR) {
+            // N itself (before diag(beta)), for the backward
+            if (p.nout) {
+                float *nb = p.nout + (slot * H + h) * CH * CH + irow * CH + 16 * J + 4 * g4;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) nb[jj] = 16 * J + 4 * g4 + jj < irow ? acck[jj] : 0.f;
+            }
+        }
         res_q[s] = aq;
         res_k[s] = mk;
     }
@@ -1517,9 +1525,9 @@ static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hip
     if constexpr (sizeof(E) == 2) {
         // 16-bit elements: the pipelined kernel (chain, output and producer waves)
         constexpr bool VEC = GATE == 2;
-        if constexpr (!VEC && DELTA) {
+        if constexpr (DELTA) {
             if (p.hs) {                                       // a training forward: entry states saved
-                launch_pipe<DK, CH, E, false, true, true>(p, nw, state_blocks, stream);
+                launch_pipe<DK, CH, E, VEC, true, true>(p, nw, state_blocks, stream);
                 return;
             }
         }

@@ -80,6 +80,21 @@ struct RowRegs {
             }
         });
     }
+    // rows in the paired-column order of chunk prep's gated tiles (16-byte unit
+    // pu = 4 q + g holds columns 32 q + 4 g .. + 3 and 32 q + 16 + 4 g .. + 3),
+    // written to LDS in natural column order
+    __device__ __forceinline__ void store_unpaired(E *dst, int pitch, int tid) const {
+        static_assert(VE == 8 && DK % 32 == 0, "paired rows are 16-bit, 32-column groups");
+        typedef E V4 __attribute__((ext_vector_type(4)));
+        unroll<N>([&](auto i) __attribute__((always_inline)) {
+            const int u = tid + (int)i * NT;
+            if (u < UNITS) {
+                const int row = u / UPR, pu = u % UPR, c0 = 32 * (pu >> 2) + 4 * (pu & 3);
+                *reinterpret_cast<V4 *>(dst + row * pitch + c0) = __builtin_shufflevector(x[i], x[i], 0, 1, 2, 3);
+                *reinterpret_cast<V4 *>(dst + row * pitch + c0 + 16) = __builtin_shufflevector(x[i], x[i], 4, 5, 6, 7);
+            }
+        });
+    }
 };
 
 // NCB column blocks (16 columns each) of a state checkpoint (ckpt_pos order, a
@@ -440,23 +455,31 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
 // slot while the compute waves work on the other half; one barrier per chunk
 // hands a slot over.  The two roles run separate loops with the same barrier
 // count.  The compute waves load their own dO rows one chunk ahead.
-template <int DK, int CH, int NWC, typename E>
+// VEC (per-channel gate, 16-bit): the operands are chunk prep's gated tiles
+// instead of K and Q rows with per-row factors: K*G (Ks) and scale Q*G (Qs)
+// for dS, K*Gend (KEs) for dU, and Gc per key channel:
+//     dU = A^T dO + (K*Gend) dS'     dS = diag(Gc) dS' + (scale Q*G)^T dO - (K*G)^T dX
+template <int DK, int CH, int NWC, typename E, bool VEC = false>
 __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
     using F = typename EL::frag;
-    using CB = ChunkBlock<E, CH, DK, 1>;
+    using CB = ChunkBlock<E, CH, DK, VEC ? 2 : 1>;
+    static_assert(!VEC || CB::VEC, "the per-channel walk reads the 16-bit gated tiles");
     constexpr int NTP = 64 * NWC, NB = CH / 16, NKB = DK / 16;
     constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value;
+    constexpr int NGF = VEC ? DK : 3 * CH + 4;
     __shared__ __attribute__((aligned(16))) E Ks0[CH * PK];
     __shared__ __attribute__((aligned(16))) E Ks1[CH * PK];
     __shared__ __attribute__((aligned(16))) E Qs0[CH * PK];
     __shared__ __attribute__((aligned(16))) E Qs1[CH * PK];
+    __shared__ __attribute__((aligned(16))) E KE0[VEC ? CH * PK : 8];
+    __shared__ __attribute__((aligned(16))) E KE1[VEC ? CH * PK : 8];
     __shared__ __attribute__((aligned(16))) E TE0[CH * PT];
     __shared__ __attribute__((aligned(16))) E TE1[CH * PT];
     __shared__ __attribute__((aligned(16))) E Am0[CH * PT];
     __shared__ __attribute__((aligned(16))) E Am1[CH * PT];
-    __shared__ __attribute__((aligned(16))) float gt0[3 * CH + 4];   // GX, GO, GE, then Gc
-    __shared__ __attribute__((aligned(16))) float gt1[3 * CH + 4];
+    __shared__ __attribute__((aligned(16))) float gt0[NGF];          // GX, GO, GE, then Gc (VEC: Gc per channel)
+    __shared__ __attribute__((aligned(16))) float gt1[NGF];
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g4 = lane >> 4, r16 = lane & 15;
@@ -476,15 +499,23 @@ __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdPara
         const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
         const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
         RowRegs<E, CH, DK, NTP> rk, rq;
+        RowRegs<E, CH, VEC ? DK : 32, NTP> rke;                 // VEC: K*Gend rows
         BlockRegs<E, CH, NTP> rte, ra;
-        constexpr int NG = 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
+        constexpr int NG = VEC ? DK : 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
         float gv[GPT];
         auto fetch = [&](int c) __attribute__((always_inline)) {
             const int64_t t0 = u.bos + (int64_t)c * CH;
             const int clen = clen_of(c);
-            rk.load(kg + t0 * sqk, sqk, clen, ptid);
-            rq.load(qg + t0 * sqk, sqk, clen, ptid);
             const char *blkb = reinterpret_cast<const char *>(p.blocks) + ((u.cbase + c) * H + h) * CB::BYTES;
+            if constexpr (VEC) {
+                const E *tiles = reinterpret_cast<const E *>(blkb) + CB::TEA;      // K*G, scale Q*G, K*Gend
+                rk.load(tiles, DK, CH, ptid);
+                rq.load(tiles + CH * DK, DK, CH, ptid);
+                rke.load(tiles + 2 * CH * DK, DK, CH, ptid);
+            } else {
+                rk.load(kg + t0 * sqk, sqk, clen, ptid);
+                rq.load(qg + t0 * sqk, sqk, clen, ptid);
+            }
             rte.load(reinterpret_cast<const E *>(blkb), ptid);
             ra.load(reinterpret_cast<const E *>(blkb) + CH * CH, ptid);
 #pragma unroll
@@ -496,8 +527,14 @@ __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdPara
         auto put = [&](auto tag, int c) __attribute__((always_inline)) {
             constexpr int SL = decltype(tag)::value;
             const int clen = clen_of(c);
-            rk.store(SL ? Ks1 : Ks0, PK, clen, ptid);
-            rq.store(SL ? Qs1 : Qs0, PK, clen, ptid);
+            if constexpr (VEC) {
+                rk.store_unpaired(SL ? Ks1 : Ks0, PK, ptid);
+                rq.store(SL ? Qs1 : Qs0, PK, CH, ptid);
+                rke.store_unpaired(SL ? KE1 : KE0, PK, ptid);
+            } else {
+                rk.store(SL ? Ks1 : Ks0, PK, clen, ptid);
+                rq.store(SL ? Qs1 : Qs0, PK, clen, ptid);
+            }
             rte.store(SL ? TE1 : TE0, PT, ptid);
             ra.store(SL ? Am1 : Am0, PT, ptid);
 #pragma unroll
@@ -554,6 +591,7 @@ __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdPara
         constexpr int SL = decltype(tag)::value;
         const E *Ks = SL ? Ks1 : Ks0;
         const E *Qs = SL ? Qs1 : Qs0;
+        const E *KEs = VEC ? (SL ? KE1 : KE0) : Ks;
         const E *TEm = SL ? TE1 : TE0;
         const E *Am = SL ? Am1 : Am0;
         const float *gt = SL ? gt1 : gt0;
@@ -578,14 +616,14 @@ __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdPara
             for (int I = 0; I < NB; ++I) dOb[I] = EL::cvt(dO[I]);
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) dSb[kt] = EL::cvt(dS[kt]);
-            // dU = A^T dO + diag(GE) K dS'
+            // dU = A^T dO + diag(GE) K dS'   (VEC: (K*Gend) dS')
             F Yb[NB];
 #pragma unroll
             for (int I = 0; I < NB; ++I) {
                 f32x4 Y = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
-                    [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
+                    [&](int kt) { return ld_frag<E>(KEs + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return dSb[kt]; });
-                Y *= ld4(gt + 2 * CH + 16 * I + 4 * g4);
+                if constexpr (!VEC) Y *= ld4(gt + 2 * CH + 16 * I + 4 * g4);
                 Y = contract(Y, NB, [&](int kb) { return ld_colfrag<E>(Am, PT, 16 * kb, 16 * I, lane); },
                              [&](int kb) { return dOb[kb]; });
                 Yb[I] = EL::cvt(Y);
@@ -602,14 +640,19 @@ __global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdPara
                     const int row = 16 * I + 4 * g4 + j;
                     if (row < clen) dvg[(t0 + row) * sv] = EL::from_f(dX[j]);
                 }
-                Ob[I] = EL::cvt(dO[I] * ld4(gt + CH + 16 * I + 4 * g4));
-                Xb[I] = EL::cvt(-dX * ld4(gt + 16 * I + 4 * g4));
+                if constexpr (VEC) {                           // the factors are in the tiles
+                    Ob[I] = EL::cvt(dO[I]);
+                    Xb[I] = EL::cvt(-dX);
+                } else {
+                    Ob[I] = EL::cvt(dO[I] * ld4(gt + CH + 16 * I + 4 * g4));
+                    Xb[I] = EL::cvt(-dX * ld4(gt + 16 * I + 4 * g4));
+                }
             }
-            // dS = Gc dS' + Q^T diag(GO) dO - K^T diag(GX) dX
-            const float gc = gt[3 * CH];
+            // dS = Gc dS' + Q^T diag(GO) dO - K^T diag(GX) dX   (VEC: Gc per key channel, gated tiles)
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) {
-                f32x4 s = contract(dS[kt] * gc, NB,
+                const f32x4 dsg = VEC ? dS[kt] * ld4(gt + 16 * kt + 4 * g4) : dS[kt] * gt[3 * CH];
+                f32x4 s = contract(dsg, NB,
                     [&](int kb) { return ld_colfrag<E>(Qs, PK, 16 * kb, 16 * kt, lane); },
                     [&](int kb) { return Ob[kb]; });
                 dS[kt] = contract(s, NB,
@@ -666,14 +709,21 @@ struct GradLayout {
 // Eight waves, two per SIMD: the kernel's phases are chains of short products
 // with LDS round trips in between, and a second wave on each SIMD covers them
 // (one workgroup per CU: its LDS is above half of the CU's).
-template <int DK, int CH, typename E>
+//
+// VEC (per-channel gate, 16-bit): only the staging and the column phase run,
+// with chunk prep's gated tiles K*G in place of K (P = (K*G) S, X = V - P) and
+// K*Gend in place of Q's slot (dU = A^T dO + (K*Gend) dS'); the sums over dv
+// (dO S^T, dX S^T, U dS'^T, dO U^T, dU X^T, and per key channel the sum of
+// S * dS') go to p.gw for chunk_grad_vec_kernel.
+template <int DK, int CH, typename E, bool VEC = false>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 chunk_grad_kernel(const ChunkBwdParams p) {
     using L = GradLayout<DK, CH, E>;
     static_assert(L::FITS, "LDS budget exceeded");
     using EL = Elem<E>;
     using F = typename EL::frag;
-    using CB = ChunkBlock<E, CH, DK, 1>;
+    using CB = ChunkBlock<E, CH, DK, VEC ? 2 : 1>;
+    static_assert(!VEC || CB::VEC, "the per-channel column phase reads the 16-bit gated tiles");
     constexpr int NT = 512, NW = 8, NB = CH / 16, NKB = DK / 16, NBH = NB / 2;
     constexpr int NCW = L::NCW, DVB = L::DVB, NKD = DVB / 16;
     constexpr int PK = L::PK, PT = L::PT, PV = L::PV, PF = L::PF;
@@ -728,16 +778,23 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     const E *dhsb = reinterpret_cast<const E *>(p.dhs) + (slot * H + h) * DK * DV;
 
     // ---- stage: every load of the chunk issued at once --------------------
+    // (VEC: Ks holds K*G and Qs K*Gend, from the gated tiles)
     RowRegs<E, CH, DK, NT> rk, rq;
     BlockRegs<E, CH, NT> ra, rte;                              // A, TE
-    rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
-    rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+    if constexpr (VEC) {
+        rk.load(TEb + CB::TEA, DK, CH, tid);
+        rq.load(TEb + CB::TEA + 2 * CH * DK, DK, CH, tid);
+    } else {
+        rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+        rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+    }
     ra.load(Ab, tid);
     rte.load(TEb, tid);
     const int tc = tid < CH ? tid : 0, tg = tc < clen ? tc : 0;
-    const float gx_v = gf[tc], go_v = gf[CH + tc], ge_v = gf[2 * CH + tc], gc_v = gf[3 * CH];
-    const float be_v = p.beta[(t0 + tg) * H + h];
-    const float g_v = p.g ? p.g[(t0 + (lane < clen ? lane : 0)) * H + h] : 0.f;
+    const float gx_v = VEC ? 0.f : gf[tc], go_v = VEC ? 0.f : gf[CH + tc], ge_v = VEC ? 0.f : gf[2 * CH + tc];
+    const float gc_v = VEC ? 0.f : gf[3 * CH];
+    const float be_v = VEC ? 0.f : p.beta[(t0 + tg) * H + h];
+    const float g_v = (!VEC && p.g) ? p.g[(t0 + (lane < clen ? lane : 0)) * H + h] : 0.f;
     const int Iw = wave % NB, J0 = (wave / NB) * JPW;          // this wave's C x DK tiles (Iw, J0 + s)
     auto tile_of = [&](int l, int &I, int &J) __attribute__((always_inline)) {
         I = 0;
@@ -783,11 +840,17 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         cdX.store(dXs, PV, clen, tid, ncol);
     };
     colload(0);
-    rk.store(Ks, PK, clen, tid);
-    rq.store(Qs, PK, clen, tid);
+    if constexpr (VEC) {
+        rk.store_unpaired(Ks, PK, tid);
+        rq.store_unpaired(Qs, PK, tid);
+        if (tid < DK) sm[tid] = 0.f;                           // per-channel sums of S * dS'
+    } else {
+        rk.store(Ks, PK, clen, tid);
+        rq.store(Qs, PK, clen, tid);
+    }
     ra.store(Am, PT, tid);
     rte.store(TEs, PT, tid);
-    if (tid < CH) {
+    if (!VEC && tid < CH) {
         gx[tid] = gx_v;
         go[tid] = go_v;
         ge[tid] = ge_v;
@@ -795,11 +858,11 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         dgam[tid] = 0.f;
         dbet[tid] = 0.f;
     }
-    if (tid == 0) {
+    if (!VEC && tid == 0) {
         misc[0] = gc_v;
         misc[1] = 0.f;
     }
-    if (wave == 0) {                                           // gamma: in-chunk inclusive sum of g
+    if (!VEC && wave == 0) {                                   // gamma: in-chunk inclusive sum of g
         float x = lane < clen ? g_v : 0.f;
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) {
@@ -819,6 +882,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 #pragma unroll
     for (int s = 0; s < LPW; ++s) aA[s] = aT[s] = f32x4{0.f, 0.f, 0.f, 0.f};
     float gcacc = 0.f;
+    float gcv[VEC ? NKB : 1][4] = {};                          // VEC: S * dS' per key channel of this lane
     const int ndb = (DV + DVB - 1) / DVB;
     const int cw = 16 * cwave + r16;                           // column within the block
     for (int db = 0; db < ndb; ++db) {
@@ -834,7 +898,12 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 dSb[kt] = ld_frag<E>(dSs + cw * PK + 16 * kt + 4 * g4);
                 if (half == 0) {
                     const f32x4 a = EL::tof(Sb[kt]), b = EL::tof(dSb[kt]);
-                    gcacc += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+                    if constexpr (VEC) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) gcv[kt][j] += a[j] * b[j];
+                    } else {
+                        gcacc += a[0] * b[0] + a[1] * b[1] + a[2] * b[2] + a[3] * b[3];
+                    }
                 }
             }
 #pragma unroll
@@ -844,11 +913,16 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                     [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return Sb[kt]; });
                 const f32x4 P2 = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NKB,
-                    [&](int kt) { return ld_frag<E>(Ks + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
+                    [&](int kt) { return ld_frag<E>((VEC ? Qs : Ks) + (16 * I + r16) * PK + 16 * kt + 4 * g4); },
                     [&](int kt) { return dSb[kt]; });
                 const f32x4 V = EL::tof(ld_colfrag<E>(Vs, PV, 16 * I, 16 * cwave, lane));
-                st_frag<E>(Xs + cw * PT + 16 * I + 4 * g4, EL::cvt(V - ld4(gx + 16 * I + 4 * g4) * P));
-                Y0[ii] = ld4(ge + 16 * I + 4 * g4) * P2;
+                if constexpr (VEC) {
+                    st_frag<E>(Xs + cw * PT + 16 * I + 4 * g4, EL::cvt(V - P));
+                    Y0[ii] = P2;
+                } else {
+                    st_frag<E>(Xs + cw * PT + 16 * I + 4 * g4, EL::cvt(V - ld4(gx + 16 * I + 4 * g4) * P));
+                    Y0[ii] = ld4(ge + 16 * I + 4 * g4) * P2;
+                }
             }
         }
         __syncthreads();                                       // X of both halves in LDS
@@ -897,6 +971,50 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         }
     }
     __syncthreads();                                           // the region now holds the CH x CH phase
+
+    if constexpr (VEC) {
+        // the sums over dv for chunk_grad_vec_kernel
+        float *gwb = p.gw + (slot * H + h) * grad_vec_work_floats(CH, DK);
+        float *gQ = gwb, *gX = gwb + CH * DK, *gE = gwb + 2 * CH * DK;
+        float *gA = gwb + 3 * CH * DK, *gT = gA + CH * CH, *gC = gT + CH * CH;
+#pragma unroll
+        for (int s = 0; s < JPW; ++s) {
+            const int d = 16 * (J0 + s) + r16;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 16 * Iw + 4 * g4 + j;
+                gQ[i * DK + d] = aQ[s][j];
+                gX[i * DK + d] = aX[s][j];
+                gE[i * DK + d] = aE[s][j];
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < LPW; ++s) {
+            const int l = wave + NW * s;
+            if (l < NL) {
+                int I, J;
+                tile_of(l, I, J);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 16 * I + 4 * g4 + j, jj = 16 * J + r16;
+                    gA[i * CH + jj] = aA[s][j];
+                    gT[i * CH + jj] = aT[s][j];
+                }
+            }
+        }
+        if (half == 0 && colw_ok) {
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float t = sum16(gcv[kt][j]);         // over this wave's 16 columns
+                    if (r16 == 0) atomicAdd(&sm[16 * kt + 4 * g4 + j], t);
+                }
+        }
+        __syncthreads();
+        if (tid < DK) gC[tid] = sm[tid];
+        return;
+    }
 
     // ---- CH x CH phase ----------------------------------------------------
     // Every matrix is written tile by tile over the lower tiles (W_A and WS
@@ -1114,6 +1232,212 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 }
 
 // ===========================================================================
+// chunk_grad_vec_kernel: dQ, dK, dbeta, dg of one (chunk, head), per-channel gate
+// ===========================================================================
+// With the per-channel gate the CH x CH products are gated per key channel c,
+// E_ij[c] = exp(gamma_i[c] - gamma_j[c]) (i >= j, so E <= 1):
+//     N_ij = sum_c k_i[c] k_j[c] E_ij[c] (i > j)      A_ij = scale sum_c q_i[c] k_j[c] E_ij[c] (i >= j)
+// and the other gated operands are the tiles K*G = k e^gamma, scale Q*G and
+// K*Gend = k e^(gamma_C - gamma).  From dA, dTE and the dv sums the column phase
+// left in p.gw (chunk_grad_kernel<VEC>) and N (chunk prep):
+//     T0 = I - TE N,  Z = T0^T dTE,  dM = -strict_lower(Z TE^T),  dN = diag(beta) dM,
+//     dbeta_i = Z_ii + sum_j dM_ij N_ij,   W_A = scale dA
+//     dq_i = sum_j W_A_ij k_j E_ij + scale e^gamma_i (dO S^T)_i
+//     dk_i = sum_j dN_ij k_j E_ij + sum_j' (W_A_j'i q_j' + dN_j'i k_j') E_j'i
+//            - e^gamma_i (dX S^T)_i + e^(gamma_C - gamma_i) (U dS'^T)_i
+//     dgamma_i = q_i (sum_j W_A_ij k_j E_ij) + k_i (sum_j dN_ij k_j E_ij)
+//                - k_i (sum_j' (W_A_j'i q_j' + dN_j'i k_j') E_j'i)
+//                + (scale q e^gamma) (dO S^T) - (k e^gamma) (dX S^T) - (k e^(gamma_C - gamma)) (U dS'^T)
+//     dgamma_C += sum_i (k e^(gamma_C - gamma))_i (U dS'^T)_i + e^gamma_C sum_cols S dS'
+//     dg_t = dgamma_C + sum_{i >= t} dgamma_i            (all per key channel)
+// The gated sums run exactly, one exponential per (i, j, c) and no
+// factorisation, so no decay range can overflow them.  Thread (c, row group)
+// owns key channel c of rows rg, rg + NRG, ...; the CH x CH algebra runs with
+// thread (i, jl) owning row i, columns jl, jl + 8, ...
+template <int DK, int CH, typename E>
+__global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParams p) {
+    using EL = Elem<E>;
+    using CB = ChunkBlock<E, CH, DK, 2>;
+    static_assert(CB::VEC && CH == 64, "per-channel gated tiles, 64-token chunks");
+    constexpr int NT = 512, NB = CH / 16, NRG = NT / DK, RPT = CH / NRG, CPT = CH / 8;
+    constexpr int FF = CH * CH;
+    static_assert(NT % DK == 0 && CH % NRG == 0, "thread layout");
+    __shared__ __attribute__((aligned(16))) E qs[CH * DK];
+    __shared__ __attribute__((aligned(16))) E ks[CH * DK];
+    __shared__ __attribute__((aligned(16))) float gms[CH * DK];     // gamma, later dgamma
+    __shared__ __attribute__((aligned(16))) float te[FF];           // TE (lower)
+    __shared__ __attribute__((aligned(16))) float nn[FF];           // N (strict lower)
+    __shared__ __attribute__((aligned(16))) float b1[FF];           // T0, then Z
+    __shared__ __attribute__((aligned(16))) float b2[FF];           // dTE, then dN
+    __shared__ __attribute__((aligned(16))) float b3[FF];           // W_A
+    __shared__ float bet[CH], dbet[CH], dgc[DK];
+
+    const int tid = threadIdx.x;
+    const int c = tid % DK, rg = tid / DK;                   // channel phase
+    const int ri = tid >> 3, jl = tid & 7;                   // CH x CH phase: row ri, columns jl + 8 m
+    const int H = p.H;
+    const int h = blockIdx.x % H;
+    const int64_t slot = blockIdx.x / H;
+    int seq;
+    int64_t cin;
+    if (!locate_chunk(p.geo, slot, seq, cin)) return;
+    int64_t bos, eos;
+    seq_bounds(p.geo, seq, bos, eos);
+    const int64_t t0 = bos + cin * CH;
+    const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
+    const int64_t sqk = (int64_t)H * DK;
+    const char *blkb = reinterpret_cast<const char *>(p.blocks) + (slot * H + h) * CB::BYTES;
+    const E *TEb = reinterpret_cast<const E *>(blkb);
+    const float *nb = p.nbuf + (slot * H + h) * FF;
+    const float *gwb = p.gw + (slot * H + h) * grad_vec_work_floats(CH, DK);
+    const float *gQ = gwb, *gX = gwb + CH * DK, *gE = gwb + 2 * CH * DK;
+    const float *gA = gwb + 3 * CH * DK, *gT = gA + FF, *gC = gT + FF;
+
+    // ---- stage -------------------------------------------------------------
+    {
+        RowRegs<E, CH, DK, NT> rk, rq;
+        rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+        rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+        float gv[RPT];
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int i = rg + NRG * r;
+            gv[r] = i < clen ? p.g[(t0 + i) * sqk + (int64_t)h * DK + c] : 0.f;
+        }
+        rk.store(ks, DK, clen, tid);
+        rq.store(qs, DK, clen, tid);
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) gms[(rg + NRG * r) * DK + c] = gv[r];
+#pragma unroll
+        for (int m = 0; m < CPT; ++m) {
+            const int j = jl + 8 * m;
+            te[ri * CH + j] = j <= ri ? EL::to_f(TEb[blk_pos<NB>(ri, j)]) : 0.f;
+            nn[ri * CH + j] = j < ri ? nb[ri * CH + j] : 0.f;
+            b2[ri * CH + j] = j <= ri ? gT[ri * CH + j] : 0.f;
+            b3[ri * CH + j] = j <= ri ? p.scale * gA[ri * CH + j] : 0.f;
+        }
+        if (tid < CH) {
+            bet[tid] = tid < clen ? p.beta[(t0 + tid) * H + h] : 0.f;
+            dbet[tid] = 0.f;
+        }
+        if (tid < DK) dgc[tid] = 0.f;
+    }
+    __syncthreads();
+    if (rg == 0) {                                           // gamma: in-chunk inclusive sums, per channel
+        float acc = 0.f;
+        for (int i = 0; i < CH; ++i) {
+            acc += gms[i * DK + c];
+            gms[i * DK + c] = acc;
+        }
+    }
+    // T0 = I - TE N (lower): T0_ij = [i == j] - sum_{j < m <= i} TE_im N_mj
+    {
+        float t0v[CPT];
+#pragma unroll
+        for (int m = 0; m < CPT; ++m) {
+            const int j = jl + 8 * m;
+            float acc = 0.f;
+            for (int mm = j + 1; mm <= ri; ++mm) acc += te[ri * CH + mm] * nn[mm * CH + j];
+            t0v[m] = j <= ri ? (ri == j ? 1.f : 0.f) - acc : 0.f;
+        }
+#pragma unroll
+        for (int m = 0; m < CPT; ++m) b1[ri * CH + jl + 8 * m] = t0v[m];
+    }
+    __syncthreads();
+    // Z = T0^T dTE (lower): Z_ij = sum_{m >= i} T0_mi dTE_mj;  dbeta_i += Z_ii
+    {
+        float zv[CPT];
+#pragma unroll
+        for (int m = 0; m < CPT; ++m) {
+            const int j = jl + 8 * m;
+            float acc = 0.f;
+            if (j <= ri)
+                for (int mm = ri; mm < CH; ++mm) acc += b1[mm * CH + ri] * b2[mm * CH + j];
+            zv[m] = acc;
+        }
+        __syncthreads();                                     // T0 and dTE are consumed
+#pragma unroll
+        for (int m = 0; m < CPT; ++m) {
+            const int j = jl + 8 * m;
+            b1[ri * CH + j] = zv[m];
+            if (j == ri) dbet[ri] += zv[m];                  // one thread owns (ri, ri)
+        }
+    }
+    __syncthreads();
+    // dM = -strict_lower(Z TE^T): dM_ij = -sum_{m <= j} Z_im TE_jm;  dbeta_i += sum_j dM_ij N_ij;
+    // dN = diag(beta) dM -> b2
+    {
+        float dnv[CPT], rb = 0.f;
+#pragma unroll
+        for (int m = 0; m < CPT; ++m) {
+            const int j = jl + 8 * m;
+            float acc = 0.f;
+            if (j < ri)
+                for (int mm = 0; mm <= j; ++mm) acc += b1[ri * CH + mm] * te[j * CH + mm];
+            const float dm = j < ri ? -acc : 0.f;
+            rb += dm * nn[ri * CH + j];
+            dnv[m] = bet[ri] * dm;
+        }
+        rb += __shfl_xor(rb, 1);
+        rb += __shfl_xor(rb, 2);
+        rb += __shfl_xor(rb, 4);
+#pragma unroll
+        for (int m = 0; m < CPT; ++m) b2[ri * CH + jl + 8 * m] = dnv[m];
+        __syncthreads();                                     // the Z_ii terms are in dbet
+        if (jl == 0) dbet[ri] += rb;
+    }
+    __syncthreads();
+
+    // ---- the gated sums and the direct terms, per (row, channel) -------------
+    const float gC_ = gms[(CH - 1) * DK + c];                // gamma_C (rows past the end add no decay)
+    float dgam[RPT];
+    float dgc_acc = 0.f;
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+        const int i = rg + NRG * r;
+        dgam[r] = 0.f;
+        if (i >= clen) continue;
+        const float qi = EL::to_f(qs[i * DK + c]), ki = EL::to_f(ks[i * DK + c]), gi = gms[i * DK + c];
+        // i side: sum_j W_A_ij k_j E_ij, sum_j dN_ij k_j E_ij
+        float sa = 0.f, sn = 0.f;
+        for (int j = 0; j <= i; ++j) {
+            const float e = __expf(gi - gms[j * DK + c]) * EL::to_f(ks[j * DK + c]);
+            sa += b3[i * CH + j] * e;
+            sn += b2[i * CH + j] * e;                        // dN is zero on the diagonal
+        }
+        // j side (this row as j): sum_i' (W_A_i'i q_i' + dN_i'i k_i') E_i'i
+        float tj = 0.f;
+        for (int i2 = i; i2 < clen; ++i2) {
+            const float e = __expf(gms[i2 * DK + c] - gi);
+            tj += (b3[i2 * CH + i] * EL::to_f(qs[i2 * DK + c]) + b2[i2 * CH + i] * EL::to_f(ks[i2 * DK + c])) * e;
+        }
+        // direct terms
+        const float eg = __expf(gi), egc = __expf(gC_ - gi);
+        const float dqg = gQ[i * DK + c], dxs = gX[i * DK + c], dke = gE[i * DK + c];
+        const float dq = sa + p.scale * eg * dqg;
+        const float dk = sn + tj - eg * dxs + egc * dke;
+        dgam[r] = qi * sa + ki * sn - ki * tj + p.scale * qi * eg * dqg - ki * eg * dxs - ki * egc * dke;
+        dgc_acc += ki * egc * dke;
+        reinterpret_cast<E *>(p.dq)[(t0 + i) * sqk + (int64_t)h * DK + c] = EL::from_f(dq);
+        reinterpret_cast<E *>(p.dk)[(t0 + i) * sqk + (int64_t)h * DK + c] = EL::from_f(dk);
+    }
+    atomicAdd(&dgc[c], dgc_acc);
+    __syncthreads();                                         // every read of gamma is done
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) gms[(rg + NRG * r) * DK + c] = dgam[r];
+    __syncthreads();
+    if (rg == 0) {
+        // dg_t = dgamma_C + sum_{i >= t} dgamma_i, with dgamma_C = (the U dS'^T terms) + e^gamma_C sum S dS'
+        float acc = dgc[c] + __expf(gC_) * gC[c];
+        for (int i = clen - 1; i >= 0; --i) {
+            acc += gms[i * DK + c];
+            if (p.dg) p.dg[(t0 + i) * sqk + (int64_t)h * DK + c] = acc;
+        }
+    }
+    if (tid < clen) p.dbeta[(t0 + tid) * H + h] = dbet[tid];
+}
+
+// ===========================================================================
 // launch
 // ===========================================================================
 template <int DK, int CH, typename E>
@@ -1137,18 +1461,50 @@ static hipError_t run_bwd(ChunkBwdParams p, bool saved, hipStream_t stream) {
     return hipGetLastError();
 }
 
-hipError_t chunk_bwd(int dtype, int dk, int chunk, const ChunkParams &fwd, ChunkBwdParams p, int32_t *table,
-                     bool saved, hipStream_t stream) {
+// Per-channel gate: the entry states come from the forward's state kernel
+// (chunk_fwd with ChunkParams::hs), then the dS walk on the gated tiles, the
+// column phase into p.gw and the per-channel gated gradients.
+template <int DK, int CH, typename E>
+static hipError_t run_bwd_vec(ChunkBwdParams p, hipStream_t stream) {
+    const int64_t units = (int64_t)p.geo.n_seqs * p.H;
+    if (units > 0) {
+        p.n_tiles = (p.DV + 31) / 32;
+        hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E, true>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
+                           dim3(256), 0, stream, p);
+    }
+    const int64_t grad_blocks = (int64_t)p.n_chunk_slots * p.H;
+    if (grad_blocks > 0) {
+        hipLaunchKernelGGL((chunk_grad_kernel<DK, CH, E, true>), dim3((unsigned)grad_blocks), dim3(512), 0, stream, p);
+        hipLaunchKernelGGL((chunk_grad_vec_kernel<DK, CH, E>), dim3((unsigned)grad_blocks), dim3(512), 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
+hipError_t chunk_bwd(int dtype, int dk, int chunk, int gate_vector, const ChunkParams &fwd, ChunkBwdParams p,
+                     int32_t *table, bool saved, hipStream_t stream) {
     if (p.geo.n_seqs == 0) return hipSuccess;
+    const bool vec = gate_vector != 0;
+    if (vec && (dtype == 0 || chunk != 64 || !fwd.hs || !fwd.nout || !p.nbuf || !p.gw))
+        return hipErrorInvalidValue;                           // the per-channel backward: 16-bit, 64-token chunks
     // TE, A and the gate factors of every chunk, as the forward built them
-    // (already in the workspace after a saving forward)
+    // (already in the workspace after a saving forward); the per-channel gate
+    // also runs the forward's state kernel for the entry states
     if (!saved) {
-        hipError_t e = chunk_fwd(dtype, dk, chunk, 0, fwd, table, CHUNK_PREP, stream);
+        hipError_t e = chunk_fwd(dtype, dk, chunk, vec ? 1 : 0, fwd, table, vec ? CHUNK_PREP | CHUNK_STATE : CHUNK_PREP,
+                                 stream);
         if (e != hipSuccess) return e;
     }
     if (p.geo.cu) {
         p.geo.chunk_offs = table + 2 * p.geo.n_seqs;
         p.geo.order = table + 3 * p.geo.n_seqs + 1;
+    }
+    if (vec) {
+        if (dtype == 1) {
+            if (dk == 64) return run_bwd_vec<64, 64, __bf16>(p, stream);
+            return run_bwd_vec<128, 64, __bf16>(p, stream);
+        }
+        if (dk == 64) return run_bwd_vec<64, 64, _Float16>(p, stream);
+        return run_bwd_vec<128, 64, _Float16>(p, stream);
     }
 #define VGDR_BWD(DK_, CH_, E_) return run_bwd<DK_, CH_, E_>(p, saved, stream);
     if (dtype == 1) {

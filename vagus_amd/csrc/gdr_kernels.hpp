@@ -86,27 +86,31 @@ struct ChunkParams {
     float scale;
     Fusion fz;
     const void *w;                // [n_tokens, H, dk] write vectors in place of beta k (per-channel gate), or NULL
-    void *hs;                     // [chunk slots, H, dv, dk] entry states for the backward (16-bit, scalar gate), or NULL
+    void *hs;                     // [chunk slots, H, dv, dk] entry states for the backward (16-bit), or NULL
+    float *nout;                  // per-channel gate: [chunk slots, H, CH, CH] N = strict_lower(gated K K^T)
+                                  // for the backward (chunk prep writes the lower tiles), or NULL
 };
 
-// Backward of the chunked scan (scalar gate or none, delta rule).  q, k are the
-// normalised inputs the forward scanned; the gradients come back in the
-// element type (dq, dk, dv) or fp32 (dg, dbeta, dh0).
+// Backward of the chunked scan (scalar gate, per-channel gate or none, delta
+// rule).  q, k are the normalised inputs the forward scanned; the gradients
+// come back in the element type (dq, dk, dv) or fp32 (dg, dbeta, dh0).
 struct ChunkBwdParams {
     SeqGeom geo;
     const void *q, *k, *v;        // [n_tokens, H, dk|dv] in the element type
-    const float *g;               // [n_tokens, H] or NULL (no gate)
+    const float *g;               // [n_tokens, H] or [n_tokens, H, dk] (per-channel); NULL = no gate
     const float *beta;            // [n_tokens, H]
     const void *dout;             // [n_tokens, H, dv] gradient of o
     const float *h0;              // [n_seqs, H, dk, dv] or NULL
     const float *dht;             // [n_seqs, H, dk, dv] gradient of the final state, or NULL
     void *dq, *dk, *dv;           // [n_tokens, H, dk|dv]
-    float *dg;                    // [n_tokens, H] (NULL without a gate)
+    float *dg;                    // [n_tokens, H] or [n_tokens, H, dk] (NULL without a gate)
     float *dbeta;                 // [n_tokens, H]
     float *dh0;                   // [n_seqs, H, dk, dv] or NULL
     const void *blocks;           // chunk_prep's per-(chunk, head) blocks
     void *hs;                     // [chunk slots, H, dv, dk] each chunk's entry state (element type, transposed)
     void *dhs;                    // [chunk slots, H, dv, dk] gradient of each chunk's exit state (same)
+    const float *nbuf;            // per-channel gate: chunk prep's N (ChunkParams::nout)
+    float *gw;                    // per-channel gate: [chunk slots, H, grad_vec_work_floats] the column phase's sums
     int H, DV;
     int n_tiles;                  // dv tiles of the walk kernels (set by the launcher)
     int n_chunk_slots;
@@ -170,8 +174,15 @@ int64_t chunk_blocks_bytes(int dtype, int chunk, int64_t chunk_slots, int64_t H,
 // gradients.  table: the packed-batch schedule (as chunk_fwd).  saved: a
 // forward with ChunkParams::hs = p.hs already left the schedule, the blocks
 // and the entry states in the workspace; the prep and the entry walk are skipped.
-hipError_t chunk_bwd(int dtype, int dk, int chunk, const ChunkParams &fwd, ChunkBwdParams p, int32_t *table,
-                     bool saved, hipStream_t stream);
+hipError_t chunk_bwd(int dtype, int dk, int chunk, int gate_vector, const ChunkParams &fwd, ChunkBwdParams p,
+                     int32_t *table, bool saved, hipStream_t stream);
+
+// the per-channel-gate backward's per-(chunk, head) work area (fp32 elements):
+// dO S^T, dX S^T, U dS'^T (CH x DK each), dO U^T and dU X^T (CH x CH each,
+// lower tiles), and per key channel the sum over columns of S * dS' (DK)
+constexpr int64_t grad_vec_work_floats(int chunk, int dk) {
+    return 3 * (int64_t)chunk * dk + 2 * (int64_t)chunk * chunk + dk;
+}
 
 // the token-recurrence backward: the forward and backward walks per (sequence,
 // head, column tile), the per-block gradients, then the per-(token, head)

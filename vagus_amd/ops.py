@@ -244,20 +244,34 @@ class _Call:
         return S[:, :, :self.dk, :self.dv].contiguous()
 
 
+def _gate_of(g):
+    """The gate form of a log-decay tensor: None, (B, T, H) or (B, T, H, dk)."""
+    return 'none' if g is None else ('vector' if g.dim() == 4 else 'scalar')
+
+
+def _chunk_bwd_covers(q, g, chunk_size):
+    """Whether vgdr_chunk_bwd takes this delta-rule call: a scalar gate or
+    none at any dtype, a per-channel gate with 16-bit q, k, v in 64-token
+    chunks (the token-recurrence backward takes the rest)."""
+    return g is None or g.dim() == 3 or (q.dtype != torch.float32 and chunk_size > 32)
+
+
 def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, cu_seqlens=None,
                                chunk_size=64, saved_workspace=None):
-    """Backward of chunk_gated_delta_rule without autograd (vgdr_chunk_bwd):
-    the gradients of (o, final_state) under the cotangents do (and dht, None =
-    zero) with respect to q, k, v, g, beta and initial_state, for the delta
-    rule with a scalar gate (g (B, T, H)) or none (g None).  q, k as the
-    forward scanned them (normalised), beta in [0, 1].  Returns (dq, dk, dv,
-    dg, dbeta, dh0) in the inputs' dtypes; dg is None without a gate and dh0
-    None without an initial state.  The gradients the reference's training
-    takes through chunk_scan (linear_attention.py:237-309) or fla's backward.
+    """Backward of chunk_gated_delta_rule / chunk_kda without autograd
+    (vgdr_chunk_bwd): the gradients of (o, final_state) under the cotangents
+    do (and dht, None = zero) with respect to q, k, v, g, beta and
+    initial_state, for the delta rule with a scalar gate (g (B, T, H)), a
+    per-channel gate (g (B, T, H, dk); 16-bit q, k, v, 64-token chunks) or
+    none (g None).  q, k as the forward scanned them (normalised), beta in
+    [0, 1], g the log-decay.  Returns (dq, dk, dv, dg, dbeta, dh0) in the
+    inputs' dtypes; dg is None without a gate and dh0 None without an initial
+    state.  The gradients the reference's training takes through chunk_scan /
+    chunk_scan_vec (linear_attention.py:237-309, :312-425) or fla's backward.
     saved_workspace: the workspace a saving forward (_chunk_fwd_saving, same
     inputs) filled; the backward then skips rebuilding the chunk blocks and
     the per-chunk entry states."""
-    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate='scalar' if g is not None else 'none', delta=True,
+    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=_gate_of(g), delta=True,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
@@ -269,7 +283,8 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     new = lambda *shape, dt=torch.float32: torch.empty(*shape, dtype=dt, device=c.device)
     dq, dk = new(c.B, c.T, c.H, c.dkp, dt=c.dtype), new(c.B, c.T, c.H, c.dkp, dt=c.dtype)
     dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
-    dg = new(c.B, c.T, c.H) if g is not None else None
+    vec = c.gate_kind == _lib.VGDR_GATE_VECTOR
+    dg = None if g is None else (new(c.B, c.T, c.H, c.dkp) if vec else new(c.B, c.T, c.H))
     db = new(c.B, c.T, c.H)
     dS0 = new(c.N, c.H, c.dkp, c.dvp) if initial_state is not None else None
     L = _lib.load()
@@ -288,6 +303,7 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
                                     c.N, scale, int(chunk_size), _stream(c.device)))
     if c.dkp != c.dk:
         dq, dk = dq[..., :c.dk], dk[..., :c.dk]
+        dg = dg[..., :c.dk] if vec else dg
     if c.dvp != c.dv:
         dv = dv[..., :c.dv]
     if dS0 is not None:
@@ -296,11 +312,11 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
 
 
 def _chunk_fwd_saving(q, k, v, g, beta, initial_state, *, scale, cu_seqlens, chunk_size):
-    """vgdr_chunk_fwd_saving: the chunked forward (16-bit, scalar gate or none,
-    delta rule) run in a backward workspace, which keeps the chunk blocks and
-    every chunk's entry state for vgdr_chunk_bwd_saved.  Returns (o,
-    final_state, workspace)."""
-    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate='scalar' if g is not None else 'none', delta=True,
+    """vgdr_chunk_fwd_saving: the chunked forward (16-bit, any gate, delta
+    rule) run in a backward workspace, which keeps the chunk blocks and every
+    chunk's entry state for vgdr_chunk_bwd_saved.  Returns (o, final_state,
+    workspace)."""
+    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=_gate_of(g), delta=True,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
     o, S = c.new_output(), c.new_state()
     L = _lib.load()
@@ -401,7 +417,8 @@ class _ScanRule(torch.autograd.Function):
 
 
 class _ChunkDeltaRule(torch.autograd.Function):
-    """The chunked delta rule with a scalar gate or none, differentiable.
+    """The chunked delta rule with a scalar gate, a per-channel gate (16-bit,
+    64-token chunks) or none, differentiable.
     16-bit inputs: forward vgdr_chunk_fwd_saving, which keeps the chunk blocks
     and the per-chunk entry states in the backward's workspace, and backward
     vgdr_chunk_bwd_saved (fla's disable_recompute trade: about 2 dk dv bytes
@@ -416,7 +433,7 @@ class _ChunkDeltaRule(torch.autograd.Function):
             o, S, ctx.ws = _chunk_fwd_saving(q, k, v, g, beta, S0, scale=scale, cu_seqlens=cu,
                                              chunk_size=chunk_size)
         else:
-            o, S = chunk_scan(q, k, v, g, beta, gate='scalar' if g is not None else 'none', delta=True,
+            o, S = chunk_scan(q, k, v, g, beta, gate=_gate_of(g), delta=True,
                               scale=scale, initial_state=S0, output_final_state=True, cu_seqlens=cu,
                               chunk_size=chunk_size)
         ctx.save_for_backward(q, k, v, g, beta, S0, cu)
@@ -447,8 +464,9 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
 
     With grads enabled and an input that requires grad, the fused producers
     (L2 norm, beta sigmoid, gate activation) run in torch, differentiably, and
-    the scan through _ChunkDeltaRule (delta rule, scalar gate or none) or
-    _ScanRule (every other form)."""
+    the scan through _ChunkDeltaRule (delta rule: scalar gate or none, or the
+    per-channel gate with 16-bit inputs in 64-token chunks) or _ScanRule
+    (every other form)."""
     if _wants_grad(q, k, v, g, beta, initial_state):
         if fusion.l2norm:
             q, k = _l2norm_rows(q), _l2norm_rows(k)
@@ -458,7 +476,7 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
             g = _gate_activation_rows(g, fusion)
         scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
         gk = None if gate == 'none' else g
-        if gate == 'vector' or not delta:
+        if not delta or not _chunk_bwd_covers(q, gk, chunk_size):
             o, S = _ScanRule.apply(q, k, v, gk, beta if delta else None, initial_state, None, scale, cu_seqlens,
                                    chunk_size, delta)
         else:
@@ -766,12 +784,6 @@ def fused_recurrent_kda(q, k, v, g, beta, scale=None, initial_state=None, output
     return _recurrent(q, k, v, g, beta, gate='vector', delta=True, scale=scale,
                       initial_state=initial_state, output_final_state=output_final_state,
                       cu_seqlens=cu_seqlens, inplace_final_state=inplace_final_state, fusion=fz)
-
-
-def _gate_of(g) -> str:
-    if g is None:
-        return 'none'
-    return 'vector' if g.dim() == 4 else 'scalar'
 
 
 def hip_scan(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_size: int = 64,
