@@ -1242,38 +1242,55 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 // left in p.gw (chunk_grad_kernel<VEC>) and N (chunk prep):
 //     T0 = I - TE N,  Z = T0^T dTE,  dM = -strict_lower(Z TE^T),  dN = diag(beta) dM,
 //     dbeta_i = Z_ii + sum_j dM_ij N_ij,   W_A = scale dA
-//     dq_i = sum_j W_A_ij k_j E_ij + scale e^gamma_i (dO S^T)_i
-//     dk_i = sum_j dN_ij k_j E_ij + sum_j' (W_A_j'i q_j' + dN_j'i k_j') E_j'i
-//            - e^gamma_i (dX S^T)_i + e^(gamma_C - gamma_i) (U dS'^T)_i
-//     dgamma_i = q_i (sum_j W_A_ij k_j E_ij) + k_i (sum_j dN_ij k_j E_ij)
-//                - k_i (sum_j' (W_A_j'i q_j' + dN_j'i k_j') E_j'i)
+//     SA_i = sum_{j<=i} W_A_ij k_j E_ij     SN_i = sum_{j<i} dN_ij k_j E_ij
+//     TJ_j = sum_{i>=j} (W_A_ij q_i + dN_ij k_i) E_ij                      (per channel)
+//     dq_i = SA_i + scale e^gamma_i (dO S^T)_i
+//     dk_i = SN_i + TJ_i - e^gamma_i (dX S^T)_i + e^(gamma_C - gamma_i) (U dS'^T)_i
+//     dgamma_i = q_i SA_i + k_i SN_i - k_i TJ_i
 //                + (scale q e^gamma) (dO S^T) - (k e^gamma) (dX S^T) - (k e^(gamma_C - gamma)) (U dS'^T)
 //     dgamma_C += sum_i (k e^(gamma_C - gamma))_i (U dS'^T)_i + e^gamma_C sum_cols S dS'
-//     dg_t = dgamma_C + sum_{i >= t} dgamma_i            (all per key channel)
-// The gated sums run exactly, one exponential per (i, j, c) and no
-// factorisation, so no decay range can overflow them.  Thread (c, row group)
-// owns key channel c of rows rg, rg + NRG, ...; the CH x CH algebra runs with
-// thread (i, jl) owning row i, columns jl, jl + 8, ...
+//     dg_t = dgamma_C + sum_{i >= t} dgamma_i
+// SA, SN and TJ are MFMA products over 16-row blocks with one reference row
+// per output block, as chunk prep builds N and A: for output rows in block I,
+// E_ij = e^(gamma_i - gamma_r) e^(gamma_r - gamma_j) with r = 16 I (SA, SN) or
+// r = 16 I + 15 (TJ), so that off the diagonal block both factors are <= 1.
+// Every lane builds its own gated B fragments (its key channel c, rows
+// 16 J + 4 g + 0..3) in registers.  The products run in fp32
+// (v_mfma_f32_16x16x4f32; they are small): dgamma subtracts sums of like
+// size (q SA against k TJ), which 16-bit operands would leave with a
+// correlated error.  On a diagonal block the second factor reaches
+// e^(gamma_16I - gamma_16I+15); a block whose range exceeds 60 nats on any
+// channel takes exact per-pair exponentials there instead.  Wave w owns key-channel tile w % (DK / 16) and row blocks
+// w / (DK / 16) + (8 / (DK / 16)) s; its MFMA output rows and column are the
+// rows and channel whose q, k and gamma it holds, so the epilogue runs in
+// registers.
 template <int DK, int CH, typename E>
 __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
+    using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, 2>;
     static_assert(CB::VEC && CH == 64, "per-channel gated tiles, 64-token chunks");
-    constexpr int NT = 512, NB = CH / 16, NRG = NT / DK, RPT = CH / NRG, CPT = CH / 8;
-    constexpr int FF = CH * CH;
-    static_assert(NT % DK == 0 && CH % NRG == 0, "thread layout");
-    __shared__ __attribute__((aligned(16))) E qs[CH * DK];
-    __shared__ __attribute__((aligned(16))) E ks[CH * DK];
+    constexpr int NT = 512, NW = 8, NB = CH / 16, NRG = NT / DK, RPT = CH / NRG, CPT = CH / 8;
+    constexpr int FF = CH * CH, PW = CH + 4;                          // W pitch (floats)
+    constexpr int NCT = DK / 16, WPC = NW / NCT, IPW = NB / WPC;   // channel tiles, waves per tile, blocks per wave
+    static_assert(NT % DK == 0 && CH % NRG == 0 && NW % NCT == 0 && NB % WPC == 0, "thread layout");
+    constexpr int VE = 16 / (int)sizeof(E), UPR = DK / VE, OUT_N = (CH * UPR + NT - 1) / NT;
+    typedef E V __attribute__((ext_vector_type(VE)));
+    __shared__ __attribute__((aligned(16))) E qs[CH * DK];          // q, later dq
+    __shared__ __attribute__((aligned(16))) E ks[CH * DK];          // k, later dk
     __shared__ __attribute__((aligned(16))) float gms[CH * DK];     // gamma, later dgamma
-    __shared__ __attribute__((aligned(16))) float te[FF];           // TE (lower)
-    __shared__ __attribute__((aligned(16))) float nn[FF];           // N (strict lower)
-    __shared__ __attribute__((aligned(16))) float b1[FF];           // T0, then Z
-    __shared__ __attribute__((aligned(16))) float b2[FF];           // dTE, then dN
-    __shared__ __attribute__((aligned(16))) float b3[FF];           // W_A
+    // the CH x CH algebra's matrices (fp32, pitch PW), then (same memory) the
+    // A operands of the gated sums
+    constexpr int MM = CH * PW, NL = NB * (NB + 1) / 2, LPW = (NL + NW - 1) / NW;   // lower 16 x 16 tiles
+    __shared__ __attribute__((aligned(16))) float alg[4 * MM];
+    float *te = alg, *nn = alg + MM, *b1 = alg + 2 * MM, *b2 = alg + 3 * MM;   // TE, N, T0 then Z, dTE
+    float *wa = alg, *wn = alg + MM;                         // W_A = scale dA (lower), dN (strict lower)
     __shared__ float bet[CH], dbet[CH], dgc[DK];
+    __shared__ float part[NRG][DK];                          // per row group: sums of g, later of dgamma
+    __shared__ int flag[NB];
 
     const int tid = threadIdx.x;
-    const int c = tid % DK, rg = tid / DK;                   // channel phase
+    const int c = tid % DK, rg = tid / DK;                   // channel phases
     const int ri = tid >> 3, jl = tid & 7;                   // CH x CH phase: row ri, columns jl + 8 m
     const int H = p.H;
     const int h = blockIdx.x % H;
@@ -1294,144 +1311,299 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     const float *gA = gwb + 3 * CH * DK, *gT = gA + FF, *gC = gT + FF;
 
     // ---- stage -------------------------------------------------------------
+    float wav[CPT];                                          // W_A at (ri, jl + 8 m), stored after the algebra
     {
         RowRegs<E, CH, DK, NT> rk, rq;
         rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
         rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+        // gamma: inclusive sums over rows rg RPT .. + RPT - 1 here, the earlier groups' totals added below
         float gv[RPT];
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
-            const int i = rg + NRG * r;
+            const int i = rg * RPT + r;
             gv[r] = i < clen ? p.g[(t0 + i) * sqk + (int64_t)h * DK + c] : 0.f;
         }
         rk.store(ks, DK, clen, tid);
         rq.store(qs, DK, clen, tid);
 #pragma unroll
-        for (int r = 0; r < RPT; ++r) gms[(rg + NRG * r) * DK + c] = gv[r];
+        for (int r = 1; r < RPT; ++r) gv[r] += gv[r - 1];
+        part[rg][c] = gv[RPT - 1];
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) gms[(rg * RPT + r) * DK + c] = gv[r];
 #pragma unroll
         for (int m = 0; m < CPT; ++m) {
             const int j = jl + 8 * m;
-            te[ri * CH + j] = j <= ri ? EL::to_f(TEb[blk_pos<NB>(ri, j)]) : 0.f;
-            nn[ri * CH + j] = j < ri ? nb[ri * CH + j] : 0.f;
-            b2[ri * CH + j] = j <= ri ? gT[ri * CH + j] : 0.f;
-            b3[ri * CH + j] = j <= ri ? p.scale * gA[ri * CH + j] : 0.f;
+            te[ri * PW + j] = j <= ri ? EL::to_f(TEb[blk_pos<NB>(ri, j)]) : 0.f;
+            nn[ri * PW + j] = j < ri ? nb[ri * CH + j] : 0.f;
+            b2[ri * PW + j] = j <= ri ? gT[ri * CH + j] : 0.f;
+            wav[m] = j <= ri ? p.scale * gA[ri * CH + j] : 0.f;
         }
         if (tid < CH) {
             bet[tid] = tid < clen ? p.beta[(t0 + tid) * H + h] : 0.f;
             dbet[tid] = 0.f;
         }
         if (tid < DK) dgc[tid] = 0.f;
+        if (tid < NB) flag[tid] = 0;
     }
     __syncthreads();
-    if (rg == 0) {                                           // gamma: in-chunk inclusive sums, per channel
-        float acc = 0.f;
-        for (int i = 0; i < CH; ++i) {
-            acc += gms[i * DK + c];
-            gms[i * DK + c] = acc;
-        }
+    if (rg > 0) {                                            // gamma: in-chunk inclusive sums, per channel
+        float pre = 0.f;
+        for (int r = 0; r < rg; ++r) pre += part[r][c];
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) gms[(rg * RPT + r) * DK + c] += pre;
     }
-    // T0 = I - TE N (lower): T0_ij = [i == j] - sum_{j < m <= i} TE_im N_mj
-    {
-        float t0v[CPT];
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+    const int g4 = lane >> 4, r16 = lane & 15;
+    auto tile_of = [](int l, int &I, int &J) __attribute__((always_inline)) {
+        I = 0;
+        J = l;
+        while (J > I) { J -= I + 1; ++I; }
+    };
+    // T0 = I - TE N over the lower tiles (fp32 MFMA)
 #pragma unroll
-        for (int m = 0; m < CPT; ++m) {
-            const int j = jl + 8 * m;
-            float acc = 0.f;
-            for (int mm = j + 1; mm <= ri; ++mm) acc += te[ri * CH + mm] * nn[mm * CH + j];
-            t0v[m] = j <= ri ? (ri == j ? 1.f : 0.f) - acc : 0.f;
+    for (int s = 0; s < LPW; ++s) {
+        const int l = wave + NW * s;
+        if (l < NL) {
+            int I, J;
+            tile_of(l, I, J);
+            f32x4 t = {0.f, 0.f, 0.f, 0.f};
+            for (int kb = J; kb <= I; ++kb)
+                t = mfma_kb1(ld4(te + (16 * I + r16) * PW + 16 * kb + 4 * g4), col4(nn, PW, 16 * kb + 4 * g4, 16 * J + r16),
+                             t);
+            const int jj = 16 * J + r16;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int i = 16 * I + 4 * g4 + j;
+                b1[i * PW + jj] = jj <= i ? (i == jj ? 1.f : 0.f) - t[j] : 0.f;
+            }
         }
-#pragma unroll
-        for (int m = 0; m < CPT; ++m) b1[ri * CH + jl + 8 * m] = t0v[m];
     }
     __syncthreads();
-    // Z = T0^T dTE (lower): Z_ij = sum_{m >= i} T0_mi dTE_mj;  dbeta_i += Z_ii
-    {
-        float zv[CPT];
+    // blocks whose in-block decay range leaves the factorised form's limit
+    if (rg == 0) {
 #pragma unroll
-        for (int m = 0; m < CPT; ++m) {
-            const int j = jl + 8 * m;
-            float acc = 0.f;
-            if (j <= ri)
-                for (int mm = ri; mm < CH; ++mm) acc += b1[mm * CH + ri] * b2[mm * CH + j];
-            zv[m] = acc;
+        for (int b = 0; b < NB; ++b)
+            if (gms[16 * b * DK + c] - gms[(16 * b + 15) * DK + c] > 60.f) flag[b] = 1;
+    }
+    // Z = T0^T dTE (lower tiles); dbeta_i += Z_ii
+    {
+        f32x4 zt[LPW];
+#pragma unroll
+        for (int s = 0; s < LPW; ++s) {
+            zt[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int l = wave + NW * s;
+            if (l < NL) {
+                int I, J;
+                tile_of(l, I, J);
+                for (int kb = I; kb < NB; ++kb)
+                    zt[s] = mfma_kb1(col4(b1, PW, 16 * kb + 4 * g4, 16 * I + r16),
+                                     col4(b2, PW, 16 * kb + 4 * g4, 16 * J + r16), zt[s]);
+                if (I == J) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (4 * g4 + j == r16) dbet[16 * I + r16] += zt[s][j];     // one lane per diagonal entry
+                }
+            }
         }
         __syncthreads();                                     // T0 and dTE are consumed
 #pragma unroll
-        for (int m = 0; m < CPT; ++m) {
-            const int j = jl + 8 * m;
-            b1[ri * CH + j] = zv[m];
-            if (j == ri) dbet[ri] += zv[m];                  // one thread owns (ri, ri)
+        for (int s = 0; s < LPW; ++s) {
+            const int l = wave + NW * s;
+            if (l < NL) {
+                int I, J;
+                tile_of(l, I, J);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) b1[(16 * I + 4 * g4 + j) * PW + 16 * J + r16] = zt[s][j];
+            }
         }
     }
     __syncthreads();
-    // dM = -strict_lower(Z TE^T): dM_ij = -sum_{m <= j} Z_im TE_jm;  dbeta_i += sum_j dM_ij N_ij;
-    // dN = diag(beta) dM -> b2
+    // dM = -strict_lower(Z TE^T) (lower tiles); dbeta_i += sum_j dM_ij N_ij; dN = diag(beta) dM;
+    // then W_A and dN replace the algebra's matrices
     {
-        float dnv[CPT], rb = 0.f;
+        f32x4 dn[LPW];
 #pragma unroll
-        for (int m = 0; m < CPT; ++m) {
-            const int j = jl + 8 * m;
-            float acc = 0.f;
-            if (j < ri)
-                for (int mm = 0; mm <= j; ++mm) acc += b1[ri * CH + mm] * te[j * CH + mm];
-            const float dm = j < ri ? -acc : 0.f;
-            rb += dm * nn[ri * CH + j];
-            dnv[m] = bet[ri] * dm;
+        for (int s = 0; s < LPW; ++s) {
+            dn[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+            const int l = wave + NW * s;
+            if (l < NL) {
+                int I, J;
+                tile_of(l, I, J);
+                f32x4 m = {0.f, 0.f, 0.f, 0.f};
+                for (int kb = 0; kb <= J; ++kb)
+                    m = mfma_kb1(ld4(b1 + (16 * I + r16) * PW + 16 * kb + 4 * g4),
+                                 ld4(te + (16 * J + r16) * PW + 16 * kb + 4 * g4), m);
+                const int jj = 16 * J + r16;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = 16 * I + 4 * g4 + j;
+                    const float dm = jj < i ? -m[j] : 0.f;
+                    const float rb = sum16(dm * nn[i * PW + jj]);
+                    if (r16 == 0) atomicAdd(&dbet[i], rb);
+                    dn[s][j] = bet[i] * dm;
+                }
+            }
         }
-        rb += __shfl_xor(rb, 1);
-        rb += __shfl_xor(rb, 2);
-        rb += __shfl_xor(rb, 4);
+        __syncthreads();                                     // Z, TE and N are consumed
 #pragma unroll
-        for (int m = 0; m < CPT; ++m) b2[ri * CH + jl + 8 * m] = dnv[m];
-        __syncthreads();                                     // the Z_ii terms are in dbet
-        if (jl == 0) dbet[ri] += rb;
+        for (int m = 0; m < CPT; ++m) wa[ri * PW + jl + 8 * m] = wav[m];
+#pragma unroll
+        for (int s = 0; s < LPW; ++s) {
+            const int l = wave + NW * s;
+            if (l < NL) {
+                int I, J;
+                tile_of(l, I, J);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wn[(16 * I + 4 * g4 + j) * PW + 16 * J + r16] = dn[s][j];
+            }
+        }
     }
     __syncthreads();
 
-    // ---- the gated sums and the direct terms, per (row, channel) -------------
-    const float gC_ = gms[(CH - 1) * DK + c];                // gamma_C (rows past the end add no decay)
-    float dgam[RPT];
+    // ---- the gated sums (MFMA) and the direct terms ----------------------------
+    const int cc = 16 * (wave % NCT) + r16;                  // this lane's key channel
+    float kr[NB][4], qr[NB][4], gr[NB][4];                   // rows 16 J + 4 g4 + jj of channel cc
+#pragma unroll
+    for (int J = 0; J < NB; ++J)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int row = 16 * J + 4 * g4 + jj;
+            kr[J][jj] = EL::to_f(ks[row * DK + cc]);
+            qr[J][jj] = EL::to_f(qs[row * DK + cc]);
+            gr[J][jj] = gms[row * DK + cc];
+        }
+    const float gCc = gms[(CH - 1) * DK + cc];               // gamma_C (rows past the end add no decay)
+    const float gCt = gms[(CH - 1) * DK + c];                // the same for the dg pass's channel
+    float dqv[IPW][4], dkv[IPW][4], dgv[IPW][4];
     float dgc_acc = 0.f;
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) {
-        const int i = rg + NRG * r;
-        dgam[r] = 0.f;
-        if (i >= clen) continue;
-        const float qi = EL::to_f(qs[i * DK + c]), ki = EL::to_f(ks[i * DK + c]), gi = gms[i * DK + c];
-        // i side: sum_j W_A_ij k_j E_ij, sum_j dN_ij k_j E_ij
-        float sa = 0.f, sn = 0.f;
-        for (int j = 0; j <= i; ++j) {
-            const float e = __expf(gi - gms[j * DK + c]) * EL::to_f(ks[j * DK + c]);
-            sa += b3[i * CH + j] * e;
-            sn += b2[i * CH + j] * e;                        // dN is zero on the diagonal
+    for (int s = 0; s < IPW; ++s) {
+        const int I = wave / NCT + WPC * s;
+        float dqg[4], dxs[4], dke[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int i = 16 * I + 4 * g4 + jj;
+            dqg[jj] = gQ[i * DK + cc];
+            dxs[jj] = gX[i * DK + cc];
+            dke[jj] = gE[i * DK + cc];
         }
-        // j side (this row as j): sum_i' (W_A_i'i q_i' + dN_i'i k_i') E_i'i
-        float tj = 0.f;
-        for (int i2 = i; i2 < clen; ++i2) {
-            const float e = __expf(gms[i2 * DK + c] - gi);
-            tj += (b3[i2 * CH + i] * EL::to_f(qs[i2 * DK + c]) + b2[i2 * CH + i] * EL::to_f(ks[i2 * DK + c])) * e;
+        const bool exact = flag[I] != 0;                     // uniform over the workgroup
+        const float gref = gms[16 * I * DK + cc], gend = gms[(16 * I + 15) * DK + cc];
+        f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sn = sa, tj = sa;
+        // SA, SN: B = k_j e^(gamma_r - gamma_j) over row blocks J <= I
+#pragma unroll
+        for (int J = 0; J < NB; ++J) {
+            if (J < I || (J == I && !exact)) {
+                f32x4 b;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) b[jj] = kr[J][jj] * __expf(gref - gr[J][jj]);
+                sa = mfma_kb1(ld4(wa + (16 * I + r16) * PW + 16 * J + 4 * g4), b, sa);
+                sn = mfma_kb1(ld4(wn + (16 * I + r16) * PW + 16 * J + 4 * g4), b, sn);
+            }
+        }
+        // TJ: B = (q_i, k_i) e^(gamma_i - gamma_r') over row blocks I2 >= I, A = W^T
+#pragma unroll
+        for (int I2 = 0; I2 < NB; ++I2) {
+            if (I2 > I || (I2 == I && !exact)) {
+                f32x4 bq, bk;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) {
+                    const float e = __expf(gr[I2][jj] - gend);
+                    bq[jj] = qr[I2][jj] * e;
+                    bk[jj] = kr[I2][jj] * e;
+                }
+                tj = mfma_kb1(col4(wa, PW, 16 * I2 + 4 * g4, 16 * I + r16), bq, tj);
+                tj = mfma_kb1(col4(wn, PW, 16 * I2 + 4 * g4, 16 * I + r16), bk, tj);
+            }
+        }
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const float gi = gr[I][jj];
+            const float fa = __expf(gi - gref), ft = __expf(gend - gi);
+            sa[jj] *= fa;
+            sn[jj] *= fa;
+            tj[jj] *= ft;
+        }
+        if (exact) {
+            // the diagonal block with per-pair exponentials
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) {
+                const int i = 16 * I + 4 * g4 + jj;
+                const float gi = gr[I][jj];
+                float a = 0.f, n = 0.f, t = 0.f;
+                for (int j = 16 * I; j <= i; ++j) {
+                    const float kj = EL::to_f(ks[j * DK + cc]) * __expf(gi - gms[j * DK + cc]);
+                    a += wa[i * PW + j] * kj;
+                    n += wn[i * PW + j] * kj;
+                }
+                for (int i2 = i; i2 < 16 * I + 16; ++i2) {
+                    const float e = __expf(gms[i2 * DK + cc] - gi);
+                    t += (wa[i2 * PW + i] * EL::to_f(qs[i2 * DK + cc]) + wn[i2 * PW + i] * EL::to_f(ks[i2 * DK + cc])) * e;
+                }
+                sa[jj] += a;
+                sn[jj] += n;
+                tj[jj] += t;
+            }
         }
         // direct terms
-        const float eg = __expf(gi), egc = __expf(gC_ - gi);
-        const float dqg = gQ[i * DK + c], dxs = gX[i * DK + c], dke = gE[i * DK + c];
-        const float dq = sa + p.scale * eg * dqg;
-        const float dk = sn + tj - eg * dxs + egc * dke;
-        dgam[r] = qi * sa + ki * sn - ki * tj + p.scale * qi * eg * dqg - ki * eg * dxs - ki * egc * dke;
-        dgc_acc += ki * egc * dke;
-        reinterpret_cast<E *>(p.dq)[(t0 + i) * sqk + (int64_t)h * DK + c] = EL::from_f(dq);
-        reinterpret_cast<E *>(p.dk)[(t0 + i) * sqk + (int64_t)h * DK + c] = EL::from_f(dk);
-    }
-    atomicAdd(&dgc[c], dgc_acc);
-    __syncthreads();                                         // every read of gamma is done
 #pragma unroll
-    for (int r = 0; r < RPT; ++r) gms[(rg + NRG * r) * DK + c] = dgam[r];
+        for (int jj = 0; jj < 4; ++jj) {
+            const int i = 16 * I + 4 * g4 + jj;
+            const float qi = qr[I][jj], ki = kr[I][jj], gi = gr[I][jj];
+            const float eg = __expf(gi), egc = __expf(gCc - gi);
+            const bool ok = i < clen;
+            dqv[s][jj] = ok ? sa[jj] + p.scale * eg * dqg[jj] : 0.f;
+            dkv[s][jj] = ok ? sn[jj] + tj[jj] - eg * dxs[jj] + egc * dke[jj] : 0.f;
+            dgv[s][jj] = ok ? qi * sa[jj] + ki * sn[jj] - ki * tj[jj] + p.scale * qi * eg * dqg[jj] -
+                                  ki * eg * dxs[jj] - ki * egc * dke[jj]
+                            : 0.f;
+            dgc_acc += ok ? ki * egc * dke[jj] : 0.f;
+        }
+    }
+    atomicAdd(&dgc[cc], dgc_acc);
+    __syncthreads();                                         // every read of q, k and gamma is done
+#pragma unroll
+    for (int s = 0; s < IPW; ++s) {
+        const int I = wave / NCT + WPC * s;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int i = 16 * I + 4 * g4 + jj;
+            qs[i * DK + cc] = EL::from_f(dqv[s][jj]);
+            ks[i * DK + cc] = EL::from_f(dkv[s][jj]);
+            gms[i * DK + cc] = dgv[s][jj];
+        }
+    }
     __syncthreads();
-    if (rg == 0) {
-        // dg_t = dgamma_C + sum_{i >= t} dgamma_i, with dgamma_C = (the U dS'^T terms) + e^gamma_C sum S dS'
-        float acc = dgc[c] + __expf(gC_) * gC[c];
-        for (int i = clen - 1; i >= 0; --i) {
-            acc += gms[i * DK + c];
-            if (p.dg) p.dg[(t0 + i) * sqk + (int64_t)h * DK + c] = acc;
+    // dq, dk rows as 16-byte units
+    {
+        E *dqg = reinterpret_cast<E *>(p.dq) + t0 * sqk + (int64_t)h * DK;
+        E *dkg = reinterpret_cast<E *>(p.dk) + t0 * sqk + (int64_t)h * DK;
+#pragma unroll
+        for (int n = 0; n < OUT_N; ++n) {
+            const int u = tid + n * NT;
+            const int row = u / UPR, c0 = (u % UPR) * VE;
+            if (u < CH * UPR && row < clen) {
+                *reinterpret_cast<V *>(dqg + row * sqk + c0) = *reinterpret_cast<const V *>(qs + row * DK + c0);
+                *reinterpret_cast<V *>(dkg + row * sqk + c0) = *reinterpret_cast<const V *>(ks + row * DK + c0);
+            }
+        }
+    }
+    // dg_t = dgamma_C + sum_{i >= t} dgamma_i, with dgamma_C = (the U dS'^T terms) + e^gamma_C sum S dS':
+    // suffix sums over this thread's rows, then the later groups' totals
+    float dv[RPT];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) dv[r] = gms[(rg * RPT + r) * DK + c];
+#pragma unroll
+    for (int r = RPT - 2; r >= 0; --r) dv[r] += dv[r + 1];
+    part[rg][c] = dv[0];
+    __syncthreads();
+    if (p.dg) {
+        float post = dgc[c] + __expf(gCt) * gC[c];
+        for (int r = rg + 1; r < NRG; ++r) post += part[r][c];
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int i = rg * RPT + r;
+            if (i < clen) p.dg[(t0 + i) * sqk + (int64_t)h * DK + c] = dv[r] + post;
         }
     }
     if (tid < clen) p.dbeta[(t0 + tid) * H + h] = dbet[tid];
