@@ -294,6 +294,46 @@ int vgdr_chunk_bwd_saved(int dtype, int gate_kind,
                          float scale, int chunk_size, hipStream_t stream);
 
 /*
+ * The training pair with the producer fusions the backward can take through
+ * (no reference counterpart as entry points: fla's chunk_kda /
+ * chunk_gated_delta_rule with use_beta_sigmoid_in_kernel and
+ * use_gate_in_kernel differentiate through them, linear_attention.py:474-479,
+ * :487-491).  fusion as in vgdr_chunk_fwd_fused, with qk_l2norm 0 (q, k arrive
+ * normalised): beta_sigmoid: beta holds logits and grad_beta receives their
+ * gradient; gate_activation (gate_kind 2): g holds the pre-activation f
+ * [n_tokens, H, dk] (gate_dtype fp32 or dtype), grad_g receives df (fp32,
+ * [n_tokens, H, dk]), grad_A_log [H] and grad_dt_bias [H * dk] (fp32,
+ * overwritten) receive the gradients of the activation's parameters, summed
+ * over every token in a fixed order (no atomics).  A NULL fusion is the
+ * unfused call.  The saving forward and the saved backward take the same
+ * fusion.
+ */
+int vgdr_chunk_fwd_saving_fused(int dtype, int gate_kind, const void *q, const void *k, const void *v,
+                                const float *g, const float *beta, void *o, const float *initial_state,
+                                float *final_state, const int32_t *cu_seqlens, void *workspace,
+                                int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                                int64_t n_seqs, float scale, int chunk_size, const vgdr_fusion *fusion,
+                                hipStream_t stream);
+int vgdr_chunk_bwd_fused(int dtype, int gate_kind,
+                         const void *q, const void *k, const void *v, const float *g, const float *beta,
+                         const float *initial_state, const void *grad_o, const float *grad_final_state,
+                         void *grad_q, void *grad_k, void *grad_v, float *grad_g, float *grad_beta,
+                         float *grad_initial_state,
+                         const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                         int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                         float scale, int chunk_size, const vgdr_fusion *fusion, float *grad_A_log,
+                         float *grad_dt_bias, hipStream_t stream);
+int vgdr_chunk_bwd_saved_fused(int dtype, int gate_kind,
+                               const void *q, const void *k, const void *v, const float *g, const float *beta,
+                               const float *initial_state, const void *grad_o, const float *grad_final_state,
+                               void *grad_q, void *grad_k, void *grad_v, float *grad_g, float *grad_beta,
+                               float *grad_initial_state,
+                               const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                               int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                               float scale, int chunk_size, const vgdr_fusion *fusion, float *grad_A_log,
+                               float *grad_dt_bias, hipStream_t stream);
+
+/*
  * Backward of every scan form: the per-channel (KDA) gate, the explicit write
  * vector w (the asymmetric delta rule) and the plain recurrence without the
  * delta rule, besides the scalar gate and no gate.  Replaces the autograd of

@@ -17,6 +17,8 @@ is too slow: the chunk backward against the token-recurrence backward
 (vgdr_scan_bwd, whose fp32 gradients are pinned at that shape by a
 directional derivative in tests/test_scan_bwd.py) on the same inputs.
 """
+import ctypes
+
 import pytest
 import torch
 import torch.nn.functional as F
@@ -60,6 +62,33 @@ def test_kda_chunk_bwd_argument_checks():
     slots = B * T // 64
     per = 2 * dk * dv * 2 + 64 * 64 * 4 + (3 * 64 * dk + 2 * 64 * 64 + dk) * 4
     assert vec >= slots * H * per + L.vgdr_chunk_workspace_size(1, 2, B, T, H, dk, B, 0, 64)
+
+
+def test_kda_fused_backward_argument_checks():
+    """vgdr_chunk_bwd_fused / _saved_fused / vgdr_chunk_fwd_saving_fused:
+    the fused L2 norm is refused (q, k arrive normalised), the gate
+    activation needs the per-channel gate and its gradient outputs."""
+    L = _lib.load()
+    A = torch.zeros(2)
+    D = torch.zeros(2 * 64)
+
+    def fz(l2=0, beta=0, gate=1):
+        return _lib.Fusion(l2, beta, gate, _lib.VGDR_F32, A.data_ptr(), D.data_ptr(), 0, 0.0)
+
+    def call(fusion, gate=2, dA=8192, ddt=12288, saved=False):
+        fn = L.vgdr_chunk_bwd_saved_fused if saved else L.vgdr_chunk_bwd_fused
+        return fn(1, gate, 4096, 8192, 12288, 16384, 20480, None, 24576, None, 28672, 32768, 36864, 40960, 45056,
+                  None, None, 49152, 1 << 40, 2, 64, 2, 64, 64, 2, 0.125, 64, ctypes.byref(fusion), dA, ddt, None)
+    assert call(fz(l2=1)) == _lib.VGDR_ERR_UNSUPPORTED
+    assert b'L2 norm' in L.vgdr_last_error()
+    assert call(fz(l2=1), saved=True) == _lib.VGDR_ERR_UNSUPPORTED
+    assert call(fz(), gate=1) == _lib.VGDR_ERR_INVALID                # the activation is per channel
+    assert call(fz(), dA=None) == _lib.VGDR_ERR_INVALID
+    assert call(fz(), ddt=None) == _lib.VGDR_ERR_INVALID
+    f = fz(l2=1)
+    assert L.vgdr_chunk_fwd_saving_fused(1, 2, 4096, 8192, 12288, 16384, 20480, 24576, None, None, None, 49152,
+                                         1 << 40, 2, 64, 2, 64, 64, 2, 0.125, 64, ctypes.byref(f),
+                                         None) == _lib.VGDR_ERR_UNSUPPORTED
 
 
 def _inputs(B, T, H, dk, dv, dtype, seed, s0=True, strong=False):
@@ -192,3 +221,50 @@ def test_kda_chunk_bwd_full_size_matches_token_backward():
     got = ops.chunk_gated_delta_rule_bwd(q, k, v, g, beta, S0, do, dST, scale=scale)
     ref = ops.scan_bwd(q, k, v, g, beta, S0, do, dST, scale=scale)
     _compare(got, ref[:6], 2e-2, 'kda full size vs scan_bwd')
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('lower_bound', [None, -5.0])
+def test_kda_training_keeps_no_fp32_gate_tensor(lower_bound):
+    """chunk_kda with the fused L2 norm, beta sigmoid and gate activation under
+    autograd: the activation and the sigmoid run inside the kernels, forward
+    and backward, and the L2 norm saves its 16-bit input and one float per
+    row, so autograd keeps no fp32 (B, T, H, dk) tensor (the reference's
+    fused-gate memory saving, linear_attention.py:84-91); the gradients of
+    every input and of A_log, dt_bias still match the oracle's (the full check
+    at the oracle bar is tests/test_scan_bwd.py's fused-producer test)."""
+    B, T, H, dk, dv = 1, 100, 2, 64, 64
+    gen = torch.Generator().manual_seed(31)
+    r = lambda *s: torch.randn(*s, generator=gen)
+    q, k, v = r(B, T, H, dk).bfloat16(), r(B, T, H, dk).bfloat16(), r(B, T, H, dv).bfloat16()
+    f, bl = r(B, T, H, dk).bfloat16(), r(B, T, H)
+    A_log, dt_bias = 0.2 * r(H), 0.1 * r(H * dk)
+    do = r(B, T, H, dv).bfloat16()
+    print(f'\n[case] kda training saved tensors lower_bound={lower_bound}', flush=True)
+    dev = [x.cuda().requires_grad_(True) for x in (q, k, v, f, bl, A_log, dt_bias)]
+    saved = []
+
+    def pack(t):
+        saved.append((tuple(t.shape), t.dtype))
+        return t
+    with torch.autograd.graph.saved_tensors_hooks(pack, lambda t: t):
+        o, _ = ops.chunk_kda(*dev[:5], use_qk_l2norm_in_kernel=True, use_beta_sigmoid_in_kernel=True,
+                             use_gate_in_kernel=True, A_log=dev[5], dt_bias=dev[6],
+                             safe_gate=lower_bound is not None, lower_bound=lower_bound)
+    big = [sd for sd in saved if sd[1] == torch.float32 and len(sd[0]) == 4 and sd[0][-1] == dk]
+    print(f'[saved] {saved}', flush=True)
+    assert not big, big
+    o.backward(do.cuda())
+    leaves = [x.double().requires_grad_(True) for x in (q, k, v, f, bl, A_log, dt_bias)]
+    gg = gdr.gate_activation(leaves[3], leaves[5], leaves[6], lower_bound)
+    oo, _ = gdr.recurrent(gdr.l2norm(leaves[0]), gdr.l2norm(leaves[1]), leaves[2], gg,
+                          gdr.beta_sigmoid(leaves[4]), None, scale=dk ** -0.5)
+    ref = torch.autograd.grad(oo, leaves, do.double())
+    # (dA_log, a sum over every token and channel, is held to the bar over its
+    # summands in tests/test_scan_bwd.py; here it only has to exist)
+    assert dev[5].grad is not None and torch.isfinite(dev[5].grad).all()
+    for name, a, b in zip(('q', 'k', 'v', 'f', 'beta', 'dt_bias'), [x.grad for x in dev[:5] + dev[6:]],
+                          ref[:5] + ref[6:]):
+        err = _rel(a, b)
+        print(f'[parity] kda fused training d{name} rel_l2={err:.3e}', flush=True)
+        assert err <= 2e-2, f'd{name}: {err:.3e}'

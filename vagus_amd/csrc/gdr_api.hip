@@ -166,7 +166,7 @@ ChunkWs chunk_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, 
 // (chunk, head)) and the column phase's sums (grad_vec_work_floats each)
 struct BwdWs {
     ChunkWs fwd;
-    int64_t hs_off, dhs_off, nbuf_off, gw_off, total;
+    int64_t hs_off, dhs_off, nbuf_off, gw_off, dpart_off, total;
 };
 BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
                  int64_t n_seqs, bool varlen) {
@@ -176,13 +176,16 @@ BwdWs bwd_layout(int dtype, int gate_kind, int chunk, int64_t B, int64_t T, int6
     w.hs_off = (w.fwd.total + 255) / 256 * 256;
     w.dhs_off = w.hs_off + (states + 255) / 256 * 256;
     w.total = states > 0 ? w.dhs_off + states : w.fwd.total;
-    w.nbuf_off = w.gw_off = w.total;
+    w.nbuf_off = w.gw_off = w.dpart_off = w.total;
     if (gate_kind == VGDR_GATE_VECTOR && dtype != VGDR_F32 && states > 0) {
+        // plus N, the column phase's sums and (fused gate activation) the per-chunk parameter sums
         const int64_t nb = w.fwd.slots * H * chunk * chunk * 4;
         const int64_t gw = w.fwd.slots * H * vgdr::grad_vec_work_floats(chunk, (int)dk) * 4;
+        const int64_t dp = w.fwd.slots * H * (dk + 1) * 4;
         w.nbuf_off = (w.total + 255) / 256 * 256;
         w.gw_off = w.nbuf_off + (nb + 255) / 256 * 256;
-        w.total = w.gw_off + gw;
+        w.dpart_off = w.gw_off + (gw + 255) / 256 * 256;
+        w.total = w.dpart_off + dp;
     }
     return w;
 }
@@ -344,17 +347,32 @@ int64_t vgdr_chunk_bwd_workspace_size(int dtype, int gate_kind, int64_t B, int64
         void *grad_k, void *grad_v, float *grad_g, float *grad_beta, float *grad_initial_state,                 \
         const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H,    \
         int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size, hipStream_t stream
+#define VGDR_BWD_ARGS_FUSED                                                                                  \
+    int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g, const float *beta,   \
+        const float *initial_state, const void *grad_o, const float *grad_final_state, void *grad_q,            \
+        void *grad_k, void *grad_v, float *grad_g, float *grad_beta, float *grad_initial_state,                 \
+        const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H,    \
+        int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size, const vgdr_fusion *fusion,          \
+        float *grad_A_log, float *grad_dt_bias, hipStream_t stream
 #define VGDR_BWD_PASS                                                                                        \
     dtype, gate_kind, q, k, v, g, beta, initial_state, grad_o, grad_final_state, grad_q, grad_k, grad_v,        \
         grad_g, grad_beta, grad_initial_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk, dv, n_seqs, \
         scale, chunk_size, stream
 
 namespace {
-// both backward entry points; saved: the workspace holds what a saving forward left
-int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS) {
+// the backward entry points; saved: the workspace holds what a saving forward left
+int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS, const vgdr_fusion *fusion, float *grad_A_log,
+             float *grad_dt_bias) {
     g_err[0] = 0;
     int rc = check_common(fn, dtype, gate_kind, 1, q, k, v, g, beta, grad_o, cu_seqlens, B, T, H, dk, dv, n_seqs);
     if (rc) return rc;
+    vgdr::Fusion fz;
+    rc = check_fusion(fn, fusion, dtype, gate_kind, 1, true, fz);
+    if (rc) return rc;
+    if (fz.qk_l2norm)
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: the fused L2 norm has no backward here: pass normalised q, k", fn);
+    if (fz.gate_act && B * T > 0 && (!grad_A_log || !grad_dt_bias || !grad_g))
+        return fail(VGDR_ERR_INVALID, "%s: the fused gate activation needs grad_g, grad_A_log and grad_dt_bias", fn);
     if (dv <= 0 || dv % 16)
         return fail(VGDR_ERR_UNSUPPORTED, "%s: dv=%lld (must be a positive multiple of 16)", fn, (long long)dv);
     if (gate_kind == VGDR_GATE_VECTOR && (dtype == VGDR_F32 || effective_chunk(dtype, dk, chunk_size) != 64))
@@ -389,7 +407,9 @@ int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS) {
     f.n_chunk_slots = (int)ws.fwd.slots;
     f.use_delta = 1;
     f.scale = scale;
+    f.fz = fz;
     vgdr::ChunkBwdParams p{};
+    p.fz = fz;
     p.geo = f.geo;
     p.q = q; p.k = k; p.v = v;
     p.g = f.g;
@@ -411,6 +431,9 @@ int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS) {
     if (gate_kind == VGDR_GATE_VECTOR) {
         p.nbuf = reinterpret_cast<const float *>(wsb + ws.nbuf_off);
         p.gw = reinterpret_cast<float *>(wsb + ws.gw_off);
+        p.dpart = reinterpret_cast<float *>(wsb + ws.dpart_off);
+        p.dA_log = grad_A_log;
+        p.ddt_bias = grad_dt_bias;
         // the forward run for the entry states writes N and the states where
         // the backward reads them; its output o goes to the exit-gradient
         // region (n_tokens x dv <= chunk slots x CH x dv <= its dk x dv per
@@ -428,9 +451,20 @@ int bwd_call(const char *fn, bool saved, VGDR_BWD_ARGS) {
 }
 }  // namespace
 
-int vgdr_chunk_bwd(VGDR_BWD_ARGS) { return bwd_call("vgdr_chunk_bwd", false, VGDR_BWD_PASS); }
-int vgdr_chunk_bwd_saved(VGDR_BWD_ARGS) { return bwd_call("vgdr_chunk_bwd_saved", true, VGDR_BWD_PASS); }
+int vgdr_chunk_bwd(VGDR_BWD_ARGS) {
+    return bwd_call("vgdr_chunk_bwd", false, VGDR_BWD_PASS, nullptr, nullptr, nullptr);
+}
+int vgdr_chunk_bwd_saved(VGDR_BWD_ARGS) {
+    return bwd_call("vgdr_chunk_bwd_saved", true, VGDR_BWD_PASS, nullptr, nullptr, nullptr);
+}
+int vgdr_chunk_bwd_fused(VGDR_BWD_ARGS_FUSED) {
+    return bwd_call("vgdr_chunk_bwd_fused", false, VGDR_BWD_PASS, fusion, grad_A_log, grad_dt_bias);
+}
+int vgdr_chunk_bwd_saved_fused(VGDR_BWD_ARGS_FUSED) {
+    return bwd_call("vgdr_chunk_bwd_saved_fused", true, VGDR_BWD_PASS, fusion, grad_A_log, grad_dt_bias);
+}
 #undef VGDR_BWD_ARGS
+#undef VGDR_BWD_ARGS_FUSED
 #undef VGDR_BWD_PASS
 
 }  // extern "C"
@@ -494,20 +528,45 @@ int vgdr_chunk_fwd_noalloc(int dtype, int gate_kind, int use_delta, const void *
                       chunk_size, fusion, stream);
 }
 
-int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
-                          const float *beta, void *o, const float *initial_state, float *final_state,
-                          const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T,
-                          int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
-                          hipStream_t stream) {
-    const char *fn = "vgdr_chunk_fwd_saving";
+namespace {
+int fwd_saving(const char *fn, int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
+               const float *beta, void *o, const float *initial_state, float *final_state,
+               const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T, int64_t H,
+               int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size, const vgdr_fusion *fusion,
+               hipStream_t stream) {
     if (dtype == VGDR_F32 || (gate_kind == VGDR_GATE_VECTOR && effective_chunk(dtype, dk, chunk_size) != 64)) {
         g_err[0] = 0;
         return fail(VGDR_ERR_UNSUPPORTED, "%s: saving runs the 16-bit kernel (64-token chunks with a per-channel g)",
                     fn);
     }
+    if (fusion && fusion->qk_l2norm) {                        // the backward reads q, k as given
+        g_err[0] = 0;
+        return fail(VGDR_ERR_UNSUPPORTED, "%s: the fused L2 norm has no backward here: pass normalised q, k", fn);
+    }
     return chunk_call(fn, vgdr::CHUNK_PREP | vgdr::CHUNK_STATE, dtype, gate_kind, 1, q, k, v, g, beta, o,
                       initial_state, final_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk, dv, n_seqs,
-                      scale, chunk_size, nullptr, stream, nullptr, workspace);
+                      scale, chunk_size, fusion, stream, nullptr, workspace);
+}
+}  // namespace
+
+int vgdr_chunk_fwd_saving(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
+                          const float *beta, void *o, const float *initial_state, float *final_state,
+                          const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T,
+                          int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
+                          hipStream_t stream) {
+    return fwd_saving("vgdr_chunk_fwd_saving", dtype, gate_kind, q, k, v, g, beta, o, initial_state, final_state,
+                      cu_seqlens, workspace, workspace_bytes, B, T, H, dk, dv, n_seqs, scale, chunk_size, nullptr,
+                      stream);
+}
+int vgdr_chunk_fwd_saving_fused(int dtype, int gate_kind, const void *q, const void *k, const void *v,
+                                const float *g, const float *beta, void *o, const float *initial_state,
+                                float *final_state, const int32_t *cu_seqlens, void *workspace,
+                                int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                                int64_t n_seqs, float scale, int chunk_size, const vgdr_fusion *fusion,
+                                hipStream_t stream) {
+    return fwd_saving("vgdr_chunk_fwd_saving_fused", dtype, gate_kind, q, k, v, g, beta, o, initial_state,
+                      final_state, cu_seqlens, workspace, workspace_bytes, B, T, H, dk, dv, n_seqs, scale, chunk_size,
+                      fusion, stream);
 }
 
 namespace {

@@ -459,13 +459,13 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
 // instead of K and Q rows with per-row factors: K*G (Ks) and scale Q*G (Qs)
 // for dS, K*Gend (KEs) for dU, and Gc per key channel:
 //     dU = A^T dO + (K*Gend) dS'     dS = diag(Gc) dS' + (scale Q*G)^T dO - (K*G)^T dX
-template <int DK, int CH, int NWC, typename E, bool VEC = false>
-__global__ void __launch_bounds__(128 * NWC) chunk_dhs_kernel(const ChunkBwdParams p) {
+template <int DK, int CH, int NWC, typename E, bool VEC = false, int NPW = NWC>
+__global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
     using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, VEC ? 2 : 1>;
     static_assert(!VEC || CB::VEC, "the per-channel walk reads the 16-bit gated tiles");
-    constexpr int NTP = 64 * NWC, NB = CH / 16, NKB = DK / 16;
+    constexpr int NTP = 64 * NPW, NB = CH / 16, NKB = DK / 16;
     constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value;
     constexpr int NGF = VEC ? DK : 3 * CH + 4;
     __shared__ __attribute__((aligned(16))) E Ks0[CH * PK];
@@ -793,7 +793,8 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     const int tc = tid < CH ? tid : 0, tg = tc < clen ? tc : 0;
     const float gx_v = VEC ? 0.f : gf[tc], go_v = VEC ? 0.f : gf[CH + tc], ge_v = VEC ? 0.f : gf[2 * CH + tc];
     const float gc_v = VEC ? 0.f : gf[3 * CH];
-    const float be_v = VEC ? 0.f : p.beta[(t0 + tg) * H + h];
+    const float be_raw = VEC ? 0.f : p.beta[(t0 + tg) * H + h];
+    const float be_v = p.fz.beta_sigmoid ? sigmoidf_(be_raw) : be_raw;
     const float g_v = (!VEC && p.g) ? p.g[(t0 + (lane < clen ? lane : 0)) * H + h] : 0.f;
     const int Iw = wave % NB, J0 = (wave / NB) * JPW;          // this wave's C x DK tiles (Iw, J0 + s)
     auto tile_of = [&](int l, int &I, int &J) __attribute__((always_inline)) {
@@ -1226,9 +1227,19 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         }
         if (lane < clen) {
             if (p.dg) p.dg[(t0 + lane) * H + h] = x;
-            p.dbeta[(t0 + lane) * H + h] = dbet[lane];
+            const float b = bet[lane];                         // sigmoid(logit) when fused: its derivative b (1 - b)
+            p.dbeta[(t0 + lane) * H + h] = p.fz.beta_sigmoid ? dbet[lane] * b * (1.f - b) : dbet[lane];
         }
     }
+}
+
+// g per channel, or with the fused activation its pre-activation f (fp32, or
+// the element type when Fusion::gate_16), at element offset off
+template <typename E>
+__device__ __forceinline__ float load_gate(const ChunkBwdParams &p, int64_t off) {
+    if constexpr (sizeof(E) == 2)
+        if (p.fz.gate_act && p.fz.gate_16) return Elem<E>::to_f(reinterpret_cast<const E *>(p.g)[off]);
+    return p.g[off];
 }
 
 // ===========================================================================
@@ -1267,7 +1278,6 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 template <int DK, int CH, typename E>
 __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
-    using F = typename EL::frag;
     using CB = ChunkBlock<E, CH, DK, 2>;
     static_assert(CB::VEC && CH == 64, "per-channel gated tiles, 64-token chunks");
     constexpr int NT = 512, NW = 8, NB = CH / 16, NRG = NT / DK, RPT = CH / NRG, CPT = CH / 8;
@@ -1286,7 +1296,8 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     float *te = alg, *nn = alg + MM, *b1 = alg + 2 * MM, *b2 = alg + 3 * MM;   // TE, N, T0 then Z, dTE
     float *wa = alg, *wn = alg + MM;                         // W_A = scale dA (lower), dN (strict lower)
     __shared__ float bet[CH], dbet[CH], dgc[DK];
-    __shared__ float part[NRG][DK];                          // per row group: sums of g, later of dgamma
+    __shared__ float part[NRG][DK];                          // per row group: sums of g, of dgamma, of df
+    __shared__ float dbet_w[NW];                             // per wave: dA_log sums (fused activation)
     __shared__ int flag[NB];
 
     const int tid = threadIdx.x;
@@ -1317,11 +1328,18 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
         rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
         rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
         // gamma: inclusive sums over rows rg RPT .. + RPT - 1 here, the earlier groups' totals added below
+        // (fused activation: g = act(f) from the pre-activation, as chunk prep computes it)
         float gv[RPT];
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
             const int i = rg * RPT + r;
-            gv[r] = i < clen ? p.g[(t0 + i) * sqk + (int64_t)h * DK + c] : 0.f;
+            gv[r] = i < clen ? load_gate<E>(p, (t0 + i) * sqk + (int64_t)h * DK + c) : 0.f;
+        }
+        if (p.fz.gate_act) {
+            const float a_log = p.fz.A_log[h], dt = p.fz.dt_bias[(int64_t)h * DK + c];
+#pragma unroll
+            for (int r = 0; r < RPT; ++r)
+                gv[r] = rg * RPT + r < clen ? gate_activation(gv[r], a_log, dt, p.fz.lb_set, p.fz.lb) : 0.f;
         }
         rk.store(ks, DK, clen, tid);
         rq.store(qs, DK, clen, tid);
@@ -1339,7 +1357,8 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             wav[m] = j <= ri ? p.scale * gA[ri * CH + j] : 0.f;
         }
         if (tid < CH) {
-            bet[tid] = tid < clen ? p.beta[(t0 + tid) * H + h] : 0.f;
+            const float b = tid < clen ? p.beta[(t0 + tid) * H + h] : 0.f;
+            bet[tid] = tid < clen ? (p.fz.beta_sigmoid ? sigmoidf_(b) : b) : 0.f;
             dbet[tid] = 0.f;
         }
         if (tid < DK) dgc[tid] = 0.f;
@@ -1597,16 +1616,78 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     for (int r = RPT - 2; r >= 0; --r) dv[r] += dv[r + 1];
     part[rg][c] = dv[0];
     __syncthreads();
-    if (p.dg) {
-        float post = dgc[c] + __expf(gCt) * gC[c];
-        for (int r = rg + 1; r < NRG; ++r) post += part[r][c];
+    float post = dgc[c] + __expf(gCt) * gC[c];
+    for (int r = rg + 1; r < NRG; ++r) post += part[r][c];
+    if (p.fz.gate_act) {
+        // through the activation: df = dg dg/dz (z = f + dt_bias), and this chunk's sums of
+        // ddt_bias = sum_t df and dA_log = sum_{t, c} dg dg/dA_log
+        //   softplus form g = -a sp(z), a = e^A_log:  dg/dz = -a sigmoid(z),  dg/dA_log = g
+        //   bounded form  g = lb sigmoid(a z):        dg/dz = lb s (1 - s) a,  dg/dA_log = z dg/dz
+        const float a_log = p.fz.A_log[h], dt = p.fz.dt_bias[(int64_t)h * DK + c], a = __expf(a_log);
+        float sdt = 0.f, sda = 0.f;
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int i = rg * RPT + r;
+            if (i < clen) {
+                const int64_t off = (t0 + i) * sqk + (int64_t)h * DK + c;
+                const float z = load_gate<E>(p, off) + dt, dg = dv[r] + post;
+                float dz, dA;
+                if (p.fz.lb_set) {
+                    const float s = sigmoidf_(a * z);
+                    dz = p.fz.lb * s * (1.f - s) * a;
+                    dA = dz * z;
+                } else {
+                    dz = -a * sigmoidf_(z);
+                    dA = -a * softplusf_(z);
+                }
+                p.dg[off] = dg * dz;
+                sdt += dg * dz;
+                sda += dg * dA;
+            }
+        }
+        __syncthreads();                                     // the suffix totals are read
+        part[rg][c] = sdt;
+        const float w = sum64(sda);
+        if ((tid & 63) == 0) dbet_w[tid >> 6] = w;
+        __syncthreads();
+        float *dp = p.dpart + (slot * H + h) * (DK + 1);
+        if (rg == 0) {
+            float t = 0.f;
+            for (int r = 0; r < NRG; ++r) t += part[r][c];
+            dp[c] = t;
+        }
+        if (tid == 0) {
+            float t = 0.f;
+            for (int w8 = 0; w8 < NT / 64; ++w8) t += dbet_w[w8];
+            dp[DK] = t;
+        }
+    } else if (p.dg) {
 #pragma unroll
         for (int r = 0; r < RPT; ++r) {
             const int i = rg * RPT + r;
             if (i < clen) p.dg[(t0 + i) * sqk + (int64_t)h * DK + c] = dv[r] + post;
         }
     }
-    if (tid < clen) p.dbeta[(t0 + tid) * H + h] = dbet[tid];
+    if (tid < clen) {
+        const float b = bet[tid];                            // sigmoid(logit) when fused: its derivative b (1 - b)
+        p.dbeta[(t0 + tid) * H + h] = p.fz.beta_sigmoid ? dbet[tid] * b * (1.f - b) : dbet[tid];
+    }
+}
+
+// dA_log and dt_bias of the fused gate activation: the per-chunk sums
+// chunk_grad_vec_kernel left, added over the chunks in slot order (one
+// workgroup per head, a thread per dt_bias channel and one for A_log), so the
+// result does not depend on scheduling
+template <int DK>
+__global__ void __launch_bounds__(256) gate_param_grad_kernel(const ChunkBwdParams p) {
+    const int h = blockIdx.x, c = threadIdx.x;
+    if (c > DK) return;
+    int64_t n = p.geo.cu ? (int64_t)p.geo.chunk_offs[p.geo.n_seqs] : (int64_t)p.n_chunk_slots;
+    n = n < p.n_chunk_slots ? n : p.n_chunk_slots;
+    float acc = 0.f;
+    for (int64_t s = 0; s < n; ++s) acc += p.dpart[(s * p.H + h) * (DK + 1) + c];
+    if (c < DK) p.ddt_bias[(int64_t)h * DK + c] = acc;
+    else p.dA_log[h] = acc;
 }
 
 // ===========================================================================
@@ -1648,6 +1729,8 @@ static hipError_t run_bwd_vec(ChunkBwdParams p, hipStream_t stream) {
     if (grad_blocks > 0) {
         hipLaunchKernelGGL((chunk_grad_kernel<DK, CH, E, true>), dim3((unsigned)grad_blocks), dim3(512), 0, stream, p);
         hipLaunchKernelGGL((chunk_grad_vec_kernel<DK, CH, E>), dim3((unsigned)grad_blocks), dim3(512), 0, stream, p);
+        if (p.fz.gate_act)
+            hipLaunchKernelGGL((gate_param_grad_kernel<DK>), dim3((unsigned)p.H), dim3(256), 0, stream, p);
     }
     return hipGetLastError();
 }
@@ -1658,6 +1741,8 @@ hipError_t chunk_bwd(int dtype, int dk, int chunk, int gate_vector, const ChunkP
     const bool vec = gate_vector != 0;
     if (vec && (dtype == 0 || chunk != 64 || !fwd.hs || !fwd.nout || !p.nbuf || !p.gw))
         return hipErrorInvalidValue;                           // the per-channel backward: 16-bit, 64-token chunks
+    if (p.fz.qk_l2norm || (p.fz.gate_act && (!vec || !p.dpart || !p.dA_log || !p.ddt_bias || !p.dg)))
+        return hipErrorInvalidValue;
     // TE, A and the gate factors of every chunk, as the forward built them
     // (already in the workspace after a saving forward); the per-channel gate
     // also runs the forward's state kernel for the entry states

@@ -111,6 +111,10 @@ struct ChunkBwdParams {
     void *dhs;                    // [chunk slots, H, dv, dk] gradient of each chunk's exit state (same)
     const float *nbuf;            // per-channel gate: chunk prep's N (ChunkParams::nout)
     float *gw;                    // per-channel gate: [chunk slots, H, grad_vec_work_floats] the column phase's sums
+    Fusion fz;                    // beta_sigmoid: beta holds logits, dbeta is their gradient; gate_act
+                                  // (per-channel gate): g holds the pre-activation f, dg is df
+    float *dpart;                 // gate_act: [chunk slots, H, dk + 1] per-chunk sums of ddt_bias, then dA_log
+    float *dA_log, *ddt_bias;     // gate_act: [H], [H * dk]
     int H, DV;
     int n_tiles;                  // dv tiles of the walk kernels (set by the launcher)
     int n_chunk_slots;

@@ -133,11 +133,32 @@ def _gate_activation_rows(f, fz):
     return -a * F.softplus(x)
 
 
+class _L2NormRows(torch.autograd.Function):
+    """y = x r, r = rsqrt(sum x^2 + 1e-6) per (token, head), computed in >= fp32
+    and rounded to x's type (linear_attention.py:703-706).  Saves x (its own
+    type) and r (one float per row): autograd through the torch expression
+    would keep fp32 copies of the whole (B, T, H, dk) row block.
+    dx = r dy - r^3 x <x, dy>."""
+
+    @staticmethod
+    def forward(ctx, x):
+        xf = x if x.dtype == torch.float64 else x.float()
+        r = torch.rsqrt((xf * xf).sum(-1, keepdim=True) + 1e-6)
+        ctx.save_for_backward(x, r)
+        return (xf * r).to(x.dtype)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, r = ctx.saved_tensors
+        xf = x.to(r.dtype)
+        dyf = dy.to(r.dtype)
+        return (r * dyf - r * r * r * xf * (xf * dyf).sum(-1, keepdim=True)).to(x.dtype)
+
+
 def _l2norm_rows(x):
     """x rsqrt(sum x^2 + 1e-6) per (token, head) in >= fp32, cast back
-    (linear_attention.py:703-706): the q, k producer, differentiable in torch."""
-    xf = x if x.dtype == torch.float64 else x.float()
-    return (xf * torch.rsqrt((xf * xf).sum(-1, keepdim=True) + 1e-6)).to(x.dtype)
+    (linear_attention.py:703-706): the q, k producer, differentiable."""
+    return _L2NormRows.apply(x)
 
 
 class _Fusion:
@@ -257,7 +278,7 @@ def _chunk_bwd_covers(q, g, chunk_size):
 
 
 def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, cu_seqlens=None,
-                               chunk_size=64, saved_workspace=None):
+                               chunk_size=64, saved_workspace=None, fusion: _Fusion = _NO_FUSION):
     """Backward of chunk_gated_delta_rule / chunk_kda without autograd
     (vgdr_chunk_bwd): the gradients of (o, final_state) under the cotangents
     do (and dht, None = zero) with respect to q, k, v, g, beta and
@@ -270,9 +291,14 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     chunk_scan_vec (linear_attention.py:237-309, :312-425) or fla's backward.
     saved_workspace: the workspace a saving forward (_chunk_fwd_saving, same
     inputs) filled; the backward then skips rebuilding the chunk blocks and
-    the per-chunk entry states."""
+    the per-chunk entry states.
+    fusion: the producer fusions the kernels differentiate through (16-bit;
+    no L2 norm): beta as logits (dbeta is their gradient) and, with a
+    per-channel g, the gate activation (g is its pre-activation f, dg is df,
+    and the tuple gains dA_log and ddt_bias)."""
+    assert not fusion.l2norm, 'the fused L2 norm is differentiated in torch, before the kernels'
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=_gate_of(g), delta=True,
-              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
     assert dht is None or dht.shape == (c.N, c.H, c.dk, c.dv), \
@@ -293,14 +319,23 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
                                              int(c.cu is not None), int(chunk_size))
     if saved_workspace is not None:
         assert saved_workspace.numel() >= nbytes, 'saved_workspace is smaller than this backward needs'
-        ws, fn = saved_workspace, L.vgdr_chunk_bwd_saved
+        ws, saved = saved_workspace, True
     else:
-        ws, fn = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device), L.vgdr_chunk_bwd
+        ws, saved = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device), False
+    head = (dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g), _ptr(c.beta), _ptr(c.h0), _ptr(dop),
+            _ptr(dSp), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg), _ptr(db), _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes,
+            c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size))
+    dA = ddt = None
     with torch.cuda.device(c.device):
-        _lib.check(fn(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g), _ptr(c.beta),
-                                    _ptr(c.h0), _ptr(dop), _ptr(dSp), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dg),
-                                    _ptr(db), _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes, c.B, c.T, c.H, c.dkp, c.dvp,
-                                    c.N, scale, int(chunk_size), _stream(c.device)))
+        if fusion.any:
+            fz, keep = fusion.struct(c)
+            if fusion.gate:
+                dA, ddt = new(c.H), new(c.H * c.dkp)
+            fn = L.vgdr_chunk_bwd_saved_fused if saved else L.vgdr_chunk_bwd_fused
+            _lib.check(fn(*head, ctypes.byref(fz), _ptr(dA), _ptr(ddt), _stream(c.device)))
+        else:
+            fn = L.vgdr_chunk_bwd_saved if saved else L.vgdr_chunk_bwd
+            _lib.check(fn(*head, _stream(c.device)))
     if c.dkp != c.dk:
         dq, dk = dq[..., :c.dk], dk[..., :c.dk]
         dg = dg[..., :c.dk] if vec else dg
@@ -308,27 +343,36 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
         dv = dv[..., :c.dv]
     if dS0 is not None:
         dS0 = c.unpad_state(dS0).to(initial_state.dtype)
-    return dq, dk, dv, None if dg is None else dg.to(g.dtype), db.to(beta.dtype), dS0
+    out = (dq, dk, dv, None if dg is None else dg.to(g.dtype), db.to(beta.dtype), dS0)
+    if fusion.gate:
+        ddt = ddt.reshape(c.H, c.dkp)[:, :c.dk].reshape(fusion.dt_bias.shape).to(fusion.dt_bias.dtype)
+        out += (dA.reshape(fusion.A_log.shape).to(fusion.A_log.dtype), ddt)
+    return out
 
 
-def _chunk_fwd_saving(q, k, v, g, beta, initial_state, *, scale, cu_seqlens, chunk_size):
+def _chunk_fwd_saving(q, k, v, g, beta, initial_state, *, scale, cu_seqlens, chunk_size,
+                      fusion: _Fusion = _NO_FUSION):
     """vgdr_chunk_fwd_saving: the chunked forward (16-bit, any gate, delta
     rule) run in a backward workspace, which keeps the chunk blocks and every
-    chunk's entry state for vgdr_chunk_bwd_saved.  Returns (o, final_state,
-    workspace)."""
+    chunk's entry state for vgdr_chunk_bwd_saved.  fusion: beta logits and
+    the gate activation in the kernels (no L2 norm).  Returns (o,
+    final_state, workspace)."""
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=_gate_of(g), delta=True,
-              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
     o, S = c.new_output(), c.new_state()
     L = _lib.load()
     dtype = _DTYPES[c.dtype]
     nbytes = L.vgdr_chunk_bwd_workspace_size(dtype, c.gate_kind, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
                                              int(c.cu is not None), int(chunk_size))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+    head = (dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g), _ptr(c.beta), _ptr(o), _ptr(c.h0),
+            _ptr(S), _ptr(c.cu), _ptr(ws), nbytes, c.B, c.T, c.H, c.dkp, c.dvp, c.N, float(scale), int(chunk_size))
     with torch.cuda.device(c.device):
-        _lib.check(L.vgdr_chunk_fwd_saving(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
-                                           _ptr(c.beta), _ptr(o), _ptr(c.h0), _ptr(S), _ptr(c.cu), _ptr(ws), nbytes,
-                                           c.B, c.T, c.H, c.dkp, c.dvp, c.N, float(scale), int(chunk_size),
-                                           _stream(c.device)))
+        if fusion.any:
+            fz, keep = fusion.struct(c)
+            _lib.check(L.vgdr_chunk_fwd_saving_fused(*head, ctypes.byref(fz), _stream(c.device)))
+        else:
+            _lib.check(L.vgdr_chunk_fwd_saving(*head, _stream(c.device)))
     return c.unpad_o(o), c.unpad_state(S), ws
 
 
@@ -424,31 +468,39 @@ class _ChunkDeltaRule(torch.autograd.Function):
     vgdr_chunk_bwd_saved (fla's disable_recompute trade: about 2 dk dv bytes
     per chunk and head of device memory held from forward to backward for
     skipping two of the backward's kernels).  fp32: forward vgdr_chunk_fwd,
-    backward vgdr_chunk_bwd.  q, k arrive normalised, beta in [0, 1]."""
+    backward vgdr_chunk_bwd.  q, k arrive normalised.  fusion (16-bit only):
+    beta as logits and the per-channel gate as its pre-activation f with
+    A_log, dt_bias, both differentiated inside the kernels; otherwise beta in
+    [0, 1] and g the log-decay."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, S0, scale, cu, chunk_size):
+    def forward(ctx, q, k, v, g, beta, S0, A_log, dt_bias, scale, cu, chunk_size, fusion):
         ctx.ws = None
         if q.dtype != torch.float32:
             o, S, ctx.ws = _chunk_fwd_saving(q, k, v, g, beta, S0, scale=scale, cu_seqlens=cu,
-                                             chunk_size=chunk_size)
+                                             chunk_size=chunk_size, fusion=fusion)
         else:
+            assert not fusion.any, 'the kernel fusions take 16-bit q, k, v'
             o, S = chunk_scan(q, k, v, g, beta, gate=_gate_of(g), delta=True,
                               scale=scale, initial_state=S0, output_final_state=True, cu_seqlens=cu,
                               chunk_size=chunk_size)
-        ctx.save_for_backward(q, k, v, g, beta, S0, cu)
-        ctx.scale, ctx.chunk_size = scale, chunk_size
+        ctx.save_for_backward(q, k, v, g, beta, S0, cu, A_log, dt_bias)
+        ctx.scale, ctx.chunk_size, ctx.fusion = scale, chunk_size, fusion
         return o, S
 
     @staticmethod
     def backward(ctx, do, dS):
-        q, k, v, g, beta, S0, cu = ctx.saved_tensors
+        q, k, v, g, beta, S0, cu, A_log, dt_bias = ctx.saved_tensors
         if do is None:
             do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
+        fz = ctx.fusion
+        if fz.gate:                                            # the saved tensors, not the forward's references
+            fz = _Fusion(beta=fz.beta, gate=True, A_log=A_log, dt_bias=dt_bias, lower_bound=fz.lower_bound)
         grads = chunk_gated_delta_rule_bwd(q, k, v, g, beta, S0, do, dS, scale=ctx.scale, cu_seqlens=cu,
-                                           chunk_size=ctx.chunk_size, saved_workspace=ctx.ws)
+                                           chunk_size=ctx.chunk_size, saved_workspace=ctx.ws, fusion=fz)
         ctx.ws = None
-        return grads + (None, None, None)
+        dA, ddt = grads[6:] if fz.gate else (None, None)
+        return grads[:6] + (dA, ddt, None, None, None, None)
 
 
 def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None, output_final_state=False,
@@ -462,25 +514,37 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
     either way), so that a caller can time the two phases separately.
     fusion: the producer fusions (_Fusion).
 
-    With grads enabled and an input that requires grad, the fused producers
-    (L2 norm, beta sigmoid, gate activation) run in torch, differentiably, and
-    the scan through _ChunkDeltaRule (delta rule: scalar gate or none, or the
-    per-channel gate with 16-bit inputs in 64-token chunks) or _ScanRule
-    (every other form)."""
-    if _wants_grad(q, k, v, g, beta, initial_state):
+    With grads enabled and an input that requires grad, the scan runs through
+    _ChunkDeltaRule (delta rule: scalar gate or none, or the per-channel gate
+    with 16-bit inputs in 64-token chunks) or _ScanRule (every other form).
+    The fused L2 norm then runs in torch, differentiably; the beta sigmoid and
+    the gate activation stay inside the kernels, forward and backward, on the
+    16-bit _ChunkDeltaRule path (no fp32 (B, T, H, dk) gate tensor is made),
+    and run in torch elsewhere."""
+    if _wants_grad(q, k, v, g, beta, initial_state, fusion.A_log, fusion.dt_bias):
         if fusion.l2norm:
             q, k = _l2norm_rows(q), _l2norm_rows(k)
+        scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
+        gk = None if gate == 'none' else g
+        chunked = delta and _chunk_bwd_covers(q, gk, chunk_size)
+        if chunked and q.dtype != torch.float32 and (fusion.beta or fusion.gate):
+            # beta sigmoid and the gate activation inside the kernels, forward and backward
+            kf = _Fusion(beta=fusion.beta, gate=fusion.gate, A_log=fusion.A_log, dt_bias=fusion.dt_bias,
+                         lower_bound=fusion.lower_bound)
+            o, S = _ChunkDeltaRule.apply(q, k, v, gk, beta, initial_state, fusion.A_log, fusion.dt_bias, scale,
+                                         cu_seqlens, chunk_size, kf)
+            return o, (S if output_final_state else None)
         if fusion.beta:
             beta = torch.sigmoid(beta.float())
         if fusion.gate:
             g = _gate_activation_rows(g, fusion)
-        scale = q.shape[-1] ** -0.5 if scale is None else float(scale)
         gk = None if gate == 'none' else g
-        if not delta or not _chunk_bwd_covers(q, gk, chunk_size):
+        if not chunked:
             o, S = _ScanRule.apply(q, k, v, gk, beta if delta else None, initial_state, None, scale, cu_seqlens,
                                    chunk_size, delta)
         else:
-            o, S = _ChunkDeltaRule.apply(q, k, v, gk, beta, initial_state, scale, cu_seqlens, chunk_size)
+            o, S = _ChunkDeltaRule.apply(q, k, v, gk, beta, initial_state, None, None, scale, cu_seqlens, chunk_size,
+                                         _NO_FUSION)
         return o, (S if output_final_state else None)
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=gate, delta=delta,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
