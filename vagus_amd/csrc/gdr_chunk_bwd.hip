@@ -1280,7 +1280,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     using EL = Elem<E>;
     using CB = ChunkBlock<E, CH, DK, 2>;
     static_assert(CB::VEC && CH == 64, "per-channel gated tiles, 64-token chunks");
-    constexpr int NT = 512, NW = 8, NB = CH / 16, NRG = NT / DK, RPT = CH / NRG, CPT = CH / 8;
+    constexpr int NT = 512, NW = 8, NB = CH / 16, NRG = NT / DK, RPT = CH / NRG;
     constexpr int FF = CH * CH, PW = CH + 4;                          // W pitch (floats)
     constexpr int NCT = DK / 16, WPC = NW / NCT, IPW = NB / WPC;   // channel tiles, waves per tile, blocks per wave
     static_assert(NT % DK == 0 && CH % NRG == 0 && NW % NCT == 0 && NB % WPC == 0, "thread layout");
@@ -1289,11 +1289,13 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     __shared__ __attribute__((aligned(16))) E qs[CH * DK];          // q, later dq
     __shared__ __attribute__((aligned(16))) E ks[CH * DK];          // k, later dk
     __shared__ __attribute__((aligned(16))) float gms[CH * DK];     // gamma, later dgamma
-    // the CH x CH algebra's matrices (fp32, pitch PW), then (same memory) the
-    // A operands of the gated sums
+    // TE (element type, as chunk prep wrote it), the CH x CH algebra's fp32
+    // matrices (pitch PW), then (same memory) the A operands of the gated sums
+    constexpr int PT = Pitch<E, CH>::value;
     constexpr int MM = CH * PW, NL = NB * (NB + 1) / 2, LPW = (NL + NW - 1) / NW;   // lower 16 x 16 tiles
-    __shared__ __attribute__((aligned(16))) float alg[4 * MM];
-    float *te = alg, *nn = alg + MM, *b1 = alg + 2 * MM, *b2 = alg + 3 * MM;   // TE, N, T0 then Z, dTE
+    __shared__ __attribute__((aligned(16))) E tes[CH * PT];
+    __shared__ __attribute__((aligned(16))) float alg[3 * MM];
+    float *nn = alg, *b1 = alg + MM, *b2 = alg + 2 * MM;     // N, T0 then Z, dTE
     float *wa = alg, *wn = alg + MM;                         // W_A = scale dA (lower), dN (strict lower)
     __shared__ float bet[CH], dbet[CH], dgc[DK];
     __shared__ float part[NRG][DK];                          // per row group: sums of g, of dgamma, of df
@@ -1302,7 +1304,6 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
 
     const int tid = threadIdx.x;
     const int c = tid % DK, rg = tid / DK;                   // channel phases
-    const int ri = tid >> 3, jl = tid & 7;                   // CH x CH phase: row ri, columns jl + 8 m
     const int H = p.H;
     const int h = blockIdx.x % H;
     const int64_t slot = blockIdx.x / H;
@@ -1322,8 +1323,20 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     const float *gA = gwb + 3 * CH * DK, *gT = gA + FF, *gC = gT + FF;
 
     // ---- stage -------------------------------------------------------------
-    float wav[CPT];                                          // W_A at (ri, jl + 8 m), stored after the algebra
+    constexpr int U4 = FF / 4 / NT;                          // 16-byte units of a CH x CH fp32 matrix per thread
+    static_assert(FF % (4 * NT) == 0, "CH x CH units split evenly");
+    f32x4 wav[U4];                                           // W_A units, stored after the algebra
     {
+        BlockRegs<E, CH, NT> rte;
+        rte.load(TEb, tid);
+        f32x4 nv[U4], tv[U4];
+#pragma unroll
+        for (int m = 0; m < U4; ++m) {
+            const int u = tid + NT * m;
+            nv[m] = ld4(nb + 4 * u);
+            tv[m] = ld4(gT + 4 * u);
+            wav[m] = ld4(gA + 4 * u);
+        }
         RowRegs<E, CH, DK, NT> rk, rq;
         rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
         rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
@@ -1348,13 +1361,18 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
         part[rg][c] = gv[RPT - 1];
 #pragma unroll
         for (int r = 0; r < RPT; ++r) gms[(rg * RPT + r) * DK + c] = gv[r];
+        rte.store(tes, PT, tid);
 #pragma unroll
-        for (int m = 0; m < CPT; ++m) {
-            const int j = jl + 8 * m;
-            te[ri * PW + j] = j <= ri ? EL::to_f(TEb[blk_pos<NB>(ri, j)]) : 0.f;
-            nn[ri * PW + j] = j < ri ? nb[ri * CH + j] : 0.f;
-            b2[ri * PW + j] = j <= ri ? gT[ri * CH + j] : 0.f;
-            wav[m] = j <= ri ? p.scale * gA[ri * CH + j] : 0.f;
+        for (int m = 0; m < U4; ++m) {
+            const int u = tid + NT * m, row = (4 * u) / CH, c0 = (4 * u) % CH;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                nv[m][e] = c0 + e < row ? nv[m][e] : 0.f;
+                tv[m][e] = c0 + e <= row ? tv[m][e] : 0.f;
+                wav[m][e] = c0 + e <= row ? p.scale * wav[m][e] : 0.f;
+            }
+            st4(nn + row * PW + c0, nv[m]);
+            st4(b2 + row * PW + c0, tv[m]);
         }
         if (tid < CH) {
             const float b = tid < clen ? p.beta[(t0 + tid) * H + h] : 0.f;
@@ -1387,8 +1405,8 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             tile_of(l, I, J);
             f32x4 t = {0.f, 0.f, 0.f, 0.f};
             for (int kb = J; kb <= I; ++kb)
-                t = mfma_kb1(ld4(te + (16 * I + r16) * PW + 16 * kb + 4 * g4), col4(nn, PW, 16 * kb + 4 * g4, 16 * J + r16),
-                             t);
+                t = mfma_kb1(EL::tof(ld_frag<E>(tes + (16 * I + r16) * PT + 16 * kb + 4 * g4)),
+                             col4(nn, PW, 16 * kb + 4 * g4, 16 * J + r16), t);
             const int jj = 16 * J + r16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
@@ -1451,7 +1469,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
                 f32x4 m = {0.f, 0.f, 0.f, 0.f};
                 for (int kb = 0; kb <= J; ++kb)
                     m = mfma_kb1(ld4(b1 + (16 * I + r16) * PW + 16 * kb + 4 * g4),
-                                 ld4(te + (16 * J + r16) * PW + 16 * kb + 4 * g4), m);
+                                 EL::tof(ld_frag<E>(tes + (16 * J + r16) * PT + 16 * kb + 4 * g4)), m);
                 const int jj = 16 * J + r16;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -1463,9 +1481,12 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
                 }
             }
         }
-        __syncthreads();                                     // Z, TE and N are consumed
+        __syncthreads();                                     // Z and N are consumed
 #pragma unroll
-        for (int m = 0; m < CPT; ++m) wa[ri * PW + jl + 8 * m] = wav[m];
+        for (int m = 0; m < U4; ++m) {
+            const int u = tid + NT * m;
+            st4(wa + ((4 * u) / CH) * PW + (4 * u) % CH, wav[m]);
+        }
 #pragma unroll
         for (int s = 0; s < LPW; ++s) {
             const int l = wave + NW * s;
