@@ -387,6 +387,10 @@ def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
                                        saved_workspace=ws)
 
     pair_us = _event_us(torch, pair, steps, warmup)
+    # the plain recurrence (no delta rule, chunk_scan_vec(delta=False)) through the same kernels
+    nodelta_us = _event_us(torch, lambda i: ops.chunk_gated_delta_rule_bwd(x.q, x.k, x.v, x.g, None, x.initial_state,
+                                                                           do, dST, scale=scale, delta=False),
+                           steps, warmup)
     walk_us = None
     if token_walk:
         walk_us = _event_us(torch, lambda i: ops.scan_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST,
@@ -403,7 +407,10 @@ def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
          'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5),
          'train_pair_us': round(pair_us, 1),
          'train_pair': 'vgdr_chunk_fwd_saving + vgdr_chunk_bwd_saved (what autograd runs for 16-bit inputs)',
-         'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2)}
+         'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2),
+         'nodelta_us': round(nodelta_us, 1),
+         'nodelta': 'the recurrence without the delta rule (vgdr_chunk_bwd_nodelta: the same kernels on blocks '
+                    'with TE = I and no K decay)'}
     if walk_us is not None:
         r['token_walk_us'] = round(walk_us, 1)
         r['token_walk'] = 'vgdr_scan_bwd (scan_walks_kernel + scan_grad_kernel + scan_bwd_finish_kernel)'

@@ -294,6 +294,23 @@ int vgdr_chunk_bwd_saved(int dtype, int gate_kind,
                          float scale, int chunk_size, hipStream_t stream);
 
 /*
+ * Backward of the chunked scan without the delta rule (the plain gated
+ * recurrence S_t = g_t S_{t-1} + k_t v_t^T: chunk_simple_gla, and
+ * chunk_scan_vec / chunk_scan with delta=False, linear_attention.py:237-309,
+ * :312-425, autograd): vgdr_chunk_bwd's arguments and workspace
+ * (vgdr_chunk_bwd_workspace_size) without beta and grad_beta.  gate_kind 0 and
+ * 1 at every dtype, 2 with 16-bit q, k, v in 64-token chunks.  The delta-form
+ * kernels run it: chunk prep writes TE = I and zeroes the K decay factor, so
+ * U = V.
+ */
+int vgdr_chunk_bwd_nodelta(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
+                           const float *initial_state, const void *grad_o, const float *grad_final_state,
+                           void *grad_q, void *grad_k, void *grad_v, float *grad_g, float *grad_initial_state,
+                           const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes,
+                           int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv, int64_t n_seqs,
+                           float scale, int chunk_size, hipStream_t stream);
+
+/*
  * The training pair with the producer fusions the backward can take through
  * (no reference counterpart as entry points: fla's chunk_kda /
  * chunk_gated_delta_rule with use_beta_sigmoid_in_kernel and

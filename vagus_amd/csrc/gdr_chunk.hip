@@ -275,7 +275,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     float beta_v = 0.f, g_v = 0.f;
     if (wave == 0) {
         const int row = lane < clen ? lane : 0;
-        if (!WR && p.use_delta) beta_v = p.beta[(t0 + row) * H + h];
+        if (!WR && p.use_delta && !p.te_identity) beta_v = p.beta[(t0 + row) * H + h];
         if constexpr (GATE != 2)
             if (p.g) g_v = p.g[(t0 + row) * H + h];
     }
@@ -368,7 +368,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             const float fk = nrm ? rkf[lane] : 1.f, fq = nrm ? rqf[lane] : 1.f;
             const float gx = __expf(x);
             float *gblk = reinterpret_cast<float *>(blk_base + CB::GOFF);
-            gblk[lane] = gx * fk;
+            gblk[lane] = p.te_identity ? 0.f : gx * fk;          // GX = 0: X = V without the delta rule
             gblk[CH + lane] = p.scale * gx * fq;
             // zero past the end of the sequence: the state update scales those
             // rows of U~ (or V without the delta rule) by it, and the state
@@ -509,7 +509,9 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             const f32x4 k0 = EL::tof(ld_frag<E>(Kst + SK::at(t, c0))), k1 = EL::tof(ld_frag<E>(Kst + SK::at(t, c1)));
             const f32x4 q0 = EL::tof(ld_frag<E>(Qst + SK::at(t, c0))), q1 = EL::tof(ld_frag<E>(Qst + SK::at(t, c1)));
             E *row = tg + t * DK + 8 * pu;
-            *reinterpret_cast<F2 *>(row) = EL::cvt2(k0 * e0, k1 * e1);
+            // a zero K*G tile without the delta rule (X = V)
+            *reinterpret_cast<F2 *>(row) = p.te_identity ? EL::cvt2(f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f})
+                                                         : EL::cvt2(k0 * e0, k1 * e1);
             E *qrow = tg + CH * DK + t * DK;
             st_frag<E>(qrow + c0, EL::cvt(q0 * e0 * p.scale));
             st_frag<E>(qrow + c1, EL::cvt(q1 * e1 * p.scale));
@@ -538,6 +540,19 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         st_frag<E>(blk + frag_pos<NB>(2 * wave, 2 * wave + 1, lane), zero);
     }
     if (!p.use_delta) return;
+    if (p.te_identity) {
+        // TE = I: the delta form's blocks for U = V (no solve, beta unused)
+        for (int tjob = wave; tjob < NL; tjob += NW) {
+            int I = 0, kb = tjob;
+            while (kb > I) { kb -= I + 1; ++I; }
+            const int row = 16 * I + r16, c0 = 16 * kb + 4 * g4;
+            f32x4 t;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t[e] = c0 + e == row ? 1.f : 0.f;
+            st_frag<E>(blk + frag_pos<NB>(I, kb, lane), EL::cvt(t));
+        }
+        return;
+    }
     __syncthreads();
 
     // ---- T = (I + M)^-1: 16x16 diagonal blocks by forward substitution ---

@@ -793,7 +793,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     const int tc = tid < CH ? tid : 0, tg = tc < clen ? tc : 0;
     const float gx_v = VEC ? 0.f : gf[tc], go_v = VEC ? 0.f : gf[CH + tc], ge_v = VEC ? 0.f : gf[2 * CH + tc];
     const float gc_v = VEC ? 0.f : gf[3 * CH];
-    const float be_raw = VEC ? 0.f : p.beta[(t0 + tg) * H + h];
+    const float be_raw = (VEC || !p.beta) ? 0.f : p.beta[(t0 + tg) * H + h];   // no delta rule: beta 0
     const float be_v = p.fz.beta_sigmoid ? sigmoidf_(be_raw) : be_raw;
     const float g_v = (!VEC && p.g) ? p.g[(t0 + (lane < clen ? lane : 0)) * H + h] : 0.f;
     const int Iw = wave % NB, J0 = (wave / NB) * JPW;          // this wave's C x DK tiles (Iw, J0 + s)
@@ -1228,7 +1228,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         if (lane < clen) {
             if (p.dg) p.dg[(t0 + lane) * H + h] = x;
             const float b = bet[lane];                         // sigmoid(logit) when fused: its derivative b (1 - b)
-            p.dbeta[(t0 + lane) * H + h] = p.fz.beta_sigmoid ? dbet[lane] * b * (1.f - b) : dbet[lane];
+            if (p.dbeta) p.dbeta[(t0 + lane) * H + h] = p.fz.beta_sigmoid ? dbet[lane] * b * (1.f - b) : dbet[lane];
         }
     }
 }
@@ -1375,7 +1375,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             st4(b2 + row * PW + c0, tv[m]);
         }
         if (tid < CH) {
-            const float b = tid < clen ? p.beta[(t0 + tid) * H + h] : 0.f;
+            const float b = tid < clen && p.beta ? p.beta[(t0 + tid) * H + h] : 0.f;   // no delta rule: 0
             bet[tid] = tid < clen ? (p.fz.beta_sigmoid ? sigmoidf_(b) : b) : 0.f;
             dbet[tid] = 0.f;
         }
@@ -1591,6 +1591,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             const int i = 16 * I + 4 * g4 + jj;
             const float qi = qr[I][jj], ki = kr[I][jj], gi = gr[I][jj];
             const float eg = __expf(gi), egc = __expf(gCc - gi);
+            dxs[jj] = p.delta ? dxs[jj] : 0.f;                 // without the delta rule K*G does not enter
             const bool ok = i < clen;
             dqv[s][jj] = ok ? sa[jj] + p.scale * eg * dqg[jj] : 0.f;
             dkv[s][jj] = ok ? sn[jj] + tj[jj] - eg * dxs[jj] + egc * dke[jj] : 0.f;
@@ -1689,7 +1690,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             if (i < clen) p.dg[(t0 + i) * sqk + (int64_t)h * DK + c] = dv[r] + post;
         }
     }
-    if (tid < clen) {
+    if (tid < clen && p.dbeta) {
         const float b = bet[tid];                            // sigmoid(logit) when fused: its derivative b (1 - b)
         p.dbeta[(t0 + tid) * H + h] = p.fz.beta_sigmoid ? dbet[tid] * b * (1.f - b) : dbet[tid];
     }

@@ -89,6 +89,9 @@ struct ChunkParams {
     void *hs;                     // [chunk slots, H, dv, dk] entry states for the backward (16-bit), or NULL
     float *nout;                  // per-channel gate: [chunk slots, H, CH, CH] N = strict_lower(gated K K^T)
                                   // for the backward (chunk prep writes the lower tiles), or NULL
+    int te_identity;              // (with use_delta) the recurrence without the delta rule, U = V, in the
+                                  // delta form's blocks: TE = I and GX = 0 (per-channel gate: a zero K*G
+                                  // tile); beta is not read.  For the chunked backward of that recurrence.
 };
 
 // Backward of the chunked scan (scalar gate, per-channel gate or none, delta
@@ -115,6 +118,8 @@ struct ChunkBwdParams {
                                   // (per-channel gate): g holds the pre-activation f, dg is df
     float *dpart;                 // gate_act: [chunk slots, H, dk + 1] per-chunk sums of ddt_bias, then dA_log
     float *dA_log, *ddt_bias;     // gate_act: [H], [H * dk]
+    int delta;                    // 0: the recurrence without the delta rule (blocks from
+                                  // ChunkParams::te_identity; beta and dbeta NULL)
     int H, DV;
     int n_tiles;                  // dv tiles of the walk kernels (set by the launcher)
     int n_chunk_slots;

@@ -278,7 +278,7 @@ def _chunk_bwd_covers(q, g, chunk_size):
 
 
 def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, cu_seqlens=None,
-                               chunk_size=64, saved_workspace=None, fusion: _Fusion = _NO_FUSION):
+                               chunk_size=64, saved_workspace=None, fusion: _Fusion = _NO_FUSION, delta=True):
     """Backward of chunk_gated_delta_rule / chunk_kda without autograd
     (vgdr_chunk_bwd): the gradients of (o, final_state) under the cotangents
     do (and dht, None = zero) with respect to q, k, v, g, beta and
@@ -295,9 +295,14 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     fusion: the producer fusions the kernels differentiate through (16-bit;
     no L2 norm): beta as logits (dbeta is their gradient) and, with a
     per-channel g, the gate activation (g is its pre-activation f, dg is df,
-    and the tuple gains dA_log and ddt_bias)."""
+    and the tuple gains dA_log and ddt_bias).
+    delta=False: the recurrence without the delta rule (chunk_simple_gla,
+    chunk_scan_vec(delta=False)) through vgdr_chunk_bwd_nodelta; beta is None
+    and so is dbeta."""
     assert not fusion.l2norm, 'the fused L2 norm is differentiated in torch, before the kernels'
-    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=_gate_of(g), delta=True,
+    assert delta or (beta is None and not fusion.any and saved_workspace is None), \
+        'without the delta rule there is no beta, fusion or saved workspace'
+    c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=_gate_of(g), delta=delta,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
@@ -311,7 +316,7 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
     vec = c.gate_kind == _lib.VGDR_GATE_VECTOR
     dg = None if g is None else (new(c.B, c.T, c.H, c.dkp) if vec else new(c.B, c.T, c.H))
-    db = new(c.B, c.T, c.H)
+    db = new(c.B, c.T, c.H) if delta else None
     dS0 = new(c.N, c.H, c.dkp, c.dvp) if initial_state is not None else None
     L = _lib.load()
     dtype = _DTYPES[c.dtype]
@@ -327,7 +332,12 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
             c.B, c.T, c.H, c.dkp, c.dvp, c.N, scale, int(chunk_size))
     dA = ddt = None
     with torch.cuda.device(c.device):
-        if fusion.any:
+        if not delta:
+            _lib.check(L.vgdr_chunk_bwd_nodelta(dtype, c.gate_kind, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
+                                                _ptr(c.h0), _ptr(dop), _ptr(dSp), _ptr(dq), _ptr(dk), _ptr(dv),
+                                                _ptr(dg), _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes, c.B, c.T, c.H,
+                                                c.dkp, c.dvp, c.N, scale, int(chunk_size), _stream(c.device)))
+        elif fusion.any:
             fz, keep = fusion.struct(c)
             if fusion.gate:
                 dA, ddt = new(c.H), new(c.H * c.dkp)
@@ -343,7 +353,7 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
         dv = dv[..., :c.dv]
     if dS0 is not None:
         dS0 = c.unpad_state(dS0).to(initial_state.dtype)
-    out = (dq, dk, dv, None if dg is None else dg.to(g.dtype), db.to(beta.dtype), dS0)
+    out = (dq, dk, dv, None if dg is None else dg.to(g.dtype), None if db is None else db.to(beta.dtype), dS0)
     if fusion.gate:
         ddt = ddt.reshape(c.H, c.dkp)[:, :c.dk].reshape(fusion.dt_bias.shape).to(fusion.dt_bias.dtype)
         out += (dA.reshape(fusion.A_log.shape).to(fusion.A_log.dtype), ddt)
@@ -503,6 +513,31 @@ class _ChunkDeltaRule(torch.autograd.Function):
         return grads[:6] + (dA, ddt, None, None, None, None)
 
 
+class _ChunkPlain(torch.autograd.Function):
+    """The chunked recurrence without the delta rule (chunk_simple_gla,
+    chunk_scan_vec / chunk_scan with delta=False), differentiable: forward
+    vgdr_chunk_fwd, backward vgdr_chunk_bwd_nodelta (the delta form's
+    kernels on blocks with TE = I and no K decay, so U = V; they recompute
+    the entry states)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, S0, scale, cu, chunk_size):
+        o, S = chunk_scan(q, k, v, g, None, gate=_gate_of(g), delta=False, scale=scale, initial_state=S0,
+                          output_final_state=True, cu_seqlens=cu, chunk_size=chunk_size)
+        ctx.save_for_backward(q, k, v, g, S0, cu)
+        ctx.scale, ctx.chunk_size = scale, chunk_size
+        return o, S
+
+    @staticmethod
+    def backward(ctx, do, dS):
+        q, k, v, g, S0, cu = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
+        dq, dk, dv, dg, _, dS0 = chunk_gated_delta_rule_bwd(q, k, v, g, None, S0, do, dS, scale=ctx.scale,
+                                                            cu_seqlens=cu, chunk_size=ctx.chunk_size, delta=False)
+        return dq, dk, dv, dg, dS0, None, None, None
+
+
 def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None, output_final_state=False,
                cu_seqlens=None, chunk_size=64, phase_event=None, fusion: _Fusion = _NO_FUSION):
     """Chunkwise prefill, the general form behind chunk_gated_delta_rule,
@@ -516,7 +551,8 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
 
     With grads enabled and an input that requires grad, the scan runs through
     _ChunkDeltaRule (delta rule: scalar gate or none, or the per-channel gate
-    with 16-bit inputs in 64-token chunks) or _ScanRule (every other form).
+    with 16-bit inputs in 64-token chunks), _ChunkPlain (no delta rule, the
+    same gate forms) or _ScanRule (every other form).
     The fused L2 norm then runs in torch, differentiably; the beta sigmoid and
     the gate activation stay inside the kernels, forward and backward, on the
     16-bit _ChunkDeltaRule path (no fp32 (B, T, H, dk) gate tensor is made),
@@ -539,7 +575,9 @@ def chunk_scan(q, k, v, g, beta, *, gate, delta, scale=None, initial_state=None,
         if fusion.gate:
             g = _gate_activation_rows(g, fusion)
         gk = None if gate == 'none' else g
-        if not chunked:
+        if not delta and _chunk_bwd_covers(q, gk, chunk_size):
+            o, S = _ChunkPlain.apply(q, k, v, gk, initial_state, scale, cu_seqlens, chunk_size)
+        elif not chunked:
             o, S = _ScanRule.apply(q, k, v, gk, beta if delta else None, initial_state, None, scale, cu_seqlens,
                                    chunk_size, delta)
         else:
