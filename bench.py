@@ -391,6 +391,11 @@ def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
     nodelta_us = _event_us(torch, lambda i: ops.chunk_gated_delta_rule_bwd(x.q, x.k, x.v, x.g, None, x.initial_state,
                                                                            do, dST, scale=scale, delta=False),
                            steps, warmup)
+    # explicit write vectors (chunk_scan_vec(..., w=)) through the same kernels on chunk prep's WR blocks
+    wv = (0.5 * torch.nn.functional.normalize(torch.randn(*x.q.shape, generator=g).cuda(), dim=-1)).to(x.q.dtype)
+    w_us = _event_us(torch, lambda i: ops.chunk_write_bwd(x.q, x.k, x.v, wv, x.g, x.initial_state, do, dST,
+                                                          scale=scale), steps, warmup)
+    del wv
     walk_us = None
     if token_walk:
         walk_us = _event_us(torch, lambda i: ops.scan_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST,
@@ -408,6 +413,8 @@ def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
          'train_pair_us': round(pair_us, 1),
          'train_pair': 'vgdr_chunk_fwd_saving + vgdr_chunk_bwd_saved (what autograd runs for 16-bit inputs)',
          'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2),
+         'w_us': round(w_us, 1),
+         'w': 'explicit write vectors (vgdr_chunk_bwd_w: the same kernels on chunk prep\'s WR blocks, dw for dbeta)',
          'nodelta_us': round(nodelta_us, 1),
          'nodelta': 'the recurrence without the delta rule (vgdr_chunk_bwd_nodelta: the same kernels on blocks '
                     'with TE = I and no K decay)'}

@@ -311,6 +311,21 @@ int vgdr_chunk_bwd_nodelta(int dtype, int gate_kind, const void *q, const void *
                            float scale, int chunk_size, hipStream_t stream);
 
 /*
+ * Backward of the chunked scan with explicit write vectors (vgdr_chunk_fwd_w's
+ * recurrence, chunk_scan_vec(..., w=) with grads, linear_attention.py:312-425,
+ * :340-353, :389-396): vgdr_chunk_bwd's arguments for gate_kind 2 with w in
+ * place of beta, grad_w [n_tokens, H, dk] (dtype, 16-byte aligned like w) in
+ * place of grad_beta; 16-bit q, k, v, w, 64-token chunks.  The workspace is
+ * vgdr_chunk_bwd_workspace_size's for gate_kind 2.
+ */
+int vgdr_chunk_bwd_w(int dtype, const void *q, const void *k, const void *v, const void *w, const float *g,
+                     const float *initial_state, const void *grad_o, const float *grad_final_state,
+                     void *grad_q, void *grad_k, void *grad_v, void *grad_w, float *grad_g,
+                     float *grad_initial_state, const int32_t *cu_seqlens, void *workspace,
+                     int64_t workspace_bytes, int64_t B, int64_t T, int64_t H, int64_t dk, int64_t dv,
+                     int64_t n_seqs, float scale, int chunk_size, hipStream_t stream);
+
+/*
  * The training pair with the producer fusions the backward can take through
  * (no reference counterpart as entry points: fla's chunk_kda /
  * chunk_gated_delta_rule with use_beta_sigmoid_in_kernel and

@@ -268,3 +268,112 @@ def test_kda_training_keeps_no_fp32_gate_tensor(lower_bound):
         err = _rel(a, b)
         print(f'[parity] kda fused training d{name} rel_l2={err:.3e}', flush=True)
         assert err <= 2e-2, f'd{name}: {err:.3e}'
+
+
+# ---- explicit write vectors (vgdr_chunk_bwd_w) ----------------------------------
+
+def test_write_bwd_argument_checks():
+    L = _lib.load()
+
+    def call(**over):
+        a = dict(dtype=1, q=4096, k=8192, v=12288, w=16384, g=20480, h0=None, do=24576, dht=None, dq=28672,
+                 dk=32768, dv=36864, dw=40960, dg=45056, dh0=None, cu=None, ws=49152, wsb=1 << 40, B=2, T=64, H=2,
+                 dk_=64, dv_=64, N=2, chunk=64)
+        a.update(over)
+        return L.vgdr_chunk_bwd_w(a['dtype'], a['q'], a['k'], a['v'], a['w'], a['g'], a['h0'], a['do'], a['dht'],
+                                  a['dq'], a['dk'], a['dv'], a['dw'], a['dg'], a['dh0'], a['cu'], a['ws'], a['wsb'],
+                                  a['B'], a['T'], a['H'], a['dk_'], a['dv_'], a['N'], 0.125, a['chunk'], None)
+    assert call(dtype=0) == _lib.VGDR_ERR_UNSUPPORTED
+    assert call(chunk=32) == _lib.VGDR_ERR_UNSUPPORTED
+    assert call(w=None) == _lib.VGDR_ERR_INVALID
+    assert call(w=16392) == _lib.VGDR_ERR_INVALID                   # alignment
+    assert call(dw=None) == _lib.VGDR_ERR_INVALID
+    assert call(dw=16384) == _lib.VGDR_ERR_INVALID                  # grad_w aliasing w
+    assert call(B=0, N=0, T=0) == _lib.VGDR_OK
+
+
+def _w_inputs(B, T, H, dk, dv, dtype, seed, strong=False):
+    q, k, v, g, _, S0, do, dST = _inputs(B, T, H, dk, dv, dtype, seed, strong=strong)
+    gen = torch.Generator().manual_seed(seed + 1000)
+    w = (0.5 * F.normalize(torch.randn(B, T, H, dk, generator=gen), dim=-1)).to(dtype)
+    return q, k, v, w, g, S0, do, dST
+
+
+def _w_device_grads(q, k, v, w, g, S0, do, dST, scale, cu=None):
+    leaves = [None if x is None else x.cuda().requires_grad_(True) for x in (q, k, v, g, S0, w)]
+    o, S = ops.chunk_scan_vec(*leaves[:4], None, leaves[4], scale=scale, delta=True, w=leaves[5],
+                              cu_seqlens=None if cu is None else cu.cuda())
+    torch.autograd.backward([o, S], [do.cuda(), dST.cuda()])
+    dq, dk, dv, dg, dS0, dw = (None if x is None else x.grad for x in leaves)
+    return dq, dk, dv, dg, dS0, dw
+
+
+W_NAMES = ('dq', 'dk', 'dv', 'dg', 'dS0', 'dw')
+
+
+def _w_compare(got, r, tol, case):
+    ref = (r[0], r[1], r[2], r[3], r[5], r[6])                 # recurrent_grads with w: dbeta (zero) dropped
+    for name, a, b in zip(W_NAMES, got, ref):
+        if b is None:
+            assert a is None, name
+            continue
+        err = _rel(a, b)
+        print(f'[parity] {case} {name} rel_l2={err:.3e}', flush=True)
+        assert err <= tol, f'{name}: {err:.3e} > {tol:g}'
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize('shape', [(2, 100, 2, 64, 64), (1, 70, 2, 128, 128), (1, 45, 1, 100, 48)])
+@pytest.mark.parametrize('strong', [False, True])
+def test_write_chunk_bwd_matches_oracle(dtype, shape, strong):
+    B, T, H, dk, dv = shape
+    print(f'\n[case] w chunk_bwd dtype={dtype} shape={shape} strong={strong}', flush=True)
+    q, k, v, w, g, S0, do, dST = _w_inputs(B, T, H, dk, dv, dtype, seed=T + dk + 3 * strong, strong=strong)
+    scale = dk ** -0.5
+    r = gdr.recurrent_grads(q, k, v, g, None, S0, do, dST, scale=scale, w=w)
+    got = _w_device_grads(q, k, v, w, g, S0, do, dST, scale)
+    _w_compare(got, r, 2e-2, f'w {dtype} {shape} strong={strong}')
+
+
+@pytest.mark.gpu
+def test_write_chunk_bwd_varlen_and_full_size():
+    """A packed batch (empty, one-token, multi-chunk segments) against the
+    oracle, then B4 T8192 H8 against vgdr_scan_bwd with w on the same inputs."""
+    cu = torch.tensor([0, 0, 1, 70, 75, 200], dtype=torch.int32)
+    N, T, H, dk, dv = 5, 200, 2, 64, 64
+    q, k, v, w, g, _, do, _ = _w_inputs(1, T, H, dk, dv, torch.bfloat16, seed=43)
+    gen = torch.Generator().manual_seed(44)
+    S0 = 0.3 * torch.randn(N, H, dk, dv, generator=gen)
+    dST = torch.randn(N, H, dk, dv, generator=gen)
+    print('\n[case] w chunk_bwd varlen', flush=True)
+    scale = dk ** -0.5
+    parts = [[] for _ in range(7)]
+    for n in range(N):
+        a, b = int(cu[n]), int(cu[n + 1])
+        sl = lambda x: x[:, a:b]
+        r = gdr.recurrent_grads(sl(q), sl(k), sl(v), sl(g), None, S0[n:n + 1], sl(do), dST[n:n + 1],
+                                scale=scale, w=sl(w))
+        for i in (0, 1, 2, 3, 5, 6):
+            parts[i].append(r[i])
+    ref = [torch.cat(parts[i], 0 if i == 5 else 1) if parts[i] else None for i in range(7)]
+    got = _w_device_grads(q, k, v, w, g, S0, do, dST, scale, cu=cu)
+    _w_compare(got, ref, 2e-2, 'w varlen')
+
+    B, T, H, dk, dv = 4, 8192, 8, 128, 128
+    print('\n[case] w chunk_bwd full size vs scan_bwd', flush=True)
+    g0 = torch.Generator(device='cpu').manual_seed(45)
+    rr = lambda *s: torch.randn(*s, generator=g0).cuda()
+    q = F.normalize(rr(B, T, H, dk), dim=-1).bfloat16()
+    k = F.normalize(rr(B, T, H, dk), dim=-1).bfloat16()
+    w = (0.5 * F.normalize(rr(B, T, H, dk), dim=-1)).bfloat16()
+    v = rr(B, T, H, dv).bfloat16()
+    g = F.logsigmoid(rr(B, T, H, dk) + 4.0)
+    S0 = 0.1 * rr(B, H, dk, dv)
+    do, dST = rr(B, T, H, dv).bfloat16(), rr(B, H, dk, dv)
+    got = ops.chunk_write_bwd(q, k, v, w, g, S0, do, dST, scale=dk ** -0.5)
+    ref = ops.scan_bwd(q, k, v, g, None, S0, do, dST, scale=dk ** -0.5, w=w)
+    for name, a, b in zip(('dq', 'dk', 'dv', 'dw', 'dg', 'dS0'), got, (ref[0], ref[1], ref[2], ref[6], ref[3], ref[5])):
+        err = _rel(a, b)
+        print(f'[parity] w full size vs scan_bwd {name} rel_l2={err:.3e}', flush=True)
+        assert err <= 2e-2, f'{name}: {err:.3e}'

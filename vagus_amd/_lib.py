@@ -74,6 +74,7 @@ SIGNATURES = {
                                   _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P, _P, _P]),
     'vgdr_chunk_bwd_saved_fused': (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                         _L, _L, _L, _L, _L, _L, _L, _F, _I, _FZ, _P, _P, _P]),
+    'vgdr_chunk_bwd_w': (_I, [_I] + [_P] * 16 + [_L, _L, _L, _L, _L, _L, _L, _F, _I, _P]),
     'vgdr_chunk_bwd_nodelta': (_I, [_I, _I] + [_P] * 14 + [_L, _L, _L, _L, _L, _L, _L, _F, _I, _P]),
     'vgdr_scan_bwd_workspace_size': (_L, [_L, _L, _L, _L, _L, _L]),
     'vgdr_scan_bwd': (_I, [_I, _I, _I] + [_P] * 18 + [_L, _L, _L, _L, _L, _L, _L, _F, _P]),

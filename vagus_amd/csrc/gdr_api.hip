@@ -362,13 +362,22 @@ int64_t vgdr_chunk_bwd_workspace_size(int dtype, int gate_kind, int64_t B, int64
 namespace {
 // the backward entry points; saved: the workspace holds what a saving forward left
 // delta: the delta rule (else the plain recurrence: no beta, no grad_beta)
+// w: explicit write vectors (the delta rule without beta; grad_w receives their gradient)
 int bwd_call(const char *fn, bool saved, bool delta, VGDR_BWD_ARGS, const vgdr_fusion *fusion, float *grad_A_log,
-             float *grad_dt_bias) {
+             float *grad_dt_bias, const void *w = nullptr, void *grad_w = nullptr) {
     g_err[0] = 0;
-    int rc = check_common(fn, dtype, gate_kind, delta ? 1 : 0, q, k, v, g, beta, grad_o, cu_seqlens, B, T, H, dk,
-                          dv, n_seqs);
+    int rc = check_common(fn, dtype, gate_kind, delta && !w ? 1 : 0, q, k, v, g, beta, grad_o, cu_seqlens, B, T, H,
+                          dk, dv, n_seqs);
     if (rc) return rc;
-    if (!delta) beta = grad_beta = nullptr;
+    if (!delta || w) beta = grad_beta = nullptr;
+    if (w) {
+        if (dtype == VGDR_F32 || gate_kind != VGDR_GATE_VECTOR)
+            return fail(VGDR_ERR_UNSUPPORTED, "%s: the chunked explicit write takes 16-bit q, k, v, w and a "
+                        "per-channel g", fn);
+        if (!aligned16(w)) return fail(VGDR_ERR_INVALID, "%s: w must be 16-byte aligned", fn);
+        if (B * T > 0 && !grad_w) return fail(VGDR_ERR_INVALID, "%s: grad_w is required", fn);
+        if (grad_w == w) return fail(VGDR_ERR_INVALID, "%s: the gradients must not alias the inputs", fn);
+    }
     vgdr::Fusion fz;
     rc = check_fusion(fn, fusion, dtype, gate_kind, delta ? 1 : 0, true, fz);
     if (rc) return rc;
@@ -381,8 +390,9 @@ int bwd_call(const char *fn, bool saved, bool delta, VGDR_BWD_ARGS, const vgdr_f
     if (gate_kind == VGDR_GATE_VECTOR && (dtype == VGDR_F32 || effective_chunk(dtype, dk, chunk_size) != 64))
         return fail(VGDR_ERR_UNSUPPORTED, "%s: the per-channel-gate backward runs 16-bit q, k, v in 64-token chunks",
                     fn);
-    if (B * T > 0 && (!grad_q || !grad_k || !grad_v || (delta && !grad_beta)))
-        return fail(VGDR_ERR_INVALID, "%s: grad_q, grad_k, grad_v%s are required", fn, delta ? " and grad_beta" : "");
+    if (B * T > 0 && (!grad_q || !grad_k || !grad_v || (delta && !w && !grad_beta)))
+        return fail(VGDR_ERR_INVALID, "%s: grad_q, grad_k, grad_v%s are required", fn,
+                    delta && !w ? " and grad_beta" : "");
     if (grad_v == v || grad_q == q || grad_k == k)
         return fail(VGDR_ERR_INVALID, "%s: the gradients must not alias the inputs", fn);
     if (!aligned16(grad_o) || !aligned16(grad_v))
@@ -410,6 +420,7 @@ int bwd_call(const char *fn, bool saved, bool delta, VGDR_BWD_ARGS, const vgdr_f
     f.n_chunk_slots = (int)ws.fwd.slots;
     f.use_delta = 1;                                          // the delta form's blocks; without the delta
     f.te_identity = delta ? 0 : 1;                            // rule TE = I and GX = 0 make U = V
+    f.w = w;
     f.scale = scale;
     f.fz = fz;
     vgdr::ChunkBwdParams p{};
@@ -433,6 +444,8 @@ int bwd_call(const char *fn, bool saved, bool delta, VGDR_BWD_ARGS, const vgdr_f
     p.n_chunk_slots = (int)ws.fwd.slots;
     p.scale = scale;
     p.delta = delta ? 1 : 0;
+    p.w = w;
+    p.dw = grad_w;
     if (gate_kind == VGDR_GATE_VECTOR) {
         p.nbuf = reinterpret_cast<const float *>(wsb + ws.nbuf_off);
         p.gw = reinterpret_cast<float *>(wsb + ws.gw_off);
@@ -467,6 +480,22 @@ int vgdr_chunk_bwd_fused(VGDR_BWD_ARGS_FUSED) {
 }
 int vgdr_chunk_bwd_saved_fused(VGDR_BWD_ARGS_FUSED) {
     return bwd_call("vgdr_chunk_bwd_saved_fused", true, true, VGDR_BWD_PASS, fusion, grad_A_log, grad_dt_bias);
+}
+int vgdr_chunk_bwd_w(int dtype, const void *q, const void *k, const void *v, const void *w, const float *g,
+                     const float *initial_state, const void *grad_o, const float *grad_final_state, void *grad_q,
+                     void *grad_k, void *grad_v, void *grad_w, float *grad_g, float *grad_initial_state,
+                     const int32_t *cu_seqlens, void *workspace, int64_t workspace_bytes, int64_t B, int64_t T,
+                     int64_t H, int64_t dk, int64_t dv, int64_t n_seqs, float scale, int chunk_size,
+                     hipStream_t stream) {
+    if (B * T > 0 && !w) {
+        g_err[0] = 0;
+        return fail(VGDR_ERR_INVALID, "vgdr_chunk_bwd_w: w is required");
+    }
+    static const char dummy[16] __attribute__((aligned(16))) = {};     // w for an empty call: never read
+    return bwd_call("vgdr_chunk_bwd_w", false, true, dtype, VGDR_GATE_VECTOR, q, k, v, g, nullptr, initial_state,
+                    grad_o, grad_final_state, grad_q, grad_k, grad_v, grad_g, nullptr, grad_initial_state, cu_seqlens,
+                    workspace, workspace_bytes, B, T, H, dk, dv, n_seqs, scale, chunk_size, stream, nullptr, nullptr,
+                    nullptr, w ? w : dummy, grad_w);
 }
 int vgdr_chunk_bwd_nodelta(int dtype, int gate_kind, const void *q, const void *k, const void *v, const float *g,
                            const float *initial_state, const void *grad_o, const float *grad_final_state, void *grad_q,

@@ -481,8 +481,8 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             aq[jj] = (jt <= irow) ? p.scale * accq[jj] * d : 0.f;
             mk[jj] = (jt < irow) ? bet[irow] * acck[jj] * d : 0.f;
         }
-        if constexpr (GATE == 2 && !WR) {
-            // N itself (before diag(beta)), for the backward
+        if constexpr (GATE == 2) {
+            // N itself (before diag(beta); with W, M = <k_i, w_j>), for the backward
             if (p.nout) {
                 float *nb = p.nout + (slot * H + h) * CH * CH + irow * CH + 16 * J + 4 * g4;
 #pragma unroll

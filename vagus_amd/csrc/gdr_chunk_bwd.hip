@@ -1275,7 +1275,15 @@ __device__ __forceinline__ float load_gate(const ChunkBwdParams &p, int64_t off)
 // w / (DK / 16) + (8 / (DK / 16)) s; its MFMA output rows and column are the
 // rows and channel whose q, k and gamma it holds, so the epilogue runs in
 // registers.
-template <int DK, int CH, typename E>
+// WR: explicit write vectors w in place of beta k (chunk prep's WR blocks:
+// M_ij = <k_i, w_j>_E, A_ij = scale <q_i, w_j>_E, TE = (I + M)^-1, the write
+// tile W*Gend).  beta is 1 (dN = dM), the j side of M and A is w, and the
+// write tile's gradient goes to w:
+//     SA_i = sum_j W_A_ij w_j E_ij     SN_i = sum_j dM_ij w_j E_ij     TJ as above (-> dw)
+//     dk_i = SN_i - e^gamma_i (dX S^T)_i     dw_j = TJ_j + e^(gamma_C - gamma_j) (U dS'^T)_j
+//     dgamma_i = q_i SA_i + k_i SN_i - w_i TJ_i + (scale q e^gamma) (dO S^T) - (k e^gamma) (dX S^T)
+//                - (w e^(gamma_C - gamma)) (U dS'^T),  dgamma_C += sum_i (w e^(gamma_C - gamma))_i (U dS'^T)_i + ...
+template <int DK, int CH, typename E, bool WR = false>
 __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
     using CB = ChunkBlock<E, CH, DK, 2>;
@@ -1288,6 +1296,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     typedef E V __attribute__((ext_vector_type(VE)));
     __shared__ __attribute__((aligned(16))) E qs[CH * DK];          // q, later dq
     __shared__ __attribute__((aligned(16))) E ks[CH * DK];          // k, later dk
+    __shared__ __attribute__((aligned(16))) E ws[WR ? CH * DK : 8]; // w, later dw (WR)
     __shared__ __attribute__((aligned(16))) float gms[CH * DK];     // gamma, later dgamma
     // TE (element type, as chunk prep wrote it), the CH x CH algebra's fp32
     // matrices (pitch PW), then (same memory) the A operands of the gated sums
@@ -1337,9 +1346,10 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             tv[m] = ld4(gT + 4 * u);
             wav[m] = ld4(gA + 4 * u);
         }
-        RowRegs<E, CH, DK, NT> rk, rq;
+        RowRegs<E, CH, DK, NT> rk, rq, rw;
         rk.load(reinterpret_cast<const E *>(p.k) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
         rq.load(reinterpret_cast<const E *>(p.q) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
+        if constexpr (WR) rw.load(reinterpret_cast<const E *>(p.w) + t0 * sqk + (int64_t)h * DK, sqk, clen, tid);
         // gamma: inclusive sums over rows rg RPT .. + RPT - 1 here, the earlier groups' totals added below
         // (fused activation: g = act(f) from the pre-activation, as chunk prep computes it)
         float gv[RPT];
@@ -1356,6 +1366,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
         }
         rk.store(ks, DK, clen, tid);
         rq.store(qs, DK, clen, tid);
+        if constexpr (WR) rw.store(ws, DK, clen, tid);
 #pragma unroll
         for (int r = 1; r < RPT; ++r) gv[r] += gv[r - 1];
         part[rg][c] = gv[RPT - 1];
@@ -1375,7 +1386,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             st4(b2 + row * PW + c0, tv[m]);
         }
         if (tid < CH) {
-            const float b = tid < clen && p.beta ? p.beta[(t0 + tid) * H + h] : 0.f;   // no delta rule: 0
+            const float b = WR ? 1.f : (tid < clen && p.beta ? p.beta[(t0 + tid) * H + h] : 0.f);   // no delta rule: 0
             bet[tid] = tid < clen ? (p.fz.beta_sigmoid ? sigmoidf_(b) : b) : 0.f;
             dbet[tid] = 0.f;
         }
@@ -1503,6 +1514,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     // ---- the gated sums (MFMA) and the direct terms ----------------------------
     const int cc = 16 * (wave % NCT) + r16;                  // this lane's key channel
     float kr[NB][4], qr[NB][4], gr[NB][4];                   // rows 16 J + 4 g4 + jj of channel cc
+    float wr[WR ? NB : 1][4];                                // (WR) w at the same rows
 #pragma unroll
     for (int J = 0; J < NB; ++J)
 #pragma unroll
@@ -1511,10 +1523,12 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             kr[J][jj] = EL::to_f(ks[row * DK + cc]);
             qr[J][jj] = EL::to_f(qs[row * DK + cc]);
             gr[J][jj] = gms[row * DK + cc];
+            if constexpr (WR) wr[J][jj] = EL::to_f(ws[row * DK + cc]);
         }
+    const E *js = WR ? ws : ks;                              // the j side of M and A: w, or k
     const float gCc = gms[(CH - 1) * DK + cc];               // gamma_C (rows past the end add no decay)
     const float gCt = gms[(CH - 1) * DK + c];                // the same for the dg pass's channel
-    float dqv[IPW][4], dkv[IPW][4], dgv[IPW][4];
+    float dqv[IPW][4], dkv[IPW][4], dgv[IPW][4], dwv[WR ? IPW : 1][4];
     float dgc_acc = 0.f;
 #pragma unroll
     for (int s = 0; s < IPW; ++s) {
@@ -1536,7 +1550,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             if (J < I || (J == I && !exact)) {
                 f32x4 b;
 #pragma unroll
-                for (int jj = 0; jj < 4; ++jj) b[jj] = kr[J][jj] * __expf(gref - gr[J][jj]);
+                for (int jj = 0; jj < 4; ++jj) b[jj] = (WR ? wr[J][jj] : kr[J][jj]) * __expf(gref - gr[J][jj]);
                 sa = mfma_kb1(ld4(wa + (16 * I + r16) * PW + 16 * J + 4 * g4), b, sa);
                 sn = mfma_kb1(ld4(wn + (16 * I + r16) * PW + 16 * J + 4 * g4), b, sn);
             }
@@ -1572,7 +1586,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
                 const float gi = gr[I][jj];
                 float a = 0.f, n = 0.f, t = 0.f;
                 for (int j = 16 * I; j <= i; ++j) {
-                    const float kj = EL::to_f(ks[j * DK + cc]) * __expf(gi - gms[j * DK + cc]);
+                    const float kj = EL::to_f(js[j * DK + cc]) * __expf(gi - gms[j * DK + cc]);
                     a += wa[i * PW + j] * kj;
                     n += wn[i * PW + j] * kj;
                 }
@@ -1594,11 +1608,21 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             dxs[jj] = p.delta ? dxs[jj] : 0.f;                 // without the delta rule K*G does not enter
             const bool ok = i < clen;
             dqv[s][jj] = ok ? sa[jj] + p.scale * eg * dqg[jj] : 0.f;
-            dkv[s][jj] = ok ? sn[jj] + tj[jj] - eg * dxs[jj] + egc * dke[jj] : 0.f;
-            dgv[s][jj] = ok ? qi * sa[jj] + ki * sn[jj] - ki * tj[jj] + p.scale * qi * eg * dqg[jj] -
-                                  ki * eg * dxs[jj] - ki * egc * dke[jj]
-                            : 0.f;
-            dgc_acc += ok ? ki * egc * dke[jj] : 0.f;
+            if constexpr (WR) {
+                const float wi = wr[I][jj];
+                dkv[s][jj] = ok ? sn[jj] - eg * dxs[jj] : 0.f;
+                dwv[s][jj] = ok ? tj[jj] + egc * dke[jj] : 0.f;
+                dgv[s][jj] = ok ? qi * sa[jj] + ki * sn[jj] - wi * tj[jj] + p.scale * qi * eg * dqg[jj] -
+                                      ki * eg * dxs[jj] - wi * egc * dke[jj]
+                                : 0.f;
+                dgc_acc += ok ? wi * egc * dke[jj] : 0.f;
+            } else {
+                dkv[s][jj] = ok ? sn[jj] + tj[jj] - eg * dxs[jj] + egc * dke[jj] : 0.f;
+                dgv[s][jj] = ok ? qi * sa[jj] + ki * sn[jj] - ki * tj[jj] + p.scale * qi * eg * dqg[jj] -
+                                      ki * eg * dxs[jj] - ki * egc * dke[jj]
+                                : 0.f;
+                dgc_acc += ok ? ki * egc * dke[jj] : 0.f;
+            }
         }
     }
     atomicAdd(&dgc[cc], dgc_acc);
@@ -1611,6 +1635,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             const int i = 16 * I + 4 * g4 + jj;
             qs[i * DK + cc] = EL::from_f(dqv[s][jj]);
             ks[i * DK + cc] = EL::from_f(dkv[s][jj]);
+            if constexpr (WR) ws[i * DK + cc] = EL::from_f(dwv[s][jj]);
             gms[i * DK + cc] = dgv[s][jj];
         }
     }
@@ -1619,6 +1644,7 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     {
         E *dqg = reinterpret_cast<E *>(p.dq) + t0 * sqk + (int64_t)h * DK;
         E *dkg = reinterpret_cast<E *>(p.dk) + t0 * sqk + (int64_t)h * DK;
+        E *dwg = WR ? reinterpret_cast<E *>(p.dw) + t0 * sqk + (int64_t)h * DK : nullptr;
 #pragma unroll
         for (int n = 0; n < OUT_N; ++n) {
             const int u = tid + n * NT;
@@ -1626,6 +1652,8 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             if (u < CH * UPR && row < clen) {
                 *reinterpret_cast<V *>(dqg + row * sqk + c0) = *reinterpret_cast<const V *>(qs + row * DK + c0);
                 *reinterpret_cast<V *>(dkg + row * sqk + c0) = *reinterpret_cast<const V *>(ks + row * DK + c0);
+                if constexpr (WR)
+                    *reinterpret_cast<V *>(dwg + row * sqk + c0) = *reinterpret_cast<const V *>(ws + row * DK + c0);
             }
         }
     }
@@ -1750,7 +1778,12 @@ static hipError_t run_bwd_vec(ChunkBwdParams p, hipStream_t stream) {
     const int64_t grad_blocks = (int64_t)p.n_chunk_slots * p.H;
     if (grad_blocks > 0) {
         hipLaunchKernelGGL((chunk_grad_kernel<DK, CH, E, true>), dim3((unsigned)grad_blocks), dim3(512), 0, stream, p);
-        hipLaunchKernelGGL((chunk_grad_vec_kernel<DK, CH, E>), dim3((unsigned)grad_blocks), dim3(512), 0, stream, p);
+        if (p.w)
+            hipLaunchKernelGGL((chunk_grad_vec_kernel<DK, CH, E, true>), dim3((unsigned)grad_blocks), dim3(512), 0,
+                               stream, p);
+        else
+            hipLaunchKernelGGL((chunk_grad_vec_kernel<DK, CH, E>), dim3((unsigned)grad_blocks), dim3(512), 0, stream,
+                               p);
         if (p.fz.gate_act)
             hipLaunchKernelGGL((gate_param_grad_kernel<DK>), dim3((unsigned)p.H), dim3(256), 0, stream, p);
     }

@@ -120,6 +120,8 @@ struct ChunkBwdParams {
     float *dA_log, *ddt_bias;     // gate_act: [H], [H * dk]
     int delta;                    // 0: the recurrence without the delta rule (blocks from
                                   // ChunkParams::te_identity; beta and dbeta NULL)
+    const void *w;                // per-channel gate: [n_tokens, H, dk] explicit write vectors in place of
+    void *dw;                     // beta k (chunk prep's WR blocks; beta and dbeta NULL), and their gradient
     int H, DV;
     int n_tiles;                  // dv tiles of the walk kernels (set by the launcher)
     int n_chunk_slots;

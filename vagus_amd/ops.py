@@ -1019,6 +1019,69 @@ def causal_conv1d(x, weight, bias=None, residual=None, initial_state=None, outpu
     return y, (st_out if output_final_state else None)
 
 
+def chunk_write_bwd(q, k, v, w, g, initial_state, do, dht=None, *, scale=None, cu_seqlens=None, chunk_size=64):
+    """Backward of chunk_scan_vec with explicit write vectors w (B, T, H, dk)
+    without autograd (vgdr_chunk_bwd_w; 16-bit q, k, v, w, per-channel g,
+    64-token chunks): the gradients of (o, final_state) under do (and dht,
+    None = zero).  Returns (dq, dk, dv, dw, dg, dh0), dh0 None without an
+    initial state."""
+    c = _Call(q, k, v, g, None, initial_state, cu_seqlens, gate='vector', delta=False,
+              dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+    scale = c.dk ** -0.5 if scale is None else float(scale)
+    assert w.shape == q.shape, f'w must be {tuple(q.shape)} (B, T, H, dk); got {tuple(w.shape)}'
+    assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
+    _check_device(w, do, dht)
+    wk = _aligned(_pad_to(w.to(c.dtype), {1: c.dkp}))
+    dop = _aligned(_pad_to(do.to(c.dtype), {1: c.dvp}))
+    dSp = None if dht is None else _aligned(_pad_to(dht.float(), {1: c.dvp, 2: c.dkp}))
+    new = lambda *shape, dt=torch.float32: torch.empty(*shape, dtype=dt, device=c.device)
+    dq, dk, dw = (new(c.B, c.T, c.H, c.dkp, dt=c.dtype) for _ in range(3))
+    dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
+    dg = new(c.B, c.T, c.H, c.dkp)
+    dS0 = new(c.N, c.H, c.dkp, c.dvp) if initial_state is not None else None
+    L = _lib.load()
+    dtype = _DTYPES[c.dtype]
+    nbytes = L.vgdr_chunk_bwd_workspace_size(dtype, _lib.VGDR_GATE_VECTOR, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
+                                             int(c.cu is not None), int(chunk_size))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=c.device)
+    with torch.cuda.device(c.device):
+        _lib.check(L.vgdr_chunk_bwd_w(dtype, _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(wk), _ptr(c.g), _ptr(c.h0),
+                                      _ptr(dop), _ptr(dSp), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dw), _ptr(dg),
+                                      _ptr(dS0), _ptr(c.cu), _ptr(ws), nbytes, c.B, c.T, c.H, c.dkp, c.dvp, c.N,
+                                      scale, int(chunk_size), _stream(c.device)))
+    if c.dkp != c.dk:
+        dq, dk, dw, dg = dq[..., :c.dk], dk[..., :c.dk], dw[..., :c.dk], dg[..., :c.dk]
+    if c.dvp != c.dv:
+        dv = dv[..., :c.dv]
+    if dS0 is not None:
+        dS0 = c.unpad_state(dS0).to(initial_state.dtype)
+    return dq, dk, dv, dw.to(w.dtype), dg.to(g.dtype), dS0
+
+
+class _ChunkWrite(torch.autograd.Function):
+    """chunk_scan_vec with explicit write vectors, differentiable: forward
+    vgdr_chunk_fwd_w, backward vgdr_chunk_bwd_w (the per-channel chunk
+    backward on chunk prep's WR blocks, which it rebuilds with the entry
+    states).  16-bit q, k, v, w, per-channel g, 64-token chunks."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, S0, w, scale, cu, chunk_size):
+        o, S = chunk_scan_vec(q, k, v, g, None, S0, scale=scale, delta=True, chunk_size=chunk_size, w=w,
+                              cu_seqlens=cu)
+        ctx.save_for_backward(q, k, v, g, S0, w, cu)
+        ctx.scale, ctx.chunk_size = scale, chunk_size
+        return o, S
+
+    @staticmethod
+    def backward(ctx, do, dS):
+        q, k, v, g, S0, w, cu = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
+        dq, dk, dv, dw, dg, dS0 = chunk_write_bwd(q, k, v, w, g, S0, do, dS, scale=ctx.scale, cu_seqlens=cu,
+                                                  chunk_size=ctx.chunk_size)
+        return dq, dk, dv, dg, dS0, dw, None, None, None
+
+
 def chunk_scan_vec(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_size: int = 64, w=None,
                    cu_seqlens=None):
     """The reference's chunk_scan_vec (linear_attention.py:312-425) on the GPU,
@@ -1029,16 +1092,20 @@ def chunk_scan_vec(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_siz
     in place of beta_t k_t (the asymmetric delta rule, :340-353, :389-396;
     beta unused), run chunkwise with 16-bit q, k, v and token by token (the
     same rule, vgdr_recurrent_fwd_w) in fp32.  Without w it is chunk_kda.
-    Differentiable (vgdr_scan_bwd) when an input requires grad."""
+    Differentiable when an input requires grad: with w, vgdr_chunk_bwd_w for
+    16-bit inputs in 64-token chunks, vgdr_scan_bwd otherwise."""
     B, T, H, dk = q.shape
     if w is not None and _wants_grad(q, k, v, g, beta, S0, w):
         assert delta, 'an explicit write vector needs the delta rule'
         scale = dk ** -0.5 if scale is None else float(scale)
-        return _ScanRule.apply(q, k, v, g, None, S0, w, scale, cu_seqlens, chunk_size, True)
+        if q.dtype == torch.float32 or chunk_size <= 32:
+            return _ScanRule.apply(q, k, v, g, None, S0, w, scale, cu_seqlens, chunk_size, True)
     if g is None:
         g = torch.zeros(B, T, H, dk, dtype=torch.float32, device=q.device)
     elif g.dim() == 3:
         g = g.float().unsqueeze(-1).expand(B, T, H, dk)
+    if w is not None and _wants_grad(q, k, v, g, beta, S0, w):
+        return _ChunkWrite.apply(q, k, v, g, S0, w, scale, cu_seqlens, chunk_size)
     if w is None:
         return chunk_scan(q, k, v, g, beta, gate='vector', delta=delta, scale=scale, initial_state=S0,
                           output_final_state=True, cu_seqlens=cu_seqlens, chunk_size=chunk_size)
