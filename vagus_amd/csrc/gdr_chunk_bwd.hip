@@ -360,7 +360,16 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
         for (int j = 0; j < 4; ++j)
             S[kt][j] = (p.h0 && wvalid) ? p.h0[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
     auto store_state = [&](int c) __attribute__((always_inline)) {
-        if (wvalid) {
+        if constexpr (sizeof(E) == 2) {
+            // branch-free (a wave past dv stores into a zero-byte resource), so the
+            // next wait for this wave's loads does not wait for these stores too
+            const __amdgpu_buffer_rsrc_t rs =
+                buffer_rsrc(reinterpret_cast<E *>(p.hs) + ((u.cbase + c) * H + h) * (int64_t)DK * DV,
+                            wvalid ? (uint32_t)(DK * DV * sizeof(E)) : 0u);
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt)
+                buffer_store_8b(EL::cvt(S[kt]), rs, (uint32_t)(ckpt_pos<DK>(colw >> 4, kt, lane) * sizeof(E)));
+        } else if (wvalid) {
             E *hs = reinterpret_cast<E *>(p.hs) + ((u.cbase + c) * H + h) * (int64_t)DK * DV;
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(hs + ckpt_pos<DK>(colw >> 4, kt, lane), EL::cvt(S[kt]));
@@ -599,7 +608,16 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
         const int64_t slot = u.cbase + c;
         const int64_t t0 = u.bos + (int64_t)c * CH;
         const int clen = clen_of(c);
-        if (wvalid) {
+        if constexpr (sizeof(E) == 2) {
+            // branch-free (a wave past dv stores into a zero-byte resource): a store
+            // under a branch made the join below wait for it to reach memory
+            const __amdgpu_buffer_rsrc_t rs =
+                buffer_rsrc(reinterpret_cast<E *>(p.dhs) + (slot * H + h) * (int64_t)DK * DV,
+                            wvalid ? (uint32_t)(DK * DV * sizeof(E)) : 0u);
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt)
+                buffer_store_8b(EL::cvt(dS[kt]), rs, (uint32_t)(ckpt_pos<DK>(colw >> 4, kt, lane) * sizeof(E)));
+        } else if (wvalid) {
             E *dhs = reinterpret_cast<E *>(p.dhs) + (slot * H + h) * (int64_t)DK * DV;
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(dhs + ckpt_pos<DK>(colw >> 4, kt, lane), EL::cvt(dS[kt]));
@@ -635,10 +653,20 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
                 const f32x4 dX = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NB,
                     [&](int kb) { return ld_colfrag<E>(TEm, PT, 16 * kb, 16 * I, lane); },
                     [&](int kb) { return Yb[kb]; });
+                if constexpr (sizeof(E) == 2) {
+                    // rows past the chunk's end fall outside the resource (no branch)
+                    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(
+                        reinterpret_cast<E *>(p.dv) + t0 * sv + (int64_t)h * DV, (uint32_t)(clen * sv * sizeof(E)));
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int row = 16 * I + 4 * g4 + j;
-                    if (row < clen) dvg[(t0 + row) * sv] = EL::from_f(dX[j]);
+                    for (int j = 0; j < 4; ++j)
+                        buffer_store_2b(EL::from_f(dX[j]), rv,
+                                        (uint32_t)(((16 * I + 4 * g4 + j) * sv + col) * sizeof(E)));
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int row = 16 * I + 4 * g4 + j;
+                        if (row < clen) dvg[(t0 + row) * sv] = EL::from_f(dX[j]);
+                    }
                 }
                 if constexpr (VEC) {                           // the factors are in the tiles
                     Ob[I] = EL::cvt(dO[I]);

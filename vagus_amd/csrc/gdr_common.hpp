@@ -183,6 +183,21 @@ __device__ __forceinline__ f32x4 buffer_load_nt4(__amdgpu_buffer_rsrc_t r, uint3
 __device__ __forceinline__ void buffer_store_nt4(f32x4 x, __amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, x), r, (int)voff, (int)soff, CPOL_NT);
 }
+// Stores that need no branch: a lane (or a wave, with a zero-byte resource)
+// whose store must not happen gets an offset outside the block.  A store under
+// a branch makes the join wait for every memory operation in flight (the wave
+// cannot know which path issued how many), stores included.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+template <typename F8>
+__device__ __forceinline__ void buffer_store_8b(F8 x, __amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    static_assert(sizeof(F8) == 8, "an 8-byte fragment");
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, x), r, (int)voff, 0, 0);
+}
+template <typename E2>
+__device__ __forceinline__ void buffer_store_2b(E2 x, __amdgpu_buffer_rsrc_t r, uint32_t voff) {
+    static_assert(sizeof(E2) == 2, "a 16-bit element");
+    __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, x), r, (int)voff, 0, 0);
+}
 
 // the reference's producer activations (linear_attention.py:703-706, :719-736)
 // 1 / (1 + e^-x) with the hardware reciprocal (v_rcp_f32, about 1 ulp): an IEEE
