@@ -1556,7 +1556,11 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
     const E *js = WR ? ws : ks;                              // the j side of M and A: w, or k
     const float gCc = gms[(CH - 1) * DK + cc];               // gamma_C (rows past the end add no decay)
     const float gCt = gms[(CH - 1) * DK + c];                // the same for the dg pass's channel
-    float dqv[IPW][4], dkv[IPW][4], dgv[IPW][4], dwv[WR ? IPW : 1][4];
+    // Each block's dq, dk (dw) and dgamma replace its q, k (w) and gamma in LDS as
+    // soon as it is done: a lane reads and writes only its own channel there, and
+    // after this point only the rows of its own blocks.  Where two waves share a
+    // channel tile, the barrier keeps the writes behind both waves' loads above.
+    if constexpr (WPC > 1) __syncthreads();
     float dgc_acc = 0.f;
 #pragma unroll
     for (int s = 0; s < IPW; ++s) {
@@ -1635,39 +1639,29 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
             const float eg = __expf(gi), egc = __expf(gCc - gi);
             dxs[jj] = p.delta ? dxs[jj] : 0.f;                 // without the delta rule K*G does not enter
             const bool ok = i < clen;
-            dqv[s][jj] = ok ? sa[jj] + p.scale * eg * dqg[jj] : 0.f;
+            float dkv, dgv;
+            qs[i * DK + cc] = EL::from_f(ok ? sa[jj] + p.scale * eg * dqg[jj] : 0.f);
             if constexpr (WR) {
                 const float wi = wr[I][jj];
-                dkv[s][jj] = ok ? sn[jj] - eg * dxs[jj] : 0.f;
-                dwv[s][jj] = ok ? tj[jj] + egc * dke[jj] : 0.f;
-                dgv[s][jj] = ok ? qi * sa[jj] + ki * sn[jj] - wi * tj[jj] + p.scale * qi * eg * dqg[jj] -
-                                      ki * eg * dxs[jj] - wi * egc * dke[jj]
-                                : 0.f;
+                dkv = ok ? sn[jj] - eg * dxs[jj] : 0.f;
+                ws[i * DK + cc] = EL::from_f(ok ? tj[jj] + egc * dke[jj] : 0.f);
+                dgv = ok ? qi * sa[jj] + ki * sn[jj] - wi * tj[jj] + p.scale * qi * eg * dqg[jj] -
+                               ki * eg * dxs[jj] - wi * egc * dke[jj]
+                         : 0.f;
                 dgc_acc += ok ? wi * egc * dke[jj] : 0.f;
             } else {
-                dkv[s][jj] = ok ? sn[jj] + tj[jj] - eg * dxs[jj] + egc * dke[jj] : 0.f;
-                dgv[s][jj] = ok ? qi * sa[jj] + ki * sn[jj] - ki * tj[jj] + p.scale * qi * eg * dqg[jj] -
-                                      ki * eg * dxs[jj] - ki * egc * dke[jj]
-                                : 0.f;
+                dkv = ok ? sn[jj] + tj[jj] - eg * dxs[jj] + egc * dke[jj] : 0.f;
+                dgv = ok ? qi * sa[jj] + ki * sn[jj] - ki * tj[jj] + p.scale * qi * eg * dqg[jj] -
+                               ki * eg * dxs[jj] - ki * egc * dke[jj]
+                         : 0.f;
                 dgc_acc += ok ? ki * egc * dke[jj] : 0.f;
             }
+            ks[i * DK + cc] = EL::from_f(dkv);
+            gms[i * DK + cc] = dgv;
         }
     }
     atomicAdd(&dgc[cc], dgc_acc);
-    __syncthreads();                                         // every read of q, k and gamma is done
-#pragma unroll
-    for (int s = 0; s < IPW; ++s) {
-        const int I = wave / NCT + WPC * s;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int i = 16 * I + 4 * g4 + jj;
-            qs[i * DK + cc] = EL::from_f(dqv[s][jj]);
-            ks[i * DK + cc] = EL::from_f(dkv[s][jj]);
-            if constexpr (WR) ws[i * DK + cc] = EL::from_f(dwv[s][jj]);
-            gms[i * DK + cc] = dgv[s][jj];
-        }
-    }
-    __syncthreads();
+    __syncthreads();                                         // dq, dk (dw) and dgamma of every block are in LDS
     // dq, dk rows as 16-byte units
     {
         E *dqg = reinterpret_cast<E *>(p.dq) + t0 * sqk + (int64_t)h * DK;
