@@ -1453,16 +1453,16 @@ chunk_pipe_kernel(const ChunkParams p) {
                 });
             });
         });
+        // the chunk's o rows as one buffer: rows past the sequence's end fall
+        // outside it and their stores are dropped, with no lane-dependent branch
+        const __amdgpu_buffer_rsrc_t ors =
+            buffer_rsrc(reinterpret_cast<E *>(p.o) + t0 * sv + (int64_t)h * DV + col0, (uint32_t)(clen * sv * sizeof(E)));
         unroll<NW>([&](auto s) {
             if (col0 + 16 * s >= DV) return;
-            E *orow = reinterpret_cast<E *>(p.o) + (t0 + r16) * sv + (int64_t)h * DV + col0 + 16 * s + 4 * g4;
             unroll<NR>([&](auto i) {
                 const int I = rb(i);
-                // convert before the lane-dependent store condition: the accumulator
-                // is read in straight-line code, not behind an exec-skip branch
-                const typename EL::frag ob = EL::cvt(ot[s][i]);
-                pin_v(ob);
-                if (16 * I + r16 < clen) *reinterpret_cast<typename EL::frag *>(orow + (int64_t)(16 * I) * sv) = ob;
+                buffer_store_8b(EL::cvt(ot[s][i]), ors,
+                                (uint32_t)(((16 * I + r16) * sv + 16 * s + 4 * g4) * sizeof(E)));
             });
             if constexpr (HS) {
                 // the checkpoint's fragment order: lane (g, r) holds rows 16 kt + 4 g .. + 3
