@@ -70,6 +70,31 @@ def test_causal_conv_dense_matches_oracle(dtype, K, act, cached):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize('B,T,D', [(2, 300, 1040), (1, 1000, 256), (4, 9, 2048)])
+def test_causal_conv_workgroup_tiling(dtype, B, T, D):
+    """Shapes whose channel units (16 bytes each) fill several 16-unit workgroup
+    columns, the last one partly (1040 bf16 = 130 units), and runs of 8 tokens that
+    span several workgroup rows with a partial last one; window rows that cross
+    workgroups; a sequence shorter than two runs."""
+    from vagus_amd import ops
+    g = torch.Generator().manual_seed(T + D)
+    K = 4
+    x = torch.randn(B, T, D, generator=g).to(dtype)
+    w = 0.5 * torch.randn(D, 1, K, generator=g)
+    cache = torch.randn(B, K, D, generator=g).to(dtype)
+    print(f'\n[case] causal_conv tiling dtype={dtype} B={B} T={T} D={D}', flush=True)
+    ref, ref_cache = gdr.short_conv(x, w, cache, activation='silu')
+    y, fs = ops.causal_conv1d(x.cuda(), w.cuda(), activation='silu', conv_cache=cache.cuda(),
+                              output_final_state=True)
+    tol = 1e-6 if dtype == torch.float32 else 1e-2
+    err = _rel(y, ref)
+    exact = torch.equal(fs.cpu(), ref_cache)
+    print(f'[parity] causal_conv tiling y={err:.3e} cache exact={exact} (tol {tol:g})', flush=True)
+    assert err <= tol and exact
+
+
+@pytest.mark.gpu
 def test_causal_conv_varlen_matches_oracle():
     from vagus_amd import ops
     g = torch.Generator().manual_seed(5)

@@ -4,8 +4,9 @@
 // token; here it is one HBM pass over x.
 //
 // A thread owns VE = 16 / sizeof(E) consecutive channels (one 16-byte unit)
-// for a run of RUN = 8 consecutive tokens, so a wavefront reads 64 neighbouring
-// units of one token row per load.  The run's K - 1 + RUN input rows are all
+// for a run of RUN = 8 consecutive tokens.  A workgroup holds 16 units x 16
+// consecutive runs, so a wavefront reads 16 neighbouring units (256 bytes) of
+// four token rows per load.  The run's K - 1 + RUN input rows are all
 // loaded before any arithmetic and kept as loaded (16-bit values unconverted),
 // which keeps a thread within 128 VGPRs and so the whole grid of a 340M-shaped
 // projection (B8 T4096 D1024: 4096 waves) resident at once.  Each input unit is
@@ -14,7 +15,9 @@
 // previous call's last K inputs, linear_attention.py:929-941) or are zero; a run
 // that crosses into the next packed segment goes token by token and restarts its
 // window there.  Measured at that shape: RUN 16 (occupancy 3) 25.2 us, RUN 8
-// 23.2 us, RUN 4 26.7 us; a plain copy of the same bytes 22.2 us.
+// 23.2 us, RUN 4 26.7 us with one run of all 128 units per 128 threads; RUN 8
+// with 16 x 16 workgroups 22.6 us (32 x 8: 23.2, 8 x 32: 22.9, 4 x 64: 33.9);
+// a plain copy of the same bytes 22.2 us.
 #include <type_traits>
 
 #include "gdr_common.hpp"
@@ -25,6 +28,13 @@ namespace vgdr {
 namespace {
 
 constexpr int RUN = 8;
+constexpr int CG_PER_GROUP = 16;
+
+// channel units (16 bytes each) per workgroup of the prefill conv: CG_PER_GROUP,
+// or all of them when there are fewer
+__host__ __device__ __forceinline__ int conv_cg_per_group(int64_t ncg) {
+    return ncg < CG_PER_GROUP ? (int)ncg : CG_PER_GROUP;
+}
 
 __device__ __forceinline__ int64_t clamp_tok(int32_t c, int64_t n_tokens) {
     return c < 0 ? 0 : (c > n_tokens ? n_tokens : c);
@@ -67,21 +77,20 @@ __global__ void __launch_bounds__(256) causal_conv_kernel(const ConvParams p) {
     constexpr int VE = 16 / (int)sizeof(E);
     typedef E V __attribute__((ext_vector_type(VE)));
     const int64_t ncg = p.D / VE;
-    // (consecutive workgroups run on different XCDs, so about half of the window rows
-    // are fetched from HBM a second time; renumbering the workgroups so that each XCD
-    // streams one contiguous range measured slower, 24.5 against 23.3 us)
-    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-    int64_t cg, run;
-    if (gridDim.x <= (1u << 24)) {           // gid < 2^32: 32-bit division
-        const uint32_t g = (uint32_t)gid, n = (uint32_t)ncg;
-        cg = g % n;
-        run = g / n;
-    } else {
-        cg = gid % ncg;
-        run = gid / ncg;
-    }
+    // A workgroup covers 256 / CG_PER_GROUP consecutive runs of CG_PER_GROUP channel
+    // units (of all of them when there are fewer): a run's K - 1 window rows are the previous run's last rows, read
+    // by a thread of the same workgroup (so from this CU's cache) except for the
+    // workgroup's first run.  (With one run per 128 channel units, consecutive runs sat
+    // in consecutive workgroups, on different XCDs, and about half of the window rows
+    // were fetched from HBM a second time.)
+    const int cgw = conv_cg_per_group(ncg), rpw = 256 / cgw;
+    const int tid = threadIdx.x;
+    if (tid >= cgw * rpw) return;
+    const uint32_t ncb = (uint32_t)((ncg + cgw - 1) / cgw);
+    const int64_t cg = (int64_t)(blockIdx.x % ncb) * cgw + tid % cgw;
+    const int64_t run = (int64_t)(blockIdx.x / ncb) * rpw + tid / cgw;
     const int64_t t0 = run * RUN;
-    if (t0 >= p.n_tokens) return;
+    if (cg >= ncg || t0 >= p.n_tokens) return;
     const int64_t c0 = cg * VE;
     const E *x = reinterpret_cast<const E *>(p.x);
     const E *st = reinterpret_cast<const E *>(p.state_in);
@@ -210,9 +219,11 @@ static hipError_t conv_k(const ConvParams &p, hipStream_t stream) {
     constexpr int VE = 16 / (int)sizeof(E);
     const int64_t ncg = p.D / VE;
     const int64_t runs = (p.n_tokens + RUN - 1) / RUN;
-    const int64_t threads = runs * ncg;
-    if (threads > 0) {
-        const dim3 grid((unsigned)((threads + 255) / 256));
+    if (runs > 0 && ncg > 0) {
+        const int cgw = conv_cg_per_group(ncg), rpw = 256 / cgw;
+        const int64_t groups = (ncg + cgw - 1) / cgw * ((runs + rpw - 1) / rpw);
+        if (groups > 0x7fffffff) return hipErrorInvalidValue;
+        const dim3 grid((unsigned)groups);
         const bool wv = ((uintptr_t)p.w & 15) == 0;
         if (p.w_f32 && !std::is_same<E, float>::value) {
             if (wv) hipLaunchKernelGGL((causal_conv_kernel<E, float, K, true>), grid, dim3(256), 0, stream, p);
