@@ -485,6 +485,38 @@ int vgdr_causal_conv1d(int dtype, const void *x, const void *weight, int weight_
 int vgdr_norm_gate(int dtype, const void *o, const vgdr_epilogue *epilogue, void *out, int64_t n_rows,
                    int64_t dv, hipStream_t stream);
 
+/* The pre-norm blocks' RMSNorm (infra/components/norm_layer.py:15-23) over rows
+ * rows of dim elements, with the residual add in front of it that the blocks
+ * make before each norm (infra/components/block.py:57-59, :85-87):
+ *     h = x + residual   (rounded to dtype; h = x when residual is NULL)
+ *     y = dtype(dtype(h * rsqrt(mean(h^2) + eps)) * gamma)
+ * and h is written to x_out unless x_out is NULL.  x, residual, x_out, y:
+ * [rows, dim]; gamma: [dim]; all in dtype and 16-byte aligned.  x_out may be x
+ * or residual (the residual stream updated in place); y must differ from x,
+ * residual and x_out.  dim a multiple of 16 / sizeof(dtype), at most 2048
+ * such units (16,384 elements of a 16-bit type). */
+int vgdr_rms_norm(int dtype, const void *x, const void *residual, void *x_out, const void *gamma, void *y,
+                  int64_t rows, int64_t dim, float eps, hipStream_t stream);
+
+/* The scalar gate and the beta logits of the LM's one-token decode step
+ * (GatedDeltaNet._gates, linear_attention.py:719-721 and :734-735), from the
+ * layer input x [rows, dim] and the projection weights stacked as
+ * w_ab = [W_a; W_b] ([2H, dim], or W_a alone [H, dim] without beta), all in
+ * dtype:
+ *     p    = dtype(w_ab x)                       (nn.Linear's output)
+ *     g    = neg_exp_a * softplus(p[:H] + dt_bias)    -> g [rows, H], fp32
+ *     beta = p[H:]                                     -> beta [rows, H], fp32
+ * neg_exp_a = -exp(A_log) and dt_bias in fp32, [H].  beta NULL = no W_b rows.
+ * x and w_ab 16-byte aligned; dim a multiple of 16 / sizeof(dtype); H <= 4096. */
+int vgdr_scalar_gates(int dtype, const void *x, const void *w_ab, const float *neg_exp_a, const float *dt_bias,
+                      float *g, float *beta, int64_t rows, int64_t dim, int64_t H, hipStream_t stream);
+
+/* The FFN's SwiGLU (infra/components/ffn.py:48-50): y = dtype(dtype(SiLU(a)) * b)
+ * for each row x = [a | b] of 2 * hidden elements, y [rows, hidden], in dtype
+ * (fp32, bf16, fp16), 16-byte aligned; hidden a multiple of 16 / sizeof(dtype).
+ * y must not alias x. */
+int vgdr_swiglu(int dtype, const void *x, void *y, int64_t rows, int64_t hidden, hipStream_t stream);
+
 /*
  * Packed-batch schedule.  No reference counterpart (the reference has no
  * cu_seqlens, see infra/inference/generator.py:19-22); fla builds the same

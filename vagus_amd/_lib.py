@@ -85,6 +85,9 @@ SIGNATURES = {
     'vgdr_recurrent_fwd_epilogue': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                          _L, _L, _L, _L, _L, _L, _F, _FZ, _EP, _P]),
     'vgdr_norm_gate': (_I, [_I, _P, _EP, _P, _L, _L, _P]),
+    'vgdr_rms_norm': (_I, [_I, _P, _P, _P, _P, _P, _L, _L, _F, _P]),
+    'vgdr_scalar_gates': (_I, [_I, _P, _P, _P, _P, _P, _P, _L, _L, _L, _P]),
+    'vgdr_swiglu': (_I, [_I, _P, _P, _L, _L, _P]),
     'vgdr_recurrent_fwd_w': (_I, [_I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                   _L, _L, _L, _L, _L, _L, _F, _FZ, _P]),
     'vgdr_decode_step': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,

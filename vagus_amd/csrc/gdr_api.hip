@@ -826,6 +826,68 @@ int vgdr_norm_gate(int dtype, const void *o, const vgdr_epilogue *epilogue, void
     return hip_status(vgdr::norm_gate(dtype, o, ep, out, n_rows, (int)dv, stream), "vgdr_norm_gate launch");
 }
 
+int vgdr_rms_norm(int dtype, const void *x, const void *residual, void *x_out, const void *gamma, void *y,
+                  int64_t rows, int64_t dim, float eps, hipStream_t stream) {
+    g_err[0] = 0;
+    if (dtype != VGDR_F32 && dtype != VGDR_BF16 && dtype != VGDR_F16)
+        return fail(VGDR_ERR_INVALID, "vgdr_rms_norm: unknown dtype %d", dtype);
+    const int64_t ve = dtype == VGDR_F32 ? 4 : 8;
+    if (rows < 0) return fail(VGDR_ERR_INVALID, "vgdr_rms_norm: rows=%lld", (long long)rows);
+    if (dim <= 0 || dim % ve || dim / ve > 2048)
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_rms_norm: dim=%lld (supported: a multiple of %lld, at most %lld)",
+                    (long long)dim, (long long)ve, (long long)(2048 * ve));
+    if (!(eps >= 0.f)) return fail(VGDR_ERR_INVALID, "vgdr_rms_norm: eps must be >= 0");
+    if (rows == 0) return VGDR_OK;
+    if (rows > 0x7fffffffLL) return fail(VGDR_ERR_INVALID, "vgdr_rms_norm: too many rows");
+    if (!x || !gamma || !y) return fail(VGDR_ERR_INVALID, "vgdr_rms_norm: x, gamma and y are required");
+    if (!aligned16(x) || !aligned16(gamma) || !aligned16(y) || (residual && !aligned16(residual)) ||
+        (x_out && !aligned16(x_out)))
+        return fail(VGDR_ERR_INVALID, "vgdr_rms_norm: every tensor must be 16-byte aligned");
+    if (y == x || (residual && y == residual) || (x_out && y == x_out))
+        return fail(VGDR_ERR_INVALID, "vgdr_rms_norm: y must not alias x, residual or x_out");
+    return hip_status(vgdr::rms_norm(dtype, x, residual, x_out, gamma, y, rows, (int)dim, eps, stream),
+                      "vgdr_rms_norm launch");
+}
+
+int vgdr_scalar_gates(int dtype, const void *x, const void *w_ab, const float *neg_exp_a, const float *dt_bias,
+                      float *g, float *beta, int64_t rows, int64_t dim, int64_t H, hipStream_t stream) {
+    g_err[0] = 0;
+    if (dtype != VGDR_F32 && dtype != VGDR_BF16 && dtype != VGDR_F16)
+        return fail(VGDR_ERR_INVALID, "vgdr_scalar_gates: unknown dtype %d", dtype);
+    const int64_t ve = dtype == VGDR_F32 ? 4 : 8;
+    if (rows < 0 || H <= 0 || H > 4096)
+        return fail(VGDR_ERR_INVALID, "vgdr_scalar_gates: rows=%lld H=%lld", (long long)rows, (long long)H);
+    if (dim <= 0 || dim % ve || dim > 0x7fffffffLL)
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_scalar_gates: dim=%lld (a multiple of %lld)", (long long)dim,
+                    (long long)ve);
+    if (rows == 0) return VGDR_OK;
+    if (rows > 0x7fffffffLL) return fail(VGDR_ERR_INVALID, "vgdr_scalar_gates: too many rows");
+    if (!x || !w_ab || !neg_exp_a || !dt_bias || !g)
+        return fail(VGDR_ERR_INVALID, "vgdr_scalar_gates: x, w_ab, neg_exp_a, dt_bias and g are required");
+    if (!aligned16(x) || !aligned16(w_ab)) return fail(VGDR_ERR_INVALID, "vgdr_scalar_gates: x and w_ab must be 16-byte aligned");
+    return hip_status(vgdr::scalar_gates(dtype, x, w_ab, neg_exp_a, dt_bias, g, beta, rows, (int)dim, (int)H,
+                                         beta != nullptr, stream),
+                      "vgdr_scalar_gates launch");
+}
+
+int vgdr_swiglu(int dtype, const void *x, void *y, int64_t rows, int64_t hidden, hipStream_t stream) {
+    g_err[0] = 0;
+    if (dtype != VGDR_F32 && dtype != VGDR_BF16 && dtype != VGDR_F16)
+        return fail(VGDR_ERR_INVALID, "vgdr_swiglu: unknown dtype %d", dtype);
+    const int64_t ve = dtype == VGDR_F32 ? 4 : 8;
+    if (rows < 0) return fail(VGDR_ERR_INVALID, "vgdr_swiglu: rows=%lld", (long long)rows);
+    if (hidden <= 0 || hidden % ve || hidden > 0x3fffffffLL)
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_swiglu: hidden=%lld (a multiple of %lld)", (long long)hidden,
+                    (long long)ve);
+    if (rows == 0) return VGDR_OK;
+    if (!x || !y) return fail(VGDR_ERR_INVALID, "vgdr_swiglu: x and y are required");
+    if (!aligned16(x) || !aligned16(y)) return fail(VGDR_ERR_INVALID, "vgdr_swiglu: x and y must be 16-byte aligned");
+    if (x == y) return fail(VGDR_ERR_INVALID, "vgdr_swiglu: y must not alias x");
+    if (rows * (hidden / ve) > (int64_t)0xffffffffLL * 256)
+        return fail(VGDR_ERR_INVALID, "vgdr_swiglu: too many rows");
+    return hip_status(vgdr::swiglu(dtype, x, y, rows, (int)hidden, stream), "vgdr_swiglu launch");
+}
+
 int vgdr_recurrent_fwd(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
                        const float *g, const float *beta, void *o, const float *initial_state,
                        float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H,

@@ -88,4 +88,85 @@ hipError_t norm_gate(int dtype, const void *o, const Epilogue &ep, void *out, in
     return norm_gate_t<float>(o, ep, out, n_rows, dv, stream);
 }
 
+// The pre-norm blocks' RMSNorm (norm_layer.py:15-23) with the residual add in
+// front of it (block.py:57-59, :85-87): h = x + res rounded to E (the stream's
+// new value, stored to x_out), then y = E(E(h * rsqrt(mean(h^2) + eps)) * gamma),
+// the module's order of roundings.  One workgroup per row; a thread holds up to U
+// 16-byte units of the row in registers between the two passes.  Decode feeds
+// a handful of rows of a few thousand elements, so one kernel here replaces the
+// eight elementwise and reduction kernels of the module's expression.
+template <typename E, int U>
+__global__ void __launch_bounds__(256) rms_norm_kernel(const E *__restrict__ x, const E *__restrict__ res, E *x_out,
+                                                       const E *__restrict__ gamma, float eps, E *y, int dim) {
+    constexpr int VE = 16 / (int)sizeof(E);
+    typedef E V __attribute__((ext_vector_type(VE)));
+    __shared__ float part[4];
+    const int tid = threadIdx.x, nu = dim / VE;
+    const int64_t base = (int64_t)blockIdx.x * dim;
+    float h[U][VE];
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = tid + 256 * u;
+        if (i < nu) {
+            V hv = *reinterpret_cast<const V *>(x + base + (int64_t)i * VE);
+            if (res) {
+                const V rv = *reinterpret_cast<const V *>(res + base + (int64_t)i * VE);
+#pragma unroll
+                for (int e = 0; e < VE; ++e) hv[e] = (E)((float)hv[e] + (float)rv[e]);
+            }
+            if (x_out) *reinterpret_cast<V *>(x_out + base + (int64_t)i * VE) = hv;
+#pragma unroll
+            for (int e = 0; e < VE; ++e) {
+                h[u][e] = (float)hv[e];
+                ss += h[u][e] * h[u][e];
+            }
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m);
+    if ((tid & 63) == 0) part[tid >> 6] = ss;
+    __syncthreads();
+    const float r = rsqrtf((part[0] + part[1] + part[2] + part[3]) / (float)dim + eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int i = tid + 256 * u;
+        if (i < nu) {
+            const V gv = *reinterpret_cast<const V *>(gamma + (int64_t)i * VE);
+            V o;
+#pragma unroll
+            for (int e = 0; e < VE; ++e) o[e] = (E)((float)(E)(h[u][e] * r) * (float)gv[e]);
+            *reinterpret_cast<V *>(y + base + (int64_t)i * VE) = o;
+        }
+    }
+}
+
+template <typename E>
+static hipError_t rms_norm_t(const void *x, const void *res, void *x_out, const void *gamma, void *y, int64_t rows,
+                             int dim, float eps, hipStream_t stream) {
+    constexpr int VE = 16 / (int)sizeof(E);
+    const int units = dim / VE;
+    const E *xe = reinterpret_cast<const E *>(x), *re = reinterpret_cast<const E *>(res),
+            *ge = reinterpret_cast<const E *>(gamma);
+    E *xo = reinterpret_cast<E *>(x_out), *ye = reinterpret_cast<E *>(y);
+    const dim3 grid((unsigned)rows);
+    if (units <= 256)
+        hipLaunchKernelGGL((rms_norm_kernel<E, 1>), grid, dim3(256), 0, stream, xe, re, xo, ge, eps, ye, dim);
+    else if (units <= 512)
+        hipLaunchKernelGGL((rms_norm_kernel<E, 2>), grid, dim3(256), 0, stream, xe, re, xo, ge, eps, ye, dim);
+    else if (units <= 1024)
+        hipLaunchKernelGGL((rms_norm_kernel<E, 4>), grid, dim3(256), 0, stream, xe, re, xo, ge, eps, ye, dim);
+    else
+        hipLaunchKernelGGL((rms_norm_kernel<E, 8>), grid, dim3(256), 0, stream, xe, re, xo, ge, eps, ye, dim);
+    return hipGetLastError();
+}
+
+hipError_t rms_norm(int dtype, const void *x, const void *res, void *x_out, const void *gamma, void *y, int64_t rows,
+                    int dim, float eps, hipStream_t stream) {
+    if (rows == 0) return hipSuccess;
+    if (dtype == 1) return rms_norm_t<__bf16>(x, res, x_out, gamma, y, rows, dim, eps, stream);
+    if (dtype == 2) return rms_norm_t<_Float16>(x, res, x_out, gamma, y, rows, dim, eps, stream);
+    return rms_norm_t<float>(x, res, x_out, gamma, y, rows, dim, eps, stream);
+}
+
 }  // namespace vgdr

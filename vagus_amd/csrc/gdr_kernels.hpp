@@ -210,6 +210,21 @@ hipError_t recurrent_fwd(int dtype, int dk, int dv, int gate_vector, const RecPa
 hipError_t norm_gate(int dtype, const void *o, const Epilogue &ep, void *out, int64_t n_rows, int dv,
                      hipStream_t stream);
 
+// The blocks' RMSNorm with an optional residual add first (res, x_out may be
+// null): x_out = x + res, y = RMSNorm(x + res) * gamma over rows of dim
+// elements.  dim / (16 / sizeof(E)) <= 2048.
+hipError_t rms_norm(int dtype, const void *x, const void *res, void *x_out, const void *gamma, void *y, int64_t rows,
+                    int dim, float eps, hipStream_t stream);
+
+// The LM decode step's scalar gate and beta logits from x [rows, dim] and the
+// stacked projection weight [W_a; W_b] ([2H or H, dim]): g [rows, H] (fp32),
+// beta [rows, H] (fp32, with_beta).  dim % (16 / sizeof(E)) == 0.
+hipError_t scalar_gates(int dtype, const void *x, const void *w, const float *neg_a, const float *dt_bias, float *g,
+                        float *beta, int64_t rows, int dim, int H, bool with_beta, hipStream_t stream);
+
+// SiLU(x[:, :h]) * x[:, h:] over rows of 2h elements; h % (16 / sizeof(E)) == 0.
+hipError_t swiglu(int dtype, const void *x, void *y, int64_t rows, int hidden, hipStream_t stream);
+
 hipError_t causal_conv(int dtype, const ConvParams &p, hipStream_t stream);
 
 hipError_t varlen_prepare(const int32_t *cu, int n_seqs, int64_t n_tokens, int chunk,

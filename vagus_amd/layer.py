@@ -413,6 +413,55 @@ class GatedDeltaNet(nn.Module):
         return (self.short_conv_size is not None and self.key_head_dim in (64, 128)
                 and self.value_head_dim in (64, 128))
 
+    def _decode_weights(self):
+        """The one-token decode step's projection weights regrouped, rebuilt
+        whenever a parameter changed (its storage or version): W_q, W_k, W_v
+        and W_g transposed into one contiguous (4, dim, H*dv) tensor, so that one
+        batched product replaces four skinny GEMMs (when H*dk == H*dv); for the
+        scalar gate [W_a; W_b] as one (2H, dim) weight (W_a alone without the
+        delta rule) and the gate's constants -exp(A_log) and dt_bias in fp32.
+        The copies hold one more set of these weights (4 dim H dv + 2 H dim
+        elements per layer)."""
+        ps = [self.wq.weight, self.wk.weight, self.wv.weight, self.wg.weight]
+        scalar = self.gate == 'scalar'
+        if scalar:
+            ps += [self.wa.weight, self.A_log, self.dt_bias]
+        if self.delta:
+            ps.append(self.wb.weight)
+        key = tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in ps)
+        c = self.__dict__.get('_decode_w')
+        if c is None or c[0] != key:
+            same = len({p.shape for p in ps[:4]}) == 1
+            w4 = torch.stack([p.t() for p in ps[:4]]).contiguous() if same else None
+            wab = gconst = None
+            if scalar:
+                wab = torch.cat([self.wa.weight] + ([self.wb.weight] if self.delta else [])).contiguous()
+                gconst = (-self.A_log.float().exp(), self.dt_bias.float())
+            c = (key, w4, wab, gconst)
+            self.__dict__['_decode_w'] = c
+        return c[1:]
+
+    def _decode_inputs(self, x):
+        """(qp, kp, vp, out_gate, g, beta) for the one-token decode kernel: the
+        projections of x (B, 1, dim), the log-decay in fp32 (or the KDA gate's
+        pre-activation) and the beta logits, with the regrouped weights of
+        _decode_weights.  The values are those of the separate projections and
+        of _gates(raw_gate=vector, raw_beta=delta) up to the GEMMs' summation
+        order."""
+        B, L = x.shape[0], x.shape[1]
+        w4, wab, gconst = self._decode_weights()
+        if w4 is not None:
+            x4 = x.reshape(1, B * L, x.shape[-1]).expand(4, -1, -1).contiguous()
+            y = torch.bmm(x4, w4)
+            qp, kp, vp, og = (y[i].view(B, L, -1) for i in range(4))
+        else:
+            qp, kp, vp, og = self.wq(x), self.wk(x), self.wv(x), self.wg(x)
+        if wab is None:
+            g, beta = self._gates(x, raw_gate=self.gate == 'vector', raw_beta=self.delta)
+            return qp, kp, vp, og, g, beta
+        g, beta = ops.scalar_gates(x, wab, *gconst, with_beta=self.delta)
+        return qp, kp, vp, og, g, beta
+
     @torch.no_grad()
     def decode_step(self, x):
         """Consume the next block (B, L, dim), advancing the state (:918-952).
@@ -424,21 +473,21 @@ class GatedDeltaNet(nn.Module):
         assert B == self.state.shape[0], 'Batch size does not match the state. Reset or load cache first.'
         if L == 0:
             return x
-        qp, kp, vp = self.wq(x), self.wk(x), self.wv(x)
-        self._pick_impl(qp)
+        self._pick_impl(x)
         H, dk, dv = self.head_count, self.key_head_dim, self.value_head_dim
         if L == 1 and type(self)._write is GatedDeltaNet._write and self._decode_kernel_fits():
             vec = self.gate == 'vector'
-            g, beta = self._gates(x, raw_gate=vec, raw_beta=self.delta)
+            qp, kp, vp, og, g, beta = self._decode_inputs(x)
             o = ops.hip_decode_step(qp, kp, vp, g, beta, self.state, scale=self.scale, delta=self.delta,
                                     conv_weights=self._conv_weights(), conv_cache=self._caches(), l2norm=True,
                                     beta_logits=self.delta, gate_in_kernel=vec,
                                     A_log=self.A_log if vec else None, dt_bias=self.dt_bias if vec else None,
-                                    lower_bound=self.gate_lower_bound, out_gate=self.wg(x),
+                                    lower_bound=self.gate_lower_bound, out_gate=og,
                                     out_norm_weight=self.o_norm.gamma, out_norm_eps=self.o_norm.eps)
             self.cache_len += L
             o = o.reshape(B, L, H * dv)
             return self.wo(o) if self.out_proj else o
+        qp, kp, vp = self.wq(x), self.wk(x), self.wv(x)
         if self.short_conv_size is not None:
             qp = self.conv_q(qp, 'silu', conv_cache=self.qp_cache)
             kp = self.conv_k(kp, 'silu', conv_cache=self.kp_cache)

@@ -29,7 +29,36 @@ import math
 import torch
 from torch import nn
 
+from . import ops
 from .layer import GatedDeltaNet, RMSNorm
+
+
+def _add_norm(norm: RMSNorm, x, delta=None, *, inplace: bool = False):
+    """(x + delta, norm(x + delta)) -- the residual add a pre-norm block makes
+    before each norm (block.py:57-59) and the norm -- as one HIP pass
+    (ops.rms_norm) for GPU tensors; x + delta lands in x itself with inplace.
+    Without delta: (x, norm(x)).  Other devices and shapes take the module's
+    expression."""
+    D = x.shape[-1]
+    ve = 16 // x.element_size() if x.dtype in (torch.bfloat16, torch.float16, torch.float32) else 0
+    if x.is_cuda and ve and norm.gamma.dtype == x.dtype and D % ve == 0 and D // ve <= 2048:
+        if delta is None:
+            return x, ops.rms_norm(x, norm.gamma, norm.eps)
+        y, h = ops.rms_norm(x, norm.gamma, norm.eps, residual=delta,
+                            out_residual=x if inplace and x.is_contiguous() else None)
+        return h, y
+    if delta is not None:
+        x = x.add_(delta) if inplace else x + delta
+    return x, norm(x)
+
+
+def _ffn(ffn: 'FFN', h):
+    """The FFN with its SwiGLU as one HIP pass (ops.swiglu) for GPU tensors
+    without autograd; the module's expression otherwise."""
+    if (h.is_cuda and not torch.is_grad_enabled() and h.dtype in (torch.bfloat16, torch.float16, torch.float32)
+            and ffn.hidden_dim % (16 // h.element_size()) == 0):
+        return ffn.l2(ops.swiglu(ffn.l1(h)))
+    return ffn(h)
 
 
 class FFN(nn.Module):
@@ -79,13 +108,23 @@ class Block(nn.Module):
 
     @torch.no_grad()
     def decode_step(self, x):
-        x = x + self.att.decode_step(self.rmsnorm1(x))
-        return x + self.ffn(self.rmsnorm2(x))
+        _, h = _add_norm(self.rmsnorm1, x)
+        x, h = _add_norm(self.rmsnorm2, x, self.att.decode_step(h))
+        return x + _ffn(self.ffn, h)
 
     @torch.no_grad()
     def prefill_packed(self, x, cu_seqlens, rows=None):
-        x = x + self.att.prefill_packed(self.rmsnorm1(x), cu_seqlens, rows=rows)
-        return x + self.ffn(self.rmsnorm2(x))
+        _, h = _add_norm(self.rmsnorm1, x)
+        x, h = _add_norm(self.rmsnorm2, x, self.att.prefill_packed(h, cu_seqlens, rows=rows))
+        return x + _ffn(self.ffn, h)
+
+    def _stream(self, x, delta, step):
+        """One block over the residual stream x with the previous block's
+        pending FFN output `delta` folded into this block's first norm:
+        returns (x, this block's FFN output).  x is updated in place."""
+        x, h = _add_norm(self.rmsnorm1, x, delta, inplace=True)
+        x, h = _add_norm(self.rmsnorm2, x, step(h), inplace=True)
+        return x, _ffn(self.ffn, h)
 
 
 class GDNLM(nn.Module):
@@ -198,11 +237,12 @@ class GDNLM(nn.Module):
     def decode_step(self, tokens, return_logits: bool = True):
         """Consume tokens (B, L) into the streams; logits (B, L, vocab) or None."""
         x = self.embedding(tokens)
+        delta = None
         for blk in self.blocks:
-            x = blk.decode_step(x)
+            x, delta = blk._stream(x, delta, blk.att.decode_step)
         if not return_logits:
             return None
-        return self.head(self.rms_head(x))
+        return self.head(_add_norm(self.rms_head, x, delta, inplace=True)[1])
 
     @torch.no_grad()
     def prefill_packed(self, tokens, cu_seqlens, *, rows=None, last_logits: bool = True):
@@ -210,12 +250,14 @@ class GDNLM(nn.Module):
         cu_seqlens (N + 1), into cache rows (default: block n -> row n).
         Returns the logits (N, vocab) at each block's last token, or None."""
         x = self.embedding(tokens.reshape(1, -1))
+        delta = None
         for blk in self.blocks:
-            x = blk.prefill_packed(x, cu_seqlens, rows=rows)
+            x, delta = blk._stream(x, delta, lambda h, blk=blk: blk.att.prefill_packed(h, cu_seqlens, rows=rows))
         if not last_logits:
             return None
         last = (cu_seqlens[1:] - 1).long()
-        return self.head(self.rms_head(x[0].index_select(0, last)))
+        x = x[0].index_select(0, last) + delta[0].index_select(0, last)
+        return self.head(_add_norm(self.rms_head, x)[1])
 
 
 class RaggedGenerator:

@@ -722,6 +722,86 @@ def rms_norm_gated(x, g, weight, bias=None, activation='swish', residual=None, p
     return _norm_gate(x, _Epilogue(g, weight, eps))
 
 
+def rms_norm(x, weight, eps: float = 1e-6, residual=None, out_residual=None):
+    """The blocks' RMSNorm (infra/components/norm_layer.py:15-23) in one HIP
+    pass over the last dim: dtype(dtype(h rsqrt(mean h^2 + eps)) * weight).
+    With `residual`, h = x + residual (rounded to x's dtype: the residual add
+    each block makes before its norm, infra/components/block.py:57-59), written
+    into `out_residual` (a new tensor by default; x itself updates the stream in
+    place) and returned with the norm: (y, h).  Without it h = x and only y is
+    returned.  x, residual, weight in one dtype; no autograd."""
+    _check_device(x, weight, residual, out_residual)
+    _check_grad(x, weight, residual)
+    if x.dtype not in _DTYPES:
+        raise NotImplementedError(f'x must be one of {list(_DTYPES)}; got {x.dtype}')
+    D = x.shape[-1]
+    assert weight.shape == (D,) and weight.dtype == x.dtype, \
+        f'weight must be ({D},) in {x.dtype}; got {tuple(weight.shape)} {weight.dtype}'
+    xs = _aligned(x)
+    w = _aligned(weight)
+    r = h = None
+    if residual is not None:
+        assert residual.shape == x.shape and residual.dtype == x.dtype, 'residual must match x'
+        r = _aligned(residual)
+        if out_residual is None:
+            h = torch.empty_like(xs)
+        else:
+            assert out_residual.shape == x.shape and out_residual.dtype == x.dtype and out_residual.is_contiguous() \
+                and out_residual.data_ptr() % 16 == 0, 'out_residual: contiguous, aligned, shaped and typed as x'
+            h = out_residual
+    y = torch.empty_like(xs)
+    rows = xs.numel() // max(D, 1)
+    with torch.cuda.device(xs.device):
+        _lib.check(_lib.load().vgdr_rms_norm(_DTYPES[xs.dtype], _ptr(xs), _ptr(r), _ptr(h), _ptr(w), _ptr(y), rows,
+                                             D, float(eps), _stream(xs.device)))
+    return y if residual is None else (y, h)
+
+
+def scalar_gates(x, w_ab, neg_exp_a, dt_bias, with_beta: bool = True):
+    """The scalar gate and the beta logits of a decode token in one HIP pass
+    (GatedDeltaNet._gates, linear_attention.py:719-721, :734-735): x (..., dim),
+    w_ab = [W_a; W_b] (2H, dim) (W_a (H, dim) without beta), both in one dtype;
+    neg_exp_a = -exp(A_log) and dt_bias fp32 (H,).  Returns g = neg_exp_a *
+    softplus(W_a x + dt_bias) and beta = W_b x (the logits), fp32 (..., H), the
+    projections rounded to x's dtype as nn.Linear returns them; beta is None
+    without it.  No autograd."""
+    _check_device(x, w_ab, neg_exp_a, dt_bias)
+    _check_grad(x, w_ab)
+    if x.dtype not in _DTYPES or w_ab.dtype != x.dtype:
+        raise NotImplementedError(f'x and w_ab in one of {list(_DTYPES)}; got {x.dtype}, {w_ab.dtype}')
+    D = x.shape[-1]
+    H = w_ab.shape[0] // (2 if with_beta else 1)
+    assert w_ab.shape == ((2 if with_beta else 1) * H, D), f'w_ab must be ({(2 if with_beta else 1)}H, {D})'
+    na = neg_exp_a.float().contiguous()
+    dtb = dt_bias.float().contiguous()
+    assert na.shape == (H,) and dtb.shape == (H,), f'neg_exp_a and dt_bias must be ({H},)'
+    xs, w = _aligned(x), _aligned(w_ab)
+    g = torch.empty(*x.shape[:-1], H, dtype=torch.float32, device=x.device)
+    beta = torch.empty_like(g) if with_beta else None
+    with torch.cuda.device(xs.device):
+        _lib.check(_lib.load().vgdr_scalar_gates(_DTYPES[xs.dtype], _ptr(xs), _ptr(w), _ptr(na), _ptr(dtb), _ptr(g),
+                                                 _ptr(beta), xs.numel() // max(D, 1), D, H, _stream(xs.device)))
+    return g, beta
+
+
+def swiglu(x):
+    """SiLU(x1) * xgate for x = [x1 | xgate] over the last dim in one HIP pass
+    (the FFN's activation, infra/components/ffn.py:48-50), with the module's
+    roundings (SiLU's result in x's dtype, then the product).  No autograd."""
+    _check_device(x)
+    _check_grad(x)
+    if x.dtype not in _DTYPES:
+        raise NotImplementedError(f'x must be one of {list(_DTYPES)}; got {x.dtype}')
+    h2 = x.shape[-1]
+    assert h2 % 2 == 0, 'swiglu needs an even last dim'
+    xs = _aligned(x)
+    y = torch.empty(*x.shape[:-1], h2 // 2, dtype=x.dtype, device=x.device)
+    with torch.cuda.device(xs.device):
+        _lib.check(_lib.load().vgdr_swiglu(_DTYPES[xs.dtype], _ptr(xs), _ptr(y), xs.numel() // max(h2, 1), h2 // 2,
+                                           _stream(xs.device)))
+    return y
+
+
 class _ShortConv:
     """The q, k, v short conv + SiLU (opt.py:15-93) and its decode caches
     (linear_attention.py:929-941) for one decode call."""
