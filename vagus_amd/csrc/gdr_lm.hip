@@ -8,7 +8,7 @@
 //        g    = -exp(A_log) * softplus(W_a x + dt_bias)      (fp32)
 //        beta = W_b x                                         (fp32, the logits)
 //    -exp(A_log) comes in precomputed.  The projections are 2H dot products of
-//    dim elements per token: a wavefront owns a share of them, its lanes split
+//    dim elements per token: a wavefront owns eight of them, its lanes split
 //    the row, and a shuffle reduction closes each one.
 //
 //  * swiglu_kernel: the FFN's SiLU(x1) x xgate (infra/components/ffn.py:48-50)
@@ -30,33 +30,53 @@ __device__ __forceinline__ float softplus_t(float x) { return x > 20.f ? x : log
 
 }  // namespace
 
+// One wavefront per (token, OPW outputs): every lane loads its slice of the
+// row and of the OPW weight rows at once, so the call costs about one trip to
+// memory rather than one per output.
+constexpr int GATE_OPW = 8;
+
 template <typename E>
-__global__ void __launch_bounds__(256) scalar_gates_kernel(const E *__restrict__ x, const E *__restrict__ w,
-                                                           const float *__restrict__ neg_a,
-                                                           const float *__restrict__ dt_bias, float *g, float *beta,
-                                                           int dim, int H, int n_out) {
+__global__ void __launch_bounds__(64) scalar_gates_kernel(const E *__restrict__ x, const E *__restrict__ w,
+                                                          const float *__restrict__ neg_a,
+                                                          const float *__restrict__ dt_bias, float *g, float *beta,
+                                                          int dim, int H, int n_out) {
     constexpr int VE = 16 / (int)sizeof(E);
     typedef E V __attribute__((ext_vector_type(VE)));
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x;
     const int64_t row = blockIdx.x;
+    const int n0 = blockIdx.y * GATE_OPW;
     const int nu = dim / VE;
     const E *xr = x + row * dim;
-    for (int n = wave; n < n_out; n += 4) {
-        const E *wr = w + (int64_t)n * dim;
-        float acc = 0.f;
-        for (int u = lane; u < nu; u += 64) {
-            const V xv = *reinterpret_cast<const V *>(xr + (int64_t)u * VE);
-            const V wv = *reinterpret_cast<const V *>(wr + (int64_t)u * VE);
+    float acc[GATE_OPW];
 #pragma unroll
-            for (int e = 0; e < VE; ++e) acc += (float)xv[e] * (float)wv[e];
+    for (int j = 0; j < GATE_OPW; ++j) acc[j] = 0.f;
+#pragma unroll 2
+    for (int u = lane; u < nu; u += 64) {
+        const V xv = *reinterpret_cast<const V *>(xr + (int64_t)u * VE);
+        V wv[GATE_OPW];
+#pragma unroll
+        for (int j = 0; j < GATE_OPW; ++j) {
+            const int n = n0 + j < n_out ? n0 + j : n_out - 1;            // rows past the end: reread the last
+            wv[j] = *reinterpret_cast<const V *>(w + (int64_t)n * dim + (int64_t)u * VE);
         }
 #pragma unroll
-        for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
-        const float p = (float)(E)acc;                         // nn.Linear's output in E
-        if (lane == 0) {
-            if (n < H) g[row * H + n] = neg_a[n] * softplus_t(p + dt_bias[n]);
-            else beta[row * H + (n - H)] = p;
-        }
+        for (int j = 0; j < GATE_OPW; ++j)
+#pragma unroll
+            for (int e = 0; e < VE; ++e) acc[j] += (float)xv[e] * (float)wv[j][e];
+    }
+#pragma unroll
+    for (int j = 0; j < GATE_OPW; ++j) {
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) acc[j] += __shfl_xor(acc[j], m);
+    }
+    if (lane < GATE_OPW && n0 + lane < n_out) {
+        float a = acc[0];
+#pragma unroll
+        for (int j = 1; j < GATE_OPW; ++j) a = lane == j ? acc[j] : a;
+        const int n = n0 + lane;
+        const float p = (float)(E)a;                                      // nn.Linear's output in E
+        if (n < H) g[row * H + n] = neg_a[n] * softplus_t(p + dt_bias[n]);
+        else beta[row * H + (n - H)] = p;
     }
 }
 
@@ -85,9 +105,11 @@ __global__ void __launch_bounds__(256) swiglu_kernel(const E *__restrict__ x, E 
 template <typename E>
 static hipError_t scalar_gates_t(const void *x, const void *w, const float *neg_a, const float *dt_bias, float *g,
                                  float *beta, int64_t rows, int dim, int H, bool with_beta, hipStream_t stream) {
-    hipLaunchKernelGGL((scalar_gates_kernel<E>), dim3((unsigned)rows), dim3(256), 0, stream,
+    const int n_out = with_beta ? 2 * H : H;
+    hipLaunchKernelGGL((scalar_gates_kernel<E>), dim3((unsigned)rows, (unsigned)((n_out + GATE_OPW - 1) / GATE_OPW)),
+                       dim3(64), 0, stream,
                        reinterpret_cast<const E *>(x), reinterpret_cast<const E *>(w), neg_a, dt_bias, g, beta, dim,
-                       H, with_beta ? 2 * H : H);
+                       H, n_out);
     return hipGetLastError();
 }
 
