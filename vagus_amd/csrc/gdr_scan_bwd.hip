@@ -117,7 +117,8 @@ struct Blk {
 
 template <int RPL, typename E>
 __device__ __forceinline__ void load_blk(const ScanBwdParams &p, Blk<RPL, E> &b, int64_t bos, int64_t L, int64_t t0,
-                                         int h, int row0, int lane, int col0, bool bwd, const float *ck) {
+                                         int h, int row0, int lane, int col0, bool bwd, const float *ck,
+                                         bool need_uv = true) {
     constexpr int DK = RPL * 64;
     const int H = p.H, DV = p.DV;
     auto th = [&](int64_t i) {
@@ -134,8 +135,13 @@ __device__ __forceinline__ void load_blk(const ScanBwdParams &p, Blk<RPL, E> &b,
     });
     const int li = lane & 31;
     const int64_t tu = th(li >> 2) * DV + col0 + (li & 3);
-    if (bwd && p.mode != 2) b.uf = p.u[tu];
-    else b.vr = reinterpret_cast<const E *>(p.v)[tu];
+    // (the reverse walk reads neither: its dS recurrence needs q, k, the write
+    // vector, the gate and do, and u is being written by the forward walk of
+    // the same launch)
+    if (need_uv) {
+        if (bwd && p.mode != 2) b.uf = p.u[tu];
+        else b.vr = reinterpret_cast<const E *>(p.v)[tu];
+    }
     if (bwd) b.dr = reinterpret_cast<const E *>(p.dout)[tu];
     const int64_t ts = th(lane & (SB_CT - 1));
     if (p.gate == 1) b.gs = p.g[ts];
@@ -290,12 +296,12 @@ __global__ void __launch_bounds__(256) scan_walks_kernel(ScanBwdParams p) {
     };
     {
         Blk<RPL, E> A, B;
-        if (nblk > 0) load_blk<RPL, E>(p, A, bos, L, (nblk - 1) * CT, h, row0, lane, col0, true, nullptr);
+        if (nblk > 0) load_blk<RPL, E>(p, A, bos, L, (nblk - 1) * CT, h, row0, lane, col0, true, nullptr, false);
         for (int64_t b = nblk - 1; b >= 0; b -= 2) {
-            load_blk<RPL, E>(p, B, bos, L, (b > 0 ? b - 1 : 0) * CT, h, row0, lane, col0, true, nullptr);
+            load_blk<RPL, E>(p, B, bos, L, (b > 0 ? b - 1 : 0) * CT, h, row0, lane, col0, true, nullptr, false);
             back_block(A, b);
             if (b >= 1) {
-                load_blk<RPL, E>(p, A, bos, L, (b > 1 ? b - 2 : 0) * CT, h, row0, lane, col0, true, nullptr);
+                load_blk<RPL, E>(p, A, bos, L, (b > 1 ? b - 2 : 0) * CT, h, row0, lane, col0, true, nullptr, false);
                 back_block(B, b - 1);
             }
         }
