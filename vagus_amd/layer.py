@@ -416,8 +416,8 @@ class GatedDeltaNet(nn.Module):
     def _decode_weights(self):
         """The one-token decode step's projection weights regrouped, rebuilt
         whenever a parameter changed (its storage or version): W_q, W_k, W_v
-        and W_g transposed into one contiguous (4, dim, H*dv) tensor, so that one
-        batched product replaces four skinny GEMMs (when H*dk == H*dv); for the
+        and W_g concatenated into one (4 H*dv, dim) weight, so that one GEMM
+        replaces four skinny ones (when H*dk == H*dv); for the
         scalar gate [W_a; W_b] as one (2H, dim) weight (W_a alone without the
         delta rule) and the gate's constants -exp(A_log) and dt_bias in fp32.
         The copies hold one more set of these weights (4 dim H dv + 2 H dim
@@ -432,7 +432,7 @@ class GatedDeltaNet(nn.Module):
         c = self.__dict__.get('_decode_w')
         if c is None or c[0] != key:
             same = len({p.shape for p in ps[:4]}) == 1
-            w4 = torch.stack([p.t() for p in ps[:4]]).contiguous() if same else None
+            w4 = torch.cat(ps[:4]).contiguous() if same else None
             wab = gconst = None
             if scalar:
                 wab = torch.cat([self.wa.weight] + ([self.wb.weight] if self.delta else [])).contiguous()
@@ -451,8 +451,10 @@ class GatedDeltaNet(nn.Module):
         B, L = x.shape[0], x.shape[1]
         w4, wab, gconst = self._decode_weights()
         if w4 is not None:
-            x4 = x.reshape(1, B * L, x.shape[-1]).expand(4, -1, -1).contiguous()
-            y = torch.bmm(x4, w4)
+            # one GEMM over the concatenated weights, then one copy into four
+            # contiguous (B*L, H*dv) blocks, which the decode kernel reads
+            y = F.linear(x.reshape(B * L, -1), w4)
+            y = y.view(B * L, 4, -1).transpose(0, 1).contiguous()
             qp, kp, vp, og = (y[i].view(B, L, -1) for i in range(4))
         else:
             qp, kp, vp, og = self.wq(x), self.wk(x), self.wv(x), self.wg(x)
