@@ -88,8 +88,13 @@ def log(msg):
 
 def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
     """Timed chunked prefill.  Each step issues chunk_prep, an event, then
-    chunk_state on the current stream; returns host-clock totals and the two
-    kernels' event-timed durations."""
+    chunk_state and another event on the current stream; returns host-clock
+    totals and the two kernels' event-timed durations.  Two events per step,
+    around the state kernel: a third at each step's start cost about 3 us per
+    step (161.1 against 158.3 us at gdn_340m; 151.1 with no events), so the
+    prep time is the interval from the previous step's end to the state
+    kernel's start (chunk_prep plus the launch gap before it), over steps
+    1 .. K - 1."""
     xs = [workloads.workload(name, device='cuda') for _ in range(copies)]
     x0 = xs[0]
     gate = 'none' if x0.g is None else ('vector' if x0.g.dim() == 4 else 'scalar')
@@ -103,17 +108,16 @@ def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
         step(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(steps)]
+    ev = [tuple(torch.cuda.Event(enable_timing=True) for _ in range(2)) for _ in range(steps)]
     t0 = time.perf_counter()
     for i in range(steps):
-        a, m, b = ev[i]
-        a.record(stream)
+        m, b = ev[i]
         step(i, m)
         b.record(stream)
     torch.cuda.synchronize()
     total = time.perf_counter() - t0
-    prep_ms = [a.elapsed_time(m) for a, m, _ in ev]
-    state_ms = [m.elapsed_time(b) for _, m, b in ev]
+    prep_ms = [ev[i - 1][1].elapsed_time(ev[i][0]) for i in range(1, steps)] or [0.0]
+    state_ms = [m.elapsed_time(b) for m, b in ev]
     tokens = x0.q.shape[0] * x0.q.shape[1]
     H = x0.q.shape[2]
     del xs
