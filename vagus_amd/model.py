@@ -44,8 +44,8 @@ def _add_norm(norm: RMSNorm, x, delta=None, *, inplace: bool = False):
     if x.is_cuda and ve and norm.gamma.dtype == x.dtype and D % ve == 0 and D // ve <= 2048:
         if delta is None:
             return x, ops.rms_norm(x, norm.gamma, norm.eps)
-        y, h = ops.rms_norm(x, norm.gamma, norm.eps, residual=delta,
-                            out_residual=x if inplace and x.is_contiguous() else None)
+        in_place = inplace and x.is_contiguous() and x.data_ptr() % 16 == 0
+        y, h = ops.rms_norm(x, norm.gamma, norm.eps, residual=delta, out_residual=x if in_place else None)
         return h, y
     if delta is not None:
         x = x.add_(delta) if inplace else x + delta
