@@ -210,8 +210,8 @@ def bench_generate(torch, workloads, reps=2):
     weight_bytes = sum(p.numel() * p.element_size() for p in m.parameters())
     assert toks.shape == (N, new) and int(toks.min()) >= 0 and int(toks.max()) < c['vocab_size']
     del gen, m
-    return {'workload': 'gdn_lm_1p3b: 24-layer GDN LM, d2048 H16 dk=dv=128, vocab 32000, bf16, random init; '
-                        f'{N} prompts U[64, 2048] ({fed + N} tokens), ragged prefill, {new} greedy steps',
+    return {'workload': 'gdn_lm_1p3b: 24-layer GDN LM, d2048 H16 dk=dv=128, vocab 32000, bf16, random init, '
+                        f'la_fused=True; {N} prompts U[64, 2048] ({fed + N} tokens), ragged prefill, {new} greedy steps',
             'prefill_ms': round((t1 - t0) * 1e3, 2), 'prefill_tok_s': round(fed / (t1 - t0), 1),
             'decode_ms': round((t2 - t1) * 1e3, 2), 'decode_step_ms': round(step_s * 1e3, 4),
             'gen_tok_s': round(N * new / (t2 - t1), 1),

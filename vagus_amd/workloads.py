@@ -11,7 +11,9 @@ The shapes and distributions are the benchmark's:
                 [128, 8192], H=16 dk=dv=128, zero entry states
     gdn_lm_1p3b greedy generation with the 1.3B-shape GDN language model
                 (24 layers, hidden 2048, H=16 dk=dv=128, vocab 32000, scalar
-                gate, bf16 weights, random init): 64 prompts with token ids
+                gate, bf16 weights, random init; la_fused=True, the module's
+                option that runs the q, k L2 norm and the beta sigmoid inside
+                the scan kernels): 64 prompts with token ids
                 uniform over the vocabulary and lengths uniform in [64, 2048],
                 ragged prefill, then 256 decode steps (lm_workload)
 
@@ -44,7 +46,8 @@ WORKLOADS = {
 
 LM_WORKLOADS = {
     'gdn_lm_1p3b': dict(model=dict(vocab_size=32000, dim=2048, layer_count=24, head_count=16, key_head_dim=128,
-                                   value_head_dim=128, gate='scalar', short_conv_size=4, chunk_size=64),
+                                   value_head_dim=128, gate='scalar', short_conv_size=4, chunk_size=64,
+                                   la_fused=True),
                         dtype=torch.bfloat16, n_prompts=64, len_lo=64, len_hi=2048, new_tokens=256, seed=4),
 }
 
