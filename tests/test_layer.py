@@ -14,6 +14,8 @@ GPU:
     reproduces forward; export / load mid-stream is exact; L == 0 is a no-op;
     the layer is causal;
   * ragged packed prefill into cache rows against each sequence alone;
+  * the one-token step's regrouped weight copies follow in-place parameter
+    changes (bit-equal to a layer rebuilt from the changed state);
   * the explicit-write route (_write returning w) into chunk_scan_vec.
 Bars: rel-L2 <= 2e-2 for bf16 modules, <= 1e-4 for fp32 modules (fp32
 projections and fp32 kernels against the fp64 oracle).
@@ -178,6 +180,35 @@ def test_decode_matches_forward(gate, delta, conv, dtype, dk, dv):
     b2 = m.decode_step(x[:, 11:])
     assert torch.equal(a, b) and torch.equal(a2, b2) and m.cache_len == 23
     assert torch.equal(m.decode_step(x[:, :0]), x[:, :0])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('gate', ['scalar', 'vector'])
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float32])
+def test_decode_weight_copies_follow_the_parameters(gate, dtype):
+    """The one-token decode step reads regrouped copies of its projection
+    weights (and the scalar gate's constants); an in-place change of a
+    parameter between steps must reach the next step.  Two identical layers
+    step through the same tokens; one has W_q, W_a (or W_a2), A_log and dt_bias
+    changed in place after its first step, the other is rebuilt from that
+    state: their later outputs and states are equal."""
+    import copy
+    m = make(gate, True, 4, dtype=dtype, device='cuda')
+    x = torch.randn(2, 4, 256, generator=torch.Generator().manual_seed(5)).to(dtype).cuda()
+    m.reset_cache(2)
+    m.decode_step(x[:, :1])
+    with torch.no_grad():
+        m.wq.weight.mul_(0.5)
+        (m.wa if gate == 'scalar' else m.wa2).weight.add_(0.01)
+        m.A_log.add_(0.1)
+        m.dt_bias.sub_(0.05)
+    fresh = copy.deepcopy(m)
+    fresh.__dict__.pop('_decode_w', None)                     # a layer that never cached anything
+    for t in range(1, 4):
+        a = m.decode_step(x[:, t:t + 1])
+        b = fresh.decode_step(x[:, t:t + 1])
+        assert torch.equal(a, b), t
+    assert torch.equal(m.state, fresh.state)
 
 
 @pytest.mark.gpu
