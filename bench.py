@@ -1,14 +1,17 @@
 #!/usr/bin/env python
 """Benchmark of the gated delta-rule core on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--settle S] [--no-cpu-baseline]
 
 Headline (the JSON line's `value`): chunked GDN prefill of the 340M layer
 shape, B=8 T=4096 H=8 dk=dv=128, chunk 64, bf16 q/k/v, fp32 gates / beta /
 states (entry state 0.1 N(0,1)); a step is one `chunk_gated_delta_rule` call
 over the whole batch with its inputs resident in HBM; value = tokens/s
 (B*T tokens per step).  Three copies of the inputs (3 x 218 MB) are rotated
-so that no step finds its operands in the 256 MB Infinity Cache.
+so that no step finds its operands in the 256 MB Infinity Cache.  Before
+any timed leg, a fixed clock-settle phase (--settle, default 2 s of untimed
+headline steps, reported as settle_s) brings the GPU's clocks to their loaded
+state, so a short --warmup times the same level as a long one.
 
 The prefill runs as two kernels per call: chunk_prep (every (chunk, head) in
 parallel: the intra-chunk Q K^T and K K^T products and the triangular
@@ -80,6 +83,13 @@ STATE_FLOP_PER_TOKEN_HEAD = 6 * DK * DV + 4 * CHUNK * DV                    # 13
 # chunk_state bytes per token-head: q, k, v (bf16), scalar g, TE + A blocks (2 C^2 bf16 per chunk),
 # o (bf16), entry + final state (2 dk dv fp32 per sequence-head, amortised over T = 4096)
 STATE_BYTES_PER_TOKEN_HEAD = 2 * (2 * DK + DV) + 4 + 2 * 2 * CHUNK + 2 * DV + 2 * DK * DV * 4 // 4096
+# graph-replayed legs (decode, layer kernels): timed replays (at least; --steps when larger) and
+# untimed replays before them, each replay 24 launches
+GRAPH_REPLAYS = 30
+GRAPH_WARM_REPLAYS = 10
+# default clock-settle phase: back-to-back headline prefill steps before the warmup, outside the
+# timed region (short runs after an idle GPU otherwise time the first steps up to 8% slow)
+SETTLE_S = 2.0
 
 
 def log(msg):
@@ -128,6 +138,24 @@ def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
                 state_tflops=tokens * H * STATE_FLOP_PER_TOKEN_HEAD / (statistics.mean(state_ms) * 1e-3) / 1e12)
 
 
+def settle(torch, ops, workloads, seconds):
+    """Untimed headline prefill steps, back to back, for `seconds` of host
+    clock (synchronised every few steps), so that the GPU's clocks have
+    reached their loaded state before any timed leg.  Returns the seconds
+    spent."""
+    if seconds <= 0:
+        return 0.0
+    x = workloads.workload('gdn_340m', device='cuda')
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            ops.chunk_gated_delta_rule(x.q, x.k, x.v, x.g, x.beta, initial_state=x.initial_state,
+                                       output_final_state=True)
+        torch.cuda.synchronize()
+    del x
+    return time.perf_counter() - t0
+
+
 def time_steps(torch, fn, steps, warmup, rotate):
     """`warmup` untimed steps, then exactly `steps` timed ones; returns (host
     seconds around synchronize, per-step event ms)."""
@@ -168,7 +196,7 @@ def bench_decode(torch, ops, workloads, steps, warmup, B=64, H=16, layers=24):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step_all()
-    total, ms = time_steps(torch, lambda i: graph.replay(), max(3, steps // 3), max(2, warmup // 2), 1)
+    total, ms = time_steps(torch, lambda i: graph.replay(), max(GRAPH_REPLAYS, steps), GRAPH_WARM_REPLAYS, 1)
     per_layer_ms = statistics.mean(ms) / layers
     byts = B * H * DECODE_BYTES_PER_SEQ_HEAD
     del graph, states
@@ -260,7 +288,7 @@ def bench_layer_kernels(torch, ops, workloads, steps, warmup):
         with torch.cuda.graph(graph):
             for i in range(calls):
                 fn(i)
-        _, ms = time_steps(torch, lambda i: graph.replay(), max(3, steps // 3), max(2, warmup // 2), 1)
+        _, ms = time_steps(torch, lambda i: graph.replay(), max(GRAPH_REPLAYS, steps), GRAPH_WARM_REPLAYS, 1)
         del graph
         return statistics.mean(ms) / calls * 1e3
 
@@ -302,7 +330,7 @@ def bench_layer_kernels(torch, ops, workloads, steps, warmup):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         step_all()
-    _, ms = time_steps(torch, lambda i: graph.replay(), max(3, steps // 3), max(2, warmup // 2), 1)
+    _, ms = time_steps(torch, lambda i: graph.replay(), max(GRAPH_REPLAYS, steps), GRAPH_WARM_REPLAYS, 1)
     dec_us = statistics.mean(ms) / layers * 1e3
     # per (sequence, head): the plain step's bytes (state read and written, q k v o, g, beta), the three
     # conv caches read and written (K rows of the head's channels each), the epilogue gate row
@@ -550,6 +578,9 @@ def main():
     ap.add_argument('--steps', type=int, default=60)
     ap.add_argument('--warmup', type=int, default=100)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--settle', type=float, default=SETTLE_S, metavar='SECONDS',
+                    help='clock-settle phase before the timed legs: back-to-back untimed headline prefill '
+                         f'steps for this long (default {SETTLE_S}; reported as settle_s)')
     ap.add_argument('--prefill-only', nargs='?', const='gdn_340m', default=None, metavar='WORKLOAD',
                     help='only one prefill workload: gdn_340m (default, the headline line), kda_prefill or '
                          'gdn_varlen (for profiling)')
@@ -611,6 +642,8 @@ def main():
                           'path_tflops': round(r['path_tflops'], 2), 'state_tflops': round(r['state_tflops'], 2)}),
               flush=True)
         return
+    log(f'[bench] clock settle: {args.settle:.1f} s of gdn_340m prefill steps')
+    settle_s = settle(torch, ops, workloads, args.settle)
     log('[bench] prefill gdn_340m')
     pre = bench_prefill(torch, ops, workloads, 'gdn_340m', args.steps, args.warmup)
     extra = {}
@@ -654,6 +687,7 @@ def main():
         'n_gpus': 1,
         'steps': args.steps,
         'warmup': args.warmup,
+        'settle_s': round(settle_s, 3),
         'ms_per_step': round(pre['total_s'] * 1e3 / args.steps, 4),
         'higher_is_better': True,
         'scaling': 'weak',

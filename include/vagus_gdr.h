@@ -203,9 +203,11 @@ int vgdr_chunk_prep_fused(int dtype, int gate_kind, int use_delta,
  * vgdr_chunk_fwd_fused without a workspace argument and without allocating
  * (no reference counterpart: for callers that cannot allocate device memory,
  * such as code under HIP graph capture or a serving loop that forbids
- * hipMalloc).  The chunk workspace lives in a device array the library holds
- * per GPU, VGDR_CHUNK_SCRATCH_BYTES long, from the first call on that GPU to
- * the end of the process.  A call whose vgdr_chunk_workspace_size exceeds it
+ * hipMalloc).  The chunk workspace lives in a file-scope device array,
+ * VGDR_CHUNK_SCRATCH_BYTES long, which exists on every GPU where the library's
+ * code object is loaded (its first kernel launch of any entry point there)
+ * until the end of the process: every process using the library holds it on
+ * each GPU it runs on, whether or not it calls this entry point.  A call whose vgdr_chunk_workspace_size exceeds it
  * returns VGDR_ERR_INVALID (use vgdr_chunk_fwd_fused with a workspace).
  * Calls that overlap on one GPU (two streams, two threads) share that array
  * and race; serialise them.  Otherwise the arguments, checks and results are

@@ -129,3 +129,37 @@ def test_forward_and_packed_prefill_agree():
     last = m.prefill_packed(ids, cu)
     for i in range(2):
         assert rel(last[i], full[i]) < 1e-5
+
+
+@pytest.mark.gpu
+def test_graph_follows_weight_and_cache_changes():
+    """A recorded decode step is dropped when what it holds by address
+    changes: load_state_dict of other weights (in place, new versions) and a
+    cache reset that reallocates (dtype change) both lead to the eager
+    tokens, and recording does not advance the layers' cache_len."""
+    m, other = tiny(torch.float32, seed=0), tiny(torch.float32, seed=5)
+    ps = prompts([9, 40, 3], seed=6)
+    gen = RaggedGenerator(m)
+    gen.prefill(ps)
+    gen.generate(4, graph=True)
+    assert gen._graph is not None
+    # packed prefill leaves cache_len at 0; the eager first step counts once,
+    # the recording and the replays not at all
+    assert all(blk.att.cache_len == 1 for blk in m.blocks)
+    lens = [blk.att.cache_len for blk in m.blocks]
+    gen.generate(1, graph=True)
+    assert [blk.att.cache_len for blk in m.blocks] == lens   # replays leave the host counters alone
+    m.load_state_dict(other.state_dict())
+    gen.prefill(ps)
+    replay = gen.generate(6, graph=True)
+    ref = RaggedGenerator(other)
+    ref.prefill(ps)
+    eager = ref.generate(6, graph=False)
+    torch.cuda.synchronize()
+    assert torch.equal(replay, eager)
+    # a different batch size records again; the same size after load_cache keeps the graph valid
+    gen.prefill(ps[:2])
+    a = gen.generate(3, graph=True)
+    ref.prefill(ps[:2])
+    b = ref.generate(3, graph=False)
+    assert torch.equal(a, b)

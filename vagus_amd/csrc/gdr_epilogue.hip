@@ -96,7 +96,9 @@ hipError_t norm_gate(int dtype, const void *o, const Epilogue &ep, void *out, in
 // a handful of rows of a few thousand elements, so one kernel here replaces the
 // eight elementwise and reduction kernels of the module's expression.
 template <typename E, int U>
-__global__ void __launch_bounds__(256) rms_norm_kernel(const E *__restrict__ x, const E *__restrict__ res, E *x_out,
+// x_out may be x or res itself (the residual stream updated in place), so
+// neither input is declared __restrict__.
+__global__ void __launch_bounds__(256) rms_norm_kernel(const E *x, const E *res, E *x_out,
                                                        const E *__restrict__ gamma, float eps, E *y, int dim) {
     constexpr int VE = 16 / (int)sizeof(E);
     typedef E V __attribute__((ext_vector_type(VE)));

@@ -271,6 +271,7 @@ class RaggedGenerator:
         self.pending: torch.Tensor | None = None
         self.fed_len: list[int] = []
         self._graph = None
+        self._graph_key = None
 
     def reset(self, batch_size: int) -> None:
         """batch_size empty streams.  The caches are zeroed in place when the
@@ -319,26 +320,49 @@ class RaggedGenerator:
         self.pending.copy_(nxt)
         return nxt
 
+    def _fingerprint(self) -> tuple:
+        """What a recorded decode step holds by address: every parameter
+        (storage and version: load_state_dict, an optimizer step or .to()
+        change one of them), each layer's state and conv-cache buffers, and
+        the regrouped decode weights.  A replay is valid only while this is
+        unchanged."""
+        key = [(p.data_ptr(), p._version) for p in self.model.parameters()]
+        for blk in self.model.blocks:
+            att = blk.att
+            key += [(t.data_ptr(), t.dtype) for t in (att.state,) + (att._caches() if att.short_conv_size else ())]
+            c = att.__dict__.get('_decode_w')
+            key.append(None if c is None else tuple(None if t is None else t.data_ptr()
+                                                    for t in (c[1], c[2]) + (c[3] or ())))
+        return tuple(key)
+
     @torch.no_grad()
     def generate(self, steps: int, *, graph: bool = True) -> torch.Tensor:
         """`steps` greedy decode steps for every stream: (N, steps) int64.
         With graph=True the first step ever taken runs eagerly and is then
         recorded into a HIP graph (recording executes nothing); every later
-        step, in this call or a later one, replays it.  Replays read and
-        advance the caches and the pending tokens in place; the layers'
-        host-side cache_len counters are not advanced by them (fed_len here
-        is)."""
+        step, in this call or a later one, replays it, until a parameter or a
+        cache buffer it holds changes (then the next step runs eagerly and
+        is recorded again).  Replays read and advance the caches and the
+        pending tokens in place; the layers' host-side cache_len counters are
+        not advanced by them (fed_len here is)."""
         assert self.pending is not None and self.batch_size > 0, 'prefill first'
         out = torch.empty(self.batch_size, steps, dtype=torch.int64, device=self.device)
         for i in range(steps):
+            if graph and self._graph is not None and self._graph_key != self._fingerprint():
+                self._graph = None                    # a captured tensor moved or changed: record again
             if graph and self._graph is not None:
                 self._graph.replay()
                 out[:, i].copy_(self.pending)
             else:
                 out[:, i].copy_(self._step())
                 if graph and self._graph is None:
+                    # recording runs no kernel: the layers' cache_len must not count it
+                    lens = [blk.att.cache_len for blk in self.model.blocks]
                     self._graph = torch.cuda.CUDAGraph()
                     with torch.cuda.graph(self._graph):
                         self._step()
+                    for blk, n in zip(self.model.blocks, lens):
+                        blk.att.cache_len = n
+                    self._graph_key = self._fingerprint()
             self.fed_len = [n + 1 for n in self.fed_len]
         return out
