@@ -1457,13 +1457,36 @@ chunk_pipe_kernel(const ChunkParams p) {
         // outside it and their stores are dropped, with no lane-dependent branch
         const __amdgpu_buffer_rsrc_t ors =
             buffer_rsrc(reinterpret_cast<E *>(p.o) + t0 * sv + (int64_t)h * DV + col0, (uint32_t)(clen * sv * sizeof(E)));
-        unroll<NW>([&](auto s) {
-            if (col0 + 16 * s >= DV) return;
+        if constexpr (NW % 2 == 0) {
+            // strips 2 m and 2 m + 1 leave as 16-byte units: lanes l and l ^ 16 trade
+            // halves (v_permlane16_swap), after which lane (g, r) holds eight consecutive
+            // columns of row r -- strip 2 m + (g & 1), columns 8 (g >> 1) .. + 7 -- and
+            // each store writes 64 contiguous bytes of 16 rows (8-byte stores wrote
+            // 32-byte pieces, a quarter of a cache line, which cost HBM write
+            // efficiency).  A lane whose columns lie past dv gets an offset outside
+            // the buffer, so its store is dropped without a branch.
             unroll<NR>([&](auto i) {
                 const int I = rb(i);
-                buffer_store_8b(EL::cvt(ot[s][i]), ors,
-                                (uint32_t)(((16 * I + r16) * sv + 16 * s + 4 * g4) * sizeof(E)));
+                unroll<NW / 2>([&](auto m) {
+                    const u32x2 x = __builtin_bit_cast(u32x2, EL::cvt(ot[2 * m][i]));
+                    const u32x2 y = __builtin_bit_cast(u32x2, EL::cvt(ot[2 * m + 1][i]));
+                    const auto a = __builtin_amdgcn_permlane16_swap(x[0], y[0], false, false);
+                    const auto b = __builtin_amdgcn_permlane16_swap(x[1], y[1], false, false);
+                    const int col = 32 * m + 16 * (g4 & 1) + 8 * (g4 >> 1);
+                    const uint32_t off = col0 + col < DV ? (uint32_t)(((16 * I + r16) * sv + col) * sizeof(E))
+                                                         : 0x80000000u;
+                    __builtin_amdgcn_raw_buffer_store_b128(u32x4{a[0], b[0], a[1], b[1]}, ors, (int)off, 0, 0);
+                });
             });
+        }
+        unroll<NW>([&](auto s) {
+            if (col0 + 16 * s >= DV) return;
+            if constexpr (NW % 2 != 0)
+                unroll<NR>([&](auto i) {
+                    const int I = rb(i);
+                    buffer_store_8b(EL::cvt(ot[s][i]), ors,
+                                    (uint32_t)(((16 * I + r16) * sv + 16 * s + 4 * g4) * sizeof(E)));
+                });
             if constexpr (HS) {
                 // the checkpoint's fragment order: lane (g, r) holds rows 16 kt + 4 g .. + 3
                 // of column 16 cb + r.  Output wave o stores key blocks o, o + 2, ..
