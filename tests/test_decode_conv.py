@@ -198,3 +198,33 @@ def test_decode_step_conv_misuse():
     with pytest.raises(AssertionError):                      # caches are updated in place: q's dtype
         ops.hip_decode_step(dev(qp), dev(kp), dev(vp), dev(gl), dev(beta), dev(S0), scale=0.1,
                             conv_weights=tuple(dev(w) for w in ws), conv_cache=tuple(dev(c.float()) for c in cs))
+
+
+@pytest.mark.gpu
+def test_decode_step_at_lm_layer_shape():
+    """The one-token step exactly as the 1.3B LM's layers call it (B64 H16
+    dk=dv=128, K4, bf16 projections and weights, the L2 norm, beta from its
+    logits, the scalar gate, the RMSNorm x SiLU(gate) epilogue): decode_conv_kernel<128, 128>
+    against the oracle's decode_step + norm_gate in fp64."""
+    from vagus_amd import ops
+    B, H, dk, dv, K = 64, 16, 128, 128, 4
+    qp, kp, vp, ws, cs, gl, beta, S0 = _decode_inputs(B, 1, H, dk, dv, K, 'scalar', torch.bfloat16, seed=41,
+                                                      w_dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(42)
+    blog = torch.randn(B, 1, H, generator=g)                   # beta logits
+    og = torch.randn(B, 1, H, dv, generator=g).bfloat16()
+    gamma = (torch.rand(dv, generator=g) + 0.5).bfloat16()
+    print(f'\n[case] decode step at the LM layer shape B{B} H{H} dk={dk} dv={dv}', flush=True)
+    o_ref, S_ref, c_ref = gdr.decode_step(qp, kp, vp, gl.double(), torch.sigmoid(blog).double(), S0.double(), ws, cs,
+                                          scale=dk ** -0.5)
+    o_ref = gdr.norm_gate(o_ref.to(torch.bfloat16).double(), og.double(), gamma.double(), 1e-6)
+    dev = lambda t: t.cuda()
+    S = dev(S0.clone())
+    caches = tuple(dev(c.clone()) for c in cs)
+    o = ops.hip_decode_step(dev(qp), dev(kp), dev(vp), dev(gl), dev(blog), S, scale=dk ** -0.5,
+                            conv_weights=tuple(dev(w) for w in ws), conv_cache=caches, l2norm=True,
+                            beta_logits=True, out_gate=dev(og), out_norm_weight=dev(gamma))
+    eo, es = _rel(o, o_ref), _rel(S, S_ref)
+    exact = all(torch.equal(a.cpu(), b) for a, b in zip(caches, c_ref))
+    print(f'[parity] LM-shape decode step o={eo:.3e} S={es:.3e} caches exact={exact} (tol {TOL:g})', flush=True)
+    assert eo <= TOL and es <= TOL and exact

@@ -122,3 +122,53 @@ def test_lm_tied_head_and_param_layout():
         assert want in keys, want
     # Llama's SwiGLU sizing: 8/3 dim rounded up to 256 (block.py:43-44)
     assert sd['blocks.0.ffn.l1.weight'].shape == (2 * 256, 32)
+
+
+# --- closed forms of the oracle's FFN and scalar gates ------------------------
+
+def test_swiglu_closed_form():
+    """swiglu(x) = SiLU(first half of l1 x) * (second half) projected by l2
+    (ffn.py:46-50).  With l1 = [I; 2I] and l2 = I it is x * 2x / (1 + e^-x)
+    elementwise; a swapped pair of halves would give 2x * x / (1 + e^-2x)."""
+    import math
+    x = torch.tensor([[0.0, 1.0, -1.0, 2.0, -3.0]], dtype=torch.float64)
+    n = x.shape[1]
+    eye = torch.eye(n, dtype=torch.float64)
+    y = om.swiglu(x, torch.cat([eye, 2 * eye]), eye)
+    want = torch.tensor([[2 * v * v / (1 + math.exp(-v)) for v in x[0].tolist()]], dtype=torch.float64)
+    assert torch.allclose(y, want, rtol=1e-14, atol=1e-14)
+    swapped = torch.tensor([[2 * v * v / (1 + math.exp(-2 * v)) for v in x[0].tolist()]], dtype=torch.float64)
+    assert not torch.allclose(y, swapped)
+    # l2 maps back: a permutation of the hidden units permutes nothing in the result's meaning
+    l2 = torch.zeros(2, n, dtype=torch.float64)
+    l2[0, 1] = 1.0
+    l2[1, 3] = -0.5
+    y2 = om.swiglu(x, torch.cat([eye, 2 * eye]), l2)
+    assert torch.allclose(y2, torch.tensor([[want[0, 1].item(), -0.5 * want[0, 3].item()]], dtype=torch.float64))
+
+
+def test_scalar_gates_closed_form():
+    """_gates for the scalar gate (linear_attention.py:719-721, :734-735):
+    g = -exp(A_log) softplus(W_a x + dt_bias), beta = sigmoid(W_b x), checked
+    at points where both have closed values: softplus(0) = ln 2,
+    softplus(ln(e - 1)) = 1, sigmoid(0) = 1/2, sigmoid(ln 3) = 3/4."""
+    import math
+    cfg = dict(head_count=2, key_head_dim=4, value_head_dim=4, gate='scalar', delta=True)
+    dim = 3
+    x = torch.tensor([[[1.0, 0.0, 0.0], [0.0, 1.0, 0.0]]], dtype=torch.float64)     # (B=1, L=2, dim)
+    sd = {
+        'A_log': torch.tensor([math.log(2.0), 0.0], dtype=torch.float64),
+        'dt_bias': torch.tensor([0.0, math.log(math.e - 1.0)], dtype=torch.float64),
+        # head 0 reads nothing; head 1 reads -ln(e - 1) of token 1's second feature
+        'wa.weight': torch.tensor([[0.0, 0.0, 0.0], [0.0, -math.log(math.e - 1.0), 0.0]], dtype=torch.float64),
+        # head 0: 0 everywhere; head 1: ln 3 of the first feature
+        'wb.weight': torch.tensor([[0.0, 0.0, 0.0], [math.log(3.0), 0.0, 0.0]], dtype=torch.float64),
+    }
+    g, beta = om._gates(sd, '', x, cfg, torch.float64)
+    ln2 = math.log(2.0)
+    want_g = torch.tensor([[[-2.0 * ln2, -1.0],          # token 0: head 0 = -2 ln 2, head 1 = -1 * softplus(ln(e-1)) = -1
+                            [-2.0 * ln2, -ln2]]],        # token 1: head 1's pre-activation is 0 -> -ln 2
+                          dtype=torch.float64)
+    want_b = torch.tensor([[[0.5, 0.75], [0.5, 0.5]]], dtype=torch.float64)
+    assert torch.allclose(g, want_g, rtol=1e-14, atol=1e-14), g
+    assert torch.allclose(beta, want_b, rtol=1e-14, atol=1e-14), beta
