@@ -336,6 +336,8 @@ def bench_layer_kernels(torch, ops, workloads, steps, warmup):
     # conv caches read and written (K rows of the head's channels each), the epilogue gate row
     dec_bytes = Bd * Hd * (DECODE_BYTES_PER_SEQ_HEAD + 3 * 2 * K * D * 2 + D * 2)
     del graph, states, caches
+    dec256_us, dec256_bytes = bench_decode_wide(torch, ops, steps, g)
+    dec256b_us, dec256b_bytes = bench_decode_wide(torch, ops, steps, g, B=128)
     return {
         'short_conv': {'workload': 'causal_conv1d + SiLU, B8 T4096 D1024 K4 bf16, bf16 weights', 'us': round(conv_us, 2),
                        'achieved_GBs': round(conv_bytes / conv_us / 1e3, 1),
@@ -349,7 +351,58 @@ def bench_layer_kernels(torch, ops, workloads, steps, warmup):
                                           'epilogue) B64 H16 dk=dv=128 K4, 24 layers graph-replayed',
                               'us_per_step': round(dec_us, 2), 'achieved_GBs': round(dec_bytes / dec_us / 1e3, 1),
                               'frac_hbm': round(dec_bytes / dec_us / 1e3 / PEAK_HBM_GBS, 4)},
+        'decode_step_fused_dv256': {
+            'workload': 'vgdr_decode_step (conv + caches, L2 norm, beta sigmoid, KDA gate activation, recurrence, '
+                        'epilogue) B64 H4 dk=128 dv=256 K4 (the dk 128 / dv 256 mixer heads), 24 layers graph-replayed',
+            'us_per_step': round(dec256_us, 2), 'bytes_per_step': dec256_bytes,
+            'achieved_GBs': round(dec256_bytes / dec256_us / 1e3, 1),
+            'frac_hbm': round(dec256_bytes / dec256_us / 1e3 / PEAK_HBM_GBS, 4),
+            'B128_us_per_step': round(dec256b_us, 2),
+            'B128_frac_hbm': round(dec256b_bytes / dec256b_us / 1e3 / PEAK_HBM_GBS, 4)},
     }
+
+
+def bench_decode_wide(torch, ops, steps, g, B=64, H=4, dk=128, dv=256, K=4, layers=24):
+    """The one-kernel decode step at the dk 128 / dv 256 head shape (the
+    reference's LAX1 / HAX mixers and its own layer bench): conv with its
+    caches, L2 norm, beta sigmoid, the KDA gate activation, the recurrence
+    and the epilogue, 24 rotating layers replayed from a HIP graph.  Returns
+    (us per layer step, algorithmic bytes per step)."""
+    import torch.nn.functional as F
+    states = [torch.randn(B, H, dk, dv, generator=g).cuda() for _ in range(layers)]
+    caches = [[torch.randn(B, K, H * d, generator=g).bfloat16().cuda() for d in (dk, dk, dv)] for _ in range(layers)]
+    cw = [(0.5 * torch.randn(H * d, 1, K, generator=g)).bfloat16().cuda() for d in (dk, dk, dv)]
+    qp, kp = (torch.randn(B, 1, H * dk, generator=g).bfloat16().cuda() for _ in range(2))
+    vp = torch.randn(B, 1, H * dv, generator=g).bfloat16().cuda()
+    f = torch.randn(B, 1, H, dk, generator=g).cuda()
+    A_log = torch.rand(H, generator=g).cuda()
+    dt_bias = torch.randn(H * dk, generator=g).cuda()
+    bl = torch.randn(B, 1, H, generator=g).cuda()
+    og = [torch.randn(B, 1, H, dv, generator=g).bfloat16().cuda() for _ in range(layers)]
+    gamma = (torch.rand(dv, generator=g) + 0.5).bfloat16().cuda()
+
+    def step_all():
+        for i in range(layers):
+            ops.hip_decode_step(qp, kp, vp, f, bl, states[i], scale=dk ** -0.5, conv_weights=cw,
+                                conv_cache=caches[i], beta_logits=True, gate_in_kernel=True, A_log=A_log,
+                                dt_bias=dt_bias, out_gate=og[i], out_norm_weight=gamma)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            step_all()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step_all()
+    _, ms = time_steps(torch, lambda i: graph.replay(), max(GRAPH_REPLAYS, steps), GRAPH_WARM_REPLAYS, 1)
+    us = statistics.mean(ms) / layers * 1e3
+    # per (sequence, head): the fp32 state read and written, q k (bf16, dk), v o (bf16, dv), the fp32 gate
+    # pre-activation row (dk) and beta, the three conv caches read and written (K rows each), the gate row
+    per = 2 * dk * dv * 4 + (2 * dk + 2 * dv) * 2 + dk * 4 + 4 + 2 * K * (2 * dk + dv) * 2 + dv * 2
+    del graph, states, caches
+    return us, B * H * per
 
 
 def bench_backward(torch, ops, workloads, steps, warmup):

@@ -732,8 +732,19 @@ int recurrent_call(int dtype, int gate_kind, int use_delta, const void *q, const
     vgdr::ShortConv cv;
     rc = check_conv("vgdr_recurrent_fwd", conv, dtype, cv);
     if (rc) return rc;
-    if (dv != 64 && dv != 128)
-        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_recurrent_fwd: dv=%lld (supported: 64, 128)", (long long)dv);
+    if (dv == 256) {
+        // the layer's one-token decode step only: a state, the four-tap conv with
+        // 16-byte aligned weights, one token per sequence, no packed offsets
+        const bool ok = conv && cv.K == 4 && T == 1 && !cu_seqlens && initial_state && !w &&
+                        aligned16(cv.wq) && aligned16(cv.wk) && aligned16(cv.wv);
+        if (!ok)
+            return fail(VGDR_ERR_UNSUPPORTED,
+                        "vgdr_recurrent_fwd: dv=256 runs the one-token decode step with the four-tap short conv "
+                        "(T=1, no cu_seqlens, a state, 16-byte aligned conv weights) only");
+    } else if (dv != 64 && dv != 128) {
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_recurrent_fwd: dv=%lld (supported: 64, 128; 256 for the decode step "
+                    "with the short conv)", (long long)dv);
+    }
     if (!aligned16(initial_state) || !aligned16(final_state))
         return fail(VGDR_ERR_INVALID, "vgdr_recurrent_fwd: states must be 16-byte aligned");
     vgdr::RecParams p{};

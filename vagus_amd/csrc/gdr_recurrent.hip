@@ -339,17 +339,30 @@ recurrent_kernel(const RecParams p) {
 // loads ahead of the state's, 25.7 us in this order before the decay folding.  A
 // producer wave of its own (5 waves per workgroup) needs more than 96 VGPRs and
 // spills: 31 us.
+// dv = 256 (the reference's dk 128 / dv 256 mixer heads) runs 512 threads with
+// another layout: wave w owns columns 32 w .. 32 w + 31 of every row (lane (rg,
+// cg): rows rg + 8 i, columns 32 w + 4 cg .. + 3), so a thread's share of the
+// 128 KiB state is 64 fp32 registers and kS, qS are reduced inside the wave.
+// No barrier then separates a wave's state loads from its state stores: waves
+// whose rows arrive first update and store them while the others still load.
+// With one workgroup per CU (B64 H4), a layout whose reduction spans the waves
+// made every wave of the chip load, then every wave store (58 % of HBM).
+template <int DV> constexpr int decode_threads() { return DV > 128 ? 512 : 256; }
+
 template <int DK, int DV, typename E, int GATE, int MODE, typename WT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATE == 2 || (MODE & 4) ? 1 : 4)))
+__global__ void __launch_bounds__(decode_threads<DV>())
+__attribute__((amdgpu_waves_per_eu(GATE == 2 || (MODE & 4) || DV > 128 ? 1 : 4)))
 decode_conv_kernel(const RecParams p) {
     constexpr bool EPI = MODE & 1, WR = MODE & 4;
-    constexpr int NT = 256;
-    constexpr int NCG = DV / 4;
-    constexpr int NRG = NT / NCG;
+    constexpr bool WIDE = DV > 128;                             // one wave per 32 columns
+    constexpr int NT = decode_threads<DV>();
+    constexpr int NCG = WIDE ? 8 : DV / 4;                      // column groups (WIDE: per wave)
+    constexpr int NRG = WIDE ? 8 : NT / NCG;                    // row groups (WIDE: per wave)
     constexpr int RPT = DK / NRG;
     constexpr int NWV = NT / 64;
     constexpr int K = 4;
-    static_assert(NT % NCG == 0 && DK % NRG == 0 && 64 % NCG == 0 && DK <= NT && DV <= NT, "thread layout");
+    static_assert(WIDE ? (NWV * 32 == DV && DK % NRG == 0 && DK <= NT)
+                       : (NT % NCG == 0 && DK % NRG == 0 && 64 % NCG == 0 && DK <= NT && DV <= NT), "thread layout");
     using EL = Elem<E>;
 
     // qs, ks: q (scaled) and k, times the per-channel decay with GATE 2; kr: k itself
@@ -358,15 +371,18 @@ decode_conv_kernel(const RecParams p) {
     __shared__ __attribute__((aligned(16))) float kr[GATE == 2 ? DK : 1];
     __shared__ __attribute__((aligned(16))) float vs[DV];
     __shared__ __attribute__((aligned(16))) float gv[GATE == 2 ? DK : 1];
-    __shared__ __attribute__((aligned(16))) float red[NWV][2][DV];
+    __shared__ __attribute__((aligned(16))) float red[WIDE ? 1 : NWV][2][WIDE ? 4 : DV];
     __shared__ float nrm[NWV][3];           // per-wave sums: q^2, k^2, then q . k (q . w)
+    __shared__ float ssq[WIDE ? NWV : 1];   // WIDE epilogue: per-wave sums of o^2
     __shared__ float sc[2];                 // decay (scalar gate), beta
     __shared__ __attribute__((aligned(16))) float wsv[WR ? DK : 4];
     __shared__ __attribute__((aligned(16))) float gts[EPI ? DV : 4];
     __shared__ __attribute__((aligned(16))) float gms[EPI ? DV : 4];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int cg = tid % NCG, rg = tid / NCG;
+    // cg: the thread's column group (columns 4 cg .. + 3); rg: its first row
+    const int cg = WIDE ? NCG * wave + (lane & (NCG - 1)) : tid % NCG;
+    const int rg = WIDE ? lane / NCG : tid / NCG;
     const int H = p.H;
     const int h = blockIdx.x % H;
     const int seq = blockIdx.x / H;
@@ -491,6 +507,7 @@ decode_conv_kernel(const RecParams p) {
         kS *= a0;
         qS *= a0;
     }
+    // the sums over the row groups: lanes l ^ NCG .. l ^ 32 (WIDE: all of them)
 #pragma unroll
     for (int off = NCG; off < 64; off <<= 1) {
 #pragma unroll
@@ -499,23 +516,70 @@ decode_conv_kernel(const RecParams p) {
             qS[e] += __shfl_xor(qS[e], off);
         }
     }
-    if (lane < NCG) {
-        st4(&red[wave][0][4 * cg], kS);
-        st4(&red[wave][1][4 * cg], qS);
-    }
-    lds_barrier();
-    kS = ld4(&red[0][0][4 * cg]);
-    qS = ld4(&red[0][1][4 * cg]);
     float qk = nrm[0][2];
 #pragma unroll
-    for (int w = 1; w < NWV; ++w) {
-        kS += ld4(&red[w][0][4 * cg]);
-        qS += ld4(&red[w][1][4 * cg]);
-        qk += nrm[w][2];
+    for (int w = 1; w < NWV; ++w) qk += nrm[w][2];
+    if constexpr (!WIDE) {
+        // ... and over the waves
+        if (lane < NCG) {
+            st4(&red[wave][0][4 * cg], kS);
+            st4(&red[wave][1][4 * cg], qS);
+        }
+        lds_barrier();
+        kS = ld4(&red[0][0][4 * cg]);
+        qS = ld4(&red[0][1][4 * cg]);
+#pragma unroll
+        for (int w = 1; w < NWV; ++w) {
+            kS += ld4(&red[w][0][4 * cg]);
+            qS += ld4(&red[w][1][4 * cg]);
+        }
     }
     const f32x4 v4 = ld4(&vs[4 * cg]);
     const f32x4 u = p.use_delta ? sc[1] * (v4 - kS) : v4;
     const f32x4 o = qS + qk * u;                     // o = q^T (diag(a) S + k u^T)
+    if constexpr (WIDE) {
+        // the state first: its stores leave before the epilogue's barrier
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+            const int r = rg + NRG * i;
+            const float a = GATE == 2 ? gv[r] : a0;
+            S[i] = a * S[i] + (WR ? wsv[r] : GATE == 2 ? kr[r] : ks[r]) * u;
+        }
+        if (p.ht) {
+            const __amdgpu_buffer_rsrc_t s_out = buffer_rsrc(p.ht + sbase, DK * DV * 4);
+#pragma unroll
+            for (int i = 0; i < RPT; ++i) buffer_store_nt4(S[i], s_out, so, (uint32_t)(NRG * i * DV * 4));
+        }
+        float x[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = EL::to_f(EL::from_f(o[e]));
+        if constexpr (EPI) {
+            // the output epilogue (linear_attention.py:814-825): the row's sum of
+            // squares over the wave's 32 columns (lanes 0 .. NCG - 1 hold them;
+            // every row group has a copy), then over the waves
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) ss += x[e] * x[e];
+#pragma unroll
+            for (int m = 1; m < NCG; m <<= 1) ss += __shfl_xor(ss, m);
+            if (lane == 0) ssq[wave] = ss;
+            lds_barrier();
+            ss = 0.f;
+#pragma unroll
+            for (int w = 0; w < NWV; ++w) ss += ssq[w];
+            const float r = rsqrtf(ss * (1.f / DV) + p.ep.eps);
+            if (rg == 0) {
+                const f32x4 gt = ld4(&gts[4 * cg]), gm = ld4(&gms[4 * cg]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    og[vo + 4 * cg + e] = EL::from_f(x[e] * r * gm[e] * (gt[e] * sigmoidf_(gt[e])));
+            }
+        } else if (rg == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) og[vo + 4 * cg + e] = EL::from_f(x[e]);
+        }
+        return;
+    }
     if constexpr (EPI) {
         // the output epilogue (linear_attention.py:814-825); wave 0 holds every column
         if (wave == 0) {
@@ -585,13 +649,37 @@ static hipError_t launch_rec(const RecParams &p, hipStream_t stream) {
     return hipGetLastError();
 }
 
+template <int DK, int DV, typename E, int GATE>
+static hipError_t launch_dec_wide(const RecParams &p, hipStream_t stream) {
+    // dv = 256: the one-token decode step with the short conv only (the API refuses
+    // every other call at this width)
+    const int64_t blocks = (int64_t)p.n_seqs * p.H;
+    if (blocks == 0) return hipSuccess;
+    const bool aligned = (((uintptr_t)p.cv.wq | (uintptr_t)p.cv.wk | (uintptr_t)p.cv.wv) & 15) == 0;
+    if (p.cu || p.T != 1 || !p.h0 || p.cv.K != 4 || !aligned || p.w) return hipErrorInvalidValue;
+    const bool wf = p.cv.w_f32 && !std::is_same<E, float>::value;
+    const dim3 grid((unsigned)blocks), block(decode_threads<DV>());
+    if (p.ep.gate) {
+        if (wf) hipLaunchKernelGGL((decode_conv_kernel<DK, DV, E, GATE, 1, float>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((decode_conv_kernel<DK, DV, E, GATE, 1, E>), grid, block, 0, stream, p);
+    } else {
+        if (wf) hipLaunchKernelGGL((decode_conv_kernel<DK, DV, E, GATE, 0, float>), grid, block, 0, stream, p);
+        else hipLaunchKernelGGL((decode_conv_kernel<DK, DV, E, GATE, 0, E>), grid, block, 0, stream, p);
+    }
+    return hipGetLastError();
+}
+
 template <int DK, int DV, typename E>
 static hipError_t rec_gate(int gate_vector, const RecParams &p, hipStream_t s) {
-    return gate_vector ? launch_rec<DK, DV, E, 2>(p, s) : launch_rec<DK, DV, E, 1>(p, s);
+    if constexpr (DV > 128)
+        return gate_vector ? launch_dec_wide<DK, DV, E, 2>(p, s) : launch_dec_wide<DK, DV, E, 1>(p, s);
+    else
+        return gate_vector ? launch_rec<DK, DV, E, 2>(p, s) : launch_rec<DK, DV, E, 1>(p, s);
 }
 
 template <typename E>
 static hipError_t rec_shape(int dk, int dv, int gate_vector, const RecParams &p, hipStream_t s) {
+    if (dv == 256) return dk == 64 ? rec_gate<64, 256, E>(gate_vector, p, s) : rec_gate<128, 256, E>(gate_vector, p, s);
     if (dk == 64) return dv == 64 ? rec_gate<64, 64, E>(gate_vector, p, s) : rec_gate<64, 128, E>(gate_vector, p, s);
     return dv == 64 ? rec_gate<128, 64, E>(gate_vector, p, s) : rec_gate<128, 128, E>(gate_vector, p, s);
 }

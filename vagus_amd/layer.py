@@ -410,8 +410,10 @@ class GatedDeltaNet(nn.Module):
         return (self.qp_cache, self.kp_cache, self.vp_cache)
 
     def _decode_kernel_fits(self) -> bool:
+        # dv = 256 (the reference's dk 128 / dv 256 heads) runs the one-kernel step
+        # with the usual four conv taps
         return (self.short_conv_size is not None and self.key_head_dim in (64, 128)
-                and self.value_head_dim in (64, 128))
+                and (self.value_head_dim in (64, 128) or (self.value_head_dim == 256 and self.short_conv_size == 4)))
 
     def _decode_weights(self):
         """The one-token decode step's projection weights regrouped, rebuilt

@@ -42,6 +42,7 @@ from . import _lib
 _DTYPES = {torch.float32: _lib.VGDR_F32, torch.bfloat16: _lib.VGDR_BF16, torch.float16: _lib.VGDR_F16}
 _CHUNK_TILE_DV = 16          # the chunk kernel takes dv in multiples of 16
 _REC_DVS = (64, 128)         # the recurrent kernel's column widths
+_DEC_DVS = (64, 128, 256)    # the one-token decode step with the short conv (one kernel)
 
 
 def _ptr(t):
@@ -835,8 +836,8 @@ class _ShortConv:
     def struct(self, c):
         """(vgdr_short_conv, tensors to keep alive) for the validated call c."""
         if c.padded:
-            raise NotImplementedError(f'the fused short conv needs dk, dv in {_REC_DVS} (no padding); '
-                                      f'got dk={c.dk}, dv={c.dv}')
+            raise NotImplementedError(f'the fused short conv needs dk in {_REC_DVS} and dv in {_DEC_DVS} '
+                                      f'(no padding); got dk={c.dk}, dv={c.dv}')
         D = (c.H * c.dk, c.H * c.dk, c.H * c.dv)
         for w, d in zip(self.weights, D):
             assert w.shape == (d, self.K), f'conv weight must be ({d}, {self.K}) or ({d}, 1, {self.K}); got {tuple(w.shape)}'
@@ -874,15 +875,21 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
         assert w.shape == q.shape, f'w must be {tuple(q.shape)} (B, T, H, dk); got {tuple(w.shape)}'
         if conv is not None or epilogue is not None:
             raise NotImplementedError('the explicit write vector runs without the short conv and the epilogue')
-    if conv is not None and (dv not in _REC_DVS or q.shape[-1] not in _REC_DVS):
-        raise NotImplementedError(f'the fused short conv needs dk, dv in {_REC_DVS}; got dk={q.shape[-1]}, dv={dv}')
-    if epilogue is not None and dv not in _REC_DVS:
+    # dv = 256 runs in one kernel as the layer's one-token decode step (the conv's
+    # four taps, T = 1, no packed offsets, a state); other calls at that width
+    # take 128-column slices (no conv, the epilogue as its own pass)
+    wide_step = (conv is not None and dv == 256 and q.shape[1] == 1 and cu_seqlens is None
+                 and initial_state is not None and w is None)
+    if conv is not None and ((dv not in _REC_DVS and not wide_step) or q.shape[-1] not in _REC_DVS):
+        raise NotImplementedError(f'the fused short conv needs dk in {_REC_DVS} and dv in {_REC_DVS} (or dv = 256 '
+                                  f'for a one-token step from a state); got dk={q.shape[-1]}, dv={dv}')
+    if epilogue is not None and dv not in _REC_DVS and not wide_step:
         # the fused epilogue needs the kernel's whole, unpadded dv row: apply it as its own pass
         o, S = _recurrent(q, k, v, g, beta, gate=gate, delta=delta, scale=scale, initial_state=initial_state,
                           output_final_state=output_final_state, cu_seqlens=cu_seqlens,
                           inplace_final_state=inplace_final_state, fusion=fusion)
         return _norm_gate(o, epilogue), S
-    if dv > max(_REC_DVS):
+    if dv > max(_REC_DVS) and not wide_step:
         # the recurrence is column-separable: independent 128-wide column blocks
         outs, states = [], []
         want_S = output_final_state or (inplace_final_state and initial_state is not None)
@@ -900,8 +907,9 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
             S = initial_state
         return torch.cat(outs, -1), S
     # with w the delta rule's strength is in w: no beta is validated or passed
+    dvs = _DEC_DVS if wide_step else _REC_DVS
     c = _Call(q, k, v, g, None if w is not None else beta, initial_state, cu_seqlens, gate=gate,
-              delta=delta and w is None, dv_to=lambda d: next(x for x in _REC_DVS if x >= d), fusion=fusion)
+              delta=delta and w is None, dv_to=lambda d: next(x for x in dvs if x >= d), fusion=fusion)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     o = c.new_output()
     in_place = (inplace_final_state and initial_state is not None and not c.padded
@@ -1041,7 +1049,8 @@ def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = T
     gate activation with gate_in_kernel (g is then the pre-activation), the
     recurrence from `state`, which it updates in place (:945-950), and with
     out_gate / out_norm_weight the RMSNorm x SiLU(gate) epilogue (:814-825).
-    Returns o (B, L, H, dv) in q's dtype.  dk, dv in {64, 128}."""
+    Returns o (B, L, H, dv) in q's dtype.  dk, dv in {64, 128}; dv = 256 for
+    a one-token step (L = 1, no cu_seqlens) with the four-tap conv."""
     B, L = qp.shape[0], qp.shape[1]
     H = state.shape[1]
     dk, dv = state.shape[2], state.shape[3]
