@@ -481,6 +481,16 @@ def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
     w_us = _event_us(torch, lambda i: ops.chunk_write_bwd(x.q, x.k, x.v, wv, x.g, x.initial_state, do, dST,
                                                           scale=scale), steps, warmup)
     del wv
+    # the reference's HAX1 / HAX2 training setting: chunk_kda with chunk_size=32 through autograd
+    # (the per-channel backward runs 64-token chunks), forward and backward together
+    leaves = [t.detach().clone().requires_grad_(True) for t in (x.q, x.k, x.v, x.g, x.beta)]
+
+    def c32_pair(i):
+        o, S = ops.chunk_kda(*leaves, scale=scale, initial_state=None, output_final_state=True, chunk_size=32)
+        torch.autograd.backward([o, S], [do, dST])
+
+    c32_us = _event_us(torch, c32_pair, steps, warmup)
+    del leaves
     walk_us = None
     if token_walk:
         walk_us = _event_us(torch, lambda i: ops.scan_bwd(x.q, x.k, x.v, x.g, x.beta, x.initial_state, do, dST,
@@ -498,6 +508,8 @@ def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
          'train_pair_us': round(pair_us, 1),
          'train_pair': 'vgdr_chunk_fwd_saving + vgdr_chunk_bwd_saved (what autograd runs for 16-bit inputs)',
          'train_pair_tflops': round(th * 3 * FLOP_PER_TOKEN_HEAD / (pair_us * 1e-6) / 1e12, 2),
+         'c32_autograd_pair_us': round(c32_us, 1),
+         'c32_autograd_pair': 'chunk_kda(chunk_size=32) forward + autograd backward (the 64-token chunked backward)',
          'w_us': round(w_us, 1),
          'w': 'explicit write vectors (vgdr_chunk_bwd_w: the same kernels on chunk prep\'s WR blocks, dw for dbeta)',
          'nodelta_us': round(nodelta_us, 1),

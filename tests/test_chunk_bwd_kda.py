@@ -377,3 +377,58 @@ def test_write_chunk_bwd_varlen_and_full_size():
         err = _rel(a, b)
         print(f'[parity] w full size vs scan_bwd {name} rel_l2={err:.3e}', flush=True)
         assert err <= 2e-2, f'{name}: {err:.3e}'
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('dtype', [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize('strong', [False, True])
+def test_kda_autograd_in_32_token_chunks(dtype, strong):
+    """chunk_kda(..., chunk_size=32) under autograd (the reference's HAX1 / HAX2
+    training setting, recipe/model/hax1_340M.yaml:94) runs the chunked
+    per-channel backward in 64-token chunks (the gradient does not depend on
+    the blocking): every gradient against the fp64 recurrence's."""
+    B, T, H, dk, dv = 1, 150, 2, 128, 128
+    print(f'\n[case] kda autograd chunk_size=32 dtype={dtype} strong={strong}', flush=True)
+    q, k, v, g, beta, S0, do, dST = _inputs(B, T, H, dk, dv, dtype, seed=91 + strong, strong=strong)
+    scale = dk ** -0.5
+    ref = gdr.recurrent_grads(q, k, v, g, beta, S0, do, dST, scale=scale)
+    leaves = [x.cuda().requires_grad_(True) for x in (q, k, v, g, beta, S0)]
+    o, S = ops.chunk_kda(*leaves[:5], scale=scale, initial_state=leaves[5], output_final_state=True, chunk_size=32)
+    torch.autograd.backward([o, S], [do.cuda(), dST.cuda()])
+    _compare(tuple(x.grad for x in leaves), ref, 2e-2, f'kda C=32 {dtype} strong={strong}')
+
+
+@pytest.mark.gpu
+def test_write_and_plain_autograd_in_32_token_chunks():
+    """chunk_scan_vec with explicit write vectors and without the delta rule,
+    chunk_size=32, under autograd: the 64-token chunked backwards, against the
+    oracle's gradients."""
+    B, T, H, dk, dv = 1, 90, 2, 64, 64
+    q, k, v, g, beta, S0, do, dST = _inputs(B, T, H, dk, dv, torch.bfloat16, seed=93)
+    gen = torch.Generator().manual_seed(94)
+    w = (0.5 * F.normalize(torch.randn(B, T, H, dk, generator=gen), dim=-1)).bfloat16()
+    print('\n[case] chunk_scan_vec w autograd chunk_size=32', flush=True)
+    ref = gdr.recurrent_grads(q, k, v, g, None, S0, do, dST, scale=0.2, w=w)
+    leaves = [x.cuda().requires_grad_(True) for x in (q, k, v, g, S0, w)]
+    o, S = ops.chunk_scan_vec(leaves[0], leaves[1], leaves[2], leaves[3], None, leaves[4], scale=0.2, delta=True,
+                              chunk_size=32, w=leaves[5])
+    torch.autograd.backward([o, S], [do.cuda(), dST.cuda()])
+    got = tuple(x.grad for x in leaves)
+    names = ('dq', 'dk', 'dv', 'dg', 'dS0', 'dw')
+    refm = dict(zip(('dq', 'dk', 'dv', 'dg', 'dbeta', 'dS0', 'dw'), ref)) if len(ref) == 7 else None
+    assert refm is not None, len(ref)
+    for n, a in zip(names, got):
+        e = _rel(a, refm[n])
+        print(f'[parity] w C=32 {n} rel_l2={e:.3e}', flush=True)
+        assert e <= 2e-2, (n, e)
+    print('\n[case] chunk_simple_gla-like per-channel, no delta rule, chunk_size=32', flush=True)
+    ref = gdr.recurrent_grads(q, k, v, g, None, S0, do, dST, scale=0.2, delta=False)
+    leaves = [x.cuda().requires_grad_(True) for x in (q, k, v, g, S0)]
+    o, S = ops.chunk_scan_vec(leaves[0], leaves[1], leaves[2], leaves[3], None, leaves[4], scale=0.2, delta=False,
+                              chunk_size=32)
+    torch.autograd.backward([o, S], [do.cuda(), dST.cuda()])
+    for n, a, r in zip(('dq', 'dk', 'dv', 'dg', 'dS0'), (x.grad for x in leaves),
+                       (ref[0], ref[1], ref[2], ref[3], ref[5])):
+        e = _rel(a, r)
+        print(f'[parity] nodelta C=32 {n} rel_l2={e:.3e}', flush=True)
+        assert e <= 2e-2, (n, e)

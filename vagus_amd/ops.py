@@ -287,11 +287,26 @@ def _gate_of(g):
     return 'none' if g is None else ('vector' if g.dim() == 4 else 'scalar')
 
 
+# The per-channel-gate chunked backward runs 64-token chunks (its gradient
+# kernel holds a chunk's gated products in LDS at that size).  The chunk size
+# is a blocking choice, not part of the function: a per-channel 16-bit call
+# asked for 32-token chunks under autograd runs the forward it saves for the
+# backward, and the backward, in 64-token chunks (the reference's HAX1 / HAX2
+# recipes train KDA with chunk_size 32, recipe/model/hax1_340M.yaml:94).
+_VEC_BWD_CHUNK = 64
+
+
 def _chunk_bwd_covers(q, g, chunk_size):
     """Whether vgdr_chunk_bwd takes this delta-rule call: a scalar gate or
-    none at any dtype, a per-channel gate with 16-bit q, k, v in 64-token
-    chunks (the token-recurrence backward takes the rest)."""
-    return g is None or g.dim() == 3 or (q.dtype != torch.float32 and chunk_size > 32)
+    none at any dtype, a per-channel gate with 16-bit q, k, v (in 64-token
+    chunks whatever chunk_size asks; the token-recurrence backward takes
+    fp32 per-channel calls)."""
+    return g is None or g.dim() == 3 or q.dtype != torch.float32
+
+
+def _bwd_chunk(q, g, chunk_size):
+    """The chunk size the chunked backward (and a saving forward) runs."""
+    return _VEC_BWD_CHUNK if (g is not None and g.dim() == 4 and q.dtype != torch.float32) else chunk_size
 
 
 def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *, scale=None, cu_seqlens=None,
@@ -300,8 +315,8 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     (vgdr_chunk_bwd): the gradients of (o, final_state) under the cotangents
     do (and dht, None = zero) with respect to q, k, v, g, beta and
     initial_state, for the delta rule with a scalar gate (g (B, T, H)), a
-    per-channel gate (g (B, T, H, dk); 16-bit q, k, v, 64-token chunks) or
-    none (g None).  q, k as the forward scanned them (normalised), beta in
+    per-channel gate (g (B, T, H, dk); 16-bit q, k, v, run in 64-token chunks
+    whatever chunk_size asks) or none (g None).  q, k as the forward scanned them (normalised), beta in
     [0, 1], g the log-decay.  Returns (dq, dk, dv, dg, dbeta, dh0) in the
     inputs' dtypes; dg is None without a gate and dh0 None without an initial
     state.  The gradients the reference's training takes through chunk_scan /
@@ -332,6 +347,7 @@ def chunk_gated_delta_rule_bwd(q, k, v, g, beta, initial_state, do, dht=None, *,
     dq, dk = new(c.B, c.T, c.H, c.dkp, dt=c.dtype), new(c.B, c.T, c.H, c.dkp, dt=c.dtype)
     dv = new(c.B, c.T, c.H, c.dvp, dt=c.dtype)
     vec = c.gate_kind == _lib.VGDR_GATE_VECTOR
+    chunk_size = _bwd_chunk(q, g, chunk_size)
     dg = None if g is None else (new(c.B, c.T, c.H, c.dkp) if vec else new(c.B, c.T, c.H))
     db = new(c.B, c.T, c.H) if delta else None
     dS0 = new(c.N, c.H, c.dkp, c.dvp) if initial_state is not None else None
@@ -386,6 +402,7 @@ def _chunk_fwd_saving(q, k, v, g, beta, initial_state, *, scale, cu_seqlens, chu
     final_state, workspace)."""
     c = _Call(q, k, v, g, beta, initial_state, cu_seqlens, gate=_gate_of(g), delta=True,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV, fusion=fusion)
+    chunk_size = _bwd_chunk(q, g, chunk_size)                  # the backward's blocking
     o, S = c.new_output(), c.new_state()
     L = _lib.load()
     dtype = _DTYPES[c.dtype]
@@ -503,6 +520,7 @@ class _ChunkDeltaRule(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, g, beta, S0, A_log, dt_bias, scale, cu, chunk_size, fusion):
         ctx.ws = None
+        chunk_size = _bwd_chunk(q, g, chunk_size)
         if q.dtype != torch.float32:
             o, S, ctx.ws = _chunk_fwd_saving(q, k, v, g, beta, S0, scale=scale, cu_seqlens=cu,
                                              chunk_size=chunk_size, fusion=fusion)
@@ -551,7 +569,8 @@ class _ChunkPlain(torch.autograd.Function):
         if do is None:
             do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
         dq, dk, dv, dg, _, dS0 = chunk_gated_delta_rule_bwd(q, k, v, g, None, S0, do, dS, scale=ctx.scale,
-                                                            cu_seqlens=cu, chunk_size=ctx.chunk_size, delta=False)
+                                                            cu_seqlens=cu, chunk_size=_bwd_chunk(q, g, ctx.chunk_size),
+                                                            delta=False)
         return dq, dk, dv, dg, dS0, None, None, None
 
 
@@ -1127,11 +1146,12 @@ def causal_conv1d(x, weight, bias=None, residual=None, initial_state=None, outpu
 def chunk_write_bwd(q, k, v, w, g, initial_state, do, dht=None, *, scale=None, cu_seqlens=None, chunk_size=64):
     """Backward of chunk_scan_vec with explicit write vectors w (B, T, H, dk)
     without autograd (vgdr_chunk_bwd_w; 16-bit q, k, v, w, per-channel g,
-    64-token chunks): the gradients of (o, final_state) under do (and dht,
-    None = zero).  Returns (dq, dk, dv, dw, dg, dh0), dh0 None without an
-    initial state."""
+    run in 64-token chunks whatever chunk_size asks): the gradients of (o,
+    final_state) under do (and dht, None = zero).  Returns (dq, dk, dv, dw,
+    dg, dh0), dh0 None without an initial state."""
     c = _Call(q, k, v, g, None, initial_state, cu_seqlens, gate='vector', delta=False,
               dv_to=lambda d: -(-d // _CHUNK_TILE_DV) * _CHUNK_TILE_DV)
+    chunk_size = _VEC_BWD_CHUNK
     scale = c.dk ** -0.5 if scale is None else float(scale)
     assert w.shape == q.shape, f'w must be {tuple(q.shape)} (B, T, H, dk); got {tuple(w.shape)}'
     assert do.shape == (c.B, c.T, c.H, c.dv), f'do must be {(c.B, c.T, c.H, c.dv)}, got {tuple(do.shape)}'
@@ -1167,7 +1187,7 @@ class _ChunkWrite(torch.autograd.Function):
     """chunk_scan_vec with explicit write vectors, differentiable: forward
     vgdr_chunk_fwd_w, backward vgdr_chunk_bwd_w (the per-channel chunk
     backward on chunk prep's WR blocks, which it rebuilds with the entry
-    states).  16-bit q, k, v, w, per-channel g, 64-token chunks."""
+    states, in 64-token chunks).  16-bit q, k, v, w, per-channel g."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, S0, w, scale, cu, chunk_size):
@@ -1183,7 +1203,7 @@ class _ChunkWrite(torch.autograd.Function):
         if do is None:
             do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
         dq, dk, dv, dw, dg, dS0 = chunk_write_bwd(q, k, v, w, g, S0, do, dS, scale=ctx.scale, cu_seqlens=cu,
-                                                  chunk_size=ctx.chunk_size)
+                                                  chunk_size=_VEC_BWD_CHUNK)
         return dq, dk, dv, dg, dS0, dw, None, None, None
 
 
@@ -1198,12 +1218,12 @@ def chunk_scan_vec(q, k, v, g, beta, S0, *, scale: float, delta: bool, chunk_siz
     beta unused), run chunkwise with 16-bit q, k, v and token by token (the
     same rule, vgdr_recurrent_fwd_w) in fp32.  Without w it is chunk_kda.
     Differentiable when an input requires grad: with w, vgdr_chunk_bwd_w for
-    16-bit inputs in 64-token chunks, vgdr_scan_bwd otherwise."""
+    16-bit inputs (in 64-token chunks), vgdr_scan_bwd for fp32."""
     B, T, H, dk = q.shape
     if w is not None and _wants_grad(q, k, v, g, beta, S0, w):
         assert delta, 'an explicit write vector needs the delta rule'
         scale = dk ** -0.5 if scale is None else float(scale)
-        if q.dtype == torch.float32 or chunk_size <= 32:
+        if q.dtype == torch.float32:
             return _ScanRule.apply(q, k, v, g, None, S0, w, scale, cu_seqlens, chunk_size, True)
     if g is None:
         g = torch.zeros(B, T, H, dk, dtype=torch.float32, device=q.device)
