@@ -637,6 +637,261 @@ def write_traffic(run_dir):
     print(json.dumps(out))
 
 
+# ---------------------------------------------------------------------------
+# GEMM-phase MFMA utilisation (bench.py --gemm-phase): an instrumented copy of
+# gdr_chunk.hip, built in a temporary directory from the current sources,
+# stamps s_memtime around the state kernel's product stages for eight
+# workgroups: the chain wave's P = K S stage (16 MFMAs, up to X), its TE X
+# stage (6, up to the bf16 W), its state update (16, up to a read of S), and
+# the first output wave's products (22 with 32-column tiles, 11 with 16).
+# Empty asm statements pin each stage's operands after its first stamp and
+# consume its results before its last, so the products cannot move across the
+# stamps.  A stage's MFMA utilisation is (its MFMAs x 16 cycles) over its
+# duration: at the bf16 peak (2.5 PFLOP/s over 1024 SIMDs at 2.4 GHz, 1017
+# FLOP per SIMD-cycle) a 16x16x32 MFMA (16,384 FLOP) issues every 16 cycles;
+# a calibration kernel's dependent chain (one MFMA per 15.9 cycles of the same
+# counter) agrees.
+# ---------------------------------------------------------------------------
+PROBE_PATCHES = [
+    ("namespace vgdr {", """namespace vgdr {
+constexpr int GP_WG = 8, GP_STEPS = 128;
+__device__ unsigned long long g_gp[GP_WG][GP_STEPS][8];
+__device__ __forceinline__ int gp_slot(int b) {
+    const int ids[GP_WG] = {0, 1, 37, 66, 101, 130, 199, 255};
+#pragma unroll
+    for (int i = 0; i < GP_WG; ++i) if (b == ids[i]) return i;
+    return -1;
+}
+__device__ __forceinline__ unsigned long long gp_time() {
+    __builtin_amdgcn_sched_barrier(0);
+    const unsigned long long t = __builtin_amdgcn_s_memtime();
+    __builtin_amdgcn_sched_barrier(0);
+    return t;
+}
+__global__ void gp_calib_kernel(unsigned long long *out) {
+    typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+    b8 a, b;
+    for (int i = 0; i < 8; ++i) { a[i] = (__bf16)(0.001f * (threadIdx.x + i)); b[i] = (__bf16)(0.002f * i); }
+    f32x4 acc[8];
+    for (int j = 0; j < 8; ++j) acc[j] = f32x4{(float)j, 0.5f * j, 0.25f * j + threadIdx.x, 1.f + j};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(acc[j]));
+    const unsigned long long t0 = gp_time();
+    asm volatile("" : "+v"(a), "+v"(b));
+#pragma unroll
+    for (int r = 0; r < 64; ++r)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[j], 0, 0, 0);
+    float s = 0.f;
+    for (int j = 0; j < 8; ++j) s += acc[j][0];
+    asm volatile("" :: "v"(s));
+    const unsigned long long t1 = gp_time();
+    asm volatile("" : "+v"(a), "+v"(b));
+    f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 64; ++r) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, d, 0, 0, 0);
+    asm volatile("" :: "v"(d[0]));
+    const unsigned long long t2 = gp_time();
+    if (threadIdx.x == 0) { out[0] = t1 - t0; out[1] = t2 - t1; }
+}
+}  // namespace vgdr
+extern "C" int vgdr_probe_read(void *dst, long long n) {
+    return (int)hipMemcpyFromSymbol(dst, HIP_SYMBOL(vgdr::g_gp), (size_t)n, 0, hipMemcpyDeviceToHost);
+}
+extern "C" int vgdr_probe_clear() {
+    static unsigned long long z[vgdr::GP_WG][vgdr::GP_STEPS][8];
+    return (int)hipMemcpyToSymbol(HIP_SYMBOL(vgdr::g_gp), z, sizeof(z), 0, hipMemcpyHostToDevice);
+}
+extern "C" int vgdr_probe_calib(void *dst) {
+    unsigned long long *d = nullptr;
+    if (hipMalloc(&d, 16) != hipSuccess) return 1;
+    hipLaunchKernelGGL(vgdr::gp_calib_kernel, dim3(1), dim3(64), 0, 0, d);
+    hipError_t e = hipMemcpy(dst, d, 16, hipMemcpyDeviceToHost);
+    hipFree(d);
+    return (int)e;
+}
+namespace vgdr {"""),
+    ("""            f32x4 U[NB];
+            if constexpr (DELTA) {
+                // P = K S (C layout), NB independent accumulation chains""", """            f32x4 U[NB];
+            const int gps = gp_slot(blockIdx.x);
+            unsigned long long gt0 = 0, gt1 = 0, gt2 = 0, gt3 = 0;
+            gt0 = gp_time();
+#pragma unroll
+            for (int q = 0; q < NKB / 2; ++q) asm volatile("" : "+v"(Sb[q]));
+            if constexpr (DELTA) {
+                // P = K S (C layout), NB independent accumulation chains"""),
+    ("""#pragma unroll
+                for (int I = 0; I < NB; ++I) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};""", """#pragma unroll
+                for (int q = 0; q < NB / 2; ++q) asm volatile("" :: "v"(Xb[q]));
+                gt1 = gp_time();
+#pragma unroll
+                for (int q = 0; q < NB / 2; ++q) asm volatile("" : "+v"(Xb[q]));
+#pragma unroll
+                for (int I = 0; I < NB; ++I) {
+                    f32x4 acc = {0.f, 0.f, 0.f, 0.f};"""),
+    ("""            // S <- Gc S + (K*Gend)^T U~
+            if constexpr (VEC) {""", """#pragma unroll
+            for (int q = 0; q < NB / 2; ++q) asm volatile("" :: "v"(Wb[q]));
+            gt2 = gp_time();
+#pragma unroll
+            for (int q = 0; q < NB / 2; ++q) asm volatile("" : "+v"(Wb[q]));
+            // S <- Gc S + (K*Gend)^T U~
+            if constexpr (VEC) {"""),
+    ("""                                                    Ktr + (32 * q + 16) * PK + KQ::col(16 * kt)), Wb[q], S[kt]);
+        }
+        if (nchunks > 0) lds_barrier();                       // barrier n""", """                                                    Ktr + (32 * q + 16) * PK + KQ::col(16 * kt)), Wb[q], S[kt]);
+            {
+                float tmp = 0.f;
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt) tmp += S[kt][0];
+                asm volatile("" :: "v"(tmp));
+            }
+            gt3 = gp_time();
+            if (gps >= 0 && wave == 0 && lane == 0 && c < GP_STEPS) {
+                g_gp[gps][c][0] = gt0; g_gp[gps][c][1] = gt1; g_gp[gps][c][2] = gt2; g_gp[gps][c][3] = gt3;
+            }
+        }
+        if (nchunks > 0) lds_barrier();                       // barrier n"""),
+    ("""        unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] = f32x4{0.f, 0.f, 0.f, 0.f}; }); });""",
+     """        unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] = f32x4{0.f, 0.f, 0.f, 0.f}; }); });
+        const unsigned long long ot0 = gp_time();
+#pragma unroll
+        for (int s = 0; s < NW; ++s)
+#pragma unroll
+            for (int k = 0; k < NKB / 2; ++k) asm volatile("" : "+v"(Sn[s][k]));"""),
+    ("""        // the chunk's o rows as one buffer: rows past the sequence's end fall
+        // outside it and their stores are dropped, with no lane-dependent branch""", """        {
+            float tmp = 0.f;
+            unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { tmp += ot[s][i][0]; }); });
+            asm volatile("" :: "v"(tmp));
+        }
+        const unsigned long long ot1 = gp_time();
+        {
+            const int gps = gp_slot(blockIdx.x);
+            if (gps >= 0 && o == 0 && lane == 0 && c < GP_STEPS) { g_gp[gps][c][4] = ot0; g_gp[gps][c][5] = ot1; }
+        }
+        // the chunk's o rows as one buffer: rows past the sequence's end fall
+        // outside it and their stores are dropped, with no lane-dependent branch"""),
+    ("""    if (dtype == 1) {
+        if (dk == 64) { if (chunk == 32) { VGDR_GATES(64, 32, __bf16) } VGDR_GATES(64, 64, __bf16) }""",
+     """    if (dtype == 1 && dk == 128 && chunk == 64) { VGDR_GATES(128, 64, __bf16) }
+    return hipErrorInvalidValue;
+    if (dtype == 1) {
+        if (dk == 64) { if (chunk == 32) { VGDR_GATES(64, 32, __bf16) } VGDR_GATES(64, 64, __bf16) }"""),
+]
+
+
+def build_phase_probe(outdir):
+    """The instrumented library: gdr_chunk.hip with PROBE_PATCHES applied (each
+    anchor must occur once in the current source), written to outdir beside
+    copies of the headers, and the other sources as they are, compiled with
+    the library's flags.  Returns the library path."""
+    import concurrent.futures as cf
+    import shutil
+    import subprocess
+    from vagus_amd import build as b
+    os.makedirs(outdir, exist_ok=True)
+    for f in os.listdir(b.CSRC):
+        if f.endswith('.hpp'):
+            shutil.copy(os.path.join(b.CSRC, f), os.path.join(outdir, f))
+    path = os.path.join(outdir, 'gdr_chunk.hip')
+    src = open(os.path.join(b.CSRC, 'gdr_chunk.hip')).read()
+    for anchor, repl in PROBE_PATCHES:
+        assert src.count(anchor) == 1, f'probe anchor not found once: {anchor[:60]!r}'
+        src = src.replace(anchor, repl)
+    open(path, 'w').write(src)
+    # the instrumented file from outdir (beside the headers), every other file from the package
+    srcs = [path] + [s for s in b.sources() if os.path.basename(s) != 'gdr_chunk.hip']
+    objs = [os.path.join(outdir, os.path.basename(s)[:-4] + '.o') for s in srcs]
+
+    def comp(so):
+        r = subprocess.run([b.hipcc(), *b.HIPCC_FLAGS, '-c', so[0], '-o', so[1]], capture_output=True, text=True)
+        if r.returncode:
+            raise RuntimeError(r.stdout + r.stderr)
+    with cf.ThreadPoolExecutor(len(srcs)) as ex:
+        list(ex.map(comp, zip(srcs, objs)))
+    lib = os.path.join(outdir, 'libphaseprobe.so')
+    r = subprocess.run([b.hipcc(), f'--offload-arch={b.ARCH}', '-shared', '-fPIC', *objs, '-o', lib],
+                       capture_output=True, text=True)
+    if r.returncode:
+        raise RuntimeError(r.stdout + r.stderr)
+    return lib
+
+
+def gemm_phase(torch, workloads, lib_path, name):
+    """Per-stage MFMA utilisation of the instrumented state kernel on `name`
+    (gdn_340m or kda_prefill): stage medians in cycles of the s_memtime
+    counter and the utilisation of every traced stage summed."""
+    import ctypes
+    import numpy as np
+    from vagus_amd import _lib, ops
+    lib = _lib.load(lib_path)
+    for fn in ('vgdr_probe_read', 'vgdr_probe_calib'):
+        getattr(lib, fn).argtypes = [ctypes.c_void_p, ctypes.c_longlong][:1 + (fn == 'vgdr_probe_read')]
+    prev, _lib._lib = _lib._lib, lib
+    try:
+        xs = [workloads.workload(name, device='cuda') for _ in range(3)]
+        gate = 'vector' if xs[0].g.dim() == 4 else 'scalar'
+
+        def run(i, ev=None):
+            x = xs[i % 3]
+            return ops.chunk_scan(x.q, x.k, x.v, x.g, x.beta, gate=gate, delta=True, initial_state=x.initial_state,
+                                  output_final_state=True, cu_seqlens=x.cu_seqlens, phase_event=ev)
+        for i in range(200):
+            run(i)
+        torch.cuda.synchronize()
+        cal = (ctypes.c_ulonglong * 2)()
+        assert lib.vgdr_probe_calib(ctypes.addressof(cal)) == 0
+        st = torch.cuda.current_stream()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(50)]
+        for i in range(50):
+            run(i, ev[i][0])
+            ev[i][1].record(st)
+        torch.cuda.synchronize()
+        state_us = statistics.mean(a.elapsed_time(b) for a, b in ev) * 1e3
+        lib.vgdr_probe_clear()
+        run(0)
+        torch.cuda.synchronize()
+        buf = (ctypes.c_ulonglong * (8 * 128 * 8))()
+        assert lib.vgdr_probe_read(ctypes.addressof(buf), ctypes.sizeof(buf)) == 0
+    finally:
+        _lib._lib = prev
+    a = np.frombuffer(buf, dtype=np.uint64).reshape(8, 128, 8).astype(np.int64)
+    nsteps = xs[0].q.shape[1] // CHUNK
+    a = a[:, :nsteps]
+    ok = (a[:, :, 0] > 0) & (a[:, :, 3] > a[:, :, 0]) & (a[:, :, 5] > a[:, :, 4])
+    p_st, te_st = (a[:, :, 1] - a[:, :, 0])[ok], (a[:, :, 2] - a[:, :, 1])[ok]
+    up_st, ch = (a[:, :, 3] - a[:, :, 2])[ok], (a[:, :, 3] - a[:, :, 0])[ok]
+    out = (a[:, :, 5] - a[:, :, 4])[ok]
+    step = np.diff(a[:, :, 0], axis=1)[:, 1:-1]
+    n = int(ok.sum())
+    n_chain, n_out = 38, (22 if gate == 'scalar' else 11)      # 32-column tiles (gdn_340m) or 16 (kda_prefill)
+    c = 16.0
+    frac = lambda m, d: round(m * c * n / float(d.sum()), 4)
+    return {'workload': name, 'instrumented_state_us': round(state_us, 1), 'samples': n,
+            'calib_cycles_independent_mfma': round(cal[0] / 512.0, 2), 'calib_cycles_dependent_mfma': round(cal[1] / 64.0, 2),
+            'chain_step_cycles': float(np.median(step)),
+            'chain_P_cycles': float(np.median(p_st)), 'chain_TE_cycles': float(np.median(te_st)),
+            'chain_update_cycles': float(np.median(up_st)), 'output_cycles': float(np.median(out)),
+            'chain_P_frac': frac(16, p_st), 'chain_TE_frac': frac(6, te_st), 'chain_update_frac': frac(16, up_st),
+            'chain_frac': frac(n_chain, ch), 'output_frac': frac(n_out, out),
+            'gemm_phase_frac': round((n_chain + n_out) * c * n / float(ch.sum() + out.sum()), 4),
+            'chain_phase_share_of_step': round(float(np.median(ch)) / float(np.median(step)), 4)}
+
+
+def measured_gemm_phase(workload):
+    """The committed GEMM-phase record (profiles/gemm_phase.json) for workload,
+    or None when it was measured on other kernel sources."""
+    try:
+        with open(os.path.join(ROOT, 'profiles', 'gemm_phase.json')) as f:
+            rec = json.load(f)[workload]
+        return rec if rec.get('sources_sha') == sources_sha('chunk_state') else None
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument('--gpus', type=int, default=1)
@@ -658,6 +913,11 @@ def main():
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='run only a plain 1 GiB device copy (x5): the reference point that scales '
                          'rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes')
+    ap.add_argument('--gemm-phase', action='store_true',
+                    help='build the instrumented state kernel (PROBE_PATCHES) and print the MFMA utilisation of its '
+                         'product stages on gdn_340m and kda_prefill; with --write-gemm-phase also write '
+                         'profiles/gemm_phase.json')
+    ap.add_argument('--write-gemm-phase', action='store_true', help=argparse.SUPPRESS)
     ap.add_argument('--write-traffic', metavar='RUN_DIR',
                     help='write profiles/traffic.json from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs '
                          '(see write_traffic) and exit; needs no GPU')
@@ -684,6 +944,17 @@ def main():
         print(json.dumps({'calibrate_copy_bytes': src.numel() * 4, 'launches': 5}), flush=True)
         return
 
+    if args.gemm_phase:
+        import tempfile
+        lib = build_phase_probe(tempfile.mkdtemp(prefix='vgdr_probe_'))
+        out = {}
+        for name in ('gdn_340m', 'kda_prefill'):
+            out[name] = dict(gemm_phase(torch, workloads, lib, name), sources_sha=sources_sha('chunk_state'))
+            print(json.dumps(out[name]), flush=True)
+        if args.write_gemm_phase:
+            with open(os.path.join(ROOT, 'profiles', 'gemm_phase.json'), 'w') as f:
+                json.dump(out, f, indent=1)
+        return
     if args.generate_only:
         print(json.dumps(bench_generate(torch, workloads)), flush=True)
         return
@@ -731,7 +1002,9 @@ def main():
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
             r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))
-            extra[name] = {'tok_s': round(r['tok_s'], 1), 'op_ms': round(r['op_ms'], 4),
+            gpn = measured_gemm_phase(name)
+            extra[name] = {'gemm_phase_frac': None if gpn is None else gpn['gemm_phase_frac'],
+                           'tok_s': round(r['tok_s'], 1), 'op_ms': round(r['op_ms'], 4),
                            'prep_ms': round(r['prep_ms'], 4), 'state_ms': round(r['state_ms'], 4),
                            'path_tflops': round(r['path_tflops'], 2),
                            'path_frac_mfma': round(r['path_tflops'] / PEAK_BF16_TFLOPS, 5),
@@ -743,6 +1016,7 @@ def main():
 
     tokens, H = pre['tokens'], pre['H']
     achieved = pre['state_tflops']
+    gp = measured_gemm_phase('gdn_340m')
     state_gbs = tokens * H * STATE_BYTES_PER_TOKEN_HEAD / (pre['state_ms'] * 1e-3) / 1e9
     path_gbs = tokens * H * PREFILL_BYTES_PER_TOKEN_HEAD / (pre['op_ms'] * 1e-3) / 1e9
     line = {
@@ -768,7 +1042,14 @@ def main():
                      'kernel': 'chunk_pipe_kernel', 'kernel_avg_ms': round(pre['state_ms'], 4),
                      'flop_per_launch': tokens * H * STATE_FLOP_PER_TOKEN_HEAD,
                      'algorithmic_bytes_per_launch': tokens * H * STATE_BYTES_PER_TOKEN_HEAD,
-                     'hbm_algorithmic_GBs': round(state_gbs, 1)},
+                     'hbm_algorithmic_GBs': round(state_gbs, 1),
+                     'gemm_phase_frac': None if gp is None else gp['gemm_phase_frac'],
+                     'gemm_phase': None if gp is None else
+                     {k: gp[k] for k in ('chain_frac', 'output_frac', 'chain_P_frac', 'chain_TE_frac',
+                                         'chain_update_frac', 'chain_phase_share_of_step')},
+                     'gemm_phase_method': 'MFMAs x 16 cycles over the s_memtime duration of the state kernel\'s '
+                                          'product stages (chain P, TE X, update; output products) in an '
+                                          'instrumented build (bench.py --gemm-phase, profiles/gemm_phase.json)'},
         'path': {'kernels': 'chunk_prep_kernel + chunk_pipe_kernel', 'op_ms': round(pre['op_ms'], 4),
                  'prep_ms': round(pre['prep_ms'], 4), 'state_ms': round(pre['state_ms'], 4),
                  'achieved_tflops': round(pre['path_tflops'], 2),
