@@ -453,7 +453,9 @@ int vgdr_recurrent_fwd_w(int dtype, int gate_kind,
  * conv + SiLU (advancing its caches), then the producer fusions (the q, k L2
  * norm, beta sigmoid, KDA gate activation), the recurrence from
  * initial_state, and with `epilogue` the RMSNorm x SiLU(gate) output.
- * dk, dv in {64, 128}. */
+ * dk, dv in {64, 128}; dv = 256 (dk 128 / dv 256 heads) for one token per
+ * sequence (T = 1, cu_seqlens NULL) from an initial_state with the four-tap
+ * conv and 16-byte aligned conv weights, else VGDR_ERR_UNSUPPORTED. */
 int vgdr_decode_step(int dtype, int gate_kind, int use_delta,
                      const void *q, const void *k, const void *v,
                      const float *g, const float *beta,
