@@ -1089,6 +1089,46 @@ struct FlatCopy {
     }
 };
 
+// The TE block's tile pairs that can be nonzero (frag_pair_pos order, pair (I, q)
+// with 2 q <= I; the chain never reads the others): with four row blocks, six of
+// the eight pairs, 384 of the 512 16-byte units.  Unit n of the copy is unit n % 64
+// of the (n / 64)-th such pair.  A lane past the last unit reads through a buffer
+// resource at an offset outside it (no memory request, zeros) and stores nothing,
+// so every wave runs the same instructions without a branch around a load.
+template <int NB, int NPT>
+struct TECopy {
+    static constexpr int NPAIRS = NB * (NB / 2);                         // all tile pairs of the block
+    static constexpr int LIVE = NB == 4 ? 384 : 64 * NPAIRS;             // units of the pairs with 2 q <= I
+    static constexpr int PER = (LIVE + NPT - 1) / NPT;
+    static_assert(NB == 4 || NB == 2, "four or two row blocks");
+    u32x4 r[PER];
+    // byte offset of unit n within the block (n < LIVE)
+    __device__ static __forceinline__ uint32_t unit_off(int n) {
+        if constexpr (NB == 4) {
+            const int j = n >> 6;                                          // 0..5 -> pairs 0, 2, 4, 5, 6, 7
+            const int pair = j == 0 ? 0 : (j == 1 ? 2 : j + 2);
+            return (uint32_t)((pair * 64 + (n & 63)) * 16);
+        } else {
+            return (uint32_t)(n * 16);
+        }
+    }
+    __device__ __forceinline__ void load(const void *src, int pt) {
+        const __amdgpu_buffer_rsrc_t rs = buffer_rsrc(src, (uint32_t)(NPAIRS * 64 * 16));
+        unroll<PER>([&](auto i) {
+            const int n = pt + NPT * i;
+            const uint32_t off = (LIVE % NPT == 0 || n < LIVE) ? unit_off(n) : 0x80000000u;
+            r[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, (int)off, 0, 0));
+        });
+    }
+    __device__ __forceinline__ void store(void *lds, int pt) const {
+        unroll<PER>([&](auto i) {
+            const int n = pt + NPT * i;
+            if (LIVE % NPT == 0 || n < LIVE)
+                *reinterpret_cast<u32x4 *>(reinterpret_cast<char *>(lds) + unit_off(n)) = r[i];
+        });
+    }
+};
+
 template <typename E>
 __device__ __forceinline__ typename Elem<E>::frag2 ld_pair(const E *p) {
     return *reinterpret_cast<const typename Elem<E>::frag2 *>(p);
@@ -1198,7 +1238,7 @@ chunk_pipe_kernel(const ChunkParams p) {
         struct Staged {
             CK k, e;
             CV v;
-            FlatCopy<TEB / 16, NPT> t;
+            TECopy<NB, NPT> t;
             FlatCopy<FB / 16, NPT> f;
         };
         struct Plans {
