@@ -1129,6 +1129,43 @@ struct TECopy {
     }
 };
 
+// Q rows (VEC: the scaled Q*G tile) for the output waves.  The global units are
+// the K copy's (its Plan: sixteen consecutive lanes read one whole row, so each
+// load instruction covers whole cache lines; loading the MFMA operand straight
+// from global memory spread every instruction over sixteen rows, 64 bytes
+// each, which measured 4 % slower on the whole state kernel).  In LDS the rows
+// are unpadded and 16-byte unit u of row r sits at unit u ^ qswz(r): the output
+// waves' operand reads (one unit of each of sixteen rows per lane group) then
+// hit distinct banks.
+template <int DK>
+__device__ __forceinline__ int qswz(int row) {
+    if constexpr (DK == 128) return row & 15;
+    else return (row ^ (row >> 3)) & 7;                      // DK = 64: two rows per 256 bytes
+}
+template <typename E, int CH, int DK, int NPT>
+struct QCopy {
+    static_assert(DK == 128 || DK == 64, "key dims 64 and 128");
+    static constexpr int UPR = DK / 8, UNITS = CH * UPR;
+    static constexpr int PER = (UNITS + NPT - 1) / NPT;
+    u32x4 r[PER];
+    template <typename Plan>
+    __device__ __forceinline__ void load(const E *src, const Plan &pl, int valid_rows) {
+        unroll<PER>([&](auto i) {
+            const bool ok = (pl.exists & pl.cols) >> (int)i & 1u && pl.row[i] < valid_rows;
+            r[i] = *reinterpret_cast<const u32x4 *>(src + (ok ? pl.goff[i] : 0));
+        });
+    }
+    __device__ __forceinline__ void store(E *lds, int pt) const {
+        unroll<PER>([&](auto i) {
+            const int u = pt + NPT * i;
+            if (UNITS % NPT == 0 || u < UNITS) {
+                const int row = u / UPR, cu = u % UPR;
+                *reinterpret_cast<u32x4 *>(lds + row * DK + 8 * (cu ^ qswz<DK>(row))) = r[i];
+            }
+        });
+    }
+};
+
 template <typename E>
 __device__ __forceinline__ typename Elem<E>::frag2 ld_pair(const E *p) {
     return *reinterpret_cast<const typename Elem<E>::frag2 *>(p);
@@ -1154,13 +1191,16 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 //                                  S <- Gc S + (GE K)^T U~  (per-channel gate: K*G,
 //                                  K*Gend tiles and Gc per key channel).  For each
 //                                  chunk it leaves S_c (element type) and U~_c in LDS.
-//   output waves  NW .. 2 NW - 1   wave NW + w computes chunk c's O^T = S_c^T (GO Q)^T
-//                                  + U~_c^T A^T for the same columns while the chain
-//                                  runs chunk c + 1.  Q (or scale Q*G) and A come from
-//                                  global memory straight into registers, issued before
-//                                  the hand-over barrier and consumed after it.
-//   producers     2 NW ..          copy chunk c + 1's K (K*G and K*Gend), V, TE and gate
-//                                  factors into the idle half of the double buffer.
+//   output waves  NW, NW + 1       compute chunk c's O^T = S_c^T (GO Q)^T + U~_c^T A^T
+//                                  for all NW column strips, half the token blocks
+//                                  each, while the chain runs chunk c + 1.  A comes
+//                                  from global memory straight into registers, issued
+//                                  two hand-overs before it is used; Q (or scale Q*G)
+//                                  from LDS (four producer waves) or, like A, from
+//                                  global memory (two).
+//   producers     NW + 2 ..        copy chunk c + 1's K (K*G and K*Gend), V, TE and gate
+//                                  factors into the idle half of the double buffer,
+//                                  and chunk c's Q into its own double buffer.
 // The chain waves thus issue 38 of the 60 MFMAs per chunk and column strip, and
 // the output products run on the other SIMDs (waves w and NW + w sit on
 // different SIMDs of the CU whenever NW <= 2).
@@ -1169,12 +1209,13 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 // to the chain waves and hand-over buffer (b - 1) & 1 (chunk b - 1) to the output
 // waves; every role passes all n + 1 of them.  Writes to a hand-over buffer
 // (chain, during step c) and its reads (output, during step c + 1) are separated
-// by barrier c + 1, and the next write to it (step c + 2) by barrier c + 2.
+// by barrier c + 1, and the next write to it (step c + 2) by barrier c + 2.  The
+// same holds for Q slot c & 1: written during step c, read during step c + 1.
 //
 // Hand-over layout per chain wave and buffer:
 //   SH: the state in the element type, one row of DK + 8 elements per state
 //       column (natural key order), so the output wave reads eight consecutive
-//       keys per lane and its Q operand is a plain 16-byte load of a q row;
+//       keys per lane and its Q operand is eight consecutive keys of a q row;
 //   UH: U~ in the MFMA A-operand order the chain wave holds it (lane-to-lane).
 // HS: the output waves also store each chunk's entry state to p.hs
 // ([chunk slot, H] checkpoints in ckpt_pos order), for the chunked backward.
@@ -1195,6 +1236,11 @@ chunk_pipe_kernel(const ChunkParams p) {
     constexpr int FB = CB::FLOATS * 4;                           // bytes of the gate factors
     static_assert(NB % 2 == 0 && NKB % 2 == 0, "k-blocks are consumed in pairs");
     static_assert(TEB % 16 == 0 && FB % 16 == 0, "slots are copied in 16-byte units");
+    // Q through LDS (copied by the producers) when there are four producer waves;
+    // with two, their registers are full and the output waves load the Q operand
+    // straight from global memory (the whole-row loads and an LDS transpose in
+    // the output waves measured no faster there)
+    constexpr bool QL = NP >= 4;
 
     __shared__ __attribute__((aligned(16))) E K0[CH * PK];
     __shared__ __attribute__((aligned(16))) E K1[CH * PK];
@@ -1206,6 +1252,7 @@ chunk_pipe_kernel(const ChunkParams p) {
     __shared__ __attribute__((aligned(16))) char B1[TEB + FB];
     __shared__ __attribute__((aligned(16))) E SH[2 * NW * 16 * SP];
     __shared__ __attribute__((aligned(16))) E UH[2 * NW * (NB / 2) * 64 * 8];
+    __shared__ __attribute__((aligned(16))) E QS[QL ? 2 * CH * DK : 8];  // Q (VEC: Q*G), slot c & 1: chunk c
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int H = p.H, DV = p.DV;
@@ -1241,6 +1288,7 @@ chunk_pipe_kernel(const ChunkParams p) {
             TECopy<NB, NPT> t;
             FlatCopy<FB / 16, NPT> f;
         };
+        using CQ = QCopy<E, CH, DK, NPT>;
         struct Plans {
             typename CK::Plan k;
             typename CV::Plan v;
@@ -1272,12 +1320,28 @@ chunk_pipe_kernel(const ChunkParams p) {
             st.v.store((odd ? V1 : V0) + z, pl.v);
             if constexpr (VEC) st.e.store((odd ? KE1 : KE0) + z, pl.k);
         };
+        // Q of chunk c goes to Q slot c & 1 between barriers c and c + 1 (the output
+        // waves read it one step after the chain reads chunk c's K).  One register
+        // set, loaded one step ahead and issued before the next K loads, so that
+        // the wait for it leaves those in flight.
+        auto load_q = [&](CQ &qc, const Plans &pl, int c) __attribute__((always_inline)) {
+            c = c < nchunks ? c : nchunks - 1;
+            if constexpr (VEC) {
+                const char *bq = blocks + ((cbase + c) * H + h) * (int64_t)CB::BYTES;
+                qc.load(reinterpret_cast<const E *>(bq) + CB::TEA + CH * DK, pl.k, CH);
+            } else {
+                const int64_t tq = bos + (int64_t)c * CH;
+                qc.load(qg + tq * sqk, pl.k, (int)(eos - tq < CH ? eos - tq : CH));
+            }
+        };
         if (nchunks > 0) {
             const int pt = tid - 64 * (NW + 2);
             const Plans pl{CK::plan(VEC ? DK : sqk, DK, pt), CV::plan(sv, DV - col0, pt)};
             Staged s0, s1;
+            CQ qc;
             load(s0, pl, 0, pt);
             store(s0, pl, 0, 0, pt);
+            if constexpr (QL) load_q(qc, pl, 0);
             load(s1, pl, 1, pt);
             load(s0, pl, 2, pt);
             int c = 0;
@@ -1285,13 +1349,25 @@ chunk_pipe_kernel(const ChunkParams p) {
                 int z = opaque_s(0);
                 lds_barrier();                                // barrier c: chunk c in place, chunk c-1 consumed
                 store(s1, pl, c + 1, z, pt);                  // into the slot chunk c-1 used
+                if constexpr (QL) {
+                    qc.store(QS + z, pt);                     // Q of chunk c (even)
+                    load_q(qc, pl, c + 1);
+                }
                 load(s1, pl, c + 3, pt);
                 z = opaque_s(0);
                 lds_barrier();                                // barrier c + 1
                 store(s0, pl, c + 2, z, pt);
+                if constexpr (QL) {
+                    qc.store(QS + CH * DK + z, pt);           // Q of chunk c + 1 (odd)
+                    load_q(qc, pl, c + 2);
+                }
                 load(s0, pl, c + 4, pt);
             }
-            if (c < nchunks) lds_barrier();                   // barrier n - 1 (n odd)
+            if (c < nchunks) {                                // n odd: c = n - 1, even
+                const int z = opaque_s(0);
+                lds_barrier();                                // barrier n - 1
+                if constexpr (QL) qc.store(QS + z, pt);       // the last chunk's Q
+            }
             lds_barrier();                                    // barrier n: the last chunk's outputs
             __builtin_amdgcn_s_waitcnt(0);                    // no load left in flight at exit
         }
@@ -1440,7 +1516,7 @@ chunk_pipe_kernel(const ChunkParams p) {
     if (nchunks == 0) return;
     const int g4 = lane >> 4, r16 = lane & 15;
     struct Ops {
-        F2 q[NR][NKB / 2];                                     // Q rows 16 rb(i) + r, keys 32 k + 8 g .. + 7
+        F2 q[QL ? 1 : NR][NKB / 2];                            // !QL: Q rows 16 rb(i) + r, keys 32 k + 8 g .. + 7
         F2 a[NR][NB / 2];                                      // A tile pairs (rb(i), k), 2 k <= rb(i)
         float go[NR];
     };
@@ -1453,11 +1529,13 @@ chunk_pipe_kernel(const ChunkParams p) {
         const float *gof = reinterpret_cast<const float *>(bk + CB::GOFF) + CH;
         unroll<NR>([&](auto i) {
             const int I = rb(i), row = 16 * I + r16;
-            // rows past the end of the sequence read its last row (not stored)
-            const E *qrow;
-            if constexpr (VEC) qrow = reinterpret_cast<const E *>(bk) + CB::TEA + CH * DK + row * DK;
-            else qrow = qg + (t0 + (row < clen ? row : clen - 1)) * sqk;
-            unroll<NKB / 2>([&](auto k) { op.q[i][k] = *reinterpret_cast<const F2 *>(qrow + 32 * k + 8 * g4); });
+            if constexpr (!QL) {
+                // rows past the end of the sequence read its last row (not stored)
+                const E *qrow;
+                if constexpr (VEC) qrow = reinterpret_cast<const E *>(bk) + CB::TEA + CH * DK + row * DK;
+                else qrow = qg + (t0 + (row < clen ? row : clen - 1)) * sqk;
+                unroll<NKB / 2>([&](auto k) { op.q[i][k] = *reinterpret_cast<const F2 *>(qrow + 32 * k + 8 * g4); });
+            }
             unroll<NB / 2>([&](auto k) {
                 if (2 * k <= I) op.a[i][k] = *reinterpret_cast<const F2 *>(Ab + frag_pair_pos<NB>(I, k, lane));
             });
@@ -1472,7 +1550,20 @@ chunk_pipe_kernel(const ChunkParams p) {
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
         const bool odd = c & 1;
-        F2 Sn[NW][NKB / 2], Ub[NW][NB / 2];
+        F2 Sn[NW][NKB / 2], Ub[NW][NB / 2], Qv[NR][NKB / 2];
+        // Q rows 16 rb(i) + r, keys 32 k + 8 g .. + 7 (rows past the end of the
+        // sequence hold other rows' values; their outputs are not stored)
+        unroll<NR>([&](auto i) {
+            if constexpr (QL) {
+                const int row = 16 * rb(i) + r16;
+                const E *qs = QS + (odd ? CH * DK : 0) + z + row * DK;
+                unroll<NKB / 2>([&](auto k) {
+                    Qv[i][k] = *reinterpret_cast<const F2 *>(qs + 8 * ((4 * k + g4) ^ qswz<DK>(row)));
+                });
+            } else {
+                unroll<NKB / 2>([&](auto k) { Qv[i][k] = op.q[i][k]; });
+            }
+        });
         unroll<NW>([&](auto s) {
             const E *sh = SH + ((odd ? NW : 0) + s) * 16 * SP + z + r16 * SP;
             const E *uh = UH + ((odd ? NW : 0) + s) * (NB / 2) * 512 + z + 8 * lane;
@@ -1482,7 +1573,7 @@ chunk_pipe_kernel(const ChunkParams p) {
         f32x4 ot[NW][NR];
         unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] = f32x4{0.f, 0.f, 0.f, 0.f}; }); });
         unroll<NKB / 2>([&](auto k) {
-            unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] = mfma_pair(Sn[s][k], op.q[i][k], ot[s][i]); }); });
+            unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] = mfma_pair(Sn[s][k], Qv[i][k], ot[s][i]); }); });
         });
         if constexpr (!VEC)                                    // VEC: scale and G are in Q*G
             unroll<NW>([&](auto s) { unroll<NR>([&](auto i) { ot[s][i] *= op.go[i]; }); });
