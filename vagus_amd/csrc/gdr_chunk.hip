@@ -193,9 +193,21 @@ __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 template <int DK, int CH, typename E, int GATE, bool WR = false>
 struct PrepLayout {
     static constexpr int PF = CH + 4, PG = DK + 4;
-    static constexpr int STAGE = (WR ? 3 : 2) * CH * DK * (int)sizeof(E);    // K, Q (and W) rows (swizzled)
-    static constexpr int SOLVE = 2 * CH * PF * 4;                  // M, T (reuse the stage)
-    static constexpr int UNION = cmax(STAGE, SOLVE);
+    static constexpr int NL = (CH / 16) * (CH / 16 + 1) / 2;      // lower tile pairs
+    // Per-channel gate: Q rows are not staged and the cumulative decay sits
+    // after the K (W) stage; with 16-bit elements (FAST) the products' gated
+    // operands, built once per row, then replace both (GTILES).  M, T reuse it
+    // all: 53 KB at dk = 128, C = 64, three workgroups per CU instead of two
+    // (measured: the kernel's time follows its occupancy, 218 us at one
+    // workgroup per CU, 137 at two).
+    static constexpr bool QREG = GATE == 2;
+    static constexpr bool FAST = GATE == 2 && sizeof(E) == 2;
+    static constexpr int STAGE = ((WR ? 2 : 1) + (QREG ? 0 : 1)) * CH * DK * (int)sizeof(E);  // K (Q, W) rows, swizzled
+    static constexpr int GAMB = GATE == 2 ? CH * PG * 4 : 0;      // cumulative decay per channel
+    static constexpr int NORM = GATE == 2 ? 2 * CH * 4 : 0;       // rows' L2-norm factors of K, Q
+    static constexpr int GTILES = FAST ? 3 * CH * DK * (int)sizeof(E) + NL * DK * 4 : 0;  // Qh, Kh, Kt, pair factors
+    static constexpr int SOLVE = 2 * CH * PF * 4;                  // M, T
+    static constexpr int UNION = cmax(cmax(STAGE + GAMB + NORM, GTILES), SOLVE);
 };
 
 // WR: an explicit write vector w_t in place of beta_t k_t (the asymmetric
@@ -204,7 +216,8 @@ struct PrepLayout {
 // TE = (I + M)^-1 (no beta), and the third gated tile is W * Gend; the state
 // kernel is the per-channel one, unchanged.
 template <int DK, int CH, typename E, int GATE, bool WR = false>
-__global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATE == 2 && DK == 128 && !WR ? 3 : 1)))
+chunk_prep_kernel(const ChunkParams p) {
     static_assert(!WR || GATE == 2, "the explicit write runs on the per-channel-gate path");
     using EL = Elem<E>;
     using F = typename EL::frag;
@@ -223,14 +236,17 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
     constexpr int JPW = RB ? NB : (NL + NW - 1) / NW;           // tile jobs per wave
 
     __shared__ __attribute__((aligned(16))) char smem[L::UNION];
-    __shared__ __attribute__((aligned(16))) float gam[GATE == 2 ? CH * PG : CH];
+    __shared__ __attribute__((aligned(16))) float gam_s[GATE == 2 ? 4 : CH];
     __shared__ __attribute__((aligned(16))) float bet[CH];
-    __shared__ __attribute__((aligned(16))) float rkf[CH];     // rows' L2-norm factors (fused norm)
-    __shared__ __attribute__((aligned(16))) float rqf[CH];
+    __shared__ __attribute__((aligned(16))) float rkf_s[GATE == 2 ? 4 : CH];  // rows' L2-norm factors (fused norm)
+    __shared__ __attribute__((aligned(16))) float rqf_s[GATE == 2 ? 4 : CH];
     __shared__ int flag[4];
     E *Kst = reinterpret_cast<E *>(smem);
-    E *Qst = Kst + CH * DK;
-    E *Wst = WR ? Qst + CH * DK : Kst;                          // the writing slot: W rows, or K
+    E *Qst = L::QREG ? nullptr : Kst + CH * DK;
+    E *Wst = WR ? Kst + CH * DK : Kst;                          // the writing slot: W rows, or K
+    float *gam = GATE == 2 ? reinterpret_cast<float *>(smem + L::STAGE) : gam_s;
+    float *rkf = GATE == 2 ? reinterpret_cast<float *>(smem + L::STAGE + L::GAMB) : rkf_s;
+    float *rqf = GATE == 2 ? rkf + CH : rqf_s;
     float *Mf = reinterpret_cast<float *>(smem);                // after the products are done
     float *Tf = Mf + CH * PF;
 
@@ -356,9 +372,110 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
             rq.l2norm_rows(rqf, tid);
         }
     }
-    rk.store(Kst, tid);
-    rq.store(Qst, tid);
-    if constexpr (WR) rw.store(Wst, tid);
+    // ---- per-channel gate, 16-bit: one pass over the thread's K, Q (W) units
+    // (unit i: global column unit c of row `row`, the swizzled load order) writes
+    // the state kernel's gated tiles, K*G and K*Gend (W*Gend) in paired-column
+    // order (16-byte unit pu = 4 q + g holds columns 32 q + 4 g .. + 3 and
+    // 32 q + 16 + 4 g .. + 3) and scale Q*G in natural order, and forms the
+    // products' operands with one exponential per (row, channel), relative to
+    // the first row a = 16 I of the row's block:
+    //   Qh = q e^(g - g_a), Kh = k e^(g - g_a)  (<= 1),  Kt = k e^(g_a - g)  (w with WR;
+    //   at most e^gate_range when no block is flagged),
+    // and per tile pair (I, J) the channel factors PF_IJ = e^(g_16I - g_16J)
+    // (<= 1; 1 for J = I), so that the pair contracts Qh_i, Kh_i with
+    // Kt_j * PF_IJ = k_j e^(g_16I - g_j) exactly as the per-pair factorisation
+    // does, with no row after i involved (the diagonal tiles are those products
+    // themselves; the others take one more rounding).  Rows past the end are
+    // zero.  A chunk with a flagged block (range above gate_range) runs the
+    // per-pair exponentials on the decay table instead.
+    constexpr int UPR = SK::UPR, PER = decltype(rk)::PER, NPF = (L::NL * DK + NT - 1) / NT;
+    u32x4 oq[L::FAST ? PER : 1], ok_[L::FAST ? PER : 1];
+    float opf[L::FAST ? NPF : 1];
+    bool fast = false;
+    if constexpr (L::FAST) {
+        using V8 = typename EL::frag2;
+        E *tg = reinterpret_cast<E *>(blk_base) + CB::TEA;
+        // LDS of the fast path: Kt over the K stage (free now), then Qh, Kh and the
+        // pair factors over the decay table once every thread has read it
+        E *Kt = reinterpret_cast<E *>(smem), *Qh = Kt + CH * DK, *Kh = Qh + CH * DK;
+        float *PFs = reinterpret_cast<float *>(smem + 3 * CH * DK * (int)sizeof(E));
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+        // the thread's units lie in rows r0 + (NT / UPR) i and share one column
+        // unit c, so gamma_C is read once; each unit runs in two halves of four
+        // channels
+        static_assert(64 % UPR == 0 && (NT / UPR) % UPR == 0, "units of one thread share their column unit");
+        const int c = (lane % UPR) ^ (((wave * 64 + lane) / UPR) & (UPR - 1));
+        f32x4 gC[2];
+        gC[0] = ld4(gam + (CH - 1) * PG + 8 * c);
+        gC[1] = ld4(gam + (CH - 1) * PG + 8 * c + 4);
+        unroll<PER>([&](auto i) {
+            const int u = (wave + (NT / 64) * (int)i) * 64 + lane;
+            const int row = u / UPR, ra = row & ~15;
+            const bool ok = (rk.ok >> (int)i) & 1u;
+            const V8 xk = __builtin_bit_cast(V8, rk.r[(int)i]), xq = __builtin_bit_cast(V8, rq.r[(int)i]);
+            V8 xw;
+            if constexpr (WR) xw = __builtin_bit_cast(V8, rw.r[(int)i]);
+            else xw = xk;
+            F hq[2], hk[2], hqg[2];
+            char *rowb = reinterpret_cast<char *>(tg + row * DK);
+            // paired-order byte offset of the unit's first 4-column piece (the second: + 16)
+            const int pb = 16 * (4 * (c >> 2) + 2 * (c & 1)) + 8 * ((c & 3) >> 1);
+            unroll<2>([&](auto hh) {
+                const int cc = 8 * c + 4 * (int)hh;
+                const f32x4 g = ld4(gam + row * PG + cc), a = ld4(gam + ra * PG + cc);
+                f32x4 k, q, w;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    k[e] = ok ? (float)xk[4 * (int)hh + e] : 0.f;
+                    q[e] = ok ? (float)xq[4 * (int)hh + e] : 0.f;
+                    w[e] = ok ? (float)xw[4 * (int)hh + e] : 0.f;
+                }
+                const f32x4 eg = exp4(g), ed = exp4(gC[(int)hh] - g), ea = exp4(g - a), eb = exp4(a - g);
+                *reinterpret_cast<F *>(rowb + pb + 16 * (int)hh) = EL::cvt(p.te_identity ? f32x4{0.f, 0.f, 0.f, 0.f} : k * eg);
+                hqg[(int)hh] = EL::cvt(q * eg * p.scale);
+                *reinterpret_cast<F *>(rowb + 2 * CH * DK * (int)sizeof(E) + pb + 16 * (int)hh) = EL::cvt(w * ed);
+                hq[(int)hh] = EL::cvt(q * ea);
+                hk[(int)hh] = EL::cvt(k * ea);
+                *reinterpret_cast<F *>(Kt + u * SK::VE + 4 * (int)hh) = EL::cvt(w * eb);
+            });
+            *reinterpret_cast<V8 *>(tg + CH * DK + row * DK + 8 * c) =
+                __builtin_shufflevector(hqg[0], hqg[1], 0, 1, 2, 3, 4, 5, 6, 7);
+            oq[(int)i] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hq[0], hq[1], 0, 1, 2, 3, 4, 5, 6, 7));
+            ok_[(int)i] = __builtin_bit_cast(u32x4, __builtin_shufflevector(hk[0], hk[1], 0, 1, 2, 3, 4, 5, 6, 7));
+        });
+        unroll<NPF>([&](auto m) {
+            const int v = tid + NT * (int)m, vv = v < L::NL * DK ? v : 0;
+            const int l = vv / DK, ch = vv % DK;
+            int I = 0, J = l;
+            while (J > I) { J -= I + 1; ++I; }
+            opf[(int)m] = __expf(gam[16 * I * PG + ch] - gam[16 * J * PG + ch]);
+        });
+        float *gcb = reinterpret_cast<float *>(blk_base + CB::GOFF);
+        for (int cc = tid; cc < DK; cc += NT) gcb[cc] = __expf(gam[(CH - 1) * PG + cc]);
+        __syncthreads();                                       // flags set, decay table read
+        int anyf = 0;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) anyf |= flag[b];
+        fast = anyf == 0;
+        if (fast) {
+            unroll<PER>([&](auto i) {
+                const int u = (wave + (NT / 64) * (int)i) * 64 + lane;
+                *reinterpret_cast<u32x4 *>(Qh + u * SK::VE) = oq[(int)i];
+                *reinterpret_cast<u32x4 *>(Kh + u * SK::VE) = ok_[(int)i];
+            });
+            unroll<NPF>([&](auto m) {
+                const int v = tid + NT * (int)m;
+                if (v < L::NL * DK) PFs[v] = opf[(int)m];
+            });
+        } else {
+            rk.store(Kst, tid);
+            if constexpr (WR) rw.store(Wst, tid);
+        }
+    } else {
+        rk.store(Kst, tid);
+        if constexpr (!L::QREG) rq.store(Qst, tid);
+        if constexpr (WR) rw.store(Wst, tid);
+    }
     __syncthreads();
     if constexpr (GATE != 2) {
         // the state kernel's row factors (ChunkBlock)
@@ -406,13 +523,75 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
         }
     }
     f32x4 res_q[JPW], res_k[JPW];
+    // A and M tiles from the products' sums (C layout: row irow, columns 16 J + 4 g ..)
+    auto job_tail = [&](int s, int I, int J, int irow, const f32x4 &accq, const f32x4 &acck)
+        __attribute__((always_inline)) {
+        f32x4 aq, mk;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+            const int jt = 16 * J + 4 * g4 + jj;
+            // computed for every lane and then selected: a lane-dependent branch
+            // here becomes an exec-skip right after the MFMAs above
+            float d = 1.f;
+            if constexpr (GATE != 2) {
+                const float e = __expf(gam[irow] - gam[jt]);
+                d = (jt <= irow) ? e : 0.f;
+            }
+            aq[jj] = (jt <= irow) ? p.scale * accq[jj] * d : 0.f;
+            mk[jj] = (jt < irow) ? bet[irow] * acck[jj] * d : 0.f;
+        }
+        if constexpr (GATE == 2) {
+            // N itself (before diag(beta); with W, M = <k_i, w_j>), for the backward
+            if (p.nout) {
+                float *nb = p.nout + (slot * H + h) * CH * CH + irow * CH + 16 * J + 4 * g4;
+#pragma unroll
+                for (int jj = 0; jj < 4; ++jj) nb[jj] = 16 * J + 4 * g4 + jj < irow ? acck[jj] : 0.f;
+            }
+        }
+        res_q[s] = aq;
+        res_k[s] = mk;
+    };
+    if constexpr (L::FAST) {
+        if (fast) {
+            // gated operands from LDS: i side Qh, Kh; j side Kt * PF_IJ (pair l = job)
+            const E *Kt = reinterpret_cast<const E *>(smem), *Qh = Kt + CH * DK, *Kh = Qh + CH * DK;
+            const float *PFs = reinterpret_cast<const float *>(smem + 3 * CH * DK * (int)sizeof(E));
+#pragma unroll
+            for (int s = 0; s < JPW; ++s) {
+                res_q[s] = res_k[s] = f32x4{0.f, 0.f, 0.f, 0.f};
+                int I, J;
+                if (!job_ij(s, I, J)) continue;
+                const int l = wave + NW * s;
+                const int jrow = 16 * J + r16, irow = 16 * I + r16;
+                F a[NKB], bq[NKB], bk[NKB];
+#pragma unroll
+                for (int kt = 0; kt < NKB; ++kt) {
+                    const int cc = 16 * kt + 4 * g4;
+                    a[kt] = EL::cvt(EL::tof(ld_frag<E>(Kt + SK::at(jrow, cc))) * ld4(PFs + l * DK + cc));
+                    bq[kt] = ld_frag<E>(Qh + SK::at(irow, cc));
+                    bk[kt] = ld_frag<E>(Kh + SK::at(irow, cc));
+                }
+                f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int kt = 0; kt < NKB; kt += 2) {
+                    accq = mfma_kb2(a[kt], bq[kt], a[kt + 1], bq[kt + 1], accq);
+                    acck = mfma_kb2(a[kt], bk[kt], a[kt + 1], bk[kt + 1], acck);
+                }
+                job_tail(s, I, J, irow, accq, acck);
+            }
+        }
+    }
 #pragma unroll
     for (int s = 0; s < JPW; ++s) {
+        if (fast) break;
         res_q[s] = res_k[s] = f32x4{0.f, 0.f, 0.f, 0.f};
         int I, J;
         if (!job_ij(s, I, J)) continue;
         const int jrow = 16 * J + r16, irow = 16 * I + r16;
         F a[NKB], bq[NKB], bk[NKB];
+        // QREG: Q row irow from global memory (a valid row, zeroed past the end),
+        // rounded after the fused L2 norm as the staged rows are
+        const E *qsrc = qg + (int64_t)(irow < clen ? irow : clen - 1) * sqk;
 #pragma unroll
         for (int kt = 0; kt < NKB; ++kt) {
             const int cc = 16 * kt + 4 * g4;
@@ -421,8 +600,18 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
                 bq[kt] = bq_rb[kt];
                 bk[kt] = bk_rb[kt];
             } else {
-                bq[kt] = ld_frag<E>(Qst + SK::at(irow, cc));
+                if constexpr (L::QREG) bq[kt] = *reinterpret_cast<const F *>(qsrc + cc);
+                else bq[kt] = ld_frag<E>(Qst + SK::at(irow, cc));
                 bk[kt] = ld_frag<E>(Kst + SK::at(irow, cc));
+            }
+        }
+        if constexpr (L::QREG) {
+            const bool qn = sizeof(E) == 2 && fz.qk_l2norm;
+            const float fq = qn ? rqf[irow] : 1.f;
+#pragma unroll
+            for (int kt = 0; kt < NKB; ++kt) {
+                if (qn) bq[kt] = EL::cvt(EL::tof(bq[kt]) * fq);
+                if (irow >= clen) bq[kt] = EL::cvt(f32x4{0.f, 0.f, 0.f, 0.f});
             }
         }
         bool pairwise = false;
@@ -454,10 +643,19 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
                 const int jt = 16 * J + 4 * g4 + jj;
                 float sq = 0.f, sk = 0.f;
                 if (jt <= irow) {
+#pragma unroll 1
                     for (int cc = 0; cc < DK; cc += 4) {
                         const f32x4 e = exp4(ld4(gam + irow * PG + cc) - ld4(gam + jt * PG + cc));
                         const f32x4 kj = EL::tof(ld_frag<E>(Wst + SK::at(jt, cc))) * e;
-                        const f32x4 yq = EL::tof(ld_frag<E>(Qst + SK::at(irow, cc))) * kj;
+                        f32x4 qv;
+                        if constexpr (L::QREG) {                 // as bq above, before the gate
+                            F qf = *reinterpret_cast<const F *>(qsrc + cc);
+                            if (sizeof(E) == 2 && fz.qk_l2norm) qf = EL::cvt(EL::tof(qf) * rqf[irow]);
+                            qv = irow < clen ? EL::tof(qf) : f32x4{0.f, 0.f, 0.f, 0.f};
+                        } else {
+                            qv = EL::tof(ld_frag<E>(Qst + SK::at(irow, cc)));
+                        }
+                        const f32x4 yq = qv * kj;
                         const f32x4 yk = EL::tof(ld_frag<E>(Kst + SK::at(irow, cc))) * kj;
                         sq += yq[0] + yq[1] + yq[2] + yq[3];
                         sk += yk[0] + yk[1] + yk[2] + yk[3];
@@ -467,63 +665,7 @@ __global__ void __launch_bounds__(256) chunk_prep_kernel(const ChunkParams p) {
                 acck[jj] = sk;
             }
         }
-        f32x4 aq, mk;
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int jt = 16 * J + 4 * g4 + jj;
-            // computed for every lane and then selected: a lane-dependent branch
-            // here becomes an exec-skip right after the MFMAs above
-            float d = 1.f;
-            if constexpr (GATE != 2) {
-                const float e = __expf(gam[irow] - gam[jt]);
-                d = (jt <= irow) ? e : 0.f;
-            }
-            aq[jj] = (jt <= irow) ? p.scale * accq[jj] * d : 0.f;
-            mk[jj] = (jt < irow) ? bet[irow] * acck[jj] * d : 0.f;
-        }
-        if constexpr (GATE == 2) {
-            // N itself (before diag(beta); with W, M = <k_i, w_j>), for the backward
-            if (p.nout) {
-                float *nb = p.nout + (slot * H + h) * CH * CH + irow * CH + 16 * J + 4 * g4;
-#pragma unroll
-                for (int jj = 0; jj < 4; ++jj) nb[jj] = 16 * J + 4 * g4 + jj < irow ? acck[jj] : 0.f;
-            }
-        }
-        res_q[s] = aq;
-        res_k[s] = mk;
-    }
-    if constexpr (CB::VEC) {
-        // gated tiles for the state kernel: K*G and K*Gend with rows in
-        // paired-column order (16-byte unit pu = 4 q + g holds columns 32 q + 4 g
-        // .. + 3 and 32 q + 16 + 4 g .. + 3), scale Q*G in natural column order,
-        // then Gc = exp(gamma_C)
-        using F2 = typename EL::frag2;
-        E *tg = reinterpret_cast<E *>(blk_base) + CB::TEA;
-        constexpr int UPR = DK / 8;
-        for (int it = tid; it < CH * UPR; it += NT) {
-            const int t = it / UPR, pu = it % UPR;
-            const int c0 = 32 * (pu >> 2) + 4 * (pu & 3), c1 = c0 + 16;
-            const f32x4 gt0 = ld4(gam + t * PG + c0), gt1 = ld4(gam + t * PG + c1);
-            const f32x4 gl0 = ld4(gam + (CH - 1) * PG + c0), gl1 = ld4(gam + (CH - 1) * PG + c1);
-            const f32x4 e0 = exp4(gt0), e1 = exp4(gt1), d0 = exp4(gl0 - gt0), d1 = exp4(gl1 - gt1);
-            const f32x4 k0 = EL::tof(ld_frag<E>(Kst + SK::at(t, c0))), k1 = EL::tof(ld_frag<E>(Kst + SK::at(t, c1)));
-            const f32x4 q0 = EL::tof(ld_frag<E>(Qst + SK::at(t, c0))), q1 = EL::tof(ld_frag<E>(Qst + SK::at(t, c1)));
-            E *row = tg + t * DK + 8 * pu;
-            // a zero K*G tile without the delta rule (X = V)
-            *reinterpret_cast<F2 *>(row) = p.te_identity ? EL::cvt2(f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f})
-                                                         : EL::cvt2(k0 * e0, k1 * e1);
-            E *qrow = tg + CH * DK + t * DK;
-            st_frag<E>(qrow + c0, EL::cvt(q0 * e0 * p.scale));
-            st_frag<E>(qrow + c1, EL::cvt(q1 * e1 * p.scale));
-            if constexpr (WR) {                                  // the state update writes with W * Gend
-                const f32x4 w0 = EL::tof(ld_frag<E>(Wst + SK::at(t, c0))), w1 = EL::tof(ld_frag<E>(Wst + SK::at(t, c1)));
-                *reinterpret_cast<F2 *>(row + 2 * CH * DK) = EL::cvt2(w0 * d0, w1 * d1);
-            } else {
-                *reinterpret_cast<F2 *>(row + 2 * CH * DK) = EL::cvt2(k0 * d0, k1 * d1);
-            }
-        }
-        float *gcb = reinterpret_cast<float *>(blk_base + CB::GOFF);
-        for (int cc = tid; cc < DK; cc += NT) gcb[cc] = __expf(gam[(CH - 1) * PG + cc]);
+        job_tail(s, I, J, irow, accq, acck);
     }
     __syncthreads();                                           // K, Q reads done: M, T reuse the stage
 #pragma unroll
