@@ -760,7 +760,11 @@ namespace vgdr {"""),
 #pragma unroll
         for (int s = 0; s < NW; ++s)
 #pragma unroll
-            for (int k = 0; k < NKB / 2; ++k) asm volatile("" : "+v"(Sn[s][k]));"""),
+            for (int k = 0; k < NKB / 2; ++k) asm volatile("" : "+v"(Sn[s][k]));
+#pragma unroll
+        for (int i = 0; i < NR; ++i)
+#pragma unroll
+            for (int k = 0; k < NKB / 2; ++k) asm volatile("" : "+v"(Qv[i][k]));"""),
     ("""        // the chunk's o rows as one buffer: rows past the sequence's end fall
         // outside it and their stores are dropped, with no lane-dependent branch""", """        {
             float tmp = 0.f;
