@@ -459,11 +459,16 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
 // ===========================================================================
 
 // NWC compute waves (16 state columns each) and NWC producer waves.  The
-// producers load each chunk's K, Q rows, TE and A blocks and gate factors
-// into registers and stage them into the idle half of a double-buffered LDS
-// slot while the compute waves work on the other half; one barrier per chunk
-// hands a slot over.  The two roles run separate loops with the same barrier
-// count.  The compute waves load their own dO rows one chunk ahead.
+// producers load each chunk's K, Q rows, TE and A blocks, gate factors and the
+// tile's dO rows into registers and stage them into the idle half of a
+// double-buffered LDS slot while the compute waves work on the other half; one
+// barrier per chunk hands a slot over.  The two roles run separate loops with
+// the same barrier count.  (The compute waves had loaded dO themselves, two
+// bytes per load in the MFMA layout: 22 us more at gdn_340m.)  16-bit dV
+// leaves as 16-byte units: the compute waves also form dX^T = dU^T TE (the dX
+// product with its operands swapped), whose C layout gives a lane four
+// consecutive columns of one token, and pair token blocks through
+// v_permlane16_swap for eight.
 // VEC (per-channel gate, 16-bit): the operands are chunk prep's gated tiles
 // instead of K and Q rows with per-row factors: K*G (Ks) and scale Q*G (Qs)
 // for dS, K*Gend (KEs) for dU, and Gc per key channel:
@@ -477,6 +482,7 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
     constexpr int NTP = 64 * NPW, NB = CH / 16, NKB = DK / 16;
     constexpr int PK = Pitch<E, DK>::value, PT = Pitch<E, CH>::value;
     constexpr int NGF = VEC ? DK : 3 * CH + 4;
+    constexpr int DW = 16 * NWC, PD = DW + 8;                  // the tile's dO columns, their LDS pitch
     __shared__ __attribute__((aligned(16))) E Ks0[CH * PK];
     __shared__ __attribute__((aligned(16))) E Ks1[CH * PK];
     __shared__ __attribute__((aligned(16))) E Qs0[CH * PK];
@@ -489,6 +495,8 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
     __shared__ __attribute__((aligned(16))) E Am1[CH * PT];
     __shared__ __attribute__((aligned(16))) float gt0[NGF];          // GX, GO, GE, then Gc (VEC: Gc per channel)
     __shared__ __attribute__((aligned(16))) float gt1[NGF];
+    __shared__ __attribute__((aligned(16))) E dO0[CH * PD];
+    __shared__ __attribute__((aligned(16))) E dO1[CH * PD];
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g4 = lane >> 4, r16 = lane & 15;
@@ -509,6 +517,9 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
         const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
         RowRegs<E, CH, DK, NTP> rk, rq;
         RowRegs<E, CH, VEC ? DK : 32, NTP> rke;                 // VEC: K*Gend rows
+        RowRegs<E, CH, DW, NTP> rdo;                            // dO rows, the tile's columns
+        const int cb = u.tile * DW;
+        const E *dot = reinterpret_cast<const E *>(p.dout) + (int64_t)h * DV + cb;
         BlockRegs<E, CH, NTP> rte, ra;
         constexpr int NG = VEC ? DK : 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
         float gv[GPT];
@@ -527,6 +538,7 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
             }
             rte.load(reinterpret_cast<const E *>(blkb), ptid);
             ra.load(reinterpret_cast<const E *>(blkb) + CH * CH, ptid);
+            rdo.load(dot + t0 * sv, sv, clen, ptid, DV - cb);
 #pragma unroll
             for (int i = 0; i < GPT; ++i) {
                 const int gi = ptid + i * NTP;
@@ -546,6 +558,7 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
             }
             rte.store(SL ? TE1 : TE0, PT, ptid);
             ra.store(SL ? Am1 : Am0, PT, ptid);
+            rdo.store(SL ? dO1 : dO0, PD, clen, ptid, DV - cb);   // zero past the chunk's end and dv
 #pragma unroll
             for (int i = 0; i < GPT; ++i)
                 if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = gv[i];
@@ -575,7 +588,6 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
     const int colw = u.tile * 16 * NWC + 16 * wave;
     const bool wvalid = colw < DV;
     const int col = wvalid ? colw + r16 : r16;
-    const E *dog = reinterpret_cast<const E *>(p.dout) + (int64_t)h * DV + col;
     E *dvg = reinterpret_cast<E *>(p.dv) + (int64_t)h * DV + col;
     f32x4 dS[NKB];
     const int64_t sbase = ((int64_t)u.seq * H + h) * DK * DV + col;
@@ -584,18 +596,6 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             dS[kt][j] = (p.dht && wvalid) ? p.dht[sbase + (int64_t)(16 * kt + 4 * g4 + j) * DV] : 0.f;
-    E don[NB][4];                                              // dO rows of the next chunk (C layout, raw)
-    auto fetch_do = [&](int c) __attribute__((always_inline)) {
-        const int64_t t0 = u.bos + (int64_t)c * CH;
-        const int clen = clen_of(c);
-#pragma unroll
-        for (int I = 0; I < NB; ++I)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int row = 16 * I + 4 * g4 + j;
-                don[I][j] = dog[(t0 + (row < clen ? row : 0)) * sv];
-            }
-    };
     auto step = [&](auto tag, int k) __attribute__((always_inline)) {
         constexpr int SL = decltype(tag)::value;
         const E *Ks = SL ? Ks1 : Ks0;
@@ -622,13 +622,12 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
 #pragma unroll
             for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(dhs + ckpt_pos<DK>(colw >> 4, kt, lane), EL::cvt(dS[kt]));
         }
-        f32x4 dO[NB];
-#pragma unroll
-        for (int I = 0; I < NB; ++I)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) dO[I][j] = 16 * I + 4 * g4 + j < clen ? EL::to_f(don[I][j]) : 0.f;
-        if (c > 0) fetch_do(c - 1);
         if (wvalid) {
+            // dO rows 16 I + 4 g .. + 3 of column r (the B-operand layout; zero past the end)
+            const E *dOs = SL ? dO1 : dO0;
+            f32x4 dO[NB];
+#pragma unroll
+            for (int I = 0; I < NB; ++I) dO[I] = EL::tof(ld_colfrag<E>(dOs, PD, 16 * I, 16 * wave, lane));
             F dOb[NB], dSb[NKB];
 #pragma unroll
             for (int I = 0; I < NB; ++I) dOb[I] = EL::cvt(dO[I]);
@@ -648,20 +647,38 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
             }
             // dX = TE^T dU  -> dV;  operands of the state update
             F Ob[NB], Xb[NB];
+            if constexpr (sizeof(E) == 2) {
+                // dV: dX^T = dU^T TE, lane (g, r) holding columns 4 g .. + 3 of token
+                // 16 I + r; token blocks 2 m and 2 m + 1 trade halves (lanes l and
+                // l ^ 16), after which a lane holds columns 8 (g >> 1) .. + 7 of token
+                // 16 (2 m + (g & 1)) + r.  Rows past the chunk's end fall outside the
+                // resource (no branch).
+                static_assert(NB % 2 == 0, "token blocks go in pairs");
+                const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(
+                    reinterpret_cast<E *>(p.dv) + t0 * sv + (int64_t)h * DV, (uint32_t)(clen * sv * sizeof(E)));
+#pragma unroll
+                for (int m = 0; m < NB / 2; ++m) {
+                    u32x2 xt[2];
+#pragma unroll
+                    for (int e = 0; e < 2; ++e) {
+                        const int I = 2 * m + e;
+                        const f32x4 dXT = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NB, [&](int kb) { return Yb[kb]; },
+                            [&](int kb) { return ld_colfrag<E>(TEm, PT, 16 * kb, 16 * I, lane); });
+                        xt[e] = __builtin_bit_cast(u32x2, EL::cvt(dXT));
+                    }
+                    const auto a = __builtin_amdgcn_permlane16_swap(xt[0][0], xt[1][0], false, false);
+                    const auto b = __builtin_amdgcn_permlane16_swap(xt[0][1], xt[1][1], false, false);
+                    const int tok = 16 * (2 * m + (g4 & 1)) + r16, cc = colw + 8 * (g4 >> 1);
+                    __builtin_amdgcn_raw_buffer_store_b128(u32x4{a[0], b[0], a[1], b[1]}, rv,
+                                                           (int)((tok * sv + cc) * sizeof(E)), 0, 0);
+                }
+            }
 #pragma unroll
             for (int I = 0; I < NB; ++I) {
                 const f32x4 dX = contract(f32x4{0.f, 0.f, 0.f, 0.f}, NB,
                     [&](int kb) { return ld_colfrag<E>(TEm, PT, 16 * kb, 16 * I, lane); },
                     [&](int kb) { return Yb[kb]; });
-                if constexpr (sizeof(E) == 2) {
-                    // rows past the chunk's end fall outside the resource (no branch)
-                    const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(
-                        reinterpret_cast<E *>(p.dv) + t0 * sv + (int64_t)h * DV, (uint32_t)(clen * sv * sizeof(E)));
-#pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        buffer_store_2b(EL::from_f(dX[j]), rv,
-                                        (uint32_t)(((16 * I + 4 * g4 + j) * sv + col) * sizeof(E)));
-                } else {
+                if constexpr (sizeof(E) != 2) {
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int row = 16 * I + 4 * g4 + j;
@@ -689,10 +706,7 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
             }
         }
     };
-    if (nchunks > 0) {
-        fetch_do(nchunks - 1);
-        __syncthreads();                                       // slot 0 holds the last chunk
-    }
+    if (nchunks > 0) __syncthreads();                          // slot 0 holds the last chunk
     for (int k = 0; k < nchunks; k += 2) {
         step(SlotTag<0>{}, k);
         __syncthreads();
