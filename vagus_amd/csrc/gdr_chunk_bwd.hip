@@ -272,10 +272,12 @@ __device__ __forceinline__ bool locate_chunk(const SeqGeom &g, int64_t slot, int
 template <int V_> struct SlotTag { static constexpr int value = V_; };
 
 // NWC compute waves (16 state columns each) re-run the forward recurrence and
-// store each chunk's entry state; NWC producer waves stage each chunk's K rows
-// and gate factors into the idle half of a double-buffered LDS slot (one
-// barrier per chunk hands a slot over; separate loops, equal barrier counts).
-// The compute waves load their own V rows and TE fragments one chunk ahead.
+// store each chunk's entry state; NWC producer waves stage each chunk's K rows,
+// the tile's V rows and the gate factors into the idle half of a
+// double-buffered LDS slot (one barrier per chunk hands a slot over; separate
+// loops, equal barrier counts).  The compute waves load their own TE fragments
+// one chunk ahead.  (They had loaded V too, two bytes per load in the MFMA
+// layout.)
 template <int DK, int CH, int NWC, typename E>
 __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParams p) {
     using EL = Elem<E>;
@@ -283,10 +285,13 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
     using CB = ChunkBlock<E, CH, DK, 1>;
     constexpr int NTP = 64 * NWC, NB = CH / 16, NKB = DK / 16;
     constexpr int PK = Pitch<E, DK>::value;
+    constexpr int DW = 16 * NWC, PD = DW + 8;                  // the tile's V columns, their LDS pitch
     __shared__ __attribute__((aligned(16))) E Ks0[CH * PK];
     __shared__ __attribute__((aligned(16))) E Ks1[CH * PK];
     __shared__ __attribute__((aligned(16))) float gt0[3 * CH + 4];   // GX, GO, GE, then Gc
     __shared__ __attribute__((aligned(16))) float gt1[3 * CH + 4];
+    __shared__ __attribute__((aligned(16))) E Vs0[CH * PD];
+    __shared__ __attribute__((aligned(16))) E Vs1[CH * PD];
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g4 = lane >> 4, r16 = lane & 15;
@@ -310,9 +315,13 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
         const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
         constexpr int NG = 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
         RowRegs<E, CH, DK, NTP> rk;
+        RowRegs<E, CH, DW, NTP> rv;
+        const int cb = u.tile * DW;
+        const E *vt = reinterpret_cast<const E *>(p.v) + (int64_t)h * DV + cb;
         float gv[GPT];
         auto fetch = [&](int c) __attribute__((always_inline)) {
             rk.load(kg + (u.bos + (int64_t)c * CH) * sqk, sqk, clen_of(c), ptid);
+            rv.load(vt + (u.bos + (int64_t)c * CH) * sv, sv, clen_of(c), ptid, DV - cb);
 #pragma unroll
             for (int i = 0; i < GPT; ++i) {
                 const int gi = ptid + i * NTP;
@@ -322,6 +331,7 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
         auto put = [&](auto tag, int c) __attribute__((always_inline)) {
             constexpr int SL = decltype(tag)::value;
             rk.store(SL ? Ks1 : Ks0, PK, clen_of(c), ptid);
+            rv.store(SL ? Vs1 : Vs0, PD, clen_of(c), ptid, DV - cb);   // zero past the chunk's end and dv
 #pragma unroll
             for (int i = 0; i < GPT; ++i)
                 if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = gv[i];
@@ -351,7 +361,6 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
     const int colw = u.tile * 16 * NWC + 16 * wave;
     const bool wvalid = colw < DV;                             // DV % 16 == 0
     const int col = wvalid ? colw + r16 : r16;                 // in bounds for the unconditional loads
-    const E *vg = reinterpret_cast<const E *>(p.v) + (int64_t)h * DV + col;
     f32x4 S[NKB];
     const int64_t sbase = ((int64_t)u.seq * H + h) * DK * DV + col;
 #pragma unroll
@@ -375,38 +384,28 @@ __global__ void __launch_bounds__(128 * NWC) chunk_hs_kernel(const ChunkBwdParam
             for (int kt = 0; kt < NKB; ++kt) st_gfrag<E>(hs + ckpt_pos<DK>(colw >> 4, kt, lane), EL::cvt(S[kt]));
         }
     };
-    // V rows (C layout) and TE fragments (lower tiles) of the next chunk, raw:
-    // a conversion next to its load would wait for every load before it
-    E vn[NB][4];
+    // TE fragments (lower tiles) of the next chunk, raw: a conversion next to
+    // its load would wait for every load before it
     F ten[NB * NB];
     auto fetch_own = [&](int c) __attribute__((always_inline)) {
-        const int64_t t0 = u.bos + (int64_t)c * CH;
-        const int clen = clen_of(c);
         const E *TEb = reinterpret_cast<const E *>(blk_of(c));
 #pragma unroll
         for (int I = 0; I < NB; ++I)
 #pragma unroll
             for (int kb = 0; kb <= I; ++kb) ten[I * NB + kb] = gfrag<E>(TEb + frag_pos<NB>(I, kb, lane));
-#pragma unroll
-        for (int I = 0; I < NB; ++I)
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int row = 16 * I + 4 * g4 + j;
-                vn[I][j] = vg[(t0 + (row < clen ? row : 0)) * sv];
-            }
     };
     auto step = [&](auto tag, int c) __attribute__((always_inline)) {
         constexpr int SL = decltype(tag)::value;
         const E *Ks = SL ? Ks1 : Ks0;
         const float *gt = SL ? gt1 : gt0;
         store_state(c);
-        const int clen = clen_of(c);
+        // V rows 16 I + 4 g .. + 3 of column r (the B-operand layout; zero past the end)
+        const E *Vs = SL ? Vs1 : Vs0;
         f32x4 V[NB];
         F TEf[NB * NB];
 #pragma unroll
         for (int I = 0; I < NB; ++I) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) V[I][j] = 16 * I + 4 * g4 + j < clen ? EL::to_f(vn[I][j]) : 0.f;
+            V[I] = EL::tof(ld_colfrag<E>(Vs, PD, 16 * I, 16 * wave, lane));
 #pragma unroll
             for (int kb = 0; kb <= I; ++kb) TEf[I * NB + kb] = ten[I * NB + kb];
         }
