@@ -1234,6 +1234,12 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     }
     E *dqg = reinterpret_cast<E *>(p.dq) + t0 * sqk + (int64_t)h * DK;
     E *dkg = reinterpret_cast<E *>(p.dk) + t0 * sqk + (int64_t)h * DK;
+    // 16-bit, C = 64: dQ, dK rows staged in LDS over N, dTE and Z (dead since the dM
+    // step; the products below read only W_A, WS, K and Q), then written as
+    // 16-byte units (the C layout gave two-byte stores: 10 us at gdn_340m)
+    constexpr int PQ = DK + 8;
+    constexpr bool STG = sizeof(E) == 2 && 2 * CH * PQ * (int)sizeof(E) <= 3 * CH * PF * 4;   // C = 64
+    E *dQs = reinterpret_cast<E *>(R), *dKs = dQs + CH * PQ;
     const f32x4 GOr = ld4(go + 16 * Iw + 4 * g4), GXr = ld4(gx + 16 * Iw + 4 * g4), GEr = ld4(ge + 16 * Iw + 4 * g4);
 #pragma unroll
     for (int s = 0; s < JPW; ++s) {
@@ -1250,13 +1256,27 @@ chunk_grad_kernel(const ChunkBwdParams p) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int i = 16 * Iw + 4 * g4 + j;
-            if (i < clen) {
+            if constexpr (STG) {
+                dQs[i * PQ + 16 * J + r16] = EL::from_f(q[j]);
+                dKs[i * PQ + 16 * J + r16] = EL::from_f(k[j]);
+            } else if (i < clen) {
                 dqg[i * sqk + 16 * J + r16] = EL::from_f(q[j]);
                 dkg[i * sqk + 16 * J + r16] = EL::from_f(k[j]);
             }
         }
     }
     __syncthreads();
+    if constexpr (STG) {
+        constexpr int VE = 16 / (int)sizeof(E), UPR = DK / VE;
+        typedef E V __attribute__((ext_vector_type(VE)));
+        for (int u = tid; u < CH * UPR; u += NT) {
+            const int row = u / UPR, c0 = (u % UPR) * VE;
+            if (row < clen) {
+                *reinterpret_cast<V *>(dqg + row * sqk + c0) = *reinterpret_cast<const V *>(dQs + row * PQ + c0);
+                *reinterpret_cast<V *>(dkg + row * sqk + c0) = *reinterpret_cast<const V *>(dKs + row * PQ + c0);
+            }
+        }
+    }
     // ---- dg (suffix sums of dgamma; gamma_C is gamma at the last token) and dbeta
     if (wave == 0) {
         float x = lane < clen ? dgam[lane] : 0.f;
