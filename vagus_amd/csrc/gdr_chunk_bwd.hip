@@ -1826,9 +1826,18 @@ template <int DK, int CH, typename E>
 static hipError_t run_bwd_vec(ChunkBwdParams p, hipStream_t stream) {
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
     if (units > 0) {
-        p.n_tiles = (p.DV + 31) / 32;
-        hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E, true>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
-                           dim3(256), 0, stream, p);
+        // 32-column tiles once they give every CU a walk, 16-column tiles (one
+        // compute wave, two producer waves) below that: the 128 dependent chunk
+        // steps of a B4 T8192 H8 call ran on half the CUs with 32 columns
+        if (units * ((p.DV + 31) / 32) >= device_cu_count()) {
+            p.n_tiles = (p.DV + 31) / 32;
+            hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E, true>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
+                               dim3(256), 0, stream, p);
+        } else {
+            p.n_tiles = (p.DV + 15) / 16;
+            hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 1, E, true, 2>),
+                               dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)), dim3(192), 0, stream, p);
+        }
     }
     const int64_t grad_blocks = (int64_t)p.n_chunk_slots * p.H;
     if (grad_blocks > 0) {
