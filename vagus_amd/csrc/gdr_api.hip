@@ -453,12 +453,10 @@ int bwd_call(const char *fn, bool saved, bool delta, VGDR_BWD_ARGS, const vgdr_f
         p.dA_log = grad_A_log;
         p.ddt_bias = grad_dt_bias;
         // the forward run for the entry states writes N and the states where
-        // the backward reads them; its output o goes to the exit-gradient
-        // region (n_tokens x dv <= chunk slots x CH x dv <= its dk x dv per
-        // slot), which the dS walk then overwrites
+        // the backward reads them, and no output (ChunkParams::states_only,
+        // set by the backward's launcher)
         f.hs = p.hs;
         f.nout = const_cast<float *>(p.nbuf);
-        f.o = p.dhs;
         f.h0 = initial_state;
     }
     int32_t *table = cu_seqlens ? reinterpret_cast<int32_t *>(wsb) : nullptr;

@@ -1361,7 +1361,10 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 //   UH: U~ in the MFMA A-operand order the chain wave holds it (lane-to-lane).
 // HS: the output waves also store each chunk's entry state to p.hs
 // ([chunk slot, H] checkpoints in ckpt_pos order), for the chunked backward.
-template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA, bool HS = false>
+// OUT false (with HS): only those states -- no outputs, so no U~ hand-over,
+// no Q copy and no A, Q loads or products in the output waves; the backward's
+// entry-state walk.
+template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA, bool HS = false, bool OUT = true>
 __global__ void __launch_bounds__(64 * (NW + 2 + NP))
 __attribute__((amdgpu_waves_per_eu(1, (NW + 2 + NP + 3) / 4)))
 chunk_pipe_kernel(const ChunkParams p) {
@@ -1382,7 +1385,8 @@ chunk_pipe_kernel(const ChunkParams p) {
     // with two, their registers are full and the output waves load the Q operand
     // straight from global memory (the whole-row loads and an LDS transpose in
     // the output waves measured no faster there)
-    constexpr bool QL = NP >= 4;
+    constexpr bool QL = NP >= 4 && OUT;
+    static_assert(OUT || HS, "a walk without outputs stores the entry states");
 
     __shared__ __attribute__((aligned(16))) E K0[CH * PK];
     __shared__ __attribute__((aligned(16))) E K1[CH * PK];
@@ -1616,7 +1620,7 @@ chunk_pipe_kernel(const ChunkParams p) {
 #pragma unroll
             for (int q = 0; q < NB / 2; ++q) {
                 const F2 ub = EL::cvt2(U[2 * q], U[2 * q + 1]);
-                *reinterpret_cast<F2 *>(uh + 512 * q) = ub;
+                if constexpr (OUT) *reinterpret_cast<F2 *>(uh + 512 * q) = ub;
                 if constexpr (VEC) Wb[q] = ub;                     // Gend is in the K*Gend tile
                 else Wb[q] = EL::cvt2(U[2 * q] * gev[2 * q], U[2 * q + 1] * gev[2 * q + 1]);
             }
@@ -1663,6 +1667,7 @@ chunk_pipe_kernel(const ChunkParams p) {
         float go[NR];
     };
     auto oload = [&](Ops &op, int c) __attribute__((always_inline)) {
+        if constexpr (!OUT) return;
         c = c < nchunks ? c : nchunks - 1;                     // past the end: the last chunk again
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
@@ -1688,7 +1693,7 @@ chunk_pipe_kernel(const ChunkParams p) {
     // 16 s + 4 g .. + 3 of token 16 I + r.  The hand-over of every strip is read
     // first; the NW x NR accumulators then advance together (independent MFMA
     // chains, interleaved).
-    auto ocompute = [&](const Ops &op, int c, int z) __attribute__((always_inline)) {
+    auto oproducts = [&](const Ops &op, int c, int z) __attribute__((always_inline)) {
         const int64_t t0 = bos + (int64_t)c * CH;
         const int clen = (int)(eos - t0 < CH ? eos - t0 : CH);
         const bool odd = c & 1;
@@ -1752,15 +1757,22 @@ chunk_pipe_kernel(const ChunkParams p) {
                 });
             });
         }
-        unroll<NW>([&](auto s) {
-            if (col0 + 16 * s >= DV) return;
-            if constexpr (NW % 2 != 0)
+        if constexpr (NW % 2 != 0)
+            unroll<NW>([&](auto s) {
+                if (col0 + 16 * s >= DV) return;
                 unroll<NR>([&](auto i) {
                     const int I = rb(i);
                     buffer_store_8b(EL::cvt(ot[s][i]), ors,
                                     (uint32_t)(((16 * I + r16) * sv + 16 * s + 4 * g4) * sizeof(E)));
                 });
-            if constexpr (HS) {
+            });
+    };
+    auto ocompute = [&](const Ops &op, int c, int z) __attribute__((always_inline)) {
+        const bool odd = c & 1;
+        if constexpr (OUT) oproducts(op, c, z);
+        if constexpr (HS)
+            unroll<NW>([&](auto s) {
+                if (col0 + 16 * s >= DV) return;
                 // the checkpoint's fragment order: lane (g, r) holds rows 16 kt + 4 g .. + 3
                 // of column 16 cb + r.  Output wave o stores key blocks o, o + 2, ..
                 const E *sh = SH + ((odd ? NW : 0) + s) * 16 * SP + z + r16 * SP;
@@ -1771,8 +1783,7 @@ chunk_pipe_kernel(const ChunkParams p) {
                     *reinterpret_cast<E4 *>(hs + ckpt_pos<DK>(cb, kt, lane)) =
                         *reinterpret_cast<const E4 *>(sh + 16 * kt + 4 * g4);
                 });
-            }
-        });
+            });
     };
     Ops o0, o1, o2;
     oload(o0, 0);
@@ -1816,19 +1827,20 @@ chunk_pipe_kernel(const ChunkParams p) {
 // then emitted reads of that MFMA's accumulators without the required wait
 // states (wrong outputs in token block 3).  Without the join there is no
 // such read.
-template <int DK, int CH, typename E, bool VEC, bool DELTA, bool HS>
+template <int DK, int CH, typename E, bool VEC, bool DELTA, bool HS, bool OUT = true>
 static void launch_pipe(const ChunkParams &p, int nw, int64_t state_blocks, hipStream_t stream) {
     const dim3 grid((unsigned)state_blocks);
     if constexpr (!VEC) {
         if (nw == 4) {
-            hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 4, 2, E, VEC, DELTA, HS>), grid, dim3(64 * 8), 0, stream, p);
+            hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 4, 2, E, VEC, DELTA, HS, OUT>), grid, dim3(64 * 8), 0, stream,
+                               p);
             return;
         }
     }
     if (nw == 2)
-        hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 2, 4, E, VEC, DELTA, HS>), grid, dim3(64 * 8), 0, stream, p);
+        hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 2, 4, E, VEC, DELTA, HS, OUT>), grid, dim3(64 * 8), 0, stream, p);
     else
-        hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 1, 4, E, VEC, DELTA, HS>), grid, dim3(64 * 7), 0, stream, p);
+        hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 1, 4, E, VEC, DELTA, HS, OUT>), grid, dim3(64 * 7), 0, stream, p);
 }
 
 template <int DK, int CH, typename E, int GATE, bool DELTA>
@@ -1838,7 +1850,10 @@ static void launch_state(const ChunkParams &p, int nw, int64_t state_blocks, hip
         constexpr bool VEC = GATE == 2;
         if constexpr (DELTA) {
             if (p.hs) {                                       // a training forward: entry states saved
-                launch_pipe<DK, CH, E, VEC, true, true>(p, nw, state_blocks, stream);
+                if (p.states_only)                            // the backward's walk: no outputs
+                    launch_pipe<DK, CH, E, VEC, true, true, false>(p, nw, state_blocks, stream);
+                else
+                    launch_pipe<DK, CH, E, VEC, true, true>(p, nw, state_blocks, stream);
                 return;
             }
         }

@@ -1807,7 +1807,9 @@ static hipError_t run_bwd(ChunkBwdParams p, bool saved, hipStream_t stream) {
     // their own operands, 1.00 ms with producers; 1.02 ms with 64-column tiles).
     if (units > 0) {
         p.n_tiles = (p.DV + 31) / 32;
-        if (!saved)                                            // else a training forward stored the states
+        // 16-bit: the states came from the forward's state kernel (chunk_bwd), or a
+        // training forward stored them
+        if (!saved && sizeof(E) == 4)
             hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
                                dim3(256), 0, stream, p);
         hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
@@ -1863,10 +1865,18 @@ hipError_t chunk_bwd(int dtype, int dk, int chunk, int gate_vector, const ChunkP
     if (p.fz.qk_l2norm || (p.fz.gate_act && (!vec || !p.dpart || !p.dA_log || !p.ddt_bias || !p.dg)))
         return hipErrorInvalidValue;
     // TE, A and the gate factors of every chunk, as the forward built them
-    // (already in the workspace after a saving forward); the per-channel gate
-    // also runs the forward's state kernel for the entry states
+    // (already in the workspace after a saving forward); with 16-bit elements
+    // the forward's state kernel, run for the entry states alone (no outputs),
+    // also walks the chunks (fp32: chunk_hs_kernel, in run_bwd)
     if (!saved) {
-        hipError_t e = chunk_fwd(dtype, dk, chunk, vec ? 1 : 0, fwd, table, vec ? CHUNK_PREP | CHUNK_STATE : CHUNK_PREP,
+        ChunkParams f = fwd;
+        const bool walk = dtype != 0;
+        if (walk) {
+            f.hs = p.hs;
+            f.h0 = p.h0;
+            f.states_only = 1;
+        }
+        hipError_t e = chunk_fwd(dtype, dk, chunk, vec ? 1 : 0, f, table, walk ? CHUNK_PREP | CHUNK_STATE : CHUNK_PREP,
                                  stream);
         if (e != hipSuccess) return e;
     }

@@ -92,6 +92,8 @@ struct ChunkParams {
     int te_identity;              // (with use_delta) the recurrence without the delta rule, U = V, in the
                                   // delta form's blocks: TE = I and GX = 0 (per-channel gate: a zero K*G
                                   // tile); beta is not read.  For the chunked backward of that recurrence.
+    int states_only;              // (with hs, 16-bit) the state kernel stores the entry states and computes
+                                  // no outputs (o is not written): the backward's entry-state walk
 };
 
 // Backward of the chunked scan (scalar gate, per-channel gate or none, delta
