@@ -139,23 +139,49 @@ struct CkptRegs {
 // so each is one 8-byte (16-bit types) or 16-byte (fp32) store.  Tiles above
 // the diagonal are written as zeros (chunk_prep leaves them unwritten, except
 // the partner of a diagonal tile pair, and zeros inside the diagonal tiles).
-template <typename E, int CH, int NT>
+//
+// LIVE (16-bit, four row blocks): only the six tile pairs (I, q) with 2 q <= I
+// are copied (unit n of the copy is unit n % 64 of the (n / 64)-th of them);
+// the other two pairs hold only tiles above the diagonal, zero_dead() writes
+// their tiles as zeros once and no later store touches them.
+template <typename E, int CH, int NT, bool LIVE = false>
 struct BlockRegs {
-    static constexpr int VE = 16 / (int)sizeof(E), UNITS = CH * CH / VE, N = (UNITS + NT - 1) / NT;
+    static constexpr int VE = 16 / (int)sizeof(E), ALL = CH * CH / VE;
     static constexpr int NB = CH / 16;
+    static_assert(!LIVE || (sizeof(E) == 2 && NB == 4), "live pairs: 16-bit, 64-token blocks");
+    static constexpr int UNITS = LIVE ? 384 : ALL, N = (UNITS + NT - 1) / NT;
     typedef E V __attribute__((ext_vector_type(VE)));
     V x[N];
+    // unit of the block that copy unit n holds
+    __device__ static __forceinline__ int unit(int n) {
+        if constexpr (LIVE) {
+            const int j = n >> 6;                                          // 0..5 -> pairs 0, 2, 4, 5, 6, 7
+            return ((j == 0 ? 0 : (j == 1 ? 2 : j + 2)) << 6) + (n & 63);
+        } else {
+            return n;
+        }
+    }
     __device__ __forceinline__ void load(const E *blk, int tid) {
         unroll<N>([&](auto i) __attribute__((always_inline)) {
-            const int u = tid + (int)i * NT;
-            x[i] = *reinterpret_cast<const V *>(blk + (u < UNITS ? u : 0) * VE);
+            const int n = tid + (int)i * NT;
+            x[i] = *reinterpret_cast<const V *>(blk + unit(n < UNITS ? n : 0) * VE);
         });
+    }
+    // the tiles of the pairs LIVE skips: rows 0 .. 31, columns 32 .. 63
+    __device__ static __forceinline__ void zero_dead(E *dst, int pitch, int tid) {
+        if constexpr (LIVE) {
+            using F = typename Elem<E>::frag;
+            for (int f = tid; f < 32 * 8; f += NT) {                       // 4-column fragments
+                const int row = f >> 3, c = 32 + 4 * (f & 7);
+                *reinterpret_cast<F *>(dst + row * pitch + c) = F{};
+            }
+        }
     }
     __device__ __forceinline__ void store(E *dst, int pitch, int tid) const {
         using F = typename Elem<E>::frag;
         unroll<N>([&](auto i) __attribute__((always_inline)) {
-            const int u = tid + (int)i * NT;
-            if (u < UNITS) {
+            const int n = tid + (int)i * NT, u = unit(n);
+            if (n < UNITS) {
                 const int p = u * VE;                              // first element of the unit
                 const int ln = (p >> 3) & 63, pr = p >> 9;         // pr = I (NB / 2) + q
                 const int I = pr / (NB / 2), q = pr % (NB / 2);
@@ -519,7 +545,9 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
         RowRegs<E, CH, DW, NTP> rdo;                            // dO rows, the tile's columns
         const int cb = u.tile * DW;
         const E *dot = reinterpret_cast<const E *>(p.dout) + (int64_t)h * DV + cb;
-        BlockRegs<E, CH, NTP> rte, ra;
+        constexpr bool LIVEB = sizeof(E) == 2 && CH == 64;     // TE, A: the six pairs that can be nonzero
+        using BR = BlockRegs<E, CH, NTP, LIVEB>;
+        BR rte, ra;
         constexpr int NG = VEC ? DK : 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
         float gv[GPT];
         auto fetch = [&](int c) __attribute__((always_inline)) {
@@ -563,6 +591,10 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
                 if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = gv[i];
         };
         if (nchunks == 0) return;
+        BR::zero_dead(TE0, PT, ptid);
+        BR::zero_dead(TE1, PT, ptid);
+        BR::zero_dead(Am0, PT, ptid);
+        BR::zero_dead(Am1, PT, ptid);
         fetch(nchunks - 1);
         put(SlotTag<0>{}, nchunks - 1);
         __syncthreads();
