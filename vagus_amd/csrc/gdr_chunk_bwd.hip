@@ -1051,16 +1051,14 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         float *gwb = p.gw + (slot * H + h) * grad_vec_work_floats(CH, DK);
         float *gQ = gwb, *gX = gwb + CH * DK, *gE = gwb + 2 * CH * DK;
         float *gA = gwb + 3 * CH * DK, *gT = gA + CH * CH, *gC = gT + CH * CH;
+        // dO S^T, dX S^T, U dS'^T transposed ([DK][CH]): a lane's four C-layout rows
+        // of one key are one 16-byte unit (and chunk_grad_vec_kernel reads them so)
 #pragma unroll
         for (int s = 0; s < JPW; ++s) {
-            const int d = 16 * (J0 + s) + r16;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int i = 16 * Iw + 4 * g4 + j;
-                gQ[i * DK + d] = aQ[s][j];
-                gX[i * DK + d] = aX[s][j];
-                gE[i * DK + d] = aE[s][j];
-            }
+            const int d = 16 * (J0 + s) + r16, i0 = 16 * Iw + 4 * g4;
+            *reinterpret_cast<f32x4 *>(gQ + d * CH + i0) = aQ[s];
+            *reinterpret_cast<f32x4 *>(gX + d * CH + i0) = aX[s];
+            *reinterpret_cast<f32x4 *>(gE + d * CH + i0) = aE[s];
         }
 #pragma unroll
         for (int s = 0; s < LPW; ++s) {
@@ -1630,14 +1628,9 @@ __global__ void __launch_bounds__(512) chunk_grad_vec_kernel(const ChunkBwdParam
 #pragma unroll
     for (int s = 0; s < IPW; ++s) {
         const int I = wave / NCT + WPC * s;
-        float dqg[4], dxs[4], dke[4];
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-            const int i = 16 * I + 4 * g4 + jj;
-            dqg[jj] = gQ[i * DK + cc];
-            dxs[jj] = gX[i * DK + cc];
-            dke[jj] = gE[i * DK + cc];
-        }
+        // rows 16 I + 4 g .. + 3 of key cc (the work area holds the sums transposed)
+        f32x4 dqg = ld4(gQ + cc * CH + 16 * I + 4 * g4), dxs = ld4(gX + cc * CH + 16 * I + 4 * g4),
+              dke = ld4(gE + cc * CH + 16 * I + 4 * g4);
         const bool exact = flag[I] != 0;                     // uniform over the workgroup
         const float gref = gms[16 * I * DK + cc], gend = gms[(16 * I + 15) * DK + cc];
         f32x4 sa = {0.f, 0.f, 0.f, 0.f}, sn = sa, tj = sa;
