@@ -1099,6 +1099,8 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     }
     __syncthreads();
     // dA: the A terms of dgamma; W_A = scale dA * D kept in aA.  dTE -> Fdte.  N -> Fn.
+    // D and N of the wave's own tile elements stay in registers for the dM step.
+    float Dk[LPW][4], Nk[LPW][4];
 #pragma unroll
     for (int s = 0; s < LPW; ++s) {
         const int l = wave + NW * s;
@@ -1120,7 +1122,9 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 cs += rs[j];
                 aA[s][j] = p.scale * da * D;
                 Fdte[i * PF + jj] = low ? aT[s][j] : 0.f;
-                Fn[i * PF + jj] = jj < i ? kk[j] * D : 0.f;
+                Nk[s][j] = jj < i ? kk[j] * D : 0.f;
+                Dk[s][j] = D;
+                Fn[i * PF + jj] = Nk[s][j];
             }
             cs += __shfl_xor(cs, 16);
             cs += __shfl_xor(cs, 32);
@@ -1204,13 +1208,13 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 const int i = 16 * I + 4 * g4 + j;
                 const bool strict = jj < i;
                 const float dm = strict ? -m[j] : 0.f;
-                const float n = Fn[i * PF + jj];                 // 0 off the strict lower triangle
+                const float n = Nk[s][j];                        // 0 off the strict lower triangle
                 const float dn = bet[i] * dm;
                 rb[j] = dm * n;
                 rg[j] = dn * n;
                 cg += dn * n;
                 if (strict) {
-                    const E wn = EL::from_f(dn * __expf(gam[i] - gam[jj]));
+                    const E wn = EL::from_f(dn * Dk[s][j]);
                     WS[i * PT + jj] = wn;
                     WS[jj * PT + i] = wn;
                 }
