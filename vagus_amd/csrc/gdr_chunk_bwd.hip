@@ -1246,14 +1246,14 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         float rq[4] = {0.f, 0.f, 0.f, 0.f}, rx[4] = {0.f, 0.f, 0.f, 0.f}, re[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < JPW; ++s) {
-            const int d = 16 * (J0 + s) + r16;
+            // q, k at rows 16 Iw + 4 g .. + 3 of column 16 (J0 + s) + r: one transpose read each
+            const f32x4 qv = EL::tof(ld_colfrag<E>(Qs, PK, 16 * Iw, 16 * (J0 + s), lane));
+            const f32x4 kv = EL::tof(ld_colfrag<E>(Ks, PK, 16 * Iw, 16 * (J0 + s), lane));
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const int i = 16 * Iw + 4 * g4 + j;
-                const float qv = EL::to_f(Qs[i * PK + d]), kv = EL::to_f(Ks[i * PK + d]);
-                rq[j] += qv * aQ[s][j];
-                rx[j] += kv * aX[s][j];
-                re[j] += kv * aE[s][j];
+                rq[j] += qv[j] * aQ[s][j];
+                rx[j] += kv[j] * aX[s][j];
+                re[j] += kv[j] * aE[s][j];
             }
         }
         float ce = 0.f;
