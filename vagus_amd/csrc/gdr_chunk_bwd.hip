@@ -820,9 +820,11 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     E *Ss = Ys + DVB * PT;                        // Ss[c][d] = S[d][c]
     E *dSs = Ss + DVB * PK;
     // CH x CH phase
+    // N, dTE and T0 are stored transposed (element (i, j) at [j][i]), so that the
+    // products below read their column operands as 16-byte rows; Z row-major
     float *Fn = reinterpret_cast<float *>(R);
     float *Fdte = Fn + CH * PF;
-    float *Ft0 = Fdte + CH * PF;                  // T0, then Z
+    float *Ft0 = Fdte + CH * PF;                  // T0 (transposed), then Z
     E *WA = reinterpret_cast<E *>(Ft0 + CH * PF);
     E *WS = WA + CH * PT;
     float *sm = reinterpret_cast<float *>(R + L::REGION);
@@ -875,19 +877,6 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         J = l;
         while (J > I) { J -= I + 1; ++I; }
     };
-    // A at this wave's dA elements (the A terms of dgamma)
-    E aval[LPW][4];                                            // raw: converted where used
-#pragma unroll
-    for (int s = 0; s < LPW; ++s) {
-        const int l = wave + NW * s;
-        int I = 0, J = 0;
-        if (l < NL) tile_of(l, I, J);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int i = 16 * I + 4 * g4 + j, jj = 16 * J + r16;
-            aval[s][j] = Ab[blk_pos<NB>(i, jj <= i ? jj : i)];
-        }
-    }
     // The column phase's global operands of one dv block, as whole 16-byte
     // units: S and dS' columns (the checkpoints' contiguous runs), and the V, dO,
     // dX rows.  Loaded a dv block ahead: block 0 with the staging loads, block
@@ -946,6 +935,19 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         if (lane < CH) gam[lane] = x;
     }
     __syncthreads();
+    // A at this wave's dA elements (the A terms of dgamma): rows 16 I + 4 g .. + 3
+    // of column 16 J + r of the staged A block (zero above the diagonal), one
+    // transpose read per tile
+    typename EL::frag aval[LPW];
+    if constexpr (!VEC) {
+#pragma unroll
+        for (int s = 0; s < LPW; ++s) {
+            const int l = wave + NW * s;
+            int I = 0, J = 0;
+            if (l < NL) tile_of(l, I, J);
+            aval[s] = ld_colfrag<E>(Am, PT, 16 * I, 16 * J, lane);
+        }
+    }
 
     // ---- column phase: dv blocks of DVB columns ---------------------------
     // then every wave accumulates its tiles of the products that contract over dv
@@ -1121,10 +1123,10 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 rs[j] = da * EL::to_f(aval[s][j]);
                 cs += rs[j];
                 aA[s][j] = p.scale * da * D;
-                Fdte[i * PF + jj] = low ? aT[s][j] : 0.f;
+                Fdte[jj * PF + i] = low ? aT[s][j] : 0.f;
                 Nk[s][j] = jj < i ? kk[j] * D : 0.f;
                 Dk[s][j] = D;
-                Fn[i * PF + jj] = Nk[s][j];
+                Fn[jj * PF + i] = Nk[s][j];
             }
             cs += __shfl_xor(cs, 16);
             cs += __shfl_xor(cs, 32);
@@ -1148,12 +1150,12 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             f32x4 t = {0.f, 0.f, 0.f, 0.f};
             for (int kb = J; kb <= I; ++kb)
                 t = mfma_kb1(EL::tof(ld_frag<E>(TEs + (16 * I + r16) * PT + 16 * kb + 4 * g4)),
-                             col4(Fn, PF, 16 * kb + 4 * g4, 16 * J + r16), t);
+                             ld4(Fn + (16 * J + r16) * PF + 16 * kb + 4 * g4), t);
             const int jj = 16 * J + r16;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int i = 16 * I + 4 * g4 + j;
-                Ft0[i * PF + jj] = jj <= i ? (i == jj ? 1.f : 0.f) - t[j] : 0.f;
+                Ft0[jj * PF + i] = jj <= i ? (i == jj ? 1.f : 0.f) - t[j] : 0.f;
             }
         }
     }
@@ -1168,8 +1170,8 @@ chunk_grad_kernel(const ChunkBwdParams p) {
             int I, J;
             tile_of(l, I, J);
             for (int kb = I; kb < NB; ++kb)
-                zt[s] = mfma_kb1(col4(Ft0, PF, 16 * kb + 4 * g4, 16 * I + r16),
-                                 col4(Fdte, PF, 16 * kb + 4 * g4, 16 * J + r16), zt[s]);
+                zt[s] = mfma_kb1(ld4(Ft0 + (16 * I + r16) * PF + 16 * kb + 4 * g4),
+                                 ld4(Fdte + (16 * J + r16) * PF + 16 * kb + 4 * g4), zt[s]);
             if (I == J) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
