@@ -436,7 +436,7 @@ def bench_backward(torch, ops, workloads, steps, warmup):
     del xs, dos
     tflops = th * 2 * FLOP_PER_TOKEN_HEAD / (us * 1e-6) / 1e12
     return {'workload': 'gdn_340m backward: dq, dk, dv, dg, dbeta, dh0 from do and dht, B8 T4096 H8 dk=dv=128 bf16',
-            'kernels': 'chunk_prep_kernel + chunk_hs_kernel + chunk_dhs_kernel + chunk_grad_kernel',
+            'kernels': 'chunk_prep_kernel + chunk_pipe_kernel (entry states only) + chunk_dhs_kernel + chunk_grad_kernel',
             'us': round(us, 1), 'tok_s': round(x0.q.shape[0] * x0.q.shape[1] / (us * 1e-6), 1),
             'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
             'frac_mfma': round(tflops / PEAK_BF16_TFLOPS, 5),
@@ -500,7 +500,7 @@ def bench_kda_backward(torch, ops, workloads, steps, warmup, token_walk=True):
     tflops = th * 2 * FLOP_PER_TOKEN_HEAD / (us * 1e-6) / 1e12
     r = {'workload': 'kda_prefill backward: dq, dk, dv, dg (per channel), dbeta, dh0 from do and dht, '
                      'B4 T8192 H8 dk=dv=128 bf16',
-         'kernels': 'chunk_prep_kernel + chunk_pipe_kernel (entry states) + chunk_dhs_kernel + chunk_grad_kernel '
+         'kernels': 'chunk_prep_kernel + chunk_pipe_kernel (entry states only) + chunk_dhs_kernel + chunk_grad_kernel '
                     '+ chunk_grad_vec_kernel',
          'us': round(us, 1), 'tok_s': round(B * T / (us * 1e-6), 1),
          'flop_per_token_head': 2 * FLOP_PER_TOKEN_HEAD, 'achieved_tflops': round(tflops, 2),
