@@ -190,6 +190,10 @@ __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0); }
 // ===========================================================================
 // chunk_prep_kernel: per (chunk, head) TE and A
 // ===========================================================================
+// the 16x16x32 operand type of a 16-bit element (a placeholder otherwise)
+template <typename EL, bool B> struct Frag2Of { using type = f32x4; };
+template <typename EL> struct Frag2Of<EL, true> { using type = typename EL::frag2; };
+
 template <int DK, int CH, typename E, int GATE, bool WR = false>
 struct PrepLayout {
     static constexpr int PF = CH + 4, PG = DK + 4;
@@ -200,13 +204,25 @@ struct PrepLayout {
     // all: 53 KB at dk = 128, C = 64, three workgroups per CU instead of two
     // (measured: the kernel's time follows its occupancy, 218 us at one
     // workgroup per CU, 137 at two).
-    static constexpr bool QREG = GATE == 2;
+    // Scalar gate or none, 16-bit, C = 64 (LEAN): each wave owns one row block
+    // and takes its Q rows as MFMA operands straight from global memory (no Q
+    // stage); M and T are kept as their lower 16x16 tiles; A and M are written
+    // as each product finishes, M into a region of its own, and T then reuses
+    // the K stage.  29 KB at dk = 128 (35 KB before): five workgroups per CU
+    // (measured at gdn_340m: 47.8 -> 45.1 us; six, with M held in registers
+    // until the barrier and 26 KB, ran no faster and lengthened every
+    // workgroup's loads).
+    static constexpr bool LEAN = GATE != 2 && sizeof(E) == 2 && CH == 64 && !WR;
+    static constexpr int TP = 20;                                  // LEAN: row pitch of a lower tile (floats)
+    static constexpr int MT = NL * 16 * TP * 4;                    // LEAN: one matrix as lower tiles
+    static constexpr bool QREG = GATE == 2 || LEAN;
     static constexpr bool FAST = GATE == 2 && sizeof(E) == 2;
     static constexpr int STAGE = ((WR ? 2 : 1) + (QREG ? 0 : 1)) * CH * DK * (int)sizeof(E);  // K (Q, W) rows, swizzled
     static constexpr int GAMB = GATE == 2 ? CH * PG * 4 : 0;      // cumulative decay per channel
     static constexpr int NORM = GATE == 2 ? 2 * CH * 4 : 0;       // rows' L2-norm factors of K, Q
     static constexpr int GTILES = FAST ? 3 * CH * DK * (int)sizeof(E) + NL * DK * 4 : 0;  // Qh, Kh, Kt, pair factors
-    static constexpr int SOLVE = 2 * CH * PF * 4;                  // M, T
+    static constexpr int MOFF = LEAN ? cmax(STAGE, MT) : 0;        // byte offset of M (LEAN: past the stage)
+    static constexpr int SOLVE = LEAN ? MOFF + MT : 2 * CH * PF * 4;  // M, T
     static constexpr int UNION = cmax(cmax(STAGE + GAMB + NORM, GTILES), SOLVE);
 };
 
@@ -216,7 +232,8 @@ struct PrepLayout {
 // TE = (I + M)^-1 (no beta), and the third gated tile is W * Gend; the state
 // kernel is the per-channel one, unchanged.
 template <int DK, int CH, typename E, int GATE, bool WR = false>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GATE == 2 && DK == 128 && !WR ? 3 : 1)))
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(
+    GATE == 2 && DK == 128 && !WR ? 3 : (PrepLayout<DK, CH, E, GATE, WR>::LEAN ? 5 : 1))))
 chunk_prep_kernel(const ChunkParams p) {
     static_assert(!WR || GATE == 2, "the explicit write runs on the per-channel-gate path");
     using EL = Elem<E>;
@@ -247,8 +264,15 @@ chunk_prep_kernel(const ChunkParams p) {
     float *gam = GATE == 2 ? reinterpret_cast<float *>(smem + L::STAGE) : gam_s;
     float *rkf = GATE == 2 ? reinterpret_cast<float *>(smem + L::STAGE + L::GAMB) : rkf_s;
     float *rqf = GATE == 2 ? rkf + CH : rqf_s;
-    float *Mf = reinterpret_cast<float *>(smem);                // after the products are done
-    float *Tf = Mf + CH * PF;
+    // M and T after the products are done (LEAN: M from the products on);
+    // mpos(I, J, r, c): element (16 I + r, 16 J + c) of a lower tile, rows RS apart
+    float *Mf = reinterpret_cast<float *>(smem + L::MOFF);
+    float *Tf = L::LEAN ? reinterpret_cast<float *>(smem) : Mf + CH * PF;
+    constexpr int RS = L::LEAN ? L::TP : PF;
+    auto mpos = [](int I, int J, int r, int c) __attribute__((always_inline)) {
+        if constexpr (L::LEAN) return ((I * (I + 1) / 2 + J) * 16 + r) * L::TP + c;
+        else return (16 * I + r) * PF + 16 * J + c;
+    };
 
     const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g4 = lane >> 4, r16 = lane & 15;
@@ -323,7 +347,18 @@ chunk_prep_kernel(const ChunkParams p) {
     rk.load(kg, sqk, clen, DK, tid);
     if constexpr (WR)
         rw.load(reinterpret_cast<const E *>(p.w) + t0 * sqk + (int64_t)h * DK, sqk, clen, DK, tid);
-    rq.load(qg, sqk, clen, DK, tid);
+    // LEAN: this wave's Q rows 16 wave + r, as operands of 16x16x32 products whose
+    // k slots are 32 m + 8 g .. + 7 (16-byte loads; rows past the end zeroed below)
+    using V8 = typename Frag2Of<EL, L::LEAN>::type;
+    V8 qfr[L::LEAN ? NKB / 2 : 1];
+    if constexpr (L::LEAN) {
+        const int qrow = 16 * wave + r16;
+        const E *qsrc = qg + (int64_t)(qrow < clen ? qrow : 0) * sqk + 8 * g4;
+#pragma unroll
+        for (int m = 0; m < NKB / 2; ++m) qfr[m] = *reinterpret_cast<const V8 *>(qsrc + 32 * m);
+    } else {
+        rq.load(qg, sqk, clen, DK, tid);
+    }
     if (wave == 0 && lane < CH)
         bet[lane] = lane < clen ? (WR ? 1.f : (fz.beta_sigmoid ? sigmoidf_(beta_v) : beta_v)) : 0.f;
     if constexpr (GATE == 2) {
@@ -369,7 +404,24 @@ chunk_prep_kernel(const ChunkParams p) {
     if constexpr (sizeof(E) == 2) {
         if (fz.qk_l2norm) {                                     // normalised rows, factors in rkf / rqf
             rk.l2norm_rows(rkf, tid);
-            rq.l2norm_rows(rqf, tid);
+            if constexpr (L::LEAN) {
+                // the row's sum of squares over its four lanes (l, l ^ 16, l ^ 32, l ^ 48)
+                float ss = 0.f;
+#pragma unroll
+                for (int m = 0; m < NKB / 2; ++m)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) ss += (float)qfr[m][e] * (float)qfr[m][e];
+                ss += __shfl_xor(ss, 16);
+                ss += __shfl_xor(ss, 32);
+                const float f = rsqrtf(ss + 1e-6f);
+#pragma unroll
+                for (int m = 0; m < NKB / 2; ++m)
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) qfr[m][e] = (E)((float)qfr[m][e] * f);
+                if (g4 == 0) rqf[16 * wave + r16] = f;
+            } else {
+                rq.l2norm_rows(rqf, tid);
+            }
         }
     }
     // ---- per-channel gate, 16-bit: one pass over the thread's K, Q (W) units
@@ -513,8 +565,8 @@ chunk_prep_kernel(const ChunkParams p) {
             return job < NL;
         }
     };
-    F bq_rb[RB ? NKB : 1], bk_rb[RB ? NKB : 1];                 // row block I = wave, read once
-    if constexpr (RB) {
+    F bq_rb[RB && !L::LEAN ? NKB : 1], bk_rb[RB && !L::LEAN ? NKB : 1];  // row block I = wave, read once
+    if constexpr (RB && !L::LEAN) {
 #pragma unroll
         for (int kt = 0; kt < NKB; ++kt) {
             const int cc = 16 * kt + 4 * g4, irow = 16 * wave + r16;
@@ -581,9 +633,36 @@ chunk_prep_kernel(const ChunkParams p) {
             }
         }
     }
+    if constexpr (L::LEAN) {
+        // row block I = wave against J = 0 .. I; A and M of each tile stored at once
+        static_assert(RB, "one row block per wave");
+        const int I = wave, irow = 16 * I + r16;
+        if (irow >= clen) {
+#pragma unroll
+            for (int m = 0; m < NKB / 2; ++m) qfr[m] = V8{};
+        }
+        V8 bkr[NKB / 2];
+#pragma unroll
+        for (int m = 0; m < NKB / 2; ++m) bkr[m] = *reinterpret_cast<const V8 *>(Kst + SK::at(irow, 32 * m + 8 * g4));
+        unroll<NB>([&](auto Jc) {
+            constexpr int J = Jc;
+            if (J > I) return;
+            const int jrow = 16 * J + r16;
+            f32x4 accq = {0.f, 0.f, 0.f, 0.f}, acck = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int m = 0; m < NKB / 2; ++m) {
+                const V8 a = *reinterpret_cast<const V8 *>(Kst + SK::at(jrow, 32 * m + 8 * g4));
+                accq = mfma_pair(a, qfr[m], accq);
+                acck = mfma_pair(a, bkr[m], acck);
+            }
+            job_tail(J, I, J, irow, accq, acck);
+            st_frag<E>(blk + CH * CH + frag_pos<NB>(I, J, lane), EL::cvt(res_q[J]));
+            if (p.use_delta) st4(Mf + mpos(I, J, r16, 4 * g4), res_k[J]);
+        });
+    }
 #pragma unroll
     for (int s = 0; s < JPW; ++s) {
-        if (fast) break;
+        if (fast || L::LEAN) break;
         res_q[s] = res_k[s] = f32x4{0.f, 0.f, 0.f, 0.f};
         int I, J;
         if (!job_ij(s, I, J)) continue;
@@ -671,9 +750,9 @@ chunk_prep_kernel(const ChunkParams p) {
 #pragma unroll
     for (int s = 0; s < JPW; ++s) {
         int I, J;
-        if (!job_ij(s, I, J)) continue;
-        st_frag<E>(blk + CH * CH + frag_pos<NB>(I, J, lane), EL::cvt(res_q[s]));
-        if (p.use_delta) st4(Mf + (16 * I + r16) * PF + 16 * J + 4 * g4, res_k[s]);
+        if (L::LEAN || !job_ij(s, I, J)) continue;
+        if (!L::LEAN) st_frag<E>(blk + CH * CH + frag_pos<NB>(I, J, lane), EL::cvt(res_q[s]));
+        if (p.use_delta) st4(Mf + mpos(I, J, r16, 4 * g4), res_k[s]);
     }
     // the upper tile (I, I + 1) shares a pair with diagonal tile (I, I) for even I: zeros
     if (wave < NB / 2) {
@@ -703,7 +782,7 @@ chunk_prep_kernel(const ChunkParams p) {
         float t[16];
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float *mrow = Mf + (16 * b + i) * PF + 16 * b;
+            const float *mrow = Mf + mpos(b, b, i, 0);
             float acc = (i == jc) ? 1.f : 0.f;
 #pragma unroll
             for (int m4 = 0; m4 < 16; m4 += 4) {
@@ -716,7 +795,7 @@ chunk_prep_kernel(const ChunkParams p) {
             t[i] = acc;
         }
 #pragma unroll
-        for (int i = 0; i < 16; ++i) Tf[(16 * b + i) * PF + 16 * b + jc] = t[i];
+        for (int i = 0; i < 16; ++i) Tf[mpos(b, b, i, jc)] = t[i];
     }
     __syncthreads();
     // off-diagonal blocks by distance: T_IJ = -T_II sum_{K=J}^{I-1} M_IK T_KJ
@@ -726,14 +805,12 @@ chunk_prep_kernel(const ChunkParams p) {
             const int I = J + dist;
             f32x4 X = {0.f, 0.f, 0.f, 0.f};
             for (int K = J; K < I; ++K) {
-                const float *tc = Tf + (16 * K + 4 * g4) * PF + 16 * J + r16;    // column of T_KJ
-                X = mfma_kb1(ld4(Mf + (16 * I + r16) * PF + 16 * K + 4 * g4),
-                             f32x4{tc[0], tc[PF], tc[2 * PF], tc[3 * PF]}, X);
+                const float *tc = Tf + mpos(K, J, 4 * g4, r16);                   // column of T_KJ
+                X = mfma_kb1(ld4(Mf + mpos(I, K, r16, 4 * g4)), f32x4{tc[0], tc[RS], tc[2 * RS], tc[3 * RS]}, X);
             }
-            const f32x4 Y = mfma_kb1(ld4(Tf + (16 * I + r16) * PF + 16 * I + 4 * g4), X,
-                                     f32x4{0.f, 0.f, 0.f, 0.f});
+            const f32x4 Y = mfma_kb1(ld4(Tf + mpos(I, I, r16, 4 * g4)), X, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int j = 0; j < 4; ++j) Tf[(16 * I + 4 * g4 + j) * PF + 16 * J + r16] = -Y[j];
+            for (int j = 0; j < 4; ++j) Tf[mpos(I, J, 4 * g4 + j, r16)] = -Y[j];
         }
         __syncthreads();
     }
@@ -742,7 +819,7 @@ chunk_prep_kernel(const ChunkParams p) {
         int I = 0, kb = tjob;
         while (kb > I) { kb -= I + 1; ++I; }
         const int row = 16 * I + r16, c0 = 16 * kb + 4 * g4;
-        f32x4 t = ld4(Tf + row * PF + c0) * ld4(bet + c0);
+        f32x4 t = ld4(Tf + mpos(I, kb, r16, 4 * g4)) * ld4(bet + c0);
 #pragma unroll
         for (int e = 0; e < 4; ++e)
             if (c0 + e > row) t[e] = 0.f;
