@@ -9,9 +9,10 @@ states (entry state 0.1 N(0,1)); a step is one `chunk_gated_delta_rule` call
 over the whole batch with its inputs resident in HBM; value = tokens/s
 (B*T tokens per step).  Three copies of the inputs (3 x 218 MB) are rotated
 so that no step finds its operands in the 256 MB Infinity Cache.  Before
-any timed leg, a fixed clock-settle phase (--settle, default 2 s of untimed
-headline steps, reported as settle_s) brings the GPU's clocks to their loaded
-state, so a short --warmup times the same level as a long one.
+the timed headline steps, a fixed clock-settle phase (--settle, default 2 s of
+untimed steps on the same rotating copies, right before the warmup, reported
+as settle_s) brings the GPU's clocks to their loaded state, so a short
+--warmup times the same level as a long one; the later legs follow it.
 
 The prefill runs as two kernels per call: chunk_prep (every (chunk, head) in
 parallel: the intra-chunk Q K^T and K K^T products and the triangular
@@ -87,8 +88,8 @@ STATE_BYTES_PER_TOKEN_HEAD = 2 * (2 * DK + DV) + 4 + 2 * 2 * CHUNK + 2 * DV + 2 
 # untimed replays before them, each replay 24 launches
 GRAPH_REPLAYS = 30
 GRAPH_WARM_REPLAYS = 10
-# default clock-settle phase: back-to-back headline prefill steps before the warmup, outside the
-# timed region (short runs after an idle GPU otherwise time the first steps up to 8% slow)
+# default clock-settle phase: back-to-back headline prefill steps right before the warmup, outside
+# the timed region (short runs after an idle GPU otherwise time the first steps up to 8% slow)
 SETTLE_S = 2.0
 
 
@@ -96,8 +97,11 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
-    """Timed chunked prefill.  Each step issues chunk_prep, an event, then
+def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3, settle_s=0.0):
+    """Timed chunked prefill.  `settle_s` seconds of untimed steps on the same
+    rotating copies come first (clock settle, right before the warmup: an idle
+    GPU, such as while the copies are generated, drops its clocks), then
+    `warmup` untimed steps.  Each step issues chunk_prep, an event, then
     chunk_state and another event on the current stream; returns host-clock
     totals and the two kernels' event-timed durations.  Two events per step,
     around the state kernel: a third at each step's start cost about 3 us per
@@ -114,6 +118,16 @@ def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
         ops.chunk_scan(x.q, x.k, x.v, x.g, x.beta, gate=gate, delta=True, initial_state=x.initial_state,
                        output_final_state=True, cu_seqlens=x.cu_seqlens, phase_event=mid)
 
+    settled = 0.0
+    if settle_s > 0:
+        t0 = time.perf_counter()
+        i = 0
+        while time.perf_counter() - t0 < settle_s:
+            for _ in range(20):
+                step(i)
+                i += 1
+            torch.cuda.synchronize()
+        settled = time.perf_counter() - t0
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
@@ -132,28 +146,10 @@ def bench_prefill(torch, ops, workloads, name, steps, warmup, copies=3):
     H = x0.q.shape[2]
     del xs
     op_ms = statistics.mean(p + q for p, q in zip(prep_ms, state_ms))
-    return dict(tokens=tokens, H=H, total_s=total, tok_s=steps * tokens / total,
+    return dict(tokens=tokens, H=H, total_s=total, tok_s=steps * tokens / total, settle_s=settled,
                 prep_ms=statistics.mean(prep_ms), state_ms=statistics.mean(state_ms), op_ms=op_ms,
                 path_tflops=tokens * H * FLOP_PER_TOKEN_HEAD / (op_ms * 1e-3) / 1e12,
                 state_tflops=tokens * H * STATE_FLOP_PER_TOKEN_HEAD / (statistics.mean(state_ms) * 1e-3) / 1e12)
-
-
-def settle(torch, ops, workloads, seconds):
-    """Untimed headline prefill steps, back to back, for `seconds` of host
-    clock (synchronised every few steps), so that the GPU's clocks have
-    reached their loaded state before any timed leg.  Returns the seconds
-    spent."""
-    if seconds <= 0:
-        return 0.0
-    x = workloads.workload('gdn_340m', device='cuda')
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        for _ in range(20):
-            ops.chunk_gated_delta_rule(x.q, x.k, x.v, x.g, x.beta, initial_state=x.initial_state,
-                                       output_final_state=True)
-        torch.cuda.synchronize()
-    del x
-    return time.perf_counter() - t0
 
 
 def time_steps(torch, fn, steps, warmup, rotate):
@@ -903,8 +899,8 @@ def main():
     ap.add_argument('--warmup', type=int, default=100)
     ap.add_argument('--no-cpu-baseline', action='store_true')
     ap.add_argument('--settle', type=float, default=SETTLE_S, metavar='SECONDS',
-                    help='clock-settle phase before the timed legs: back-to-back untimed headline prefill '
-                         f'steps for this long (default {SETTLE_S}; reported as settle_s)')
+                    help='clock-settle phase before the timed headline steps: back-to-back untimed prefill '
+                         f'steps on the same inputs for this long (default {SETTLE_S}; reported as settle_s)')
     ap.add_argument('--prefill-only', nargs='?', const='gdn_340m', default=None, metavar='WORKLOAD',
                     help='only one prefill workload: gdn_340m (default, the headline line), kda_prefill or '
                          'gdn_varlen (for profiling)')
@@ -982,10 +978,9 @@ def main():
                           'path_tflops': round(r['path_tflops'], 2), 'state_tflops': round(r['state_tflops'], 2)}),
               flush=True)
         return
-    log(f'[bench] clock settle: {args.settle:.1f} s of gdn_340m prefill steps')
-    settle_s = settle(torch, ops, workloads, args.settle)
-    log('[bench] prefill gdn_340m')
-    pre = bench_prefill(torch, ops, workloads, 'gdn_340m', args.steps, args.warmup)
+    log(f'[bench] prefill gdn_340m (after {args.settle:.1f} s of clock settle on the same steps)')
+    pre = bench_prefill(torch, ops, workloads, 'gdn_340m', args.steps, args.warmup, settle_s=args.settle)
+    settle_s = pre['settle_s']
     extra = {}
     if not args.prefill_only:
         log('[bench] decode 1.3B layer shape')
