@@ -239,16 +239,27 @@ __device__ __forceinline__ f32x4 col4(const float *m, int pitch, int k0, int c) 
     return f32x4{m[k0 * pitch + c], m[(k0 + 1) * pitch + c], m[(k0 + 2) * pitch + c], m[(k0 + 3) * pitch + c]};
 }
 
+// The sum over the 16 lanes of x's row (lanes 16 m .. 16 m + 15), in every lane
+// of the row, by DPP row rotations: four VALU adds instead of four dependent
+// __shfl_xor round trips through the LDS crossbar (ds_bpermute_b32).  Each lane
+// adds in its own order, so lanes of a row may differ in the last bit.
+template <int CTRL>
+__device__ __forceinline__ float row_rot(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
 __device__ __forceinline__ float sum16(float x) {
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) x += __shfl_xor(x, o);
+    x += row_rot<0x128>(x);                                   // row_ror:8
+    x += row_rot<0x124>(x);                                   // row_ror:4
+    x += row_rot<0x122>(x);                                   // row_ror:2
+    x += row_rot<0x121>(x);                                   // row_ror:1
     return x;
 }
-__device__ __forceinline__ float sum64(float x) {
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) x += __shfl_xor(x, o);
-    return x;
+// the sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (one lane of each row)
+__device__ __forceinline__ float sum_rows(float x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
 }
+__device__ __forceinline__ float sum64(float x) { return sum_rows(sum16(x)); }
 
 // (sequence, head, dv tile) of a walk workgroup; the dv tiles of one
 // (sequence, head) share an XCD (the forward state kernel's order)
@@ -1128,8 +1139,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 Dk[s][j] = D;
                 Fn[jj * PF + i] = Nk[s][j];
             }
-            cs += __shfl_xor(cs, 16);
-            cs += __shfl_xor(cs, 32);
+            cs = sum_rows(cs);
 #pragma unroll
             for (int j = 0; j < 4; ++j) rs[j] = sum16(rs[j]);
             if (r16 == 0) {
@@ -1224,8 +1234,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
                 WA[i * PT + jj] = EL::from_f(jj <= i ? aA[s][j] : 0.f);
                 if (jj < i) WA[jj * PT + i] = EL::from_f(0.f);      // the upper tiles
             }
-            cg += __shfl_xor(cg, 16);
-            cg += __shfl_xor(cg, 32);
+            cg = sum_rows(cg);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 rb[j] = sum16(rb[j]);
