@@ -551,76 +551,82 @@ __global__ void __launch_bounds__(64 * (NWC + NPW)) chunk_dhs_kernel(const Chunk
         const int ptid = tid - 64 * NWC;
         const E *kg = reinterpret_cast<const E *>(p.k) + (int64_t)h * DK;
         const E *qg = reinterpret_cast<const E *>(p.q) + (int64_t)h * DK;
-        RowRegs<E, CH, DK, NTP> rk, rq;
-        RowRegs<E, CH, VEC ? DK : 32, NTP> rke;                 // VEC: K*Gend rows
-        RowRegs<E, CH, DW, NTP> rdo;                            // dO rows, the tile's columns
         const int cb = u.tile * DW;
         const E *dot = reinterpret_cast<const E *>(p.dout) + (int64_t)h * DV + cb;
         constexpr bool LIVEB = sizeof(E) == 2 && CH == 64;     // TE, A: the six pairs that can be nonzero
         using BR = BlockRegs<E, CH, NTP, LIVEB>;
-        BR rte, ra;
         constexpr int NG = VEC ? DK : 3 * CH + 1, GPT = (NG + NTP - 1) / NTP;   // gate floats, per producer thread
-        float gv[GPT];
-        auto fetch = [&](int c) __attribute__((always_inline)) {
+        // one chunk's operands in registers; two sets, so that each chunk's loads
+        // are issued two steps before its LDS slot is filled (with one set, each
+        // fill waited for loads issued just before it)
+        struct Stage {
+            RowRegs<E, CH, DK, NTP> rk, rq;
+            RowRegs<E, CH, VEC ? DK : 32, NTP> rke;             // VEC: K*Gend rows
+            RowRegs<E, CH, DW, NTP> rdo;                        // dO rows, the tile's columns
+            BR rte, ra;
+            float gv[GPT];
+        };
+        auto fetch = [&](Stage &st, int c) __attribute__((always_inline)) {
             const int64_t t0 = u.bos + (int64_t)c * CH;
             const int clen = clen_of(c);
             const char *blkb = reinterpret_cast<const char *>(p.blocks) + ((u.cbase + c) * H + h) * CB::BYTES;
             if constexpr (VEC) {
                 const E *tiles = reinterpret_cast<const E *>(blkb) + CB::TEA;      // K*G, scale Q*G, K*Gend
-                rk.load(tiles, DK, CH, ptid);
-                rq.load(tiles + CH * DK, DK, CH, ptid);
-                rke.load(tiles + 2 * CH * DK, DK, CH, ptid);
+                st.rk.load(tiles, DK, CH, ptid);
+                st.rq.load(tiles + CH * DK, DK, CH, ptid);
+                st.rke.load(tiles + 2 * CH * DK, DK, CH, ptid);
             } else {
-                rk.load(kg + t0 * sqk, sqk, clen, ptid);
-                rq.load(qg + t0 * sqk, sqk, clen, ptid);
+                st.rk.load(kg + t0 * sqk, sqk, clen, ptid);
+                st.rq.load(qg + t0 * sqk, sqk, clen, ptid);
             }
-            rte.load(reinterpret_cast<const E *>(blkb), ptid);
-            ra.load(reinterpret_cast<const E *>(blkb) + CH * CH, ptid);
-            rdo.load(dot + t0 * sv, sv, clen, ptid, DV - cb);
+            st.rte.load(reinterpret_cast<const E *>(blkb), ptid);
+            st.ra.load(reinterpret_cast<const E *>(blkb) + CH * CH, ptid);
+            st.rdo.load(dot + t0 * sv, sv, clen, ptid, DV - cb);
 #pragma unroll
             for (int i = 0; i < GPT; ++i) {
                 const int gi = ptid + i * NTP;
-                gv[i] = reinterpret_cast<const float *>(blkb + CB::GOFF)[gi < NG ? gi : 0];
+                st.gv[i] = reinterpret_cast<const float *>(blkb + CB::GOFF)[gi < NG ? gi : 0];
             }
         };
-        auto put = [&](auto tag, int c) __attribute__((always_inline)) {
+        auto put = [&](auto tag, const Stage &st, int c) __attribute__((always_inline)) {
             constexpr int SL = decltype(tag)::value;
             const int clen = clen_of(c);
             if constexpr (VEC) {
-                rk.store_unpaired(SL ? Ks1 : Ks0, PK, ptid);
-                rq.store(SL ? Qs1 : Qs0, PK, CH, ptid);
-                rke.store_unpaired(SL ? KE1 : KE0, PK, ptid);
+                st.rk.store_unpaired(SL ? Ks1 : Ks0, PK, ptid);
+                st.rq.store(SL ? Qs1 : Qs0, PK, CH, ptid);
+                st.rke.store_unpaired(SL ? KE1 : KE0, PK, ptid);
             } else {
-                rk.store(SL ? Ks1 : Ks0, PK, clen, ptid);
-                rq.store(SL ? Qs1 : Qs0, PK, clen, ptid);
+                st.rk.store(SL ? Ks1 : Ks0, PK, clen, ptid);
+                st.rq.store(SL ? Qs1 : Qs0, PK, clen, ptid);
             }
-            rte.store(SL ? TE1 : TE0, PT, ptid);
-            ra.store(SL ? Am1 : Am0, PT, ptid);
-            rdo.store(SL ? dO1 : dO0, PD, clen, ptid, DV - cb);   // zero past the chunk's end and dv
+            st.rte.store(SL ? TE1 : TE0, PT, ptid);
+            st.ra.store(SL ? Am1 : Am0, PT, ptid);
+            st.rdo.store(SL ? dO1 : dO0, PD, clen, ptid, DV - cb);   // zero past the chunk's end and dv
 #pragma unroll
             for (int i = 0; i < GPT; ++i)
-                if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = gv[i];
+                if (ptid + i * NTP < NG) (SL ? gt1 : gt0)[ptid + i * NTP] = st.gv[i];
         };
         if (nchunks == 0) return;
         BR::zero_dead(TE0, PT, ptid);
         BR::zero_dead(TE1, PT, ptid);
         BR::zero_dead(Am0, PT, ptid);
         BR::zero_dead(Am1, PT, ptid);
-        fetch(nchunks - 1);
-        put(SlotTag<0>{}, nchunks - 1);
+        // step k works on chunk n - 1 - k from slot k & 1, filled during step k - 1
+        // from register set k & 1, whose loads were issued during step k - 2
+        auto chunk_of = [&](int k) __attribute__((always_inline)) { return nchunks - 1 - k; };
+        Stage s0, s1;
+        fetch(s0, chunk_of(0));
+        if (1 < nchunks) fetch(s1, chunk_of(1));
+        put(SlotTag<0>{}, s0, chunk_of(0));
         __syncthreads();
         for (int k = 0; k < nchunks; k += 2) {
-            if (k + 1 < nchunks) {                             // step k reads slot 0: fill slot 1
-                fetch(nchunks - 2 - k);
-                put(SlotTag<1>{}, nchunks - 2 - k);
-            }
-            __syncthreads();
+            if (k + 2 < nchunks) fetch(s0, chunk_of(k + 2));
+            if (k + 1 < nchunks) put(SlotTag<1>{}, s1, chunk_of(k + 1));
+            __syncthreads();                                   // end of step k
             if (k + 1 < nchunks) {
-                if (k + 2 < nchunks) {                         // step k + 1 reads slot 1: fill slot 0
-                    fetch(nchunks - 3 - k);
-                    put(SlotTag<0>{}, nchunks - 3 - k);
-                }
-                __syncthreads();
+                if (k + 3 < nchunks) fetch(s1, chunk_of(k + 3));
+                if (k + 2 < nchunks) put(SlotTag<0>{}, s0, chunk_of(k + 2));
+                __syncthreads();                               // end of step k + 1
             }
         }
         return;
