@@ -347,6 +347,24 @@ recurrent_kernel(const RecParams p) {
 // whose rows arrive first update and store them while the others still load.
 // With one workgroup per CU (B64 H4), a layout whose reduction spans the waves
 // made every wave of the chip load, then every wave store (58 % of HBM).
+// Cross-lane sums for the decode step in VALU: DPP row rotations sum a 16-lane
+// row; the two row broadcasts carry rows 0 .. 2 into row 3, and lane 63's value
+// is read out (the wave's total, in every lane)
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dec_dpp(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xf,
+                                                                 false));
+}
+__device__ __forceinline__ float dec_wave_sum(float x) {
+    x += dec_dpp<0x128>(x);                                   // row_ror:8
+    x += dec_dpp<0x124>(x);                                   // row_ror:4
+    x += dec_dpp<0x122>(x);                                   // row_ror:2
+    x += dec_dpp<0x121>(x);                                   // row_ror:1
+    x += dec_dpp<0x142, 0xa>(x);                              // row_bcast:15 into rows 1 and 3
+    x += dec_dpp<0x143, 0xc>(x);                              // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+
 template <int DV> constexpr int decode_threads() { return DV > 128 ? 512 : 256; }
 
 template <int DK, int DV, typename E, int GATE, int MODE, typename WT>
@@ -395,9 +413,15 @@ decode_conv_kernel(const RecParams p) {
     // (1) the state
     const __amdgpu_buffer_rsrc_t s_in = buffer_rsrc(p.h0 + sbase, DK * DV * 4);
     const uint32_t so = (uint32_t)(rg * DV + 4 * cg) * 4;
+    // dv = 128 (several workgroups per CU) issues the state first; WIDE (one
+    // workgroup per CU) issues it after the token's operands, so that the conv,
+    // norm and gate work below waits for those alone and runs while the state
+    // arrives (measured at B64 H4: 15.5 -> 15.0 us)
     f32x4 S[RPT];
+    if constexpr (!WIDE) {
 #pragma unroll
-    for (int i = 0; i < RPT; ++i) S[i] = buffer_load_nt4(s_in, so, (uint32_t)(NRG * i * DV * 4));
+        for (int i = 0; i < RPT; ++i) S[i] = buffer_load_nt4(s_in, so, (uint32_t)(NRG * i * DV * 4));
+    }
 
     // (2) the token's operands
     const int64_t HDK = (int64_t)H * DK, HDV = (int64_t)H * DV;
@@ -431,6 +455,10 @@ decode_conv_kernel(const RecParams p) {
         if (!WR && p.use_delta) bsc = p.beta[t * H + h];
     }
 
+    if constexpr (WIDE) {
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) S[i] = buffer_load_nt4(s_in, so, (uint32_t)(NRG * i * DV * 4));
+    }
     // (3) producers: conv + SiLU (linear_attention.py:741-745) advancing the caches
     // (:929-941), the L2 norm (:703-706), q . k
     float qv = 0.f, kv = 0.f;
@@ -439,12 +467,7 @@ decode_conv_kernel(const RecParams p) {
         kv = tk.apply(cache_k, HDK, cq);
     }
     if (p.fz.qk_l2norm) {
-        float sq = qv * qv, sk = kv * kv;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) {
-            sq += __shfl_xor(sq, off);
-            sk += __shfl_xor(sk, off);
-        }
+        float sq = dec_wave_sum(qv * qv), sk = dec_wave_sum(kv * kv);
         if (lane == 0) {
             nrm[wave][0] = sq;
             nrm[wave][1] = sk;
@@ -462,8 +485,7 @@ decode_conv_kernel(const RecParams p) {
     qv *= p.scale;
     {
         float qk = qv * (WR ? EL::to_f(wr) : kv);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) qk += __shfl_xor(qk, off);
+        qk = dec_wave_sum(qk);
         if (lane == 0) nrm[wave][2] = qk;
     }
     if (own) {
@@ -512,8 +534,13 @@ decode_conv_kernel(const RecParams p) {
     for (int off = NCG; off < 64; off <<= 1) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            kS[e] += __shfl_xor(kS[e], off);
-            qS[e] += __shfl_xor(qS[e], off);
+            if (off == 8) {                                    // lanes l ^ 8: the other half of the row
+                kS[e] += dec_dpp<0x128>(kS[e]);
+                qS[e] += dec_dpp<0x128>(qS[e]);
+            } else {
+                kS[e] += __shfl_xor(kS[e], off);
+                qS[e] += __shfl_xor(qS[e], off);
+            }
         }
     }
     float qk = nrm[0][2];
