@@ -392,12 +392,7 @@ chunk_prep_kernel(const ChunkParams p) {
         }
     } else {
         if (wave == 0) {
-            float x = lane < clen ? g_v : 0.f;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const float y = __shfl_up(x, o);
-                if (lane >= o) x += y;
-            }
+            const float x = wave_scan(lane < clen ? g_v : 0.f);
             if (lane < CH) gam[lane] = x;
         }
     }

@@ -239,21 +239,8 @@ __device__ __forceinline__ f32x4 col4(const float *m, int pitch, int k0, int c) 
     return f32x4{m[k0 * pitch + c], m[(k0 + 1) * pitch + c], m[(k0 + 2) * pitch + c], m[(k0 + 3) * pitch + c]};
 }
 
-// The sum over the 16 lanes of x's row (lanes 16 m .. 16 m + 15), in every lane
-// of the row, by DPP row rotations: four VALU adds instead of four dependent
-// __shfl_xor round trips through the LDS crossbar (ds_bpermute_b32).  Each lane
-// adds in its own order, so lanes of a row may differ in the last bit.
-template <int CTRL>
-__device__ __forceinline__ float row_rot(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float sum16(float x) {
-    x += row_rot<0x128>(x);                                   // row_ror:8
-    x += row_rot<0x124>(x);                                   // row_ror:4
-    x += row_rot<0x122>(x);                                   // row_ror:2
-    x += row_rot<0x121>(x);                                   // row_ror:1
-    return x;
-}
+// the sum over the 16 lanes of x's row, in every lane of the row (DPP)
+__device__ __forceinline__ float sum16(float x) { return row_sum16(x); }
 // the sum over lanes l, l ^ 16, l ^ 32, l ^ 48 (one lane of each row)
 __device__ __forceinline__ float sum_rows(float x) {
     x += __shfl_xor(x, 16);
@@ -943,12 +930,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
         misc[1] = 0.f;
     }
     if (!VEC && wave == 0) {                                   // gamma: in-chunk inclusive sum of g
-        float x = lane < clen ? g_v : 0.f;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_up(x, o);
-            if (lane >= o) x += y;
-        }
+        const float x = wave_scan(lane < clen ? g_v : 0.f);
         if (lane < CH) gam[lane] = x;
     }
     __syncthreads();
@@ -1332,11 +1314,7 @@ chunk_grad_kernel(const ChunkBwdParams p) {
     if (wave == 0) {
         float x = lane < clen ? dgam[lane] : 0.f;
         if (lane == clen - 1) x += misc[1];
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const float y = __shfl_down(x, o);
-            if (lane + o < 64) x += y;
-        }
+        x = wave_suffix(x);
         if (lane < clen) {
             if (p.dg) p.dg[(t0 + lane) * H + h] = x;
             const float b = bet[lane];                         // sigmoid(logit) when fused: its derivative b (1 - b)

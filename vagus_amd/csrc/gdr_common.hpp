@@ -229,4 +229,50 @@ __device__ __forceinline__ void unroll(F &&f) {
     unroll_seq(f, std::make_integer_sequence<int, N>{});
 }
 
+// ---- cross-lane sums and scans in VALU (DPP) ---------------------------------
+// A __shfl_* is a round trip through the LDS crossbar (ds_bpermute_b32); these
+// read the neighbour lane through a DPP operand of the add instead.
+// dpp_f<CTRL>(x): x from the lane the DPP control names (row_ror, row_shr,
+// row_bcast ..); a lane whose source lies outside its row, or whose row
+// ROW_MASK leaves out, reads 0.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_f(float x) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xf,
+                                                                 false));
+}
+// the sum over the 16 lanes of x's row (lanes 16 m .. 16 m + 15), in every lane
+// of the row (each lane adds in its own order: lanes may differ in the last bit)
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp_f<0x128>(x);                                     // row_ror:8
+    x += dpp_f<0x124>(x);                                     // row_ror:4
+    x += dpp_f<0x122>(x);                                     // row_ror:2
+    x += dpp_f<0x121>(x);                                     // row_ror:1
+    return x;
+}
+// the sum over the wave, in every lane: the rows' sums, the two row broadcasts
+// carry rows 0 .. 2 into row 3, and lane 63's value is read out
+__device__ __forceinline__ float wave_sum64(float x) {
+    x = row_sum16(x);
+    x += dpp_f<0x142, 0xa>(x);                                // row_bcast:15 into rows 1 and 3
+    x += dpp_f<0x143, 0xc>(x);                                // row_bcast:31 into rows 2 and 3
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
+}
+// inclusive prefix sum over lanes 0 .. l: row shifts 1, 2, 4, 8, then the rows'
+// totals carried forward by the two row broadcasts
+__device__ __forceinline__ float wave_scan(float x) {
+    x += dpp_f<0x111>(x);                                     // row_shr:1
+    x += dpp_f<0x112>(x);                                     // row_shr:2
+    x += dpp_f<0x114>(x);                                     // row_shr:4
+    x += dpp_f<0x118>(x);                                     // row_shr:8
+    x += dpp_f<0x142, 0xa>(x);                                // row_bcast:15
+    x += dpp_f<0x143, 0xc>(x);                                // row_bcast:31
+    return x;
+}
+// suffix sum over lanes l .. 63: the total less the exclusive prefix
+__device__ __forceinline__ float wave_suffix(float x) {
+    const float inc = wave_scan(x);
+    const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, inc), 63));
+    return tot - (inc - x);
+}
+
 }  // namespace vgdr

@@ -347,24 +347,6 @@ recurrent_kernel(const RecParams p) {
 // whose rows arrive first update and store them while the others still load.
 // With one workgroup per CU (B64 H4), a layout whose reduction spans the waves
 // made every wave of the chip load, then every wave store (58 % of HBM).
-// Cross-lane sums for the decode step in VALU: DPP row rotations sum a 16-lane
-// row; the two row broadcasts carry rows 0 .. 2 into row 3, and lane 63's value
-// is read out (the wave's total, in every lane)
-template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ float dec_dpp(float x) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, ROW_MASK, 0xf,
-                                                                 false));
-}
-__device__ __forceinline__ float dec_wave_sum(float x) {
-    x += dec_dpp<0x128>(x);                                   // row_ror:8
-    x += dec_dpp<0x124>(x);                                   // row_ror:4
-    x += dec_dpp<0x122>(x);                                   // row_ror:2
-    x += dec_dpp<0x121>(x);                                   // row_ror:1
-    x += dec_dpp<0x142, 0xa>(x);                              // row_bcast:15 into rows 1 and 3
-    x += dec_dpp<0x143, 0xc>(x);                              // row_bcast:31 into rows 2 and 3
-    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
-}
-
 template <int DV> constexpr int decode_threads() { return DV > 128 ? 512 : 256; }
 
 template <int DK, int DV, typename E, int GATE, int MODE, typename WT>
@@ -467,7 +449,7 @@ decode_conv_kernel(const RecParams p) {
         kv = tk.apply(cache_k, HDK, cq);
     }
     if (p.fz.qk_l2norm) {
-        float sq = dec_wave_sum(qv * qv), sk = dec_wave_sum(kv * kv);
+        float sq = wave_sum64(qv * qv), sk = wave_sum64(kv * kv);
         if (lane == 0) {
             nrm[wave][0] = sq;
             nrm[wave][1] = sk;
@@ -485,7 +467,7 @@ decode_conv_kernel(const RecParams p) {
     qv *= p.scale;
     {
         float qk = qv * (WR ? EL::to_f(wr) : kv);
-        qk = dec_wave_sum(qk);
+        qk = wave_sum64(qk);
         if (lane == 0) nrm[wave][2] = qk;
     }
     if (own) {
@@ -535,8 +517,8 @@ decode_conv_kernel(const RecParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             if (off == 8) {                                    // lanes l ^ 8: the other half of the row
-                kS[e] += dec_dpp<0x128>(kS[e]);
-                qS[e] += dec_dpp<0x128>(qS[e]);
+                kS[e] += dpp_f<0x128>(kS[e]);
+                qS[e] += dpp_f<0x128>(qS[e]);
             } else {
                 kS[e] += __shfl_xor(kS[e], off);
                 qS[e] += __shfl_xor(qS[e], off);
