@@ -118,16 +118,24 @@ def test_chunk_bwd_matches_oracle(dtype, gate, shape):
     _compare(got, ref, 1e-5 if dtype == torch.float32 else 2e-2, f'{dtype} gate={gate} {shape}')
 
 
+# packed batches: empty, one-token, two-chunk and short segments; and segments
+# of 3, 5, 3 (exactly) and 4 chunks, so that the dS walk's producers, which fill
+# each step's slot from one of two register sets loaded two steps ahead, end on
+# either set and with one or two loads in flight
+VARLEN_CU = [[0, 0, 1, 70, 75, 160], [0, 130, 387, 579, 835]]
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize('dtype', [torch.float32, torch.bfloat16])
-def test_chunk_bwd_varlen_matches_per_segment_oracle(dtype):
-    cu = torch.tensor([0, 0, 1, 70, 75, 160], dtype=torch.int32)    # empty, one token, multi-chunk, short
-    N, T, H, dk, dv = 5, 160, 2, 64, 64
+@pytest.mark.parametrize('cu_list', VARLEN_CU)
+def test_chunk_bwd_varlen_matches_per_segment_oracle(dtype, cu_list):
+    cu = torch.tensor(cu_list, dtype=torch.int32)
+    N, T, H, dk, dv = len(cu_list) - 1, cu_list[-1], 2, 64, 64
     q, k, v, g, beta, _, do, _ = _inputs(1, T, H, dk, dv, dtype, seed=3)
     gen = torch.Generator().manual_seed(4)
     S0 = 0.3 * torch.randn(N, H, dk, dv, generator=gen)
     dST = torch.randn(N, H, dk, dv, generator=gen)
-    print(f'\n[case] chunk_bwd varlen dtype={dtype}', flush=True)
+    print(f'\n[case] chunk_bwd varlen dtype={dtype} cu={cu_list}', flush=True)
     scale = dk ** -0.5
     parts = [[] for _ in range(6)]
     for n in range(N):

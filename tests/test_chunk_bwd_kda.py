@@ -147,14 +147,16 @@ def test_kda_chunk_bwd_matches_oracle(dtype, shape, strong):
 
 
 @pytest.mark.gpu
-def test_kda_chunk_bwd_varlen_matches_per_segment_oracle():
-    cu = torch.tensor([0, 0, 1, 70, 75, 200], dtype=torch.int32)    # empty, one token, multi-chunk, short
-    N, T, H, dk, dv = 5, 200, 2, 64, 64
+@pytest.mark.parametrize('cu_list', [[0, 0, 1, 70, 75, 200],      # empty, one token, multi-chunk, short
+                                     [0, 130, 387, 579, 835]])     # 3, 5, 3 (exactly) and 4 chunks
+def test_kda_chunk_bwd_varlen_matches_per_segment_oracle(cu_list):
+    cu = torch.tensor(cu_list, dtype=torch.int32)
+    N, T, H, dk, dv = len(cu_list) - 1, cu_list[-1], 2, 64, 64
     q, k, v, g, beta, _, do, _ = _inputs(1, T, H, dk, dv, torch.bfloat16, seed=13)
     gen = torch.Generator().manual_seed(14)
     S0 = 0.3 * torch.randn(N, H, dk, dv, generator=gen)
     dST = torch.randn(N, H, dk, dv, generator=gen)
-    print('\n[case] kda chunk_bwd varlen', flush=True)
+    print(f'\n[case] kda chunk_bwd varlen cu={cu_list}', flush=True)
     scale = dk ** -0.5
     parts = [[] for _ in range(6)]
     for n in range(N):
