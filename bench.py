@@ -12,7 +12,9 @@ so that no step finds its operands in the 256 MB Infinity Cache.  Before
 the timed headline steps, a fixed clock-settle phase (--settle, default 2 s of
 untimed steps on the same rotating copies, right before the warmup, reported
 as settle_s) brings the GPU's clocks to their loaded state, so a short
---warmup times the same level as a long one; the later legs follow it.
+--warmup times the same level as a long one; each later event-timed leg first
+runs its own operation untimed for LEG_SETTLE_S (0.3 s, reported as
+leg_settle_s).
 
 The prefill runs as two kernels per call: chunk_prep (every (chunk, head) in
 parallel: the intra-chunk Q K^T and K K^T products and the triangular
@@ -91,6 +93,9 @@ GRAPH_WARM_REPLAYS = 10
 # default clock-settle phase: back-to-back headline prefill steps right before the warmup, outside
 # the timed region (short runs after an idle GPU otherwise time the first steps up to 8% slow)
 SETTLE_S = 2.0
+# each later timed leg first runs its own operation, untimed, for this long (a leg
+# that follows a different workload otherwise timed its first calls up to 8 % slow)
+LEG_SETTLE_S = 0.3
 
 
 def log(msg):
@@ -246,8 +251,20 @@ def bench_generate(torch, workloads, reps=2):
             'end_to_end_s': round(t2 - t0, 4)}
 
 
+def _settle(torch, fn, seconds):
+    """Untimed calls of fn for `seconds` of host clock (synchronised every few calls)."""
+    t0, i = time.perf_counter(), 0
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(4):
+            fn(i)
+            i += 1
+        torch.cuda.synchronize()
+
+
 def _event_us(torch, fn, steps, warmup):
-    """Mean event-timed microseconds of fn() over `steps` back-to-back calls."""
+    """Mean event-timed microseconds of fn() over `steps` back-to-back calls,
+    after LEG_SETTLE_S of untimed calls and `warmup` more."""
+    _settle(torch, fn, LEG_SETTLE_S)
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
@@ -1000,7 +1017,8 @@ def main():
         extra['generation'] = bench_generate(torch, workloads)
         for name in ('kda_prefill', 'gdn_varlen'):
             log(f'[bench] prefill {name}')
-            r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2))
+            r = bench_prefill(torch, ops, workloads, name, max(3, args.steps // 3), max(2, args.warmup // 2),
+                              settle_s=LEG_SETTLE_S)
             gpn = measured_gemm_phase(name)
             extra[name] = {'gemm_phase_frac': None if gpn is None else gpn['gemm_phase_frac'],
                            'tok_s': round(r['tok_s'], 1), 'op_ms': round(r['op_ms'], 4),
@@ -1026,6 +1044,7 @@ def main():
         'steps': args.steps,
         'warmup': args.warmup,
         'settle_s': round(settle_s, 3),
+        'leg_settle_s': LEG_SETTLE_S,
         'ms_per_step': round(pre['total_s'] * 1e3 / args.steps, 4),
         'higher_is_better': True,
         'scaling': 'weak',
