@@ -1826,9 +1826,12 @@ template <int DK, int CH, typename E>
 static hipError_t run_bwd(ChunkBwdParams p, bool saved, hipStream_t stream) {
     const int64_t units = (int64_t)p.geo.n_seqs * p.H;
     // Both walks take 32-column tiles (256 workgroups at B = 8, H = 8, dv =
-    // 128) with two compute and two producer waves (measured at B8 T4096 H8
+    // 128) with two compute waves and producer waves (measured at B8 T4096 H8
     // d128, whole backward: 1.13 ms with the dS walk's compute waves staging
     // their own operands, 1.00 ms with producers; 1.02 ms with 64-column tiles).
+    // The 16-bit dS walk runs four producers, each holding a quarter of a
+    // chunk's operands in each of its two register sets (two producers: 256
+    // VGPRs and 89 AGPRs; four: 162; gdn_340m backward 672 -> 661 us).
     if (units > 0) {
         p.n_tiles = (p.DV + 31) / 32;
         // 16-bit: the states came from the forward's state kernel (chunk_bwd), or a
@@ -1836,8 +1839,12 @@ static hipError_t run_bwd(ChunkBwdParams p, bool saved, hipStream_t stream) {
         if (!saved && sizeof(E) == 4)
             hipLaunchKernelGGL((chunk_hs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
                                dim3(256), 0, stream, p);
-        hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
-                           dim3(256), 0, stream, p);
+        if constexpr (sizeof(E) == 2)
+            hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E, false, 4>),
+                               dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)), dim3(384), 0, stream, p);
+        else
+            hipLaunchKernelGGL((chunk_dhs_kernel<DK, CH, 2, E>), dim3((unsigned)((units + 7) / 8 * 8 * p.n_tiles)),
+                               dim3(256), 0, stream, p);
     }
     const int64_t grad_blocks = (int64_t)p.n_chunk_slots * p.H;
     if (grad_blocks > 0)
