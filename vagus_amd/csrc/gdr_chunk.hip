@@ -1539,9 +1539,9 @@ chunk_pipe_kernel(const ChunkParams p) {
             if constexpr (VEC) st.e.store((odd ? KE1 : KE0) + z, pl.k);
         };
         // Q of chunk c goes to Q slot c & 1 between barriers c and c + 1 (the output
-        // waves read it one step after the chain reads chunk c's K).  One register
-        // set, loaded one step ahead and issued before the next K loads, so that
-        // the wait for it leaves those in flight.
+        // waves read it one step after the chain reads chunk c's K).  Each Q load is
+        // issued before the next K loads, so that the wait for it leaves those in
+        // flight.
         auto load_q = [&](CQ &qc, const Plans &pl, int c) __attribute__((always_inline)) {
             c = c < nchunks ? c : nchunks - 1;
             if constexpr (VEC) {
@@ -1556,10 +1556,19 @@ chunk_pipe_kernel(const ChunkParams p) {
             const int pt = tid - 64 * (NW + 2);
             const Plans pl{CK::plan(VEC ? DK : sqk, DK, pt), CV::plan(sv, DV - col0, pt)};
             Staged s0, s1;
-            CQ qc;
+            // per-channel gate: Q*G of the even chunks in qa, of the odd ones in qb,
+            // each loaded two steps ahead (kda_prefill state kernel 194.4 -> 190.9 us);
+            // the scalar gate loads Q one step ahead into qa alone (two sets measured
+            // 93.4 -> 94.5 us at gdn_340m)
+            constexpr bool Q2 = VEC;
+            CQ qa, qb;
+            CQ &qo = Q2 ? qb : qa;
             load(s0, pl, 0, pt);
             store(s0, pl, 0, 0, pt);
-            if constexpr (QL) load_q(qc, pl, 0);
+            if constexpr (QL) {
+                load_q(qa, pl, 0);
+                if constexpr (Q2) load_q(qb, pl, 1);
+            }
             load(s1, pl, 1, pt);
             load(s0, pl, 2, pt);
             int c = 0;
@@ -1568,23 +1577,23 @@ chunk_pipe_kernel(const ChunkParams p) {
                 lds_barrier();                                // barrier c: chunk c in place, chunk c-1 consumed
                 store(s1, pl, c + 1, z, pt);                  // into the slot chunk c-1 used
                 if constexpr (QL) {
-                    qc.store(QS + z, pt);                     // Q of chunk c (even)
-                    load_q(qc, pl, c + 1);
+                    qa.store(QS + z, pt);                     // Q of chunk c (even)
+                    load_q(qa, pl, Q2 ? c + 2 : c + 1);
                 }
                 load(s1, pl, c + 3, pt);
                 z = opaque_s(0);
                 lds_barrier();                                // barrier c + 1
                 store(s0, pl, c + 2, z, pt);
                 if constexpr (QL) {
-                    qc.store(QS + CH * DK + z, pt);           // Q of chunk c + 1 (odd)
-                    load_q(qc, pl, c + 2);
+                    qo.store(QS + CH * DK + z, pt);           // Q of chunk c + 1 (odd)
+                    load_q(qo, pl, Q2 ? c + 3 : c + 2);
                 }
                 load(s0, pl, c + 4, pt);
             }
             if (c < nchunks) {                                // n odd: c = n - 1, even
                 const int z = opaque_s(0);
                 lds_barrier();                                // barrier n - 1
-                if constexpr (QL) qc.store(QS + z, pt);       // the last chunk's Q
+                if constexpr (QL) qa.store(QS + z, pt);       // the last chunk's Q
             }
             lds_barrier();                                    // barrier n: the last chunk's outputs
             __builtin_amdgcn_s_waitcnt(0);                    // no load left in flight at exit
