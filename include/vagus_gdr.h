@@ -465,6 +465,25 @@ int vgdr_decode_step(int dtype, int gate_kind, int use_delta,
                      float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
                      const vgdr_epilogue *epilogue, hipStream_t stream);
 
+/* vgdr_decode_step (GatedDeltaNet.decode_step, linear_attention.py:918-952)
+ * for one token per sequence (T = 1, n_seqs = B, no cu_seqlens) whose inputs
+ * are rows of a wider buffer: token b's q, k are at
+ * q + b * ld_qk, k + b * ld_qk and its v and epilogue gate at v + b * ld_v,
+ * gate + b * ld_v (elements; each row's H * d block dense).  The layer's four
+ * projections from one GEMM over their concatenated weights are read in place
+ * this way, with no copy into separate tensors (the reference's projections
+ * are separate nn.Linear outputs, :929 and :816, so it has no such form).  Needs `conv`
+ * with K = 4 and 16-byte aligned weights and an initial_state
+ * (VGDR_ERR_UNSUPPORTED otherwise); ld_qk >= H * dk, ld_v >= H * dv
+ * (VGDR_ERR_INVALID otherwise). */
+int vgdr_decode_step_strided(int dtype, int gate_kind, int use_delta,
+                             const void *q, const void *k, const void *v,
+                             const float *g, const float *beta,
+                             void *o, const float *initial_state, float *final_state,
+                             int64_t B, int64_t H, int64_t dk, int64_t dv, int64_t ld_qk, int64_t ld_v,
+                             float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
+                             const vgdr_epilogue *epilogue, hipStream_t stream);
+
 /* The short conv + SiLU (vgdr_short_conv's semantics) over a whole call's
  * tokens, for prefill: y[t] from x[t - K + 1 .. t] of the same sequence.
  * Replaces the module's ShortConv (opt.py:15-100; fla's causal_conv1d as the

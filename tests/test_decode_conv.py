@@ -114,6 +114,24 @@ def test_short_conv_argument_checks():
     assert call(_lib.ShortConv(**{**good, 'weight_dtype': _lib.VGDR_F16})) == _lib.VGDR_ERR_INVALID
 
 
+def test_strided_decode_step_argument_checks():
+    """vgdr_decode_step_strided refuses row strides below a dense row, and a call
+    the decode kernel would not run (no conv), before touching a device."""
+    L = _lib.load()
+
+    def call(ld_qk, ld_v, sc):
+        return L.vgdr_decode_step_strided(1, 1, 1, None, None, None, None, None, None, None, None,
+                                          4, 16, 128, 128, ld_qk, ld_v, 1.0, None, sc, None, None)
+    assert call(1024, 8192, None) == _lib.VGDR_ERR_INVALID
+    assert b'row strides' in L.vgdr_last_error()
+    assert call(8192, 2047, None) == _lib.VGDR_ERR_INVALID
+    assert call(8192, 8192, None) == _lib.VGDR_ERR_UNSUPPORTED
+    assert b'four-tap' in L.vgdr_last_error()
+    sc = _lib.ShortConv(weight_q=None, weight_k=None, weight_v=None, cache_q=None, cache_k=None, cache_v=None,
+                        kernel_size=2, weight_dtype=_lib.VGDR_F32)
+    assert call(8192, 8192, ctypes.byref(sc)) == _lib.VGDR_ERR_UNSUPPORTED
+
+
 # --- GPU ----------------------------------------------------------------------
 
 def _run(gate, dtype, K, L, epilogue, w_dtype, seed, B=4, H=2, dk=128, dv=64):
@@ -228,3 +246,48 @@ def test_decode_step_at_lm_layer_shape():
     exact = all(torch.equal(a.cpu(), b) for a, b in zip(caches, c_ref))
     print(f'[parity] LM-shape decode step o={eo:.3e} S={es:.3e} caches exact={exact} (tol {TOL:g})', flush=True)
     assert eo <= TOL and es <= TOL and exact
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('dk,dv,gate,epilogue', [(128, 128, 'scalar', True), (64, 64, 'scalar', False),
+                                                 (128, 256, 'scalar', True), (128, 128, 'vector', True)])
+def test_decode_step_reads_projection_rows_in_place(dk, dv, gate, epilogue):
+    """q, k, v and the output gate as column blocks of one (B, 1, 2 H dk + 2 H dv)
+    projection output, as the layer's concatenated GEMM leaves them: the kernel
+    reads the rows in place (vgdr_decode_step_strided) and gives exactly what it
+    gives on dense copies of the same values (o, the state and the conv caches
+    bit-exact), which is within the tolerance of the oracle's decode step."""
+    from vagus_amd import ops
+    B, H, K = 16, 4, 4
+    qp, kp, vp, ws, cs, gl, beta, S0 = _decode_inputs(B, 1, H, dk, dv, K, gate, torch.bfloat16, seed=51,
+                                                      w_dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(52)
+    og = torch.randn(B, 1, H * dv, generator=g).bfloat16()
+    gamma = (torch.rand(dv, generator=g) + 0.5).bfloat16()
+    print(f'\n[case] strided decode step dk={dk} dv={dv} gate={gate} epilogue={epilogue}', flush=True)
+    dev = lambda t: t.cuda()
+    y = dev(torch.cat([qp.reshape(B, 1, -1), kp.reshape(B, 1, -1), vp.reshape(B, 1, -1), og], -1))
+    a, b_, c_ = H * dk, 2 * H * dk, 2 * H * dk + H * dv
+    views = (y[..., :a], y[..., a:b_], y[..., b_:c_], y[..., c_:])
+    assert all(not t.is_contiguous() for t in views)
+
+    def step(q_, k_, v_, og_):
+        S = dev(S0.clone())
+        caches = tuple(dev(c.clone()) for c in cs)
+        o = ops.hip_decode_step(q_, k_, v_, dev(gl), dev(beta), S, scale=dk ** -0.5,
+                                conv_weights=tuple(dev(w) for w in ws), conv_cache=caches,
+                                out_gate=og_ if epilogue else None, out_norm_weight=dev(gamma) if epilogue else None)
+        torch.cuda.synchronize()
+        return o, S, caches
+
+    o1, S1, c1 = step(*views)
+    o2, S2, c2 = step(*(t.contiguous() for t in views))
+    same = torch.equal(o1, o2) and torch.equal(S1, S2) and all(torch.equal(x1, x2) for x1, x2 in zip(c1, c2))
+    o_ref, S_ref, _ = gdr.decode_step(qp, kp, vp, gl.double(), beta.double(), S0.double(), ws, cs, scale=dk ** -0.5)
+    if epilogue:
+        o_ref = gdr.norm_gate(o_ref.to(torch.bfloat16).double(), og.reshape(B, 1, H, dv).double(),
+                              gamma.double(), 1e-6)
+    eo, es = _rel(o1, o_ref), _rel(S1, S_ref)
+    print(f'[parity] strided decode step: equal to dense={same}, o={eo:.3e} S={es:.3e} (tol {TOL:g})', flush=True)
+    assert same and eo <= TOL and es <= TOL
+

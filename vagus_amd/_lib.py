@@ -92,6 +92,8 @@ SIGNATURES = {
                                   _L, _L, _L, _L, _L, _L, _F, _FZ, _P]),
     'vgdr_decode_step': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                               _L, _L, _L, _L, _L, _L, _F, _FZ, _SC, _EP, _P]),
+    'vgdr_decode_step_strided': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                                      _L, _L, _L, _L, _L, _L, _F, _FZ, _SC, _EP, _P]),
     'vgdr_causal_conv1d': (_I, [_I, _P, _P, _I, _P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _P]),
     'vgdr_varlen_workspace_size': (_L, [_L]),
     'vgdr_varlen_prepare': (_I, [_P, _L, _L, _I, _P, _P]),

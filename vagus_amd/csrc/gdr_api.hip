@@ -714,7 +714,7 @@ int recurrent_call(int dtype, int gate_kind, int use_delta, const void *q, const
                    const void *w, const float *g, const float *beta, void *o, const float *initial_state,
                    float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H, int64_t dk,
                    int64_t dv, int64_t n_seqs, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
-                   const vgdr_epilogue *epilogue, hipStream_t stream) {
+                   const vgdr_epilogue *epilogue, hipStream_t stream, int64_t ld_qk = 0, int64_t ld_v = 0) {
     g_err[0] = 0;
     // with an explicit write vector, beta is not read
     int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, w ? 0 : use_delta, q, k, v, g, beta, o,
@@ -763,6 +763,8 @@ int recurrent_call(int dtype, int gate_kind, int use_delta, const void *q, const
     p.ep = ep;
     p.cv = cv;
     p.w = w;
+    p.ld_qk = ld_qk;
+    p.ld_v = ld_v;
     return hip_status(vgdr::recurrent_fwd(dtype, (int)dk, (int)dv, gate_kind == VGDR_GATE_VECTOR, p, stream),
                       "vgdr_recurrent_fwd launch");
 }
@@ -776,6 +778,26 @@ int vgdr_decode_step(int dtype, int gate_kind, int use_delta, const void *q, con
                      const vgdr_epilogue *epilogue, hipStream_t stream) {
     return recurrent_call(dtype, gate_kind, use_delta, q, k, v, nullptr, g, beta, o, initial_state, final_state,
                           cu_seqlens, B, T, H, dk, dv, n_seqs, scale, fusion, conv, epilogue, stream);
+}
+
+int vgdr_decode_step_strided(int dtype, int gate_kind, int use_delta, const void *q, const void *k, const void *v,
+                             const float *g, const float *beta, void *o, const float *initial_state,
+                             float *final_state, int64_t B, int64_t H, int64_t dk, int64_t dv, int64_t ld_qk,
+                             int64_t ld_v, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
+                             const vgdr_epilogue *epilogue, hipStream_t stream) {
+    // the strides reach only the one-token decode kernel: it needs a state and the
+    // four-tap conv with 16-byte aligned weights (any other call would run the
+    // token walk, which reads dense rows)
+    g_err[0] = 0;
+    if (ld_qk < H * dk || ld_v < H * dv)
+        return fail(VGDR_ERR_INVALID, "vgdr_decode_step_strided: row strides (%lld, %lld) below H*dk = %lld, "
+                    "H*dv = %lld", (long long)ld_qk, (long long)ld_v, (long long)(H * dk), (long long)(H * dv));
+    if (!conv || conv->kernel_size != 4 || !aligned16(conv->weight_q) || !aligned16(conv->weight_k) ||
+        !aligned16(conv->weight_v) || !initial_state)
+        return fail(VGDR_ERR_UNSUPPORTED, "vgdr_decode_step_strided: strided rows need the four-tap short conv "
+                    "with 16-byte aligned weights and an initial state");
+    return recurrent_call(dtype, gate_kind, use_delta, q, k, v, nullptr, g, beta, o, initial_state, final_state,
+                          nullptr, B, 1, H, dk, dv, B, scale, fusion, conv, epilogue, stream, ld_qk, ld_v);
 }
 
 int vgdr_recurrent_fwd_w(int dtype, int gate_kind, const void *q, const void *k, const void *v, const void *w,

@@ -171,6 +171,10 @@ struct RecParams {
     Epilogue ep;                  // applied to o before it is stored
     ShortConv cv;                 // applied to q, k, v where they are read
     const void *w;                // [n_tokens, H, dk] write vectors in place of beta k, or NULL
+    // the one-token decode step's token row strides, in elements: q and k (ld_qk)
+    // and v and the epilogue gate (ld_v); 0 for dense rows (H dk, H dv).  Rows of
+    // one fused projection output [n_tokens, 4 H d] are read in place this way
+    int64_t ld_qk, ld_v;
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.

@@ -45,10 +45,11 @@ struct ConvTaps {
     typedef WT WV __attribute__((ext_vector_type(4)));
     E xs[4];
     WV w4;
-    __device__ __forceinline__ void load(const E *x, const E *cache, const void *w, int64_t HD, int64_t c,
-                                         int64_t t) {
+    // x: the token's input row at x[t * LD]; the cache rows [K, HD]
+    __device__ __forceinline__ void load(const E *x, const E *cache, const void *w, int64_t HD, int64_t LD,
+                                         int64_t c, int64_t t) {
         unroll<4>([&](auto j) __attribute__((always_inline)) {
-            xs[j] = j == 3 ? x[t * HD + c] : cache[(int64_t)(j + 1) * HD + c];
+            xs[j] = j == 3 ? x[t * LD + c] : cache[(int64_t)(j + 1) * HD + c];
         });
         w4 = reinterpret_cast<const WV *>(w)[c];
     }
@@ -407,6 +408,7 @@ decode_conv_kernel(const RecParams p) {
 
     // (2) the token's operands
     const int64_t HDK = (int64_t)H * DK, HDV = (int64_t)H * DV;
+    const int64_t LDQ = p.ld_qk ? p.ld_qk : HDK, LDV = p.ld_v ? p.ld_v : HDV;   // input token rows
     const int64_t cq = (int64_t)h * DK + tid, cvc = (int64_t)h * DV + tid;
     E *cache_q = reinterpret_cast<E *>(p.cv.cq) + (int64_t)seq * K * HDK;
     E *cache_k = reinterpret_cast<E *>(p.cv.ck) + (int64_t)seq * K * HDK;
@@ -416,8 +418,8 @@ decode_conv_kernel(const RecParams p) {
     uint32_t gr = 0;
     float gsc = 0.f, bsc = 0.f, gmv = 0.f;
     if (own) {
-        tq.load(reinterpret_cast<const E *>(p.q), cache_q, p.cv.wq, HDK, cq, t);
-        tk.load(reinterpret_cast<const E *>(p.k), cache_k, p.cv.wk, HDK, cq, t);
+        tq.load(reinterpret_cast<const E *>(p.q), cache_q, p.cv.wq, HDK, LDQ, cq, t);
+        tk.load(reinterpret_cast<const E *>(p.k), cache_k, p.cv.wk, HDK, LDQ, cq, t);
         if constexpr (WR) wr = reinterpret_cast<const E *>(p.w)[qo + tid];
         if constexpr (GATE == 2)
             gr = p.fz.gate_act && p.fz.gate_16 && sizeof(E) == 2
@@ -425,9 +427,9 @@ decode_conv_kernel(const RecParams p) {
                      : reinterpret_cast<const uint32_t *>(p.g)[qo + tid];
     }
     if (vown) {
-        tv.load(reinterpret_cast<const E *>(p.v), cache_v, p.cv.wv, HDV, cvc, t);
+        tv.load(reinterpret_cast<const E *>(p.v), cache_v, p.cv.wv, HDV, LDV, cvc, t);
         if constexpr (EPI) {
-            gtr = reinterpret_cast<const E *>(p.ep.gate)[vo + tid];
+            gtr = reinterpret_cast<const E *>(p.ep.gate)[t * LDV + cvc];
             gmv = p.ep.gamma_f32 ? reinterpret_cast<const float *>(p.ep.gamma)[tid]
                                  : EL::to_f(reinterpret_cast<const E *>(p.ep.gamma)[tid]);
         }

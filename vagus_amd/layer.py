@@ -453,11 +453,16 @@ class GatedDeltaNet(nn.Module):
         B, L = x.shape[0], x.shape[1]
         w4, wab, gconst = self._decode_weights()
         if w4 is not None:
-            # one GEMM over the concatenated weights, then one copy into four
-            # contiguous (B*L, H*dv) blocks, which the decode kernel reads
+            # one GEMM over the concatenated weights; for one token the decode
+            # kernel reads the four column blocks of its rows in place, otherwise
+            # one copy makes them four contiguous (B*L, H*dv) blocks
             y = F.linear(x.reshape(B * L, -1), w4)
-            y = y.view(B * L, 4, -1).transpose(0, 1).contiguous()
-            qp, kp, vp, og = (y[i].view(B, L, -1) for i in range(4))
+            n = y.shape[-1] // 4
+            if L == 1:
+                qp, kp, vp, og = (y[:, i * n:(i + 1) * n].view(B, L, n) for i in range(4))
+            else:
+                y = y.view(B * L, 4, -1).transpose(0, 1).contiguous()
+                qp, kp, vp, og = (y[i].view(B, L, -1) for i in range(4))
         else:
             qp, kp, vp, og = self.wq(x), self.wk(x), self.wv(x), self.wg(x)
         if wab is None:

@@ -212,11 +212,23 @@ class _Fusion:
 _NO_FUSION = _Fusion()
 
 
+def _row_stride(t):
+    """The token row stride, in elements, of a one-token-per-sequence input t
+    (B, 1, H, d) whose (H, d) block is dense and 16-byte aligned, else None."""
+    B, T, H, d = t.shape
+    if T != 1 or t.stride(3) != 1 or t.stride(2) != d or t.data_ptr() % 16:
+        return None
+    ld = t.stride(0) if B > 1 else H * d
+    return ld if ld >= H * d else None
+
+
 class _Call:
-    """Validated, padded, contiguous operands of one kernel call."""
+    """Validated, padded, contiguous operands of one kernel call.  rows: q, k, v
+    of a one-token call may stay rows of a wider buffer (ld_qk, ld_v: their token
+    row strides; 0 when the operands are dense)."""
 
     def __init__(self, q, k, v, g, beta, initial_state, cu_seqlens, *, gate: str, delta: bool,
-                 dv_to, fusion: _Fusion = _NO_FUSION):
+                 dv_to, fusion: _Fusion = _NO_FUSION, rows: bool = False):
         _check_device(q, k, v, g, beta, initial_state, cu_seqlens)
         _check_grad(q, k, v, g, beta, initial_state)
         assert q.dim() == 4 and k.shape == q.shape and v.dim() == 4 and v.shape[:3] == q.shape[:3], \
@@ -250,9 +262,17 @@ class _Call:
         self.dkp, self.dvp = dkp, dvp
         self.dtype = q.dtype
         self.device = q.device
-        self.q = _aligned(_pad_to(q, {1: dkp}))
-        self.k = _aligned(_pad_to(k, {1: dkp}))
-        self.v = _aligned(_pad_to(v, {1: dvp}))
+        self.ld_qk = self.ld_v = 0
+        if rows and cu is None and dkp == dk and dvp == dv:
+            lq, lk, lv = _row_stride(q), _row_stride(k), _row_stride(v)
+            if lq is not None and lq == lk and lv is not None and (lq, lv) != (H * dk, H * dv):
+                self.ld_qk, self.ld_v = lq, lv                  # (dense rows keep the dense entry point)
+        if self.ld_qk:
+            self.q, self.k, self.v = q, k, v
+        else:
+            self.q = _aligned(_pad_to(q, {1: dkp}))
+            self.k = _aligned(_pad_to(k, {1: dkp}))
+            self.v = _aligned(_pad_to(v, {1: dvp}))
         if gate == 'none' or g is None:
             self.g, self.gate_kind = None, _lib.VGDR_GATE_NONE
         elif gate == 'vector':
@@ -718,11 +738,12 @@ class _Epilogue:
         _check_device(gate, gamma)
         self.gate, self.gamma, self.eps = gate, gamma, float(eps)
 
-    def struct(self, dtype):
-        """(vgdr_epilogue, tensors to keep alive) for o in `dtype`."""
+    def struct(self, dtype, rows: bool = False):
+        """(vgdr_epilogue, tensors to keep alive) for o in `dtype`; rows: the gate
+        is passed as it is, rows of a wider buffer (the caller checked its stride)."""
         if self.gate.dtype != dtype:
             raise NotImplementedError(f'the epilogue gate must have o\'s dtype {dtype}; got {self.gate.dtype}')
-        gate = _aligned(self.gate)
+        gate = self.gate if rows else _aligned(self.gate)
         gamma = _aligned(self.gamma if self.gamma.dtype in (torch.float32, dtype) else self.gamma.float())
         ep = _lib.Epilogue(gate=_ptr(gate), gamma=_ptr(gamma), gamma_dtype=_DTYPES[gamma.dtype], eps=self.eps)
         return ep, (gate, gamma)
@@ -874,7 +895,7 @@ class _ShortConv:
 
 def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state,
                cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION, epilogue=None,
-               conv: _ShortConv | None = None, w=None):
+               conv: _ShortConv | None = None, w=None, rows: bool = False):
     if (conv is None and epilogue is None and not inplace_final_state
             and _wants_grad(q, k, v, g, beta, initial_state, w)):
         # differentiable: the producers in torch, then the kernel with vgdr_scan_bwd as its backward
@@ -927,8 +948,15 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
         return torch.cat(outs, -1), S
     # with w the delta rule's strength is in w: no beta is validated or passed
     dvs = _DEC_DVS if wide_step else _REC_DVS
+    # rows (the layer's one-token step, the four-tap conv, a state): q, k, v and the
+    # epilogue gate may be read in place as rows of one projection output
+    rows = (rows and conv is not None and w is None and cu_seqlens is None and initial_state is not None
+            and conv.K == 4 and (epilogue is None or _row_stride(epilogue.gate.reshape(v.shape)) is not None))
     c = _Call(q, k, v, g, None if w is not None else beta, initial_state, cu_seqlens, gate=gate,
-              delta=delta and w is None, dv_to=lambda d: next(x for x in dvs if x >= d), fusion=fusion)
+              delta=delta and w is None, dv_to=lambda d: next(x for x in dvs if x >= d), fusion=fusion, rows=rows)
+    if c.ld_qk and epilogue is not None and _row_stride(epilogue.gate.reshape(v.shape)) != c.ld_v:
+        c.ld_qk = c.ld_v = 0                               # the gate's rows differ from v's: dense copies
+        c.q, c.k, c.v = _aligned(c.q), _aligned(c.k), _aligned(c.v)
     scale = c.dk ** -0.5 if scale is None else float(scale)
     o = c.new_output()
     in_place = (inplace_final_state and initial_state is not None and not c.padded
@@ -957,10 +985,17 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
             if epilogue is not None:
                 assert epilogue.gate.shape == (c.B, c.T, c.H, c.dv), \
                     f'the epilogue gate must be {(c.B, c.T, c.H, c.dv)}; got {tuple(epilogue.gate.shape)}'
-                ep, keep_ep = epilogue.struct(c.dtype)
+                ep, keep_ep = epilogue.struct(c.dtype, rows=bool(c.ld_qk))
             sc, keep_sc = conv.struct(c)
-            _lib.check(L.vgdr_decode_step(*head, None if fz is None else ctypes.byref(fz), ctypes.byref(sc),
-                                          None if ep is None else ctypes.byref(ep), _stream(c.device)))
+            fzp, scp, epp = (None if fz is None else ctypes.byref(fz)), ctypes.byref(sc), \
+                (None if ep is None else ctypes.byref(ep))
+            if c.ld_qk:
+                _lib.check(L.vgdr_decode_step_strided(
+                    _DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
+                    _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), c.B, c.H, c.dkp, c.dvp, c.ld_qk, c.ld_v, scale,
+                    fzp, scp, epp, _stream(c.device)))
+            else:
+                _lib.check(L.vgdr_decode_step(*head, fzp, scp, epp, _stream(c.device)))
             del keep, keep_ep, keep_sc
         elif epilogue is not None:
             assert epilogue.gate.shape == (c.B, c.T, c.H, c.dv), \
@@ -1060,7 +1095,9 @@ def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = T
     projections to the input of W_o, in one kernel.
 
     qp, kp: (B, L, H*dk) or (B, L, H, dk), vp: (B, L, H*dv) or (B, L, H, dv), the
-    raw projections W_q x, W_k x, W_v x.  conv_weights (w_q, w_k, w_v): the
+    raw projections W_q x, W_k x, W_v x.  For one token per sequence they (and
+    out_gate) may be column slices of one (B, 1, n) projection output: the kernel
+    then reads them in place (vgdr_decode_step_strided) instead of from copies.  conv_weights (w_q, w_k, w_v): the
     ShortConv weights, (D, 1, K) or (D, K); conv_cache (qp_cache, kp_cache,
     vp_cache): (N, K, D) in q's dtype, advanced in place (:929-941).  The
     kernel applies the conv and SiLU (:741-745), the q, k L2 norm unless
@@ -1087,7 +1124,7 @@ def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = T
                        out_norm_eps)
     o, _ = _recurrent(q, k, v, g, beta, gate=gate, delta=delta, scale=scale, initial_state=state,
                       output_final_state=True, cu_seqlens=cu_seqlens, inplace_final_state=True, fusion=fz,
-                      epilogue=ep, conv=_ShortConv(conv_weights, conv_cache))
+                      epilogue=ep, conv=_ShortConv(conv_weights, conv_cache), rows=True)
     return o
 
 
