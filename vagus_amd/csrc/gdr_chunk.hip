@@ -1405,14 +1405,14 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 //                                  S <- Gc S + (GE K)^T U~  (per-channel gate: K*G,
 //                                  K*Gend tiles and Gc per key channel).  For each
 //                                  chunk it leaves S_c (element type) and U~_c in LDS.
-//   output waves  NW, NW + 1       compute chunk c's O^T = S_c^T (GO Q)^T + U~_c^T A^T
-//                                  for all NW column strips, half the token blocks
-//                                  each, while the chain runs chunk c + 1.  A comes
+//   output waves  NW .. NW + NO - 1  compute chunk c's O^T = S_c^T (GO Q)^T + U~_c^T A^T
+//                                  for all NW column strips, 1 / NO of the token
+//                                  blocks each, while the chain runs chunk c + 1.  A comes
 //                                  from global memory straight into registers, issued
 //                                  two hand-overs before it is used; Q (or scale Q*G)
 //                                  from LDS (four producer waves) or, like A, from
 //                                  global memory (two).
-//   producers     NW + 2 ..        copy chunk c + 1's K (K*G and K*Gend), V, TE and gate
+//   producers     NW + NO ..       copy chunk c + 1's K (K*G and K*Gend), V, TE and gate
 //                                  factors into the idle half of the double buffer,
 //                                  and chunk c's Q into its own double buffer.
 // The chain waves thus issue 38 of the 60 MFMAs per chunk and column strip, and
@@ -1436,9 +1436,10 @@ __device__ __forceinline__ typename Elem<E>::frag2 ld_tr_pair(const E *p0, const
 // OUT false (with HS): only those states -- no outputs, so no U~ hand-over,
 // no Q copy and no A, Q loads or products in the output waves; the backward's
 // entry-state walk.
-template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA, bool HS = false, bool OUT = true>
-__global__ void __launch_bounds__(64 * (NW + 2 + NP))
-__attribute__((amdgpu_waves_per_eu(1, (NW + 2 + NP + 3) / 4)))
+template <int DK, int CH, int NW, int NP, typename E, bool VEC, bool DELTA, bool HS = false, bool OUT = true,
+          int NO = 2>
+__global__ void __launch_bounds__(64 * (NW + NO + NP))
+__attribute__((amdgpu_waves_per_eu(1, (NW + NO + NP + 3) / 4)))
 chunk_pipe_kernel(const ChunkParams p) {
     static_assert(sizeof(E) == 2, "transpose reads take 16-bit elements");
     using EL = Elem<E>;
@@ -1497,7 +1498,7 @@ chunk_pipe_kernel(const ChunkParams p) {
     const int nchunks = (int)((len + CH - 1) / CH);
 
     // ======================= producers ======================================
-    if (wave >= NW + 2) {
+    if (wave >= NW + NO) {
         using CK = RowCopy<E, CH, DK, NPT, !VEC, PK>;            // K rows (VEC: K*G and K*Gend tiles)
         using CV = RowCopy<E, CH, DVT, NPT, false, PV>;
         struct Staged {
@@ -1553,7 +1554,7 @@ chunk_pipe_kernel(const ChunkParams p) {
             }
         };
         if (nchunks > 0) {
-            const int pt = tid - 64 * (NW + 2);
+            const int pt = tid - 64 * (NW + NO);
             const Plans pl{CK::plan(VEC ? DK : sqk, DK, pt), CV::plan(sv, DV - col0, pt)};
             Staged s0, s1;
             // per-channel gate: Q*G of the even chunks in qa, of the odd ones in qb,
@@ -1737,9 +1738,10 @@ chunk_pipe_kernel(const ChunkParams p) {
     // CH = 64, the same A tile pairs each) of every column strip of the tile.
     // Three register sets of operands: chunk c + 2's loads are issued when chunk
     // c's outputs start, two hand-overs before they are used.
-    constexpr int NR = NB / 2;                                 // token blocks per output wave
+    static_assert(NO == 2 || NO == NB, "two output waves, or one per token block");
+    constexpr int NR = NB / NO;                                // token blocks per output wave
     const int o = wave - NW;
-    auto rb = [&](int i) { return i == 0 ? o : NB - 1 - o; };
+    auto rb = [&](int i) { return NO == NB ? o : (i == 0 ? o : NB - 1 - o); };
     if (nchunks == 0) return;
     const int g4 = lane >> 4, r16 = lane & 15;
     struct Ops {
@@ -1855,12 +1857,12 @@ chunk_pipe_kernel(const ChunkParams p) {
             unroll<NW>([&](auto s) {
                 if (col0 + 16 * s >= DV) return;
                 // the checkpoint's fragment order: lane (g, r) holds rows 16 kt + 4 g .. + 3
-                // of column 16 cb + r.  Output wave o stores key blocks o, o + 2, ..
+                // of column 16 cb + r.  Output wave o stores key blocks o, o + NO, ..
                 const E *sh = SH + ((odd ? NW : 0) + s) * 16 * SP + z + r16 * SP;
                 E *hs = reinterpret_cast<E *>(p.hs) + ((cbase + c) * H + h) * (int64_t)DK * DV;
                 const int cb = (col0 >> 4) + s;
-                unroll<NKB / 2>([&](auto k) {
-                    const int kt = 2 * k + o;
+                unroll<NKB / NO>([&](auto k) {
+                    const int kt = NO * k + o;
                     *reinterpret_cast<E4 *>(hs + ckpt_pos<DK>(cb, kt, lane)) =
                         *reinterpret_cast<const E4 *>(sh + 16 * kt + 4 * g4);
                 });
@@ -1913,8 +1915,13 @@ static void launch_pipe(const ChunkParams &p, int nw, int64_t state_blocks, hipS
     const dim3 grid((unsigned)state_blocks);
     if constexpr (!VEC) {
         if (nw == 4) {
-            hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 4, 2, E, VEC, DELTA, HS, OUT>), grid, dim3(64 * 8), 0, stream,
-                               p);
+            // 64-column tiles (packed batches with many (sequence, head) pairs): four
+            // producers (Q through LDS) and one output wave per token block, 12 waves
+            // at 164 VGPRs; gdn_varlen 604.5 -> 585.4 us against two producers and two
+            // output waves (four producers with two output waves: 590.0 us)
+            constexpr int NO = CH / 16;                       // one output wave per token block
+            hipLaunchKernelGGL((chunk_pipe_kernel<DK, CH, 4, 4, E, VEC, DELTA, HS, OUT, NO>), grid,
+                               dim3(64 * (8 + NO)), 0, stream, p);
             return;
         }
     }
