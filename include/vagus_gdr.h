@@ -465,6 +465,23 @@ int vgdr_decode_step(int dtype, int gate_kind, int use_delta,
                      float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
                      const vgdr_epilogue *epilogue, hipStream_t stream);
 
+/* The scalar gate and beta of a one-token decode step formed inside the
+ * decode kernel from the layer's input row (GatedDeltaNet._gates,
+ * linear_attention.py:719-721 and :734-735): p_a = W_a x and p_b = W_b x
+ * rounded to dtype (nn.Linear's outputs), g = neg_exp_a * softplus(p_a +
+ * dt_bias) and beta = p_b (logits; vgdr_fusion.beta_sigmoid activates them).
+ * x [B, dim] and w [H, dim] (W_a), followed by [H, dim] (W_b) with the delta
+ * rule, are in dtype with 16-byte aligned rows; dim a multiple of 16 bytes,
+ * at most 4096 elements for 16-bit dtypes and dv <= 128 (twice that at
+ * dv = 256, half for fp32). */
+typedef struct vgdr_gate_proj {
+    const void *x;
+    const void *w;
+    const float *neg_exp_a;  /* [H]: -exp(A_log) */
+    const float *dt_bias;    /* [H] */
+    int64_t dim;
+} vgdr_gate_proj;
+
 /* vgdr_decode_step (GatedDeltaNet.decode_step, linear_attention.py:918-952)
  * for one token per sequence (T = 1, n_seqs = B, no cu_seqlens) whose inputs
  * are rows of a wider buffer: token b's q, k are at
@@ -475,14 +492,17 @@ int vgdr_decode_step(int dtype, int gate_kind, int use_delta,
  * are separate nn.Linear outputs, :929 and :816, so it has no such form).  Needs `conv`
  * with K = 4 and 16-byte aligned weights and an initial_state
  * (VGDR_ERR_UNSUPPORTED otherwise); ld_qk >= H * dk, ld_v >= H * dv
- * (VGDR_ERR_INVALID otherwise). */
+ * (VGDR_ERR_INVALID otherwise).  With gate_proj (scalar gate only) the kernel
+ * forms g and beta itself and the g and beta arguments are not read: the
+ * layer's separate gate kernel is then not launched. */
 int vgdr_decode_step_strided(int dtype, int gate_kind, int use_delta,
                              const void *q, const void *k, const void *v,
                              const float *g, const float *beta,
                              void *o, const float *initial_state, float *final_state,
                              int64_t B, int64_t H, int64_t dk, int64_t dv, int64_t ld_qk, int64_t ld_v,
                              float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
-                             const vgdr_epilogue *epilogue, hipStream_t stream);
+                             const vgdr_epilogue *epilogue, const vgdr_gate_proj *gate_proj,
+                             hipStream_t stream);
 
 /* The short conv + SiLU (vgdr_short_conv's semantics) over a whole call's
  * tokens, for prefill: y[t] from x[t - K + 1 .. t] of the same sequence.

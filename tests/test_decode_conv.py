@@ -119,9 +119,10 @@ def test_strided_decode_step_argument_checks():
     the decode kernel would not run (no conv), before touching a device."""
     L = _lib.load()
 
-    def call(ld_qk, ld_v, sc):
-        return L.vgdr_decode_step_strided(1, 1, 1, None, None, None, None, None, None, None, None,
-                                          4, 16, 128, 128, ld_qk, ld_v, 1.0, None, sc, None, None)
+    def call(ld_qk, ld_v, sc, gp=None, gate_kind=1, h0=None):
+        # q, k, v NULL: were a check below ever to pass, the common check refuses the call
+        return L.vgdr_decode_step_strided(1, gate_kind, 1, None, None, None, None, None, None, h0, None,
+                                          4, 16, 128, 128, ld_qk, ld_v, 1.0, None, sc, None, gp, None)
     assert call(1024, 8192, None) == _lib.VGDR_ERR_INVALID
     assert b'row strides' in L.vgdr_last_error()
     assert call(8192, 2047, None) == _lib.VGDR_ERR_INVALID
@@ -130,6 +131,21 @@ def test_strided_decode_step_argument_checks():
     sc = _lib.ShortConv(weight_q=None, weight_k=None, weight_v=None, cache_q=None, cache_k=None, cache_v=None,
                         kernel_size=2, weight_dtype=_lib.VGDR_F32)
     assert call(8192, 8192, ctypes.byref(sc)) == _lib.VGDR_ERR_UNSUPPORTED
+    # the gate projections: scalar gate only, their pointers, dim a multiple of 8 up to 4096 (bf16, dv 128)
+    sc4 = _lib.ShortConv(weight_q=256, weight_k=512, weight_v=768, cache_q=1024, cache_k=1280, cache_v=1536,
+                         kernel_size=4, weight_dtype=_lib.VGDR_F32)
+    good = dict(x=4096, w=8192, neg_exp_a=12288, dt_bias=16384, dim=2048)
+    h0 = 20480
+    gp = _lib.GateProj(**good)
+    assert call(8192, 8192, ctypes.byref(sc4), ctypes.byref(gp), gate_kind=2, h0=h0) == _lib.VGDR_ERR_UNSUPPORTED
+    assert b'scalar gate' in L.vgdr_last_error()
+    for k_, v_, err in (('x', None, _lib.VGDR_ERR_INVALID), ('w', 8200, _lib.VGDR_ERR_INVALID),
+                        ('dim', 2044, _lib.VGDR_ERR_UNSUPPORTED), ('dim', 4104, _lib.VGDR_ERR_UNSUPPORTED)):
+        gp = _lib.GateProj(**{**good, k_: v_})
+        assert call(8192, 8192, ctypes.byref(sc4), ctypes.byref(gp), h0=h0) == err, (k_, v_)
+    gp = _lib.GateProj(**good)                       # passes its checks, then q, k, v NULL are refused
+    assert call(8192, 8192, ctypes.byref(sc4), ctypes.byref(gp), h0=h0) == _lib.VGDR_ERR_INVALID
+    assert b'q, k, v and o are required' in L.vgdr_last_error()
 
 
 # --- GPU ----------------------------------------------------------------------
@@ -291,3 +307,51 @@ def test_decode_step_reads_projection_rows_in_place(dk, dv, gate, epilogue):
     print(f'[parity] strided decode step: equal to dense={same}, o={eo:.3e} S={es:.3e} (tol {TOL:g})', flush=True)
     assert same and eo <= TOL and es <= TOL
 
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('dv,delta', [(128, True), (256, True), (128, False)])
+def test_decode_step_forms_the_scalar_gate_in_kernel(dv, delta):
+    """gate_proj: the decode kernel forms g = -exp(A_log) softplus(W_a x + dt_bias)
+    and the beta logits W_b x from the layer's input row itself (one kernel less
+    per layer), as the separate gate kernel does (vgdr_scalar_gates: the same
+    roundings; only the order of the fp32 sums over dim differs).  Checked
+    against the step fed that kernel's g and beta, and against the oracle."""
+    from vagus_amd import ops
+    B, H, dk, K, dim = 16, 4, 128, 4, 2048
+    qp, kp, vp, ws, cs, _, _, S0 = _decode_inputs(B, 1, H, dk, dv, K, 'scalar', torch.bfloat16, seed=61,
+                                                  w_dtype=torch.bfloat16)
+    g_ = torch.Generator().manual_seed(62)
+    x = torch.randn(B, 1, dim, generator=g_).bfloat16()
+    wab = (0.02 * torch.randn((2 if delta else 1) * H, dim, generator=g_)).bfloat16()
+    neg_a = -torch.exp(torch.rand(H, generator=g_) * 2.0 - 1.0)
+    dt_bias = torch.randn(H, generator=g_) * 0.5
+    print(f'\n[case] in-kernel scalar gate dv={dv} delta={delta}', flush=True)
+    dev = lambda t: t.cuda()
+
+    def step(gp):
+        S = dev(S0.clone())
+        caches = tuple(dev(c.clone()) for c in cs)
+        if gp:
+            g, beta, proj = None, None, (dev(x), dev(wab), dev(neg_a), dev(dt_bias))
+        else:
+            g, beta = ops.scalar_gates(dev(x), dev(wab), dev(neg_a), dev(dt_bias), with_beta=delta)
+            proj = None
+        o = ops.hip_decode_step(dev(qp), dev(kp), dev(vp), g, beta, S, scale=dk ** -0.5, delta=delta,
+                                conv_weights=tuple(dev(w) for w in ws), conv_cache=caches, beta_logits=delta,
+                                gate_proj=proj)
+        torch.cuda.synchronize()
+        return o, S, caches, g, beta
+
+    o1, S1, c1, _, _ = step(True)
+    o2, S2, c2, g2, b2 = step(False)
+    d_o, d_s = _rel(o1, o2), _rel(S1, S2)
+    caches_same = all(torch.equal(a, b) for a, b in zip(c1, c2))
+    # the oracle fed the gate kernel's g and beta (that kernel is checked against the module's _gates)
+    o_ref, S_ref, _ = gdr.decode_step(qp, kp, vp, g2.cpu().double(),
+                                      torch.sigmoid(b2.cpu().double()) if delta else None, S0.double(), ws, cs,
+                                      scale=dk ** -0.5, delta=delta)
+    eo, es = _rel(o1, o_ref), _rel(S1, S_ref)
+    print(f'[parity] in-kernel gate vs gate kernel: o {d_o:.2e} S {d_s:.2e} caches equal={caches_same}; '
+          f'vs oracle o {eo:.3e} S {es:.3e} (tol {TOL:g})', flush=True)
+    assert d_o <= 1e-3 and d_s <= 1e-3 and caches_same and eo <= TOL and es <= TOL

@@ -38,11 +38,18 @@ class ShortConv(ctypes.Structure):
                 ('kernel_size', ctypes.c_int), ('weight_dtype', ctypes.c_int)]
 
 
+class GateProj(ctypes.Structure):
+    """struct vgdr_gate_proj: the decode kernel's own scalar-gate and beta projections."""
+    _fields_ = [('x', ctypes.c_void_p), ('w', ctypes.c_void_p), ('neg_exp_a', ctypes.c_void_p),
+                ('dt_bias', ctypes.c_void_p), ('dim', ctypes.c_int64)]
+
+
 # every symbol the header declares, with its ctypes signature
 _P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
 _FZ = ctypes.POINTER(Fusion)
 _EP = ctypes.POINTER(Epilogue)
 _SC = ctypes.POINTER(ShortConv)
+_GP = ctypes.POINTER(GateProj)
 SIGNATURES = {
     'vgdr_version': (_I, []),
     'vgdr_last_error': (ctypes.c_char_p, []),
@@ -93,7 +100,7 @@ SIGNATURES = {
     'vgdr_decode_step': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                               _L, _L, _L, _L, _L, _L, _F, _FZ, _SC, _EP, _P]),
     'vgdr_decode_step_strided': (_I, [_I, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P,
-                                      _L, _L, _L, _L, _L, _L, _F, _FZ, _SC, _EP, _P]),
+                                      _L, _L, _L, _L, _L, _L, _F, _FZ, _SC, _EP, _GP, _P]),
     'vgdr_causal_conv1d': (_I, [_I, _P, _P, _I, _P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _P]),
     'vgdr_varlen_workspace_size': (_L, [_L]),
     'vgdr_varlen_prepare': (_I, [_P, _L, _L, _I, _P, _P]),

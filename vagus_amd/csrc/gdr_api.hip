@@ -714,11 +714,13 @@ int recurrent_call(int dtype, int gate_kind, int use_delta, const void *q, const
                    const void *w, const float *g, const float *beta, void *o, const float *initial_state,
                    float *final_state, const int32_t *cu_seqlens, int64_t B, int64_t T, int64_t H, int64_t dk,
                    int64_t dv, int64_t n_seqs, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
-                   const vgdr_epilogue *epilogue, hipStream_t stream, int64_t ld_qk = 0, int64_t ld_v = 0) {
+                   const vgdr_epilogue *epilogue, hipStream_t stream, int64_t ld_qk = 0, int64_t ld_v = 0,
+                   const vgdr_gate_proj *gp = nullptr) {
     g_err[0] = 0;
-    // with an explicit write vector, beta is not read
-    int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, w ? 0 : use_delta, q, k, v, g, beta, o,
-                          cu_seqlens, B, T, H, dk, dv, n_seqs);
+    // with an explicit write vector, beta is not read; with gate projections
+    // (checked by the caller) neither g nor beta is
+    int rc = check_common("vgdr_recurrent_fwd", dtype, gate_kind, w ? 0 : use_delta, q, k, v,
+                          gp ? gp->neg_exp_a : g, gp ? gp->dt_bias : beta, o, cu_seqlens, B, T, H, dk, dv, n_seqs);
     if (rc) return rc;
     if (w && !use_delta) return fail(VGDR_ERR_INVALID, "vgdr_recurrent_fwd: an explicit write vector needs the delta rule");
     vgdr::Fusion fz;
@@ -765,6 +767,11 @@ int recurrent_call(int dtype, int gate_kind, int use_delta, const void *q, const
     p.w = w;
     p.ld_qk = ld_qk;
     p.ld_v = ld_v;
+    if (gp) {
+        p.g = nullptr;
+        p.beta = nullptr;
+        p.gp = vgdr::GateProj{gp->x, gp->w, gp->neg_exp_a, gp->dt_bias, (int)gp->dim};
+    }
     return hip_status(vgdr::recurrent_fwd(dtype, (int)dk, (int)dv, gate_kind == VGDR_GATE_VECTOR, p, stream),
                       "vgdr_recurrent_fwd launch");
 }
@@ -784,7 +791,7 @@ int vgdr_decode_step_strided(int dtype, int gate_kind, int use_delta, const void
                              const float *g, const float *beta, void *o, const float *initial_state,
                              float *final_state, int64_t B, int64_t H, int64_t dk, int64_t dv, int64_t ld_qk,
                              int64_t ld_v, float scale, const vgdr_fusion *fusion, const vgdr_short_conv *conv,
-                             const vgdr_epilogue *epilogue, hipStream_t stream) {
+                             const vgdr_epilogue *epilogue, const vgdr_gate_proj *gate_proj, hipStream_t stream) {
     // the strides reach only the one-token decode kernel: it needs a state and the
     // four-tap conv with 16-byte aligned weights (any other call would run the
     // token walk, which reads dense rows)
@@ -796,8 +803,20 @@ int vgdr_decode_step_strided(int dtype, int gate_kind, int use_delta, const void
         !aligned16(conv->weight_v) || !initial_state)
         return fail(VGDR_ERR_UNSUPPORTED, "vgdr_decode_step_strided: strided rows need the four-tap short conv "
                     "with 16-byte aligned weights and an initial state");
+    if (gate_proj) {
+        const int64_t ve = dtype == VGDR_F32 ? 4 : 8, nt = dv > 128 ? 512 : 256;
+        if (gate_kind != VGDR_GATE_SCALAR)
+            return fail(VGDR_ERR_UNSUPPORTED, "vgdr_decode_step_strided: gate projections are for the scalar gate");
+        if (!gate_proj->x || !gate_proj->w || !gate_proj->neg_exp_a || !gate_proj->dt_bias ||
+            !aligned16(gate_proj->x) || !aligned16(gate_proj->w))
+            return fail(VGDR_ERR_INVALID, "vgdr_decode_step_strided: gate projections need x, w (16-byte aligned), "
+                        "neg_exp_a and dt_bias");
+        if (gate_proj->dim <= 0 || gate_proj->dim % ve || gate_proj->dim > 2 * nt * ve)
+            return fail(VGDR_ERR_UNSUPPORTED, "vgdr_decode_step_strided: gate projection dim=%lld (a multiple of "
+                        "%lld up to %lld)", (long long)gate_proj->dim, (long long)ve, (long long)(2 * nt * ve));
+    }
     return recurrent_call(dtype, gate_kind, use_delta, q, k, v, nullptr, g, beta, o, initial_state, final_state,
-                          nullptr, B, 1, H, dk, dv, B, scale, fusion, conv, epilogue, stream, ld_qk, ld_v);
+                          nullptr, B, 1, H, dk, dv, B, scale, fusion, conv, epilogue, stream, ld_qk, ld_v, gate_proj);
 }
 
 int vgdr_recurrent_fwd_w(int dtype, int gate_kind, const void *q, const void *k, const void *v, const void *w,

@@ -154,6 +154,19 @@ struct ScanBwdParams {
     float scale;
 };
 
+// The scalar gate and the beta logits of a one-token decode step formed in the
+// decode kernel from the layer's input row (GatedDeltaNet._gates,
+// linear_attention.py:719-721, :734-735): p = W_a x and W_b x rounded to the
+// element type (nn.Linear's output), g = neg_a softplus(p + dt_bias), beta = the
+// rounded W_b x (logits).  x NULL: g and beta come in as tensors.
+struct GateProj {
+    const void *x;                // [n_tokens, dim] in the element type, 16-byte aligned rows
+    const void *w;                // [H, dim] W_a, then [H, dim] W_b (delta rule), 16-byte aligned rows
+    const float *neg_a;           // [H]: -exp(A_log)
+    const float *dt_bias;         // [H]
+    int dim;                      // a multiple of 8
+};
+
 struct RecParams {
     const void *q, *k, *v;
     const float *g;
@@ -175,6 +188,7 @@ struct RecParams {
     // and v and the epilogue gate (ld_v); 0 for dense rows (H dk, H dv).  Rows of
     // one fused projection output [n_tokens, 4 H d] are read in place this way
     int64_t ld_qk, ld_v;
+    GateProj gp;                  // the decode kernel's own gate projections (scalar gate), or x NULL
 };
 
 // dtype: 0 fp32, 1 bf16, 2 fp16.  gate_vector: per-channel (KDA) decay.

@@ -350,6 +350,9 @@ recurrent_kernel(const RecParams p) {
 // made every wave of the chip load, then every wave store (58 % of HBM).
 template <int DV> constexpr int decode_threads() { return DV > 128 ? 512 : 256; }
 
+// torch's softplus at beta 1, threshold 20, with the accurate expf / log1pf
+__device__ __forceinline__ float softplus_acc(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
 template <int DK, int DV, typename E, int GATE, int MODE, typename WT>
 __global__ void __launch_bounds__(decode_threads<DV>())
 __attribute__((amdgpu_waves_per_eu(GATE == 2 || (MODE & 4) || DV > 128 ? 1 : 4)))
@@ -375,6 +378,7 @@ decode_conv_kernel(const RecParams p) {
     __shared__ __attribute__((aligned(16))) float red[WIDE ? 1 : NWV][2][WIDE ? 4 : DV];
     __shared__ float nrm[NWV][3];           // per-wave sums: q^2, k^2, then q . k (q . w)
     __shared__ float ssq[WIDE ? NWV : 1];   // WIDE epilogue: per-wave sums of o^2
+    __shared__ float gpart[GATE == 1 ? NWV : 1][2];   // per-wave sums of W_a x, W_b x (gate projections)
     __shared__ float sc[2];                 // decay (scalar gate), beta
     __shared__ __attribute__((aligned(16))) float wsv[WR ? DK : 4];
     __shared__ __attribute__((aligned(16))) float gts[EPI ? DV : 4];
@@ -434,7 +438,30 @@ decode_conv_kernel(const RecParams p) {
                                  : EL::to_f(reinterpret_cast<const E *>(p.ep.gamma)[tid]);
         }
     }
-    if (tid == 0) {
+    // the gate projections W_a[h] . x and W_b[h] . x (GateProj): every thread up
+    // to GU 16-byte slices of the row, loaded with the token's other operands and
+    // summed after the conv (dim <= GU NT VE, checked by the API)
+    const bool gproj = GATE == 1 && p.gp.x != nullptr;
+    constexpr int GVE = 16 / (int)sizeof(E), GU = 2;
+    typedef E GV __attribute__((ext_vector_type(GVE)));
+    GV gxv[GU], gav[GU], gbv[GU];
+    if (gproj) {
+        const int nu = p.gp.dim / GVE;
+        const E *xr = reinterpret_cast<const E *>(p.gp.x) + t * (int64_t)p.gp.dim;
+        const E *wa = reinterpret_cast<const E *>(p.gp.w) + (int64_t)h * p.gp.dim;
+        const E *wb = wa + (int64_t)H * p.gp.dim;
+        const bool wbeta = !WR && p.use_delta;
+#pragma unroll
+        for (int i = 0; i < GU; ++i) {
+            const int u = tid + i * NT;
+            gxv[i] = gav[i] = gbv[i] = GV{};
+            if (u < nu) {
+                gxv[i] = *reinterpret_cast<const GV *>(xr + (int64_t)u * GVE);
+                gav[i] = *reinterpret_cast<const GV *>(wa + (int64_t)u * GVE);
+                if (wbeta) gbv[i] = *reinterpret_cast<const GV *>(wb + (int64_t)u * GVE);
+            }
+        }
+    } else if (tid == 0) {
         if (GATE == 1 && p.g) gsc = p.g[t * H + h];
         if (!WR && p.use_delta) bsc = p.beta[t * H + h];
     }
@@ -449,6 +476,23 @@ decode_conv_kernel(const RecParams p) {
     if (own) {
         qv = tq.apply(cache_q, HDK, cq);
         kv = tk.apply(cache_k, HDK, cq);
+    }
+    if (gproj) {
+        float pa = 0.f, pb = 0.f;
+#pragma unroll
+        for (int i = 0; i < GU; ++i)
+#pragma unroll
+            for (int e = 0; e < GVE; ++e) {
+                pa += (float)gxv[i][e] * (float)gav[i][e];
+                pb += (float)gxv[i][e] * (float)gbv[i][e];
+            }
+        pa = wave_sum64(pa);
+        pb = wave_sum64(pb);
+        if (lane == 0) {
+            gpart[wave][0] = pa;
+            gpart[wave][1] = pb;
+        }
+        if (!p.fz.qk_l2norm) lds_barrier();                  // else the norm's barrier below
     }
     if (p.fz.qk_l2norm) {
         float sq = wave_sum64(qv * qv), sk = wave_sum64(kv * kv);
@@ -495,7 +539,18 @@ decode_conv_kernel(const RecParams p) {
         }
     }
     if (tid == 0) {
-        sc[0] = (GATE == 1 && p.g) ? __expf(gsc) : 1.f;
+        if (gproj) {
+            float sa = 0.f, sb = 0.f;
+#pragma unroll
+            for (int w = 0; w < NWV; ++w) {
+                sa += gpart[w][0];
+                sb += gpart[w][1];
+            }
+            // nn.Linear's outputs in the element type, then the gate (fp32)
+            gsc = p.gp.neg_a[h] * softplus_acc(EL::to_f(EL::from_f(sa)) + p.gp.dt_bias[h]);
+            bsc = EL::to_f(EL::from_f(sb));
+        }
+        sc[0] = (GATE == 1 && (p.g || gproj)) ? __expf(gsc) : 1.f;
         sc[1] = WR ? 1.f : (p.use_delta && p.fz.beta_sigmoid ? sigmoidf_(bsc) : bsc);
     }
     lds_barrier();

@@ -444,12 +444,14 @@ class GatedDeltaNet(nn.Module):
         return c[1:]
 
     def _decode_inputs(self, x):
-        """(qp, kp, vp, out_gate, g, beta) for the one-token decode kernel: the
-        projections of x (B, 1, dim), the log-decay in fp32 (or the KDA gate's
-        pre-activation) and the beta logits, with the regrouped weights of
-        _decode_weights.  The values are those of the separate projections and
-        of _gates(raw_gate=vector, raw_beta=delta) up to the GEMMs' summation
-        order."""
+        """(qp, kp, vp, out_gate, g, beta, gate_proj) for the one-token decode
+        kernel: the projections of x (B, 1, dim), the log-decay in fp32 (or the
+        KDA gate's pre-activation) and the beta logits, with the regrouped
+        weights of _decode_weights.  With the scalar gate, g and beta are None
+        and gate_proj = (x, [W_a; W_b], -exp(A_log), dt_bias): the decode
+        kernel forms them itself.  The values are those of the separate
+        projections and of _gates(raw_gate=vector, raw_beta=delta) up to the
+        GEMMs' summation order."""
         B, L = x.shape[0], x.shape[1]
         w4, wab, gconst = self._decode_weights()
         if w4 is not None:
@@ -467,9 +469,8 @@ class GatedDeltaNet(nn.Module):
             qp, kp, vp, og = self.wq(x), self.wk(x), self.wv(x), self.wg(x)
         if wab is None:
             g, beta = self._gates(x, raw_gate=self.gate == 'vector', raw_beta=self.delta)
-            return qp, kp, vp, og, g, beta
-        g, beta = ops.scalar_gates(x, wab, *gconst, with_beta=self.delta)
-        return qp, kp, vp, og, g, beta
+            return qp, kp, vp, og, g, beta, None
+        return qp, kp, vp, og, None, None, (x, wab, *gconst)
 
     @torch.no_grad()
     def decode_step(self, x):
@@ -486,8 +487,9 @@ class GatedDeltaNet(nn.Module):
         H, dk, dv = self.head_count, self.key_head_dim, self.value_head_dim
         if L == 1 and type(self)._write is GatedDeltaNet._write and self._decode_kernel_fits():
             vec = self.gate == 'vector'
-            qp, kp, vp, og, g, beta = self._decode_inputs(x)
+            qp, kp, vp, og, g, beta, gp = self._decode_inputs(x)
             o = ops.hip_decode_step(qp, kp, vp, g, beta, self.state, scale=self.scale, delta=self.delta,
+                                    gate_proj=gp,
                                     conv_weights=self._conv_weights(), conv_cache=self._caches(), l2norm=True,
                                     beta_logits=self.delta, gate_in_kernel=vec,
                                     A_log=self.A_log if vec else None, dt_bias=self.dt_bias if vec else None,

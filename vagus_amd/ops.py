@@ -228,7 +228,7 @@ class _Call:
     row strides; 0 when the operands are dense)."""
 
     def __init__(self, q, k, v, g, beta, initial_state, cu_seqlens, *, gate: str, delta: bool,
-                 dv_to, fusion: _Fusion = _NO_FUSION, rows: bool = False):
+                 dv_to, fusion: _Fusion = _NO_FUSION, rows: bool = False, gate_proj: bool = False):
         _check_device(q, k, v, g, beta, initial_state, cu_seqlens)
         _check_grad(q, k, v, g, beta, initial_state)
         assert q.dim() == 4 and k.shape == q.shape and v.dim() == 4 and v.shape[:3] == q.shape[:3], \
@@ -241,10 +241,10 @@ class _Call:
         if gate == 'vector':
             assert g is not None and g.shape == (B, T, H, dk), \
                 f'a per-channel gate is (B, T, H, dk); got {None if g is None else tuple(g.shape)}'
-        elif gate == 'scalar':
+        elif gate == 'scalar' and not gate_proj:
             assert g is not None and g.shape == (B, T, H), \
                 f'a scalar gate is (B, T, H); got {None if g is None else tuple(g.shape)}'
-        if delta:
+        if delta and not gate_proj:
             assert beta is not None and beta.shape == (B, T, H), 'the delta rule needs beta (B, T, H)'
         if cu_seqlens is not None:
             assert B == 1, f'packed varlen input (cu_seqlens) has batch 1, got {B}'
@@ -273,15 +273,17 @@ class _Call:
             self.q = _aligned(_pad_to(q, {1: dkp}))
             self.k = _aligned(_pad_to(k, {1: dkp}))
             self.v = _aligned(_pad_to(v, {1: dvp}))
-        if gate == 'none' or g is None:
+        if gate == 'none' or (g is None and not gate_proj):
             self.g, self.gate_kind = None, _lib.VGDR_GATE_NONE
         elif gate == 'vector':
             # a fused gate pre-activation stays in q's 16-bit type (no fp32 copy)
             gk = g if (fusion.gate and g.dtype == q.dtype and q.dtype != torch.float32) else g.float()
             self.g, self.gate_kind = _aligned(_pad_to(gk, {1: dkp})), _lib.VGDR_GATE_VECTOR
+        elif gate_proj:                                   # the decode kernel forms g and beta itself
+            self.g, self.gate_kind = None, _lib.VGDR_GATE_SCALAR
         else:
             self.g, self.gate_kind = g.float().contiguous(), _lib.VGDR_GATE_SCALAR
-        self.beta = beta.float().contiguous() if delta else None
+        self.beta = beta.float().contiguous() if delta and not gate_proj else None
         self.h0 = None if initial_state is None else \
             _aligned(_pad_to(initial_state.float(), {1: dvp, 2: dkp}))
         self.cu = cu
@@ -895,7 +897,7 @@ class _ShortConv:
 
 def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_final_state,
                cu_seqlens, inplace_final_state=False, fusion: _Fusion = _NO_FUSION, epilogue=None,
-               conv: _ShortConv | None = None, w=None, rows: bool = False):
+               conv: _ShortConv | None = None, w=None, rows: bool = False, gate_proj=None):
     if (conv is None and epilogue is None and not inplace_final_state
             and _wants_grad(q, k, v, g, beta, initial_state, w)):
         # differentiable: the producers in torch, then the kernel with vgdr_scan_bwd as its backward
@@ -950,10 +952,28 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
     dvs = _DEC_DVS if wide_step else _REC_DVS
     # rows (the layer's one-token step, the four-tap conv, a state): q, k, v and the
     # epilogue gate may be read in place as rows of one projection output
-    rows = (rows and conv is not None and w is None and cu_seqlens is None and initial_state is not None
-            and conv.K == 4 and (epilogue is None or _row_stride(epilogue.gate.reshape(v.shape)) is not None))
+    one_token = (conv is not None and w is None and cu_seqlens is None and initial_state is not None
+                 and conv.K == 4 and q.shape[1] == 1)
+    rows = rows and one_token and (epilogue is None or _row_stride(epilogue.gate.reshape(v.shape)) is not None)
+    if gate_proj is not None:
+        # (x, W_ab, -exp(A_log), dt_bias): the decode kernel forms the scalar gate and
+        # beta from x; any other call takes them from the gate kernel first
+        x_, w_, na_, db_ = gate_proj
+        dim = x_.shape[-1]
+        fits = (one_token and gate == 'scalar' and x_.dtype == q.dtype and w_.dtype == q.dtype
+                and dim % (16 // q.element_size()) == 0
+                and dim <= 2 * (512 if dv > 128 else 256) * (16 // q.element_size()))
+        if fits:
+            gp_x = _aligned(x_.reshape(-1, dim))
+            gp_w = _aligned(w_)
+            gp_na, gp_db = na_.float().contiguous(), db_.float().contiguous()
+        else:
+            g, beta = scalar_gates(x_, w_, na_, db_, with_beta=delta)
+            g, beta = g.reshape(q.shape[:3]), (beta.reshape(q.shape[:3]) if delta else None)
+            gate_proj = None
     c = _Call(q, k, v, g, None if w is not None else beta, initial_state, cu_seqlens, gate=gate,
-              delta=delta and w is None, dv_to=lambda d: next(x for x in dvs if x >= d), fusion=fusion, rows=rows)
+              delta=delta and w is None, dv_to=lambda d: next(x for x in dvs if x >= d), fusion=fusion, rows=rows,
+              gate_proj=gate_proj is not None)
     if c.ld_qk and epilogue is not None and _row_stride(epilogue.gate.reshape(v.shape)) != c.ld_v:
         c.ld_qk = c.ld_v = 0                               # the gate's rows differ from v's: dense copies
         c.q, c.k, c.v = _aligned(c.q), _aligned(c.k), _aligned(c.v)
@@ -989,11 +1009,16 @@ def _recurrent(q, k, v, g, beta, *, gate, delta, scale, initial_state, output_fi
             sc, keep_sc = conv.struct(c)
             fzp, scp, epp = (None if fz is None else ctypes.byref(fz)), ctypes.byref(sc), \
                 (None if ep is None else ctypes.byref(ep))
-            if c.ld_qk:
+            if c.ld_qk or gate_proj is not None:
+                gp = None
+                if gate_proj is not None:
+                    gp = _lib.GateProj(x=_ptr(gp_x), w=_ptr(gp_w), neg_exp_a=_ptr(gp_na), dt_bias=_ptr(gp_db),
+                                       dim=dim)
                 _lib.check(L.vgdr_decode_step_strided(
                     _DTYPES[c.dtype], c.gate_kind, int(delta), _ptr(c.q), _ptr(c.k), _ptr(c.v), _ptr(c.g),
-                    _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), c.B, c.H, c.dkp, c.dvp, c.ld_qk, c.ld_v, scale,
-                    fzp, scp, epp, _stream(c.device)))
+                    _ptr(c.beta), _ptr(o), _ptr(h0), _ptr(S), c.B, c.H, c.dkp, c.dvp, c.ld_qk or c.H * c.dkp,
+                    c.ld_v or c.H * c.dvp, scale, fzp, scp, epp, None if gp is None else ctypes.byref(gp),
+                    _stream(c.device)))
             else:
                 _lib.check(L.vgdr_decode_step(*head, fzp, scp, epp, _stream(c.device)))
             del keep, keep_ep, keep_sc
@@ -1090,14 +1115,19 @@ def hip_recurrent(q, k, v, g, beta, S0, *, scale: float, delta: bool, cu_seqlens
 def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = True, conv_weights=None,
                     conv_cache=None, l2norm: bool = True, beta_logits: bool = False, gate_in_kernel: bool = False,
                     A_log=None, dt_bias=None, lower_bound: float | None = None, out_gate=None,
-                    out_norm_weight=None, out_norm_eps: float = 1e-6, cu_seqlens=None):
+                    out_norm_weight=None, out_norm_eps: float = 1e-6, cu_seqlens=None, gate_proj=None):
     """GatedDeltaNet.decode_step (linear_attention.py:918-952) from the
     projections to the input of W_o, in one kernel.
 
     qp, kp: (B, L, H*dk) or (B, L, H, dk), vp: (B, L, H*dv) or (B, L, H, dv), the
     raw projections W_q x, W_k x, W_v x.  For one token per sequence they (and
     out_gate) may be column slices of one (B, 1, n) projection output: the kernel
-    then reads them in place (vgdr_decode_step_strided) instead of from copies.  conv_weights (w_q, w_k, w_v): the
+    then reads them in place (vgdr_decode_step_strided) instead of from copies.
+    gate_proj (x, W_ab, -exp(A_log), dt_bias), for the scalar gate in place of g
+    and beta: x (B, 1, dim) is the layer's input, W_ab [W_a; W_b] (W_a alone
+    without the delta rule); the kernel forms g = -exp(A_log) softplus(W_a x +
+    dt_bias) and the beta logits W_b x itself (linear_attention.py:719-721,
+    :734-735), with nn.Linear's rounding of W_a x and W_b x.  conv_weights (w_q, w_k, w_v): the
     ShortConv weights, (D, 1, K) or (D, K); conv_cache (qp_cache, kp_cache,
     vp_cache): (N, K, D) in q's dtype, advanced in place (:929-941).  The
     kernel applies the conv and SiLU (:741-745), the q, k L2 norm unless
@@ -1113,7 +1143,7 @@ def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = T
     q = qp.reshape(B, L, H, dk)
     k = kp.reshape(B, L, H, dk)
     v = vp.reshape(B, L, H, dv)
-    gate = _gate_of(g)
+    gate = 'scalar' if gate_proj is not None else _gate_of(g)
     if gate_in_kernel:
         assert gate == 'vector', 'the fused gate activation is a KDA (vector-gate) kernel'
     fz = _Fusion(l2norm=l2norm, beta=beta_logits, gate=gate_in_kernel, A_log=A_log, dt_bias=dt_bias,
@@ -1124,7 +1154,7 @@ def hip_decode_step(qp, kp, vp, g, beta, state, *, scale: float, delta: bool = T
                        out_norm_eps)
     o, _ = _recurrent(q, k, v, g, beta, gate=gate, delta=delta, scale=scale, initial_state=state,
                       output_final_state=True, cu_seqlens=cu_seqlens, inplace_final_state=True, fusion=fz,
-                      epilogue=ep, conv=_ShortConv(conv_weights, conv_cache), rows=True)
+                      epilogue=ep, conv=_ShortConv(conv_weights, conv_cache), rows=True, gate_proj=gate_proj)
     return o
 
 
