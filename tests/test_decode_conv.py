@@ -355,3 +355,35 @@ def test_decode_step_forms_the_scalar_gate_in_kernel(dv, delta):
     print(f'[parity] in-kernel gate vs gate kernel: o {d_o:.2e} S {d_s:.2e} caches equal={caches_same}; '
           f'vs oracle o {eo:.3e} S {es:.3e} (tol {TOL:g})', flush=True)
     assert d_o <= 1e-3 and d_s <= 1e-3 and caches_same and eo <= TOL and es <= TOL
+
+
+@pytest.mark.gpu
+def test_decode_step_gate_proj_falls_back_beyond_the_kernel_row():
+    """A gate projection row longer than the decode kernel holds (dim 8192 > 4096
+    at dv = 128) is formed by the gate kernel first: the step then equals the one
+    fed that kernel's g and beta exactly."""
+    from vagus_amd import ops
+    B, H, dk, dv, K, dim = 8, 2, 64, 128, 4, 8192
+    qp, kp, vp, ws, cs, _, _, S0 = _decode_inputs(B, 1, H, dk, dv, K, 'scalar', torch.bfloat16, seed=71,
+                                                  w_dtype=torch.bfloat16)
+    g_ = torch.Generator().manual_seed(72)
+    x = torch.randn(B, 1, dim, generator=g_).bfloat16()
+    wab = (0.01 * torch.randn(2 * H, dim, generator=g_)).bfloat16()
+    neg_a, dt_bias = -torch.rand(H, generator=g_) - 0.5, torch.randn(H, generator=g_) * 0.5
+    print('\n[case] gate projections beyond the kernel row (dim 8192)', flush=True)
+    dev = lambda t: t.cuda()
+    outs = []
+    for gp in (True, False):
+        S = dev(S0.clone())
+        caches = tuple(dev(c.clone()) for c in cs)
+        if gp:
+            g, beta, proj = None, None, (dev(x), dev(wab), dev(neg_a), dev(dt_bias))
+        else:
+            g, beta = ops.scalar_gates(dev(x), dev(wab), dev(neg_a), dev(dt_bias))
+            proj = None
+        o = ops.hip_decode_step(dev(qp), dev(kp), dev(vp), g, beta, S, scale=dk ** -0.5, beta_logits=True,
+                                conv_weights=tuple(dev(w) for w in ws), conv_cache=caches, gate_proj=proj)
+        outs.append((o, S))
+    same = torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    print(f'[parity] fallback equal={same}', flush=True)
+    assert same
