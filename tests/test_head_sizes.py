@@ -5,7 +5,7 @@ bench_linear_attention.py:18-20).  It runs through the chunk kernels as
 more dv tiles and through the token kernel as 128-column slices; the layer's
 one-token decode step (the conv with its caches, the L2 norm, the gates, the
 recurrence and the epilogue) is one kernel at this width too.  Checked against the fp64
-oracle at the north_star bars (1e-5 fp32, 2e-2 bf16).  dk = 256 (the LAX3
+oracle at the parity bars (relative L2 1e-5 fp32, 2e-2 bf16).  dk = 256 (the LAX3
 recipe, lax3_340M.yaml:83-85) is refused with NotImplementedError: the kernels
 hold at most 128 key rows per state strip."""
 import pytest

@@ -18,7 +18,7 @@ that saves each chunk's entry state (autograd), whose gradients are checked
 against the recomputing backward and, on a few (sequence, head) slices,
 against the oracle's reverse-mode gradients.
 
-Bar (north_star): relative L2 error <= 2e-2 for bf16 inputs on outputs and
+Bar: relative L2 error <= 2e-2 for bf16 inputs on outputs and
 final states; integer work bit-exact.
 """
 import pytest
