@@ -943,8 +943,8 @@ def main():
         write_traffic(args.write_traffic)
         return
     if args.gpus != 1:
-        print(f'bench.py: this build measures one GPU only (the gated delta-rule core has no '
-              f'cross-GPU path here); --gpus {args.gpus} is not supported', file=sys.stderr)
+        print(f'bench.py: measures one GPU only (the gated delta-rule core has no '
+              f'cross-GPU path); --gpus {args.gpus} is not supported', file=sys.stderr)
         sys.exit(2)
 
     import torch

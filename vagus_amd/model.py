@@ -9,7 +9,7 @@ shapes for the all-linear layout (layer_pattern 'gdn', write 'delta'):
 embedding -> [RMSNorm -> GatedDeltaNet -> residual, RMSNorm -> SwiGLU FFN
 -> residual] x layers -> RMSNorm -> head tied to the embedding
 (gdn_lm.py:188-195, block.py:54-91).  Softmax and parallel layers and the
-Kalman writes are outside this build and raise NotImplementedError.
+Kalman writes are not implemented here and raise NotImplementedError.
 
 ``RaggedGenerator`` serves a batch of prompts of any lengths, one stream per
 cache row: the prompts go through every layer as one packed call per kernel
